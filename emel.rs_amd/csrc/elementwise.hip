@@ -1,0 +1,425 @@
+// elementwise.hip -- gfx950 kernels for the elementwise family:
+// equal-count binary add/sub/mul/div (binary.rs:383-424), row broadcast
+// (broadcast.rs:352-390), 4-D modulo broadcast (OpRepeat + binary,
+// generic.rs:1641-1665), unary abs/neg/tanh/elu/relu/sigmoid/gelu/silu/exp
+// (unary.rs:472-606), scale (activation.rs:366-377) and fused SwiGLU.
+//
+// All of them are HBM-bound streams (<= 1 flop per byte except the
+// transcendental ones, which stay under the memory time).  Three kernel
+// shapes cover every accepted layout:
+//   k_dense    all operands dense and paired by linear index: 128-bit
+//              loads/stores, VPT float4 per thread, a scalar tail;
+//   k_rowbcast dense [rows, ne0] op dense row [ne0]: 128-bit loads, the
+//              row operand re-read from L2;
+//   k_rows     any strides with a contiguous dim 0 (permuted views, modulo
+//              broadcast): 128-bit accesses along dim 0, rows decoded with
+//              multiply-high division;
+//   k_ordinal  anything else: one element per thread, the reference's
+//              per-element ordinal decode.
+#include "common.hpp"
+#include "launch.hpp"
+#include "libm_replica.hpp"
+
+namespace emel {
+namespace {
+
+// ---- per-element formulas ------------------------------------------------
+
+template <Ew OP> struct Fn;
+
+#define EMEL_FN(OPV, TABLE, BINARY, EXPR)                                                          \
+    template <> struct Fn<Ew::OPV> {                                                                \
+        static constexpr bool kTable = TABLE;                                                       \
+        static constexpr bool kBinary = BINARY;                                                     \
+        __device__ __forceinline__ static float apply(float a, float b, float s, const uint64_t *t) \
+        {                                                                                           \
+            (void)b; (void)s; (void)t;                                                              \
+            return EXPR;                                                                            \
+        }                                                                                           \
+    };
+
+EMEL_FN(Add, false, true, a + b)
+EMEL_FN(Sub, false, true, a - b)
+EMEL_FN(Mul, false, true, a * b)
+EMEL_FN(Div, false, true, a / b)
+EMEL_FN(Abs, false, false, __builtin_fabsf(a))
+EMEL_FN(Neg, false, false, -a)
+EMEL_FN(Tanh, false, false, emel_tanhf(a))
+EMEL_FN(Elu, false, false, a >= 0.0f ? a : emel_expm1f(a))
+// f32::max(x, 0) as glibc fmaxf computes it: x unless x < 0 or NaN.
+EMEL_FN(Relu, false, false, a >= 0.0f ? a : 0.0f)
+EMEL_FN(Sigmoid, true, false, 1.0f / (1.0f + emel_expf(-a, t)))
+EMEL_FN(Gelu, false, false, emel_gelu(a))
+EMEL_FN(Silu, true, false, emel_silu(a, t))
+EMEL_FN(Exp, true, false, emel_expf(a, t))
+EMEL_FN(Scale, false, false, a * s)
+// silu(gate) rounded to f32, then times up: the OpSilu -> OpMul chain.
+EMEL_FN(Swiglu, true, true, emel_silu(a, t) * b)
+#undef EMEL_FN
+
+template <Ew OP>
+__device__ __forceinline__ float4 apply4(float4 a, float4 b, float s, const uint64_t *t)
+{
+    float4 r;
+    r.x = Fn<OP>::apply(a.x, b.x, s, t);
+    r.y = Fn<OP>::apply(a.y, b.y, s, t);
+    r.z = Fn<OP>::apply(a.z, b.z, s, t);
+    r.w = Fn<OP>::apply(a.w, b.w, s, t);
+    return r;
+}
+
+// Stages the 2^(i/32) table in LDS for the exp-based formulas.
+template <Ew OP>
+__device__ __forceinline__ const uint64_t *stage_table(uint64_t *lds)
+{
+    if constexpr (Fn<OP>::kTable) {
+        if (threadIdx.x < 32) lds[threadIdx.x] = kExp2Table[threadIdx.x];
+        __syncthreads();
+        return lds;
+    } else {
+        return nullptr;
+    }
+}
+
+// ---- dense: every operand contiguous, paired by linear index -------------
+
+template <Ew OP, int VPT>
+__global__ __launch_bounds__(kBlock) void k_dense(const float *a, const float *b, float *o, uint64_t nvec,
+                                                   uint64_t n, float s)
+{
+    __shared__ uint64_t lds[32];
+    const uint64_t *tab = stage_table<OP>(lds);
+    const float4 *a4 = reinterpret_cast<const float4 *>(a);
+    const float4 *b4 = reinterpret_cast<const float4 *>(b);
+    float4 *o4 = reinterpret_cast<float4 *>(o);
+    const uint64_t base = static_cast<uint64_t>(blockIdx.x) * (kBlock * VPT) + threadIdx.x;
+    float4 va[VPT], vb[VPT];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const uint64_t i = base + static_cast<uint64_t>(j) * kBlock;
+        if (i < nvec) {
+            va[j] = a4[i];
+            if constexpr (Fn<OP>::kBinary) vb[j] = b4[i];
+            else vb[j] = va[j];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const uint64_t i = base + static_cast<uint64_t>(j) * kBlock;
+        if (i < nvec) o4[i] = apply4<OP>(va[j], vb[j], s, tab);
+    }
+    const uint64_t gid = static_cast<uint64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    const uint64_t idx = nvec * 4 + gid;
+    if (idx < n) o[idx] = Fn<OP>::apply(a[idx], Fn<OP>::kBinary ? b[idx] : 0.0f, s, tab);
+}
+
+// ---- dense [rows, ne0] op dense row [ne0], ne0 % 4 == 0 --------------------
+
+template <Ew OP, int VPT>
+__global__ __launch_bounds__(kBlock) void k_rowbcast(const float *a, const float *b, float *o, uint32_t nvec,
+                                                      FastDiv nv0, float s)
+{
+    __shared__ uint64_t lds[32];
+    const uint64_t *tab = stage_table<OP>(lds);
+    const float4 *a4 = reinterpret_cast<const float4 *>(a);
+    const float4 *b4 = reinterpret_cast<const float4 *>(b);
+    float4 *o4 = reinterpret_cast<float4 *>(o);
+    const uint32_t base = blockIdx.x * (kBlock * VPT) + threadIdx.x;
+    float4 va[VPT], vb[VPT];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const uint32_t i = base + j * kBlock;
+        if (i < nvec) {
+            va[j] = a4[i];
+            vb[j] = b4[nv0.mod(i)];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const uint32_t i = base + j * kBlock;
+        if (i < nvec) o4[i] = apply4<OP>(va[j], vb[j], s, tab);
+    }
+}
+
+// ---- strided with contiguous dim 0 ---------------------------------------
+
+struct RowsGeo {
+    uint32_t nvec;   // float4 work items (< 2^32)
+    FastDiv nv0;     // float4 per row
+    FastDiv ne1, ne2;
+    int64_t a_st[4], b_st[4], o_st[4];
+    FastDiv a_mod[3], b_mod[3]; // source extents of dims 1..3
+    uint32_t a_modmask, b_modmask; // bit d-1 set: dim d needs a modulo
+    uint32_t b_splat;              // b has extent 1 along dim 0
+};
+
+__device__ __forceinline__ int64_t rows_offset(const int64_t *st, const FastDiv *md, uint32_t mask, uint32_t i1,
+                                               uint32_t i2, uint32_t i3)
+{
+    if (mask & 1u) i1 = md[0].mod(i1);
+    if (mask & 2u) i2 = md[1].mod(i2);
+    if (mask & 4u) i3 = md[2].mod(i3);
+    return static_cast<int64_t>(i1) * st[1] + static_cast<int64_t>(i2) * st[2] + static_cast<int64_t>(i3) * st[3];
+}
+
+template <Ew OP>
+__global__ __launch_bounds__(kBlock) void k_rows(RowsGeo g, const float *a, const float *b, float *o, float s)
+{
+    __shared__ uint64_t lds[32];
+    const uint64_t *tab = stage_table<OP>(lds);
+    const uint32_t i = blockIdx.x * kBlock + threadIdx.x;
+    if (i >= g.nvec) return;
+    const uint32_t row = g.nv0.div(i);
+    const uint32_t v = i - row * g.nv0.d;
+    const uint32_t r2 = g.ne1.div(row);
+    const uint32_t i1 = row - r2 * g.ne1.d;
+    const uint32_t i3 = g.ne2.div(r2);
+    const uint32_t i2 = r2 - i3 * g.ne2.d;
+    const int64_t col = 4 * static_cast<int64_t>(v);
+    const float4 va = *reinterpret_cast<const float4 *>(a + rows_offset(g.a_st, g.a_mod, g.a_modmask, i1, i2, i3) + col);
+    float4 vb = va;
+    if constexpr (Fn<OP>::kBinary) {
+        const float *bp = b + rows_offset(g.b_st, g.b_mod, g.b_modmask, i1, i2, i3);
+        if (g.b_splat) {
+            const float x = *bp;
+            vb = make_float4(x, x, x, x);
+        } else {
+            vb = *reinterpret_cast<const float4 *>(bp + col);
+        }
+    }
+    const int64_t oo = static_cast<int64_t>(i1) * g.o_st[1] + static_cast<int64_t>(i2) * g.o_st[2] +
+                       static_cast<int64_t>(i3) * g.o_st[3] + col;
+    *reinterpret_cast<float4 *>(o + oo) = apply4<OP>(va, vb, s, tab);
+}
+
+// ---- general: one element per thread, per-operand ordinal decode ----------
+
+struct OrdOperand {
+    uint64_t ne[4];
+    int64_t st[4];
+    uint32_t addr; // Addr
+};
+
+struct OrdGeo {
+    uint64_t count;
+    uint64_t ne[4]; // destination extents
+    int64_t o_st[4];
+    OrdOperand a, b;
+};
+
+__device__ __forceinline__ int64_t ord_offset(const OrdOperand &p, uint64_t k, const uint64_t *c)
+{
+    if (p.addr == static_cast<uint32_t>(Addr::Ordinal)) {
+        int64_t off = 0;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            off += static_cast<int64_t>(k % p.ne[d]) * p.st[d];
+            k /= p.ne[d];
+        }
+        return off;
+    }
+    int64_t off = 0;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        const uint64_t cd = p.addr == static_cast<uint32_t>(Addr::Broadcast) ? c[d] % p.ne[d] : c[d];
+        off += static_cast<int64_t>(cd) * p.st[d];
+    }
+    return off;
+}
+
+template <Ew OP>
+__global__ __launch_bounds__(kBlock) void k_ordinal(OrdGeo g, const float *a, const float *b, float *o, float s)
+{
+    __shared__ uint64_t lds[32];
+    const uint64_t *tab = stage_table<OP>(lds);
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kBlock;
+    for (uint64_t k = static_cast<uint64_t>(blockIdx.x) * kBlock + threadIdx.x; k < g.count; k += stride) {
+        uint64_t c[4];
+        uint64_t rem = k;
+        int64_t oo = 0;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            c[d] = rem % g.ne[d];
+            rem /= g.ne[d];
+            oo += static_cast<int64_t>(c[d]) * g.o_st[d];
+        }
+        const float va = a[ord_offset(g.a, k, c)];
+        const float vb = Fn<OP>::kBinary ? b[ord_offset(g.b, k, c)] : 0.0f;
+        o[oo] = Fn<OP>::apply(va, vb, s, tab);
+    }
+}
+
+// ---- host-side selection ---------------------------------------------------
+
+bool contiguous(const Operand &p)
+{
+    // Row-major with unit element stride; strides of extent-1 dims do not
+    // affect addressing and are ignored.
+    int64_t expect = 1;
+    for (int d = 0; d < 4; ++d) {
+        if (p.ne[d] != 1 && p.st[d] != expect) return false;
+        expect *= static_cast<int64_t>(p.ne[d]);
+    }
+    return true;
+}
+
+bool same_ne(const Operand &x, const Operand &y)
+{
+    for (int d = 0; d < 4; ++d)
+        if (x.ne[d] != y.ne[d]) return false;
+    return true;
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int vpt_choice()
+{
+    static const int v = [] {
+        const char *e = getenv("EMEL_EW_VPT");
+        const int x = e ? atoi(e) : 2;
+        return (x == 1 || x == 2 || x == 4) ? x : 2;
+    }();
+    return v;
+}
+
+template <Ew OP>
+hipError_t launch_op(const EwArgs &x, hipStream_t stream)
+{
+    constexpr bool kBin = Fn<OP>::kBinary;
+    const float *a = static_cast<const float *>(x.a.data);
+    const float *b = kBin ? static_cast<const float *>(x.b.data) : nullptr;
+    float *o = static_cast<float *>(x.o.data);
+    const uint64_t n = x.count;
+    if (n == 0) return hipSuccess;
+
+    // Linear pairing holds when each source is dense and either addressed by
+    // ordinal or shaped like the destination.
+    auto linear = [&](const Operand &p, Addr ad) {
+        return contiguous(p) && (ad == Addr::Ordinal || same_ne(p, x.o));
+    };
+    const bool all_linear = contiguous(x.o) && linear(x.a, x.a_addr) && (!kBin || linear(x.b, x.b_addr));
+    const bool vec_ok = aligned16(a) && aligned16(o) && (!kBin || aligned16(b));
+
+    if (all_linear && vec_ok) {
+        const int vpt = vpt_choice();
+        const uint64_t nvec = n / 4;
+        const uint64_t per_block = static_cast<uint64_t>(kBlock) * vpt;
+        const uint64_t tail = n - nvec * 4;
+        uint64_t blocks = (nvec + per_block - 1) / per_block;
+        const uint64_t tail_blocks = (tail + kBlock - 1) / kBlock;
+        if (blocks < tail_blocks) blocks = tail_blocks;
+        if (blocks > 0x7fffffffull) return hipErrorInvalidConfiguration;
+        const dim3 grid(static_cast<uint32_t>(blocks));
+        if (vpt == 1) k_dense<OP, 1><<<grid, kBlock, 0, stream>>>(a, b, o, nvec, n, x.scale);
+        else if (vpt == 2) k_dense<OP, 2><<<grid, kBlock, 0, stream>>>(a, b, o, nvec, n, x.scale);
+        else k_dense<OP, 4><<<grid, kBlock, 0, stream>>>(a, b, o, nvec, n, x.scale);
+        return hipGetLastError();
+    }
+
+    const uint64_t ne0 = x.o.ne[0];
+    const uint64_t rows = n / ne0;
+
+    // dense [rows, ne0] op a dense row of ne0 values
+    if (kBin && ne0 % 4 == 0 && vec_ok && contiguous(x.o) && contiguous(x.a) && same_ne(x.a, x.o) &&
+        x.a_addr != Addr::Ordinal && x.b.ne[0] == ne0 && x.b.ne[1] == 1 && x.b.ne[2] == 1 && x.b.ne[3] == 1 &&
+        x.b.st[0] == 1 && n / 4 < 0xffffffffull && x.b_addr != Addr::Ordinal) {
+        const int vpt = vpt_choice();
+        const uint32_t nvec = static_cast<uint32_t>(n / 4);
+        const uint32_t per_block = kBlock * vpt;
+        const dim3 grid((nvec + per_block - 1) / per_block);
+        const FastDiv nv0(static_cast<uint32_t>(ne0 / 4));
+        if (vpt == 1) k_rowbcast<OP, 1><<<grid, kBlock, 0, stream>>>(a, b, o, nvec, nv0, x.scale);
+        else if (vpt == 2) k_rowbcast<OP, 2><<<grid, kBlock, 0, stream>>>(a, b, o, nvec, nv0, x.scale);
+        else k_rowbcast<OP, 4><<<grid, kBlock, 0, stream>>>(a, b, o, nvec, nv0, x.scale);
+        return hipGetLastError();
+    }
+
+    // contiguous dim 0 everywhere, coordinates shared with the destination
+    auto coord_addressed = [&](const Operand &p, Addr ad) {
+        return ad != Addr::Ordinal || same_ne(p, x.o);
+    };
+    auto strides4 = [](const Operand &p) {
+        for (int d = 1; d < 4; ++d)
+            if (p.ne[d] != 1 && p.st[d] % 4 != 0) return false;
+        return true;
+    };
+    const bool b_splat = kBin && x.b.ne[0] == 1;
+    const bool rows_ok = ne0 % 4 == 0 && vec_ok && n / 4 < 0xffffffffull && rows < 0xffffffffull &&
+                         x.o.ne[1] < 0xffffffffull && x.o.ne[2] < 0xffffffffull && x.o.st[0] == 1 &&
+                         strides4(x.o) && (x.a.st[0] == 1 || x.a.ne[0] == 1) && x.a.ne[0] == ne0 &&
+                         strides4(x.a) && coord_addressed(x.a, x.a_addr) &&
+                         (!kBin || ((b_splat || (x.b.ne[0] == ne0 && x.b.st[0] == 1)) &&
+                                    (b_splat || strides4(x.b)) && coord_addressed(x.b, x.b_addr)));
+    if (rows_ok) {
+        RowsGeo g{};
+        g.nvec = static_cast<uint32_t>(n / 4);
+        g.nv0 = FastDiv(static_cast<uint32_t>(ne0 / 4));
+        g.ne1 = FastDiv(static_cast<uint32_t>(x.o.ne[1]));
+        g.ne2 = FastDiv(static_cast<uint32_t>(x.o.ne[2]));
+        uint32_t am = 0, bm = 0;
+        for (int d = 0; d < 4; ++d) {
+            g.a_st[d] = x.a.st[d];
+            g.o_st[d] = x.o.st[d];
+            g.b_st[d] = kBin ? x.b.st[d] : 0;
+        }
+        for (int d = 1; d < 4; ++d) {
+            g.a_mod[d - 1] = FastDiv(static_cast<uint32_t>(x.a.ne[d]));
+            if (x.a.ne[d] != x.o.ne[d]) am |= 1u << (d - 1);
+            if (kBin) {
+                g.b_mod[d - 1] = FastDiv(static_cast<uint32_t>(x.b.ne[d]));
+                if (x.b.ne[d] != x.o.ne[d]) bm |= 1u << (d - 1);
+            } else {
+                g.b_mod[d - 1] = FastDiv(1);
+            }
+        }
+        g.a_modmask = am;
+        g.b_modmask = bm;
+        g.b_splat = b_splat ? 1u : 0u;
+        const dim3 grid((g.nvec + kBlock - 1) / kBlock);
+        k_rows<OP><<<grid, kBlock, 0, stream>>>(g, a, b, o, x.scale);
+        return hipGetLastError();
+    }
+
+    OrdGeo g{};
+    g.count = n;
+    for (int d = 0; d < 4; ++d) {
+        g.ne[d] = x.o.ne[d];
+        g.o_st[d] = x.o.st[d];
+        g.a.ne[d] = x.a.ne[d];
+        g.a.st[d] = x.a.st[d];
+        g.b.ne[d] = kBin ? x.b.ne[d] : 1;
+        g.b.st[d] = kBin ? x.b.st[d] : 0;
+    }
+    g.a.addr = static_cast<uint32_t>(x.a_addr);
+    g.b.addr = static_cast<uint32_t>(kBin ? x.b_addr : Addr::SameCoords);
+    uint64_t blocks = (n + kBlock - 1) / kBlock;
+    if (blocks > 65536) blocks = 65536;
+    k_ordinal<OP><<<dim3(static_cast<uint32_t>(blocks)), kBlock, 0, stream>>>(g, a, b, o, x.scale);
+    return hipGetLastError();
+}
+
+} // namespace
+
+hipError_t launch_elementwise(const EwArgs &args, hipStream_t stream)
+{
+    switch (args.op) {
+    case Ew::Add: return launch_op<Ew::Add>(args, stream);
+    case Ew::Sub: return launch_op<Ew::Sub>(args, stream);
+    case Ew::Mul: return launch_op<Ew::Mul>(args, stream);
+    case Ew::Div: return launch_op<Ew::Div>(args, stream);
+    case Ew::Abs: return launch_op<Ew::Abs>(args, stream);
+    case Ew::Neg: return launch_op<Ew::Neg>(args, stream);
+    case Ew::Tanh: return launch_op<Ew::Tanh>(args, stream);
+    case Ew::Elu: return launch_op<Ew::Elu>(args, stream);
+    case Ew::Relu: return launch_op<Ew::Relu>(args, stream);
+    case Ew::Sigmoid: return launch_op<Ew::Sigmoid>(args, stream);
+    case Ew::Gelu: return launch_op<Ew::Gelu>(args, stream);
+    case Ew::Silu: return launch_op<Ew::Silu>(args, stream);
+    case Ew::Exp: return launch_op<Ew::Exp>(args, stream);
+    case Ew::Scale: return launch_op<Ew::Scale>(args, stream);
+    case Ew::Swiglu: return launch_op<Ew::Swiglu>(args, stream);
+    }
+    return hipErrorInvalidValue;
+}
+
+} // namespace emel

@@ -1,0 +1,232 @@
+// libm_replica.hpp -- scalar math with the exact bits the reference's CPU
+// path produces.
+//
+// The reference calls Rust std f32::exp / f32::tanh (unary.rs:538, :598;
+// reductions.rs:584), which on x86_64-linux-gnu are glibc expf / tanhf.
+// A correctly rounded GPU exp/tanh differs from glibc on ~6e-5 (expf) and
+// ~5% (tanhf) of inputs, so these functions restate glibc's published
+// algorithms instead:
+//
+//   emel_expf    ARM optimized-routines expf (math/expf.c, the
+//                implementation in glibc since 2.28): x*N/ln2 = k + r with
+//                N = 32, exp(x) = 2^(k/N) * p(r) evaluated in double, with
+//                the range reduction and polynomial contracted to fused
+//                multiply-adds as the x86_64 FMA build of glibc computes it.
+//   emel_expm1f  fdlibm s_expm1f.c (Sun Microsystems, 1993; glibc's
+//                sysdeps/ieee754/flt-32): reduction by ln2 split into hi/lo,
+//                a degree-5 rational correction term, no contraction.
+//   emel_tanhf   fdlibm s_tanhf.c: tanh(x) = 1 - 2/(expm1(2|x|)+2) for
+//                |x| >= 1, -t/(t+2) with t = expm1(-2|x|) below.
+//
+// The 2^(i/32) table is the correctly rounded double of 2^(i/32) with the
+// exponent contribution i << 47 subtracted, so that adding k << 47 yields
+// 2^(k/32) for any integer k.
+//
+// Every function is __host__ __device__: tests build them for the CPU and
+// compare them with the host glibc over all 2^32 float inputs.  Compile
+// with -ffp-contract=off: the only fused operations are the explicit fma().
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace emel {
+
+// tab[i] = bits(2^(i/32)) - (i << 47), i = 0..31.
+static constexpr uint64_t kExp2Table[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
+};
+
+__host__ __device__ __forceinline__ float bits_to_f32(uint32_t u) { return __builtin_bit_cast(float, u); }
+__host__ __device__ __forceinline__ uint32_t f32_to_bits(float f) { return __builtin_bit_cast(uint32_t, f); }
+__host__ __device__ __forceinline__ double bits_to_f64(uint64_t u) { return __builtin_bit_cast(double, u); }
+__host__ __device__ __forceinline__ uint64_t f64_to_bits(double d) { return __builtin_bit_cast(uint64_t, d); }
+
+// expf.  `tab` is kExp2Table or a copy of it (kernels stage it in LDS).
+__host__ __device__ __forceinline__ float emel_expf(float x, const uint64_t *tab)
+{
+    // N/ln2 with N = 32, the rounding shift 1.5*2^52, and the cubic
+    // coefficients of 2^(r/N) - 1 pre-scaled by N^-1, N^-2, N^-3.
+    constexpr double kInvLn2N = 0x1.71547652b82fep+0 * 32.0;
+    constexpr double kShift = 0x1.8p+52;
+    constexpr double kC0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+    constexpr double kC1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+    constexpr double kC2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+
+    const uint32_t ux = f32_to_bits(x);
+    const uint32_t abstop = (ux >> 20) & 0x7ffu;
+    if (abstop >= 0x42bu) { // |x| >= 88 or x is NaN/Inf
+        if (ux == 0xff800000u) return 0.0f;           // -inf
+        if (abstop >= 0x7f8u) return x + x;           // +inf or NaN
+        if (x > 0x1.62e42ep6f) return __builtin_inff(); // overflow
+        if (x < -0x1.9fe368p6f) return 0.0f;           // underflow
+    }
+    const double xd = static_cast<double>(x);
+    double kd = __builtin_fma(kInvLn2N, xd, kShift);
+    const uint64_t ki = f64_to_bits(kd);
+    kd -= kShift;
+    const double r = __builtin_fma(kInvLn2N, xd, -kd);
+    const uint64_t t = tab[ki & 31u] + (ki << 47);
+    const double s = bits_to_f64(t);
+    const double z = __builtin_fma(kC0, r, kC1);
+    const double r2 = r * r;
+    double y = __builtin_fma(kC2, r, 1.0);
+    y = __builtin_fma(z, r2, y);
+    y = y * s;
+    return static_cast<float>(y);
+}
+
+// expm1f, fdlibm float version.
+__host__ __device__ __forceinline__ float emel_expm1f(float x)
+{
+    constexpr float kLn2Hi = 6.9313812256e-01f;  // 0x3f317180
+    constexpr float kLn2Lo = 9.0580006145e-06f;  // 0x3717f7d1
+    constexpr float kInvLn2 = 1.4426950216e+00f; // 0x3fb8aa3b
+    constexpr float kQ1 = -3.3333335072e-02f;    // 0xbd088889
+    constexpr float kQ2 = 1.5873016091e-03f;     // 0x3ad00d01
+    constexpr float kQ3 = -7.9365076090e-05f;    // 0xb8a670cd
+    constexpr float kQ4 = 4.0082177293e-06f;     // 0x36867e54
+    constexpr float kQ5 = -2.0109921195e-07f;    // 0xb457edbb
+
+    uint32_t hx = f32_to_bits(x);
+    const uint32_t negative = hx & 0x80000000u;
+    hx &= 0x7fffffffu;
+    if (hx >= 0x4195b844u) { // |x| >= 27 ln2
+        if (hx >= 0x42b17218u) {
+            if (hx > 0x7f800000u) return x + x; // NaN
+            if (hx == 0x7f800000u) return negative ? -1.0f : x;
+            if (x > 8.8721679688e+01f) return __builtin_inff();
+        }
+        if (negative) return 1.0e-30f - 1.0f; // -1
+    }
+    float hi, lo, c = 0.0f, t;
+    int32_t k;
+    if (hx > 0x3eb17218u) { // |x| > ln2/2
+        if (hx < 0x3f851592u) { // |x| < 3 ln2 / 2
+            if (!negative) { hi = x - kLn2Hi; lo = kLn2Lo; k = 1; }
+            else { hi = x + kLn2Hi; lo = -kLn2Lo; k = -1; }
+        } else {
+            k = static_cast<int32_t>(kInvLn2 * x + (negative ? -0.5f : 0.5f));
+            t = static_cast<float>(k);
+            hi = x - t * kLn2Hi;
+            lo = t * kLn2Lo;
+        }
+        x = hi - lo;
+        c = (hi - x) - lo;
+    } else if (hx < 0x33000000u) { // |x| < 2^-25
+        return x;
+    } else {
+        k = 0;
+    }
+    const float hfx = 0.5f * x;
+    const float hxs = x * hfx;
+    const float r1 = 1.0f + hxs * (kQ1 + hxs * (kQ2 + hxs * (kQ3 + hxs * (kQ4 + hxs * kQ5))));
+    t = 3.0f - r1 * hfx;
+    float e = hxs * ((r1 - t) / (6.0f - x * t));
+    if (k == 0) return x - (x * e - hxs);
+    e = (x * (e - c) - c);
+    e -= hxs;
+    if (k == -1) return 0.5f * (x - e) - 0.5f;
+    if (k == 1) {
+        if (x < -0.25f) return -2.0f * (e - (x + 0.5f));
+        return 1.0f + 2.0f * (x - e);
+    }
+    float y;
+    if (k <= -2 || k > 56) {
+        y = 1.0f - (e - x);
+        y = bits_to_f32(f32_to_bits(y) + (static_cast<uint32_t>(k) << 23));
+        return y - 1.0f;
+    }
+    if (k < 23) {
+        t = bits_to_f32(0x3f800000u - (0x1000000u >> k)); // 1 - 2^-k
+        y = t - (e - x);
+    } else {
+        t = bits_to_f32(static_cast<uint32_t>(0x7f - k) << 23); // 2^-k
+        y = x - (e + t);
+        y += 1.0f;
+    }
+    return bits_to_f32(f32_to_bits(y) + (static_cast<uint32_t>(k) << 23));
+}
+
+// tanhf, fdlibm float version.
+__host__ __device__ __forceinline__ float emel_tanhf(float x)
+{
+    const uint32_t jx = f32_to_bits(x);
+    const uint32_t ix = jx & 0x7fffffffu;
+    const bool negative = (jx >> 31) != 0;
+    float z;
+    if (ix >= 0x7f800000u) { // Inf or NaN
+        return negative ? 1.0f / x - 1.0f : 1.0f / x + 1.0f;
+    }
+    if (ix < 0x41b00000u) { // |x| < 22
+        if (ix == 0) return x;
+        if (ix < 0x24000000u) return x * (1.0f + x); // |x| < 2^-55
+        const float ax = bits_to_f32(ix);
+        if (ix >= 0x3f800000u) { // |x| >= 1
+            const float t = emel_expm1f(2.0f * ax);
+            z = 1.0f - 2.0f / (t + 2.0f);
+        } else {
+            const float t = emel_expm1f(-2.0f * ax);
+            z = -t / (t + 2.0f);
+        }
+    } else {
+        z = 1.0f - 1.0e-30f; // 1 with inexact
+    }
+    return negative ? -z : z;
+}
+
+// fp32 -> binary16 bits with the reference helper's arithmetic
+// (unary.rs:546-570): round to nearest even through a scaled add, NaN -> 0x7e00.
+__host__ __device__ __forceinline__ uint16_t emel_fp32_to_fp16(float value)
+{
+    const float scale_to_inf = bits_to_f32(0x77800000u);  // 2^112
+    const float scale_to_zero = bits_to_f32(0x08800000u); // 2^-110
+    float base = (__builtin_fabsf(value) * scale_to_inf) * scale_to_zero;
+    const uint32_t w = f32_to_bits(value);
+    const uint32_t doubled = w + w;
+    const uint32_t sign = w & 0x80000000u;
+    uint32_t bias = doubled & 0xff000000u;
+    if (bias < 0x71000000u) bias = 0x71000000u;
+    base += bits_to_f32((bias >> 1) + 0x07800000u);
+    const uint32_t bb = f32_to_bits(base);
+    const uint32_t nonsign = ((bb >> 13) & 0x7c00u) + (bb & 0x0fffu);
+    return static_cast<uint16_t>((sign >> 16) | (doubled > 0xff000000u ? 0x7e00u : nonsign));
+}
+
+// binary16 bits -> fp32 (unary.rs:572-586, quant.rs:287-300).
+__host__ __device__ __forceinline__ float emel_fp16_to_f32(uint16_t h)
+{
+    const uint32_t w = static_cast<uint32_t>(h) << 16;
+    const uint32_t sign = w & 0x80000000u;
+    const uint32_t doubled = w + w;
+    const float normalized = bits_to_f32((doubled >> 4) + (0xe0u << 23)) * bits_to_f32(0x07800000u);
+    const float denormalized = bits_to_f32((doubled >> 17) | (126u << 23)) - 0.5f;
+    return bits_to_f32(sign | f32_to_bits(doubled < (1u << 27) ? denormalized : normalized));
+}
+
+// SiluFormula (unary.rs:595-600).
+__host__ __device__ __forceinline__ float emel_silu(float x, const uint64_t *tab)
+{
+    return x / (1.0f + emel_expf(-x, tab));
+}
+
+// GeluFormula (unary.rs:522-541): separate products, fp16 round trips on
+// the input and the result.
+__host__ __device__ __forceinline__ float emel_gelu(float value)
+{
+    if (value <= -10.0f) return 0.0f;
+    if (value >= 10.0f) return value;
+    const float q = emel_fp16_to_f32(emel_fp32_to_fp16(value));
+    const float inner = 0.7978846f * (q + 0.044715f * q * q * q);
+    const float approximation = 0.5f * q * (1.0f + emel_tanhf(inner));
+    return emel_fp16_to_f32(emel_fp32_to_fp16(approximation));
+}
+
+} // namespace emel

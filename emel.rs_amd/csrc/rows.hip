@@ -1,0 +1,552 @@
+// rows.hip -- gfx950 kernels for the per-row ops: rms_norm (+weight),
+// norm, soft_max (dense and strided) and the scaled + masked soft_max.
+//
+// A row is dim 0 of the view; rows enumerate (i1, i2, i3).  One wave64
+// owns one row: it loads the row once into registers (128-bit loads),
+// reduces across its 64 lanes with butterfly shuffles, and writes the
+// result once, so each row costs one HBM read and one HBM write.  Rows
+// wider than the register budget stream through global memory in several
+// passes (the later passes hit L2).  Row reductions keep the reference's
+// arithmetic: f32-rounded squares summed in f64 (normalization.rs:343-362),
+// exp(x - max) summed in f64 (reductions.rs:565-601), divisions and square
+// roots correctly rounded.  The strided soft_max keeps the reference's
+// sequential f32 sum (reductions.rs:603-638) with one row per lane.
+#include <cstdlib>
+
+#include "common.hpp"
+#include "launch.hpp"
+#include "libm_replica.hpp"
+
+namespace emel {
+namespace {
+
+struct RowGeo {
+    uint32_t rows;
+    uint32_t ncols;
+    FastDiv ne1, ne2; // row index -> (i1, i2, i3)
+    int64_t x_st[4];
+    int64_t y_st[4];
+};
+
+struct MaskGeo {
+    const uint16_t *p; // dense f16 [ncols, ne1, m2, m3] or null
+    uint32_t ne1, m2, m3;
+    uint32_t head_major; // logical row order puts i2 fastest (mask shared by all i2)
+};
+
+__device__ __forceinline__ void row_coords(const RowGeo &g, uint32_t r, uint32_t &i1, uint32_t &i2, uint32_t &i3)
+{
+    const uint32_t t = g.ne1.div(r);
+    i1 = r - t * g.ne1.d;
+    i3 = g.ne2.div(t);
+    i2 = t - i3 * g.ne2.d;
+}
+
+__device__ __forceinline__ int64_t row_base(const int64_t *st, uint32_t i1, uint32_t i2, uint32_t i3)
+{
+    return static_cast<int64_t>(i1) * st[1] + static_cast<int64_t>(i2) * st[2] + static_cast<int64_t>(i3) * st[3];
+}
+
+__device__ __forceinline__ float4 mask4(const uint16_t *m)
+{
+    const uint2 raw = *reinterpret_cast<const uint2 *>(m);
+    return make_float4(emel_fp16_to_f32(static_cast<uint16_t>(raw.x & 0xffffu)),
+                       emel_fp16_to_f32(static_cast<uint16_t>(raw.x >> 16)),
+                       emel_fp16_to_f32(static_cast<uint16_t>(raw.y & 0xffffu)),
+                       emel_fp16_to_f32(static_cast<uint16_t>(raw.y >> 16)));
+}
+
+// f32 products rounded, then accumulated in f64 (run_rms_norm).
+__device__ __forceinline__ double sumsq4(float4 v)
+{
+    const float a = v.x * v.x, b = v.y * v.y, c = v.z * v.z, d = v.w * v.w;
+    return (static_cast<double>(a) + static_cast<double>(b)) + (static_cast<double>(c) + static_cast<double>(d));
+}
+
+__device__ __forceinline__ double sum4(float4 v)
+{
+    return (static_cast<double>(v.x) + static_cast<double>(v.y)) +
+           (static_cast<double>(v.z) + static_cast<double>(v.w));
+}
+
+__device__ __forceinline__ float max4(float4 v)
+{
+    return __builtin_fmaxf(__builtin_fmaxf(v.x, v.y), __builtin_fmaxf(v.z, v.w));
+}
+
+__device__ __forceinline__ float4 mul4(float4 v, float k) { return make_float4(v.x * k, v.y * k, v.z * k, v.w * k); }
+__device__ __forceinline__ float4 mul4(float4 v, float4 w)
+{
+    return make_float4(v.x * w.x, v.y * w.y, v.z * w.z, v.w * w.w);
+}
+__device__ __forceinline__ float4 add4(float4 v, float4 w)
+{
+    return make_float4(v.x + w.x, v.y + w.y, v.z + w.z, v.w + w.w);
+}
+__device__ __forceinline__ float4 sub4(float4 v, float k) { return make_float4(v.x - k, v.y - k, v.z - k, v.w - k); }
+__device__ __forceinline__ float4 div4(float4 v, float k) { return make_float4(v.x / k, v.y / k, v.z / k, v.w / k); }
+__device__ __forceinline__ float4 exp4(float4 v, const uint64_t *t)
+{
+    return make_float4(emel_expf(v.x, t), emel_expf(v.y, t), emel_expf(v.z, t), emel_expf(v.w, t));
+}
+
+// ---- vectorized rows: contiguous dim 0, ncols % 4 == 0 ------------------
+// NV > 0: the row (nv = ncols/4 float4) is held in NV float4 per lane.
+// NV == 0: the row is streamed in passes.
+
+template <RowOp OP, int NV>
+__global__ __launch_bounds__(kBlock) void k_row_vec(RowGeo g, const float *x, float *y, const float *w, MaskGeo mg,
+                                                     float eps, float scale)
+{
+    constexpr bool kSoft = OP == RowOp::SoftMax || OP == RowOp::SoftMaxExt;
+    __shared__ uint64_t lds[32];
+    const uint64_t *tab = nullptr;
+    if constexpr (kSoft) {
+        if (threadIdx.x < 32) lds[threadIdx.x] = kExp2Table[threadIdx.x];
+        __syncthreads();
+        tab = lds;
+    }
+    const uint32_t wave = threadIdx.x / kWave;
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint32_t blk = (OP == RowOp::SoftMaxExt && mg.head_major && (gridDim.x & 7u) == 0) ? xcd_major_block(8)
+                                                                                              : blockIdx.x;
+    const uint32_t logical = blk * (kBlock / kWave) + wave;
+    if (logical >= g.rows) return;
+
+    uint32_t i1, i2, i3;
+    if (OP == RowOp::SoftMaxExt && mg.head_major) {
+        // logical order: i2 fastest, so the rows sharing one mask row run
+        // back to back on one XCD and the mask is fetched from HBM once.
+        const uint32_t t = g.ne2.div(logical);
+        i2 = logical - t * g.ne2.d;
+        i3 = g.ne1.div(t);
+        i1 = t - i3 * g.ne1.d;
+    } else {
+        row_coords(g, logical, i1, i2, i3);
+    }
+    const float4 *xr = reinterpret_cast<const float4 *>(x + row_base(g.x_st, i1, i2, i3));
+    float4 *yr = reinterpret_cast<float4 *>(y + row_base(g.y_st, i1, i2, i3));
+    const uint32_t nv = g.ncols / 4;
+    const uint16_t *mr = nullptr;
+    if (OP == RowOp::SoftMaxExt && mg.p) {
+        const uint64_t mrow = (static_cast<uint64_t>(i3 % mg.m3) * mg.m2 + (i2 % mg.m2)) * mg.ne1 + i1;
+        mr = mg.p + mrow * g.ncols;
+    }
+    auto load = [&](uint32_t idx) {
+        float4 v = xr[idx];
+        if constexpr (OP == RowOp::SoftMaxExt) {
+            v = mul4(v, scale);                         // OpScale
+            if (mr) v = add4(v, mask4(mr + 4 * idx));   // OpAdd(f16 mask -> f32)
+        }
+        return v;
+    };
+
+    if constexpr (NV > 0) {
+        float4 v[NV];
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const uint32_t idx = lane + j * kWave;
+            v[j] = idx < nv ? load(idx) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        if constexpr (OP == RowOp::RmsNorm || OP == RowOp::RmsNormMul) {
+            double acc = 0.0;
+#pragma unroll
+            for (int j = 0; j < NV; ++j)
+                if (lane + j * kWave < nv) acc += sumsq4(v[j]);
+            acc = wave_sum(acc);
+            const float mean = static_cast<float>(acc / static_cast<double>(g.ncols));
+            const float k = 1.0f / __builtin_sqrtf(mean + eps);
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                const uint32_t idx = lane + j * kWave;
+                if (idx < nv) {
+                    float4 r = mul4(v[j], k);
+                    if constexpr (OP == RowOp::RmsNormMul) r = mul4(r, reinterpret_cast<const float4 *>(w)[idx]);
+                    yr[idx] = r;
+                }
+            }
+        } else if constexpr (OP == RowOp::Norm) {
+            double acc = 0.0;
+#pragma unroll
+            for (int j = 0; j < NV; ++j)
+                if (lane + j * kWave < nv) acc += sum4(v[j]);
+            acc = wave_sum(acc);
+            const float mean = static_cast<float>(acc / static_cast<double>(g.ncols));
+            double var = 0.0;
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                if (lane + j * kWave < nv) {
+                    const float4 c = sub4(v[j], mean);
+                    var += (static_cast<double>(c.x) * c.x + static_cast<double>(c.y) * c.y) +
+                           (static_cast<double>(c.z) * c.z + static_cast<double>(c.w) * c.w);
+                }
+            }
+            var = wave_sum(var);
+            const float variance = static_cast<float>(var / static_cast<double>(g.ncols));
+            const float k = 1.0f / __builtin_sqrtf(variance + eps);
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                const uint32_t idx = lane + j * kWave;
+                if (idx < nv) yr[idx] = mul4(sub4(v[j], mean), k);
+            }
+        } else { // soft_max, f64 row sum
+            float mx = -__builtin_inff();
+#pragma unroll
+            for (int j = 0; j < NV; ++j)
+                if (lane + j * kWave < nv) mx = __builtin_fmaxf(mx, max4(v[j]));
+            mx = wave_max(mx);
+            double acc = 0.0;
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                if (lane + j * kWave < nv) {
+                    v[j] = exp4(sub4(v[j], mx), tab);
+                    acc += sum4(v[j]);
+                }
+            }
+            acc = wave_sum(acc);
+            const float den = static_cast<float>(acc);
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                const uint32_t idx = lane + j * kWave;
+                if (idx < nv) yr[idx] = div4(v[j], den);
+            }
+        }
+    } else {
+        // streamed passes for wide rows
+        if constexpr (OP == RowOp::RmsNorm || OP == RowOp::RmsNormMul) {
+            double acc = 0.0;
+            for (uint32_t idx = lane; idx < nv; idx += kWave) acc += sumsq4(xr[idx]);
+            acc = wave_sum(acc);
+            const float mean = static_cast<float>(acc / static_cast<double>(g.ncols));
+            const float k = 1.0f / __builtin_sqrtf(mean + eps);
+            for (uint32_t idx = lane; idx < nv; idx += kWave) {
+                float4 r = mul4(xr[idx], k);
+                if constexpr (OP == RowOp::RmsNormMul) r = mul4(r, reinterpret_cast<const float4 *>(w)[idx]);
+                yr[idx] = r;
+            }
+        } else if constexpr (OP == RowOp::Norm) {
+            double acc = 0.0;
+            for (uint32_t idx = lane; idx < nv; idx += kWave) acc += sum4(xr[idx]);
+            acc = wave_sum(acc);
+            const float mean = static_cast<float>(acc / static_cast<double>(g.ncols));
+            double var = 0.0;
+            for (uint32_t idx = lane; idx < nv; idx += kWave) {
+                const float4 c = sub4(xr[idx], mean);
+                var += (static_cast<double>(c.x) * c.x + static_cast<double>(c.y) * c.y) +
+                       (static_cast<double>(c.z) * c.z + static_cast<double>(c.w) * c.w);
+            }
+            var = wave_sum(var);
+            const float variance = static_cast<float>(var / static_cast<double>(g.ncols));
+            const float k = 1.0f / __builtin_sqrtf(variance + eps);
+            for (uint32_t idx = lane; idx < nv; idx += kWave) yr[idx] = mul4(sub4(xr[idx], mean), k);
+        } else {
+            float mx = -__builtin_inff();
+            for (uint32_t idx = lane; idx < nv; idx += kWave) mx = __builtin_fmaxf(mx, max4(load(idx)));
+            mx = wave_max(mx);
+            double acc = 0.0;
+            for (uint32_t idx = lane; idx < nv; idx += kWave) {
+                const float4 e = exp4(sub4(load(idx), mx), tab);
+                yr[idx] = e;
+                acc += sum4(e);
+            }
+            acc = wave_sum(acc);
+            const float den = static_cast<float>(acc);
+            for (uint32_t idx = lane; idx < nv; idx += kWave) yr[idx] = div4(yr[idx], den);
+        }
+    }
+}
+
+// ---- general rows: any strides, per-element ordinal addressing ----------
+
+struct OrdView {
+    uint64_t ne[4];
+    int64_t st[4];
+};
+
+__device__ __forceinline__ int64_t ord_index(const OrdView &v, uint64_t k)
+{
+    int64_t off = 0;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        off += static_cast<int64_t>(k % v.ne[d]) * v.st[d];
+        k /= v.ne[d];
+    }
+    return off;
+}
+
+// One wave per row; element k of row r is ordinal r*ncols + k of each view.
+template <RowOp OP>
+__global__ __launch_bounds__(kBlock) void k_row_generic(OrdView xv, OrdView yv, uint64_t rows, uint64_t ncols,
+                                                         const float *x, float *y, const float *w, int64_t w_st0,
+                                                         float eps)
+{
+    const uint32_t wave = threadIdx.x / kWave;
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint64_t r = static_cast<uint64_t>(blockIdx.x) * (kBlock / kWave) + wave;
+    if (r >= rows) return;
+    const uint64_t base = r * ncols;
+    if constexpr (OP == RowOp::RmsNorm || OP == RowOp::RmsNormMul) {
+        double acc = 0.0;
+        for (uint64_t c = lane; c < ncols; c += kWave) {
+            const float v = x[ord_index(xv, base + c)];
+            const float sq = v * v;
+            acc += static_cast<double>(sq);
+        }
+        acc = wave_sum(acc);
+        const float mean = static_cast<float>(acc / static_cast<double>(ncols));
+        const float k = 1.0f / __builtin_sqrtf(mean + eps);
+        for (uint64_t c = lane; c < ncols; c += kWave) {
+            float out = x[ord_index(xv, base + c)] * k;
+            if constexpr (OP == RowOp::RmsNormMul) out = out * w[static_cast<int64_t>(c) * w_st0];
+            y[ord_index(yv, base + c)] = out;
+        }
+    } else if constexpr (OP == RowOp::Norm) {
+        double acc = 0.0;
+        for (uint64_t c = lane; c < ncols; c += kWave) acc += static_cast<double>(x[ord_index(xv, base + c)]);
+        acc = wave_sum(acc);
+        const float mean = static_cast<float>(acc / static_cast<double>(ncols));
+        double var = 0.0;
+        for (uint64_t c = lane; c < ncols; c += kWave) {
+            const float cv = x[ord_index(xv, base + c)] - mean;
+            var += static_cast<double>(cv) * static_cast<double>(cv);
+        }
+        var = wave_sum(var);
+        const float variance = static_cast<float>(var / static_cast<double>(ncols));
+        const float k = 1.0f / __builtin_sqrtf(variance + eps);
+        for (uint64_t c = lane; c < ncols; c += kWave)
+            y[ord_index(yv, base + c)] = (x[ord_index(xv, base + c)] - mean) * k;
+    }
+}
+
+// Dense-sum soft_max over general layouts (wave per row, f64 sum).  With
+// kExt the element is first scaled and the f16 mask added (the soft_max_ext
+// composition); kExt requires x and y to share extents.
+template <bool kExt>
+__global__ __launch_bounds__(kBlock) void k_softmax_generic(OrdView xv, OrdView yv, uint64_t rows, uint64_t ncols,
+                                                             const float *x, float *y, MaskGeo mg, float scale)
+{
+    __shared__ uint64_t lds[32];
+    if (threadIdx.x < 32) lds[threadIdx.x] = kExp2Table[threadIdx.x];
+    __syncthreads();
+    const uint32_t wave = threadIdx.x / kWave;
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint64_t r = static_cast<uint64_t>(blockIdx.x) * (kBlock / kWave) + wave;
+    if (r >= rows) return;
+    const uint64_t base = r * ncols;
+    const uint16_t *mr = nullptr;
+    if (kExt && mg.p) {
+        const uint64_t i1 = r % xv.ne[1];
+        const uint64_t i2 = (r / xv.ne[1]) % xv.ne[2];
+        const uint64_t i3 = r / (xv.ne[1] * xv.ne[2]);
+        mr = mg.p + ((i3 % mg.m3) * mg.m2 + (i2 % mg.m2)) * static_cast<uint64_t>(mg.ne1) * ncols + i1 * ncols;
+    }
+    auto load = [&](uint64_t c) {
+        float v = x[ord_index(xv, base + c)];
+        if constexpr (kExt) {
+            v = v * scale;
+            if (mr) v = v + emel_fp16_to_f32(mr[c]);
+        }
+        return v;
+    };
+    float mx = -__builtin_inff();
+    for (uint64_t c = lane; c < ncols; c += kWave) mx = __builtin_fmaxf(mx, load(c));
+    mx = wave_max(mx);
+    double acc = 0.0;
+    for (uint64_t c = lane; c < ncols; c += kWave) {
+        const float e = emel_expf(load(c) - mx, lds);
+        y[ord_index(yv, base + c)] = e;
+        acc += static_cast<double>(e);
+    }
+    acc = wave_sum(acc);
+    const float den = static_cast<float>(acc);
+    for (uint64_t c = lane; c < ncols; c += kWave) {
+        const int64_t o = ord_index(yv, base + c);
+        y[o] = y[o] / den;
+    }
+}
+
+// Strided soft_max (reductions.rs:603-638): the f32 sum is sequential, so
+// each lane owns a row and adds its exponentials in column order.
+__global__ __launch_bounds__(kBlock) void k_softmax_seq(OrdView xv, OrdView yv, uint64_t rows, uint64_t ncols,
+                                                         const float *x, float *y)
+{
+    __shared__ uint64_t lds[32];
+    if (threadIdx.x < 32) lds[threadIdx.x] = kExp2Table[threadIdx.x];
+    __syncthreads();
+    const uint64_t r = static_cast<uint64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (r >= rows) return;
+    const uint64_t base = r * ncols;
+    float mx = x[ord_index(xv, base)];
+    for (uint64_t c = 1; c < ncols; ++c) {
+        const float v = x[ord_index(xv, base + c)];
+        if (v > mx) mx = v;
+    }
+    float sum = 0.0f;
+    for (uint64_t c = 0; c < ncols; ++c) {
+        const float e = emel_expf(x[ord_index(xv, base + c)] - mx, lds);
+        y[ord_index(yv, base + c)] = e;
+        sum += e;
+    }
+    for (uint64_t c = 0; c < ncols; ++c) {
+        const int64_t o = ord_index(yv, base + c);
+        y[o] = y[o] / sum;
+    }
+}
+
+// ---- host-side selection ---------------------------------------------------
+
+bool contiguous(const Operand &p)
+{
+    int64_t expect = 1;
+    for (int d = 0; d < 4; ++d) {
+        if (p.ne[d] != 1 && p.st[d] != expect) return false;
+        expect *= static_cast<int64_t>(p.ne[d]);
+    }
+    return true;
+}
+
+bool same_ne(const Operand &a, const Operand &b)
+{
+    for (int d = 0; d < 4; ++d)
+        if (a.ne[d] != b.ne[d]) return false;
+    return true;
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+OrdView ord_view(const Operand &p)
+{
+    OrdView v;
+    for (int d = 0; d < 4; ++d) {
+        v.ne[d] = p.ne[d];
+        v.st[d] = p.st[d];
+    }
+    return v;
+}
+
+template <RowOp OP, int NV>
+void launch_vec(const RowGeo &g, const RowArgs &a, const MaskGeo &mg, hipStream_t s)
+{
+    const uint32_t rows_per_block = kBlock / kWave;
+    uint32_t blocks = (g.rows + rows_per_block - 1) / rows_per_block;
+    if (OP == RowOp::SoftMaxExt && mg.head_major) blocks = (blocks + 7u) & ~7u; // XCD-major remap needs % 8
+    k_row_vec<OP, NV><<<dim3(blocks), kBlock, 0, s>>>(g, static_cast<const float *>(a.x.data),
+                                                       static_cast<float *>(a.y.data), a.w, mg, a.eps, a.scale);
+}
+
+template <RowOp OP>
+void launch_vec_nv(const RowGeo &g, const RowArgs &a, const MaskGeo &mg, hipStream_t s)
+{
+    const uint32_t nv = g.ncols / 4;
+    if (nv <= 1 * kWave) launch_vec<OP, 1>(g, a, mg, s);
+    else if (nv <= 2 * kWave) launch_vec<OP, 2>(g, a, mg, s);
+    else if (nv <= 4 * kWave) launch_vec<OP, 4>(g, a, mg, s);
+    else if (nv <= 8 * kWave) launch_vec<OP, 8>(g, a, mg, s);
+    else if (nv <= 16 * kWave) launch_vec<OP, 16>(g, a, mg, s);
+    else launch_vec<OP, 0>(g, a, mg, s);
+}
+
+} // namespace
+
+hipError_t launch_rows(const RowArgs &a, hipStream_t s)
+{
+    const bool soft = a.op == RowOp::SoftMax || a.op == RowOp::SoftMaxExt;
+    const uint64_t ncols = a.x.ne[0];
+    uint64_t count = 1;
+    for (int d = 0; d < 4; ++d) count *= a.x.ne[d];
+    if (count == 0 || ncols == 0) return hipSuccess;
+    const uint64_t rows = count / ncols;
+
+    // The strided soft_max keeps the reference's sequential f32 sum.
+    if (a.op == RowOp::SoftMax && !a.dense_sum) {
+        const uint64_t blocks = (rows + kBlock - 1) / kBlock;
+        k_softmax_seq<<<dim3(static_cast<uint32_t>(blocks)), kBlock, 0, s>>>(
+            ord_view(a.x), ord_view(a.y), rows, ncols, static_cast<const float *>(a.x.data),
+            static_cast<float *>(a.y.data));
+        return hipGetLastError();
+    }
+
+    // Vectorized rows: contiguous dim 0, 16-byte aligned row starts, and the
+    // destination row r holding the same columns as the source row r.
+    auto strides4 = [](const Operand &p) {
+        for (int d = 1; d < 4; ++d)
+            if (p.ne[d] != 1 && p.st[d] % 4 != 0) return false;
+        return true;
+    };
+    const bool rows_match = same_ne(a.x, a.y) || (contiguous(a.x) && contiguous(a.y));
+    const bool w_ok = a.op != RowOp::RmsNormMul || (a.w_st0 == 1 && aligned16(a.w));
+    const bool mask_ok = a.op != RowOp::SoftMaxExt || a.mask == nullptr || (reinterpret_cast<uintptr_t>(a.mask) & 7u) == 0;
+    const bool vec = ncols % 4 == 0 && a.x.st[0] == 1 && a.y.st[0] == 1 && strides4(a.x) && strides4(a.y) &&
+                     aligned16(a.x.data) && aligned16(a.y.data) && rows_match && w_ok && mask_ok &&
+                     rows < 0xffffffffull && ncols < 0xffffffffull;
+    if (vec) {
+        // When x and y differ in shape but are both dense, row r of each is
+        // the same linear range: describe both with x's extents.
+        RowGeo g{};
+        g.rows = static_cast<uint32_t>(rows);
+        g.ncols = static_cast<uint32_t>(ncols);
+        g.ne1 = FastDiv(static_cast<uint32_t>(a.x.ne[1]));
+        g.ne2 = FastDiv(static_cast<uint32_t>(a.x.ne[2]));
+        const bool linear = !same_ne(a.x, a.y);
+        for (int d = 0; d < 4; ++d) {
+            g.x_st[d] = a.x.st[d];
+            g.y_st[d] = linear ? a.x.st[d] : a.y.st[d];
+        }
+        if (linear) { // both dense: use x's row-major strides for y
+            int64_t e = 1;
+            for (int d = 0; d < 4; ++d) {
+                g.x_st[d] = e;
+                g.y_st[d] = e;
+                e *= static_cast<int64_t>(a.x.ne[d]);
+            }
+        }
+        MaskGeo mg{};
+        if (a.op == RowOp::SoftMaxExt) {
+            mg.p = a.mask;
+            mg.ne1 = static_cast<uint32_t>(a.x.ne[1]);
+            mg.m2 = static_cast<uint32_t>(a.mask_ne2 ? a.mask_ne2 : 1);
+            mg.m3 = static_cast<uint32_t>(a.mask_ne3 ? a.mask_ne3 : 1);
+            mg.head_major = (a.mask != nullptr && mg.m2 == 1 && a.x.ne[2] > 1) ? 1u : 0u;
+        }
+        switch (a.op) {
+        case RowOp::RmsNorm: launch_vec_nv<RowOp::RmsNorm>(g, a, mg, s); break;
+        case RowOp::RmsNormMul: launch_vec_nv<RowOp::RmsNormMul>(g, a, mg, s); break;
+        case RowOp::Norm: launch_vec_nv<RowOp::Norm>(g, a, mg, s); break;
+        case RowOp::SoftMax: launch_vec_nv<RowOp::SoftMax>(g, a, mg, s); break;
+        case RowOp::SoftMaxExt: launch_vec_nv<RowOp::SoftMaxExt>(g, a, mg, s); break;
+        }
+        return hipGetLastError();
+    }
+
+    const uint64_t blocks = (rows + (kBlock / kWave) - 1) / (kBlock / kWave);
+    if (blocks > 0x7fffffffull) return hipErrorInvalidConfiguration;
+    const dim3 grid(static_cast<uint32_t>(blocks));
+    const float *x = static_cast<const float *>(a.x.data);
+    float *y = static_cast<float *>(a.y.data);
+    if (soft) {
+        MaskGeo mg{};
+        if (a.op == RowOp::SoftMaxExt) {
+            mg.p = a.mask;
+            mg.ne1 = static_cast<uint32_t>(a.x.ne[1]);
+            mg.m2 = static_cast<uint32_t>(a.mask_ne2 ? a.mask_ne2 : 1);
+            mg.m3 = static_cast<uint32_t>(a.mask_ne3 ? a.mask_ne3 : 1);
+            k_softmax_generic<true><<<grid, kBlock, 0, s>>>(ord_view(a.x), ord_view(a.y), rows, ncols, x, y, mg,
+                                                             a.scale);
+        } else {
+            k_softmax_generic<false><<<grid, kBlock, 0, s>>>(ord_view(a.x), ord_view(a.y), rows, ncols, x, y, mg,
+                                                              1.0f);
+        }
+    } else if (a.op == RowOp::RmsNorm) {
+        k_row_generic<RowOp::RmsNorm><<<grid, kBlock, 0, s>>>(ord_view(a.x), ord_view(a.y), rows, ncols, x, y, a.w,
+                                                               a.w_st0, a.eps);
+    } else if (a.op == RowOp::RmsNormMul) {
+        k_row_generic<RowOp::RmsNormMul><<<grid, kBlock, 0, s>>>(ord_view(a.x), ord_view(a.y), rows, ncols, x, y,
+                                                                  a.w, a.w_st0, a.eps);
+    } else {
+        k_row_generic<RowOp::Norm><<<grid, kBlock, 0, s>>>(ord_view(a.x), ord_view(a.y), rows, ncols, x, y, a.w,
+                                                            a.w_st0, a.eps);
+    }
+    return hipGetLastError();
+}
+
+} // namespace emel

@@ -1,0 +1,39 @@
+"""emel_hip: MI355X (gfx950) implementation of emel.rs's tensor-library hot
+path -- elementwise, broadcast and row-reduction ops -- behind the C ABI in
+include/emel_hip.h, with a Python mirror of emel-kernels' operator API.
+"""
+from .abi import BinaryOp, DType, Status, UnarySubOp, device_count, last_error, load
+from .kernel import (
+    Kernel,
+    OpAdd,
+    OpAddBroadcastRow,
+    OpArgmax,
+    OpArgmaxRows,
+    OpBinaryBroadcast,
+    OpDiv,
+    OpGelu,
+    OpMean,
+    OpMul,
+    OpMulBroadcastRow,
+    OpNorm,
+    OpRmsNorm,
+    OpRmsNormMul,
+    OpScale,
+    OpSilu,
+    OpSoftMax,
+    OpSoftMaxExt,
+    OpSub,
+    OpSum,
+    OpSumRows,
+    OpSwiglu,
+    OpUnary,
+)
+from .views import Layout, TensorView, TensorViewMut
+
+__all__ = [
+    "BinaryOp", "DType", "Status", "UnarySubOp", "device_count", "last_error", "load",
+    "Kernel", "Layout", "TensorView", "TensorViewMut",
+    "OpAdd", "OpSub", "OpMul", "OpDiv", "OpAddBroadcastRow", "OpMulBroadcastRow", "OpBinaryBroadcast",
+    "OpUnary", "OpSilu", "OpGelu", "OpSwiglu", "OpScale", "OpRmsNorm", "OpRmsNormMul", "OpNorm",
+    "OpSoftMax", "OpSoftMaxExt", "OpSumRows", "OpSum", "OpMean", "OpArgmax", "OpArgmaxRows",
+]

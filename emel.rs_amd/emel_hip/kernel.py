@@ -1,0 +1,301 @@
+"""Operator events and the Kernel actor, mirroring emel-kernels' portable router.
+
+    kernel = Kernel()
+    status = kernel.process_event(OpAdd(TensorView(a, lay), TensorView(b, lay),
+                                        TensorViewMut(out, lay)))
+    assert status == Status.OK
+
+Each event class carries the constructor arguments of the reference event of
+the same name (cited per class) and maps onto one C-ABI entry point.
+`Kernel.process_event` dispatches on the kernel's HIP stream and, like the
+reference's run-to-completion actors (actor.rs:936-943), waits for the work
+to finish unless the kernel was created with `synchronous=False`.  Rejected
+requests return the error status without touching dst.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+from .abi import BinaryOp, Status, UnarySubOp, load
+from .views import TensorView, TensorViewMut
+
+
+def _p(view):
+    return None if view is None else ctypes.byref(view.c())
+
+
+@dataclass
+class OpAdd:
+    """binary::OpAdd::new(lhs, rhs, output) (binary.rs:47-81)."""
+
+    lhs: TensorView
+    rhs: TensorView
+    output: TensorViewMut
+
+    def _call(self, lib, s):
+        return lib.emel_op_add(_p(self.lhs), _p(self.rhs), _p(self.output), s)
+
+
+@dataclass
+class OpSub:
+    """binary::OpSub::new(lhs, rhs, output) (binary.rs:47-81)."""
+
+    lhs: TensorView
+    rhs: TensorView
+    output: TensorViewMut
+
+    def _call(self, lib, s):
+        return lib.emel_op_sub(_p(self.lhs), _p(self.rhs), _p(self.output), s)
+
+
+@dataclass
+class OpMul:
+    """binary::OpMul::new(lhs, rhs, output) (binary.rs:47-81)."""
+
+    lhs: TensorView
+    rhs: TensorView
+    output: TensorViewMut
+
+    def _call(self, lib, s):
+        return lib.emel_op_mul(_p(self.lhs), _p(self.rhs), _p(self.output), s)
+
+
+@dataclass
+class OpDiv:
+    """binary::OpDiv::new(lhs, rhs, output) (binary.rs:47-81)."""
+
+    lhs: TensorView
+    rhs: TensorView
+    output: TensorViewMut
+
+    def _call(self, lib, s):
+        return lib.emel_op_div(_p(self.lhs), _p(self.rhs), _p(self.output), s)
+
+
+@dataclass
+class OpAddBroadcastRow:
+    """broadcast::OpAddBroadcastRow::new(src0, src1, dst) (broadcast.rs:53-66)."""
+
+    src0: TensorView
+    src1: TensorView
+    dst: TensorViewMut
+
+    def _call(self, lib, s):
+        return lib.emel_op_add_broadcast_row(_p(self.src0), _p(self.src1), _p(self.dst), s)
+
+
+@dataclass
+class OpMulBroadcastRow:
+    """broadcast::OpMulBroadcastRow::new(src0, src1, dst) (broadcast.rs:68-84)."""
+
+    src0: TensorView
+    src1: TensorView
+    dst: TensorViewMut
+
+    def _call(self, lib, s):
+        return lib.emel_op_mul_broadcast_row(_p(self.src0), _p(self.src1), _p(self.dst), s)
+
+
+@dataclass
+class OpBinaryBroadcast:
+    """OpRepeat(src1 -> dst.ne) then the equal-count binary op (generic.rs:1641-1665)."""
+
+    op: BinaryOp
+    src0: TensorView
+    src1: TensorView
+    dst: TensorViewMut
+
+    def _call(self, lib, s):
+        return lib.emel_op_binary_broadcast(int(self.op), _p(self.src0), _p(self.src1), _p(self.dst), s)
+
+
+@dataclass
+class OpUnary:
+    """unary::OpUnary::new(subop, input, output) (unary.rs:150-172)."""
+
+    subop: UnarySubOp
+    input: TensorView
+    output: TensorViewMut
+
+    def _call(self, lib, s):
+        return lib.emel_op_unary(int(self.subop), _p(self.input), _p(self.output), s)
+
+
+@dataclass
+class OpSilu:
+    """unary::OpSilu::new(input, output) (unary.rs:82)."""
+
+    input: TensorView
+    output: TensorViewMut
+
+    def _call(self, lib, s):
+        return lib.emel_op_silu(_p(self.input), _p(self.output), s)
+
+
+@dataclass
+class OpGelu:
+    """unary::OpGelu::new(input, output) (unary.rs:80)."""
+
+    input: TensorView
+    output: TensorViewMut
+
+    def _call(self, lib, s):
+        return lib.emel_op_gelu(_p(self.input), _p(self.output), s)
+
+
+@dataclass
+class OpSwiglu:
+    """OpSilu(gate) then OpMul by up, fused (unary.rs:595-600, binary.rs:411-424)."""
+
+    gate: TensorView
+    up: TensorView
+    output: TensorViewMut
+
+    def _call(self, lib, s):
+        return lib.emel_op_swiglu(_p(self.gate), _p(self.up), _p(self.output), s)
+
+
+@dataclass
+class OpScale:
+    """activation::OpScale::new(input, output, scale) (activation.rs:58-72)."""
+
+    input: TensorView
+    output: TensorViewMut
+    scale: float
+
+    def _call(self, lib, s):
+        return lib.emel_op_scale(_p(self.input), _p(self.output), float(self.scale), s)
+
+
+@dataclass
+class OpRmsNorm:
+    """normalization::OpRmsNorm::new(input, output, epsilon) (normalization.rs:80-96)."""
+
+    input: TensorView
+    output: TensorViewMut
+    epsilon: float
+
+    def _call(self, lib, s):
+        return lib.emel_op_rms_norm(_p(self.input), _p(self.output), float(self.epsilon), s)
+
+
+@dataclass
+class OpRmsNormMul:
+    """OpRmsNorm then OpMulBroadcastRow by a weight row, fused."""
+
+    input: TensorView
+    weight: TensorView
+    output: TensorViewMut
+    epsilon: float
+
+    def _call(self, lib, s):
+        return lib.emel_op_rms_norm_mul(_p(self.input), _p(self.weight), _p(self.output), float(self.epsilon), s)
+
+
+@dataclass
+class OpNorm:
+    """normalization::OpNorm::new(input, output, epsilon) (normalization.rs:58-74)."""
+
+    input: TensorView
+    output: TensorViewMut
+    epsilon: float
+
+    def _call(self, lib, s):
+        return lib.emel_op_norm(_p(self.input), _p(self.output), float(self.epsilon), s)
+
+
+@dataclass
+class OpSoftMax:
+    """reductions::OpSoftMax::new(src, dst) (reductions.rs:152-163)."""
+
+    src: TensorView
+    dst: TensorViewMut
+
+    def _call(self, lib, s):
+        return lib.emel_op_soft_max(_p(self.src), _p(self.dst), s)
+
+
+@dataclass
+class OpSoftMaxExt:
+    """OpScale -> OpAdd(f16 mask) -> OpSoftMax per (ne2, ne3) slice, fused."""
+
+    src: TensorView
+    mask: TensorView | None
+    scale: float
+    dst: TensorViewMut
+
+    def _call(self, lib, s):
+        return lib.emel_op_soft_max_ext(_p(self.src), _p(self.mask), float(self.scale), _p(self.dst), s)
+
+
+@dataclass
+class OpSumRows:
+    """reductions::OpSumRows::new(src, dst) (reductions.rs:107-118)."""
+
+    src: TensorView
+    dst: TensorViewMut
+
+    def _call(self, lib, s):
+        return lib.emel_op_sum_rows(_p(self.src), _p(self.dst), s)
+
+
+@dataclass
+class OpSum:
+    """reductions::OpSum::new(src, dst) (reductions.rs:88-103)."""
+
+    src: TensorView
+    dst: TensorViewMut
+
+    def _call(self, lib, s):
+        return lib.emel_op_sum(_p(self.src), _p(self.dst), s)
+
+
+@dataclass
+class OpMean:
+    """reductions::OpMean::new(src, dst) (reductions.rs:120-133)."""
+
+    src: TensorView
+    dst: TensorViewMut
+
+    def _call(self, lib, s):
+        return lib.emel_op_mean(_p(self.src), _p(self.dst), s)
+
+
+@dataclass
+class OpArgmax:
+    """reductions::OpArgmax::new(src, dst) (reductions.rs:137-148)."""
+
+    src: TensorView
+    dst: TensorViewMut
+
+    def _call(self, lib, s):
+        return lib.emel_op_argmax(_p(self.src), _p(self.dst), s)
+
+
+@dataclass
+class OpArgmaxRows:
+    """One OpArgmax per row view, i32 indices."""
+
+    src: TensorView
+    dst: TensorViewMut
+
+    def _call(self, lib, s):
+        return lib.emel_op_argmax_rows(_p(self.src), _p(self.dst), s)
+
+
+class Kernel:
+    """Single-writer actor over one HIP stream (Kernel, actor.rs:905-949)."""
+
+    def __init__(self, stream: int | None = None, synchronous: bool = True):
+        self._lib = load()
+        self.stream = stream  # hipStream_t as an int, or None for the null stream
+        self.synchronous = synchronous
+
+    def process_event(self, event) -> Status:
+        status = Status(event._call(self._lib, self.stream))
+        if status == Status.OK and self.synchronous:
+            sync = Status(self._lib.emel_stream_synchronize(self.stream))
+            if sync != Status.OK:
+                return sync
+        return status

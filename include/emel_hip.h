@@ -1,0 +1,232 @@
+/*
+ * emel_hip.h -- C ABI of the MI355X (gfx950) implementation of emel.rs's
+ * tensor-library hot path: elementwise, broadcast and row-reduction ops.
+ *
+ * This is the drop-in boundary.  Each entry point replaces one operator
+ * event of emel-kernels' portable router (stateforward/emel.rs,
+ * crates/emel-kernels/src/any/, cited below as file:line) and keeps its
+ * argument meaning, validation order and error classification.  A Rust FFI
+ * crate binds these functions one-to-one (the binding is shown in
+ * INTEGRATION.md at the repository root).
+ *
+ * Conventions
+ *   - Views mirror the pinned C++ tensor_view {data, type, ne[4], nb[4]}
+ *     (tools/emel-kernel-binary-reference/main.cpp:14-30) plus data_bytes,
+ *     the byte length of the caller's allocation at data (the Rust slice
+ *     length that Layout::validate checks spans against,
+ *     tensor_view.rs:397-447).  data is a device pointer for every op.
+ *   - nb[0] == 0 selects the implicit row-major layout, as in
+ *     Layout::effective_f32_strides (tensor_view.rs:262-277).
+ *   - Every op runs the reference's guards on the host before anything is
+ *     enqueued.  A rejected request enqueues nothing and never writes dst.
+ *   - Ops are asynchronous on `stream` (a hipStream_t; NULL is the null
+ *     stream).  emel_stream_synchronize gives the reference's synchronous
+ *     run-to-completion semantics.
+ *   - dst may be the same view as a source (in place).  Any other overlap
+ *     between dst and a source is rejected as EMEL_ERR_INVALID_VIEW.
+ *   - There is no CPU fallback: without a usable gfx950 device an accepted
+ *     request returns EMEL_ERR_KERNEL_UNAVAILABLE.
+ */
+#ifndef EMEL_HIP_H
+#define EMEL_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EMEL_HIP_ABI_VERSION 1u
+
+/* Status codes.  One code per variant of the reference's typed errors:
+ * BinaryError / BroadcastError / UnaryError / ReductionError /
+ * ActivationError {InvalidView, ShapeMismatch, UnexpectedEvent, Internal}
+ * (binary.rs:20-29, broadcast.rs:28-38, unary.rs:22-31,
+ * reductions.rs:21-30), NormalizationError adds InvalidParameters
+ * (normalization.rs:31-42), root Error adds KernelUnavailable
+ * (actor.rs:88-101). */
+typedef enum emel_status {
+    EMEL_OK = 0,
+    EMEL_ERR_INVALID_VIEW = 1,
+    EMEL_ERR_SHAPE_MISMATCH = 2,
+    EMEL_ERR_INVALID_PARAMETERS = 3,
+    EMEL_ERR_UNEXPECTED_EVENT = 4,
+    EMEL_ERR_INTERNAL = 5,
+    EMEL_ERR_KERNEL_UNAVAILABLE = 6, /* no usable gfx950 device */
+    EMEL_ERR_DEVICE = 7,             /* a HIP runtime call failed */
+    EMEL_ERR_INVALID_ARGUMENT = 8    /* a required pointer argument is NULL */
+} emel_status;
+
+/* Wire dtype codes, DType::from_code (tensor_view.rs:111-158). */
+typedef enum emel_dtype {
+    EMEL_DTYPE_F32 = 0,
+    EMEL_DTYPE_F16 = 1,
+    EMEL_DTYPE_I32 = 26
+} emel_dtype;
+
+/* Unary wire subop codes, UnarySubOp (unary.rs:101-146). */
+typedef enum emel_unary_subop {
+    EMEL_UNARY_ABS = 0,
+    EMEL_UNARY_NEG = 2,
+    EMEL_UNARY_TANH = 4,
+    EMEL_UNARY_ELU = 5,
+    EMEL_UNARY_RELU = 6,
+    EMEL_UNARY_SIGMOID = 7,
+    EMEL_UNARY_GELU = 8,
+    EMEL_UNARY_SILU = 10,
+    EMEL_UNARY_EXP = 13
+} emel_unary_subop;
+
+typedef enum emel_binary_op {
+    EMEL_BINARY_ADD = 0,
+    EMEL_BINARY_SUB = 1,
+    EMEL_BINARY_MUL = 2,
+    EMEL_BINARY_DIV = 3
+} emel_binary_op;
+
+typedef struct emel_tensor_view {
+    const void *data;
+    uint64_t data_bytes;
+    uint32_t dtype;
+    uint32_t reserved; /* must be 0 */
+    uint64_t ne[4];
+    uint64_t nb[4];
+} emel_tensor_view;
+
+typedef struct emel_tensor_view_mut {
+    void *data;
+    uint64_t data_bytes;
+    uint32_t dtype;
+    uint32_t reserved; /* must be 0 */
+    uint64_t ne[4];
+    uint64_t nb[4];
+} emel_tensor_view_mut;
+
+typedef void *emel_stream; /* hipStream_t */
+
+/* ---- library / runtime (the FFI crate's device plumbing) ------------- */
+
+uint32_t emel_abi_version(void);
+const char *emel_status_string(emel_status status);
+/* Detail of the last failure on the calling thread ("" if none). */
+const char *emel_last_error(void);
+/* Number of visible gfx950 devices (0 when none). */
+emel_status emel_device_count(int32_t *count);
+emel_status emel_set_device(int32_t device);
+emel_status emel_malloc(void **ptr, uint64_t bytes);
+emel_status emel_free(void *ptr);
+emel_status emel_memcpy_htod(void *dst, const void *src, uint64_t bytes, emel_stream stream);
+emel_status emel_memcpy_dtoh(void *dst, const void *src, uint64_t bytes, emel_stream stream);
+emel_status emel_stream_create(emel_stream *stream);
+emel_status emel_stream_destroy(emel_stream stream);
+emel_status emel_stream_synchronize(emel_stream stream);
+/* Releases the per-stream reduction workspaces the library holds. */
+emel_status emel_release_workspaces(void);
+
+/* ---- view predicates (host only, no device access) -------------------- */
+
+/* Layout::validate / validate_binary (tensor_view.rs:365-447):
+ * allow_singleton_zero_stride != 0 selects the binary-kernel contract. */
+emel_status emel_validate_view(const emel_tensor_view *view, int32_t allow_singleton_zero_stride);
+/* normalization_view_valid (normalization.rs:237-287). */
+emel_status emel_validate_normalization_view(const emel_tensor_view *view);
+
+/* ---- equal-count binary ops --------------------------------------------
+ * binary::{OpAdd,OpSub,OpMul,OpDiv}::new(lhs, rhs, output)
+ * (binary.rs:47-81; guards :320-340; formulas :383-409; loop :411-424):
+ * the three views have equal element counts (shapes may differ) and are
+ * paired by logical ordinal.  Bit-exact IEEE f32. */
+emel_status emel_op_add(const emel_tensor_view *lhs, const emel_tensor_view *rhs,
+                        const emel_tensor_view_mut *out, emel_stream stream);
+emel_status emel_op_sub(const emel_tensor_view *lhs, const emel_tensor_view *rhs,
+                        const emel_tensor_view_mut *out, emel_stream stream);
+emel_status emel_op_mul(const emel_tensor_view *lhs, const emel_tensor_view *rhs,
+                        const emel_tensor_view_mut *out, emel_stream stream);
+emel_status emel_op_div(const emel_tensor_view *lhs, const emel_tensor_view *rhs,
+                        const emel_tensor_view_mut *out, emel_stream stream);
+
+/* ---- row broadcast -------------------------------------------------------
+ * broadcast::{OpAddBroadcastRow,OpMulBroadcastRow}::new(src0, src1, dst)
+ * (broadcast.rs:53-84; shape rule :334-350; loops :352-390):
+ * dst[r,c] = src0[r,c] (+|*) src1[c], src1.ne == [dst.ne0,1,1,1]. */
+emel_status emel_op_add_broadcast_row(const emel_tensor_view *src0, const emel_tensor_view *src1,
+                                      const emel_tensor_view_mut *dst, emel_stream stream);
+emel_status emel_op_mul_broadcast_row(const emel_tensor_view *src0, const emel_tensor_view *src1,
+                                      const emel_tensor_view_mut *dst, emel_stream stream);
+
+/* ---- 4-D modulo broadcast ------------------------------------------------
+ * Replaces the reference composition OpRepeat(src1 -> dst.ne)
+ * (generic.rs:1641-1665, guard :964-983) followed by the equal-count binary
+ * op (binary.rs:411-424): dst[i] = src0[i] op src1[i0%n0,i1%n1,i2%n2,i3%n3]
+ * with src0.ne == dst.ne and each src1.ne[d] dividing dst.ne[d]. */
+emel_status emel_op_binary_broadcast(emel_binary_op op, const emel_tensor_view *src0,
+                                     const emel_tensor_view *src1, const emel_tensor_view_mut *dst,
+                                     emel_stream stream);
+
+/* ---- unary ----------------------------------------------------------------
+ * unary::OpUnary::new(subop, input, output) (unary.rs:150-172, guards
+ * :985-1027): accepts abs, neg, tanh, elu, relu, gelu, silu, exp; any
+ * failed guard reports EMEL_ERR_UNEXPECTED_EVENT, as OpUnary does. */
+emel_status emel_op_unary(emel_unary_subop subop, const emel_tensor_view *in,
+                          const emel_tensor_view_mut *out, emel_stream stream);
+/* unary::OpSilu::new(input, output) (unary.rs:82, formula :595-600):
+ * x / (1 + expf(-x)) with expf bit-identical to glibc's. */
+emel_status emel_op_silu(const emel_tensor_view *in, const emel_tensor_view_mut *out, emel_stream stream);
+/* unary::OpGelu::new(input, output) (unary.rs:80, formula :522-586):
+ * fp16-rounded tanh approximation with tanhf bit-identical to glibc's. */
+emel_status emel_op_gelu(const emel_tensor_view *in, const emel_tensor_view_mut *out, emel_stream stream);
+/* Fused SwiGLU: the reference chain OpSilu(gate) then equal-count OpMul by
+ * up (unary.rs:595-600, binary.rs:411-424) in one pass, keeping both f32
+ * roundings.  The three views have identical shapes. */
+emel_status emel_op_swiglu(const emel_tensor_view *gate, const emel_tensor_view *up,
+                           const emel_tensor_view_mut *out, emel_stream stream);
+
+/* ---- scale ------------------------------------------------------------------
+ * activation::OpScale::new(input, output, scale) (activation.rs:58-72,
+ * guard :352-364, loop :366-377). */
+emel_status emel_op_scale(const emel_tensor_view *in, const emel_tensor_view_mut *out, float scale,
+                          emel_stream stream);
+
+/* ---- row normalization -------------------------------------------------------
+ * normalization::OpRmsNorm::new(input, output, epsilon)
+ * (normalization.rs:80-96; guards :364-386; run_rms_norm :343-362):
+ * per row, s = sum_f64(f32(x*x)), k = 1/sqrtf(f32(s/n) + eps), y = x*k. */
+emel_status emel_op_rms_norm(const emel_tensor_view *in, const emel_tensor_view_mut *out, float epsilon,
+                             emel_stream stream);
+/* Fused rms_norm then OpMulBroadcastRow by weight (broadcast.rs:372-390):
+ * y = (x*k)*w[c], two f32 roundings.  Both ops' guards are checked first. */
+emel_status emel_op_rms_norm_mul(const emel_tensor_view *in, const emel_tensor_view *weight,
+                                 const emel_tensor_view_mut *out, float epsilon, emel_stream stream);
+/* normalization::OpNorm::new(input, output, epsilon) (run_norm :316-341). */
+emel_status emel_op_norm(const emel_tensor_view *in, const emel_tensor_view_mut *out, float epsilon,
+                         emel_stream stream);
+
+/* ---- row reductions ------------------------------------------------------------
+ * reductions::OpSoftMax::new(src, dst) (reductions.rs:152-163; shape
+ * :473-495; dense f64-sum path :565-601; strided f32-sum path :603-638). */
+emel_status emel_op_soft_max(const emel_tensor_view *src, const emel_tensor_view_mut *dst, emel_stream stream);
+/* Scaled + masked soft_max: the reference composition OpScale
+ * (activation.rs:372) -> equal-count OpAdd of the f16 mask decoded by
+ * fp16_to_f32 (quant.rs:287-300) -> dense OpSoftMax, per (ne2,ne3) slice.
+ * mask (may be NULL) is dense f16 [ne0, ne1, m2, m3], m2 | ne2, m3 | ne3. */
+emel_status emel_op_soft_max_ext(const emel_tensor_view *src, const emel_tensor_view *mask, float scale,
+                                 const emel_tensor_view_mut *dst, emel_stream stream);
+/* reductions::OpSumRows::new(src, dst) (reductions.rs:107-118, :460-463,
+ * :684-700): dst.ne == [1, ne1, ne2, ne3], f64 accumulation. */
+emel_status emel_op_sum_rows(const emel_tensor_view *src, const emel_tensor_view_mut *dst, emel_stream stream);
+/* reductions::OpSum / OpMean (reductions.rs:88-133, :670-713): scalar dst. */
+emel_status emel_op_sum(const emel_tensor_view *src, const emel_tensor_view_mut *dst, emel_stream stream);
+emel_status emel_op_mean(const emel_tensor_view *src, const emel_tensor_view_mut *dst, emel_stream stream);
+/* reductions::OpArgmax::new(src, dst) (reductions.rs:137-148, :715-730):
+ * whole tensor -> f32 scalar index of the first maximum. */
+emel_status emel_op_argmax(const emel_tensor_view *src, const emel_tensor_view_mut *dst, emel_stream stream);
+/* Per-row argmax: one OpArgmax per row view ne=[ne0,1,1,1]; dst is I32
+ * with ne == [1, ne1, ne2, ne3] (first maximum; NaN never wins; a NaN in
+ * column 0 yields 0, exactly as the sequential strict-> scan). */
+emel_status emel_op_argmax_rows(const emel_tensor_view *src, const emel_tensor_view_mut *dst,
+                                emel_stream stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,81 @@
+/*
+ * emel_oracle.h -- CPU restatement of the emel.rs portable ("any") kernel
+ * path for the elementwise, broadcast and row-reduction ops.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker the HIP product is
+ * compared against.  Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load it.  The product (libemel_hip.so) never links,
+ * loads or calls it.
+ *
+ * Every function restates the reference algorithm with the same rounding
+ * order (compiled with -ffp-contract=off) and calls glibc expf/tanhf/sqrtf
+ * exactly where Rust std's f32::exp/tanh/sqrt are called.  Reference paths
+ * are relative to stateforward/emel.rs:crates/emel-kernels/src/any/.
+ */
+#ifndef EMEL_ORACLE_H
+#define EMEL_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Same memory layout as emel_tensor_view in include/emel_hip.h. */
+typedef struct orc_view {
+    void *data;          /* host pointer */
+    uint64_t data_bytes; /* bytes owned at data (Rust slice len * 4) */
+    uint32_t dtype;      /* wire dtype code: F32=0, F16=1, I32=26 */
+    uint32_t reserved;
+    uint64_t ne[4];
+    uint64_t nb[4];
+} orc_view;
+
+/* Status codes: identical numbering to emel_status in include/emel_hip.h. */
+enum {
+    ORC_OK = 0,
+    ORC_INVALID_VIEW = 1,
+    ORC_SHAPE_MISMATCH = 2,
+    ORC_INVALID_PARAMETERS = 3,
+    ORC_UNEXPECTED_EVENT = 4,
+};
+
+enum { ORC_ADD = 0, ORC_SUB = 1, ORC_MUL = 2, ORC_DIV = 3 };
+
+/* View validation (tensor_view.rs:365-447, normalization.rs:237-287). */
+int orc_layout_validate(const orc_view *v, int allow_singleton_zero_stride);
+int orc_normalization_view_valid(const orc_view *v);
+
+/* Ops.  Each returns an ORC_* status; dst is untouched on rejection. */
+int orc_op_binary(int op, const orc_view *lhs, const orc_view *rhs, const orc_view *dst);
+int orc_op_broadcast_row(int op, const orc_view *src0, const orc_view *src1, const orc_view *dst);
+int orc_op_unary(int subop, const orc_view *in, const orc_view *out);       /* OpUnary */
+int orc_op_unary_event(int subop, const orc_view *in, const orc_view *out); /* OpSilu/OpGelu/... */
+int orc_op_scale(const orc_view *in, const orc_view *out, float scale);
+int orc_op_rms_norm(const orc_view *in, const orc_view *out, float eps);
+int orc_op_norm(const orc_view *in, const orc_view *out, float eps);
+int orc_op_soft_max(const orc_view *src, const orc_view *dst);
+int orc_op_sum_rows(const orc_view *src, const orc_view *dst);
+int orc_op_sum(const orc_view *src, const orc_view *dst);
+int orc_op_mean(const orc_view *src, const orc_view *dst);
+int orc_op_argmax(const orc_view *src, const orc_view *dst);
+int orc_op_repeat(const orc_view *src, const orc_view *dst);
+
+/* Compositions of reference ops (the configured semantics the reference has
+ * no single op for).  Each is a sequence of the calls above. */
+int orc_soft_max_ext(const orc_view *src, const orc_view *mask, float scale, const orc_view *dst);
+int orc_argmax_rows(const orc_view *src, const orc_view *dst_i32);
+int orc_binary_bcast(int op, const orc_view *src0, const orc_view *src1, const orc_view *dst);
+int orc_rms_norm_mul(const orc_view *in, const orc_view *weight, const orc_view *out, float eps);
+int orc_swiglu(const orc_view *gate, const orc_view *up, const orc_view *out);
+
+/* Scalar helpers (unary.rs:522-600, quant.rs:287-300). */
+float orc_silu(float x);
+float orc_gelu(float x);
+uint16_t orc_fp32_to_fp16(float x);
+float orc_fp16_to_f32(uint16_t h);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

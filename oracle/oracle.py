@@ -1,0 +1,141 @@
+"""ctypes binding of the CPU oracle (oracle/libemel_oracle.so).
+
+TEST INFRASTRUCTURE ONLY: the checker the HIP product is compared against.
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it.
+
+Views are host numpy arrays with the reference's (ne, nb) wire layout;
+`data_bytes` defaults to the array's byte length (the Rust slice length).
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import numpy as np
+
+LIB_PATH = Path(__file__).resolve().parent / "libemel_oracle.so"
+
+OK, INVALID_VIEW, SHAPE_MISMATCH, INVALID_PARAMETERS, UNEXPECTED_EVENT = 0, 1, 2, 3, 4
+ADD, SUB, MUL, DIV = 0, 1, 2, 3
+F32, F16, I32 = 0, 1, 26
+
+
+class OView(ctypes.Structure):
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("data_bytes", ctypes.c_uint64),
+        ("dtype", ctypes.c_uint32),
+        ("reserved", ctypes.c_uint32),
+        ("ne", ctypes.c_uint64 * 4),
+        ("nb", ctypes.c_uint64 * 4),
+    ]
+
+
+def view(arr: np.ndarray, ne, nb=None, dtype: int | None = None, data_bytes: int | None = None) -> OView:
+    """A host view over a C-contiguous numpy array.  nb=None -> row-major of
+    the array's element size; keep `arr` alive while the view is used."""
+    if not arr.flags["C_CONTIGUOUS"]:
+        raise ValueError("oracle views need C-contiguous backing arrays")
+    if dtype is None:
+        dtype = {np.dtype(np.float32): F32, np.dtype(np.float16): F16, np.dtype(np.uint16): F16,
+                 np.dtype(np.int32): I32}[arr.dtype]
+    ne = [int(x) for x in ne]
+    if nb is None:
+        nb = [arr.itemsize]
+        for d in range(1, 4):
+            nb.append(nb[-1] * ne[d - 1])
+    v = OView()
+    v.data = arr.ctypes.data
+    v.data_bytes = arr.nbytes if data_bytes is None else int(data_bytes)
+    v.dtype = dtype
+    v.reserved = 0
+    for d in range(4):
+        v.ne[d] = ne[d]
+        v.nb[d] = int(nb[d])
+    v._arr = arr  # keep alive
+    return v
+
+
+_P = ctypes.POINTER(OView)
+_SIG = {
+    "orc_layout_validate": [_P, ctypes.c_int],
+    "orc_normalization_view_valid": [_P],
+    "orc_op_binary": [ctypes.c_int, _P, _P, _P],
+    "orc_op_broadcast_row": [ctypes.c_int, _P, _P, _P],
+    "orc_op_unary": [ctypes.c_int, _P, _P],
+    "orc_op_unary_event": [ctypes.c_int, _P, _P],
+    "orc_op_scale": [_P, _P, ctypes.c_float],
+    "orc_op_rms_norm": [_P, _P, ctypes.c_float],
+    "orc_op_norm": [_P, _P, ctypes.c_float],
+    "orc_op_soft_max": [_P, _P],
+    "orc_op_sum_rows": [_P, _P],
+    "orc_op_sum": [_P, _P],
+    "orc_op_mean": [_P, _P],
+    "orc_op_argmax": [_P, _P],
+    "orc_op_repeat": [_P, _P],
+    "orc_soft_max_ext": [_P, _P, ctypes.c_float, _P],
+    "orc_argmax_rows": [_P, _P],
+    "orc_binary_bcast": [ctypes.c_int, _P, _P, _P],
+    "orc_rms_norm_mul": [_P, _P, _P, ctypes.c_float],
+    "orc_swiglu": [_P, _P, _P],
+}
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} missing: run `make -C oracle` (or __graft_entry__.build())")
+        L = ctypes.CDLL(str(LIB_PATH))
+        for name, args in _SIG.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = ctypes.c_int
+        for name in ("orc_silu", "orc_gelu"):
+            getattr(L, name).argtypes = [ctypes.c_float]
+            getattr(L, name).restype = ctypes.c_float
+        L.orc_fp32_to_fp16.argtypes = [ctypes.c_float]
+        L.orc_fp32_to_fp16.restype = ctypes.c_uint16
+        L.orc_fp16_to_f32.argtypes = [ctypes.c_uint16]
+        L.orc_fp16_to_f32.restype = ctypes.c_float
+        _lib = L
+    return _lib
+
+
+def _r(v):
+    return None if v is None else ctypes.byref(v)
+
+
+def call(name: str, *args) -> int:
+    """Calls orc_<name> with OView arguments passed by reference."""
+    fn = getattr(lib(), name)
+    conv = [_r(a) if isinstance(a, OView) or a is None else a for a in args]
+    return int(fn(*conv))
+
+
+# convenience wrappers -------------------------------------------------------
+
+def binary(op, lhs, rhs, dst): return call("orc_op_binary", op, lhs, rhs, dst)
+def broadcast_row(op, src0, src1, dst): return call("orc_op_broadcast_row", op, src0, src1, dst)
+def unary(subop, src, dst): return call("orc_op_unary", subop, src, dst)
+def unary_event(subop, src, dst): return call("orc_op_unary_event", subop, src, dst)
+def scale(src, dst, s): return call("orc_op_scale", src, dst, ctypes.c_float(s))
+def rms_norm(src, dst, eps): return call("orc_op_rms_norm", src, dst, ctypes.c_float(eps))
+def norm(src, dst, eps): return call("orc_op_norm", src, dst, ctypes.c_float(eps))
+def soft_max(src, dst): return call("orc_op_soft_max", src, dst)
+def sum_rows(src, dst): return call("orc_op_sum_rows", src, dst)
+def sum_(src, dst): return call("orc_op_sum", src, dst)
+def mean(src, dst): return call("orc_op_mean", src, dst)
+def argmax(src, dst): return call("orc_op_argmax", src, dst)
+def repeat(src, dst): return call("orc_op_repeat", src, dst)
+def soft_max_ext(src, mask, s, dst): return call("orc_soft_max_ext", src, mask, ctypes.c_float(s), dst)
+def argmax_rows(src, dst): return call("orc_argmax_rows", src, dst)
+def binary_bcast(op, src0, src1, dst): return call("orc_binary_bcast", op, src0, src1, dst)
+def rms_norm_mul(src, w, dst, eps): return call("orc_rms_norm_mul", src, w, dst, ctypes.c_float(eps))
+def swiglu(gate, up, dst): return call("orc_swiglu", gate, up, dst)
+def silu_scalar(x: float) -> float: return float(lib().orc_silu(x))
+def gelu_scalar(x: float) -> float: return float(lib().orc_gelu(x))
+def fp32_to_fp16(x: float) -> int: return int(lib().orc_fp32_to_fp16(x))
+def fp16_to_f32(h: int) -> float: return float(lib().orc_fp16_to_f32(h))

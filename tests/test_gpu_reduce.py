@@ -1,0 +1,140 @@
+"""GPU parity: sum_rows, per-row argmax and whole-tensor sum / mean / argmax.
+
+argmax indices are compared exactly (ties and NaNs included); sums within
+BASELINE's 1e-5 relative tolerance (f64 accumulation in a different order),
+with an absolute floor of 1e-12 * sum|x| for rows whose sum nearly cancels.
+"""
+import numpy as np
+import pytest
+
+import emel_hip as eh
+import oracle as orc
+from helpers import Pair, normal
+
+pytestmark = pytest.mark.gpu
+
+
+def planted_logits(cols, rows, seed):
+    """N(0,1) rows with a planted maximum at a seeded index and, in every
+    other row, a tie at a higher index (the lower index must win)."""
+    g = np.random.Generator(np.random.PCG64(seed))
+    x = g.standard_normal(cols * rows, dtype=np.float64).astype(np.float32).reshape(rows, cols)
+    where = g.integers(0, cols, rows)
+    for r in range(rows):
+        x[r, where[r]] = np.float32(8.0 + r * 1e-3)
+        if r % 2 == 0 and where[r] + 1 < cols:
+            tie = g.integers(where[r] + 1, cols)
+            x[r, tie] = x[r, where[r]]
+    return x.reshape(-1), where
+
+
+def run_argmax_rows(gpu, x, ne, nb=None):
+    a = Pair(x, ne, nb).to(gpu)
+    rows = int(np.prod(ne[1:]))
+    o = Pair(np.full(rows, -7, np.int32), [1, ne[1], ne[2], ne[3]]).to(gpu)
+    assert eh.Kernel().process_event(eh.OpArgmaxRows(a.pview(), o.pview(mut=True))) == eh.Status.OK, eh.last_error()
+    want = np.full(rows, -7, np.int32)
+    assert orc.argmax_rows(a.oview(), orc.view(want, o.ne)) == orc.OK
+    got = o.result()
+    assert (got == want).all(), (np.flatnonzero(got != want)[:5], got[got != want][:5], want[got != want][:5])
+    return got
+
+
+def test_argmax_rows_config5(gpu):
+    cols, rows = 151936, 64
+    x, where = planted_logits(cols, rows, 201)
+    got = run_argmax_rows(gpu, x, [cols, rows, 1, 1])
+    assert (got == where).all()
+
+
+@pytest.mark.parametrize("cols,rows", [(1, 3), (5, 2), (1024, 1), (4095, 3), (100003, 2), (4096, 4096)])
+def test_argmax_rows_sizes(gpu, cols, rows):
+    x, _ = planted_logits(cols, rows, 202 + cols)
+    run_argmax_rows(gpu, x, [cols, rows, 1, 1])
+
+
+def test_argmax_rows_nan_inf_ties(gpu):
+    cols = 50000
+    rows = []
+    base = np.zeros(cols, np.float32)
+    r = base.copy(); r[0] = np.nan; r[10] = 5.0; rows.append(r)                 # NaN at column 0 -> 0
+    r = base.copy(); r[3] = np.nan; r[40000] = 1.0; rows.append(r)              # later NaN is skipped
+    r = np.full(cols, -np.inf, np.float32); rows.append(r)                     # all -inf -> 0
+    r = np.full(cols, -np.inf, np.float32); r[7] = np.nan; r[49999] = -1.0; rows.append(r)
+    r = base.copy(); r[5] = -0.0; r[2] = 0.0; rows.append(r)                   # +-0 tie -> lowest index
+    r = base.copy(); r[123] = np.inf; r[45000] = np.inf; rows.append(r)
+    r = np.full(cols, np.nan, np.float32); rows.append(r)
+    r = np.full(cols, 3.0, np.float32); rows.append(r)                          # all equal -> 0
+    x = np.concatenate(rows)
+    got = run_argmax_rows(gpu, x, [cols, len(rows), 1, 1])
+    assert list(got) == [0, 40000, 0, 49999, 0, 123, 0, 0]
+
+
+def test_argmax_rows_strided(gpu):
+    cols, rows, pad = 999, 6, 1024
+    x = normal(211, pad * rows * 2)
+    run_argmax_rows(gpu, x, [cols, rows, 1, 1], [8, 8 * pad, 8 * pad * rows, 8 * pad * rows])
+
+
+def sum_rows_check(gpu, x, ne, nb=None):
+    a = Pair(x, ne, nb).to(gpu)
+    o = Pair(np.zeros(int(np.prod(ne[1:])), np.float32), [1, ne[1], ne[2], ne[3]]).to(gpu)
+    assert eh.Kernel().process_event(eh.OpSumRows(a.pview(), o.pview(mut=True))) == eh.Status.OK, eh.last_error()
+    want = np.zeros(o.host.size, np.float32)
+    assert orc.sum_rows(a.oview(), orc.view(want, o.ne)) == orc.OK
+    got = o.result().astype(np.float64)
+    # condition-number floor: the f64 sums can differ by ~1e-16 * sum|x|
+    absx = np.abs(x.astype(np.float64))
+    floor = 1e-12 * max(absx.sum(), 1.0)
+    ok = np.abs(got - want) <= 1e-5 * np.abs(want) + floor
+    assert ok.all(), (got[~ok][:4], want[~ok][:4])
+
+
+def test_sum_rows_config5(gpu):
+    x, _ = planted_logits(151936, 64, 221)
+    sum_rows_check(gpu, x, [151936, 64, 1, 1])
+
+
+@pytest.mark.parametrize("ne", [[3, 2, 1, 1], [1, 7, 1, 1], [4096, 16, 2, 2], [10001, 3, 1, 2]])
+def test_sum_rows_shapes(gpu, ne):
+    sum_rows_check(gpu, normal(231, int(np.prod(ne))), ne)
+
+
+def test_sum_rows_strided(gpu):
+    cols, rows = 777, 13
+    sum_rows_check(gpu, normal(241, 3 * cols * rows), [cols, rows, 1, 1], [12, 12 * cols, 12 * cols * rows, 12 * cols * rows])
+
+
+@pytest.mark.parametrize("ne,nb", [([151936, 64, 1, 1], None), ([3, 2, 1, 1], None), ([17, 5, 3, 1], [0, 0, 0, 0]),
+                                   ([9, 4, 2, 1], [8, 72, 288, 576])])
+def test_scalar_reductions(gpu, ne, nb):
+    n = int(np.prod(ne))
+    span = n if nb is None or nb[0] == 0 else (sum((ne[d] - 1) * nb[d] for d in range(4)) // 4 + 1)
+    x, _ = planted_logits(span, 1, 251)
+    a = Pair(x, ne, nb).to(gpu)
+    k = eh.Kernel()
+    for ev, fn, exact in ((eh.OpArgmax, orc.argmax, True), (eh.OpSum, orc.sum_, False), (eh.OpMean, orc.mean, False)):
+        o = Pair(np.zeros(1, np.float32), [1, 1, 1, 1]).to(gpu)
+        assert k.process_event(ev(a.pview(), o.pview(mut=True))) == eh.Status.OK, eh.last_error()
+        want = np.zeros(1, np.float32)
+        assert fn(a.oview(), orc.view(want, [1, 1, 1, 1])) == orc.OK
+        got = o.result()
+        if exact:
+            assert got[0] == want[0], (got, want)
+        else:
+            floor = 1e-12 * np.abs(x.astype(np.float64)).sum()
+            assert abs(float(got[0]) - float(want[0])) <= 1e-5 * abs(float(want[0])) + floor, (got, want)
+
+
+def test_repeated_launches_reuse_workspace(gpu):
+    # the split-row counters are reset by each launch: results stay right
+    cols, rows = 151936, 64
+    x, where = planted_logits(cols, rows, 261)
+    a = Pair(x, [cols, rows, 1, 1]).to(gpu)
+    o = Pair(np.zeros(rows, np.int32), [1, rows, 1, 1]).to(gpu)
+    k = eh.Kernel(synchronous=False)
+    for _ in range(50):
+        assert k.process_event(eh.OpArgmaxRows(a.pview(), o.pview(mut=True))) == eh.Status.OK
+    import torch
+    torch.cuda.synchronize()
+    assert (o.result() == where).all()

@@ -1,0 +1,180 @@
+"""GPU parity: rms_norm (+weight), norm and soft_max vs the CPU oracle.
+
+The reference accumulates these row sums sequentially in f64 (rms_norm,
+norm, dense soft_max); the GPU sums the same f64 terms in a tree, so an f32
+result can differ only when the f64 sum lands next to an f32 rounding
+boundary.  The tolerance is BASELINE's: 1e-5 relative.  The strided
+soft_max keeps the reference's sequential f32 sum and is compared
+bit-exactly.
+"""
+import numpy as np
+import pytest
+
+import emel_hip as eh
+import oracle as orc
+from helpers import Pair, assert_bits_equal, assert_close_rel, normal, uniform
+
+pytestmark = pytest.mark.gpu
+
+RTOL = 1e-5
+
+
+def outlier_rows(x, cols, rows, seed, frac=0.01, factor=100.0):
+    g = np.random.Generator(np.random.PCG64(seed))
+    picked = g.choice(rows, max(1, int(rows * frac)), replace=False)
+    x = x.reshape(rows, cols).copy()
+    x[picked] *= np.float32(factor)
+    return x.reshape(-1)
+
+
+@pytest.mark.parametrize("cols,rows", [(4096, 2048), (4096, 3), (1, 5), (3, 7), (64, 64), (1000, 9),
+                                       (8192, 4), (20000, 3)])
+def test_rms_norm(gpu, cols, rows):
+    x = outlier_rows(normal(101 + cols, cols * rows), cols, rows, 7)
+    a = Pair(x, [cols, rows, 1, 1]).to(gpu)
+    o = Pair(np.zeros_like(x), [cols, rows, 1, 1]).to(gpu)
+    assert eh.Kernel().process_event(eh.OpRmsNorm(a.pview(), o.pview(mut=True), 1e-5)) == eh.Status.OK, eh.last_error()
+    want = np.zeros_like(x)
+    assert orc.rms_norm(a.oview(), orc.view(want, o.ne), 1e-5) == orc.OK
+    got = o.result()
+    assert_close_rel(got, want, RTOL, "rms_norm")
+    # informational: the tree-ordered f64 sum almost always rounds alike
+    exact = (got.view(np.uint32) == want.view(np.uint32)).mean()
+    assert exact > 0.99, f"only {exact:.4%} bit-exact"
+
+
+def test_rms_norm_mul_config3(gpu):
+    cols, rows = 4096, 2048
+    x = outlier_rows(normal(111, cols * rows), cols, rows, 8)
+    w = uniform(112, cols, 0.5, 1.5)
+    a = Pair(x, [cols, rows, 1, 1]).to(gpu)
+    wp = Pair(w, [cols, 1, 1, 1]).to(gpu)
+    o = Pair(np.zeros_like(x), [cols, rows, 1, 1]).to(gpu)
+    k = eh.Kernel()
+    assert k.process_event(eh.OpRmsNormMul(a.pview(), wp.pview(), o.pview(mut=True), 1e-5)) == eh.Status.OK
+    want = np.zeros_like(x)
+    assert orc.rms_norm_mul(a.oview(), wp.oview(), orc.view(want, o.ne), 1e-5) == orc.OK
+    assert_close_rel(o.result(), want, RTOL, "rms_norm_mul")
+    # fused == rms_norm then OpMulBroadcastRow on the GPU, bit for bit
+    t = Pair(np.zeros_like(x), o.ne).to(gpu)
+    o2 = Pair(np.zeros_like(x), o.ne).to(gpu)
+    assert k.process_event(eh.OpRmsNorm(a.pview(), t.pview(mut=True), 1e-5)) == eh.Status.OK
+    assert k.process_event(eh.OpMulBroadcastRow(t.pview(), wp.pview(), o2.pview(mut=True))) == eh.Status.OK
+    assert_bits_equal(o.result(), o2.result(), "fused vs composed rms_norm * w")
+
+
+def test_rms_norm_strided_and_implicit(gpu):
+    cols, rows = 300, 11
+    # rows padded to 320 floats, dim 0 stride 8 bytes (every other float)
+    st = Pair(normal(121, 2 * 320 * rows), [cols // 2, rows, 1, 1], [8, 4 * 320, 4 * 320 * rows, 4 * 320 * rows]).to(gpu)
+    o = Pair(np.zeros(cols // 2 * rows, np.float32), [cols // 2, rows, 1, 1]).to(gpu)
+    assert eh.Kernel().process_event(eh.OpRmsNorm(st.pview(), o.pview(mut=True), 0.5)) == eh.Status.OK, eh.last_error()
+    want = np.zeros(cols // 2 * rows, np.float32)
+    assert orc.rms_norm(st.oview(), orc.view(want, o.ne), 0.5) == orc.OK
+    assert_close_rel(o.result(), want, RTOL, "strided rms_norm")
+    im = Pair(normal(122, cols * rows), [cols, rows, 1, 1], [0, 0, 0, 0]).to(gpu)
+    o = Pair(np.zeros(cols * rows, np.float32), [cols, rows, 1, 1], [0, 0, 0, 0]).to(gpu)
+    assert eh.Kernel().process_event(eh.OpRmsNorm(im.pview(), o.pview(mut=True), 1.0)) == eh.Status.OK
+    want = np.zeros(cols * rows, np.float32)
+    assert orc.rms_norm(im.oview(), orc.view(want, o.ne, o.nb), 1.0) == orc.OK
+    assert_close_rel(o.result(), want, RTOL, "implicit rms_norm")
+
+
+@pytest.mark.parametrize("cols,rows", [(4096, 64), (7, 9), (10000, 5)])
+def test_norm(gpu, cols, rows):
+    x = normal(131, cols * rows, 3.0) + np.float32(2.0)
+    a = Pair(x, [cols, rows, 1, 1]).to(gpu)
+    o = Pair(np.zeros_like(x), a.ne).to(gpu)
+    assert eh.Kernel().process_event(eh.OpNorm(a.pview(), o.pview(mut=True), 1e-5)) == eh.Status.OK
+    want = np.zeros_like(x)
+    assert orc.norm(a.oview(), orc.view(want, a.ne), 1e-5) == orc.OK
+    assert_close_rel(o.result(), want, RTOL, "norm", atol=1e-6)
+
+
+@pytest.mark.parametrize("cols,rows", [(4096, 256), (3, 2), (5, 17), (151936, 2), (1, 4)])
+def test_soft_max_dense(gpu, cols, rows):
+    x = normal(141 + cols, cols * rows, 2.0)
+    a = Pair(x, [cols, rows, 1, 1]).to(gpu)
+    o = Pair(np.zeros_like(x), a.ne).to(gpu)
+    assert eh.Kernel().process_event(eh.OpSoftMax(a.pview(), o.pview(mut=True))) == eh.Status.OK, eh.last_error()
+    want = np.zeros_like(x)
+    assert orc.soft_max(a.oview(), orc.view(want, a.ne)) == orc.OK
+    assert_close_rel(o.result(), want, RTOL, "soft_max")
+
+
+def test_soft_max_strided_is_bit_exact(gpu):
+    cols, rows = 513, 37
+    # dim 0 stride 8 bytes: not dense, so the reference sums in sequential f32
+    a = Pair(normal(151, 2 * cols * rows, 3.0), [cols, rows, 1, 1],
+             [8, 8 * cols, 8 * cols * rows, 8 * cols * rows]).to(gpu)
+    o = Pair(np.zeros(cols * rows, np.float32), [cols, rows, 1, 1]).to(gpu)
+    assert eh.Kernel().process_event(eh.OpSoftMax(a.pview(), o.pview(mut=True))) == eh.Status.OK, eh.last_error()
+    want = np.zeros(cols * rows, np.float32)
+    assert orc.soft_max(a.oview(), orc.view(want, o.ne)) == orc.OK
+    assert_bits_equal(o.result(), want, "strided soft_max")
+
+
+def causal_mask(nkv, nq):
+    k = np.arange(nkv)[None, :]
+    q = np.arange(nq)[:, None]
+    return np.where(k <= q + (nkv - nq), np.float16(0.0), np.float16(-np.inf)).astype(np.float16).reshape(-1)
+
+
+@pytest.mark.parametrize("nkv,nq,nh", [(4096, 512, 32), (256, 64, 4), (36, 5, 3), (4096, 1, 2)])
+def test_soft_max_ext_causal(gpu, nkv, nq, nh):
+    x = normal(161, nkv * nq * nh, 2.0)  # N(0, 4)
+    scale = float(np.float32(1.0 / np.sqrt(128.0)))
+    a = Pair(x, [nkv, nq, nh, 1]).to(gpu)
+    m = Pair(causal_mask(nkv, nq).view(np.uint16), [nkv, nq, 1, 1], dtype=orc.F16).to(gpu)
+    o = Pair(np.zeros_like(x), a.ne).to(gpu)
+    assert eh.Kernel().process_event(eh.OpSoftMaxExt(a.pview(), m.pview(), scale, o.pview(mut=True))) == eh.Status.OK, \
+        eh.last_error()
+    want = np.zeros_like(x)
+    assert orc.soft_max_ext(a.oview(), m.oview(), scale, orc.view(want, a.ne)) == orc.OK
+    got = o.result()
+    assert_close_rel(got, want, RTOL, "soft_max_ext")
+    rows = got.reshape(-1, nkv).astype(np.float64).sum(axis=1)
+    assert np.abs(rows - 1.0).max() < 1e-5
+
+
+def test_soft_max_ext_reduces_to_soft_max(gpu):
+    # zero mask and scale 1 must give OpSoftMax's bits exactly
+    nkv, nq, nh = 1024, 16, 4
+    x = normal(171, nkv * nq * nh, 2.0)
+    a = Pair(x, [nkv, nq, nh, 1]).to(gpu)
+    m = Pair(np.zeros(nkv * nq, np.uint16), [nkv, nq, 1, 1], dtype=orc.F16).to(gpu)
+    o1 = Pair(np.zeros_like(x), a.ne).to(gpu)
+    o2 = Pair(np.zeros_like(x), a.ne).to(gpu)
+    k = eh.Kernel()
+    assert k.process_event(eh.OpSoftMaxExt(a.pview(), m.pview(), 1.0, o1.pview(mut=True))) == eh.Status.OK
+    assert k.process_event(eh.OpSoftMax(a.pview(), o2.pview(mut=True))) == eh.Status.OK
+    assert_bits_equal(o1.result(), o2.result(), "ext(zero mask, scale 1) vs soft_max")
+
+
+def test_soft_max_ext_general_path(gpu):
+    # ncols % 4 != 0 and a per-head mask (m2 == nh): the non-vectorized kernel
+    nkv, nq, nh = 37, 6, 4
+    x = normal(181, nkv * nq * nh, 2.0)
+    g = np.random.Generator(np.random.PCG64(182))
+    mask = g.standard_normal(nkv * nq * nh).astype(np.float16)
+    mask[g.random(mask.size) < 0.2] = np.float16(-np.inf)
+    mask.reshape(-1, nkv)[:, 0] = 0  # keep every row alive
+    a = Pair(x, [nkv, nq, nh, 1]).to(gpu)
+    m = Pair(mask.view(np.uint16), [nkv, nq, nh, 1], dtype=orc.F16).to(gpu)
+    o = Pair(np.zeros_like(x), a.ne).to(gpu)
+    assert eh.Kernel().process_event(eh.OpSoftMaxExt(a.pview(), m.pview(), 0.75, o.pview(mut=True))) == eh.Status.OK
+    want = np.zeros_like(x)
+    assert orc.soft_max_ext(a.oview(), m.oview(), 0.75, orc.view(want, a.ne)) == orc.OK
+    assert_close_rel(o.result(), want, RTOL, "soft_max_ext general")
+
+
+def test_rows_in_place(gpu):
+    cols, rows = 4096, 16
+    x = normal(191, cols * rows)
+    for ev, fn in ((lambda v, o: eh.OpRmsNorm(v, o, 1e-5), lambda a, o: orc.rms_norm(a, o, 1e-5)),
+                   (eh.OpSoftMax, orc.soft_max)):
+        a = Pair(x, [cols, rows, 1, 1]).to(gpu)
+        assert eh.Kernel().process_event(ev(a.pview(), a.pview(mut=True))) == eh.Status.OK
+        want = x.copy()
+        assert fn(orc.view(x, a.ne), orc.view(want, a.ne)) == orc.OK
+        assert_close_rel(a.result(), want, RTOL, "in place")

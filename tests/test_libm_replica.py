@@ -1,0 +1,58 @@
+"""CPU: the product's device math (emel.rs_amd/csrc/libm_replica.hpp), built
+for the host by tests/native/libm_replica_check.cpp, against independent
+checkers over ALL 2^32 float inputs:
+
+  expf, expm1f, tanhf  == the host glibc (Rust std's f32::exp/exp_m1/tanh on
+                          x86_64-linux-gnu, i.e. what the reference computes);
+  fp32 -> fp16         == IEEE round-to-nearest-even (_Float16 conversion);
+  fp16 -> fp32         == exact widening.
+
+The GPU kernels run this same code, so a GPU result can differ from the
+oracle only through the GPU's IEEE basic operations, which the GPU tests
+check separately.
+"""
+import ctypes
+import os
+from pathlib import Path
+
+import pytest
+
+LIB = Path(__file__).resolve().parent / "native" / "libm_replica_check.so"
+THREADS = max(1, min(8, os.cpu_count() or 1))
+
+
+@pytest.fixture(scope="module")
+def chk():
+    if not LIB.exists():
+        pytest.fail(f"{LIB} missing: run __graft_entry__.build()")
+    L = ctypes.CDLL(str(LIB))
+    for n in ("check_expf", "check_expm1f", "check_tanhf", "check_fp32_to_fp16"):
+        getattr(L, n).restype = ctypes.c_uint64
+        getattr(L, n).argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int]
+    L.check_fp16_to_f32.restype = ctypes.c_uint64
+    for n in ("replica_silu", "replica_gelu", "replica_expf", "replica_tanhf"):
+        getattr(L, n).restype = ctypes.c_float
+        getattr(L, n).argtypes = [ctypes.c_float]
+    return L
+
+
+@pytest.mark.parametrize("fn", ["check_expf", "check_expm1f", "check_tanhf", "check_fp32_to_fp16"])
+def test_exhaustive(chk, fn):
+    assert getattr(chk, fn)(0, 1 << 32, THREADS) == 0
+
+
+def test_fp16_widening(chk):
+    assert chk.check_fp16_to_f32() == 0
+
+
+def test_replica_matches_oracle_scalars(chk):
+    import numpy as np
+
+    import oracle as orc
+
+    xs = np.concatenate([np.linspace(-12, 12, 20001, dtype=np.float32),
+                         np.array([-10.1, -10.0, -1.2345, -0.125, 0.0, 0.12345, 10.0, 10.1], np.float32)])
+    for x in xs:
+        x = float(x)
+        assert np.float32(chk.replica_silu(x)).view(np.uint32) == np.float32(orc.silu_scalar(x)).view(np.uint32), x
+        assert np.float32(chk.replica_gelu(x)).view(np.uint32) == np.float32(orc.gelu_scalar(x)).view(np.uint32), x
