@@ -1,0 +1,395 @@
+"""Benchmark: achieved HBM bandwidth of emel.rs's elementwise, broadcast and
+row-reduction ops on one MI355X (BASELINE.json metric).
+
+One step = one launch of every op of the five BASELINE configs, each on its
+own buffers (no op reads another op's output), so each launch streams cold
+data from HBM: between two launches of the same op the other ops move
+~1 GB, far more than the 256 MB Infinity Cache.  Buffers alternate between
+two copies per op as well.  Inputs are synthetic (seeded PCG64) and already
+resident in HBM when the timed region starts.
+
+Per-op time is measured with HIP events recorded on the stream the kernels
+run on; the value is total algorithmic bytes per step / step time.  The
+roofline object describes the dominant kernel (the scaled + masked soft_max
+of config 4, over half of the step's bytes).  The CPU baseline times the C
+oracle (a single-threaded restatement of the reference's CPU path) on a
+bounded sample of the same workload.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--ops a,b] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT / "emel.rs_amd", ROOT / "oracle"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "achieved HBM GB/s and % of 8 TB/s peak per op (binary, rms_norm, softmax)"
+PEAK_GBS = 8000.0
+MB = 1e6
+
+
+def rng(seed):
+    return np.random.Generator(np.random.PCG64(seed))
+
+
+def normal(seed, n, sigma=1.0):
+    return (rng(seed).standard_normal(n, dtype=np.float64) * sigma).astype(np.float32)
+
+
+def uniform(seed, n, lo, hi):
+    return rng(seed).uniform(lo, hi, n).astype(np.float32)
+
+
+def causal_mask(nkv, nq):
+    k = np.arange(nkv)[None, :]
+    q = np.arange(nq)[:, None]
+    return np.where(k <= q + (nkv - nq), np.float16(0.0), np.float16(-np.inf)).astype(np.float16).reshape(-1)
+
+
+def config_inputs():
+    """Host arrays of the BASELINE configs (seeded)."""
+    d = {}
+    # config 1: [4096,512] + [4096], U(-1,1)
+    d["c1_src0"] = uniform(1, 4096 * 512, -1, 1)
+    d["c1_src1"] = uniform(2, 4096, -1, 1)
+    # config 2: gate, up [11008,512] N(0,1)
+    d["c2_gate"] = normal(3, 11008 * 512)
+    d["c2_up"] = normal(4, 11008 * 512)
+    # config 3: x [4096,2048] N(0,1), 1% of rows x100; w [4096] U(0.5,1.5)
+    x = normal(5, 4096 * 2048).reshape(2048, 4096)
+    x[rng(6).choice(2048, 20, replace=False)] *= np.float32(100.0)
+    d["c3_x"] = x.reshape(-1)
+    d["c3_w"] = uniform(7, 4096, 0.5, 1.5)
+    # config 4: scores [4096,512,32] N(0,4), causal f16 mask [4096,512]
+    d["c4_x"] = normal(8, 4096 * 512 * 32, 2.0)
+    d["c4_mask"] = causal_mask(4096, 512).view(np.uint16)
+    # config 5: logits [151936,64] N(0,1) with a planted max per row (+ ties)
+    lg = normal(9, 151936 * 64).reshape(64, 151936)
+    g = rng(10)
+    where = g.integers(0, 151936, 64)
+    for r in range(64):
+        lg[r, where[r]] = np.float32(8.0)
+        if r % 2 == 0 and where[r] + 1 < 151936:
+            lg[r, g.integers(where[r] + 1, 151936)] = np.float32(8.0)
+    d["c5_logits"] = lg.reshape(-1)
+    # config 5b: src0 storage [128,32,64,8] viewed as [128,64,32,8]; src1 [128,1,32,1]
+    d["c5b_src0"] = normal(11, 128 * 32 * 64 * 8)
+    d["c5b_src1"] = normal(12, 128 * 32)
+    return d
+
+
+def dense_nb(ne, elem=4):
+    nb = [elem]
+    for i in range(1, 4):
+        nb.append(nb[-1] * ne[i - 1])
+    return nb
+
+
+# (name, config, algorithmic bytes, tensors) -- the byte counts are the
+# minimum HBM traffic: every input read once and every output written once.
+OPS = [
+    ("add_broadcast_row", "config 1: f32 [4096,512] + [4096]", 8388608 + 16384 + 8388608),
+    ("silu", "config 2: silu(gate) [11008,512]", 2 * 22544384),
+    ("mul", "config 2: silu(gate) * up [11008,512]", 3 * 22544384),
+    ("swiglu", "config 2: fused silu(gate) * up [11008,512]", 3 * 22544384),
+    ("gelu", "config 2: gelu(gate) [11008,512]", 2 * 22544384),
+    ("rms_norm", "config 3: rms_norm [4096,2048] eps=1e-5", 2 * 33554432),
+    ("rms_norm_mul", "config 3: rms_norm * w [4096,2048], fused", 2 * 33554432 + 16384),
+    ("soft_max_ext", "config 4: soft_max(x*scale + mask) [4096,512,32], f16 causal mask", 2 * 268435456 + 4194304),
+    ("argmax_rows", "config 5: argmax per row [151936,64] -> i32", 38895616 + 256),
+    ("sum_rows", "config 5: sum_rows [151936,64]", 38895616 + 256),
+    ("mul_broadcast_4d", "config 5b: permuted [128,64,32,8] * [128,1,32,1]", 8388608 + 16384 + 8388608),
+]
+DOMINANT = "soft_max_ext"
+COPY_BYTES = 2 * 268435456  # the calibration copy: 256 MiB read + 256 MiB written
+
+
+class GpuSuite:
+    """Device buffers (two copies per op) and the launch closures."""
+
+    def __init__(self, host, stream, names, copies=2):
+        import torch
+
+        import emel_hip as eh
+
+        self.eh = eh
+        self.torch = torch
+        self.stream = stream
+        self.kernel = eh.Kernel(stream=stream.cuda_stream, synchronous=False)
+        dev = torch.device("cuda:0")
+        L = eh.Layout
+        F32, F16, I32 = eh.DType.F32, eh.DType.F16, eh.DType.I32
+
+        def up(arr):
+            return torch.from_numpy(arr).to(dev)
+
+        def zeros(n, dtype=torch.float32):
+            return torch.zeros(n, dtype=dtype, device=dev)
+
+        def V(t, ne, nb=None, dtype=F32):
+            return eh.TensorView(t, L(dtype, ne, nb or dense_nb(ne, 2 if dtype == F16 else 4)))
+
+        def M(t, ne, nb=None, dtype=F32):
+            return eh.TensorViewMut(t, L(dtype, ne, nb or dense_nb(ne)))
+
+        self.events = {}
+        silu_gate = np.empty_like(host["c2_gate"])  # mul's first operand: silu(gate) values
+        silu_gate[:] = host["c2_gate"] / (1 + np.exp(-host["c2_gate"].astype(np.float64)))
+        for name in names:
+            evs = []
+            for c in range(copies):
+                if name == "add_broadcast_row":
+                    a, b, o = up(host["c1_src0"]), up(host["c1_src1"]), zeros(4096 * 512)
+                    ev = eh.OpAddBroadcastRow(V(a, [4096, 512, 1, 1]), V(b, [4096, 1, 1, 1]), M(o, [4096, 512, 1, 1]))
+                elif name in ("silu", "gelu"):
+                    a, o = up(host["c2_gate"]), zeros(11008 * 512)
+                    cls = eh.OpSilu if name == "silu" else eh.OpGelu
+                    ev = cls(V(a, [11008, 512, 1, 1]), M(o, [11008, 512, 1, 1]))
+                elif name == "mul":
+                    a, b, o = up(silu_gate), up(host["c2_up"]), zeros(11008 * 512)
+                    ev = eh.OpMul(V(a, [11008, 512, 1, 1]), V(b, [11008, 512, 1, 1]), M(o, [11008, 512, 1, 1]))
+                elif name == "swiglu":
+                    a, b, o = up(host["c2_gate"]), up(host["c2_up"]), zeros(11008 * 512)
+                    ev = eh.OpSwiglu(V(a, [11008, 512, 1, 1]), V(b, [11008, 512, 1, 1]), M(o, [11008, 512, 1, 1]))
+                elif name == "rms_norm":
+                    a, o = up(host["c3_x"]), zeros(4096 * 2048)
+                    ev = eh.OpRmsNorm(V(a, [4096, 2048, 1, 1]), M(o, [4096, 2048, 1, 1]), 1e-5)
+                elif name == "rms_norm_mul":
+                    a, w, o = up(host["c3_x"]), up(host["c3_w"]), zeros(4096 * 2048)
+                    ev = eh.OpRmsNormMul(V(a, [4096, 2048, 1, 1]), V(w, [4096, 1, 1, 1]), M(o, [4096, 2048, 1, 1]), 1e-5)
+                elif name == "soft_max_ext":
+                    a, m, o = up(host["c4_x"]), up(host["c4_mask"]), zeros(4096 * 512 * 32)
+                    scale = float(np.float32(1.0 / np.sqrt(128.0)))
+                    ev = eh.OpSoftMaxExt(V(a, [4096, 512, 32, 1]), V(m, [4096, 512, 1, 1], dtype=F16), scale,
+                                         M(o, [4096, 512, 32, 1]))
+                elif name == "argmax_rows":
+                    a, o = up(host["c5_logits"]), zeros(64, torch.int32)
+                    ev = eh.OpArgmaxRows(V(a, [151936, 64, 1, 1]), M(o, [1, 64, 1, 1], dtype=I32))
+                elif name == "sum_rows":
+                    a, o = up(host["c5_logits"]), zeros(64)
+                    ev = eh.OpSumRows(V(a, [151936, 64, 1, 1]), M(o, [1, 64, 1, 1]))
+                elif name == "mul_broadcast_4d":
+                    a, b, o = up(host["c5b_src0"]), up(host["c5b_src1"]), zeros(128 * 64 * 32 * 8)
+                    snb = dense_nb([128, 32, 64, 8])
+                    vnb = [snb[0], snb[2], snb[1], snb[3]]  # dims 1 and 2 swapped
+                    ev = eh.OpBinaryBroadcast(eh.BinaryOp.MUL, V(a, [128, 64, 32, 8], vnb), V(b, [128, 1, 32, 1]),
+                                              M(o, [128, 64, 32, 8]))
+                elif name == "copy":
+                    a, o = zeros(COPY_BYTES // 8), zeros(COPY_BYTES // 8)
+                    ev = eh.OpScale(V(a, [COPY_BYTES // 8, 1, 1, 1]), M(o, [COPY_BYTES // 8, 1, 1, 1]), 1.0)
+                else:
+                    raise ValueError(name)
+                evs.append(ev)
+            self.events[name] = evs
+        torch.cuda.synchronize()
+
+    def launch(self, name, step):
+        st = self.kernel.process_event(self.events[name][step % len(self.events[name])])
+        if st != self.eh.Status.OK:
+            raise RuntimeError(f"{name}: {st.name}: {self.eh.last_error()}")
+
+
+def cpu_baseline(host, budget_s=20.0):
+    """Single-threaded oracle on a bounded sample of each op's workload:
+    the same code path the reference's CPU kernels take (view decode,
+    glibc libm), timed with a monotonic clock, median of 3 runs per op."""
+    import oracle as orc
+
+    def v(a, ne, nb=None, dtype=None):
+        return orc.view(a, ne, nb, dtype)
+
+    rows_frac = 8  # each op runs on 1/8 of its rows (or heads)
+    samples = {}
+    c1 = host["c1_src0"][: 4096 * 64]
+    samples["add_broadcast_row"] = (lambda o=np.zeros(4096 * 64, np.float32): orc.broadcast_row(
+        orc.ADD, v(c1, [4096, 64, 1, 1]), v(host["c1_src1"], [4096, 1, 1, 1]), v(o, [4096, 64, 1, 1])),
+        (8388608 + 16384 + 8388608) / rows_frac)
+    g = host["c2_gate"][: 11008 * 64]
+    u = host["c2_up"][: 11008 * 64]
+    samples["silu"] = (lambda o=np.zeros_like(g): orc.unary_event(10, v(g, [11008, 64, 1, 1]), v(o, [11008, 64, 1, 1])),
+                       2 * 22544384 / rows_frac)
+    samples["mul"] = (lambda o=np.zeros_like(g): orc.binary(orc.MUL, v(g, [11008, 64, 1, 1]), v(u, [11008, 64, 1, 1]),
+                                                            v(o, [11008, 64, 1, 1])), 3 * 22544384 / rows_frac)
+    samples["swiglu"] = (lambda o=np.zeros_like(g): orc.swiglu(v(g, [11008, 64, 1, 1]), v(u, [11008, 64, 1, 1]),
+                                                               v(o, [11008, 64, 1, 1])), 3 * 22544384 / rows_frac)
+    samples["gelu"] = (lambda o=np.zeros_like(g): orc.unary_event(8, v(g, [11008, 64, 1, 1]), v(o, [11008, 64, 1, 1])),
+                       2 * 22544384 / rows_frac)
+    x3 = host["c3_x"][: 4096 * 256]
+    samples["rms_norm"] = (lambda o=np.zeros_like(x3): orc.rms_norm(v(x3, [4096, 256, 1, 1]), v(o, [4096, 256, 1, 1]), 1e-5),
+                           2 * 33554432 / rows_frac)
+    samples["rms_norm_mul"] = (lambda o=np.zeros_like(x3): orc.rms_norm_mul(
+        v(x3, [4096, 256, 1, 1]), v(host["c3_w"], [4096, 1, 1, 1]), v(o, [4096, 256, 1, 1]), 1e-5),
+        (2 * 33554432 + 16384) / rows_frac)
+    x4 = host["c4_x"][: 4096 * 512 * 4]
+    scale = float(np.float32(1.0 / np.sqrt(128.0)))
+    samples["soft_max_ext"] = (lambda o=np.zeros_like(x4): orc.soft_max_ext(
+        v(x4, [4096, 512, 4, 1]), v(host["c4_mask"], [4096, 512, 1, 1], None, orc.F16), scale, v(o, [4096, 512, 4, 1])),
+        2 * 268435456 / rows_frac + 4194304)
+    x5 = host["c5_logits"][: 151936 * 8]
+    samples["argmax_rows"] = (lambda o=np.zeros(8, np.int32): orc.argmax_rows(v(x5, [151936, 8, 1, 1]), v(o, [1, 8, 1, 1])),
+                              (38895616 + 256) / rows_frac)
+    samples["sum_rows"] = (lambda o=np.zeros(8, np.float32): orc.sum_rows(v(x5, [151936, 8, 1, 1]), v(o, [1, 8, 1, 1])),
+                           (38895616 + 256) / rows_frac)
+    s5 = host["c5b_src0"]
+    snb = dense_nb([128, 32, 64, 8])
+    vnb = [snb[0], snb[2], snb[1], snb[3]]
+    samples["mul_broadcast_4d"] = (lambda o=np.zeros(128 * 64 * 32 * 1, np.float32): orc.binary_bcast(
+        orc.MUL, v(s5, [128, 64, 32, 1], vnb), v(host["c5b_src1"], [128, 1, 32, 1]), v(o, [128, 64, 32, 1])),
+        (8388608 + 16384 + 8388608) / rows_frac)
+    per_op = {}
+    total_bytes = 0.0
+    total_s = 0.0
+    t_start = time.monotonic()
+    for name, (fn, nbytes) in samples.items():
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            st = fn()
+            times.append(time.perf_counter() - t0)
+            if st != orc.OK:
+                raise RuntimeError(f"oracle {name} failed: {st}")
+            if time.monotonic() - t_start > budget_s:
+                break
+        t = float(np.median(times))
+        per_op[name] = {"GB/s": nbytes / t / 1e9, "ms": t * 1e3}
+        total_bytes += nbytes
+        total_s += t
+    return total_bytes / total_s / 1e9, per_op
+
+
+def host_facts():
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = os.cpu_count()
+    return {"cpu": model, "nproc": os.cpu_count(), "affinity": affinity, "glibc": platform.libc_ver()[1]}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--ops", default="")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(f"bench.py measures one GPU only (asked for {args.gpus}): every op is row-local, "
+              "so N GPUs each run their own share; see DESIGN.md on sharding", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    names = [n for n, _, _ in OPS]
+    if args.ops:
+        names = [n for n in args.ops.split(",") if n]
+    info = {n: (cfg, b) for n, cfg, b in OPS}
+    info["copy"] = ("calibration copy: scale by 1.0 over 256 MiB", COPY_BYTES)
+
+    host = config_inputs()
+    stream = torch.cuda.Stream()
+    suite = GpuSuite(host, stream, names)
+
+    with torch.cuda.stream(stream):
+        for w in range(args.warmup):
+            for n in names:
+                suite.launch(n, w)
+        stream.synchronize()
+        marks = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)] for _ in range(args.steps)]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for s in range(args.steps):
+            ev = marks[s]
+            ev[0].record(stream)
+            for i, n in enumerate(names):
+                suite.launch(n, s)
+                ev[i + 1].record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+
+    per_ms = {n: 0.0 for n in names}
+    step_ms = 0.0
+    for ev in marks:
+        step_ms += ev[0].elapsed_time(ev[-1])
+        for i, n in enumerate(names):
+            per_ms[n] += ev[i].elapsed_time(ev[i + 1])
+    step_ms /= args.steps
+    per_op = {}
+    total_bytes = 0
+    for n in names:
+        cfg, nbytes = info[n]
+        us = per_ms[n] / args.steps * 1e3
+        gbs = nbytes / (us * 1e-6) / 1e9
+        per_op[n] = {"config": cfg, "alg_bytes": nbytes, "us": round(us, 3), "GB/s": round(gbs, 1),
+                     "frac_of_peak": round(gbs / PEAK_GBS, 4)}
+        total_bytes += nbytes
+    value = total_bytes / (step_ms * 1e-3) / 1e9
+
+    dom = DOMINANT if DOMINANT in per_op else names[0]
+    roof = {"kernel": dom, "bound": "hbm", "achieved": per_op[dom]["GB/s"], "peak": PEAK_GBS, "unit": "GB/s",
+            "frac": round(per_op[dom]["GB/s"] / PEAK_GBS, 4), "traffic": None,
+            "alg_bytes_per_launch": info[dom][1], "avg_launch_us": per_op[dom]["us"]}
+    traffic_file = ROOT / "profiles" / "traffic.json"
+    if traffic_file.exists():
+        try:
+            t = json.loads(traffic_file.read_text()).get(dom)
+            if t:
+                roof["traffic"] = t["hbm_bytes_per_launch"]
+        except (ValueError, KeyError):
+            pass
+
+    cpu = None
+    if not args.no_cpu and not args.ops:
+        cpu_gbs, cpu_ops = cpu_baseline(host)
+        facts = host_facts()
+        cpu = {"value": round(cpu_gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+               "sample": "C oracle (single-threaded restatement of the reference CPU path) on 1/8 of every "
+                         "op's rows/heads, median of 3, algorithmic bytes / time",
+               "host": facts, "per_op": {k: round(v["GB/s"], 3) for k, v in cpu_ops.items()}}
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded PCG64; BASELINE config shapes and distributions)",
+        "config": {"workload": "all BASELINE configs, one launch of each op per step: " + ", ".join(names),
+                   "buffer_policy": "independent buffers per op, two copies alternating; >=1 GB moved between "
+                                    "two launches of one op (Infinity Cache is 256 MB)",
+                   "wall_s": round(wall, 3)},
+        "per_op": per_op,
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

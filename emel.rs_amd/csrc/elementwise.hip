@@ -46,8 +46,9 @@ EMEL_FN(Abs, false, false, __builtin_fabsf(a))
 EMEL_FN(Neg, false, false, -a)
 EMEL_FN(Tanh, false, false, emel_tanhf(a))
 EMEL_FN(Elu, false, false, a >= 0.0f ? a : emel_expm1f(a))
-// f32::max(x, 0) as glibc fmaxf computes it: x unless x < 0 or NaN.
-EMEL_FN(Relu, false, false, a >= 0.0f ? a : 0.0f)
+// f32::max(x, 0.0) with glibc fmaxf's results: x when x > 0, otherwise +0
+// (NaN -> +0, and -0 -> +0).
+EMEL_FN(Relu, false, false, a > 0.0f ? a : 0.0f)
 EMEL_FN(Sigmoid, true, false, 1.0f / (1.0f + emel_expf(-a, t)))
 EMEL_FN(Gelu, false, false, emel_gelu(a))
 EMEL_FN(Silu, true, false, emel_silu(a, t))

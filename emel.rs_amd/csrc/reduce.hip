@@ -211,6 +211,11 @@ __global__ __launch_bounds__(kBlock) void k_reduce(RedGeo g, const float *x, voi
 
 constexpr uint32_t kTargetBlocks = 2048; // 8 workgroups per CU on 256 CUs
 constexpr uint64_t kMinChunkCols = 4 * kBlock; // one float4 per thread at least
+// Workspace layout: a fixed block of per-row counters first (every launch
+// leaves the counters it used at zero, whatever its shape), then the
+// partials.  Rows are split only when there are fewer than kTargetBlocks of
+// them, so kTargetBlocks counters always suffice.
+constexpr uint64_t kCounterBytes = kTargetBlocks * sizeof(uint32_t);
 
 bool plan(const RedArgs &a, RedGeo &g)
 {
@@ -263,6 +268,10 @@ bool plan(const RedArgs &a, RedGeo &g)
     chunk = (chunk + 3) & ~uint64_t{3};
     uint64_t chunks = (g.ncols + chunk - 1) / chunk;
     if (chunks == 0) chunks = 1;
+    if (chunks > 1 && g.rows > kTargetBlocks) { // cannot happen with the sizing above; keep the bound explicit
+        chunks = 1;
+        chunk = g.ncols;
+    }
     if (static_cast<uint64_t>(g.rows) * chunks > 0x7fffffffull) return false;
     g.chunks = static_cast<uint32_t>(chunks);
     g.chunk_cols = chunk;
@@ -275,8 +284,7 @@ uint64_t reduce_workspace_bytes(const RedArgs &a)
 {
     RedGeo g;
     if (!plan(a, g) || g.chunks == 1) return 0;
-    const uint64_t parts = static_cast<uint64_t>(g.rows) * g.chunks * sizeof(uint64_t);
-    return ((parts + 255) & ~uint64_t{255}) + static_cast<uint64_t>(g.rows) * sizeof(uint32_t);
+    return kCounterBytes + static_cast<uint64_t>(g.rows) * g.chunks * sizeof(uint64_t);
 }
 
 hipError_t launch_reduce(const RedArgs &a, hipStream_t s)
@@ -287,10 +295,9 @@ hipError_t launch_reduce(const RedArgs &a, hipStream_t s)
     uint64_t *part = nullptr;
     uint32_t *counters = nullptr;
     if (g.chunks > 1) {
-        const uint64_t parts = static_cast<uint64_t>(g.rows) * g.chunks * sizeof(uint64_t);
-        part = static_cast<uint64_t *>(a.workspace);
-        counters = reinterpret_cast<uint32_t *>(static_cast<char *>(a.workspace) + ((parts + 255) & ~uint64_t{255}));
-        if (!part) return hipErrorInvalidValue;
+        if (!a.workspace) return hipErrorInvalidValue;
+        counters = static_cast<uint32_t *>(a.workspace);
+        part = reinterpret_cast<uint64_t *>(static_cast<char *>(a.workspace) + kCounterBytes);
     }
     const dim3 grid(g.rows * g.chunks);
     switch (a.op) {

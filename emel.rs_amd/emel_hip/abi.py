@@ -118,12 +118,25 @@ SIGNATURES = {
 _lib = None
 
 
+def _share_torch_hip_runtime() -> None:
+    """A process must hold one HIP runtime.  torch's libtorch_hip.so loads its
+    bundled libamdhip64.so by file name; libemel_hip.so asks for the soname
+    libamdhip64.so.7, which the bundled runtime also carries.  Importing torch
+    first makes libemel_hip.so bind to torch's runtime, so both see the same
+    devices and memory.  (Without torch, the system ROCm runtime is used.)"""
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+
+
 def load() -> ctypes.CDLL:
     """Loads libemel_hip.so (raises if it has not been built)."""
     global _lib
     if _lib is None:
         if not LIB_PATH.exists():
             raise RuntimeError(f"{LIB_PATH} is missing: run __graft_entry__.build() first")
+        _share_torch_hip_runtime()
         lib = ctypes.CDLL(str(LIB_PATH))
         for name, argtypes in SIGNATURES.items():
             fn = getattr(lib, name)

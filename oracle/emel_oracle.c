@@ -274,7 +274,7 @@ static float apply_unary(int subop, float x)
     case SUB_NEG: return -x;
     case SUB_TANH: return tanhf(x);
     case SUB_ELU: return x >= 0.0f ? x : expm1f(x);
-    case SUB_RELU: return fmaxf(x, 0.0f); /* f32::max: NaN -> the other operand */
+    case SUB_RELU: return fmaxf(x, 0.0f); /* f32::max: NaN -> 0; the sign of max(-0, +0) is unpinned by the reference, glibc gives +0 */
     case SUB_SIGMOID: return 1.0f / (1.0f + expf(-x));
     case SUB_GELU: return orc_gelu(x);
     case SUB_SILU: return orc_silu(x);
