@@ -217,9 +217,9 @@ emel_status ensure_device()
     return EMEL_OK;
 }
 
-// Per-(device, stream) scratch for the split-row reductions.  Calls on one
-// stream run in order, so they can share one buffer; different streams get
-// different buffers.
+// Per-(device, stream) scratch for the split-row reductions' partials.
+// Calls on one stream run in order, so they can share one buffer; different
+// streams get different buffers.
 struct Workspace {
     void *ptr = nullptr;
     uint64_t bytes = 0;
@@ -246,8 +246,6 @@ emel_status workspace_for(hipStream_t stream, uint64_t bytes, void **out)
         const uint64_t size = bytes < (uint64_t{1} << 20) ? (uint64_t{1} << 20) : bytes;
         e = hipMalloc(&w.ptr, size);
         if (e != hipSuccess) return hip_fail(e, "hipMalloc(workspace)");
-        e = hipMemset(w.ptr, 0, size); // counters start at zero; kernels leave them zero
-        if (e != hipSuccess) return hip_fail(e, "hipMemset(workspace)");
         w.bytes = size;
     }
     *out = w.ptr;

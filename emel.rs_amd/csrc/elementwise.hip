@@ -16,12 +16,52 @@
 //              multiply-high division;
 //   k_ordinal  anything else: one element per thread, the reference's
 //              per-element ordinal decode.
+#include <cstdlib>
+#include <mutex>
+#include <set>
+
 #include "common.hpp"
 #include "launch.hpp"
 #include "libm_replica.hpp"
 
 namespace emel {
 namespace {
+
+// GELU's result depends only on the fp16 rounding q of its input when
+// |x| < 10 (GeluFormula, unary.rs:522-541), so the 65536 possible results
+// are computed once per device by the same replica code and looked up.
+// Index: fp16 bits of x; entry: fp16 bits of the result.
+__device__ uint16_t g_gelu_lut[65536];
+
+__global__ __launch_bounds__(kBlock) void k_gelu_table()
+{
+    const uint32_t h = blockIdx.x * kBlock + threadIdx.x;
+    if (h < 65536u) g_gelu_lut[h] = emel_gelu_core_fp16(emel_fp16_to_f32(static_cast<uint16_t>(h)));
+}
+
+__device__ __forceinline__ float gelu_lut(float a)
+{
+    if (a <= -10.0f) return 0.0f;
+    if (a >= 10.0f) return a;
+    return hw_fp16_to_f32(g_gelu_lut[hw_fp32_to_fp16(a)]);
+}
+
+// Builds the table on the current device the first time a GELU runs there.
+hipError_t ensure_gelu_table(hipStream_t stream)
+{
+    static std::mutex mu;
+    static std::set<int> ready;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lock(mu);
+    if (ready.count(dev)) return hipSuccess;
+    k_gelu_table<<<dim3(65536 / kBlock), kBlock, 0, stream>>>();
+    e = hipGetLastError();
+    if (e == hipSuccess) e = hipStreamSynchronize(stream); // visible to every stream from now on
+    if (e == hipSuccess) ready.insert(dev);
+    return e;
+}
 
 // ---- per-element formulas ------------------------------------------------
 
@@ -50,7 +90,7 @@ EMEL_FN(Elu, false, false, a >= 0.0f ? a : emel_expm1f(a))
 // (NaN -> +0, and -0 -> +0).
 EMEL_FN(Relu, false, false, a > 0.0f ? a : 0.0f)
 EMEL_FN(Sigmoid, true, false, 1.0f / (1.0f + emel_expf(-a, t)))
-EMEL_FN(Gelu, false, false, emel_gelu(a))
+EMEL_FN(Gelu, false, false, gelu_lut(a))
 EMEL_FN(Silu, true, false, emel_silu(a, t))
 EMEL_FN(Exp, true, false, emel_expf(a, t))
 EMEL_FN(Scale, false, false, a * s)
@@ -292,6 +332,10 @@ hipError_t launch_op(const EwArgs &x, hipStream_t stream)
     float *o = static_cast<float *>(x.o.data);
     const uint64_t n = x.count;
     if (n == 0) return hipSuccess;
+    if constexpr (OP == Ew::Gelu) {
+        const hipError_t e = ensure_gelu_table(stream);
+        if (e != hipSuccess) return e;
+    }
 
     // Linear pairing holds when each source is dense and either addressed by
     // ordinal or shaped like the destination.

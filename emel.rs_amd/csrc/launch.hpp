@@ -77,8 +77,8 @@ struct RedArgs {
     void *workspace;  // per-stream scratch, see reduce_workspace_bytes
 };
 
-// Bytes of scratch the reduction needs; the scratch's counter words must be
-// zero before the first launch (each launch leaves them zero again).
+// Bytes of scratch the reduction needs for its per-chunk partials (0 when
+// every row is reduced by a single workgroup).
 uint64_t reduce_workspace_bytes(const RedArgs &args);
 hipError_t launch_reduce(const RedArgs &args, hipStream_t stream);
 

@@ -83,6 +83,50 @@ __host__ __device__ __forceinline__ float emel_expf(float x, const uint64_t *tab
     return static_cast<float>(y);
 }
 
+// expf for arguments that are <= 0 or NaN (soft_max's x - max): the same
+// bits as emel_expf, with the special cases folded into one select, since
+// only the underflow (and -inf) case can occur.
+__host__ __device__ __forceinline__ float emel_expf_nonpos(float x, const uint64_t *tab)
+{
+    constexpr double kInvLn2N = 0x1.71547652b82fep+0 * 32.0;
+    constexpr double kShift = 0x1.8p+52;
+    constexpr double kC0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+    constexpr double kC1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+    constexpr double kC2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+    const double xd = static_cast<double>(x);
+    double kd = __builtin_fma(kInvLn2N, xd, kShift);
+    const uint64_t ki = f64_to_bits(kd);
+    kd -= kShift;
+    const double r = __builtin_fma(kInvLn2N, xd, -kd);
+    const double s = bits_to_f64(tab[ki & 31u] + (ki << 47));
+    const double z = __builtin_fma(kC0, r, kC1);
+    const double r2 = r * r;
+    double y = __builtin_fma(kC2, r, 1.0);
+    y = __builtin_fma(z, r2, y);
+    y = y * s;
+    // x < log(2^-150) (including -inf): 0, as emel_expf returns
+    return x < -0x1.9fe368p6f ? 0.0f : static_cast<float>(y);
+}
+
+// Correctly rounded f32 quotient a / b through a double reciprocal:
+// RN24(RN53(a * RN53(1/b))) == RN24(a / b) for finite a and normal b >= 1
+// (no over/underflow of the intermediate).  Proof: the double product is
+// a/b * (1 + e) with |e| < 2^-51.9.  RN24 of it can differ from RN24(a/b)
+// only if a rounding midpoint m lies within that distance of a/b.  For
+// m = M * 2^k with M an odd 25-bit integer and a, b carrying 24-bit
+// significands A, B, a - b*m is a non-zero multiple of 2^(k + exponent of
+// b) whenever b is not a power of two (a/b is then never a midpoint), so
+// |a/b - m| > 2^-49 * m; for subnormal results the grid is 2^-150 and
+// |a/b - m| > 2^-174 while the error is below 2^-177.  If b is a power of
+// two the reciprocal and the product are exact.  NaN and infinite b
+// propagate as in a / b.  soft_max divides every element of a row by the
+// same row sum b >= 1, so one double reciprocal per row replaces the
+// iterative f32 division per element.
+__host__ __device__ __forceinline__ float div_by_recip(float a, double recip_b)
+{
+    return static_cast<float>(static_cast<double>(a) * recip_b);
+}
+
 // expm1f, fdlibm float version.
 __host__ __device__ __forceinline__ float emel_expm1f(float x)
 {
@@ -211,6 +255,29 @@ __host__ __device__ __forceinline__ float emel_fp16_to_f32(uint16_t h)
     return bits_to_f32(sign | f32_to_bits(doubled < (1u << 27) ? denormalized : normalized));
 }
 
+// binary16 bits -> fp32 and fp32 -> binary16 bits with the hardware
+// conversions (v_cvt_f32_f16 / v_cvt_f16_f32: exact widening and IEEE
+// round-to-nearest-even with f16 denormals, the same results as the
+// software helpers above over all inputs except NaN payloads; checked
+// exhaustively on the GPU by the test suite).
+__device__ __forceinline__ float hw_fp16_to_f32(uint16_t h)
+{
+    return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+__device__ __forceinline__ uint16_t hw_fp32_to_fp16(float x)
+{
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+}
+
+// GELU's tanh approximation for an already fp16-rounded input q, rounded
+// to fp16 bits (the inner part of GeluFormula, unary.rs:531-539).
+__host__ __device__ __forceinline__ uint16_t emel_gelu_core_fp16(float q)
+{
+    const float inner = 0.7978846f * (q + 0.044715f * q * q * q);
+    const float approximation = 0.5f * q * (1.0f + emel_tanhf(inner));
+    return emel_fp32_to_fp16(approximation);
+}
+
 // SiluFormula (unary.rs:595-600).
 __host__ __device__ __forceinline__ float emel_silu(float x, const uint64_t *tab)
 {
@@ -224,9 +291,7 @@ __host__ __device__ __forceinline__ float emel_gelu(float value)
     if (value <= -10.0f) return 0.0f;
     if (value >= 10.0f) return value;
     const float q = emel_fp16_to_f32(emel_fp32_to_fp16(value));
-    const float inner = 0.7978846f * (q + 0.044715f * q * q * q);
-    const float approximation = 0.5f * q * (1.0f + emel_tanhf(inner));
-    return emel_fp16_to_f32(emel_fp32_to_fp16(approximation));
+    return emel_fp16_to_f32(emel_gelu_core_fp16(q));
 }
 
 } // namespace emel

@@ -4,15 +4,19 @@
 //
 // Long rows (the 151,936-wide logits rows) are split into `chunks` column
 // ranges, one workgroup each, so the grid fills all 256 CUs.  Each
-// workgroup reduces its range (f64 sums; (value, index) maxima), writes one
-// partial, and the last workgroup of the row to finish (an agent-scope
-// counter) combines the partials in a fixed order and resets the counter.
-// Results are therefore deterministic run to run.
+// workgroup reduces its range (f64 sums; (value, index) maxima) and writes
+// one partial; a second kernel with one wave per row combines the row's
+// partials in a fixed tree order.  The kernel boundary makes the partials
+// visible across XCDs without in-kernel fences (an agent-scope fence costs
+// an L2 write-back and invalidate per workgroup on gfx950).  Results are
+// deterministic run to run.
 //
 // argmax keeps the reference's sequential strict-> scan semantics: the
 // winner is the lowest index among the maximal non-NaN values, NaNs never
 // win, and a NaN in column 0 makes the result 0 (nothing compares greater
 // than the initial NaN).
+#include <type_traits>
+
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -92,23 +96,13 @@ __device__ __forceinline__ void accumulate(const RedGeo &g, const float *x, int6
     }
 }
 
+// Writes the row result from its combined (sum | (value, index)) word.
 template <RedOp OP>
-__global__ __launch_bounds__(kBlock) void k_reduce(RedGeo g, const float *x, void *dst, uint64_t *part,
-                                                    uint32_t *counters)
+__device__ __forceinline__ void write_result(const RedGeo &g, const float *x, void *dst, uint32_t row, uint64_t packed)
 {
     constexpr bool kArg = Acc<OP>::kArg;
-    __shared__ double s_sum[kBlock / kWave];
-    __shared__ float s_v[kBlock / kWave];
-    __shared__ uint32_t s_i[kBlock / kWave];
-    __shared__ uint32_t s_last;
-
-    const uint32_t row = blockIdx.x / g.chunks;
-    const uint32_t chunk = blockIdx.x - row * g.chunks;
-    const uint32_t wave = threadIdx.x / kWave;
-    const uint32_t lane = threadIdx.x % kWave;
-
-    int64_t base = 0;
     uint32_t i1 = 0, i2 = 0, i3 = 0;
+    int64_t base = 0;
     if (g.mode != kModeOrdinal) {
         const uint32_t t = g.ne1.div(row);
         i1 = row - t * g.ne1.d;
@@ -117,81 +111,6 @@ __global__ __launch_bounds__(kBlock) void k_reduce(RedGeo g, const float *x, voi
         base = static_cast<int64_t>(i1) * g.x_st[1] + static_cast<int64_t>(i2) * g.x_st[2] +
                static_cast<int64_t>(i3) * g.x_st[3];
     }
-    const uint64_t c0 = static_cast<uint64_t>(chunk) * g.chunk_cols;
-    const uint64_t c1 = c0 + g.chunk_cols < g.ncols ? c0 + g.chunk_cols : g.ncols;
-
-    double sum = 0.0;
-    float bv = -__builtin_inff();
-    uint32_t bi = 0xffffffffu; // "no candidate": loses every tie on index
-    accumulate<OP>(g, x, base, c0, c1, sum, bv, bi);
-
-    // block reduction: waves, then wave 0 over the wave results
-    if constexpr (kArg) {
-        wave_argmax(bv, bi);
-        if (lane == 0) {
-            s_v[wave] = bv;
-            s_i[wave] = bi;
-        }
-    } else {
-        sum = wave_sum(sum);
-        if (lane == 0) s_sum[wave] = sum;
-    }
-    __syncthreads();
-
-    uint64_t packed = 0;
-    if (threadIdx.x == 0) {
-        if constexpr (kArg) {
-            for (int w = 1; w < kBlock / kWave; ++w) argmax_merge(s_v[0], s_i[0], s_v[w], s_i[w]);
-            const ArgPart p{s_v[0], s_i[0]};
-            packed = __builtin_bit_cast(uint64_t, p);
-        } else {
-            double t = s_sum[0];
-            for (int w = 1; w < kBlock / kWave; ++w) t += s_sum[w];
-            packed = __builtin_bit_cast(uint64_t, t);
-        }
-    }
-
-    bool finish = g.chunks == 1;
-    if (!finish) {
-        if (threadIdx.x == 0) {
-            __hip_atomic_store(&part[blockIdx.x], packed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __threadfence(); // release the partial before counting this chunk
-            const uint32_t prev =
-                __hip_atomic_fetch_add(&counters[row], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-            s_last = prev == g.chunks - 1 ? 1u : 0u;
-        }
-        __syncthreads();
-        finish = s_last != 0;
-        if (!finish) return;
-        __threadfence(); // acquire the other chunks' partials
-        if (wave != 0) return;
-        // wave 0 combines the row's partials; lane l takes chunks l, l+64, ...
-        double tsum = 0.0;
-        float tv = -__builtin_inff();
-        uint32_t ti = 0xffffffffu;
-        for (uint32_t c = lane; c < g.chunks; c += kWave) {
-            const uint64_t q = __hip_atomic_load(&part[row * g.chunks + c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if constexpr (kArg) {
-                const ArgPart p = __builtin_bit_cast(ArgPart, q);
-                argmax_merge(tv, ti, p.v, p.i);
-            } else {
-                tsum += __builtin_bit_cast(double, q);
-            }
-        }
-        if constexpr (kArg) {
-            wave_argmax(tv, ti);
-            packed = __builtin_bit_cast(uint64_t, ArgPart{tv, ti});
-        } else {
-            tsum = wave_sum(tsum);
-            packed = __builtin_bit_cast(uint64_t, tsum);
-        }
-        if (lane != 0) return;
-        __hip_atomic_store(&counters[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); // ready for reuse
-    } else if (threadIdx.x != 0) {
-        return;
-    }
-
-    // one thread writes the row result
     const int64_t doff = static_cast<int64_t>(i1) * g.d_st[1] + static_cast<int64_t>(i2) * g.d_st[2] +
                          static_cast<int64_t>(i3) * g.d_st[3];
     if constexpr (kArg) {
@@ -204,18 +123,104 @@ __global__ __launch_bounds__(kBlock) void k_reduce(RedGeo g, const float *x, voi
         else static_cast<float *>(dst)[doff] = fidx;
     } else {
         const double t = __builtin_bit_cast(double, packed);
-        if constexpr (OP == RedOp::Mean) static_cast<float *>(dst)[doff] = static_cast<float>(t / static_cast<double>(g.ncols));
-        else static_cast<float *>(dst)[doff] = static_cast<float>(t);
+        if constexpr (OP == RedOp::Mean)
+            static_cast<float *>(dst)[doff] = static_cast<float>(t / static_cast<double>(g.ncols));
+        else
+            static_cast<float *>(dst)[doff] = static_cast<float>(t);
     }
+}
+
+// Pass 1: workgroup (row, chunk) reduces its column range.  With one chunk
+// per row it writes the result; otherwise it writes its partial word.
+template <RedOp OP>
+__global__ __launch_bounds__(kBlock) void k_reduce(RedGeo g, const float *x, void *dst, uint64_t *part)
+{
+    constexpr bool kArg = Acc<OP>::kArg;
+    __shared__ double s_sum[kBlock / kWave];
+    __shared__ float s_v[kBlock / kWave];
+    __shared__ uint32_t s_i[kBlock / kWave];
+
+    const uint32_t row = blockIdx.x / g.chunks;
+    const uint32_t chunk = blockIdx.x - row * g.chunks;
+    const uint32_t wave = threadIdx.x / kWave;
+    const uint32_t lane = threadIdx.x % kWave;
+
+    int64_t base = 0;
+    if (g.mode != kModeOrdinal) {
+        const uint32_t t = g.ne1.div(row);
+        const uint32_t i1 = row - t * g.ne1.d;
+        const uint32_t i3 = g.ne2.div(t);
+        const uint32_t i2 = t - i3 * g.ne2.d;
+        base = static_cast<int64_t>(i1) * g.x_st[1] + static_cast<int64_t>(i2) * g.x_st[2] +
+               static_cast<int64_t>(i3) * g.x_st[3];
+    }
+    const uint64_t c0 = static_cast<uint64_t>(chunk) * g.chunk_cols;
+    const uint64_t c1 = c0 + g.chunk_cols < g.ncols ? c0 + g.chunk_cols : g.ncols;
+
+    double sum = 0.0;
+    float bv = -__builtin_inff();
+    uint32_t bi = 0xffffffffu; // "no candidate": loses every tie on index
+    accumulate<OP>(g, x, base, c0, c1, sum, bv, bi);
+
+    if constexpr (kArg) {
+        wave_argmax(bv, bi);
+        if (lane == 0) {
+            s_v[wave] = bv;
+            s_i[wave] = bi;
+        }
+    } else {
+        sum = wave_sum(sum);
+        if (lane == 0) s_sum[wave] = sum;
+    }
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    uint64_t packed;
+    if constexpr (kArg) {
+        for (int w = 1; w < kBlock / kWave; ++w) argmax_merge(s_v[0], s_i[0], s_v[w], s_i[w]);
+        packed = __builtin_bit_cast(uint64_t, ArgPart{s_v[0], s_i[0]});
+    } else {
+        double t = s_sum[0];
+        for (int w = 1; w < kBlock / kWave; ++w) t += s_sum[w];
+        packed = __builtin_bit_cast(uint64_t, t);
+    }
+    if (g.chunks == 1) write_result<OP>(g, x, dst, row, packed);
+    else part[blockIdx.x] = packed;
+}
+
+// Pass 2: one wave per row combines the row's partials (lane l takes
+// chunks l, l+64, ...; then a fixed butterfly) and writes the result.
+template <RedOp OP>
+__global__ __launch_bounds__(kBlock) void k_reduce_finish(RedGeo g, const float *x, void *dst, const uint64_t *part)
+{
+    constexpr bool kArg = Acc<OP>::kArg;
+    const uint32_t row = blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave;
+    const uint32_t lane = threadIdx.x % kWave;
+    if (row >= g.rows) return;
+    double tsum = 0.0;
+    float tv = -__builtin_inff();
+    uint32_t ti = 0xffffffffu;
+    for (uint32_t c = lane; c < g.chunks; c += kWave) {
+        const uint64_t q = part[static_cast<uint64_t>(row) * g.chunks + c];
+        if constexpr (kArg) {
+            const ArgPart p = __builtin_bit_cast(ArgPart, q);
+            argmax_merge(tv, ti, p.v, p.i);
+        } else {
+            tsum += __builtin_bit_cast(double, q);
+        }
+    }
+    uint64_t packed;
+    if constexpr (kArg) {
+        wave_argmax(tv, ti);
+        packed = __builtin_bit_cast(uint64_t, ArgPart{tv, ti});
+    } else {
+        tsum = wave_sum(tsum);
+        packed = __builtin_bit_cast(uint64_t, tsum);
+    }
+    if (lane == 0) write_result<OP>(g, x, dst, row, packed);
 }
 
 constexpr uint32_t kTargetBlocks = 2048; // 8 workgroups per CU on 256 CUs
 constexpr uint64_t kMinChunkCols = 4 * kBlock; // one float4 per thread at least
-// Workspace layout: a fixed block of per-row counters first (every launch
-// leaves the counters it used at zero, whatever its shape), then the
-// partials.  Rows are split only when there are fewer than kTargetBlocks of
-// them, so kTargetBlocks counters always suffice.
-constexpr uint64_t kCounterBytes = kTargetBlocks * sizeof(uint32_t);
 
 bool plan(const RedArgs &a, RedGeo &g)
 {
@@ -268,10 +273,6 @@ bool plan(const RedArgs &a, RedGeo &g)
     chunk = (chunk + 3) & ~uint64_t{3};
     uint64_t chunks = (g.ncols + chunk - 1) / chunk;
     if (chunks == 0) chunks = 1;
-    if (chunks > 1 && g.rows > kTargetBlocks) { // cannot happen with the sizing above; keep the bound explicit
-        chunks = 1;
-        chunk = g.ncols;
-    }
     if (static_cast<uint64_t>(g.rows) * chunks > 0x7fffffffull) return false;
     g.chunks = static_cast<uint32_t>(chunks);
     g.chunk_cols = chunk;
@@ -284,7 +285,7 @@ uint64_t reduce_workspace_bytes(const RedArgs &a)
 {
     RedGeo g;
     if (!plan(a, g) || g.chunks == 1) return 0;
-    return kCounterBytes + static_cast<uint64_t>(g.rows) * g.chunks * sizeof(uint64_t);
+    return static_cast<uint64_t>(g.rows) * g.chunks * sizeof(uint64_t);
 }
 
 hipError_t launch_reduce(const RedArgs &a, hipStream_t s)
@@ -292,20 +293,21 @@ hipError_t launch_reduce(const RedArgs &a, hipStream_t s)
     RedGeo g;
     if (!plan(a, g)) return hipErrorInvalidValue;
     const float *x = static_cast<const float *>(a.x.data);
-    uint64_t *part = nullptr;
-    uint32_t *counters = nullptr;
-    if (g.chunks > 1) {
-        if (!a.workspace) return hipErrorInvalidValue;
-        counters = static_cast<uint32_t *>(a.workspace);
-        part = reinterpret_cast<uint64_t *>(static_cast<char *>(a.workspace) + kCounterBytes);
-    }
+    uint64_t *part = static_cast<uint64_t *>(a.workspace);
+    if (g.chunks > 1 && !part) return hipErrorInvalidValue;
     const dim3 grid(g.rows * g.chunks);
+    const dim3 fgrid((g.rows + (kBlock / kWave) - 1) / (kBlock / kWave));
+    auto run = [&](auto op_tag) {
+        constexpr RedOp OP = decltype(op_tag)::value;
+        k_reduce<OP><<<grid, kBlock, 0, s>>>(g, x, a.dst, part);
+        if (g.chunks > 1) k_reduce_finish<OP><<<fgrid, kBlock, 0, s>>>(g, x, a.dst, part);
+    };
     switch (a.op) {
-    case RedOp::SumRows: k_reduce<RedOp::SumRows><<<grid, kBlock, 0, s>>>(g, x, a.dst, part, counters); break;
-    case RedOp::ArgmaxRows: k_reduce<RedOp::ArgmaxRows><<<grid, kBlock, 0, s>>>(g, x, a.dst, part, counters); break;
-    case RedOp::Sum: k_reduce<RedOp::Sum><<<grid, kBlock, 0, s>>>(g, x, a.dst, part, counters); break;
-    case RedOp::Mean: k_reduce<RedOp::Mean><<<grid, kBlock, 0, s>>>(g, x, a.dst, part, counters); break;
-    case RedOp::Argmax: k_reduce<RedOp::Argmax><<<grid, kBlock, 0, s>>>(g, x, a.dst, part, counters); break;
+    case RedOp::SumRows: run(std::integral_constant<RedOp, RedOp::SumRows>{}); break;
+    case RedOp::ArgmaxRows: run(std::integral_constant<RedOp, RedOp::ArgmaxRows>{}); break;
+    case RedOp::Sum: run(std::integral_constant<RedOp, RedOp::Sum>{}); break;
+    case RedOp::Mean: run(std::integral_constant<RedOp, RedOp::Mean>{}); break;
+    case RedOp::Argmax: run(std::integral_constant<RedOp, RedOp::Argmax>{}); break;
     }
     return hipGetLastError();
 }

@@ -47,13 +47,15 @@ __device__ __forceinline__ int64_t row_base(const int64_t *st, uint32_t i1, uint
     return static_cast<int64_t>(i1) * st[1] + static_cast<int64_t>(i2) * st[2] + static_cast<int64_t>(i3) * st[3];
 }
 
+// Four f16 mask values widened to f32 (fp16_to_f32, quant.rs:287-300; the
+// hardware widening is exact and gives the same values).
 __device__ __forceinline__ float4 mask4(const uint16_t *m)
 {
     const uint2 raw = *reinterpret_cast<const uint2 *>(m);
-    return make_float4(emel_fp16_to_f32(static_cast<uint16_t>(raw.x & 0xffffu)),
-                       emel_fp16_to_f32(static_cast<uint16_t>(raw.x >> 16)),
-                       emel_fp16_to_f32(static_cast<uint16_t>(raw.y & 0xffffu)),
-                       emel_fp16_to_f32(static_cast<uint16_t>(raw.y >> 16)));
+    return make_float4(hw_fp16_to_f32(static_cast<uint16_t>(raw.x & 0xffffu)),
+                       hw_fp16_to_f32(static_cast<uint16_t>(raw.x >> 16)),
+                       hw_fp16_to_f32(static_cast<uint16_t>(raw.y & 0xffffu)),
+                       hw_fp16_to_f32(static_cast<uint16_t>(raw.y >> 16)));
 }
 
 // f32 products rounded, then accumulated in f64 (run_rms_norm).
@@ -84,10 +86,17 @@ __device__ __forceinline__ float4 add4(float4 v, float4 w)
     return make_float4(v.x + w.x, v.y + w.y, v.z + w.z, v.w + w.w);
 }
 __device__ __forceinline__ float4 sub4(float4 v, float k) { return make_float4(v.x - k, v.y - k, v.z - k, v.w - k); }
-__device__ __forceinline__ float4 div4(float4 v, float k) { return make_float4(v.x / k, v.y / k, v.z / k, v.w / k); }
+// v / den for a row sum den >= 1, via the row's double reciprocal.
+__device__ __forceinline__ float4 div4(float4 v, double recip)
+{
+    return make_float4(div_by_recip(v.x, recip), div_by_recip(v.y, recip), div_by_recip(v.z, recip),
+                       div_by_recip(v.w, recip));
+}
+// exp(v - max): arguments are <= 0 or NaN.
 __device__ __forceinline__ float4 exp4(float4 v, const uint64_t *t)
 {
-    return make_float4(emel_expf(v.x, t), emel_expf(v.y, t), emel_expf(v.z, t), emel_expf(v.w, t));
+    return make_float4(emel_expf_nonpos(v.x, t), emel_expf_nonpos(v.y, t), emel_expf_nonpos(v.z, t),
+                       emel_expf_nonpos(v.w, t));
 }
 
 // ---- vectorized rows: contiguous dim 0, ncols % 4 == 0 ------------------
@@ -204,11 +213,11 @@ __global__ __launch_bounds__(kBlock) void k_row_vec(RowGeo g, const float *x, fl
                 }
             }
             acc = wave_sum(acc);
-            const float den = static_cast<float>(acc);
+            const double recip = 1.0 / static_cast<double>(static_cast<float>(acc));
 #pragma unroll
             for (int j = 0; j < NV; ++j) {
                 const uint32_t idx = lane + j * kWave;
-                if (idx < nv) yr[idx] = div4(v[j], den);
+                if (idx < nv) yr[idx] = div4(v[j], recip);
             }
         }
     } else {
@@ -250,8 +259,8 @@ __global__ __launch_bounds__(kBlock) void k_row_vec(RowGeo g, const float *x, fl
                 acc += sum4(e);
             }
             acc = wave_sum(acc);
-            const float den = static_cast<float>(acc);
-            for (uint32_t idx = lane; idx < nv; idx += kWave) yr[idx] = div4(yr[idx], den);
+            const double recip = 1.0 / static_cast<double>(static_cast<float>(acc));
+            for (uint32_t idx = lane; idx < nv; idx += kWave) yr[idx] = div4(yr[idx], recip);
         }
     }
 }
@@ -344,7 +353,7 @@ __global__ __launch_bounds__(kBlock) void k_softmax_generic(OrdView xv, OrdView 
         float v = x[ord_index(xv, base + c)];
         if constexpr (kExt) {
             v = v * scale;
-            if (mr) v = v + emel_fp16_to_f32(mr[c]);
+            if (mr) v = v + hw_fp16_to_f32(mr[c]);
         }
         return v;
     };
@@ -353,15 +362,15 @@ __global__ __launch_bounds__(kBlock) void k_softmax_generic(OrdView xv, OrdView 
     mx = wave_max(mx);
     double acc = 0.0;
     for (uint64_t c = lane; c < ncols; c += kWave) {
-        const float e = emel_expf(load(c) - mx, lds);
+        const float e = emel_expf_nonpos(load(c) - mx, lds);
         y[ord_index(yv, base + c)] = e;
         acc += static_cast<double>(e);
     }
     acc = wave_sum(acc);
-    const float den = static_cast<float>(acc);
+    const double recip = 1.0 / static_cast<double>(static_cast<float>(acc));
     for (uint64_t c = lane; c < ncols; c += kWave) {
         const int64_t o = ord_index(yv, base + c);
-        y[o] = y[o] / den;
+        y[o] = div_by_recip(y[o], recip);
     }
 }
 
@@ -383,13 +392,14 @@ __global__ __launch_bounds__(kBlock) void k_softmax_seq(OrdView xv, OrdView yv, 
     }
     float sum = 0.0f;
     for (uint64_t c = 0; c < ncols; ++c) {
-        const float e = emel_expf(x[ord_index(xv, base + c)] - mx, lds);
+        const float e = emel_expf_nonpos(x[ord_index(xv, base + c)] - mx, lds);
         y[ord_index(yv, base + c)] = e;
         sum += e;
     }
+    const double recip = 1.0 / static_cast<double>(sum);
     for (uint64_t c = 0; c < ncols; ++c) {
         const int64_t o = ord_index(yv, base + c);
-        y[o] = y[o] / sum;
+        y[o] = div_by_recip(y[o], recip);
     }
 }
 

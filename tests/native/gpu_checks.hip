@@ -1,0 +1,91 @@
+// gpu_checks.hip -- test helper (built by __graft_entry__.build()).
+//
+// Exhaustive GPU checks of the device-side shortcuts the kernels take,
+// against the reference-restating code they replace:
+//   hw_fp32_to_fp16 vs emel_fp32_to_fp16  (all 2^32 f32 inputs)
+//   hw_fp16_to_f32  vs emel_fp16_to_f32   (all 65536 f16 inputs)
+//   emel_expf_nonpos vs emel_expf         (all f32 <= 0, and NaNs)
+// NaN results match NaN results.  Each entry point launches a grid-stride
+// kernel over the range on the null stream, waits, and returns the number
+// of mismatching inputs (or UINT64_MAX on a HIP error).
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "libm_replica.hpp"
+
+namespace {
+
+__device__ unsigned long long g_bad;
+
+__device__ __forceinline__ bool nan16(uint16_t h) { return (h & 0x7c00u) == 0x7c00u && (h & 0x03ffu) != 0; }
+
+__global__ void k_f32_to_f16(uint64_t lo, uint64_t hi)
+{
+    unsigned long long bad = 0;
+    for (uint64_t u = lo + blockIdx.x * 256ull + threadIdx.x; u < hi; u += 256ull * gridDim.x) {
+        const float x = emel::bits_to_f32(static_cast<uint32_t>(u));
+        const uint16_t a = emel::hw_fp32_to_fp16(x);
+        const uint16_t b = emel::emel_fp32_to_fp16(x);
+        if (a != b && !(nan16(a) && nan16(b))) ++bad;
+    }
+    if (bad) atomicAdd(&g_bad, bad);
+}
+
+__global__ void k_f16_to_f32()
+{
+    const uint32_t h = blockIdx.x * 256u + threadIdx.x;
+    if (h >= 65536u) return;
+    const float a = emel::hw_fp16_to_f32(static_cast<uint16_t>(h));
+    const float b = emel::emel_fp16_to_f32(static_cast<uint16_t>(h));
+    if (emel::f32_to_bits(a) != emel::f32_to_bits(b) && !(a != a && b != b)) atomicAdd(&g_bad, 1ull);
+}
+
+__global__ void k_expf_nonpos(uint64_t lo, uint64_t hi)
+{
+    __shared__ uint64_t tab[32];
+    if (threadIdx.x < 32) tab[threadIdx.x] = emel::kExp2Table[threadIdx.x];
+    __syncthreads();
+    unsigned long long bad = 0;
+    for (uint64_t u = lo + blockIdx.x * 256ull + threadIdx.x; u < hi; u += 256ull * gridDim.x) {
+        const float x = emel::bits_to_f32(static_cast<uint32_t>(u));
+        if (!(x <= 0.0f) && x == x) continue; // positive inputs are outside the contract
+        const float a = emel::emel_expf_nonpos(x, tab);
+        const float b = emel::emel_expf(x, tab);
+        if (emel::f32_to_bits(a) != emel::f32_to_bits(b) && !(a != a && b != b)) ++bad;
+    }
+    if (bad) atomicAdd(&g_bad, bad);
+}
+
+template <class Launch>
+uint64_t run(Launch launch)
+{
+    const unsigned long long zero = 0;
+    if (hipMemcpyToSymbol(HIP_SYMBOL(g_bad), &zero, sizeof zero) != hipSuccess) return UINT64_MAX;
+    launch();
+    if (hipGetLastError() != hipSuccess || hipDeviceSynchronize() != hipSuccess) return UINT64_MAX;
+    unsigned long long bad = 0;
+    if (hipMemcpyFromSymbol(&bad, HIP_SYMBOL(g_bad), sizeof bad) != hipSuccess) return UINT64_MAX;
+    return bad;
+}
+
+} // namespace
+
+extern "C" {
+
+uint64_t gpu_check_fp32_to_fp16(void)
+{
+    return run([] { k_f32_to_f16<<<8192, 256>>>(0, 1ull << 32); });
+}
+
+uint64_t gpu_check_fp16_to_f32(void)
+{
+    return run([] { k_f16_to_f32<<<256, 256>>>(); });
+}
+
+uint64_t gpu_check_expf_nonpos(void)
+{
+    return run([] { k_expf_nonpos<<<8192, 256>>>(0, 1ull << 32); });
+}
+
+} // extern "C"

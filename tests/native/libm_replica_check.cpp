@@ -92,6 +92,36 @@ uint64_t check_fp16_to_f32(void)
     });
 }
 
+// div_by_recip(a, 1/b) against IEEE a / b: every a bit pattern in [lo, hi)
+// for each of the nb divisors bs[] (normal, >= 1).
+uint64_t check_div_recip(const float *bs, int nb, uint64_t lo, uint64_t hi, int threads)
+{
+    uint64_t total = 0;
+    for (int i = 0; i < nb; ++i) {
+        const float b = bs[i];
+        const double r = 1.0 / static_cast<double>(b);
+        total += count_range(lo, hi, threads, [b, r](uint32_t u) {
+            const float a = emel::bits_to_f32(u);
+            return differ(emel::div_by_recip(a, r), a / b);
+        });
+    }
+    return total;
+}
+
+// Random pairs: a any f32 bit pattern, b any f32 in [1, 2^64).
+uint64_t check_div_recip_random(uint64_t seed, uint64_t n, int threads)
+{
+    return count_range(0, n, threads, [seed](uint32_t i) {
+        uint64_t z = seed + 0x9e3779b97f4a7c15ull * (static_cast<uint64_t>(i) + 1);
+        z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+        z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+        z ^= z >> 31;
+        const float a = emel::bits_to_f32(static_cast<uint32_t>(z));
+        const float b = emel::bits_to_f32(0x3f800000u + static_cast<uint32_t>((z >> 32) % (64u << 23)));
+        return differ(emel::div_by_recip(a, 1.0 / static_cast<double>(b)), a / b);
+    });
+}
+
 // Scalar values for the golden-vector tests (unary manifest inputs).
 float replica_silu(float x) { return emel::emel_silu(x, emel::kExp2Table); }
 float replica_gelu(float x) { return emel::emel_gelu(x); }

@@ -45,6 +45,27 @@ def test_fp16_widening(chk):
     assert chk.check_fp16_to_f32() == 0
 
 
+def test_division_by_reciprocal_is_correctly_rounded(chk):
+    """soft_max divides a row by its sum b >= 1 as RN24(RN53(a * RN53(1/b)));
+    this must equal IEEE RN24(a / b).  Every a in [0, 1] (all the values a
+    soft_max numerator takes) for divisors chosen to stress the argument
+    (powers of two, all-ones significands, values near 1 and 2^k, random),
+    plus random (a, b) pairs over the whole f32 line."""
+    import numpy as np
+
+    chk.check_div_recip.restype = ctypes.c_uint64
+    chk.check_div_recip.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_int, ctypes.c_uint64, ctypes.c_uint64,
+                                     ctypes.c_int]
+    chk.check_div_recip_random.restype = ctypes.c_uint64
+    chk.check_div_recip_random.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int]
+    g = np.random.Generator(np.random.PCG64(77))
+    bs = np.array([1.0, 3.0, np.float32(2.0) - np.float32(2.0 ** -23), 1.0 + 2.0 ** -23, 4095.999755859375,
+                   np.nextafter(np.float32(1024), np.float32(0))] + list(g.uniform(1, 4096, 2)), dtype=np.float32)
+    one = int(np.float32(1.0).view(np.uint32))
+    assert chk.check_div_recip(bs.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), len(bs), 0, one + 1, THREADS) == 0
+    assert chk.check_div_recip_random(12345, 200_000_000, THREADS) == 0
+
+
 def test_replica_matches_oracle_scalars(chk):
     import numpy as np
 
