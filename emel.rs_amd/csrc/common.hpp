@@ -80,6 +80,21 @@ __device__ __forceinline__ void wave_argmax(float &bv, uint32_t &bi)
     }
 }
 
+// Non-temporal (streaming) 128-bit global accesses, for data that is read
+// once or written once: they keep row streams from displacing cached
+// operands (weight rows, masks, tables) in L2 and the Infinity Cache.
+typedef float v4f __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ld_nt(const float4 *p)
+{
+    const v4f v = __builtin_nontemporal_load(reinterpret_cast<const v4f *>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void st_nt(float4 *p, float4 a)
+{
+    const v4f v = {a.x, a.y, a.z, a.w};
+    __builtin_nontemporal_store(v, reinterpret_cast<v4f *>(p));
+}
+
 // Block index remapped so that consecutive logical blocks run on the same
 // XCD (the dispatcher places block b on XCD b % 8): logical ids
 // [x*per, (x+1)*per) execute on XCD x.  Requires gridDim.x % 8 == 0.

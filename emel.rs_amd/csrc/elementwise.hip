@@ -8,7 +8,8 @@
 // transcendental ones, which stay under the memory time).  Three kernel
 // shapes cover every accepted layout:
 //   k_dense    all operands dense and paired by linear index: 128-bit
-//              loads/stores, VPT float4 per thread, a scalar tail;
+//              non-temporal loads/stores, VPT float4 per thread, a scalar
+//              tail;
 //   k_rowbcast dense [rows, ne0] op dense row [ne0]: 128-bit loads, the
 //              row operand re-read from L2;
 //   k_rows     any strides with a contiguous dim 0 (permuted views, modulo
@@ -139,15 +140,15 @@ __global__ __launch_bounds__(kBlock) void k_dense(const float *a, const float *b
     for (int j = 0; j < VPT; ++j) {
         const uint64_t i = base + static_cast<uint64_t>(j) * kBlock;
         if (i < nvec) {
-            va[j] = a4[i];
-            if constexpr (Fn<OP>::kBinary) vb[j] = b4[i];
+            va[j] = ld_nt(a4 + i);
+            if constexpr (Fn<OP>::kBinary) vb[j] = ld_nt(b4 + i);
             else vb[j] = va[j];
         }
     }
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
         const uint64_t i = base + static_cast<uint64_t>(j) * kBlock;
-        if (i < nvec) o4[i] = apply4<OP>(va[j], vb[j], s, tab);
+        if (i < nvec) st_nt(o4 + i, apply4<OP>(va[j], vb[j], s, tab));
     }
     const uint64_t gid = static_cast<uint64_t>(blockIdx.x) * kBlock + threadIdx.x;
     const uint64_t idx = nvec * 4 + gid;
@@ -171,14 +172,14 @@ __global__ __launch_bounds__(kBlock) void k_rowbcast(const float *a, const float
     for (int j = 0; j < VPT; ++j) {
         const uint32_t i = base + j * kBlock;
         if (i < nvec) {
-            va[j] = a4[i];
-            vb[j] = b4[nv0.mod(i)];
+            va[j] = ld_nt(a4 + i);
+            vb[j] = b4[nv0.mod(i)]; // the row operand is re-read by every row: cached
         }
     }
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
         const uint32_t i = base + j * kBlock;
-        if (i < nvec) o4[i] = apply4<OP>(va[j], vb[j], s, tab);
+        if (i < nvec) st_nt(o4 + i, apply4<OP>(va[j], vb[j], s, tab));
     }
 }
 
@@ -217,7 +218,7 @@ __global__ __launch_bounds__(kBlock) void k_rows(RowsGeo g, const float *a, cons
     const uint32_t i3 = g.ne2.div(r2);
     const uint32_t i2 = r2 - i3 * g.ne2.d;
     const int64_t col = 4 * static_cast<int64_t>(v);
-    const float4 va = *reinterpret_cast<const float4 *>(a + rows_offset(g.a_st, g.a_mod, g.a_modmask, i1, i2, i3) + col);
+    const float4 va = ld_nt(reinterpret_cast<const float4 *>(a + rows_offset(g.a_st, g.a_mod, g.a_modmask, i1, i2, i3) + col));
     float4 vb = va;
     if constexpr (Fn<OP>::kBinary) {
         const float *bp = b + rows_offset(g.b_st, g.b_mod, g.b_modmask, i1, i2, i3);
@@ -230,7 +231,7 @@ __global__ __launch_bounds__(kBlock) void k_rows(RowsGeo g, const float *a, cons
     }
     const int64_t oo = static_cast<int64_t>(i1) * g.o_st[1] + static_cast<int64_t>(i2) * g.o_st[2] +
                        static_cast<int64_t>(i3) * g.o_st[3] + col;
-    *reinterpret_cast<float4 *>(o + oo) = apply4<OP>(va, vb, s, tab);
+    st_nt(reinterpret_cast<float4 *>(o + oo), apply4<OP>(va, vb, s, tab));
 }
 
 // ---- general: one element per thread, per-operand ordinal decode ----------

@@ -1,12 +1,13 @@
 // rows.hip -- gfx950 kernels for the per-row ops: rms_norm (+weight),
 // norm, soft_max (dense and strided) and the scaled + masked soft_max.
 //
-// A row is dim 0 of the view; rows enumerate (i1, i2, i3).  One wave64
-// owns one row: it loads the row once into registers (128-bit loads),
-// reduces across its 64 lanes with butterfly shuffles, and writes the
-// result once, so each row costs one HBM read and one HBM write.  Rows
-// wider than the register budget stream through global memory in several
-// passes (the later passes hit L2).  Row reductions keep the reference's
+// A row is dim 0 of the view; rows enumerate (i1, i2, i3).  A wave (short
+// rows) or a 4-wave workgroup (long rows) owns one row: it loads the row
+// once into registers (128-bit non-temporal loads), reduces with butterfly
+// shuffles and, across waves, through LDS, and writes the result once, so
+// each row costs one HBM read and one HBM write.  Rows wider than the
+// register budget stream through global memory in several passes (the later
+// passes hit L2).  Row reductions keep the reference's
 // arithmetic: f32-rounded squares summed in f64 (normalization.rs:343-362),
 // exp(x - max) summed in f64 (reductions.rs:565-601), divisions and square
 // roots correctly rounded.  The strided soft_max keeps the reference's
@@ -30,8 +31,8 @@ struct RowGeo {
 
 struct MaskGeo {
     const uint16_t *p; // dense f16 [ncols, ne1, m2, m3] or null
-    uint32_t ne1, m2, m3;
-    uint32_t head_major; // logical row order puts i2 fastest (mask shared by all i2)
+    uint32_t ne1;
+    FastDiv m2, m3;    // the mask's extents along dims 2 and 3 (divide the source's)
 };
 
 __device__ __forceinline__ void row_coords(const RowGeo &g, uint32_t r, uint32_t &i1, uint32_t &i2, uint32_t &i3)
@@ -100,167 +101,205 @@ __device__ __forceinline__ float4 exp4(float4 v, const uint64_t *t)
 }
 
 // ---- vectorized rows: contiguous dim 0, ncols % 4 == 0 ------------------
-// NV > 0: the row (nv = ncols/4 float4) is held in NV float4 per lane.
-// NV == 0: the row is streamed in passes.
+// NW waves own a row: NW = 1 puts four rows in a 256-thread workgroup (rows
+// of at most 1024 columns), NW = 4 gives each row its own workgroup.  Thread
+// t of a row holds float4 t, t + 64*NW, ... in registers, NV of them; FULL
+// means the row fills them exactly, so no per-element bounds checks run.
+// NV == 0 streams rows too wide for registers in passes.  Row data is read
+// and written with non-temporal accesses (each byte moves once); weights
+// and masks stay on the cached path.  Rows run in memory order.
 
-template <RowOp OP, int NV>
+template <int NW>
+__device__ __forceinline__ double row_sum(double v, double *lds)
+{
+    v = wave_sum(v);
+    if constexpr (NW == 1) {
+        return v;
+    } else {
+        if (threadIdx.x % kWave == 0) lds[threadIdx.x / kWave] = v;
+        __syncthreads();
+        double t = lds[0];
+#pragma unroll
+        for (int i = 1; i < NW; ++i) t += lds[i];
+        return t;
+    }
+}
+
+template <int NW>
+__device__ __forceinline__ float row_max(float v, double *lds)
+{
+    v = wave_max(v);
+    if constexpr (NW == 1) {
+        return v;
+    } else {
+        if (threadIdx.x % kWave == 0) lds[threadIdx.x / kWave] = v;
+        __syncthreads();
+        float t = static_cast<float>(lds[0]);
+#pragma unroll
+        for (int i = 1; i < NW; ++i) t = __builtin_fmaxf(t, static_cast<float>(lds[i]));
+        return t;
+    }
+}
+
+template <RowOp OP, int NW, int NV, bool FULL, bool MASK>
 __global__ __launch_bounds__(kBlock) void k_row_vec(RowGeo g, const float *x, float *y, const float *w, MaskGeo mg,
                                                      float eps, float scale)
 {
     constexpr bool kSoft = OP == RowOp::SoftMax || OP == RowOp::SoftMaxExt;
-    __shared__ uint64_t lds[32];
+    constexpr uint32_t kTPR = NW * kWave;      // threads per row
+    constexpr uint32_t kRPB = kBlock / kTPR;   // rows per workgroup
+    __shared__ uint64_t lds_tab[32];
+    __shared__ double lds_a[kBlock / kWave];   // first row reduction
+    __shared__ double lds_b[kBlock / kWave];   // second row reduction
     const uint64_t *tab = nullptr;
     if constexpr (kSoft) {
-        if (threadIdx.x < 32) lds[threadIdx.x] = kExp2Table[threadIdx.x];
-        __syncthreads();
-        tab = lds;
+        if (threadIdx.x < 32) lds_tab[threadIdx.x] = kExp2Table[threadIdx.x];
+        // with NW > 1 the max reduction's barrier orders the table before use
+        if constexpr (NW == 1) __syncthreads();
+        tab = lds_tab;
     }
-    const uint32_t wave = threadIdx.x / kWave;
-    const uint32_t lane = threadIdx.x % kWave;
-    const uint32_t blk = (OP == RowOp::SoftMaxExt && mg.head_major && (gridDim.x & 7u) == 0) ? xcd_major_block(8)
-                                                                                              : blockIdx.x;
-    const uint32_t logical = blk * (kBlock / kWave) + wave;
-    if (logical >= g.rows) return;
+    const uint32_t t = threadIdx.x % kTPR;
+    uint32_t r; // uniform across the row's waves
+    if constexpr (kRPB == 1) {
+        r = blockIdx.x;
+    } else {
+        r = blockIdx.x * kRPB + __builtin_amdgcn_readfirstlane(threadIdx.x / kTPR);
+        if (r >= g.rows) return; // no workgroup barrier follows when NW == 1
+    }
 
     uint32_t i1, i2, i3;
-    if (OP == RowOp::SoftMaxExt && mg.head_major) {
-        // logical order: i2 fastest, so the rows sharing one mask row run
-        // back to back on one XCD and the mask is fetched from HBM once.
-        const uint32_t t = g.ne2.div(logical);
-        i2 = logical - t * g.ne2.d;
-        i3 = g.ne1.div(t);
-        i1 = t - i3 * g.ne1.d;
-    } else {
-        row_coords(g, logical, i1, i2, i3);
-    }
+    row_coords(g, r, i1, i2, i3);
     const float4 *xr = reinterpret_cast<const float4 *>(x + row_base(g.x_st, i1, i2, i3));
     float4 *yr = reinterpret_cast<float4 *>(y + row_base(g.y_st, i1, i2, i3));
     const uint32_t nv = g.ncols / 4;
     const uint16_t *mr = nullptr;
-    if (OP == RowOp::SoftMaxExt && mg.p) {
-        const uint64_t mrow = (static_cast<uint64_t>(i3 % mg.m3) * mg.m2 + (i2 % mg.m2)) * mg.ne1 + i1;
+    if constexpr (MASK) {
+        const uint64_t mrow = (static_cast<uint64_t>(mg.m3.mod(i3)) * mg.m2.d + mg.m2.mod(i2)) * mg.ne1 + i1;
         mr = mg.p + mrow * g.ncols;
     }
     auto load = [&](uint32_t idx) {
-        float4 v = xr[idx];
+        float4 v = ld_nt(xr + idx);
         if constexpr (OP == RowOp::SoftMaxExt) {
-            v = mul4(v, scale);                         // OpScale
-            if (mr) v = add4(v, mask4(mr + 4 * idx));   // OpAdd(f16 mask -> f32)
+            v = mul4(v, scale);                              // OpScale
+            if constexpr (MASK) v = add4(v, mask4(mr + 4 * idx)); // OpAdd(f16 mask -> f32)
         }
         return v;
     };
+    auto in_row = [&](int j) { return FULL || t + kTPR * j < nv; };
 
     if constexpr (NV > 0) {
         float4 v[NV];
 #pragma unroll
-        for (int j = 0; j < NV; ++j) {
-            const uint32_t idx = lane + j * kWave;
-            v[j] = idx < nv ? load(idx) : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
+        for (int j = 0; j < NV; ++j) v[j] = in_row(j) ? load(t + kTPR * j) : make_float4(0.f, 0.f, 0.f, 0.f);
         if constexpr (OP == RowOp::RmsNorm || OP == RowOp::RmsNormMul) {
             double acc = 0.0;
 #pragma unroll
             for (int j = 0; j < NV; ++j)
-                if (lane + j * kWave < nv) acc += sumsq4(v[j]);
-            acc = wave_sum(acc);
+                if (in_row(j)) acc += sumsq4(v[j]);
+            acc = row_sum<NW>(acc, lds_a);
             const float mean = static_cast<float>(acc / static_cast<double>(g.ncols));
             const float k = 1.0f / __builtin_sqrtf(mean + eps);
 #pragma unroll
             for (int j = 0; j < NV; ++j) {
-                const uint32_t idx = lane + j * kWave;
-                if (idx < nv) {
-                    float4 r = mul4(v[j], k);
-                    if constexpr (OP == RowOp::RmsNormMul) r = mul4(r, reinterpret_cast<const float4 *>(w)[idx]);
-                    yr[idx] = r;
+                if (in_row(j)) {
+                    const uint32_t idx = t + kTPR * j;
+                    float4 o = mul4(v[j], k);
+                    if constexpr (OP == RowOp::RmsNormMul) o = mul4(o, reinterpret_cast<const float4 *>(w)[idx]);
+                    st_nt(yr + idx, o);
                 }
             }
         } else if constexpr (OP == RowOp::Norm) {
             double acc = 0.0;
 #pragma unroll
             for (int j = 0; j < NV; ++j)
-                if (lane + j * kWave < nv) acc += sum4(v[j]);
-            acc = wave_sum(acc);
+                if (in_row(j)) acc += sum4(v[j]);
+            acc = row_sum<NW>(acc, lds_a);
             const float mean = static_cast<float>(acc / static_cast<double>(g.ncols));
             double var = 0.0;
 #pragma unroll
             for (int j = 0; j < NV; ++j) {
-                if (lane + j * kWave < nv) {
+                if (in_row(j)) {
                     const float4 c = sub4(v[j], mean);
                     var += (static_cast<double>(c.x) * c.x + static_cast<double>(c.y) * c.y) +
                            (static_cast<double>(c.z) * c.z + static_cast<double>(c.w) * c.w);
                 }
             }
-            var = wave_sum(var);
+            var = row_sum<NW>(var, lds_b);
             const float variance = static_cast<float>(var / static_cast<double>(g.ncols));
             const float k = 1.0f / __builtin_sqrtf(variance + eps);
 #pragma unroll
-            for (int j = 0; j < NV; ++j) {
-                const uint32_t idx = lane + j * kWave;
-                if (idx < nv) yr[idx] = mul4(sub4(v[j], mean), k);
-            }
+            for (int j = 0; j < NV; ++j)
+                if (in_row(j)) st_nt(yr + t + kTPR * j, mul4(sub4(v[j], mean), k));
         } else { // soft_max, f64 row sum
             float mx = -__builtin_inff();
 #pragma unroll
             for (int j = 0; j < NV; ++j)
-                if (lane + j * kWave < nv) mx = __builtin_fmaxf(mx, max4(v[j]));
-            mx = wave_max(mx);
+                if (in_row(j)) mx = __builtin_fmaxf(mx, max4(v[j]));
+            mx = row_max<NW>(mx, lds_a);
             double acc = 0.0;
 #pragma unroll
             for (int j = 0; j < NV; ++j) {
-                if (lane + j * kWave < nv) {
+                if (in_row(j)) {
                     v[j] = exp4(sub4(v[j], mx), tab);
                     acc += sum4(v[j]);
                 }
             }
-            acc = wave_sum(acc);
+            acc = row_sum<NW>(acc, lds_b);
             const double recip = 1.0 / static_cast<double>(static_cast<float>(acc));
 #pragma unroll
-            for (int j = 0; j < NV; ++j) {
-                const uint32_t idx = lane + j * kWave;
-                if (idx < nv) yr[idx] = div4(v[j], recip);
-            }
+            for (int j = 0; j < NV; ++j)
+                if (in_row(j)) st_nt(yr + t + kTPR * j, div4(v[j], recip));
         }
     } else {
-        // streamed passes for wide rows
+        // streamed passes for rows wider than the register budget; the
+        // intermediate passes use cached accesses so re-reads hit L2
         if constexpr (OP == RowOp::RmsNorm || OP == RowOp::RmsNormMul) {
             double acc = 0.0;
-            for (uint32_t idx = lane; idx < nv; idx += kWave) acc += sumsq4(xr[idx]);
-            acc = wave_sum(acc);
+            for (uint32_t idx = t; idx < nv; idx += kTPR) acc += sumsq4(xr[idx]);
+            acc = row_sum<NW>(acc, lds_a);
             const float mean = static_cast<float>(acc / static_cast<double>(g.ncols));
             const float k = 1.0f / __builtin_sqrtf(mean + eps);
-            for (uint32_t idx = lane; idx < nv; idx += kWave) {
-                float4 r = mul4(xr[idx], k);
-                if constexpr (OP == RowOp::RmsNormMul) r = mul4(r, reinterpret_cast<const float4 *>(w)[idx]);
-                yr[idx] = r;
+            for (uint32_t idx = t; idx < nv; idx += kTPR) {
+                float4 o = mul4(xr[idx], k);
+                if constexpr (OP == RowOp::RmsNormMul) o = mul4(o, reinterpret_cast<const float4 *>(w)[idx]);
+                st_nt(yr + idx, o);
             }
         } else if constexpr (OP == RowOp::Norm) {
             double acc = 0.0;
-            for (uint32_t idx = lane; idx < nv; idx += kWave) acc += sum4(xr[idx]);
-            acc = wave_sum(acc);
+            for (uint32_t idx = t; idx < nv; idx += kTPR) acc += sum4(xr[idx]);
+            acc = row_sum<NW>(acc, lds_a);
             const float mean = static_cast<float>(acc / static_cast<double>(g.ncols));
             double var = 0.0;
-            for (uint32_t idx = lane; idx < nv; idx += kWave) {
+            for (uint32_t idx = t; idx < nv; idx += kTPR) {
                 const float4 c = sub4(xr[idx], mean);
                 var += (static_cast<double>(c.x) * c.x + static_cast<double>(c.y) * c.y) +
                        (static_cast<double>(c.z) * c.z + static_cast<double>(c.w) * c.w);
             }
-            var = wave_sum(var);
+            var = row_sum<NW>(var, lds_b);
             const float variance = static_cast<float>(var / static_cast<double>(g.ncols));
             const float k = 1.0f / __builtin_sqrtf(variance + eps);
-            for (uint32_t idx = lane; idx < nv; idx += kWave) yr[idx] = mul4(sub4(xr[idx], mean), k);
+            for (uint32_t idx = t; idx < nv; idx += kTPR) st_nt(yr + idx, mul4(sub4(xr[idx], mean), k));
         } else {
+            auto load_cached = [&](uint32_t idx) {
+                float4 v = xr[idx];
+                if constexpr (OP == RowOp::SoftMaxExt) {
+                    v = mul4(v, scale);
+                    if constexpr (MASK) v = add4(v, mask4(mr + 4 * idx));
+                }
+                return v;
+            };
             float mx = -__builtin_inff();
-            for (uint32_t idx = lane; idx < nv; idx += kWave) mx = __builtin_fmaxf(mx, max4(load(idx)));
-            mx = wave_max(mx);
+            for (uint32_t idx = t; idx < nv; idx += kTPR) mx = __builtin_fmaxf(mx, max4(load_cached(idx)));
+            mx = row_max<NW>(mx, lds_a);
             double acc = 0.0;
-            for (uint32_t idx = lane; idx < nv; idx += kWave) {
-                const float4 e = exp4(sub4(load(idx), mx), tab);
+            for (uint32_t idx = t; idx < nv; idx += kTPR) {
+                const float4 e = exp4(sub4(load_cached(idx), mx), tab);
                 yr[idx] = e;
                 acc += sum4(e);
             }
-            acc = wave_sum(acc);
+            acc = row_sum<NW>(acc, lds_b);
             const double recip = 1.0 / static_cast<double>(static_cast<float>(acc));
-            for (uint32_t idx = lane; idx < nv; idx += kWave) yr[idx] = div4(yr[idx], recip);
+            for (uint32_t idx = t; idx < nv; idx += kTPR) st_nt(yr + idx, div4(yr[idx], recip));
         }
     }
 }
@@ -347,7 +386,7 @@ __global__ __launch_bounds__(kBlock) void k_softmax_generic(OrdView xv, OrdView 
         const uint64_t i1 = r % xv.ne[1];
         const uint64_t i2 = (r / xv.ne[1]) % xv.ne[2];
         const uint64_t i3 = r / (xv.ne[1] * xv.ne[2]);
-        mr = mg.p + ((i3 % mg.m3) * mg.m2 + (i2 % mg.m2)) * static_cast<uint64_t>(mg.ne1) * ncols + i1 * ncols;
+        mr = mg.p + ((i3 % mg.m3.d) * mg.m2.d + (i2 % mg.m2.d)) * static_cast<uint64_t>(mg.ne1) * ncols + i1 * ncols;
     }
     auto load = [&](uint64_t c) {
         float v = x[ord_index(xv, base + c)];
@@ -434,26 +473,41 @@ OrdView ord_view(const Operand &p)
     return v;
 }
 
-template <RowOp OP, int NV>
+template <RowOp OP, int NW, int NV, bool FULL>
 void launch_vec(const RowGeo &g, const RowArgs &a, const MaskGeo &mg, hipStream_t s)
 {
-    const uint32_t rows_per_block = kBlock / kWave;
-    uint32_t blocks = (g.rows + rows_per_block - 1) / rows_per_block;
-    if (OP == RowOp::SoftMaxExt && mg.head_major) blocks = (blocks + 7u) & ~7u; // XCD-major remap needs % 8
-    k_row_vec<OP, NV><<<dim3(blocks), kBlock, 0, s>>>(g, static_cast<const float *>(a.x.data),
-                                                       static_cast<float *>(a.y.data), a.w, mg, a.eps, a.scale);
+    constexpr uint32_t rows_per_block = kBlock / (NW * kWave);
+    const uint32_t blocks = (g.rows + rows_per_block - 1) / rows_per_block;
+    const float *x = static_cast<const float *>(a.x.data);
+    float *y = static_cast<float *>(a.y.data);
+    if (OP == RowOp::SoftMaxExt && mg.p)
+        k_row_vec<OP, NW, NV, FULL, true><<<dim3(blocks), kBlock, 0, s>>>(g, x, y, a.w, mg, a.eps, a.scale);
+    else
+        k_row_vec<OP, NW, NV, FULL, false><<<dim3(blocks), kBlock, 0, s>>>(g, x, y, a.w, mg, a.eps, a.scale);
 }
 
+template <RowOp OP, int NW, int NV>
+void launch_fit(const RowGeo &g, const RowArgs &a, const MaskGeo &mg, hipStream_t s)
+{
+    if (g.ncols / 4 == static_cast<uint32_t>(NW * kWave * NV)) launch_vec<OP, NW, NV, true>(g, a, mg, s);
+    else launch_vec<OP, NW, NV, false>(g, a, mg, s);
+}
+
+// Rows of up to 1024 columns: a wave per row; up to 16384 columns: a
+// workgroup per row with the row in registers; wider: a workgroup per row
+// streaming in passes.
 template <RowOp OP>
 void launch_vec_nv(const RowGeo &g, const RowArgs &a, const MaskGeo &mg, hipStream_t s)
 {
     const uint32_t nv = g.ncols / 4;
-    if (nv <= 1 * kWave) launch_vec<OP, 1>(g, a, mg, s);
-    else if (nv <= 2 * kWave) launch_vec<OP, 2>(g, a, mg, s);
-    else if (nv <= 4 * kWave) launch_vec<OP, 4>(g, a, mg, s);
-    else if (nv <= 8 * kWave) launch_vec<OP, 8>(g, a, mg, s);
-    else if (nv <= 16 * kWave) launch_vec<OP, 16>(g, a, mg, s);
-    else launch_vec<OP, 0>(g, a, mg, s);
+    if (nv <= 1 * kWave) launch_fit<OP, 1, 1>(g, a, mg, s);
+    else if (nv <= 2 * kWave) launch_fit<OP, 1, 2>(g, a, mg, s);
+    else if (nv <= 4 * kWave) launch_fit<OP, 1, 4>(g, a, mg, s);
+    else if (nv <= 2 * kBlock) launch_fit<OP, 4, 2>(g, a, mg, s);
+    else if (nv <= 4 * kBlock) launch_fit<OP, 4, 4>(g, a, mg, s);
+    else if (nv <= 8 * kBlock) launch_fit<OP, 4, 8>(g, a, mg, s);
+    else if (nv <= 16 * kBlock) launch_fit<OP, 4, 16>(g, a, mg, s);
+    else launch_vec<OP, 4, 0, false>(g, a, mg, s);
 }
 
 } // namespace
@@ -511,12 +565,13 @@ hipError_t launch_rows(const RowArgs &a, hipStream_t s)
             }
         }
         MaskGeo mg{};
+        mg.m2 = FastDiv(1);
+        mg.m3 = FastDiv(1);
         if (a.op == RowOp::SoftMaxExt) {
             mg.p = a.mask;
             mg.ne1 = static_cast<uint32_t>(a.x.ne[1]);
-            mg.m2 = static_cast<uint32_t>(a.mask_ne2 ? a.mask_ne2 : 1);
-            mg.m3 = static_cast<uint32_t>(a.mask_ne3 ? a.mask_ne3 : 1);
-            mg.head_major = (a.mask != nullptr && mg.m2 == 1 && a.x.ne[2] > 1) ? 1u : 0u;
+            mg.m2 = FastDiv(static_cast<uint32_t>(a.mask_ne2 ? a.mask_ne2 : 1));
+            mg.m3 = FastDiv(static_cast<uint32_t>(a.mask_ne3 ? a.mask_ne3 : 1));
         }
         switch (a.op) {
         case RowOp::RmsNorm: launch_vec_nv<RowOp::RmsNorm>(g, a, mg, s); break;
@@ -538,8 +593,8 @@ hipError_t launch_rows(const RowArgs &a, hipStream_t s)
         if (a.op == RowOp::SoftMaxExt) {
             mg.p = a.mask;
             mg.ne1 = static_cast<uint32_t>(a.x.ne[1]);
-            mg.m2 = static_cast<uint32_t>(a.mask_ne2 ? a.mask_ne2 : 1);
-            mg.m3 = static_cast<uint32_t>(a.mask_ne3 ? a.mask_ne3 : 1);
+            mg.m2 = FastDiv(static_cast<uint32_t>(a.mask_ne2 ? a.mask_ne2 : 1));
+            mg.m3 = FastDiv(static_cast<uint32_t>(a.mask_ne3 ? a.mask_ne3 : 1));
             k_softmax_generic<true><<<grid, kBlock, 0, s>>>(ord_view(a.x), ord_view(a.y), rows, ncols, x, y, mg,
                                                              a.scale);
         } else {
