@@ -8,10 +8,13 @@ data from HBM: between two launches of the same op the other ops move
 two copies per op as well.  Inputs are synthetic (seeded PCG64) and already
 resident in HBM when the timed region starts.
 
-Times come from HIP events recorded on the stream the kernels run on: the
-value is total algorithmic bytes per step / step time over K steps (events
-only at the ends), and each op's figure is the average of back-to-back
-launches of that op alone.  The
+Times come from HIP events recorded on the stream the kernels run on.  The
+steps are captured once into a HIP graph and replayed (removing Python
+launch overhead, which is larger than the smaller kernels); the replays
+are checked bit-for-bit against eager launches, and the eager step time is
+reported beside.  The value is total algorithmic bytes per step / step
+time; each op's figure is the average over a graph of back-to-back launches
+of that op alone.  The
 roofline object describes the dominant kernel (the scaled + masked soft_max
 of config 4, over half of the step's bytes).  The CPU baseline times the C
 oracle (a single-threaded restatement of the reference's CPU path) on a
@@ -146,10 +149,12 @@ class GpuSuite:
             return eh.TensorViewMut(t, L(dtype, ne, nb or dense_nb(ne)))
 
         self.events = {}
+        self.outputs = {}
         silu_gate = np.empty_like(host["c2_gate"])  # mul's first operand: silu(gate) values
         silu_gate[:] = host["c2_gate"] / (1 + np.exp(-host["c2_gate"].astype(np.float64)))
         for name in names:
             evs = []
+            outs = []
             for c in range(copies):
                 if name == "add_broadcast_row":
                     a, b, o = up(host["c1_src0"]), up(host["c1_src1"]), zeros(4096 * 512)
@@ -193,7 +198,9 @@ class GpuSuite:
                 else:
                     raise ValueError(name)
                 evs.append(ev)
+                outs.append(o)
             self.events[name] = evs
+            self.outputs[name] = outs
         torch.cuda.synchronize()
 
     def launch(self, name, step):
@@ -317,36 +324,62 @@ def main():
             for n in names:
                 suite.launch(n, w)
         stream.synchronize()
-        # the timed region: K steps, events only at its two ends
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        start.record(stream)
-        for s in range(args.steps):
-            for n in names:
-                suite.launch(n, s)
-        end.record(stream)
-        end.synchronize()
-        wall = time.perf_counter() - t0
-        step_ms = start.elapsed_time(end) / args.steps
 
-        # per op: R back-to-back launches (alternating buffer copies), so the
-        # figure is the average launch duration including the gap between
-        # two launches, without timing markers between kernels
-        reps = max(args.steps, 20)
-        per_ms = {}
-        for n in names:
-            for i in range(2):
-                suite.launch(n, i)
+        def timed(fn, reps):
             a = torch.cuda.Event(enable_timing=True)
             b = torch.cuda.Event(enable_timing=True)
             a.record(stream)
             for i in range(reps):
-                suite.launch(n, i)
+                fn(i)
             b.record(stream)
             b.synchronize()
-            per_ms[n] = a.elapsed_time(b) / reps
+            return a.elapsed_time(b)
+
+        def capture(fn):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                fn()
+            stream.synchronize()
+            return g
+
+        def two_steps():
+            for c in range(2):
+                for n in names:
+                    suite.launch(n, c)
+
+        # eager: K steps launched from the host, events only at the ends
+        t0 = time.perf_counter()
+        eager_step_ms = timed(lambda s: [suite.launch(n, s) for n in names], args.steps) / args.steps
+        wall = time.perf_counter() - t0
+
+        # graph: one capture of two steps (both buffer copies), replayed;
+        # every replay must reproduce the eager outputs bit for bit
+        step_graph = capture(two_steps)
+        reference = {}
+        for n in names:
+            suite.launch(n, 0)
+        stream.synchronize()
+        for n in names:
+            reference[n] = suite.outputs[n][0].clone()
+        for check in range(2):
+            for n in names:
+                suite.outputs[n][0].zero_()
+            stream.synchronize()
+            step_graph.replay()
+            stream.synchronize()
+            for n in names:
+                if not torch.equal(suite.outputs[n][0], reference[n]):
+                    raise RuntimeError(f"graph replay {check} of {n} differs from the eager launch")
+        pairs = max(1, args.steps // 2)
+        step_ms = timed(lambda i: step_graph.replay(), pairs) / (2 * pairs)
+
+        # per op: a graph of R back-to-back launches (alternating copies)
+        reps = max(args.steps, 20)
+        per_ms = {}
+        for n in names:
+            g = capture(lambda n=n: [suite.launch(n, i) for i in range(reps)])
+            g.replay()
+            per_ms[n] = timed(lambda i: g.replay(), 3) / (3 * reps)
 
     per_op = {}
     total_bytes = 0
@@ -395,6 +428,9 @@ def main():
         "dtype": "f32",
         "data": "synthetic (seeded PCG64; BASELINE config shapes and distributions)",
         "config": {"workload": "all BASELINE configs, one launch of each op per step: " + ", ".join(names),
+                   "launch": "one captured HIP graph of two steps replayed K/2 times (replays checked bit-exact "
+                             "against eager launches); eager_ms_per_step: the same steps launched from Python",
+                   "eager_ms_per_step": round(eager_step_ms, 4),
                    "buffer_policy": "independent buffers per op, two copies alternating; >=1 GB moved between "
                                     "two launches of one op (Infinity Cache is 256 MB)",
                    "wall_s": round(wall, 3)},

@@ -125,6 +125,13 @@ __device__ __forceinline__ const uint64_t *stage_table(uint64_t *lds)
 
 // ---- dense: every operand contiguous, paired by linear index -------------
 
+// Streaming policy measured on MI355X: unary ops read with cached loads and
+// write non-temporally; binary ops stream both ways.
+template <Ew OP>
+struct Stream {
+    static constexpr bool kNtLoad = Fn<OP>::kBinary;
+};
+
 template <Ew OP, int VPT>
 __global__ __launch_bounds__(kBlock) void k_dense(const float *a, const float *b, float *o, uint64_t nvec,
                                                    uint64_t n, float s)
@@ -140,7 +147,7 @@ __global__ __launch_bounds__(kBlock) void k_dense(const float *a, const float *b
     for (int j = 0; j < VPT; ++j) {
         const uint64_t i = base + static_cast<uint64_t>(j) * kBlock;
         if (i < nvec) {
-            va[j] = ld_nt(a4 + i);
+            va[j] = Stream<OP>::kNtLoad ? ld_nt(a4 + i) : a4[i];
             if constexpr (Fn<OP>::kBinary) vb[j] = ld_nt(b4 + i);
             else vb[j] = va[j];
         }

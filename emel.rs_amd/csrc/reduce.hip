@@ -77,7 +77,7 @@ __device__ __forceinline__ void accumulate(const RedGeo &g, const float *x, int6
     if (g.mode == kModeVec) {
         const float4 *x4 = reinterpret_cast<const float4 *>(x + base);
         for (uint64_t v = c0 / 4 + threadIdx.x; v < c1 / 4; v += kBlock) {
-            const float4 q = ld_nt(x4 + v);
+            const float4 q = x4[v];
             const uint64_t c = 4 * v;
             if constexpr (kArg) {
                 take(q.x, c);
