@@ -304,7 +304,7 @@ def main():
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py measures one GPU only (asked for {args.gpus}): every op is row-local, "
-              "so N GPUs each run their own share; see DESIGN.md on sharding", file=sys.stderr)
+              "so N GPUs would each run the same kernels on their own rows; no multi-GPU figure is measured", file=sys.stderr)
         sys.exit(2)
 
     import torch

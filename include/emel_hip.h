@@ -6,8 +6,9 @@
  * event of emel-kernels' portable router (stateforward/emel.rs,
  * crates/emel-kernels/src/any/, cited below as file:line) and keeps its
  * argument meaning, validation order and error classification.  A Rust FFI
- * crate binds these functions one-to-one (the binding is shown in
- * INTEGRATION.md at the repository root).
+ * crate binds these functions one-to-one: #[repr(C)] mirrors of
+ * emel_tensor_view / emel_tensor_view_mut and an extern "C" block with the
+ * same signatures, status codes mapped onto the reference's error enums.
  *
  * Conventions
  *   - Views mirror the pinned C++ tensor_view {data, type, ne[4], nb[4]}
