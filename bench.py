@@ -4,21 +4,21 @@ row-reduction ops on one MI355X (BASELINE.json metric).
 One step = one launch of every op of the five BASELINE configs, each on its
 own buffers (no op reads another op's output), so each launch streams cold
 data from HBM: between two launches of the same op the other ops move
-~1 GB, far more than the 256 MB Infinity Cache.  Buffers alternate between
-two copies per op as well.  Inputs are synthetic (seeded PCG64) and already
-resident in HBM when the timed region starts.
+~1 GB, far more than the 256 MB Infinity Cache.  Inputs are synthetic
+(seeded PCG64) and already resident in HBM when the timed region starts.
 
 Times come from HIP events recorded on the stream the kernels run on.  The
 steps are captured once into a HIP graph and replayed (removing Python
 launch overhead, which is larger than the smaller kernels); the replays
 are checked bit-for-bit against eager launches, and the eager step time is
 reported beside.  The value is total algorithmic bytes per step / step
-time; each op's figure is the average over a graph of back-to-back launches
-of that op alone.  The
-roofline object describes the dominant kernel (the scaled + masked soft_max
-of config 4, over half of the step's bytes).  The CPU baseline times the C
-oracle (a single-threaded restatement of the reference's CPU path) on a
-bounded sample of the same workload.
+time.  Each op's own figure is the average over a graph of back-to-back
+launches of that op that cycle through at least 1 GiB of distinct buffer
+sets, so those launches are cold too.  The roofline object describes the
+dominant kernel (the scaled + masked soft_max of config 4, over half of the
+step's bytes).  The CPU baseline times the C oracle (a single-threaded
+restatement of the reference's CPU path) on a bounded sample of the same
+workload.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--ops a,b] [--no-cpu]
 """
@@ -120,10 +120,17 @@ DOMINANT = "soft_max_ext"
 COPY_BYTES = 2 * 268435456  # the calibration copy: 256 MiB read + 256 MiB written
 
 
-class GpuSuite:
-    """Device buffers (two copies per op) and the launch closures."""
+ROTATE_BYTES = 1 << 30  # per-op timing cycles through at least this many distinct bytes
 
-    def __init__(self, host, stream, names, copies=2):
+
+class GpuSuite:
+    """Device buffers and the launch closures.
+
+    Each op gets enough independent buffer sets that cycling through them
+    moves at least ROTATE_BYTES (four times the 256 MB Infinity Cache), so
+    back-to-back launches of one op stream from HBM, not from cache."""
+
+    def __init__(self, host, stream, names):
         import torch
 
         import emel_hip as eh
@@ -148,59 +155,66 @@ class GpuSuite:
         def M(t, ne, nb=None, dtype=F32):
             return eh.TensorViewMut(t, L(dtype, ne, nb or dense_nb(ne)))
 
-        self.events = {}
-        self.outputs = {}
         silu_gate = np.empty_like(host["c2_gate"])  # mul's first operand: silu(gate) values
         silu_gate[:] = host["c2_gate"] / (1 + np.exp(-host["c2_gate"].astype(np.float64)))
+        scale = float(np.float32(1.0 / np.sqrt(128.0)))
+        snb = dense_nb([128, 32, 64, 8])
+        vnb = [snb[0], snb[2], snb[1], snb[3]]  # dims 1 and 2 swapped
+        n2 = 11008 * 512
+        # name -> (host inputs, output (numel, dtype), event builder(inputs, output))
+        spec = {
+            "add_broadcast_row": ([host["c1_src0"], host["c1_src1"]], (4096 * 512, torch.float32),
+                                  lambda i, o: eh.OpAddBroadcastRow(V(i[0], [4096, 512, 1, 1]), V(i[1], [4096, 1, 1, 1]),
+                                                                    M(o, [4096, 512, 1, 1]))),
+            "silu": ([host["c2_gate"]], (n2, torch.float32),
+                     lambda i, o: eh.OpSilu(V(i[0], [11008, 512, 1, 1]), M(o, [11008, 512, 1, 1]))),
+            "gelu": ([host["c2_gate"]], (n2, torch.float32),
+                     lambda i, o: eh.OpGelu(V(i[0], [11008, 512, 1, 1]), M(o, [11008, 512, 1, 1]))),
+            "mul": ([silu_gate, host["c2_up"]], (n2, torch.float32),
+                    lambda i, o: eh.OpMul(V(i[0], [11008, 512, 1, 1]), V(i[1], [11008, 512, 1, 1]),
+                                          M(o, [11008, 512, 1, 1]))),
+            "swiglu": ([host["c2_gate"], host["c2_up"]], (n2, torch.float32),
+                       lambda i, o: eh.OpSwiglu(V(i[0], [11008, 512, 1, 1]), V(i[1], [11008, 512, 1, 1]),
+                                                M(o, [11008, 512, 1, 1]))),
+            "rms_norm": ([host["c3_x"]], (4096 * 2048, torch.float32),
+                         lambda i, o: eh.OpRmsNorm(V(i[0], [4096, 2048, 1, 1]), M(o, [4096, 2048, 1, 1]), 1e-5)),
+            "rms_norm_mul": ([host["c3_x"], host["c3_w"]], (4096 * 2048, torch.float32),
+                             lambda i, o: eh.OpRmsNormMul(V(i[0], [4096, 2048, 1, 1]), V(i[1], [4096, 1, 1, 1]),
+                                                          M(o, [4096, 2048, 1, 1]), 1e-5)),
+            "soft_max_ext": ([host["c4_x"], host["c4_mask"]], (4096 * 512 * 32, torch.float32),
+                             lambda i, o: eh.OpSoftMaxExt(V(i[0], [4096, 512, 32, 1]),
+                                                          V(i[1], [4096, 512, 1, 1], dtype=F16), scale,
+                                                          M(o, [4096, 512, 32, 1]))),
+            "argmax_rows": ([host["c5_logits"]], (64, torch.int32),
+                            lambda i, o: eh.OpArgmaxRows(V(i[0], [151936, 64, 1, 1]), M(o, [1, 64, 1, 1], dtype=I32))),
+            "sum_rows": ([host["c5_logits"]], (64, torch.float32),
+                         lambda i, o: eh.OpSumRows(V(i[0], [151936, 64, 1, 1]), M(o, [1, 64, 1, 1]))),
+            "mul_broadcast_4d": ([host["c5b_src0"], host["c5b_src1"]], (128 * 64 * 32 * 8, torch.float32),
+                                 lambda i, o: eh.OpBinaryBroadcast(eh.BinaryOp.MUL, V(i[0], [128, 64, 32, 8], vnb),
+                                                                   V(i[1], [128, 1, 32, 1]), M(o, [128, 64, 32, 8]))),
+            "copy": ([np.zeros(COPY_BYTES // 8, np.float32)], (COPY_BYTES // 8, torch.float32),
+                     lambda i, o: eh.OpScale(V(i[0], [COPY_BYTES // 8, 1, 1, 1]), M(o, [COPY_BYTES // 8, 1, 1, 1]),
+                                             1.0)),
+        }
+        self.events = {}
+        self.outputs = {}
+        self.copies = {}
         for name in names:
-            evs = []
-            outs = []
+            if name not in spec:
+                raise ValueError(name)
+            inputs, (numel, odt), build = spec[name]
+            alg = dict((n, b) for n, _, b in OPS).get(name, COPY_BYTES)
+            copies = max(2, -(-ROTATE_BYTES // alg))
+            first = [up(x) for x in inputs]
+            evs, outs = [], []
             for c in range(copies):
-                if name == "add_broadcast_row":
-                    a, b, o = up(host["c1_src0"]), up(host["c1_src1"]), zeros(4096 * 512)
-                    ev = eh.OpAddBroadcastRow(V(a, [4096, 512, 1, 1]), V(b, [4096, 1, 1, 1]), M(o, [4096, 512, 1, 1]))
-                elif name in ("silu", "gelu"):
-                    a, o = up(host["c2_gate"]), zeros(11008 * 512)
-                    cls = eh.OpSilu if name == "silu" else eh.OpGelu
-                    ev = cls(V(a, [11008, 512, 1, 1]), M(o, [11008, 512, 1, 1]))
-                elif name == "mul":
-                    a, b, o = up(silu_gate), up(host["c2_up"]), zeros(11008 * 512)
-                    ev = eh.OpMul(V(a, [11008, 512, 1, 1]), V(b, [11008, 512, 1, 1]), M(o, [11008, 512, 1, 1]))
-                elif name == "swiglu":
-                    a, b, o = up(host["c2_gate"]), up(host["c2_up"]), zeros(11008 * 512)
-                    ev = eh.OpSwiglu(V(a, [11008, 512, 1, 1]), V(b, [11008, 512, 1, 1]), M(o, [11008, 512, 1, 1]))
-                elif name == "rms_norm":
-                    a, o = up(host["c3_x"]), zeros(4096 * 2048)
-                    ev = eh.OpRmsNorm(V(a, [4096, 2048, 1, 1]), M(o, [4096, 2048, 1, 1]), 1e-5)
-                elif name == "rms_norm_mul":
-                    a, w, o = up(host["c3_x"]), up(host["c3_w"]), zeros(4096 * 2048)
-                    ev = eh.OpRmsNormMul(V(a, [4096, 2048, 1, 1]), V(w, [4096, 1, 1, 1]), M(o, [4096, 2048, 1, 1]), 1e-5)
-                elif name == "soft_max_ext":
-                    a, m, o = up(host["c4_x"]), up(host["c4_mask"]), zeros(4096 * 512 * 32)
-                    scale = float(np.float32(1.0 / np.sqrt(128.0)))
-                    ev = eh.OpSoftMaxExt(V(a, [4096, 512, 32, 1]), V(m, [4096, 512, 1, 1], dtype=F16), scale,
-                                         M(o, [4096, 512, 32, 1]))
-                elif name == "argmax_rows":
-                    a, o = up(host["c5_logits"]), zeros(64, torch.int32)
-                    ev = eh.OpArgmaxRows(V(a, [151936, 64, 1, 1]), M(o, [1, 64, 1, 1], dtype=I32))
-                elif name == "sum_rows":
-                    a, o = up(host["c5_logits"]), zeros(64)
-                    ev = eh.OpSumRows(V(a, [151936, 64, 1, 1]), M(o, [1, 64, 1, 1]))
-                elif name == "mul_broadcast_4d":
-                    a, b, o = up(host["c5b_src0"]), up(host["c5b_src1"]), zeros(128 * 64 * 32 * 8)
-                    snb = dense_nb([128, 32, 64, 8])
-                    vnb = [snb[0], snb[2], snb[1], snb[3]]  # dims 1 and 2 swapped
-                    ev = eh.OpBinaryBroadcast(eh.BinaryOp.MUL, V(a, [128, 64, 32, 8], vnb), V(b, [128, 1, 32, 1]),
-                                              M(o, [128, 64, 32, 8]))
-                elif name == "copy":
-                    a, o = zeros(COPY_BYTES // 8), zeros(COPY_BYTES // 8)
-                    ev = eh.OpScale(V(a, [COPY_BYTES // 8, 1, 1, 1]), M(o, [COPY_BYTES // 8, 1, 1, 1]), 1.0)
-                else:
-                    raise ValueError(name)
-                evs.append(ev)
+                ins = first if c == 0 else [t.clone() for t in first]
+                o = zeros(numel, odt)
+                evs.append(build(ins, o))
                 outs.append(o)
             self.events[name] = evs
             self.outputs[name] = outs
+            self.copies[name] = copies
         torch.cuda.synchronize()
 
     def launch(self, name, step):
@@ -373,11 +387,12 @@ def main():
         pairs = max(1, args.steps // 2)
         step_ms = timed(lambda i: step_graph.replay(), pairs) / (2 * pairs)
 
-        # per op: a graph of R back-to-back launches (alternating copies)
-        reps = max(args.steps, 20)
+        # per op: a graph of back-to-back launches cycling through all of
+        # the op's buffer sets (>= ROTATE_BYTES), so each launch is cold
         per_ms = {}
         for n in names:
-            g = capture(lambda n=n: [suite.launch(n, i) for i in range(reps)])
+            reps = max(args.steps, 20, suite.copies[n])
+            g = capture(lambda n=n, reps=reps: [suite.launch(n, i) for i in range(reps)])
             g.replay()
             per_ms[n] = timed(lambda i: g.replay(), 3) / (3 * reps)
 
@@ -431,8 +446,9 @@ def main():
                    "launch": "one captured HIP graph of two steps replayed K/2 times (replays checked bit-exact "
                              "against eager launches); eager_ms_per_step: the same steps launched from Python",
                    "eager_ms_per_step": round(eager_step_ms, 4),
-                   "buffer_policy": "independent buffers per op, two copies alternating; >=1 GB moved between "
-                                    "two launches of one op (Infinity Cache is 256 MB)",
+                   "buffer_policy": "step: >=1 GB of other ops moves between two launches of one op; per op: "
+                                    "back-to-back launches cycle through >=1 GiB of distinct buffer sets "
+                                    "(Infinity Cache is 256 MB)",
                    "wall_s": round(wall, 3)},
         "per_op": per_op,
         "roofline": roof,

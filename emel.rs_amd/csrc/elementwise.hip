@@ -18,8 +18,8 @@
 //   k_ordinal  anything else: one element per thread, the reference's
 //              per-element ordinal decode.
 #include <cstdlib>
+#include <map>
 #include <mutex>
-#include <set>
 
 #include "common.hpp"
 #include "launch.hpp"
@@ -29,39 +29,64 @@ namespace emel {
 namespace {
 
 // GELU's result depends only on the fp16 rounding q of its input when
-// |x| < 10 (GeluFormula, unary.rs:522-541), so the 65536 possible results
-// are computed once per device by the same replica code and looked up.
-// Index: fp16 bits of x; entry: fp16 bits of the result.
-__device__ uint16_t g_gelu_lut[65536];
+// |x| < 10 (GeluFormula, unary.rs:522-541), and only 34796 values of q give
+// a result other than q or -0 (libm_replica.hpp, kGeluPosLimit/NegLimit).
+// Those results are computed once per device by the same replica code and
+// looked up: from this global copy by the strided kernels, from a copy in
+// LDS by k_gelu_lds.
+__device__ __align__(16) uint16_t g_gelu_tab[kGeluTableHalfs];
+
+constexpr uint32_t kGeluBlock = 1024; // threads per k_gelu_lds workgroup
+constexpr int kGeluPerCu = 2;         // two 68 KB tables fit the 160 KB LDS of a CU
+constexpr int kGeluU = 2;             // float4 per thread per step (measured best of 1, 2, 4, 8)
 
 __global__ __launch_bounds__(kBlock) void k_gelu_table()
 {
-    const uint32_t h = blockIdx.x * kBlock + threadIdx.x;
-    if (h < 65536u) g_gelu_lut[h] = emel_gelu_core_fp16(emel_fp16_to_f32(static_cast<uint16_t>(h)));
+    const uint32_t slot = blockIdx.x * kBlock + threadIdx.x;
+    if (slot < kGeluEntries)
+        g_gelu_tab[slot] = emel_gelu_core_fp16(emel_fp16_to_f32(gelu_slot_key(slot)));
+    else if (slot < kGeluTableHalfs)
+        g_gelu_tab[slot] = 0;
 }
 
-__device__ __forceinline__ float gelu_lut(float a)
+__device__ __forceinline__ float gelu_lookup(float a, const uint16_t *tab)
 {
-    if (a <= -10.0f) return 0.0f;
-    if (a >= 10.0f) return a;
-    return hw_fp16_to_f32(g_gelu_lut[hw_fp32_to_fp16(a)]);
+    const uint16_t h = hw_fp32_to_fp16(a);
+    const uint32_t slot = gelu_slot(h);
+    const float entry = hw_fp16_to_f32(tab[slot < kGeluEntries ? slot : 0u]);
+    return gelu_finish(a, hw_fp16_to_f32(h), slot, entry);
 }
 
-// Builds the table on the current device the first time a GELU runs there.
-hipError_t ensure_gelu_table(hipStream_t stream)
+struct DeviceInfo {
+    bool gelu_ready = false;
+    int cus = 0;
+};
+
+// Per-device facts the launchers need: the GELU table (built the first time
+// a GELU runs on the device) and the compute-unit count.
+hipError_t device_info(hipStream_t stream, bool need_gelu, DeviceInfo &out)
 {
     static std::mutex mu;
-    static std::set<int> ready;
+    static std::map<int, DeviceInfo> known;
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
     std::lock_guard<std::mutex> lock(mu);
-    if (ready.count(dev)) return hipSuccess;
-    k_gelu_table<<<dim3(65536 / kBlock), kBlock, 0, stream>>>();
-    e = hipGetLastError();
-    if (e == hipSuccess) e = hipStreamSynchronize(stream); // visible to every stream from now on
-    if (e == hipSuccess) ready.insert(dev);
-    return e;
+    DeviceInfo &d = known[dev];
+    if (d.cus == 0) {
+        e = hipDeviceGetAttribute(&d.cus, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return e;
+        if (d.cus <= 0) d.cus = 1;
+    }
+    if (need_gelu && !d.gelu_ready) {
+        k_gelu_table<<<dim3((kGeluTableHalfs + kBlock - 1) / kBlock), kBlock, 0, stream>>>();
+        e = hipGetLastError();
+        if (e == hipSuccess) e = hipStreamSynchronize(stream); // visible to every stream from now on
+        if (e != hipSuccess) return e;
+        d.gelu_ready = true;
+    }
+    out = d;
+    return hipSuccess;
 }
 
 // ---- per-element formulas ------------------------------------------------
@@ -91,7 +116,7 @@ EMEL_FN(Elu, false, false, a >= 0.0f ? a : emel_expm1f(a))
 // (NaN -> +0, and -0 -> +0).
 EMEL_FN(Relu, false, false, a > 0.0f ? a : 0.0f)
 EMEL_FN(Sigmoid, true, false, 1.0f / (1.0f + emel_expf(-a, t)))
-EMEL_FN(Gelu, false, false, gelu_lut(a))
+EMEL_FN(Gelu, false, false, gelu_lookup(a, g_gelu_tab))
 EMEL_FN(Silu, true, false, emel_silu(a, t))
 EMEL_FN(Exp, true, false, emel_expf(a, t))
 EMEL_FN(Scale, false, false, a * s)
@@ -160,6 +185,58 @@ __global__ __launch_bounds__(kBlock) void k_dense(const float *a, const float *b
     const uint64_t gid = static_cast<uint64_t>(blockIdx.x) * kBlock + threadIdx.x;
     const uint64_t idx = nvec * 4 + gid;
     if (idx < n) o[idx] = Fn<OP>::apply(a[idx], Fn<OP>::kBinary ? b[idx] : 0.0f, s, tab);
+}
+
+// ---- dense GELU with the table in LDS -----------------------------------
+// A gather from the global table touches up to 64 cache lines per wave; from
+// LDS it costs a few cycles.  Each workgroup stages the 68 KB table once
+// (its first data is already in flight meanwhile) and then walks the array
+// grid-stride, U float4 per thread per step, the next step's loads issued
+// before the current step's stores.
+template <int U>
+__global__ __launch_bounds__(kGeluBlock) void k_gelu_lds(const float *a, float *o, uint64_t nvec, uint64_t n)
+{
+    __shared__ __align__(16) uint16_t tab[kGeluTableHalfs];
+    const float4 *a4 = reinterpret_cast<const float4 *>(a);
+    float4 *o4 = reinterpret_cast<float4 *>(o);
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * (kGeluBlock * U);
+    uint64_t base = static_cast<uint64_t>(blockIdx.x) * (kGeluBlock * U) + threadIdx.x;
+    float4 v[U];
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+        const uint64_t i = base + static_cast<uint64_t>(j) * kGeluBlock;
+        if (i < nvec) v[j] = a4[i];
+    }
+    {
+        const uint4 *src = reinterpret_cast<const uint4 *>(g_gelu_tab);
+        uint4 *dst = reinterpret_cast<uint4 *>(tab);
+        for (uint32_t k = threadIdx.x; k < kGeluTableHalfs / 8u; k += kGeluBlock) dst[k] = src[k];
+    }
+    __syncthreads();
+    for (; base < nvec; base += stride) {
+        float4 r[U];
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+            r[j].x = gelu_lookup(v[j].x, tab);
+            r[j].y = gelu_lookup(v[j].y, tab);
+            r[j].z = gelu_lookup(v[j].z, tab);
+            r[j].w = gelu_lookup(v[j].w, tab);
+        }
+        const uint64_t next = base + stride;
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+            const uint64_t i = next + static_cast<uint64_t>(j) * kGeluBlock;
+            if (i < nvec) v[j] = a4[i];
+        }
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+            const uint64_t i = base + static_cast<uint64_t>(j) * kGeluBlock;
+            if (i < nvec) st_nt(o4 + i, r[j]);
+        }
+    }
+    const uint64_t gid = static_cast<uint64_t>(blockIdx.x) * kGeluBlock + threadIdx.x;
+    const uint64_t idx = nvec * 4 + gid;
+    if (idx < n) o[idx] = gelu_lookup(a[idx], tab);
 }
 
 // ---- dense [rows, ne0] op dense row [ne0], ne0 % 4 == 0 --------------------
@@ -340,8 +417,9 @@ hipError_t launch_op(const EwArgs &x, hipStream_t stream)
     float *o = static_cast<float *>(x.o.data);
     const uint64_t n = x.count;
     if (n == 0) return hipSuccess;
-    if constexpr (OP == Ew::Gelu) {
-        const hipError_t e = ensure_gelu_table(stream);
+    DeviceInfo dev{};
+    {
+        const hipError_t e = device_info(stream, OP == Ew::Gelu, dev);
         if (e != hipSuccess) return e;
     }
 
@@ -354,6 +432,16 @@ hipError_t launch_op(const EwArgs &x, hipStream_t stream)
     const bool vec_ok = aligned16(a) && aligned16(o) && (!kBin || aligned16(b));
 
     if (all_linear && vec_ok) {
+        if constexpr (OP == Ew::Gelu) {
+            const uint64_t nvec = n / 4;
+            const uint64_t per_block = static_cast<uint64_t>(kGeluBlock) * kGeluU;
+            uint64_t blocks = (nvec + per_block - 1) / per_block;
+            const uint64_t resident = static_cast<uint64_t>(dev.cus) * kGeluPerCu;
+            if (blocks > resident) blocks = resident;
+            if (blocks == 0) blocks = 1; // the scalar tail (n < 4)
+            k_gelu_lds<kGeluU><<<dim3(static_cast<uint32_t>(blocks)), kGeluBlock, 0, stream>>>(a, o, nvec, n);
+            return hipGetLastError();
+        }
         const int vpt = vpt_choice();
         const uint64_t nvec = n / 4;
         const uint64_t per_block = static_cast<uint64_t>(kBlock) * vpt;

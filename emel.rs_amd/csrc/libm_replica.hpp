@@ -294,4 +294,41 @@ __host__ __device__ __forceinline__ float emel_gelu(float value)
     return emel_fp16_to_f32(emel_gelu_core_fp16(q));
 }
 
+// ---- GELU by table -----------------------------------------------------------
+// For |x| < 10 the result depends only on q = fp16(x), and it saturates:
+// every fp16 q >= 3.380859375 (bits 0x42c3) gives exactly q, and every
+// q <= -5.16015625 (bits 0xc529) gives -0.0 (the product underflows fp16).
+// The table therefore holds the results for positive magnitudes below
+// 0x42c3 (slots 0 .. 0x42c2) then negative magnitudes below 0x4529 (slots
+// 0x42c3 ..): 34796 fp16 entries.  Both thresholds and the whole lookup
+// are checked against emel_gelu over all 2^32 inputs by the test suite.
+constexpr uint32_t kGeluPosLimit = 0x42c3u;
+constexpr uint32_t kGeluNegLimit = 0x4529u;
+constexpr uint32_t kGeluEntries = kGeluPosLimit + kGeluNegLimit;
+constexpr uint32_t kGeluTableHalfs = (kGeluEntries + 7u) / 8u * 8u; // padded to 16-byte rows
+
+// fp16 bits of the q that table slot `slot` holds the result for.
+__host__ __device__ __forceinline__ uint16_t gelu_slot_key(uint32_t slot)
+{
+    return static_cast<uint16_t>(slot < kGeluPosLimit ? slot : 0x8000u | (slot - kGeluPosLimit));
+}
+
+// Table slot of fp16 bits h, or kGeluEntries when q saturates (or is NaN).
+__host__ __device__ __forceinline__ uint32_t gelu_slot(uint16_t h)
+{
+    const uint32_t mag = h & 0x7fffu;
+    if (h & 0x8000u) return mag < kGeluNegLimit ? kGeluPosLimit + mag : kGeluEntries;
+    return mag < kGeluPosLimit ? mag : kGeluEntries;
+}
+
+// GeluFormula from the looked-up entry: x the input, q = fp16(x) widened,
+// entry the widened table value at gelu_slot (ignored when saturated).
+__host__ __device__ __forceinline__ float gelu_finish(float x, float q, uint32_t slot, float entry)
+{
+    float y = slot < kGeluEntries ? entry : (q < 0.0f ? -0.0f : q);
+    if (x <= -10.0f) y = 0.0f;
+    if (x >= 10.0f || x != x) y = x;
+    return y;
+}
+
 } // namespace emel

@@ -7,9 +7,11 @@
 // workgroup reduces its range (f64 sums; (value, index) maxima) and writes
 // one partial; a second kernel with one wave per row combines the row's
 // partials in a fixed tree order.  The kernel boundary makes the partials
-// visible across XCDs without in-kernel fences (an agent-scope fence costs
-// an L2 write-back and invalidate per workgroup on gfx950).  Results are
-// deterministic run to run.
+// visible across XCDs without in-kernel fences: an agent-scope fence costs
+// an L2 write-back and invalidate per workgroup on gfx950, and a single pass
+// that hands partials over through agent-scope atomics measured 1.3-3.6x
+// slower than the second launch (contention on the per-row counter).
+// Results are deterministic run to run.
 //
 // argmax keeps the reference's sequential strict-> scan semantics: the
 // winner is the lowest index among the maximal non-NaN values, NaNs never
@@ -76,9 +78,7 @@ __device__ __forceinline__ void accumulate(const RedGeo &g, const float *x, int6
     };
     if (g.mode == kModeVec) {
         const float4 *x4 = reinterpret_cast<const float4 *>(x + base);
-        for (uint64_t v = c0 / 4 + threadIdx.x; v < c1 / 4; v += kBlock) {
-            const float4 q = x4[v];
-            const uint64_t c = 4 * v;
+        auto take4 = [&](const float4 &q, uint64_t c) {
             if constexpr (kArg) {
                 take(q.x, c);
                 take(q.y, c + 1);
@@ -88,7 +88,19 @@ __device__ __forceinline__ void accumulate(const RedGeo &g, const float *x, int6
                 sum += (static_cast<double>(q.x) + static_cast<double>(q.y)) +
                        (static_cast<double>(q.z) + static_cast<double>(q.w));
             }
+        };
+        // kUnroll loads in flight per thread, then taken in column order
+        constexpr int kUnroll = 4;
+        const uint64_t vend = c1 / 4;
+        uint64_t v = c0 / 4 + threadIdx.x;
+        for (; v + (kUnroll - 1) * kBlock < vend; v += kUnroll * kBlock) {
+            float4 q[kUnroll];
+#pragma unroll
+            for (int j = 0; j < kUnroll; ++j) q[j] = x4[v + j * kBlock];
+#pragma unroll
+            for (int j = 0; j < kUnroll; ++j) take4(q[j], 4 * (v + j * kBlock));
         }
+        for (; v < vend; v += kBlock) take4(x4[v], 4 * v);
     } else if (g.mode == kModeScalar) {
         for (uint64_t c = c0 + threadIdx.x; c < c1; c += kBlock) take(x[base + static_cast<int64_t>(c) * g.x_st[0]], c);
     } else {

@@ -109,6 +109,8 @@ __device__ __forceinline__ float4 exp4(float4 v, const uint64_t *t)
 // and written with non-temporal accesses (each byte moves once); weights
 // and masks stay on the cached path.  Rows run in memory order.
 
+// Row reductions over the NW waves of a row: wave partials go to LDS slots
+// [first wave of the row, + NW); the slots are fixed, so the sum's order is.
 template <int NW>
 __device__ __forceinline__ double row_sum(double v, double *lds)
 {
@@ -116,11 +118,13 @@ __device__ __forceinline__ double row_sum(double v, double *lds)
     if constexpr (NW == 1) {
         return v;
     } else {
-        if (threadIdx.x % kWave == 0) lds[threadIdx.x / kWave] = v;
+        const uint32_t w = threadIdx.x / kWave;
+        if (threadIdx.x % kWave == 0) lds[w] = v;
         __syncthreads();
-        double t = lds[0];
+        const double *p = lds + (w / NW) * NW;
+        double t = p[0];
 #pragma unroll
-        for (int i = 1; i < NW; ++i) t += lds[i];
+        for (int i = 1; i < NW; ++i) t += p[i];
         return t;
     }
 }
@@ -132,25 +136,28 @@ __device__ __forceinline__ float row_max(float v, double *lds)
     if constexpr (NW == 1) {
         return v;
     } else {
-        if (threadIdx.x % kWave == 0) lds[threadIdx.x / kWave] = v;
+        const uint32_t w = threadIdx.x / kWave;
+        if (threadIdx.x % kWave == 0) lds[w] = v;
         __syncthreads();
-        float t = static_cast<float>(lds[0]);
+        const double *p = lds + (w / NW) * NW;
+        float t = static_cast<float>(p[0]);
 #pragma unroll
-        for (int i = 1; i < NW; ++i) t = __builtin_fmaxf(t, static_cast<float>(lds[i]));
+        for (int i = 1; i < NW; ++i) t = __builtin_fmaxf(t, static_cast<float>(p[i]));
         return t;
     }
 }
 
-template <RowOp OP, int NW, int NV, bool FULL, bool MASK>
-__global__ __launch_bounds__(kBlock) void k_row_vec(RowGeo g, const float *x, float *y, const float *w, MaskGeo mg,
-                                                     float eps, float scale)
+template <RowOp OP, int NW, int NV, bool FULL, bool MASK, int BS = kBlock>
+__global__ __launch_bounds__(BS) void k_row_vec(RowGeo g, const float *x, float *y, const float *w, MaskGeo mg,
+                                                 float eps, float scale)
 {
     constexpr bool kSoft = OP == RowOp::SoftMax || OP == RowOp::SoftMaxExt;
     constexpr uint32_t kTPR = NW * kWave;      // threads per row
-    constexpr uint32_t kRPB = kBlock / kTPR;   // rows per workgroup
+    constexpr uint32_t kRPB = BS / kTPR;       // rows per workgroup
+    static_assert(kRPB >= 1 && BS % kTPR == 0, "a workgroup holds whole rows");
     __shared__ uint64_t lds_tab[32];
-    __shared__ double lds_a[kBlock / kWave];   // first row reduction
-    __shared__ double lds_b[kBlock / kWave];   // second row reduction
+    __shared__ double lds_a[BS / kWave];       // first row reduction
+    __shared__ double lds_b[BS / kWave];       // second row reduction
     const uint64_t *tab = nullptr;
     if constexpr (kSoft) {
         if (threadIdx.x < 32) lds_tab[threadIdx.x] = kExp2Table[threadIdx.x];
@@ -164,7 +171,12 @@ __global__ __launch_bounds__(kBlock) void k_row_vec(RowGeo g, const float *x, fl
         r = blockIdx.x;
     } else {
         r = blockIdx.x * kRPB + __builtin_amdgcn_readfirstlane(threadIdx.x / kTPR);
-        if (r >= g.rows) return; // no workgroup barrier follows when NW == 1
+        // NW == 1: no workgroup barrier follows, so a wave past the end may
+        // leave.  NW > 1: the host launches these only when kRPB divides
+        // the row count, so every row of every workgroup exists.
+        if constexpr (NW == 1) {
+            if (r >= g.rows) return;
+        }
     }
 
     uint32_t i1, i2, i3;

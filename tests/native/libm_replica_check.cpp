@@ -122,6 +122,28 @@ uint64_t check_div_recip_random(uint64_t seed, uint64_t n, int threads)
     });
 }
 
+// The table-driven GELU of the kernels (gelu_slot / gelu_finish over a
+// table filled like k_gelu_table) against emel_gelu for every input in
+// [lo, hi).  Also counts table slots whose key maps back to another slot.
+uint64_t check_gelu_table(uint64_t lo, uint64_t hi, int threads)
+{
+    std::vector<uint16_t> tab(emel::kGeluTableHalfs, 0);
+    uint64_t bad = 0;
+    for (uint32_t slot = 0; slot < emel::kGeluEntries; ++slot) {
+        const uint16_t key = emel::gelu_slot_key(slot);
+        if (emel::gelu_slot(key) != slot) ++bad;
+        tab[slot] = emel::emel_gelu_core_fp16(emel::emel_fp16_to_f32(key));
+    }
+    const uint16_t *t = tab.data();
+    return bad + count_range(lo, hi, threads, [t](uint32_t u) {
+        const float x = emel::bits_to_f32(u);
+        const uint16_t h = emel::emel_fp32_to_fp16(x);
+        const uint32_t slot = emel::gelu_slot(h);
+        const float entry = emel::emel_fp16_to_f32(t[slot < emel::kGeluEntries ? slot : 0u]);
+        return differ(emel::gelu_finish(x, emel::emel_fp16_to_f32(h), slot, entry), emel::emel_gelu(x));
+    });
+}
+
 // Scalar values for the golden-vector tests (unary manifest inputs).
 float replica_silu(float x) { return emel::emel_silu(x, emel::kExp2Table); }
 float replica_gelu(float x) { return emel::emel_gelu(x); }

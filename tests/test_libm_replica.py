@@ -5,7 +5,9 @@ checkers over ALL 2^32 float inputs:
   expf, expm1f, tanhf  == the host glibc (Rust std's f32::exp/exp_m1/tanh on
                           x86_64-linux-gnu, i.e. what the reference computes);
   fp32 -> fp16         == IEEE round-to-nearest-even (_Float16 conversion);
-  fp16 -> fp32         == exact widening.
+  fp16 -> fp32         == exact widening;
+  GELU by table        == the formula (the kernels' saturation thresholds
+                          and compact table layout).
 
 The GPU kernels run this same code, so a GPU result can differ from the
 oracle only through the GPU's IEEE basic operations, which the GPU tests
@@ -26,7 +28,7 @@ def chk():
     if not LIB.exists():
         pytest.fail(f"{LIB} missing: run __graft_entry__.build()")
     L = ctypes.CDLL(str(LIB))
-    for n in ("check_expf", "check_expm1f", "check_tanhf", "check_fp32_to_fp16"):
+    for n in ("check_expf", "check_expm1f", "check_tanhf", "check_fp32_to_fp16", "check_gelu_table"):
         getattr(L, n).restype = ctypes.c_uint64
         getattr(L, n).argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int]
     L.check_fp16_to_f32.restype = ctypes.c_uint64
@@ -36,7 +38,7 @@ def chk():
     return L
 
 
-@pytest.mark.parametrize("fn", ["check_expf", "check_expm1f", "check_tanhf", "check_fp32_to_fp16"])
+@pytest.mark.parametrize("fn", ["check_expf", "check_expm1f", "check_tanhf", "check_fp32_to_fp16", "check_gelu_table"])
 def test_exhaustive(chk, fn):
     assert getattr(chk, fn)(0, 1 << 32, THREADS) == 0
 
