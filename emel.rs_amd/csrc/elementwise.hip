@@ -151,10 +151,13 @@ __device__ __forceinline__ const uint64_t *stage_table(uint64_t *lds)
 // ---- dense: every operand contiguous, paired by linear index -------------
 
 // Streaming policy measured on MI355X: unary ops read with cached loads and
-// write non-temporally; binary ops stream both ways.
+// write non-temporally; binary ops stream both ways.  Ops with libm work per
+// element run one float4 per thread (more waves to overlap the arithmetic
+// with memory), the others two.
 template <Ew OP>
 struct Stream {
     static constexpr bool kNtLoad = Fn<OP>::kBinary;
+    static constexpr int kVpt = Fn<OP>::kTable || OP == Ew::Tanh || OP == Ew::Elu ? 1 : 2;
 };
 
 template <Ew OP, int VPT>
@@ -398,16 +401,6 @@ bool same_ne(const Operand &x, const Operand &y)
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-int vpt_choice()
-{
-    static const int v = [] {
-        const char *e = getenv("EMEL_EW_VPT");
-        const int x = e ? atoi(e) : 2;
-        return (x == 1 || x == 2 || x == 4) ? x : 2;
-    }();
-    return v;
-}
-
 template <Ew OP>
 hipError_t launch_op(const EwArgs &x, hipStream_t stream)
 {
@@ -442,7 +435,7 @@ hipError_t launch_op(const EwArgs &x, hipStream_t stream)
             k_gelu_lds<kGeluU><<<dim3(static_cast<uint32_t>(blocks)), kGeluBlock, 0, stream>>>(a, o, nvec, n);
             return hipGetLastError();
         }
-        const int vpt = vpt_choice();
+        constexpr int vpt = Stream<OP>::kVpt;
         const uint64_t nvec = n / 4;
         const uint64_t per_block = static_cast<uint64_t>(kBlock) * vpt;
         const uint64_t tail = n - nvec * 4;
@@ -451,9 +444,7 @@ hipError_t launch_op(const EwArgs &x, hipStream_t stream)
         if (blocks < tail_blocks) blocks = tail_blocks;
         if (blocks > 0x7fffffffull) return hipErrorInvalidConfiguration;
         const dim3 grid(static_cast<uint32_t>(blocks));
-        if (vpt == 1) k_dense<OP, 1><<<grid, kBlock, 0, stream>>>(a, b, o, nvec, n, x.scale);
-        else if (vpt == 2) k_dense<OP, 2><<<grid, kBlock, 0, stream>>>(a, b, o, nvec, n, x.scale);
-        else k_dense<OP, 4><<<grid, kBlock, 0, stream>>>(a, b, o, nvec, n, x.scale);
+        k_dense<OP, vpt><<<grid, kBlock, 0, stream>>>(a, b, o, nvec, n, x.scale);
         return hipGetLastError();
     }
 
@@ -464,14 +455,12 @@ hipError_t launch_op(const EwArgs &x, hipStream_t stream)
     if (kBin && ne0 % 4 == 0 && vec_ok && contiguous(x.o) && contiguous(x.a) && same_ne(x.a, x.o) &&
         x.a_addr != Addr::Ordinal && x.b.ne[0] == ne0 && x.b.ne[1] == 1 && x.b.ne[2] == 1 && x.b.ne[3] == 1 &&
         x.b.st[0] == 1 && n / 4 < 0xffffffffull && x.b_addr != Addr::Ordinal) {
-        const int vpt = vpt_choice();
+        constexpr int vpt = Stream<OP>::kVpt;
         const uint32_t nvec = static_cast<uint32_t>(n / 4);
         const uint32_t per_block = kBlock * vpt;
         const dim3 grid((nvec + per_block - 1) / per_block);
         const FastDiv nv0(static_cast<uint32_t>(ne0 / 4));
-        if (vpt == 1) k_rowbcast<OP, 1><<<grid, kBlock, 0, stream>>>(a, b, o, nvec, nv0, x.scale);
-        else if (vpt == 2) k_rowbcast<OP, 2><<<grid, kBlock, 0, stream>>>(a, b, o, nvec, nv0, x.scale);
-        else k_rowbcast<OP, 4><<<grid, kBlock, 0, stream>>>(a, b, o, nvec, nv0, x.scale);
+        k_rowbcast<OP, vpt><<<grid, kBlock, 0, stream>>>(a, b, o, nvec, nv0, x.scale);
         return hipGetLastError();
     }
 

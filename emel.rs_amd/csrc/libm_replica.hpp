@@ -49,45 +49,14 @@ __host__ __device__ __forceinline__ uint32_t f32_to_bits(float f) { return __bui
 __host__ __device__ __forceinline__ double bits_to_f64(uint64_t u) { return __builtin_bit_cast(double, u); }
 __host__ __device__ __forceinline__ uint64_t f64_to_bits(double d) { return __builtin_bit_cast(uint64_t, d); }
 
-// expf.  `tab` is kExp2Table or a copy of it (kernels stage it in LDS).
-__host__ __device__ __forceinline__ float emel_expf(float x, const uint64_t *tab)
+// The main path of expf: x*N/ln2 = k + r, 2^(k/N) from the table, the
+// cubic in r, all in double.  Defined (and in range for the table index)
+// for every x; the result is expf(x) whenever -0x1.9fe368p6 <= x <=
+// 0x1.62e42ep6, the range in which glibc takes this path.
+__host__ __device__ __forceinline__ float expf_main_path(float x, const uint64_t *tab)
 {
     // N/ln2 with N = 32, the rounding shift 1.5*2^52, and the cubic
     // coefficients of 2^(r/N) - 1 pre-scaled by N^-1, N^-2, N^-3.
-    constexpr double kInvLn2N = 0x1.71547652b82fep+0 * 32.0;
-    constexpr double kShift = 0x1.8p+52;
-    constexpr double kC0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
-    constexpr double kC1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
-    constexpr double kC2 = 0x1.62e42ff0c52d6p-1 / 32.0;
-
-    const uint32_t ux = f32_to_bits(x);
-    const uint32_t abstop = (ux >> 20) & 0x7ffu;
-    if (abstop >= 0x42bu) { // |x| >= 88 or x is NaN/Inf
-        if (ux == 0xff800000u) return 0.0f;           // -inf
-        if (abstop >= 0x7f8u) return x + x;           // +inf or NaN
-        if (x > 0x1.62e42ep6f) return __builtin_inff(); // overflow
-        if (x < -0x1.9fe368p6f) return 0.0f;           // underflow
-    }
-    const double xd = static_cast<double>(x);
-    double kd = __builtin_fma(kInvLn2N, xd, kShift);
-    const uint64_t ki = f64_to_bits(kd);
-    kd -= kShift;
-    const double r = __builtin_fma(kInvLn2N, xd, -kd);
-    const uint64_t t = tab[ki & 31u] + (ki << 47);
-    const double s = bits_to_f64(t);
-    const double z = __builtin_fma(kC0, r, kC1);
-    const double r2 = r * r;
-    double y = __builtin_fma(kC2, r, 1.0);
-    y = __builtin_fma(z, r2, y);
-    y = y * s;
-    return static_cast<float>(y);
-}
-
-// expf for arguments that are <= 0 or NaN (soft_max's x - max): the same
-// bits as emel_expf, with the special cases folded into one select, since
-// only the underflow (and -inf) case can occur.
-__host__ __device__ __forceinline__ float emel_expf_nonpos(float x, const uint64_t *tab)
-{
     constexpr double kInvLn2N = 0x1.71547652b82fep+0 * 32.0;
     constexpr double kShift = 0x1.8p+52;
     constexpr double kC0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
@@ -104,8 +73,30 @@ __host__ __device__ __forceinline__ float emel_expf_nonpos(float x, const uint64
     double y = __builtin_fma(kC2, r, 1.0);
     y = __builtin_fma(z, r2, y);
     y = y * s;
+    return static_cast<float>(y);
+}
+
+// expf.  `tab` is kExp2Table or a copy of it (kernels stage it in LDS).
+// glibc branches to its special cases (|x| >= 88, NaN, infinities) before
+// the main path; here the main path always runs and the special results
+// are selected afterwards, which keeps a wave free of divergent branches:
+// overflow (x > 0x1.62e42ep6, +inf) -> +inf, underflow (x < -0x1.9fe368p6,
+// -inf) -> 0, NaN -> x + x.
+__host__ __device__ __forceinline__ float emel_expf(float x, const uint64_t *tab)
+{
+    float y = expf_main_path(x, tab);
+    y = x > 0x1.62e42ep6f ? __builtin_inff() : y;
+    y = x < -0x1.9fe368p6f ? 0.0f : y;
+    return x != x ? x + x : y;
+}
+
+// expf for arguments that are <= 0 or NaN (soft_max's x - max): the same
+// bits as emel_expf, with the special cases folded into one select, since
+// only the underflow (and -inf) case can occur.
+__host__ __device__ __forceinline__ float emel_expf_nonpos(float x, const uint64_t *tab)
+{
     // x < log(2^-150) (including -inf): 0, as emel_expf returns
-    return x < -0x1.9fe368p6f ? 0.0f : static_cast<float>(y);
+    return x < -0x1.9fe368p6f ? 0.0f : expf_main_path(x, tab);
 }
 
 // Correctly rounded f32 quotient a / b through a double reciprocal:
