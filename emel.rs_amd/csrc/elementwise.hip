@@ -91,13 +91,20 @@ hipError_t device_info(hipStream_t stream, bool need_gelu, DeviceInfo &out)
 
 // ---- per-element formulas ------------------------------------------------
 
+// What the exp-based formulas read: the 2^(i/32) table (in LDS) and the
+// expf constants (in vector registers).
+struct ExpCtx {
+    const uint64_t *tab;
+    ExpfConsts c;
+};
+
 template <Ew OP> struct Fn;
 
 #define EMEL_FN(OPV, TABLE, BINARY, EXPR)                                                          \
     template <> struct Fn<Ew::OPV> {                                                                \
         static constexpr bool kTable = TABLE;                                                       \
         static constexpr bool kBinary = BINARY;                                                     \
-        __device__ __forceinline__ static float apply(float a, float b, float s, const uint64_t *t) \
+        __device__ __forceinline__ static float apply(float a, float b, float s, const ExpCtx &t) \
         {                                                                                           \
             (void)b; (void)s; (void)t;                                                              \
             return EXPR;                                                                            \
@@ -115,17 +122,17 @@ EMEL_FN(Elu, false, false, a >= 0.0f ? a : emel_expm1f(a))
 // f32::max(x, 0.0) with glibc fmaxf's results: x when x > 0, otherwise +0
 // (NaN -> +0, and -0 -> +0).
 EMEL_FN(Relu, false, false, a > 0.0f ? a : 0.0f)
-EMEL_FN(Sigmoid, true, false, 1.0f / (1.0f + emel_expf(-a, t)))
+EMEL_FN(Sigmoid, true, false, 1.0f / (1.0f + emel_expf(-a, t.tab, t.c)))
 EMEL_FN(Gelu, false, false, gelu_lookup(a, g_gelu_tab))
-EMEL_FN(Silu, true, false, emel_silu(a, t))
-EMEL_FN(Exp, true, false, emel_expf(a, t))
+EMEL_FN(Silu, true, false, emel_silu(a, t.tab, t.c))
+EMEL_FN(Exp, true, false, emel_expf(a, t.tab, t.c))
 EMEL_FN(Scale, false, false, a * s)
 // silu(gate) rounded to f32, then times up: the OpSilu -> OpMul chain.
-EMEL_FN(Swiglu, true, true, emel_silu(a, t) * b)
+EMEL_FN(Swiglu, true, true, emel_silu(a, t.tab, t.c) * b)
 #undef EMEL_FN
 
 template <Ew OP>
-__device__ __forceinline__ float4 apply4(float4 a, float4 b, float s, const uint64_t *t)
+__device__ __forceinline__ float4 apply4(float4 a, float4 b, float s, const ExpCtx &t)
 {
     float4 r;
     r.x = Fn<OP>::apply(a.x, b.x, s, t);
@@ -135,16 +142,17 @@ __device__ __forceinline__ float4 apply4(float4 a, float4 b, float s, const uint
     return r;
 }
 
-// Stages the 2^(i/32) table in LDS for the exp-based formulas.
+// Stages the 2^(i/32) table in LDS for the exp-based formulas and pins the
+// expf constants in vector registers.
 template <Ew OP>
-__device__ __forceinline__ const uint64_t *stage_table(uint64_t *lds)
+__device__ __forceinline__ ExpCtx stage_table(uint64_t *lds)
 {
     if constexpr (Fn<OP>::kTable) {
         if (threadIdx.x < 32) lds[threadIdx.x] = kExp2Table[threadIdx.x];
         __syncthreads();
-        return lds;
+        return ExpCtx{lds, expf_consts_in_vgprs()};
     } else {
-        return nullptr;
+        return ExpCtx{nullptr, ExpfConsts{}};
     }
 }
 
@@ -165,7 +173,7 @@ __global__ __launch_bounds__(kBlock) void k_dense(const float *a, const float *b
                                                    uint64_t n, float s)
 {
     __shared__ uint64_t lds[32];
-    const uint64_t *tab = stage_table<OP>(lds);
+    const ExpCtx tab = stage_table<OP>(lds);
     const float4 *a4 = reinterpret_cast<const float4 *>(a);
     const float4 *b4 = reinterpret_cast<const float4 *>(b);
     float4 *o4 = reinterpret_cast<float4 *>(o);
@@ -249,7 +257,7 @@ __global__ __launch_bounds__(kBlock) void k_rowbcast(const float *a, const float
                                                       FastDiv nv0, float s)
 {
     __shared__ uint64_t lds[32];
-    const uint64_t *tab = stage_table<OP>(lds);
+    const ExpCtx tab = stage_table<OP>(lds);
     const float4 *a4 = reinterpret_cast<const float4 *>(a);
     const float4 *b4 = reinterpret_cast<const float4 *>(b);
     float4 *o4 = reinterpret_cast<float4 *>(o);
@@ -295,7 +303,7 @@ template <Ew OP>
 __global__ __launch_bounds__(kBlock) void k_rows(RowsGeo g, const float *a, const float *b, float *o, float s)
 {
     __shared__ uint64_t lds[32];
-    const uint64_t *tab = stage_table<OP>(lds);
+    const ExpCtx tab = stage_table<OP>(lds);
     const uint32_t i = blockIdx.x * kBlock + threadIdx.x;
     if (i >= g.nvec) return;
     const uint32_t row = g.nv0.div(i);
@@ -360,7 +368,7 @@ template <Ew OP>
 __global__ __launch_bounds__(kBlock) void k_ordinal(OrdGeo g, const float *a, const float *b, float *o, float s)
 {
     __shared__ uint64_t lds[32];
-    const uint64_t *tab = stage_table<OP>(lds);
+    const ExpCtx tab = stage_table<OP>(lds);
     const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kBlock;
     for (uint64_t k = static_cast<uint64_t>(blockIdx.x) * kBlock + threadIdx.x; k < g.count; k += stride) {
         uint64_t c[4];

@@ -18,9 +18,10 @@
 //   emel_tanhf   fdlibm s_tanhf.c: tanh(x) = 1 - 2/(expm1(2|x|)+2) for
 //                |x| >= 1, -t/(t+2) with t = expm1(-2|x|) below.
 //
-// The 2^(i/32) table is the correctly rounded double of 2^(i/32) with the
-// exponent contribution i << 47 subtracted, so that adding k << 47 yields
-// 2^(k/32) for any integer k.
+// The table holds the correctly rounded doubles of 2^(i/32).  glibc stores
+// them with i << 47 subtracted and forms 2^(k/32) as tab[k % 32] + (k << 47)
+// on the bit patterns; here 2^(k/32) = ldexp(tab[k % 32], floor(k / 32)),
+// the same double whenever it is normal (always, on the main path).
 //
 // Every function is __host__ __device__: tests build them for the CPU and
 // compare them with the host glibc over all 2^32 float inputs.  Compile
@@ -32,16 +33,16 @@
 
 namespace emel {
 
-// tab[i] = bits(2^(i/32)) - (i << 47), i = 0..31.
+// tab[i] = bits(2^(i/32)), the double nearest 2^(i/32), i = 0..31.
 static constexpr uint64_t kExp2Table[32] = {
-    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
-    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
-    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
-    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
-    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
-    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
-    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
-    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
+    0x3ff0000000000000ull, 0x3ff059b0d3158574ull, 0x3ff0b5586cf9890full, 0x3ff11301d0125b51ull,
+    0x3ff172b83c7d517bull, 0x3ff1d4873168b9aaull, 0x3ff2387a6e756238ull, 0x3ff29e9df51fdee1ull,
+    0x3ff306fe0a31b715ull, 0x3ff371a7373aa9cbull, 0x3ff3dea64c123422ull, 0x3ff44e086061892dull,
+    0x3ff4bfdad5362a27ull, 0x3ff5342b569d4f82ull, 0x3ff5ab07dd485429ull, 0x3ff6247eb03a5585ull,
+    0x3ff6a09e667f3bcdull, 0x3ff71f75e8ec5f74ull, 0x3ff7a11473eb0187ull, 0x3ff82589994cce13ull,
+    0x3ff8ace5422aa0dbull, 0x3ff93737b0cdc5e5ull, 0x3ff9c49182a3f090ull, 0x3ffa5503b23e255dull,
+    0x3ffae89f995ad3adull, 0x3ffb7f76f2fb5e47ull, 0x3ffc199bdd85529cull, 0x3ffcb720dcef9069ull,
+    0x3ffd5818dcfba487ull, 0x3ffdfc97337b9b5full, 0x3ffea4afa2a490daull, 0x3fff50765b6e4540ull,
 };
 
 __host__ __device__ __forceinline__ float bits_to_f32(uint32_t u) { return __builtin_bit_cast(float, u); }
@@ -49,28 +50,59 @@ __host__ __device__ __forceinline__ uint32_t f32_to_bits(float f) { return __bui
 __host__ __device__ __forceinline__ double bits_to_f64(uint64_t u) { return __builtin_bit_cast(double, u); }
 __host__ __device__ __forceinline__ uint64_t f64_to_bits(double d) { return __builtin_bit_cast(uint64_t, d); }
 
+// Constants of the expf main path: N/ln2 with N = 32, the rounding shift
+// 1.5*2^52, and the cubic coefficients of 2^(r/N) - 1 pre-scaled by N^-1,
+// N^-2, N^-3.
+struct ExpfConsts {
+    double inv_ln2n = 0x1.71547652b82fep+0 * 32.0;
+    double shift = 0x1.8p+52;
+    double c0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+    double c1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+    double c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+};
+
+// The constants held in vector registers for a whole kernel.  gfx950's
+// three-operand double instructions take no literals and one scalar
+// operand, so fma(c, r, c') would otherwise rebuild a constant in vector
+// registers for every element.
+__host__ __device__ __forceinline__ ExpfConsts expf_consts_in_vgprs()
+{
+    ExpfConsts c;
+#if defined(__HIP_DEVICE_COMPILE__)
+    asm volatile("" : "+v"(c.inv_ln2n), "+v"(c.shift), "+v"(c.c0), "+v"(c.c1), "+v"(c.c2));
+#endif
+    return c;
+}
+
+// Marks y as computed on every path: the compiler may not sink its
+// computation into the branch of a later select (a divergent branch per
+// element costs more than the arithmetic it would skip).
+__host__ __device__ __forceinline__ float keep_unconditional(float y)
+{
+#if defined(__HIP_DEVICE_COMPILE__)
+    asm volatile("" : "+v"(y));
+#endif
+    return y;
+}
+
 // The main path of expf: x*N/ln2 = k + r, 2^(k/N) from the table, the
 // cubic in r, all in double.  Defined (and in range for the table index)
 // for every x; the result is expf(x) whenever -0x1.9fe368p6 <= x <=
 // 0x1.62e42ep6, the range in which glibc takes this path.
-__host__ __device__ __forceinline__ float expf_main_path(float x, const uint64_t *tab)
+__host__ __device__ __forceinline__ float expf_main_path(float x, const uint64_t *tab,
+                                                         const ExpfConsts &c = ExpfConsts{})
 {
-    // N/ln2 with N = 32, the rounding shift 1.5*2^52, and the cubic
-    // coefficients of 2^(r/N) - 1 pre-scaled by N^-1, N^-2, N^-3.
-    constexpr double kInvLn2N = 0x1.71547652b82fep+0 * 32.0;
-    constexpr double kShift = 0x1.8p+52;
-    constexpr double kC0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
-    constexpr double kC1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
-    constexpr double kC2 = 0x1.62e42ff0c52d6p-1 / 32.0;
     const double xd = static_cast<double>(x);
-    double kd = __builtin_fma(kInvLn2N, xd, kShift);
+    double kd = __builtin_fma(c.inv_ln2n, xd, c.shift);
     const uint64_t ki = f64_to_bits(kd);
-    kd -= kShift;
-    const double r = __builtin_fma(kInvLn2N, xd, -kd);
-    const double s = bits_to_f64(tab[ki & 31u] + (ki << 47));
-    const double z = __builtin_fma(kC0, r, kC1);
+    kd -= c.shift;
+    const double r = __builtin_fma(c.inv_ln2n, xd, -kd);
+    // k is the low word of kd's bits; 2^(k/N) = 2^((k mod N)/N) * 2^floor(k/N)
+    const int32_t k = static_cast<int32_t>(static_cast<uint32_t>(ki));
+    const double s = __builtin_ldexp(bits_to_f64(tab[k & 31]), k >> 5);
+    const double z = __builtin_fma(c.c0, r, c.c1);
     const double r2 = r * r;
-    double y = __builtin_fma(kC2, r, 1.0);
+    double y = __builtin_fma(c.c2, r, 1.0);
     y = __builtin_fma(z, r2, y);
     y = y * s;
     return static_cast<float>(y);
@@ -82,9 +114,10 @@ __host__ __device__ __forceinline__ float expf_main_path(float x, const uint64_t
 // are selected afterwards, which keeps a wave free of divergent branches:
 // overflow (x > 0x1.62e42ep6, +inf) -> +inf, underflow (x < -0x1.9fe368p6,
 // -inf) -> 0, NaN -> x + x.
-__host__ __device__ __forceinline__ float emel_expf(float x, const uint64_t *tab)
+__host__ __device__ __forceinline__ float emel_expf(float x, const uint64_t *tab,
+                                                    const ExpfConsts &c = ExpfConsts{})
 {
-    float y = expf_main_path(x, tab);
+    float y = keep_unconditional(expf_main_path(x, tab, c));
     y = x > 0x1.62e42ep6f ? __builtin_inff() : y;
     y = x < -0x1.9fe368p6f ? 0.0f : y;
     return x != x ? x + x : y;
@@ -93,10 +126,12 @@ __host__ __device__ __forceinline__ float emel_expf(float x, const uint64_t *tab
 // expf for arguments that are <= 0 or NaN (soft_max's x - max): the same
 // bits as emel_expf, with the special cases folded into one select, since
 // only the underflow (and -inf) case can occur.
-__host__ __device__ __forceinline__ float emel_expf_nonpos(float x, const uint64_t *tab)
+__host__ __device__ __forceinline__ float emel_expf_nonpos(float x, const uint64_t *tab,
+                                                           const ExpfConsts &c = ExpfConsts{})
 {
     // x < log(2^-150) (including -inf): 0, as emel_expf returns
-    return x < -0x1.9fe368p6f ? 0.0f : expf_main_path(x, tab);
+    const float y = keep_unconditional(expf_main_path(x, tab, c));
+    return x < -0x1.9fe368p6f ? 0.0f : y;
 }
 
 // Correctly rounded f32 quotient a / b through a double reciprocal:
@@ -270,9 +305,9 @@ __host__ __device__ __forceinline__ uint16_t emel_gelu_core_fp16(float q)
 }
 
 // SiluFormula (unary.rs:595-600).
-__host__ __device__ __forceinline__ float emel_silu(float x, const uint64_t *tab)
+__host__ __device__ __forceinline__ float emel_silu(float x, const uint64_t *tab, const ExpfConsts &c = ExpfConsts{})
 {
-    return x / (1.0f + emel_expf(-x, tab));
+    return x / (1.0f + emel_expf(-x, tab, c));
 }
 
 // GeluFormula (unary.rs:522-541): separate products, fp16 round trips on

@@ -94,10 +94,10 @@ __device__ __forceinline__ float4 div4(float4 v, double recip)
                        div_by_recip(v.w, recip));
 }
 // exp(v - max): arguments are <= 0 or NaN.
-__device__ __forceinline__ float4 exp4(float4 v, const uint64_t *t)
+__device__ __forceinline__ float4 exp4(float4 v, const uint64_t *t, const ExpfConsts &c)
 {
-    return make_float4(emel_expf_nonpos(v.x, t), emel_expf_nonpos(v.y, t), emel_expf_nonpos(v.z, t),
-                       emel_expf_nonpos(v.w, t));
+    return make_float4(emel_expf_nonpos(v.x, t, c), emel_expf_nonpos(v.y, t, c), emel_expf_nonpos(v.z, t, c),
+                       emel_expf_nonpos(v.w, t, c));
 }
 
 // ---- vectorized rows: contiguous dim 0, ncols % 4 == 0 ------------------
@@ -159,11 +159,13 @@ __global__ __launch_bounds__(BS) void k_row_vec(RowGeo g, const float *x, float 
     __shared__ double lds_a[BS / kWave];       // first row reduction
     __shared__ double lds_b[BS / kWave];       // second row reduction
     const uint64_t *tab = nullptr;
+    ExpfConsts ec;
     if constexpr (kSoft) {
         if (threadIdx.x < 32) lds_tab[threadIdx.x] = kExp2Table[threadIdx.x];
         // with NW > 1 the max reduction's barrier orders the table before use
         if constexpr (NW == 1) __syncthreads();
         tab = lds_tab;
+        ec = expf_consts_in_vgprs();
     }
     const uint32_t t = threadIdx.x % kTPR;
     uint32_t r; // uniform across the row's waves
@@ -252,7 +254,7 @@ __global__ __launch_bounds__(BS) void k_row_vec(RowGeo g, const float *x, float 
 #pragma unroll
             for (int j = 0; j < NV; ++j) {
                 if (in_row(j)) {
-                    v[j] = exp4(sub4(v[j], mx), tab);
+                    v[j] = exp4(sub4(v[j], mx), tab, ec);
                     acc += sum4(v[j]);
                 }
             }
@@ -305,7 +307,7 @@ __global__ __launch_bounds__(BS) void k_row_vec(RowGeo g, const float *x, float 
             mx = row_max<NW>(mx, lds_a);
             double acc = 0.0;
             for (uint32_t idx = t; idx < nv; idx += kTPR) {
-                const float4 e = exp4(sub4(load_cached(idx), mx), tab);
+                const float4 e = exp4(sub4(load_cached(idx), mx), tab, ec);
                 yr[idx] = e;
                 acc += sum4(e);
             }
