@@ -223,6 +223,36 @@ class GpuSuite:
             raise RuntimeError(f"{name}: {st.name}: {self.eh.last_error()}")
 
 
+def copy_ceilings(suite, sizes, steps, capture, timed):
+    """Times OpScale(1.0) moving each algorithmic byte count (half read, half
+    written) over rotating buffer sets totalling >= ROTATE_BYTES; returns
+    {bytes: ms per launch}."""
+    torch, eh = suite.torch, suite.eh
+    out = {}
+    for nbytes in sorted(set(sizes)):
+        n = (nbytes // 8) // 64 * 64  # floats per side, 256-byte aligned slices
+        slots = max(2, -(-ROTATE_BYTES // (8 * n)))
+        src = torch.zeros(slots * n, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty(slots * n, dtype=torch.float32, device="cuda:0")
+        lay = eh.Layout.contiguous(eh.DType.F32, [n, 1, 1, 1])
+        evs = [eh.OpScale(eh.TensorView(src[i * n:(i + 1) * n], lay), eh.TensorViewMut(dst[i * n:(i + 1) * n], lay), 1.0)
+               for i in range(slots)]
+
+        def launch(i, evs=evs):
+            st = suite.kernel.process_event(evs[i % len(evs)])
+            if st != eh.Status.OK:
+                raise RuntimeError(f"copy: {st.name}: {eh.last_error()}")
+
+        for i in range(2):
+            launch(i)
+        reps = max(steps, 20, slots)
+        g = capture(lambda reps=reps: [launch(i) for i in range(reps)])
+        g.replay()
+        out[nbytes] = timed(lambda i: g.replay(), 3) / (3 * reps) * (nbytes / (8.0 * n))
+        del g, evs, src, dst
+    return out
+
+
 def cpu_baseline(host, budget_s=20.0):
     """Single-threaded oracle on a bounded sample of each op's workload:
     the same code path the reference's CPU kernels take (view decode,
@@ -314,6 +344,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--ops", default="")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-copy", action="store_true", help="skip the same-size copy reference per op")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -396,6 +427,13 @@ def main():
             g.replay()
             per_ms[n] = timed(lambda i: g.replay(), 3) / (3 * reps)
 
+        # same-size copy: scale by 1.0 over a dense f32 buffer moving the op's
+        # algorithmic bytes, launched and rotated the same way; what a plain
+        # stream achieves at that size (launch ramp and tail included)
+        copy_ms = {}
+        if not args.no_copy:
+            copy_ms = copy_ceilings(suite, [info[n][1] for n in names if n != "copy"], args.steps, capture, timed)
+
     per_op = {}
     total_bytes = 0
     for n in names:
@@ -404,6 +442,10 @@ def main():
         gbs = nbytes / (us * 1e-6) / 1e9
         per_op[n] = {"config": cfg, "alg_bytes": nbytes, "us": round(us, 3), "GB/s": round(gbs, 1),
                      "frac_of_peak": round(gbs / PEAK_GBS, 4)}
+        if nbytes in copy_ms:
+            cus = copy_ms[nbytes] * 1e3
+            per_op[n]["copy_us"] = round(cus, 3)
+            per_op[n]["frac_of_copy"] = round(cus / us, 4)
         total_bytes += nbytes
     value = total_bytes / (step_ms * 1e-3) / 1e9
 

@@ -158,14 +158,13 @@ __device__ __forceinline__ ExpCtx stage_table(uint64_t *lds)
 
 // ---- dense: every operand contiguous, paired by linear index -------------
 
-// Streaming policy measured on MI355X: unary ops read with cached loads and
-// write non-temporally; binary ops stream both ways.  Ops with libm work per
-// element run one float4 per thread (more waves to overlap the arithmetic
-// with memory), the others two.
+// Streaming policy measured on MI355X with cold buffers (a 22.5 MB and a
+// 256 MB array per operand): one float4 per thread, non-temporal loads and
+// stores, was fastest or tied for copy, mul, silu and swiglu at both sizes.
 template <Ew OP>
 struct Stream {
-    static constexpr bool kNtLoad = Fn<OP>::kBinary;
-    static constexpr int kVpt = Fn<OP>::kTable || OP == Ew::Tanh || OP == Ew::Elu ? 1 : 2;
+    static constexpr bool kNtLoad = true;
+    static constexpr int kVpt = 1;
 };
 
 template <Ew OP, int VPT>
@@ -184,7 +183,7 @@ __global__ __launch_bounds__(kBlock) void k_dense(const float *a, const float *b
         const uint64_t i = base + static_cast<uint64_t>(j) * kBlock;
         if (i < nvec) {
             va[j] = Stream<OP>::kNtLoad ? ld_nt(a4 + i) : a4[i];
-            if constexpr (Fn<OP>::kBinary) vb[j] = ld_nt(b4 + i);
+            if constexpr (Fn<OP>::kBinary) vb[j] = Stream<OP>::kNtLoad ? ld_nt(b4 + i) : b4[i];
             else vb[j] = va[j];
         }
     }
