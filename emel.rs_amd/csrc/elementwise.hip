@@ -215,7 +215,7 @@ __global__ __launch_bounds__(kGeluBlock) void k_gelu_lds(const float *a, float *
 #pragma unroll
     for (int j = 0; j < U; ++j) {
         const uint64_t i = base + static_cast<uint64_t>(j) * kGeluBlock;
-        if (i < nvec) v[j] = a4[i];
+        if (i < nvec) v[j] = ld_nt(a4 + i);
     }
     {
         const uint4 *src = reinterpret_cast<const uint4 *>(g_gelu_tab);
@@ -236,7 +236,7 @@ __global__ __launch_bounds__(kGeluBlock) void k_gelu_lds(const float *a, float *
 #pragma unroll
         for (int j = 0; j < U; ++j) {
             const uint64_t i = next + static_cast<uint64_t>(j) * kGeluBlock;
-            if (i < nvec) v[j] = a4[i];
+            if (i < nvec) v[j] = ld_nt(a4 + i);
         }
 #pragma unroll
         for (int j = 0; j < U; ++j) {

@@ -89,18 +89,19 @@ __device__ __forceinline__ void accumulate(const RedGeo &g, const float *x, int6
                        (static_cast<double>(q.z) + static_cast<double>(q.w));
             }
         };
-        // kUnroll loads in flight per thread, then taken in column order
+        // kUnroll non-temporal loads in flight per thread (each byte is read
+        // once), then taken in column order
         constexpr int kUnroll = 4;
         const uint64_t vend = c1 / 4;
         uint64_t v = c0 / 4 + threadIdx.x;
         for (; v + (kUnroll - 1) * kBlock < vend; v += kUnroll * kBlock) {
             float4 q[kUnroll];
 #pragma unroll
-            for (int j = 0; j < kUnroll; ++j) q[j] = x4[v + j * kBlock];
+            for (int j = 0; j < kUnroll; ++j) q[j] = ld_nt(x4 + v + j * kBlock);
 #pragma unroll
             for (int j = 0; j < kUnroll; ++j) take4(q[j], 4 * (v + j * kBlock));
         }
-        for (; v < vend; v += kBlock) take4(x4[v], 4 * v);
+        for (; v < vend; v += kBlock) take4(ld_nt(x4 + v), 4 * v);
     } else if (g.mode == kModeScalar) {
         for (uint64_t c = c0 + threadIdx.x; c < c1; c += kBlock) take(x[base + static_cast<int64_t>(c) * g.x_st[0]], c);
     } else {
