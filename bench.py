@@ -20,7 +20,7 @@ step's bytes).  The CPU baseline times the C oracle (a single-threaded
 restatement of the reference's CPU path) on a bounded sample of the same
 workload.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--ops a,b] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--ops a,b] [--no-cpu] [--no-copy] [--pcie]
 """
 from __future__ import annotations
 
@@ -253,6 +253,44 @@ def copy_ceilings(suite, sizes, steps, capture, timed):
     return out
 
 
+def pcie_inclusive(suite, host, stream, reps=5):
+    """soft_max_ext for a caller whose tensors live in (pinned) host memory:
+    copy the scores and mask in, run the op, copy the result out, all on the
+    kernel stream.  Returns the median time and the algorithmic bytes / time
+    rate; this is never bench's `value`."""
+    torch, eh = suite.torch, suite.eh
+    x_h = torch.from_numpy(host["c4_x"]).pin_memory()
+    m_h = torch.from_numpy(host["c4_mask"].view(np.float16)).pin_memory()
+    y_h = torch.empty(x_h.numel(), dtype=torch.float32).pin_memory()
+    x_d = torch.empty(x_h.numel(), dtype=torch.float32, device="cuda:0")
+    m_d = torch.empty(m_h.numel(), dtype=torch.float16, device="cuda:0")
+    y_d = torch.empty_like(x_d)
+    F32, F16 = eh.DType.F32, eh.DType.F16
+    ev = eh.OpSoftMaxExt(eh.TensorView(x_d, eh.Layout(F32, [4096, 512, 32, 1], dense_nb([4096, 512, 32, 1]))),
+                         eh.TensorView(m_d, eh.Layout(F16, [4096, 512, 1, 1], dense_nb([4096, 512, 1, 1], 2))),
+                         float(np.float32(1.0 / np.sqrt(128.0))),
+                         eh.TensorViewMut(y_d, eh.Layout(F32, [4096, 512, 32, 1], dense_nb([4096, 512, 32, 1]))))
+    times = []
+    with torch.cuda.stream(stream):
+        for _ in range(reps + 1):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            x_d.copy_(x_h, non_blocking=True)
+            m_d.copy_(m_h, non_blocking=True)
+            st = suite.kernel.process_event(ev)
+            if st != eh.Status.OK:
+                raise RuntimeError(f"soft_max_ext: {st.name}")
+            y_h.copy_(y_d, non_blocking=True)
+            b.record(stream)
+            b.synchronize()
+            times.append(a.elapsed_time(b))
+    ms = float(np.median(times[1:]))
+    nbytes = dict((n, b) for n, _, b in OPS)["soft_max_ext"]
+    return {"op": "soft_max_ext", "ms": round(ms, 3), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "note": "inputs copied in from and the output copied out to pinned host memory around each launch"}
+
+
 def cpu_baseline(host, budget_s=20.0):
     """Single-threaded oracle on a bounded sample of each op's workload:
     the same code path the reference's CPU kernels take (view decode,
@@ -345,6 +383,7 @@ def main():
     ap.add_argument("--ops", default="")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-copy", action="store_true", help="skip the same-size copy reference per op")
+    ap.add_argument("--pcie", action="store_true", help="also time soft_max_ext with host-resident tensors")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -462,6 +501,10 @@ def main():
         except (ValueError, KeyError):
             pass
 
+    pcie = None
+    if args.pcie and "soft_max_ext" in names:
+        pcie = pcie_inclusive(suite, host, stream)
+
     cpu = None
     if not args.no_cpu and not args.ops:
         cpu_gbs, cpu_ops = cpu_baseline(host)
@@ -495,6 +538,7 @@ def main():
         "per_op": per_op,
         "roofline": roof,
         "cpu_baseline": cpu,
+        "pcie_inclusive": pcie,
     }
     print(json.dumps(out))
 
