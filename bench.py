@@ -116,6 +116,11 @@ OPS = [
     ("sum_rows", "config 5: sum_rows [151936,64]", 38895616 + 256),
     ("mul_broadcast_4d", "config 5b: permuted [128,64,32,8] * [128,1,32,1]", 8388608 + 16384 + 8388608),
 ]
+# Measured per op like the others but not part of the step (and so not of
+# `value`): adjacent ops beyond the BASELINE configs' op list.
+EXTRA_OPS = [
+    ("glu_swiglu", "config 2 as one OpGlu (glu.rs): [up | gate] -> silu(gate) * up", 3 * 22544384),
+]
 DOMINANT = "soft_max_ext"
 COPY_BYTES = 2 * 268435456  # the calibration copy: 256 MiB read + 256 MiB written
 
@@ -192,6 +197,8 @@ class GpuSuite:
             "mul_broadcast_4d": ([host["c5b_src0"], host["c5b_src1"]], (128 * 64 * 32 * 8, torch.float32),
                                  lambda i, o: eh.OpBinaryBroadcast(eh.BinaryOp.MUL, V(i[0], [128, 64, 32, 8], vnb),
                                                                    V(i[1], [128, 1, 32, 1]), M(o, [128, 64, 32, 8]))),
+            "glu_swiglu": ([np.concatenate([host["c2_up"], host["c2_gate"]])], (n2, torch.float32),
+                           lambda i, o: eh.OpGlu(i[0], o, eh.GluSubOp.SWIGLU)),
             "copy": ([np.zeros(COPY_BYTES // 8, np.float32)], (COPY_BYTES // 8, torch.float32),
                      lambda i, o: eh.OpScale(V(i[0], [COPY_BYTES // 8, 1, 1, 1]), M(o, [COPY_BYTES // 8, 1, 1, 1]),
                                              1.0)),
@@ -203,7 +210,7 @@ class GpuSuite:
             if name not in spec:
                 raise ValueError(name)
             inputs, (numel, odt), build = spec[name]
-            alg = dict((n, b) for n, _, b in OPS).get(name, COPY_BYTES)
+            alg = dict((n, b) for n, _, b in OPS + EXTRA_OPS).get(name, COPY_BYTES)
             copies = max(2, -(-ROTATE_BYTES // alg))
             first = [up(x) for x in inputs]
             evs, outs = [], []
@@ -393,19 +400,23 @@ def main():
 
     import torch
 
+    extra_names = [n for n, _, _ in EXTRA_OPS]
     names = [n for n, _, _ in OPS]
+    extra = list(extra_names)
     if args.ops:
-        names = [n for n in args.ops.split(",") if n]
-    info = {n: (cfg, b) for n, cfg, b in OPS}
+        wanted = [n for n in args.ops.split(",") if n]
+        names = [n for n in wanted if n not in extra_names]
+        extra = [n for n in wanted if n in extra_names]
+    info = {n: (cfg, b) for n, cfg, b in OPS + EXTRA_OPS}
     info["copy"] = ("calibration copy: scale by 1.0 over 256 MiB", COPY_BYTES)
 
     host = config_inputs()
     stream = torch.cuda.Stream()
-    suite = GpuSuite(host, stream, names)
+    suite = GpuSuite(host, stream, names + extra)
 
     with torch.cuda.stream(stream):
         for w in range(args.warmup):
-            for n in names:
+            for n in names + extra:
                 suite.launch(n, w)
         stream.synchronize()
 
@@ -460,7 +471,7 @@ def main():
         # per op: a graph of back-to-back launches cycling through all of
         # the op's buffer sets (>= ROTATE_BYTES), so each launch is cold
         per_ms = {}
-        for n in names:
+        for n in names + extra:
             reps = max(args.steps, 20, suite.copies[n])
             g = capture(lambda n=n, reps=reps: [suite.launch(n, i) for i in range(reps)])
             g.replay()
@@ -471,27 +482,31 @@ def main():
         # stream achieves at that size (launch ramp and tail included)
         copy_ms = {}
         if not args.no_copy:
-            copy_ms = copy_ceilings(suite, [info[n][1] for n in names if n != "copy"], args.steps, capture, timed)
+            copy_ms = copy_ceilings(suite, [info[n][1] for n in names + extra if n != "copy"], args.steps, capture,
+                                    timed)
 
-    per_op = {}
-    total_bytes = 0
-    for n in names:
+    def op_entry(n):
         cfg, nbytes = info[n]
         us = per_ms[n] * 1e3
         gbs = nbytes / (us * 1e-6) / 1e9
-        per_op[n] = {"config": cfg, "alg_bytes": nbytes, "us": round(us, 3), "GB/s": round(gbs, 1),
-                     "frac_of_peak": round(gbs / PEAK_GBS, 4)}
+        e = {"config": cfg, "alg_bytes": nbytes, "us": round(us, 3), "GB/s": round(gbs, 1),
+             "frac_of_peak": round(gbs / PEAK_GBS, 4)}
         if nbytes in copy_ms:
             cus = copy_ms[nbytes] * 1e3
-            per_op[n]["copy_us"] = round(cus, 3)
-            per_op[n]["frac_of_copy"] = round(cus / us, 4)
-        total_bytes += nbytes
+            e["copy_us"] = round(cus, 3)
+            e["frac_of_copy"] = round(cus / us, 4)
+        return e
+
+    per_op = {n: op_entry(n) for n in names}
+    extra_ops = {n: op_entry(n) for n in extra}
+    total_bytes = sum(info[n][1] for n in names)
     value = total_bytes / (step_ms * 1e-3) / 1e9
 
-    dom = DOMINANT if DOMINANT in per_op else names[0]
-    roof = {"kernel": dom, "bound": "hbm", "achieved": per_op[dom]["GB/s"], "peak": PEAK_GBS, "unit": "GB/s",
-            "frac": round(per_op[dom]["GB/s"] / PEAK_GBS, 4), "traffic": None,
-            "alg_bytes_per_launch": info[dom][1], "avg_launch_us": per_op[dom]["us"]}
+    measured = {**per_op, **extra_ops}
+    dom = DOMINANT if DOMINANT in measured else (names + extra)[0]
+    roof = {"kernel": dom, "bound": "hbm", "achieved": measured[dom]["GB/s"], "peak": PEAK_GBS, "unit": "GB/s",
+            "frac": round(measured[dom]["GB/s"] / PEAK_GBS, 4), "traffic": None,
+            "alg_bytes_per_launch": info[dom][1], "avg_launch_us": measured[dom]["us"]}
     traffic_file = ROOT / "profiles" / "traffic.json"
     if traffic_file.exists():
         try:
@@ -536,6 +551,7 @@ def main():
                                     "(Infinity Cache is 256 MB)",
                    "wall_s": round(wall, 3)},
         "per_op": per_op,
+        "extra_ops": extra_ops,
         "roofline": roof,
         "cpu_baseline": cpu,
         "pcie_inclusive": pcie,

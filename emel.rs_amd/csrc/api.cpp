@@ -631,6 +631,42 @@ emel_status emel_op_swiglu(const emel_tensor_view *gate, const emel_tensor_view 
     return elementwise(emel::Ew::Swiglu, gate, pair_addr(*gate, *out), up, pair_addr(*up, *out), out, 1.0f, stream);
 }
 
+emel_status emel_op_glu(emel_glu_subop subop, const float *input, uint64_t input_len, float *output,
+                        uint64_t output_len, emel_stream stream)
+{
+    static constexpr emel::Ew kOps[6] = {emel::Ew::GluRe, emel::Ew::GluGe, emel::Ew::GluSwi,
+                                         emel::Ew::GluSwiOai, emel::Ew::GluGeErf, emel::Ew::GluGeQuick};
+    const uint32_t code = static_cast<uint32_t>(subop);
+    if (code >= 6) return fail(EMEL_ERR_UNEXPECTED_EVENT, "unknown glu subop");
+    if (!input || !output) return fail(EMEL_ERR_INVALID_ARGUMENT, "null slice");
+    // split_len (glu.rs:85-91)
+    if (input_len == 0 || input_len % 2 != 0 || output_len != input_len / 2)
+        return fail(EMEL_ERR_SHAPE_MISMATCH, "glu input must split into two halves the size of the output");
+    const uint64_t n = output_len;
+    if (n > (UINT64_MAX / 8)) return fail(EMEL_ERR_SHAPE_MISMATCH, "glu length overflows");
+    const uintptr_t i0 = reinterpret_cast<uintptr_t>(input), i1 = i0 + input_len * 4;
+    const uintptr_t o0 = reinterpret_cast<uintptr_t>(output), o1 = o0 + n * 4;
+    if (o0 < i1 && i0 < o1) return fail(EMEL_ERR_INVALID_ARGUMENT, "glu output overlaps its input");
+    auto slice = [](const void *p, uint64_t len) {
+        emel_tensor_view v{};
+        v.data = p;
+        v.data_bytes = len * 4;
+        v.dtype = EMEL_DTYPE_F32;
+        v.ne[0] = len;
+        v.ne[1] = v.ne[2] = v.ne[3] = 1;
+        return v;
+    };
+    const emel_tensor_view values = slice(input, n), gates = slice(input + n, n);
+    emel_tensor_view_mut out{};
+    out.data = output;
+    out.data_bytes = n * 4;
+    out.dtype = EMEL_DTYPE_F32;
+    out.ne[0] = n;
+    out.ne[1] = out.ne[2] = out.ne[3] = 1;
+    return elementwise(kOps[code], &values, emel::Addr::SameCoords, &gates, emel::Addr::SameCoords, &out, 1.0f,
+                       stream);
+}
+
 emel_status emel_op_scale(const emel_tensor_view *in, const emel_tensor_view_mut *out, float scale, emel_stream stream)
 {
     if (!in || !out) return fail(EMEL_ERR_INVALID_ARGUMENT, "null view");

@@ -2,7 +2,8 @@
 // equal-count binary add/sub/mul/div (binary.rs:383-424), row broadcast
 // (broadcast.rs:352-390), 4-D modulo broadcast (OpRepeat + binary,
 // generic.rs:1641-1665), unary abs/neg/tanh/elu/relu/sigmoid/gelu/silu/exp
-// (unary.rs:472-606), scale (activation.rs:366-377) and fused SwiGLU.
+// (unary.rs:472-606), scale (activation.rs:366-377), fused SwiGLU and the
+// six OpGlu gates (glu.rs:103-141, :258-270).
 //
 // All of them are HBM-bound streams (<= 1 flop per byte except the
 // transcendental ones, which stay under the memory time).  Three kernel
@@ -129,6 +130,24 @@ EMEL_FN(Exp, true, false, emel_expf(a, t.tab, t.c))
 EMEL_FN(Scale, false, false, a * s)
 // silu(gate) rounded to f32, then times up: the OpSilu -> OpMul chain.
 EMEL_FN(Swiglu, true, true, emel_silu(a, t.tab, t.c) * b)
+// OpGlu (glu.rs:103-141, :258-270): values (a) times a gate function of
+// gates (b), every product and sum rounded separately.
+__device__ __forceinline__ float glu_gelu_erf(float g, const ExpCtx &t)
+{
+    const float sign = g < 0.0f ? -1.0f : 1.0f;
+    const float x = __builtin_fabsf(g) / 1.41421356237309504880f; // core::f32::consts::SQRT_2
+    const float u = 1.0f / (1.0f + 0.3275911f * x);
+    const float poly = (((((1.0614054f * u - 1.4531521f) * u) + 1.4214138f) * u - 0.28449672f) * u + 0.2548296f) * u;
+    const float erf = sign * (1.0f - poly * emel_expf(-x * x, t.tab, t.c));
+    return 0.5f * g * (1.0f + erf);
+}
+EMEL_FN(GluRe, false, true, a * (b > 0.0f ? b : 0.0f))
+EMEL_FN(GluGe, false, true, a * (0.5f * b * (1.0f + emel_tanhf(0.7978846f * b * (1.0f + 0.044715f * b * b)))))
+EMEL_FN(GluSwi, true, true, a * emel_silu(b, t.tab, t.c))
+EMEL_FN(GluSwiOai, true, true,
+        emel_silu(1.702f * __builtin_fminf(b, 7.0f), t.tab, t.c) / 1.702f * (__builtin_fminf(a, 7.0f) + 1.0f))
+EMEL_FN(GluGeErf, true, true, a * glu_gelu_erf(b, t))
+EMEL_FN(GluGeQuick, true, true, a * (b * (1.0f / (1.0f + emel_expf(-1.702f * b, t.tab, t.c)))))
 #undef EMEL_FN
 
 template <Ew OP>
@@ -555,6 +574,12 @@ hipError_t launch_elementwise(const EwArgs &args, hipStream_t stream)
     case Ew::Exp: return launch_op<Ew::Exp>(args, stream);
     case Ew::Scale: return launch_op<Ew::Scale>(args, stream);
     case Ew::Swiglu: return launch_op<Ew::Swiglu>(args, stream);
+    case Ew::GluRe: return launch_op<Ew::GluRe>(args, stream);
+    case Ew::GluGe: return launch_op<Ew::GluGe>(args, stream);
+    case Ew::GluSwi: return launch_op<Ew::GluSwi>(args, stream);
+    case Ew::GluSwiOai: return launch_op<Ew::GluSwiOai>(args, stream);
+    case Ew::GluGeErf: return launch_op<Ew::GluGeErf>(args, stream);
+    case Ew::GluGeQuick: return launch_op<Ew::GluGeQuick>(args, stream);
     }
     return hipErrorInvalidValue;
 }

@@ -23,7 +23,8 @@ enum class Binary : uint32_t { Add = 0, Sub = 1, Mul = 2, Div = 3 };
 enum class Ew : uint32_t {
     Add = 0, Sub, Mul, Div,                                        // binary
     Abs, Neg, Tanh, Elu, Relu, Sigmoid, Gelu, Silu, Exp, Scale,   // unary
-    Swiglu                                                         // fused
+    Swiglu,                                                        // fused
+    GluRe, GluGe, GluSwi, GluSwiOai, GluGeErf, GluGeQuick         // OpGlu: a = values, b = gates
 };
 
 // How a source operand is addressed from the destination ordinal.

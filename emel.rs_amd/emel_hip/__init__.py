@@ -2,7 +2,7 @@
 path -- elementwise, broadcast and row-reduction ops -- behind the C ABI in
 include/emel_hip.h, with a Python mirror of emel-kernels' operator API.
 """
-from .abi import BinaryOp, DType, Status, UnarySubOp, device_count, last_error, load
+from .abi import BinaryOp, DType, GluSubOp, Status, UnarySubOp, device_count, last_error, load
 from .kernel import (
     Kernel,
     OpAdd,
@@ -12,6 +12,7 @@ from .kernel import (
     OpBinaryBroadcast,
     OpDiv,
     OpGelu,
+    OpGlu,
     OpMean,
     OpMul,
     OpMulBroadcastRow,
@@ -31,9 +32,9 @@ from .kernel import (
 from .views import Layout, TensorView, TensorViewMut
 
 __all__ = [
-    "BinaryOp", "DType", "Status", "UnarySubOp", "device_count", "last_error", "load",
+    "BinaryOp", "DType", "GluSubOp", "Status", "UnarySubOp", "device_count", "last_error", "load",
     "Kernel", "Layout", "TensorView", "TensorViewMut",
     "OpAdd", "OpSub", "OpMul", "OpDiv", "OpAddBroadcastRow", "OpMulBroadcastRow", "OpBinaryBroadcast",
-    "OpUnary", "OpSilu", "OpGelu", "OpSwiglu", "OpScale", "OpRmsNorm", "OpRmsNormMul", "OpNorm",
+    "OpUnary", "OpSilu", "OpGelu", "OpGlu", "OpSwiglu", "OpScale", "OpRmsNorm", "OpRmsNormMul", "OpNorm",
     "OpSoftMax", "OpSoftMaxExt", "OpSumRows", "OpSum", "OpMean", "OpArgmax", "OpArgmaxRows",
 ]

@@ -53,6 +53,17 @@ class UnarySubOp(enum.IntEnum):
     EXP = 13
 
 
+class GluSubOp(enum.IntEnum):
+    """GluSubOp wire codes (glu.rs:22-37)."""
+
+    REGLU = 0
+    GEGLU = 1
+    SWIGLU = 2
+    SWIGLU_OAI = 3
+    GEGLU_ERF = 4
+    GEGLU_QUICK = 5
+
+
 class BinaryOp(enum.IntEnum):
     ADD = 0
     SUB = 1
@@ -90,6 +101,7 @@ SIGNATURES = {
     "emel_op_silu": [_V, _V, _S],
     "emel_op_gelu": [_V, _V, _S],
     "emel_op_swiglu": [_V, _V, _V, _S],
+    "emel_op_glu": [ctypes.c_uint32, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_uint64, _S],
     "emel_op_scale": [_V, _V, ctypes.c_float, _S],
     "emel_op_rms_norm": [_V, _V, ctypes.c_float, _S],
     "emel_op_rms_norm_mul": [_V, _V, _V, ctypes.c_float, _S],

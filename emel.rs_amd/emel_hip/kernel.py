@@ -157,6 +157,29 @@ class OpSwiglu:
 
 
 @dataclass
+class OpGlu:
+    """glu::OpGlu::new(input, output, subop) (glu.rs:69-92): input is a dense
+    f32 slice [values | gates] of 2n floats, output n floats.  `input` and
+    `output` are device tensors (or raw pointers, with the lengths given)."""
+
+    input: object
+    output: object
+    subop: int
+    input_len: int | None = None
+    output_len: int | None = None
+
+    def _call(self, lib, s):
+        def ptr_len(t, n):
+            if isinstance(t, int):
+                return t, n
+            return int(t.data_ptr()), (t.numel() if n is None else n)
+
+        ip, il = ptr_len(self.input, self.input_len)
+        op, ol = ptr_len(self.output, self.output_len)
+        return lib.emel_op_glu(int(self.subop), ip, il, op, ol, s)
+
+
+@dataclass
 class OpScale:
     """activation::OpScale::new(input, output, scale) (activation.rs:58-72)."""
 

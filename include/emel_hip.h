@@ -78,6 +78,16 @@ typedef enum emel_unary_subop {
     EMEL_UNARY_EXP = 13
 } emel_unary_subop;
 
+/* GLU wire subop codes, GluSubOp (glu.rs:22-37). */
+typedef enum emel_glu_subop {
+    EMEL_GLU_REGLU = 0,       /* x * relu(g) */
+    EMEL_GLU_GEGLU = 1,       /* x * gelu_tanh(g) */
+    EMEL_GLU_SWIGLU = 2,      /* x * silu(g) */
+    EMEL_GLU_SWIGLU_OAI = 3,  /* clamped gate and value, alpha 1.702 */
+    EMEL_GLU_GEGLU_ERF = 4,   /* x * gelu_erf(g) */
+    EMEL_GLU_GEGLU_QUICK = 5  /* x * gelu_quick(g) */
+} emel_glu_subop;
+
 typedef enum emel_binary_op {
     EMEL_BINARY_ADD = 0,
     EMEL_BINARY_SUB = 1,
@@ -181,6 +191,19 @@ emel_status emel_op_gelu(const emel_tensor_view *in, const emel_tensor_view_mut 
  * roundings.  The three views have identical shapes. */
 emel_status emel_op_swiglu(const emel_tensor_view *gate, const emel_tensor_view *up,
                            const emel_tensor_view_mut *out, emel_stream stream);
+
+/* ---- gated linear units --------------------------------------------------------
+ * glu::OpGlu::new(input, output, subop) (glu.rs:69-92; split_len :85-91;
+ * gates :103-129; apply_split :131-141; SwiGluOai :258-270): input is a dense
+ * slice of input_len floats, values in its first half and gates in its
+ * second; output gets input_len / 2 floats, output[i] = values[i] *
+ * gate(gates[i]).  GluError::InvalidShape (empty or odd input, output not
+ * half of it) is EMEL_ERR_SHAPE_MISMATCH; an unknown subop code is
+ * EMEL_ERR_UNEXPECTED_EVENT (no transition of the reference's machine
+ * accepts it); output overlapping input (impossible for Rust's borrowed
+ * slices) is EMEL_ERR_INVALID_ARGUMENT.  Lengths count floats. */
+emel_status emel_op_glu(emel_glu_subop subop, const float *input, uint64_t input_len, float *output,
+                        uint64_t output_len, emel_stream stream);
 
 /* ---- scale ------------------------------------------------------------------
  * activation::OpScale::new(input, output, scale) (activation.rs:58-72,

@@ -678,3 +678,54 @@ int orc_swiglu(const orc_view *gate, const orc_view *up, const orc_view *out)
     free(tmp);
     return s;
 }
+
+/* ------------------------------------------------------------------ */
+/* OpGlu (glu.rs:22-160, :243-282)                                     */
+/* ------------------------------------------------------------------ */
+
+/* Gate functions, glu.rs:103-129: relu = f32::max(x, 0) (glibc fmaxf),
+ * silu = x / (1 + exp(-x)), gelu_tanh = 0.5 x (1 + tanh(0.7978846 x
+ * (1 + 0.044715 x x))), gelu_quick = x (1 / (1 + exp(-1.702 x))), gelu_erf:
+ * the Abramowitz-Stegun 7.1.26 polynomial with exp(-x x).  Every product
+ * and sum rounds separately (no contraction). */
+float orc_glu_gate(int subop, float g)
+{
+    switch (subop) {
+    case ORC_REGLU: return fmaxf(g, 0.0f);
+    case ORC_GEGLU: return 0.5f * g * (1.0f + tanhf(0.7978846f * g * (1.0f + 0.044715f * g * g)));
+    case ORC_SWIGLU: return orc_silu(g);
+    case ORC_GEGLU_QUICK: return g * (1.0f / (1.0f + expf(-1.702f * g)));
+    case ORC_GEGLU_ERF: {
+        const float sign = g < 0.0f ? -1.0f : 1.0f;
+        const float x = fabsf(g) / 1.41421356237309504880f; /* core::f32::consts::SQRT_2 */
+        const float t = 1.0f / (1.0f + 0.3275911f * x);
+        const float poly = (((((1.0614054f * t - 1.4531521f) * t) + 1.4214138f) * t - 0.28449672f) * t + 0.2548296f) * t;
+        const float erf = sign * (1.0f - poly * expf(-x * x));
+        return 0.5f * g * (1.0f + erf);
+    }
+    default: return 0.0f;
+    }
+}
+
+/* split_len (glu.rs:85-91): input non-empty, even, output exactly half.
+ * apply_split (:131-141): out[i] = values[i] * gate(gates[i]); SwiGluOai
+ * (:258-270): gate and value clamped above by 7 (f32::min), then
+ * silu(1.702 g) / 1.702 * (v + 1). */
+int orc_op_glu(int subop, const float *input, uint64_t input_len, float *output, uint64_t output_len)
+{
+    if (subop < ORC_REGLU || subop > ORC_GEGLU_QUICK) return ORC_UNEXPECTED_EVENT;
+    if (input_len == 0 || input_len % 2 != 0 || output_len != input_len / 2) return ORC_SHAPE_MISMATCH;
+    const uint64_t n = input_len / 2;
+    const float *values = input, *gates = input + n;
+    for (uint64_t i = 0; i < n; i++) {
+        if (subop == ORC_SWIGLU_OAI) {
+            const float g = fminf(gates[i], 7.0f);
+            const float v = fminf(values[i], 7.0f);
+            output[i] = orc_silu(1.702f * g) / 1.702f * (v + 1.0f);
+        } else {
+            output[i] = values[i] * orc_glu_gate(subop, gates[i]);
+        }
+    }
+    return ORC_OK;
+}
+

@@ -69,6 +69,12 @@ int orc_binary_bcast(int op, const orc_view *src0, const orc_view *src1, const o
 int orc_rms_norm_mul(const orc_view *in, const orc_view *weight, const orc_view *out, float eps);
 int orc_swiglu(const orc_view *gate, const orc_view *up, const orc_view *out);
 
+/* OpGlu over a dense slice [values | gates] of 2n floats into n floats
+ * (glu.rs:22-160, :258-270).  subop: GluSubOp wire code 0..5. */
+enum { ORC_REGLU = 0, ORC_GEGLU = 1, ORC_SWIGLU = 2, ORC_SWIGLU_OAI = 3, ORC_GEGLU_ERF = 4, ORC_GEGLU_QUICK = 5 };
+int orc_op_glu(int subop, const float *input, uint64_t input_len, float *output, uint64_t output_len);
+float orc_glu_gate(int subop, float gate); /* the gate function alone (not SwiGluOai) */
+
 /* Scalar helpers (unary.rs:522-600, quant.rs:287-300). */
 float orc_silu(float x);
 float orc_gelu(float x);

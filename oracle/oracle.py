@@ -96,6 +96,10 @@ def lib() -> ctypes.CDLL:
         for name in ("orc_silu", "orc_gelu"):
             getattr(L, name).argtypes = [ctypes.c_float]
             getattr(L, name).restype = ctypes.c_float
+        L.orc_op_glu.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_uint64]
+        L.orc_op_glu.restype = ctypes.c_int
+        L.orc_glu_gate.argtypes = [ctypes.c_int, ctypes.c_float]
+        L.orc_glu_gate.restype = ctypes.c_float
         L.orc_fp32_to_fp16.argtypes = [ctypes.c_float]
         L.orc_fp32_to_fp16.restype = ctypes.c_uint16
         L.orc_fp16_to_f32.argtypes = [ctypes.c_uint16]
@@ -135,6 +139,17 @@ def argmax_rows(src, dst): return call("orc_argmax_rows", src, dst)
 def binary_bcast(op, src0, src1, dst): return call("orc_binary_bcast", op, src0, src1, dst)
 def rms_norm_mul(src, w, dst, eps): return call("orc_rms_norm_mul", src, w, dst, ctypes.c_float(eps))
 def swiglu(gate, up, dst): return call("orc_swiglu", gate, up, dst)
+REGLU, GEGLU, SWIGLU, SWIGLU_OAI, GEGLU_ERF, GEGLU_QUICK = 0, 1, 2, 3, 4, 5
+
+
+def glu(subop, inp: np.ndarray, out: np.ndarray, input_len=None, output_len=None) -> int:
+    """OpGlu over host float32 arrays (lengths default to the arrays')."""
+    assert inp.dtype == np.float32 and out.dtype == np.float32
+    return int(lib().orc_op_glu(subop, inp.ctypes.data, inp.size if input_len is None else input_len,
+                                out.ctypes.data, out.size if output_len is None else output_len))
+
+
+def glu_gate(subop, g: float) -> float: return float(lib().orc_glu_gate(subop, g))
 def silu_scalar(x: float) -> float: return float(lib().orc_silu(x))
 def gelu_scalar(x: float) -> float: return float(lib().orc_gelu(x))
 def fp32_to_fp16(x: float) -> int: return int(lib().orc_fp32_to_fp16(x))
