@@ -444,6 +444,8 @@ const char *emel_status_string(emel_status s)
     case EMEL_ERR_KERNEL_UNAVAILABLE: return "kernel unavailable (no gfx950 device)";
     case EMEL_ERR_DEVICE: return "HIP runtime error";
     case EMEL_ERR_INVALID_ARGUMENT: return "invalid argument";
+    case EMEL_ERR_INVALID_SHAPE: return "invalid kernel shape";
+    case EMEL_ERR_UNSUPPORTED_OPERATION: return "unsupported operation";
     }
     return "unknown status";
 }
@@ -631,6 +633,42 @@ emel_status emel_op_swiglu(const emel_tensor_view *gate, const emel_tensor_view 
     return elementwise(emel::Ew::Swiglu, gate, pair_addr(*gate, *out), up, pair_addr(*up, *out), out, 1.0f, stream);
 }
 
+namespace {
+
+// A caller slice of `len` floats as a contiguous [len, 1, 1, 1] view.
+emel_tensor_view slice_view(const void *p, uint64_t len)
+{
+    emel_tensor_view v{};
+    v.data = p;
+    v.data_bytes = len * 4;
+    v.dtype = EMEL_DTYPE_F32;
+    v.ne[0] = len;
+    v.ne[1] = v.ne[2] = v.ne[3] = 1;
+    return v;
+}
+
+emel_tensor_view_mut slice_view_mut(void *p, uint64_t len)
+{
+    emel_tensor_view_mut v{};
+    v.data = p;
+    v.data_bytes = len * 4;
+    v.dtype = EMEL_DTYPE_F32;
+    v.ne[0] = len;
+    v.ne[1] = v.ne[2] = v.ne[3] = 1;
+    return v;
+}
+
+// Output and input slices either are the same range or do not overlap.
+bool slices_disjoint_or_same(const float *out, uint64_t out_len, const float *in, uint64_t in_len)
+{
+    if (out == in && out_len == in_len) return true;
+    const uintptr_t o0 = reinterpret_cast<uintptr_t>(out), o1 = o0 + out_len * 4;
+    const uintptr_t i0 = reinterpret_cast<uintptr_t>(in), i1 = i0 + in_len * 4;
+    return o1 <= i0 || i1 <= o0;
+}
+
+} // namespace
+
 emel_status emel_op_glu(emel_glu_subop subop, const float *input, uint64_t input_len, float *output,
                         uint64_t output_len, emel_stream stream)
 {
@@ -647,24 +685,118 @@ emel_status emel_op_glu(emel_glu_subop subop, const float *input, uint64_t input
     const uintptr_t i0 = reinterpret_cast<uintptr_t>(input), i1 = i0 + input_len * 4;
     const uintptr_t o0 = reinterpret_cast<uintptr_t>(output), o1 = o0 + n * 4;
     if (o0 < i1 && i0 < o1) return fail(EMEL_ERR_INVALID_ARGUMENT, "glu output overlaps its input");
-    auto slice = [](const void *p, uint64_t len) {
-        emel_tensor_view v{};
-        v.data = p;
-        v.data_bytes = len * 4;
-        v.dtype = EMEL_DTYPE_F32;
-        v.ne[0] = len;
-        v.ne[1] = v.ne[2] = v.ne[3] = 1;
-        return v;
-    };
-    const emel_tensor_view values = slice(input, n), gates = slice(input + n, n);
-    emel_tensor_view_mut out{};
-    out.data = output;
-    out.data_bytes = n * 4;
-    out.dtype = EMEL_DTYPE_F32;
-    out.ne[0] = n;
-    out.ne[1] = out.ne[2] = out.ne[3] = 1;
+    const emel_tensor_view values = slice_view(input, n), gates = slice_view(input + n, n);
+    const emel_tensor_view_mut out = slice_view_mut(output, n);
     return elementwise(kOps[code], &values, emel::Addr::SameCoords, &gates, emel::Addr::SameCoords, &out, 1.0f,
                        stream);
+}
+
+// ---- dense-slice root events (event.rs:133-259, :523-568) -----------------
+
+emel_status emel_slice_dup(const float *input, uint64_t input_len, float *output, uint64_t output_len,
+                           emel_stream stream)
+{
+    // guard_dup_valid (actor.rs:2498-2501)
+    if (input_len == 0 || input_len != output_len) return fail(EMEL_ERR_INVALID_SHAPE, "dup lengths");
+    if (!input || !output) return fail(EMEL_ERR_INVALID_ARGUMENT, "null slice");
+    if (!slices_disjoint_or_same(output, output_len, input, input_len))
+        return fail(EMEL_ERR_INVALID_ARGUMENT, "output partially overlaps the input");
+    const emel_tensor_view in = slice_view(input, input_len);
+    const emel_tensor_view_mut out = slice_view_mut(output, output_len);
+    return elementwise(emel::Ew::Copy, &in, emel::Addr::SameCoords, nullptr, emel::Addr::SameCoords, &out, 1.0f,
+                       stream);
+}
+
+namespace {
+
+// guard_{add,sub,mul,div}_valid (actor.rs:2522-2560): lhs non-empty, all
+// three lengths equal; the effect zips the slices.
+emel_status slice_binary(emel::Ew op, const float *lhs, uint64_t lhs_len, const float *rhs, uint64_t rhs_len,
+                         float *output, uint64_t output_len, emel_stream stream)
+{
+    if (lhs_len == 0 || lhs_len != rhs_len || lhs_len != output_len)
+        return fail(EMEL_ERR_INVALID_SHAPE, "binary slice lengths");
+    if (!lhs || !rhs || !output) return fail(EMEL_ERR_INVALID_ARGUMENT, "null slice");
+    if (!slices_disjoint_or_same(output, output_len, lhs, lhs_len) ||
+        !slices_disjoint_or_same(output, output_len, rhs, rhs_len))
+        return fail(EMEL_ERR_INVALID_ARGUMENT, "output partially overlaps an input");
+    const emel_tensor_view a = slice_view(lhs, lhs_len), b = slice_view(rhs, rhs_len);
+    const emel_tensor_view_mut out = slice_view_mut(output, output_len);
+    return elementwise(op, &a, emel::Addr::SameCoords, &b, emel::Addr::SameCoords, &out, 1.0f, stream);
+}
+
+// op_sqr / op_sqrt (actor.rs:1521-1555): both slices become contiguous
+// [len, 1, 1, 1] views; an empty slice or unequal counts (PowerError
+// InvalidView / ShapeMismatch) map to the root InvalidShape.
+emel_status slice_power(emel::Ew op, const float *input, uint64_t input_len, float *output, uint64_t output_len,
+                        emel_stream stream)
+{
+    if (input_len == 0 || output_len == 0 || input_len != output_len)
+        return fail(EMEL_ERR_INVALID_SHAPE, "power slice lengths");
+    if (!input || !output) return fail(EMEL_ERR_INVALID_ARGUMENT, "null slice");
+    if (!slices_disjoint_or_same(output, output_len, input, input_len))
+        return fail(EMEL_ERR_INVALID_ARGUMENT, "output partially overlaps the input");
+    const emel_tensor_view in = slice_view(input, input_len);
+    const emel_tensor_view_mut out = slice_view_mut(output, output_len);
+    return elementwise(op, &in, emel::Addr::SameCoords, nullptr, emel::Addr::SameCoords, &out, 1.0f, stream);
+}
+
+// power.rs:266-273: validate both views, then equal logical counts.
+emel_status view_power(emel::Ew op, const emel_tensor_view *in, const emel_tensor_view_mut *out, emel_stream stream)
+{
+    if (!in || !out) return fail(EMEL_ERR_INVALID_ARGUMENT, "null view");
+    if (!valid_f32(*in, false) || !valid_f32(*out, false))
+        return fail(EMEL_ERR_INVALID_VIEW, "power view failed validation");
+    if (count_or_zero(*in) != count_or_zero(*out)) return fail(EMEL_ERR_SHAPE_MISMATCH, "power counts differ");
+    return elementwise(op, in, pair_addr(*in, *out), nullptr, emel::Addr::SameCoords, out, 1.0f, stream);
+}
+
+} // namespace
+
+emel_status emel_slice_add(const float *lhs, uint64_t lhs_len, const float *rhs, uint64_t rhs_len, float *output,
+                           uint64_t output_len, emel_stream stream)
+{
+    return slice_binary(emel::Ew::Add, lhs, lhs_len, rhs, rhs_len, output, output_len, stream);
+}
+
+emel_status emel_slice_sub(const float *lhs, uint64_t lhs_len, const float *rhs, uint64_t rhs_len, float *output,
+                           uint64_t output_len, emel_stream stream)
+{
+    return slice_binary(emel::Ew::Sub, lhs, lhs_len, rhs, rhs_len, output, output_len, stream);
+}
+
+emel_status emel_slice_mul(const float *lhs, uint64_t lhs_len, const float *rhs, uint64_t rhs_len, float *output,
+                           uint64_t output_len, emel_stream stream)
+{
+    return slice_binary(emel::Ew::Mul, lhs, lhs_len, rhs, rhs_len, output, output_len, stream);
+}
+
+emel_status emel_slice_div(const float *lhs, uint64_t lhs_len, const float *rhs, uint64_t rhs_len, float *output,
+                           uint64_t output_len, emel_stream stream)
+{
+    return slice_binary(emel::Ew::Div, lhs, lhs_len, rhs, rhs_len, output, output_len, stream);
+}
+
+emel_status emel_slice_sqr(const float *input, uint64_t input_len, float *output, uint64_t output_len,
+                           emel_stream stream)
+{
+    return slice_power(emel::Ew::Sqr, input, input_len, output, output_len, stream);
+}
+
+emel_status emel_slice_sqrt(const float *input, uint64_t input_len, float *output, uint64_t output_len,
+                            emel_stream stream)
+{
+    return slice_power(emel::Ew::Sqrt, input, input_len, output, output_len, stream);
+}
+
+emel_status emel_op_sqr(const emel_tensor_view *in, const emel_tensor_view_mut *out, emel_stream stream)
+{
+    return view_power(emel::Ew::Sqr, in, out, stream);
+}
+
+emel_status emel_op_sqrt(const emel_tensor_view *in, const emel_tensor_view_mut *out, emel_stream stream)
+{
+    return view_power(emel::Ew::Sqrt, in, out, stream);
 }
 
 emel_status emel_op_scale(const emel_tensor_view *in, const emel_tensor_view_mut *out, float scale, emel_stream stream)

@@ -2,8 +2,9 @@
 // equal-count binary add/sub/mul/div (binary.rs:383-424), row broadcast
 // (broadcast.rs:352-390), 4-D modulo broadcast (OpRepeat + binary,
 // generic.rs:1641-1665), unary abs/neg/tanh/elu/relu/sigmoid/gelu/silu/exp
-// (unary.rs:472-606), scale (activation.rs:366-377), fused SwiGLU and the
-// six OpGlu gates (glu.rs:103-141, :258-270).
+// (unary.rs:472-606), scale (activation.rs:366-377), fused SwiGLU, the six
+// OpGlu gates (glu.rs:103-141, :258-270), copy (event.rs:133-165) and square
+// / square root (power.rs:315-360).
 //
 // All of them are HBM-bound streams (<= 1 flop per byte except the
 // transcendental ones, which stay under the memory time).  Three kernel
@@ -141,6 +142,11 @@ __device__ __forceinline__ float glu_gelu_erf(float g, const ExpCtx &t)
     const float erf = sign * (1.0f - poly * emel_expf(-x * x, t.tab, t.c));
     return 0.5f * g * (1.0f + erf);
 }
+// OpDup copies bits; power.rs squares (v * v) and takes the IEEE square
+// root (correctly rounded: checked on the GPU over all 2^32 inputs).
+EMEL_FN(Copy, false, false, a)
+EMEL_FN(Sqr, false, false, a * a)
+EMEL_FN(Sqrt, false, false, __builtin_sqrtf(a))
 EMEL_FN(GluRe, false, true, a * (b > 0.0f ? b : 0.0f))
 EMEL_FN(GluGe, false, true, a * (0.5f * b * (1.0f + emel_tanhf(0.7978846f * b * (1.0f + 0.044715f * b * b)))))
 EMEL_FN(GluSwi, true, true, a * emel_silu(b, t.tab, t.c))
@@ -574,6 +580,9 @@ hipError_t launch_elementwise(const EwArgs &args, hipStream_t stream)
     case Ew::Exp: return launch_op<Ew::Exp>(args, stream);
     case Ew::Scale: return launch_op<Ew::Scale>(args, stream);
     case Ew::Swiglu: return launch_op<Ew::Swiglu>(args, stream);
+    case Ew::Copy: return launch_op<Ew::Copy>(args, stream);
+    case Ew::Sqr: return launch_op<Ew::Sqr>(args, stream);
+    case Ew::Sqrt: return launch_op<Ew::Sqrt>(args, stream);
     case Ew::GluRe: return launch_op<Ew::GluRe>(args, stream);
     case Ew::GluGe: return launch_op<Ew::GluGe>(args, stream);
     case Ew::GluSwi: return launch_op<Ew::GluSwi>(args, stream);

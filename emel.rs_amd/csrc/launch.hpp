@@ -24,7 +24,8 @@ enum class Ew : uint32_t {
     Add = 0, Sub, Mul, Div,                                        // binary
     Abs, Neg, Tanh, Elu, Relu, Sigmoid, Gelu, Silu, Exp, Scale,   // unary
     Swiglu,                                                        // fused
-    GluRe, GluGe, GluSwi, GluSwiOai, GluGeErf, GluGeQuick         // OpGlu: a = values, b = gates
+    GluRe, GluGe, GluSwi, GluSwiOai, GluGeErf, GluGeQuick,        // OpGlu: a = values, b = gates
+    Copy, Sqr, Sqrt                                                // dup and power.rs
 };
 
 // How a source operand is addressed from the destination ordinal.

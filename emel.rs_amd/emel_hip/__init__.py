@@ -4,6 +4,13 @@ include/emel_hip.h, with a Python mirror of emel-kernels' operator API.
 """
 from .abi import BinaryOp, DType, GluSubOp, Status, UnarySubOp, device_count, last_error, load
 from .kernel import (
+    DenseOpAdd,
+    DenseOpDiv,
+    DenseOpDup,
+    DenseOpMul,
+    DenseOpSqr,
+    DenseOpSqrt,
+    DenseOpSub,
     Kernel,
     OpAdd,
     OpAddBroadcastRow,
@@ -23,6 +30,8 @@ from .kernel import (
     OpSilu,
     OpSoftMax,
     OpSoftMaxExt,
+    OpSqr,
+    OpSqrt,
     OpSub,
     OpSum,
     OpSumRows,
@@ -37,4 +46,6 @@ __all__ = [
     "OpAdd", "OpSub", "OpMul", "OpDiv", "OpAddBroadcastRow", "OpMulBroadcastRow", "OpBinaryBroadcast",
     "OpUnary", "OpSilu", "OpGelu", "OpGlu", "OpSwiglu", "OpScale", "OpRmsNorm", "OpRmsNormMul", "OpNorm",
     "OpSoftMax", "OpSoftMaxExt", "OpSumRows", "OpSum", "OpMean", "OpArgmax", "OpArgmaxRows",
+    "OpSqr", "OpSqrt", "DenseOpDup", "DenseOpAdd", "DenseOpSub", "DenseOpMul", "DenseOpDiv", "DenseOpSqr",
+    "DenseOpSqrt",
 ]

@@ -24,6 +24,8 @@ class Status(enum.IntEnum):
     KERNEL_UNAVAILABLE = 6
     DEVICE = 7
     INVALID_ARGUMENT = 8
+    INVALID_SHAPE = 9
+    UNSUPPORTED_OPERATION = 10
 
 
 class DType(enum.IntEnum):
@@ -102,6 +104,13 @@ SIGNATURES = {
     "emel_op_gelu": [_V, _V, _S],
     "emel_op_swiglu": [_V, _V, _V, _S],
     "emel_op_glu": [ctypes.c_uint32, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_uint64, _S],
+    "emel_slice_dup": [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_uint64, _S],
+    "emel_slice_sqr": [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_uint64, _S],
+    "emel_slice_sqrt": [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_uint64, _S],
+    **{f"emel_slice_{op}": [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p,
+                            ctypes.c_uint64, _S] for op in ("add", "sub", "mul", "div")},
+    "emel_op_sqr": [_V, _V, _S],
+    "emel_op_sqrt": [_V, _V, _S],
     "emel_op_scale": [_V, _V, ctypes.c_float, _S],
     "emel_op_rms_norm": [_V, _V, ctypes.c_float, _S],
     "emel_op_rms_norm_mul": [_V, _V, _V, ctypes.c_float, _S],

@@ -179,6 +179,113 @@ class OpGlu:
         return lib.emel_op_glu(int(self.subop), ip, il, op, ol, s)
 
 
+def _slice(t, n=None):
+    """(device pointer, length in floats) of a tensor or raw pointer."""
+    if isinstance(t, int):
+        if n is None:
+            raise ValueError("a raw pointer needs its length")
+        return t, n
+    return int(t.data_ptr()), (t.numel() if n is None else n)
+
+
+@dataclass
+class DenseOpDup:
+    """event::OpDup::new(input, output) (event.rs:133-165): copy a slice."""
+
+    input: object
+    output: object
+    input_len: int | None = None
+    output_len: int | None = None
+
+    def _call(self, lib, s):
+        ip, il = _slice(self.input, self.input_len)
+        op, ol = _slice(self.output, self.output_len)
+        return lib.emel_slice_dup(ip, il, op, ol, s)
+
+
+@dataclass
+class _DenseBinary:
+    lhs: object
+    rhs: object
+    output: object
+    lhs_len: int | None = None
+    rhs_len: int | None = None
+    output_len: int | None = None
+    _fn = ""
+
+    def _call(self, lib, s):
+        lp, ll = _slice(self.lhs, self.lhs_len)
+        rp, rl = _slice(self.rhs, self.rhs_len)
+        op, ol = _slice(self.output, self.output_len)
+        return getattr(lib, self._fn)(lp, ll, rp, rl, op, ol, s)
+
+
+class DenseOpAdd(_DenseBinary):
+    """event::OpAdd::new(lhs, rhs, output) (event.rs:167-208)."""
+    _fn = "emel_slice_add"
+
+
+class DenseOpSub(_DenseBinary):
+    """event::OpSub (event.rs:210-257)."""
+    _fn = "emel_slice_sub"
+
+
+class DenseOpMul(_DenseBinary):
+    """event::OpMul (event.rs:210-258)."""
+    _fn = "emel_slice_mul"
+
+
+class DenseOpDiv(_DenseBinary):
+    """event::OpDiv (event.rs:210-259)."""
+    _fn = "emel_slice_div"
+
+
+@dataclass
+class _DenseUnary:
+    input: object
+    output: object
+    input_len: int | None = None
+    output_len: int | None = None
+    _fn = ""
+
+    def _call(self, lib, s):
+        ip, il = _slice(self.input, self.input_len)
+        op, ol = _slice(self.output, self.output_len)
+        return getattr(lib, self._fn)(ip, il, op, ol, s)
+
+
+class DenseOpSqr(_DenseUnary):
+    """event::OpSqr::new(input, output) (event.rs:523-567)."""
+    _fn = "emel_slice_sqr"
+
+
+class DenseOpSqrt(_DenseUnary):
+    """event::OpSqrt::new(input, output) (event.rs:523-568)."""
+    _fn = "emel_slice_sqrt"
+
+
+@dataclass
+class OpSqr:
+    """power::OpSqr::new(input, output) (power.rs:46-58)."""
+
+    input: TensorView
+    output: TensorViewMut
+
+    def _call(self, lib, s):
+        return lib.emel_op_sqr(_p(self.input), _p(self.output), s)
+
+
+@dataclass
+class OpSqrt:
+    """power::OpSqrt::new(input, output) (power.rs:60-73)."""
+
+    input: TensorView
+    output: TensorViewMut
+
+    def _call(self, lib, s):
+        return lib.emel_op_sqrt(_p(self.input), _p(self.output), s)
+
+
 @dataclass
 class OpScale:
     """activation::OpScale::new(input, output, scale) (activation.rs:58-72)."""

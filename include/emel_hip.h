@@ -55,7 +55,9 @@ typedef enum emel_status {
     EMEL_ERR_INTERNAL = 5,
     EMEL_ERR_KERNEL_UNAVAILABLE = 6, /* no usable gfx950 device */
     EMEL_ERR_DEVICE = 7,             /* a HIP runtime call failed */
-    EMEL_ERR_INVALID_ARGUMENT = 8    /* a required pointer argument is NULL */
+    EMEL_ERR_INVALID_ARGUMENT = 8,   /* a required pointer argument is NULL */
+    EMEL_ERR_INVALID_SHAPE = 9,      /* root Error::InvalidShape (actor.rs:88-101): dense-slice events */
+    EMEL_ERR_UNSUPPORTED_OPERATION = 10 /* root Error::UnsupportedOperation */
 } emel_status;
 
 /* Wire dtype codes, DType::from_code (tensor_view.rs:111-158). */
@@ -191,6 +193,38 @@ emel_status emel_op_gelu(const emel_tensor_view *in, const emel_tensor_view_mut 
  * roundings.  The three views have identical shapes. */
 emel_status emel_op_swiglu(const emel_tensor_view *gate, const emel_tensor_view *up,
                            const emel_tensor_view_mut *out, emel_stream stream);
+
+/* ---- dense-slice root events ----------------------------------------------------
+ * The root kernel's contiguous-buffer events (event.rs:133-259, :523-568):
+ * event::OpDup (copy), event::OpAdd / OpSub / OpMul / OpDiv and event::OpSqr
+ * / OpSqrt, each over caller slices of `len` floats.  Guards (actor.rs:
+ * 2498-2560; op_sqr / op_sqrt :1521-1555 with dense_power_layout :122-125):
+ * every length non-zero and all lengths equal, otherwise the root
+ * Error::InvalidShape (EMEL_ERR_INVALID_SHAPE).  An output that partially
+ * overlaps an input (impossible for Rust's borrowed slices) is
+ * EMEL_ERR_INVALID_ARGUMENT; the output may be exactly an input. */
+emel_status emel_slice_dup(const float *input, uint64_t input_len, float *output, uint64_t output_len,
+                           emel_stream stream);
+emel_status emel_slice_add(const float *lhs, uint64_t lhs_len, const float *rhs, uint64_t rhs_len, float *output,
+                           uint64_t output_len, emel_stream stream);
+emel_status emel_slice_sub(const float *lhs, uint64_t lhs_len, const float *rhs, uint64_t rhs_len, float *output,
+                           uint64_t output_len, emel_stream stream);
+emel_status emel_slice_mul(const float *lhs, uint64_t lhs_len, const float *rhs, uint64_t rhs_len, float *output,
+                           uint64_t output_len, emel_stream stream);
+emel_status emel_slice_div(const float *lhs, uint64_t lhs_len, const float *rhs, uint64_t rhs_len, float *output,
+                           uint64_t output_len, emel_stream stream);
+emel_status emel_slice_sqr(const float *input, uint64_t input_len, float *output, uint64_t output_len,
+                           emel_stream stream);
+emel_status emel_slice_sqrt(const float *input, uint64_t input_len, float *output, uint64_t output_len,
+                            emel_stream stream);
+
+/* ---- square and square root over views -----------------------------------------
+ * power::OpSqr / OpSqrt::new(input, output) (power.rs:46-73; guards
+ * :266-273; v * v and IEEE sqrt(v) over logical ordinals): both views must
+ * validate (EMEL_ERR_INVALID_VIEW) and hold equal element counts
+ * (EMEL_ERR_SHAPE_MISMATCH), as PowerError reports them. */
+emel_status emel_op_sqr(const emel_tensor_view *in, const emel_tensor_view_mut *out, emel_stream stream);
+emel_status emel_op_sqrt(const emel_tensor_view *in, const emel_tensor_view_mut *out, emel_stream stream);
 
 /* ---- gated linear units --------------------------------------------------------
  * glu::OpGlu::new(input, output, subop) (glu.rs:69-92; split_len :85-91;

@@ -729,3 +729,51 @@ int orc_op_glu(int subop, const float *input, uint64_t input_len, float *output,
     return ORC_OK;
 }
 
+/* ------------------------------------------------------------------ */
+/* Dense-slice root events and power.rs                                */
+/* ------------------------------------------------------------------ */
+
+/* guard_dup_valid (actor.rs:2498-2501): input non-empty, lengths equal;
+ * effect_dup_execute copies the slice. */
+int orc_slice_dup(const float *in, uint64_t in_len, float *out, uint64_t out_len)
+{
+    if (in_len == 0 || in_len != out_len) return ORC_INVALID_SHAPE;
+    memcpy(out, in, in_len * sizeof(float));
+    return ORC_OK;
+}
+
+/* guard_{add,sub,mul,div}_valid (actor.rs:2522-2560) and the zip effects. */
+int orc_slice_binary(int op, const float *lhs, uint64_t lhs_len, const float *rhs, uint64_t rhs_len, float *out,
+                     uint64_t out_len)
+{
+    if (lhs_len == 0 || lhs_len != rhs_len || lhs_len != out_len) return ORC_INVALID_SHAPE;
+    for (uint64_t i = 0; i < lhs_len; i++) out[i] = apply_binary(op, lhs[i], rhs[i]);
+    return ORC_OK;
+}
+
+/* power.rs:266-273 and the v * v / sqrt(v) effects over logical ordinals. */
+int orc_op_power(int sqrt_, const orc_view *in, const orc_view *out)
+{
+    if (orc_layout_validate(in, 0) || orc_layout_validate(out, 0)) return ORC_INVALID_VIEW;
+    const uint64_t n = count_or_zero(in);
+    if (n != count_or_zero(out)) return ORC_SHAPE_MISMATCH;
+    rview a = resolve(in), o = resolve(out);
+    for (uint64_t k = 0; k < n; k++) {
+        const float v = rd(&a, k);
+        wr(&o, k, sqrt_ ? sqrtf(v) : v * v);
+    }
+    return ORC_OK;
+}
+
+/* op_sqr / op_sqrt (actor.rs:1521-1555): slices as contiguous [len,1,1,1]
+ * views (dense_power_layout :122-125), PowerError InvalidView and
+ * ShapeMismatch both reported as InvalidShape (map_power_error :127-133). */
+int orc_slice_power(int sqrt_, const float *in, uint64_t in_len, float *out, uint64_t out_len)
+{
+    const uint64_t ine[4] = {in_len, 1, 1, 1}, one[4] = {out_len, 1, 1, 1};
+    orc_view iv = dense_f32((float *)in, ine), ov = dense_f32(out, one);
+    const int s = orc_op_power(sqrt_, &iv, &ov);
+    if (s == ORC_INVALID_VIEW || s == ORC_SHAPE_MISMATCH) return ORC_INVALID_SHAPE;
+    return s;
+}
+

@@ -38,6 +38,7 @@ enum {
     ORC_SHAPE_MISMATCH = 2,
     ORC_INVALID_PARAMETERS = 3,
     ORC_UNEXPECTED_EVENT = 4,
+    ORC_INVALID_SHAPE = 9, /* root Error::InvalidShape */
 };
 
 enum { ORC_ADD = 0, ORC_SUB = 1, ORC_MUL = 2, ORC_DIV = 3 };
@@ -68,6 +69,14 @@ int orc_argmax_rows(const orc_view *src, const orc_view *dst_i32);
 int orc_binary_bcast(int op, const orc_view *src0, const orc_view *src1, const orc_view *dst);
 int orc_rms_norm_mul(const orc_view *in, const orc_view *weight, const orc_view *out, float eps);
 int orc_swiglu(const orc_view *gate, const orc_view *up, const orc_view *out);
+
+/* Dense-slice root events (event.rs:133-259, :523-568; guards actor.rs:
+ * 2498-2560, op_sqr/op_sqrt :1521-1555) and the view power ops (power.rs). */
+int orc_slice_dup(const float *in, uint64_t in_len, float *out, uint64_t out_len);
+int orc_slice_binary(int op, const float *lhs, uint64_t lhs_len, const float *rhs, uint64_t rhs_len, float *out,
+                     uint64_t out_len);
+int orc_slice_power(int sqrt_, const float *in, uint64_t in_len, float *out, uint64_t out_len);
+int orc_op_power(int sqrt_, const orc_view *in, const orc_view *out);
 
 /* OpGlu over a dense slice [values | gates] of 2n floats into n floats
  * (glu.rs:22-160, :258-270).  subop: GluSubOp wire code 0..5. */

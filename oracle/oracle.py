@@ -16,6 +16,7 @@ import numpy as np
 LIB_PATH = Path(__file__).resolve().parent / "libemel_oracle.so"
 
 OK, INVALID_VIEW, SHAPE_MISMATCH, INVALID_PARAMETERS, UNEXPECTED_EVENT = 0, 1, 2, 3, 4
+INVALID_SHAPE = 9
 ADD, SUB, MUL, DIV = 0, 1, 2, 3
 F32, F16, I32 = 0, 1, 26
 
@@ -96,6 +97,14 @@ def lib() -> ctypes.CDLL:
         for name in ("orc_silu", "orc_gelu"):
             getattr(L, name).argtypes = [ctypes.c_float]
             getattr(L, name).restype = ctypes.c_float
+        for name in ("orc_slice_dup",):
+            getattr(L, name).argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_uint64]
+            getattr(L, name).restype = ctypes.c_int
+        L.orc_slice_power.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_uint64]
+        L.orc_slice_power.restype = ctypes.c_int
+        L.orc_slice_binary.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_uint64,
+                                       ctypes.c_void_p, ctypes.c_uint64]
+        L.orc_slice_binary.restype = ctypes.c_int
         L.orc_op_glu.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_uint64]
         L.orc_op_glu.restype = ctypes.c_int
         L.orc_glu_gate.argtypes = [ctypes.c_int, ctypes.c_float]
@@ -139,6 +148,27 @@ def argmax_rows(src, dst): return call("orc_argmax_rows", src, dst)
 def binary_bcast(op, src0, src1, dst): return call("orc_binary_bcast", op, src0, src1, dst)
 def rms_norm_mul(src, w, dst, eps): return call("orc_rms_norm_mul", src, w, dst, ctypes.c_float(eps))
 def swiglu(gate, up, dst): return call("orc_swiglu", gate, up, dst)
+def _f32p(a):
+    assert a.dtype == np.float32
+    return a.ctypes.data
+
+
+def slice_dup(inp, out, in_len=None, out_len=None) -> int:
+    return int(lib().orc_slice_dup(_f32p(inp), inp.size if in_len is None else in_len, _f32p(out),
+                                   out.size if out_len is None else out_len))
+
+
+def slice_binary(op, lhs, rhs, out) -> int:
+    return int(lib().orc_slice_binary(op, _f32p(lhs), lhs.size, _f32p(rhs), rhs.size, _f32p(out), out.size))
+
+
+def slice_power(sqrt_, inp, out) -> int:
+    return int(lib().orc_slice_power(1 if sqrt_ else 0, _f32p(inp), inp.size, _f32p(out), out.size))
+
+
+def op_power(sqrt_, src, dst): return call("orc_op_power", 1 if sqrt_ else 0, src, dst)
+
+
 REGLU, GEGLU, SWIGLU, SWIGLU_OAI, GEGLU_ERF, GEGLU_QUICK = 0, 1, 2, 3, 4, 5
 
 

@@ -158,6 +158,47 @@ def main() -> None:
         },
     }
 
+    # tools/emel-kernel-power-parity/src/main.rs:118-155 (root slice events
+    # and the view PowerKernel)
+    pw = manifest("kernel-power")
+    fx["power"] = {
+        "source": pw["source"],
+        "inputs": "tools/emel-kernel-power-parity/src/main.rs:118-155",
+        "cases": [
+            {"name": "dense_square", "route": "slice_sqr", "input": [-2.0, -0.5, 0.5, 2.0], "out_len": 4,
+             "out_fill": 0.0, **pw["cases"]["dense_square"]},
+            {"name": "strided_square", "route": "view_sqr", "input": [3.0, 99.0, -4.0, 99.0, 0.5], "ne": [3, 1, 1, 1],
+             "nb": [8, 24, 72, 72], "out_len": 5, "out_fill": 0.0, **pw["cases"]["strided_square"]},
+            {"name": "count_equal_different_dimensions", "route": "slice_sqr", "input": [1.0, 2.0, 3.0, 4.0],
+             "out_len": 4, "out_fill": 0.0, **pw["cases"]["count_equal_different_dimensions"]},
+            {"name": "implicit_contiguous_square", "route": "view_sqr", "input": [1.0, 2.0, 3.0, 4.0],
+             "ne": [4, 1, 1, 1], "nb": [0, 0, 0, 0], "out_len": 4, "out_fill": 0.0,
+             **pw["cases"]["implicit_contiguous_square"]},
+            {"name": "dense_square_root", "route": "slice_sqrt", "input": [0.0, 1.0, 4.0, 9.0], "out_len": 4,
+             "out_fill": 0.0, **pw["cases"]["dense_square_root"]},
+            {"name": "shape_rejection", "route": "slice_sqr", "input": [1.0, 2.0, 3.0, 4.0], "out_len": 3,
+             "out_fill": 9.0, **pw["cases"]["shape_rejection"]},
+        ],
+    }
+    # crates/emel-kernels/tests/any/ops.rs:13-124 (root dense-slice events)
+    fx["known_answers"]["slice_ops"] = {
+        "source": "crates/emel-kernels/tests/any/ops.rs:13-124",
+        "dup": {"input": [1.0, -2.5, 4.0], "output": [1.0, -2.5, 4.0]},
+        "add": {"lhs": [1.0, -2.5, 4.0], "rhs": [2.0, 0.5, -1.0], "output": [3.0, -2.0, 3.0]},
+        "sub": {"lhs": [9.0, -4.0, 2.0], "rhs": [3.0, 2.0, -4.0], "output": [6.0, -6.0, 6.0]},
+        "mul": {"lhs": [9.0, -4.0, 2.0], "rhs": [3.0, 2.0, -4.0], "output": [27.0, -8.0, -8.0]},
+        "div": {"lhs": [9.0, -4.0, 2.0], "rhs": [3.0, 2.0, -4.0], "output": [3.0, -2.0, -0.5]},
+        "sqr": {"input": [3.0, 2.0, -4.0], "output": [9.0, 4.0, 16.0]},
+        "sqrt": {"input": [9.0, 4.0, 16.0], "output": [3.0, 2.0, 4.0]},
+        "invalid_shape": [
+            {"event": "dup", "in_len": 2, "out_len": 1}, {"event": "add", "lhs_len": 2, "rhs_len": 1, "out_len": 2},
+            {"event": "dup", "in_len": 0, "out_len": 0}, {"event": "sub", "lhs_len": 2, "rhs_len": 1, "out_len": 2},
+            {"event": "mul", "lhs_len": 2, "rhs_len": 1, "out_len": 2},
+            {"event": "div", "lhs_len": 2, "rhs_len": 1, "out_len": 2},
+            {"event": "sqr", "in_len": 2, "out_len": 1}, {"event": "sqrt", "in_len": 2, "out_len": 1},
+        ],
+    }
+
     OUT.write_text(json.dumps(fx, indent=1) + "\n")
     print(f"wrote {OUT}")
 

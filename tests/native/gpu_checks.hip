@@ -5,6 +5,10 @@
 //   hw_fp32_to_fp16 vs emel_fp32_to_fp16  (all 2^32 f32 inputs)
 //   hw_fp16_to_f32  vs emel_fp16_to_f32   (all 65536 f16 inputs)
 //   emel_expf_nonpos vs emel_expf         (all f32 <= 0, and NaNs)
+//   __builtin_sqrtf (the power.rs kernels) correctly rounded: for every
+//   positive finite x the exact squares of the two rounding midpoints
+//   around the result bracket x (exact in double: <= 52 significant bits);
+//   sqrt(+-0) = +-0, sqrt(+inf) = +inf, negatives and NaN give NaN
 // NaN results match NaN results.  Each entry point launches a grid-stride
 // kernel over the range on the null stream, waits, and returns the number
 // of mismatching inputs (or UINT64_MAX on a HIP error).
@@ -57,6 +61,35 @@ __global__ void k_expf_nonpos(uint64_t lo, uint64_t hi)
     if (bad) atomicAdd(&g_bad, bad);
 }
 
+__global__ void k_sqrtf(uint64_t lo, uint64_t hi)
+{
+    unsigned long long bad = 0;
+    for (uint64_t u = lo + blockIdx.x * 256ull + threadIdx.x; u < hi; u += 256ull * gridDim.x) {
+        const float x = emel::bits_to_f32(static_cast<uint32_t>(u));
+        const float y = __builtin_sqrtf(x);
+        const uint32_t yb = emel::f32_to_bits(y);
+        bool ok;
+        if (x != x || x < 0.0f) {
+            ok = y != y;
+        } else if (x == 0.0f || x == __builtin_inff()) {
+            ok = yb == emel::f32_to_bits(x);
+        } else {
+            const uint32_t e = (yb >> 23) & 0xffu;
+            if (e == 0u || e == 0xffu || (yb >> 31) != 0u) {
+                ok = false;
+            } else {
+                const double ulp = __builtin_ldexp(1.0, static_cast<int>(e) - 150);
+                const double below = (yb & 0x7fffffu) == 0u ? ulp / 4 : ulp / 2; // next value down has half the ulp
+                const double d = static_cast<double>(y), xd = static_cast<double>(x);
+                const double l = d - below, h = d + ulp / 2;
+                ok = l * l < xd && xd < h * h;
+            }
+        }
+        if (!ok) ++bad;
+    }
+    if (bad) atomicAdd(&g_bad, bad);
+}
+
 template <class Launch>
 uint64_t run(Launch launch)
 {
@@ -86,6 +119,11 @@ uint64_t gpu_check_fp16_to_f32(void)
 uint64_t gpu_check_expf_nonpos(void)
 {
     return run([] { k_expf_nonpos<<<8192, 256>>>(0, 1ull << 32); });
+}
+
+uint64_t gpu_check_sqrtf(void)
+{
+    return run([] { k_sqrtf<<<8192, 256>>>(0, 1ull << 32); });
 }
 
 } // extern "C"

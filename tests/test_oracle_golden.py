@@ -167,3 +167,46 @@ def test_softmax_stability_known_answer():
     assert orc.soft_max(orc.view(x, k["ne"]), orc.view(out, k["ne"])) == orc.OK
     assert np.isfinite(out).all()
     assert abs(out[:3].sum() - 1.0) < k["row_sum_tol"] and abs(out[3:].sum() - 1.0) < k["row_sum_tol"]
+
+
+@pytest.mark.parametrize("case", FX["power"]["cases"], ids=lambda c: c["name"])
+def test_power_manifest(case):
+    """snapshots/parity/kernel-power: root OpSqr/OpSqrt over slices and the
+    view PowerKernel (strided and implicit layouts)."""
+    inp = np.array(case["input"], np.float32)
+    out = np.full(case["out_len"], case["out_fill"], np.float32)
+    if case["route"] == "view_sqr":
+        st = orc.op_power(False, orc.view(inp, case["ne"], case["nb"]), orc.view(out, case["ne"], case["nb"]))
+        got = logical(out, case["ne"], case["nb"])
+    else:
+        st = orc.slice_power(case["route"] == "slice_sqrt", inp, out)
+        got = out
+    assert (st == orc.OK) == (case["status"] == "ok")
+    if case["status"] != "ok":
+        assert st == orc.INVALID_SHAPE
+    assert list(bits(got)) == case["output_bits"]
+
+
+def test_slice_ops_known_answers():
+    """crates/emel-kernels/tests/any/ops.rs: root dense-slice events."""
+    ka = FX["known_answers"]["slice_ops"]
+    f = lambda xs: np.array(xs, np.float32)  # noqa: E731
+    out = np.zeros(3, np.float32)
+    assert orc.slice_dup(f(ka["dup"]["input"]), out) == orc.OK and list(out) == ka["dup"]["output"]
+    for name, op in (("add", orc.ADD), ("sub", orc.SUB), ("mul", orc.MUL), ("div", orc.DIV)):
+        c = ka[name]
+        assert orc.slice_binary(op, f(c["lhs"]), f(c["rhs"]), out) == orc.OK
+        assert list(out) == c["output"], name
+    assert orc.slice_power(False, f(ka["sqr"]["input"]), out) == orc.OK and list(out) == ka["sqr"]["output"]
+    assert orc.slice_power(True, f(ka["sqrt"]["input"]), out) == orc.OK and list(out) == ka["sqrt"]["output"]
+    for case in ka["invalid_shape"]:
+        ev = case["event"]
+        if ev == "dup":
+            st = orc.slice_dup(np.ones(max(case["in_len"], 1), np.float32), np.ones(max(case["out_len"], 1), np.float32),
+                               case["in_len"], case["out_len"])
+        elif ev in ("sqr", "sqrt"):
+            st = orc.slice_power(ev == "sqrt", np.ones(case["in_len"], np.float32), np.ones(case["out_len"], np.float32))
+        else:
+            st = orc.slice_binary(OPS[ev], np.ones(case["lhs_len"], np.float32), np.ones(case["rhs_len"], np.float32),
+                                  np.ones(case["out_len"], np.float32))
+        assert st == orc.INVALID_SHAPE, case
