@@ -181,6 +181,32 @@ bool overlap_ok(const emel_tensor_view_mut &dst, uint64_t delem, const S &src, u
            std::memcmp(dst.nb, src.nb, sizeof dst.nb) == 0;
 }
 
+// Whether no two elements of a validated view share a byte, by the
+// sufficient rule: with the dims of extent > 1 sorted by stride, each stride
+// is at least the span of the dims below it.  The reference's sequential
+// loops accept any layout and keep the last write to a shared element; the
+// device writes in parallel, so a view that fails this rule is refused
+// rather than written in an unspecified order.
+template <class V>
+bool elements_disjoint(const V &v, uint64_t elem)
+{
+    uint64_t st[4];
+    if (!effective_f32_strides(v, st)) std::memcpy(st, v.nb, sizeof st);
+    int dims[4];
+    int n = 0;
+    for (int d = 0; d < 4; ++d)
+        if (v.ne[d] > 1) dims[n++] = d;
+    for (int i = 1; i < n; ++i)
+        for (int j = i; j > 0 && st[dims[j]] < st[dims[j - 1]]; --j) std::swap(dims[j], dims[j - 1]);
+    u128 span = elem;
+    for (int i = 0; i < n; ++i) {
+        const int d = dims[i];
+        if (static_cast<u128>(st[d]) < span) return false;
+        span += static_cast<u128>(v.ne[d] - 1) * st[d];
+    }
+    return true;
+}
+
 template <class V>
 Operand operand(const V &v, uint64_t elem)
 {
@@ -264,15 +290,18 @@ hipStream_t as_stream(emel_stream s) { return static_cast<hipStream_t>(s); }
 // ---- op plumbing ---------------------------------------------------------------
 
 emel_status elementwise(emel::Ew op, const emel_tensor_view *a, emel::Addr aa, const emel_tensor_view *b,
-                        emel::Addr ba, const emel_tensor_view_mut *o, float scale, emel_stream stream)
+                        emel::Addr ba, const emel_tensor_view_mut *o, float scale, emel_stream stream,
+                        float scale2 = 0.0f)
 {
     if (!overlap_ok(*o, 4, *a, 4) || (b && !overlap_ok(*o, 4, *b, 4)))
         return fail(EMEL_ERR_INVALID_VIEW, "dst partially overlaps a source");
+    if (!elements_disjoint(*o, 4)) return fail(EMEL_ERR_INVALID_VIEW, "dst elements overlap one another");
     emel_status s = ensure_device();
     if (s != EMEL_OK) return s;
     emel::EwArgs args{};
     args.op = op;
     args.scale = scale;
+    args.scale2 = scale2;
     args.a = operand(*a, 4);
     if (b) args.b = operand(*b, 4);
     args.o = operand(*o, 4);
@@ -360,6 +389,7 @@ emel_status rows(const emel::RowArgs &args, const emel_tensor_view &in, const em
     if (!overlap_ok(out, 4, in, 4)) return fail(EMEL_ERR_INVALID_VIEW, "dst partially overlaps the source");
     if (extra && !overlap_ok(out, 4, *extra, extra->dtype == EMEL_DTYPE_F16 ? 2 : 4))
         return fail(EMEL_ERR_INVALID_VIEW, "dst overlaps an operand");
+    if (!elements_disjoint(out, 4)) return fail(EMEL_ERR_INVALID_VIEW, "dst elements overlap one another");
     emel_status s = ensure_device();
     if (s != EMEL_OK) return s;
     return launched(emel::launch_rows(args, as_stream(stream)));
@@ -369,6 +399,7 @@ emel_status reduce(emel::RedOp op, const emel_tensor_view &src, const emel_tenso
 {
     if (!overlap_ok(dst, 4, src, 4) || dst.data == src.data)
         return fail(EMEL_ERR_INVALID_VIEW, "dst overlaps the source");
+    if (!elements_disjoint(dst, 4)) return fail(EMEL_ERR_INVALID_VIEW, "dst elements overlap one another");
     emel_status s = ensure_device();
     if (s != EMEL_OK) return s;
     emel::RedArgs args{};
@@ -428,7 +459,8 @@ emel_status norm_op(emel::RowOp op, const emel_tensor_view *in, const emel_tenso
 
 } // namespace
 
-extern "C" {
+// The entry points below take C language linkage from their declarations in
+// emel_hip.h; the helper namespaces between them stay internal.
 
 uint32_t emel_abi_version(void) { return EMEL_HIP_ABI_VERSION; }
 
@@ -919,4 +951,593 @@ emel_status emel_op_argmax_rows(const emel_tensor_view *src, const emel_tensor_v
     return reduce(emel::RedOp::ArgmaxRows, *src, *dst, stream);
 }
 
-} // extern "C"
+// ---- generic wire envelope (generic.rs, guards actor.rs:2448-2983) ----------
+
+namespace {
+
+enum GenOpCode : uint32_t {
+    kDup = 0, kAdd = 1, kAdd1 = 3, kSub = 5, kMul = 6, kDiv = 7, kSqr = 8, kSqrt = 9, kLog = 10, kSin = 11,
+    kCos = 12, kSum = 13, kCumsum = 15, kMean = 16, kArgmax = 17, kCountEqual = 18, kRepeat = 19,
+    kRepeatBack = 20, kConcat = 21, kSiluBack = 22, kNorm = 23, kRmsNorm = 24, kRmsNormBack = 25, kL2Norm = 27,
+    kMulMat = 28, kMulMatArgmax = 29, kScale = 32, kDiag = 43, kDiagMaskInf = 44, kDiagMaskZero = 45,
+    kSoftMax = 46, kSoftMaxBack = 47, kClamp = 50, kArange = 66, kLeakyRelu = 70, kFill = 72, kUnary = 85,
+    kGenericOps = 95
+};
+
+using GView = emel_tensor_view; // the sources; dst is read through the same fields
+
+struct GenReq {
+    const emel_generic_request &r;
+    const GView *s0, *s1, *s2, *d;
+
+    explicit GenReq(const emel_generic_request &req)
+        : r(req), s0(req.src0), s1(req.src1), s2(req.src2),
+          d(reinterpret_cast<const GView *>(req.dst)) {}
+
+    bool param_bytes(uint32_t slot, uint8_t out[4]) const
+    {
+        if (r.op_params_size < 4 * (slot + 1)) return false;
+        std::memcpy(out, r.op_params + 4 * slot, 4);
+        return true;
+    }
+    bool param_f32(uint32_t slot, float &v) const
+    {
+        uint8_t b[4];
+        if (!param_bytes(slot, b)) return false;
+        std::memcpy(&v, b, 4);
+        return true;
+    }
+    bool param_i32(uint32_t slot, int32_t &v) const
+    {
+        uint8_t b[4];
+        if (!param_bytes(slot, b)) return false;
+        std::memcpy(&v, b, 4);
+        return true;
+    }
+};
+
+// The strides validate_span and byte_offset use: effective F32 strides for
+// F32, the given nb otherwise (generic.rs:850-857, :911-917).
+bool gen_strides(const GView &v, uint64_t st[4])
+{
+    if (v.dtype == EMEL_DTYPE_F32) return effective_f32_strides(v, st);
+    std::memcpy(st, v.nb, sizeof v.nb);
+    return true;
+}
+
+// validate_span (generic.rs:849-894): non-zero extents with a usize count,
+// no zero stride on an extent > 1, and the last element's first byte inside
+// the slice.
+bool gen_span(const GView &v)
+{
+    uint64_t st[4];
+    if (!gen_strides(v, st)) return false;
+    u128 count = 1;
+    for (int d = 0; d < 4; ++d) {
+        if (v.ne[d] == 0) return false;
+        count *= v.ne[d];
+        if (count > static_cast<u128>(UINT64_MAX)) return false;
+        if (v.ne[d] > 1 && st[d] == 0) return false;
+    }
+    u128 max_offset = 0;
+    for (int d = 0; d < 4; ++d) {
+        const u128 c = static_cast<u128>(v.ne[d] - 1) * st[d];
+        if (max_offset > ~static_cast<u128>(0) - c) return false;
+        max_offset += c;
+    }
+    return max_offset + 1 <= static_cast<u128>(v.data_bytes);
+}
+
+// RawTensorView::f32_valid (generic.rs:471-476).
+bool gen_f32(const GView *v)
+{
+    if (!v || v->dtype != EMEL_DTYPE_F32) return false;
+    uint64_t st[4];
+    if (!effective_f32_strides(*v, st) || !gen_span(*v)) return false;
+    for (int d = 0; d < 4; ++d)
+        if (st[d] < 4) return false;
+    return true;
+}
+
+// RawTensorView::f16_valid (generic.rs:489-493) with is_dense_contiguous_f16
+// (tensor_view.rs:293-314).
+bool gen_f16(const GView *v)
+{
+    if (!v || v->dtype != EMEL_DTYPE_F16 || !gen_span(*v)) return false;
+    u128 expect = 2;
+    for (int d = 0; d < 4; ++d) {
+        if (v->nb[d] != expect) return false;
+        expect *= v->ne[d];
+        if (expect > static_cast<u128>(UINT64_MAX)) return false;
+    }
+    return true;
+}
+
+uint64_t gen_count(const GView *v) { return count_or_zero(*v); }
+
+bool ne_eq(const GView *a, const GView *b) { return same_ne(*a, *b); }
+
+bool ne_is(const GView *v, uint64_t a, uint64_t b, uint64_t c, uint64_t e)
+{
+    return v->ne[0] == a && v->ne[1] == b && v->ne[2] == c && v->ne[3] == e;
+}
+
+// GenericRequest::validate (generic.rs:769-789).
+bool gen_request_valid(const GenReq &q)
+{
+    for (const GView *v : {q.s0, q.s1, q.s2, q.d})
+        if (v && !gen_span(*v)) return false;
+    return !(q.r.operation == kMulMatArgmax && !q.r.index_out);
+}
+
+// ---- the maintained predicates (generic.rs:935-1262) ----
+
+bool pair_valid(const GenReq &q)
+{
+    return gen_f32(q.s0) && gen_f32(q.d) && gen_count(q.s0) == gen_count(q.d);
+}
+
+bool triplet_valid(const GenReq &q)
+{
+    return gen_f32(q.s0) && gen_f32(q.s1) && gen_f32(q.d) && ne_eq(q.s0, q.s1) && ne_eq(q.s0, q.d);
+}
+
+bool scalar_valid(const GenReq &q)
+{
+    float p;
+    return pair_valid(q) && q.param_f32(0, p) && std::isfinite(p);
+}
+
+bool clamp_valid(const GenReq &q)
+{
+    float lo, hi;
+    return pair_valid(q) && q.param_f32(0, lo) && q.param_f32(1, hi) && std::isfinite(lo) && std::isfinite(hi) &&
+           lo <= hi;
+}
+
+bool cumsum_valid(const GenReq &q) { return gen_f32(q.s0) && gen_f32(q.d) && ne_eq(q.s0, q.d); }
+
+bool repeat_shape(const GView *src, const GView *dst)
+{
+    for (int d = 0; d < 4; ++d)
+        if (src->ne[d] == 0 || dst->ne[d] == 0 || dst->ne[d] % src->ne[d] != 0) return false;
+    return true;
+}
+
+bool repeat_valid(const GenReq &q) { return gen_f32(q.s0) && gen_f32(q.d) && repeat_shape(q.s0, q.d); }
+bool repeat_back_valid(const GenReq &q) { return gen_f32(q.s0) && gen_f32(q.d) && repeat_shape(q.d, q.s0); }
+
+bool concat_valid(const GenReq &q, int axis)
+{
+    int32_t p;
+    if (!gen_f32(q.s0) || !gen_f32(q.s1) || !gen_f32(q.d) || !q.param_i32(0, p) || p != axis) return false;
+    for (int d = 0; d < 4; ++d) {
+        if (d == axis) {
+            const u128 sum = static_cast<u128>(q.s0->ne[d]) + q.s1->ne[d];
+            if (sum != q.d->ne[d]) return false;
+        } else if (q.s0->ne[d] != q.s1->ne[d] || q.s0->ne[d] != q.d->ne[d]) {
+            return false;
+        }
+    }
+    return true;
+}
+
+bool fill_valid(const GenReq &q)
+{
+    float v;
+    return !q.s0 && gen_f32(q.d) && q.param_f32(0, v) && std::isfinite(v);
+}
+
+bool arange_valid(const GenReq &q)
+{
+    float a, b;
+    return !q.s0 && gen_f32(q.d) && q.param_f32(0, a) && std::isfinite(a) && q.param_f32(1, b) && std::isfinite(b);
+}
+
+bool diag_valid(const GenReq &q)
+{
+    if (!q.s0 || !q.d) return false;
+    const uint64_t n = q.s0->ne[0];
+    const u128 side = static_cast<u128>(n) * n;
+    if (side > static_cast<u128>(UINT64_MAX)) return false;
+    return gen_f32(q.s0) && gen_f32(q.d) && q.s0->ne[1] == 1 && q.s0->ne[2] == 1 && q.s0->ne[3] == 1 &&
+           ne_is(q.d, n, n, 1, 1) && gen_count(q.d) == static_cast<uint64_t>(side);
+}
+
+bool mask_valid(const GenReq &q)
+{
+    int32_t n_past;
+    if (!q.s0 || !q.d || !q.param_i32(0, n_past)) return false;
+    const GView *s = q.s0;
+    return n_past >= 0 && gen_f32(q.s0) && gen_f32(q.d) && ne_eq(q.s0, q.d) && s->ne[0] > 0 && s->ne[1] == s->ne[0] &&
+           s->ne[2] == 1 && s->ne[3] == 1;
+}
+
+bool l2_valid(const GenReq &q) { return gen_f32(q.s0) && gen_f32(q.d) && ne_eq(q.s0, q.d) && gen_count(q.s0) > 0; }
+
+bool softmax_back_valid(const GenReq &q)
+{
+    int32_t row;
+    if (!triplet_valid(q) || !q.param_i32(0, row)) return false;
+    return row > 0 && gen_count(q.s0) % static_cast<uint64_t>(row) == 0;
+}
+
+bool rms_norm_back_valid(const GenReq &q)
+{
+    float eps;
+    if (!triplet_valid(q) || !q.param_f32(0, eps)) return false;
+    return std::isfinite(eps) && eps >= 0.0f && q.s0->ne[0] > 0;
+}
+
+bool count_equal_valid(const GenReq &q)
+{
+    return gen_f32(q.s0) && gen_f32(q.s1) && gen_f32(q.d) && gen_count(q.s0) == gen_count(q.s1) &&
+           gen_count(q.d) == 1;
+}
+
+bool binary_valid(const GenReq &q)
+{
+    return gen_f32(q.s0) && gen_f32(q.s1) && gen_f32(q.d) && gen_count(q.s0) == gen_count(q.s1) &&
+           gen_count(q.s0) == gen_count(q.d);
+}
+
+bool reduce_valid(const GenReq &q) { return gen_f32(q.s0) && gen_f32(q.d) && gen_count(q.d) == 1; }
+
+bool norm_valid(const GenReq &q)
+{
+    float eps;
+    return gen_f32(q.s0) && gen_f32(q.d) && ne_eq(q.s0, q.d) && q.param_f32(0, eps) && std::isfinite(eps) &&
+           eps >= 0.0f;
+}
+
+bool matmul_f32_valid(const GenReq &q)
+{
+    if (!gen_f32(q.s0) || !gen_f32(q.s1) || !gen_f32(q.d)) return false;
+    const uint64_t *l = q.s0->ne, *r = q.s1->ne, *o = q.d->ne;
+    return l[0] > 0 && l[1] > 0 && r[0] > 0 && r[1] == l[0] && o[0] == r[0] && o[1] == l[1] && l[2] == 1 &&
+           l[3] == 1 && r[2] == 1 && r[3] == 1 && o[2] == 1 && o[3] == 1;
+}
+
+bool matmul_argmax_valid(const GenReq &q)
+{
+    if (!q.r.index_out || !gen_f32(q.s0) || !gen_f32(q.s1) || !gen_f32(q.d)) return false;
+    const uint64_t *l = q.s0->ne;
+    return l[0] > 0 && l[1] > 0 && ne_is(q.s1, l[0], 1, 1, 1) && ne_is(q.d, 1, 1, 1, 1) && l[2] == 1 && l[3] == 1;
+}
+
+bool matmul_f16_valid(const GenReq &q)
+{
+    if (!gen_f16(q.s0) || !gen_f16(q.s1) || !gen_f32(q.d)) return false;
+    const uint64_t *l = q.s0->ne, *r = q.s1->ne, *o = q.d->ne;
+    return l[0] > 0 && l[1] > 0 && r[0] == l[0] && r[1] > 0 && o[0] == l[1] && o[1] == r[1] && l[2] == 1 &&
+           l[3] == 1 && r[2] == 1 && r[3] == 1 && o[2] == 1 && o[3] == 1;
+}
+
+// The eight unary subops the generic lane executes (actor.rs:2875-2905).
+bool unary_subop_routed(uint32_t s)
+{
+    return s == EMEL_UNARY_ABS || s == EMEL_UNARY_NEG || s == EMEL_UNARY_TANH || s == EMEL_UNARY_ELU ||
+           s == EMEL_UNARY_RELU || s == EMEL_UNARY_GELU || s == EMEL_UNARY_SILU || s == EMEL_UNARY_EXP;
+}
+
+enum class Route {
+    None, Dup, Binary, Scalar, Clamp, SiluBack, Cumsum, Repeat, RepeatBack, Concat, Diag, DiagMask, SoftMaxBack,
+    RmsNormBack, L2Norm, CountEqual, Fill, Arange, MulMatF32, MulMatF16, MulMatArgmax, Power, Unsupported, Reduce,
+    SoftMax, Norm, Unary
+};
+
+// The guarded transitions of sm.rs:322-413, each `operation == X && route
+// predicate`; at most one can hold for a request.
+Route gen_route(const GenReq &q, int &concat_axis)
+{
+    switch (q.r.operation) {
+    case kDup: return pair_valid(q) ? Route::Dup : Route::None;
+    case kAdd: case kSub: case kMul: case kDiv: return binary_valid(q) ? Route::Binary : Route::None;
+    case kAdd1: case kScale: case kLeakyRelu: return scalar_valid(q) ? Route::Scalar : Route::None;
+    case kClamp: return clamp_valid(q) ? Route::Clamp : Route::None;
+    case kSiluBack: return triplet_valid(q) ? Route::SiluBack : Route::None;
+    case kCumsum: return cumsum_valid(q) ? Route::Cumsum : Route::None;
+    case kRepeat: return repeat_valid(q) ? Route::Repeat : Route::None;
+    case kRepeatBack: return repeat_back_valid(q) ? Route::RepeatBack : Route::None;
+    case kConcat:
+        for (int a = 0; a < 4; ++a)
+            if (concat_valid(q, a)) {
+                concat_axis = a;
+                return Route::Concat;
+            }
+        return Route::None;
+    case kDiag: return diag_valid(q) ? Route::Diag : Route::None;
+    case kDiagMaskInf: case kDiagMaskZero: return mask_valid(q) ? Route::DiagMask : Route::None;
+    case kSoftMaxBack: return softmax_back_valid(q) ? Route::SoftMaxBack : Route::None;
+    case kRmsNormBack: return rms_norm_back_valid(q) ? Route::RmsNormBack : Route::None;
+    case kL2Norm: return l2_valid(q) ? Route::L2Norm : Route::None;
+    case kCountEqual: return count_equal_valid(q) ? Route::CountEqual : Route::None;
+    case kFill: return fill_valid(q) ? Route::Fill : Route::None;
+    case kArange: return arange_valid(q) ? Route::Arange : Route::None;
+    case kMulMat:
+        if (matmul_f32_valid(q)) return Route::MulMatF32;
+        return matmul_f16_valid(q) ? Route::MulMatF16 : Route::None;
+    case kMulMatArgmax: return matmul_argmax_valid(q) ? Route::MulMatArgmax : Route::None;
+    case kSqr: case kSqrt: return pair_valid(q) ? Route::Power : Route::None;
+    case kLog: case kSin: case kCos: return pair_valid(q) ? Route::Unsupported : Route::None;
+    case kSum: case kMean: case kArgmax: return reduce_valid(q) ? Route::Reduce : Route::None;
+    case kSoftMax: return pair_valid(q) ? Route::SoftMax : Route::None;
+    case kNorm: case kRmsNorm: return norm_valid(q) ? Route::Norm : Route::None;
+    case kUnary: return unary_subop_routed(q.r.unary_subop) && pair_valid(q) ? Route::Unary : Route::None;
+    default: return Route::None;
+    }
+}
+
+// guard_generic_known_invalid (actor.rs:2907-2983): the maintained
+// operations whose predicate failed (gen_route gave None).
+bool gen_maintained(uint32_t op)
+{
+    switch (op) {
+    case kDup: case kAdd: case kSub: case kMul: case kDiv: case kAdd1: case kScale: case kLeakyRelu: case kClamp:
+    case kSiluBack: case kCumsum: case kRepeat: case kRepeatBack: case kConcat: case kDiag: case kDiagMaskInf:
+    case kDiagMaskZero: case kSoftMaxBack: case kRmsNormBack: case kL2Norm: case kCountEqual: case kFill:
+    case kArange: case kMulMat: case kMulMatArgmax: case kSqr: case kSqrt: case kLog: case kSin: case kCos:
+    case kSum: case kMean: case kArgmax: case kSoftMax: case kNorm: case kRmsNorm: case kUnary:
+        return true;
+    default:
+        return false;
+    }
+}
+
+// Routes where each lane reads a source element (or row) before writing the
+// same-ordinal destination element (or row), so dst may be the source view.
+bool alias_ok(Route r)
+{
+    switch (r) {
+    case Route::Dup: case Route::Binary: case Route::Scalar: case Route::Clamp: case Route::SiluBack:
+    case Route::Cumsum: case Route::Repeat: case Route::RepeatBack: case Route::DiagMask: case Route::SoftMaxBack:
+    case Route::RmsNormBack: case Route::L2Norm: case Route::Power: case Route::SoftMax: case Route::Norm:
+    case Route::Unary:
+        return true;
+    default:
+        return false;
+    }
+}
+
+bool same_view(const GView &a, const GView &b)
+{
+    if (a.data != b.data || !same_ne(a, b)) return false;
+    uint64_t sa[4], sb[4];
+    if (!gen_strides(a, sa) || !gen_strides(b, sb)) return false;
+    for (int d = 0; d < 4; ++d)
+        if (a.ne[d] > 1 && sa[d] != sb[d]) return false;
+    return true;
+}
+
+uint64_t elem_bytes(const GView &v) { return v.dtype == EMEL_DTYPE_F16 ? 2 : 4; }
+
+// The element-aligned addressing the device kernels use.
+bool gen_aligned(const GView &v)
+{
+    const uint64_t e = elem_bytes(v);
+    if (reinterpret_cast<uintptr_t>(v.data) % e != 0) return false;
+    uint64_t st[4];
+    if (!gen_strides(v, st)) return false;
+    for (int d = 0; d < 4; ++d)
+        if (v.ne[d] > 1 && st[d] % e != 0) return false;
+    return true;
+}
+
+// The whole last element inside data_bytes (validate_span checks its first
+// byte only).
+bool gen_whole(const GView &v)
+{
+    uint64_t st[4];
+    if (!gen_strides(v, st)) return false;
+    return span_fits(v, st, elem_bytes(v));
+}
+
+emel::GView gview(const GView &v)
+{
+    emel::GView g{};
+    g.data = const_cast<void *>(v.data);
+    uint64_t st[4];
+    gen_strides(v, st);
+    const uint64_t e = elem_bytes(v);
+    for (int d = 0; d < 4; ++d) {
+        g.ne[d] = v.ne[d];
+        g.st[d] = static_cast<int64_t>(st[d] / e);
+    }
+    return g;
+}
+
+emel::Ew unary_generic_fn(uint32_t s)
+{
+    switch (s) {
+    case EMEL_UNARY_ABS: return emel::Ew::Abs;
+    case EMEL_UNARY_NEG: return emel::Ew::Neg;
+    case EMEL_UNARY_TANH: return emel::Ew::Tanh;
+    case EMEL_UNARY_ELU: return emel::Ew::Elu;
+    case EMEL_UNARY_RELU: return emel::Ew::Relu;
+    case EMEL_UNARY_GELU: return emel::Ew::GeluGeneric;
+    case EMEL_UNARY_SILU: return emel::Ew::Silu;
+    default: return emel::Ew::Exp;
+    }
+}
+
+emel_status gen_execute(const GenReq &q, Route route, int concat_axis, emel_stream stream)
+{
+    const uint32_t op = q.r.operation;
+    if (route == Route::Unsupported)
+        return fail(EMEL_ERR_UNSUPPORTED_OPERATION, "log/sin/cos have no bit-exact device replica");
+    const GView &dst = *q.d;
+    const emel_tensor_view_mut &dmut = *q.r.dst;
+    const GView *used[3] = {nullptr, nullptr, nullptr};
+    int n_used = 0;
+    switch (route) {
+    case Route::Fill: case Route::Arange: break;
+    case Route::Binary: case Route::SiluBack: case Route::Concat: case Route::SoftMaxBack: case Route::RmsNormBack:
+    case Route::CountEqual: case Route::MulMatF32: case Route::MulMatF16: case Route::MulMatArgmax:
+        used[n_used++] = q.s0;
+        used[n_used++] = q.s1;
+        break;
+    default: used[n_used++] = q.s0; break;
+    }
+
+    // Divergences from the reference, refused before anything is enqueued.
+    for (int i = 0; i < n_used; ++i)
+        if (!gen_aligned(*used[i])) return fail(EMEL_ERR_UNSUPPORTED_OPERATION, "source view is not element-aligned");
+    if (!gen_aligned(dst)) return fail(EMEL_ERR_UNSUPPORTED_OPERATION, "dst view is not element-aligned");
+    for (int i = 0; i < n_used; ++i)
+        if (!gen_whole(*used[i]))
+            return fail(EMEL_ERR_INVALID_SHAPE, "a source's last element extends past data_bytes");
+    if (!gen_whole(dst)) return fail(EMEL_ERR_INVALID_SHAPE, "dst's last element extends past data_bytes");
+    if (!elements_disjoint(dst, 4))
+        return fail(EMEL_ERR_UNSUPPORTED_OPERATION, "dst elements overlap one another");
+    for (int i = 0; i < n_used; ++i) {
+        const GView &s = *used[i];
+        const auto a = byte_range(dst, 4);
+        const auto b = byte_range(s, elem_bytes(s));
+        const bool disjoint = a.second <= b.first || b.second <= a.first;
+        if (!disjoint && !(alias_ok(route) && same_view(dst, s)))
+            return fail(EMEL_ERR_INVALID_ARGUMENT, "dst overlaps a source");
+    }
+    if (route == Route::MulMatArgmax && q.s0->ne[1] > static_cast<uint64_t>(INT32_MAX))
+        return fail(EMEL_ERR_INVALID_SHAPE, "mul_mat_argmax row index does not fit i32");
+
+    emel_status s = ensure_device();
+    if (s != EMEL_OK) return s;
+    const hipStream_t hs = as_stream(stream);
+    float p0 = 0.0f, p1 = 0.0f;
+    q.param_f32(0, p0);
+    q.param_f32(1, p1);
+
+    switch (route) {
+    case Route::Dup:
+        return elementwise(emel::Ew::Copy, q.s0, pair_addr(*q.s0, dmut), nullptr, emel::Addr::SameCoords, &dmut, 0.0f,
+                           stream);
+    case Route::Binary: {
+        const emel::Ew fn = op == kAdd ? emel::Ew::Add : op == kSub ? emel::Ew::Sub : op == kMul ? emel::Ew::Mul
+                                                                                                 : emel::Ew::Div;
+        return elementwise(fn, q.s0, pair_addr(*q.s0, dmut), q.s1, pair_addr(*q.s1, dmut), &dmut, 0.0f, stream);
+    }
+    case Route::Scalar: {
+        const emel::Ew fn = op == kAdd1 ? emel::Ew::Add1 : op == kScale ? emel::Ew::Scale : emel::Ew::LeakyRelu;
+        return elementwise(fn, q.s0, pair_addr(*q.s0, dmut), nullptr, emel::Addr::SameCoords, &dmut, p0, stream);
+    }
+    case Route::Clamp:
+        return elementwise(emel::Ew::Clamp, q.s0, pair_addr(*q.s0, dmut), nullptr, emel::Addr::SameCoords, &dmut, p0,
+                           stream, p1);
+    case Route::SiluBack:
+        return elementwise(emel::Ew::SiluBack, q.s0, emel::Addr::SameCoords, q.s1, emel::Addr::SameCoords, &dmut,
+                           0.0f, stream);
+    case Route::Power:
+        return elementwise(op == kSqr ? emel::Ew::Sqr : emel::Ew::Sqrt, q.s0, pair_addr(*q.s0, dmut), nullptr,
+                           emel::Addr::SameCoords, &dmut, 0.0f, stream);
+    case Route::Unary:
+        return elementwise(unary_generic_fn(q.r.unary_subop), q.s0, pair_addr(*q.s0, dmut), nullptr,
+                           emel::Addr::SameCoords, &dmut, 0.0f, stream);
+    case Route::Repeat:
+        return elementwise(emel::Ew::Copy, q.s0, emel::Addr::Broadcast, nullptr, emel::Addr::SameCoords, &dmut, 0.0f,
+                           stream);
+    case Route::Reduce: {
+        const emel::RedOp rop = op == kSum ? emel::RedOp::Sum : op == kMean ? emel::RedOp::Mean : emel::RedOp::Argmax;
+        return reduce(rop, *q.s0, dmut, stream);
+    }
+    case Route::Cumsum: case Route::SoftMax: case Route::Norm: case Route::SoftMaxBack: case Route::RmsNormBack: {
+        emel::GenRowArgs a{};
+        a.x = gview(*q.s0);
+        a.y = gview(dst);
+        const uint64_t count = gen_count(q.s0);
+        a.width = q.s0->ne[0];
+        if (route == Route::Cumsum) a.op = emel::GenRow::Cumsum;
+        else if (route == Route::SoftMax) a.op = emel::GenRow::SoftMax;
+        else if (route == Route::Norm) a.op = op == kNorm ? emel::GenRow::Norm : emel::GenRow::RmsNorm;
+        else if (route == Route::SoftMaxBack) a.op = emel::GenRow::SoftMaxBack;
+        else a.op = emel::GenRow::RmsNormBack;
+        if (route == Route::SoftMaxBack) {
+            int32_t row = 1;
+            q.param_i32(0, row);
+            a.width = static_cast<uint64_t>(row);
+        }
+        if (route == Route::SoftMaxBack || route == Route::RmsNormBack) a.g = gview(*q.s1);
+        a.eps = p0;
+        a.rows = count / a.width;
+        return launched(emel::launch_generic_rows(a, hs));
+    }
+    case Route::RepeatBack: case Route::Concat: case Route::Diag: case Route::DiagMask: case Route::Fill:
+    case Route::Arange: {
+        emel::GenOrdArgs a{};
+        a.y = gview(dst);
+        if (q.s0) a.a = gview(*q.s0);
+        if (route == Route::Concat) a.b = gview(*q.s1);
+        a.p0 = p0;
+        a.p1 = p1;
+        a.axis = static_cast<uint32_t>(concat_axis);
+        int32_t n_past = 0;
+        if (route == Route::DiagMask) q.param_i32(0, n_past);
+        a.n_past = static_cast<uint64_t>(n_past);
+        switch (route) {
+        case Route::RepeatBack: a.op = emel::GenOrd::RepeatBack; break;
+        case Route::Concat: a.op = emel::GenOrd::Concat; break;
+        case Route::Diag: a.op = emel::GenOrd::Diag; break;
+        case Route::DiagMask: a.op = op == kDiagMaskInf ? emel::GenOrd::DiagMaskInf : emel::GenOrd::DiagMaskZero; break;
+        case Route::Fill: a.op = emel::GenOrd::Fill; break;
+        default: a.op = emel::GenOrd::Arange; break;
+        }
+        return launched(emel::launch_generic_ordinal(a, hs));
+    }
+    case Route::L2Norm: {
+        void *ws = nullptr;
+        s = workspace_for(hs, emel::generic_workspace_bytes(emel::GenWork::L2Norm), &ws);
+        if (s != EMEL_OK) return s;
+        return launched(emel::launch_generic_l2_norm(gview(*q.s0), gview(dst), ws, hs));
+    }
+    case Route::CountEqual: {
+        void *ws = nullptr;
+        s = workspace_for(hs, emel::generic_workspace_bytes(emel::GenWork::CountEqual), &ws);
+        if (s != EMEL_OK) return s;
+        return launched(emel::launch_generic_count_equal(gview(*q.s0), gview(*q.s1), static_cast<float *>(dmut.data),
+                                                         ws, hs));
+    }
+    case Route::MulMatF32: case Route::MulMatF16: case Route::MulMatArgmax: {
+        emel::GenMatArgs a{};
+        a.lhs = gview(*q.s0);
+        a.rhs = gview(*q.s1);
+        a.y = gview(dst);
+        a.k = q.s0->ne[0];
+        a.m = q.s0->ne[1];
+        a.n = route == Route::MulMatF32 ? q.s1->ne[0] : q.s1->ne[1];
+        a.f16 = route == Route::MulMatF16;
+        a.argmax = route == Route::MulMatArgmax;
+        a.index_out = q.r.index_out;
+        if (a.argmax) {
+            s = workspace_for(hs, emel::generic_workspace_bytes(emel::GenWork::MulMatArgmax), &a.workspace);
+            if (s != EMEL_OK) return s;
+        }
+        return launched(emel::launch_generic_mul_mat(a, hs));
+    }
+    default:
+        return fail(EMEL_ERR_INTERNAL, "unrouted generic request");
+    }
+}
+
+} // namespace
+
+emel_status emel_generic_dispatch(const emel_generic_request *request, emel_stream stream)
+{
+    if (!request) return fail(EMEL_ERR_INVALID_ARGUMENT, "null request");
+    const emel_generic_request &r = *request;
+    // Values no Rust GenericRequest can hold.
+    if (r.operation >= kGenericOps) return fail(EMEL_ERR_INVALID_ARGUMENT, "operation code outside 0..94");
+    if (r.unary_subop > 21 || r.glu_subop > 5 || r.pool_subop > 1)
+        return fail(EMEL_ERR_INVALID_ARGUMENT, "subop code outside its wire range");
+    if (r.op_params_size > 64 || r.reserved != 0) return fail(EMEL_ERR_INVALID_ARGUMENT, "op_params_size > 64");
+    for (const emel_tensor_view *v : {r.src0, r.src1, r.src2, reinterpret_cast<const emel_tensor_view *>(r.dst)})
+        if (v && (v->dtype > 255 || v->reserved != 0))
+            return fail(EMEL_ERR_INVALID_ARGUMENT, "view dtype outside the wire range");
+    const GenReq q(r);
+    int concat_axis = 0;
+    const Route route = gen_route(q, concat_axis);
+    if (route != Route::None) return gen_execute(q, route, concat_axis, stream);
+    const bool valid = gen_request_valid(q);
+    if (valid && gen_maintained(r.operation))
+        return fail(EMEL_ERR_INVALID_SHAPE, "the operation's maintained route rejects the request");
+    if (valid) return fail(EMEL_ERR_UNSUPPORTED_OPERATION, "no maintained route for this operation");
+    return fail(EMEL_ERR_INVALID_SHAPE, "the request failed validation");
+}

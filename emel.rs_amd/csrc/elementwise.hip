@@ -106,9 +106,10 @@ template <Ew OP> struct Fn;
     template <> struct Fn<Ew::OPV> {                                                                \
         static constexpr bool kTable = TABLE;                                                       \
         static constexpr bool kBinary = BINARY;                                                     \
-        __device__ __forceinline__ static float apply(float a, float b, float s, const ExpCtx &t) \
+        __device__ __forceinline__ static float apply(float a, float b, Scal sc, const ExpCtx &t)  \
         {                                                                                           \
-            (void)b; (void)s; (void)t;                                                              \
+            const float s = sc.x, s2 = sc.y;                                                        \
+            (void)b; (void)s; (void)s2; (void)t;                                                    \
             return EXPR;                                                                            \
         }                                                                                           \
     };
@@ -154,10 +155,26 @@ EMEL_FN(GluSwiOai, true, true,
         emel_silu(1.702f * __builtin_fminf(b, 7.0f), t.tab, t.c) / 1.702f * (__builtin_fminf(a, 7.0f) + 1.0f))
 EMEL_FN(GluGeErf, true, true, a * glu_gelu_erf(b, t))
 EMEL_FN(GluGeQuick, true, true, a * (b * (1.0f / (1.0f + emel_expf(-1.702f * b, t.tab, t.c)))))
+// Generic-envelope formulas (generic.rs:1307-1350, :1522-1583).
+EMEL_FN(Add1, false, false, a + s)
+EMEL_FN(LeakyRelu, false, false, a < 0.0f ? a * s : a)
+// f32::clamp: below min -> min, then above max -> max; NaN passes through.
+EMEL_FN(Clamp, false, false, (a < s ? s : a) > s2 ? s2 : (a < s ? s : a))
+// The generic GELU: no fp16 rounding and no saturation, one fused
+// multiply-add inside the tanh argument.
+EMEL_FN(GeluGeneric, false, false,
+        0.5f * a * (1.0f + emel_tanhf(0.7978846f * __builtin_fmaf(0.044715f * a * a, a, a))))
+// a = input, b = incoming gradient.
+__device__ __forceinline__ float silu_back(float x, float grad, const ExpCtx &t)
+{
+    const float sg = 1.0f / (1.0f + emel_expf(-x, t.tab, t.c));
+    return grad * (sg * (1.0f + x * (1.0f - sg)));
+}
+EMEL_FN(SiluBack, true, true, silu_back(a, b, t))
 #undef EMEL_FN
 
 template <Ew OP>
-__device__ __forceinline__ float4 apply4(float4 a, float4 b, float s, const ExpCtx &t)
+__device__ __forceinline__ float4 apply4(float4 a, float4 b, Scal s, const ExpCtx &t)
 {
     float4 r;
     r.x = Fn<OP>::apply(a.x, b.x, s, t);
@@ -194,7 +211,7 @@ struct Stream {
 
 template <Ew OP, int VPT>
 __global__ __launch_bounds__(kBlock) void k_dense(const float *a, const float *b, float *o, uint64_t nvec,
-                                                   uint64_t n, float s)
+                                                   uint64_t n, Scal s)
 {
     __shared__ uint64_t lds[32];
     const ExpCtx tab = stage_table<OP>(lds);
@@ -278,7 +295,7 @@ __global__ __launch_bounds__(kGeluBlock) void k_gelu_lds(const float *a, float *
 
 template <Ew OP, int VPT>
 __global__ __launch_bounds__(kBlock) void k_rowbcast(const float *a, const float *b, float *o, uint32_t nvec,
-                                                      FastDiv nv0, float s)
+                                                      FastDiv nv0, Scal s)
 {
     __shared__ uint64_t lds[32];
     const ExpCtx tab = stage_table<OP>(lds);
@@ -324,7 +341,7 @@ __device__ __forceinline__ int64_t rows_offset(const int64_t *st, const FastDiv 
 }
 
 template <Ew OP>
-__global__ __launch_bounds__(kBlock) void k_rows(RowsGeo g, const float *a, const float *b, float *o, float s)
+__global__ __launch_bounds__(kBlock) void k_rows(RowsGeo g, const float *a, const float *b, float *o, Scal s)
 {
     __shared__ uint64_t lds[32];
     const ExpCtx tab = stage_table<OP>(lds);
@@ -389,7 +406,7 @@ __device__ __forceinline__ int64_t ord_offset(const OrdOperand &p, uint64_t k, c
 }
 
 template <Ew OP>
-__global__ __launch_bounds__(kBlock) void k_ordinal(OrdGeo g, const float *a, const float *b, float *o, float s)
+__global__ __launch_bounds__(kBlock) void k_ordinal(OrdGeo g, const float *a, const float *b, float *o, Scal s)
 {
     __shared__ uint64_t lds[32];
     const ExpCtx tab = stage_table<OP>(lds);
@@ -476,7 +493,7 @@ hipError_t launch_op(const EwArgs &x, hipStream_t stream)
         if (blocks < tail_blocks) blocks = tail_blocks;
         if (blocks > 0x7fffffffull) return hipErrorInvalidConfiguration;
         const dim3 grid(static_cast<uint32_t>(blocks));
-        k_dense<OP, vpt><<<grid, kBlock, 0, stream>>>(a, b, o, nvec, n, x.scale);
+        k_dense<OP, vpt><<<grid, kBlock, 0, stream>>>(a, b, o, nvec, n, Scal{x.scale, x.scale2});
         return hipGetLastError();
     }
 
@@ -492,7 +509,7 @@ hipError_t launch_op(const EwArgs &x, hipStream_t stream)
         const uint32_t per_block = kBlock * vpt;
         const dim3 grid((nvec + per_block - 1) / per_block);
         const FastDiv nv0(static_cast<uint32_t>(ne0 / 4));
-        k_rowbcast<OP, vpt><<<grid, kBlock, 0, stream>>>(a, b, o, nvec, nv0, x.scale);
+        k_rowbcast<OP, vpt><<<grid, kBlock, 0, stream>>>(a, b, o, nvec, nv0, Scal{x.scale, x.scale2});
         return hipGetLastError();
     }
 
@@ -538,7 +555,7 @@ hipError_t launch_op(const EwArgs &x, hipStream_t stream)
         g.b_modmask = bm;
         g.b_splat = b_splat ? 1u : 0u;
         const dim3 grid((g.nvec + kBlock - 1) / kBlock);
-        k_rows<OP><<<grid, kBlock, 0, stream>>>(g, a, b, o, x.scale);
+        k_rows<OP><<<grid, kBlock, 0, stream>>>(g, a, b, o, Scal{x.scale, x.scale2});
         return hipGetLastError();
     }
 
@@ -556,7 +573,7 @@ hipError_t launch_op(const EwArgs &x, hipStream_t stream)
     g.b.addr = static_cast<uint32_t>(kBin ? x.b_addr : Addr::SameCoords);
     uint64_t blocks = (n + kBlock - 1) / kBlock;
     if (blocks > 65536) blocks = 65536;
-    k_ordinal<OP><<<dim3(static_cast<uint32_t>(blocks)), kBlock, 0, stream>>>(g, a, b, o, x.scale);
+    k_ordinal<OP><<<dim3(static_cast<uint32_t>(blocks)), kBlock, 0, stream>>>(g, a, b, o, Scal{x.scale, x.scale2});
     return hipGetLastError();
 }
 
@@ -589,6 +606,11 @@ hipError_t launch_elementwise(const EwArgs &args, hipStream_t stream)
     case Ew::GluSwiOai: return launch_op<Ew::GluSwiOai>(args, stream);
     case Ew::GluGeErf: return launch_op<Ew::GluGeErf>(args, stream);
     case Ew::GluGeQuick: return launch_op<Ew::GluGeQuick>(args, stream);
+    case Ew::Add1: return launch_op<Ew::Add1>(args, stream);
+    case Ew::LeakyRelu: return launch_op<Ew::LeakyRelu>(args, stream);
+    case Ew::Clamp: return launch_op<Ew::Clamp>(args, stream);
+    case Ew::GeluGeneric: return launch_op<Ew::GeluGeneric>(args, stream);
+    case Ew::SiluBack: return launch_op<Ew::SiluBack>(args, stream);
     }
     return hipErrorInvalidValue;
 }

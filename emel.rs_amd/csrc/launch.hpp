@@ -25,7 +25,15 @@ enum class Ew : uint32_t {
     Abs, Neg, Tanh, Elu, Relu, Sigmoid, Gelu, Silu, Exp, Scale,   // unary
     Swiglu,                                                        // fused
     GluRe, GluGe, GluSwi, GluSwiOai, GluGeErf, GluGeQuick,        // OpGlu: a = values, b = gates
-    Copy, Sqr, Sqrt                                                // dup and power.rs
+    Copy, Sqr, Sqrt,                                               // dup and power.rs
+    Add1, LeakyRelu, Clamp, GeluGeneric, SiluBack                  // generic envelope (generic.rs)
+};
+
+// The scalar parameters an elementwise functor reads: x is Scale's factor,
+// Add1's addend and LeakyRelu's slope; Clamp reads [x, y] as [min, max].
+struct Scal {
+    float x;
+    float y;
 };
 
 // How a source operand is addressed from the destination ordinal.
@@ -37,7 +45,8 @@ enum class Addr : uint32_t {
 
 struct EwArgs {
     Ew op;
-    float scale; // Ew::Scale
+    float scale;  // Scal::x
+    float scale2; // Scal::y (Ew::Clamp's maximum)
     Operand a;
     Operand b; // unused by unary ops
     Operand o;
@@ -83,5 +92,62 @@ struct RedArgs {
 // every row is reduced by a single workgroup).
 uint64_t reduce_workspace_bytes(const RedArgs &args);
 hipError_t launch_reduce(const RedArgs &args, hipStream_t stream);
+
+// ---- generic-envelope routes (generic.hip) ---------------------------------
+
+// An operand addressed by logical ordinal through its own extents.
+struct GView {
+    void *data;
+    uint64_t ne[4];
+    int64_t st[4]; // element strides
+};
+
+enum class GenRow : uint32_t { Cumsum = 0, SoftMax, Norm, RmsNorm, SoftMaxBack, RmsNormBack };
+
+// Rows are `width` consecutive ordinals of every operand.
+struct GenRowArgs {
+    GenRow op;
+    GView x; // src0
+    GView g; // src1 (SoftMaxBack, RmsNormBack)
+    GView y; // dst
+    uint64_t rows;
+    uint64_t width;
+    float eps;
+};
+
+hipError_t launch_generic_rows(const GenRowArgs &args, hipStream_t stream);
+
+enum class GenOrd : uint32_t { Fill = 0, Arange, Diag, DiagMaskInf, DiagMaskZero, Concat, RepeatBack };
+
+// One destination element per lane, addressed by destination coordinates.
+struct GenOrdArgs {
+    GenOrd op;
+    GView a; // src0
+    GView b; // src1 (Concat)
+    GView y; // dst
+    float p0, p1;    // Fill value; Arange start and step
+    uint64_t n_past; // DiagMask*
+    uint32_t axis;   // Concat
+};
+
+hipError_t launch_generic_ordinal(const GenOrdArgs &args, hipStream_t stream);
+
+enum class GenWork : uint32_t { L2Norm = 0, CountEqual, MulMatArgmax };
+uint64_t generic_workspace_bytes(GenWork which);
+
+hipError_t launch_generic_l2_norm(const GView &x, const GView &y, void *workspace, hipStream_t stream);
+hipError_t launch_generic_count_equal(const GView &a, const GView &b, float *dst, void *workspace,
+                                      hipStream_t stream);
+
+struct GenMatArgs {
+    GView lhs, rhs, y;
+    uint64_t k, m, n; // argmax: m = rows of lhs
+    bool f16;         // dense F16 operands (strides in halves)
+    bool argmax;
+    int32_t *index_out;
+    void *workspace;
+};
+
+hipError_t launch_generic_mul_mat(const GenMatArgs &args, hipStream_t stream);
 
 } // namespace emel

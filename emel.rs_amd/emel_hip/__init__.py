@@ -2,7 +2,8 @@
 path -- elementwise, broadcast and row-reduction ops -- behind the C ABI in
 include/emel_hip.h, with a Python mirror of emel-kernels' operator API.
 """
-from .abi import BinaryOp, DType, GluSubOp, Status, UnarySubOp, device_count, last_error, load
+from .abi import BinaryOp, DType, GenericOp, GluSubOp, Status, UnarySubOp, device_count, last_error, load
+from .generic import GenericEvent, GenericRequest, OpParams
 from .kernel import (
     DenseOpAdd,
     DenseOpDiv,
@@ -41,7 +42,7 @@ from .kernel import (
 from .views import Layout, TensorView, TensorViewMut
 
 __all__ = [
-    "BinaryOp", "DType", "GluSubOp", "Status", "UnarySubOp", "device_count", "last_error", "load",
+    "BinaryOp", "DType", "GenericOp", "GenericEvent", "GenericRequest", "OpParams", "GluSubOp", "Status", "UnarySubOp", "device_count", "last_error", "load",
     "Kernel", "Layout", "TensorView", "TensorViewMut",
     "OpAdd", "OpSub", "OpMul", "OpDiv", "OpAddBroadcastRow", "OpMulBroadcastRow", "OpBinaryBroadcast",
     "OpUnary", "OpSilu", "OpGelu", "OpGlu", "OpSwiglu", "OpScale", "OpRmsNorm", "OpRmsNormMul", "OpNorm",

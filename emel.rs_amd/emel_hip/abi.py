@@ -53,6 +53,14 @@ class UnarySubOp(enum.IntEnum):
     HARDSWISH = 11
     HARDSIGMOID = 12
     EXP = 13
+    EXPM1 = 14
+    SOFTPLUS = 15
+    GELU_ERF = 16
+    XIELU = 17
+    FLOOR = 18
+    CEIL = 19
+    ROUND = 20
+    TRUNC = 21
 
 
 class GluSubOp(enum.IntEnum):
@@ -64,6 +72,110 @@ class GluSubOp(enum.IntEnum):
     SWIGLU_OAI = 3
     GEGLU_ERF = 4
     GEGLU_QUICK = 5
+
+
+class GenericOp(enum.IntEnum):
+    """KernelOperation wire codes (generic.rs:24-337): the 95 entries of the
+    pinned EMEL_KERNEL_OP_EVENT_LIST, in order."""
+
+    DUP = 0
+    ADD = 1
+    ADD_ID = 2
+    ADD1 = 3
+    ACC = 4
+    SUB = 5
+    MUL = 6
+    DIV = 7
+    SQR = 8
+    SQRT = 9
+    LOG = 10
+    SIN = 11
+    COS = 12
+    SUM = 13
+    SUM_ROWS = 14
+    CUMSUM = 15
+    MEAN = 16
+    ARGMAX = 17
+    COUNT_EQUAL = 18
+    REPEAT = 19
+    REPEAT_BACK = 20
+    CONCAT = 21
+    SILU_BACK = 22
+    NORM = 23
+    RMS_NORM = 24
+    RMS_NORM_BACK = 25
+    GROUP_NORM = 26
+    L2_NORM = 27
+    MUL_MAT = 28
+    MUL_MAT_ARGMAX = 29
+    MUL_MAT_ID = 30
+    OUT_PROD = 31
+    SCALE = 32
+    SET = 33
+    CPY = 34
+    CONT = 35
+    RESHAPE = 36
+    VIEW = 37
+    PERMUTE = 38
+    TRANSPOSE = 39
+    GET_ROWS = 40
+    GET_ROWS_BACK = 41
+    SET_ROWS = 42
+    DIAG = 43
+    DIAG_MASK_INF = 44
+    DIAG_MASK_ZERO = 45
+    SOFT_MAX = 46
+    SOFT_MAX_BACK = 47
+    ROPE = 48
+    ROPE_BACK = 49
+    CLAMP = 50
+    CONV_TRANSPOSE_1D = 51
+    IM2COL = 52
+    IM2COL_BACK = 53
+    IM2COL_3D = 54
+    CONV_2D = 55
+    CONV_3D = 56
+    CONV_2D_DW = 57
+    CONV_TRANSPOSE_2D = 58
+    POOL_1D = 59
+    POOL_2D = 60
+    POOL_2D_BACK = 61
+    UPSCALE = 62
+    PAD = 63
+    PAD_REFLECT_1D = 64
+    ROLL = 65
+    ARANGE = 66
+    TIMESTEP_EMBEDDING = 67
+    ARGSORT = 68
+    TOP_K = 69
+    LEAKY_RELU = 70
+    TRI = 71
+    FILL = 72
+    FLASH_ATTN_EXT = 73
+    FLASH_ATTN_BACK = 74
+    SSM_CONV = 75
+    SSM_SCAN = 76
+    WIN_PART = 77
+    WIN_UNPART = 78
+    GET_REL_POS = 79
+    ADD_REL_POS = 80
+    RWKV_WKV6 = 81
+    GATED_LINEAR_ATTN = 82
+    RWKV_WKV7 = 83
+    SOLVE_TRI = 84
+    UNARY = 85
+    MAP_CUSTOM1 = 86
+    MAP_CUSTOM2 = 87
+    MAP_CUSTOM3 = 88
+    CUSTOM = 89
+    CROSS_ENTROPY_LOSS = 90
+    CROSS_ENTROPY_LOSS_BACK = 91
+    OPT_STEP_ADAMW = 92
+    OPT_STEP_SGD = 93
+    GLU = 94
+
+
+GENERIC_OPERATION_COUNT = 95
 
 
 class BinaryOp(enum.IntEnum):
@@ -83,6 +195,25 @@ class CView(ctypes.Structure):
         ("reserved", ctypes.c_uint32),
         ("ne", ctypes.c_uint64 * 4),
         ("nb", ctypes.c_uint64 * 4),
+    ]
+
+
+class CGenericRequest(ctypes.Structure):
+    """emel_generic_request: the pinned generic operation struct."""
+
+    _fields_ = [
+        ("operation", ctypes.c_uint32),
+        ("unary_subop", ctypes.c_uint32),
+        ("glu_subop", ctypes.c_uint32),
+        ("pool_subop", ctypes.c_uint32),
+        ("src0", ctypes.POINTER(CView)),
+        ("src1", ctypes.POINTER(CView)),
+        ("src2", ctypes.POINTER(CView)),
+        ("dst", ctypes.POINTER(CView)),
+        ("op_params", ctypes.c_uint8 * 64),
+        ("op_params_size", ctypes.c_uint32),
+        ("reserved", ctypes.c_uint32),
+        ("index_out", ctypes.c_void_p),
     ]
 
 
@@ -134,6 +265,7 @@ SIGNATURES = {
     "emel_stream_destroy": [_S],
     "emel_stream_synchronize": [_S],
     "emel_release_workspaces": [],
+    "emel_generic_dispatch": [ctypes.POINTER(CGenericRequest), _S],
 }
 
 _lib = None

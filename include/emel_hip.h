@@ -284,6 +284,90 @@ emel_status emel_op_argmax(const emel_tensor_view *src, const emel_tensor_view_m
 emel_status emel_op_argmax_rows(const emel_tensor_view *src, const emel_tensor_view_mut *dst,
                                 emel_stream stream);
 
+/* ---- generic wire envelope ----------------------------------------------------
+ * event::GenericEvent::new(GenericRequest::new(operation, src0, src1, src2,
+ * dst, OpParams).with_unary(..).with_index_out(..)) (generic.rs:634-797):
+ * the pinned emel.cpp operation struct, one entry point for every opcode.
+ *
+ * Operation codes: KernelOperation (generic.rs:24-337), 95 entries. */
+typedef enum emel_generic_op {
+    EMEL_GENERIC_DUP = 0, EMEL_GENERIC_ADD, EMEL_GENERIC_ADD_ID, EMEL_GENERIC_ADD1, EMEL_GENERIC_ACC,
+    EMEL_GENERIC_SUB, EMEL_GENERIC_MUL, EMEL_GENERIC_DIV, EMEL_GENERIC_SQR, EMEL_GENERIC_SQRT,
+    EMEL_GENERIC_LOG, EMEL_GENERIC_SIN, EMEL_GENERIC_COS, EMEL_GENERIC_SUM, EMEL_GENERIC_SUM_ROWS,
+    EMEL_GENERIC_CUMSUM, EMEL_GENERIC_MEAN, EMEL_GENERIC_ARGMAX, EMEL_GENERIC_COUNT_EQUAL, EMEL_GENERIC_REPEAT,
+    EMEL_GENERIC_REPEAT_BACK, EMEL_GENERIC_CONCAT, EMEL_GENERIC_SILU_BACK, EMEL_GENERIC_NORM,
+    EMEL_GENERIC_RMS_NORM, EMEL_GENERIC_RMS_NORM_BACK, EMEL_GENERIC_GROUP_NORM, EMEL_GENERIC_L2_NORM,
+    EMEL_GENERIC_MUL_MAT, EMEL_GENERIC_MUL_MAT_ARGMAX, EMEL_GENERIC_MUL_MAT_ID, EMEL_GENERIC_OUT_PROD,
+    EMEL_GENERIC_SCALE, EMEL_GENERIC_SET, EMEL_GENERIC_CPY, EMEL_GENERIC_CONT, EMEL_GENERIC_RESHAPE,
+    EMEL_GENERIC_VIEW, EMEL_GENERIC_PERMUTE, EMEL_GENERIC_TRANSPOSE, EMEL_GENERIC_GET_ROWS,
+    EMEL_GENERIC_GET_ROWS_BACK, EMEL_GENERIC_SET_ROWS, EMEL_GENERIC_DIAG, EMEL_GENERIC_DIAG_MASK_INF,
+    EMEL_GENERIC_DIAG_MASK_ZERO, EMEL_GENERIC_SOFT_MAX, EMEL_GENERIC_SOFT_MAX_BACK, EMEL_GENERIC_ROPE,
+    EMEL_GENERIC_ROPE_BACK, EMEL_GENERIC_CLAMP, EMEL_GENERIC_CONV_TRANSPOSE_1D, EMEL_GENERIC_IM2COL,
+    EMEL_GENERIC_IM2COL_BACK, EMEL_GENERIC_IM2COL_3D, EMEL_GENERIC_CONV_2D, EMEL_GENERIC_CONV_3D,
+    EMEL_GENERIC_CONV_2D_DW, EMEL_GENERIC_CONV_TRANSPOSE_2D, EMEL_GENERIC_POOL_1D, EMEL_GENERIC_POOL_2D,
+    EMEL_GENERIC_POOL_2D_BACK, EMEL_GENERIC_UPSCALE, EMEL_GENERIC_PAD, EMEL_GENERIC_PAD_REFLECT_1D,
+    EMEL_GENERIC_ROLL, EMEL_GENERIC_ARANGE, EMEL_GENERIC_TIMESTEP_EMBEDDING, EMEL_GENERIC_ARGSORT,
+    EMEL_GENERIC_TOP_K, EMEL_GENERIC_LEAKY_RELU, EMEL_GENERIC_TRI, EMEL_GENERIC_FILL,
+    EMEL_GENERIC_FLASH_ATTN_EXT, EMEL_GENERIC_FLASH_ATTN_BACK, EMEL_GENERIC_SSM_CONV, EMEL_GENERIC_SSM_SCAN,
+    EMEL_GENERIC_WIN_PART, EMEL_GENERIC_WIN_UNPART, EMEL_GENERIC_GET_REL_POS, EMEL_GENERIC_ADD_REL_POS,
+    EMEL_GENERIC_RWKV_WKV6, EMEL_GENERIC_GATED_LINEAR_ATTN, EMEL_GENERIC_RWKV_WKV7, EMEL_GENERIC_SOLVE_TRI,
+    EMEL_GENERIC_UNARY, EMEL_GENERIC_MAP_CUSTOM1, EMEL_GENERIC_MAP_CUSTOM2, EMEL_GENERIC_MAP_CUSTOM3,
+    EMEL_GENERIC_CUSTOM, EMEL_GENERIC_CROSS_ENTROPY_LOSS, EMEL_GENERIC_CROSS_ENTROPY_LOSS_BACK,
+    EMEL_GENERIC_OPT_STEP_ADAMW, EMEL_GENERIC_OPT_STEP_SGD, EMEL_GENERIC_GLU,
+    EMEL_GENERIC_OPERATION_COUNT /* 95, GENERIC_OPERATION_COUNT (generic.rs:19) */
+} emel_generic_op;
+
+/* The pinned operation struct (tools/emel-kernel-*-reference/main.cpp:
+ * tensor_view src0/src1/src2/dst, op_params[64] + op_params_size, subop,
+ * index_out).  Absent views are NULL.  Views of any wire dtype (0..255) are
+ * accepted for validation; data pointers are device pointers, and so is
+ * index_out (op_mul_mat_argmax's row, written on the device). */
+typedef struct emel_generic_request {
+    uint32_t operation;   /* emel_generic_op */
+    uint32_t unary_subop; /* UnarySubOp wire code, read by EMEL_GENERIC_UNARY (0..21) */
+    uint32_t glu_subop;   /* GluSubOp wire code (carried; no maintained route reads it) */
+    uint32_t pool_subop;  /* PoolSubOp wire code (carried; no maintained route reads it) */
+    const emel_tensor_view *src0;
+    const emel_tensor_view *src1;
+    const emel_tensor_view *src2;
+    const emel_tensor_view_mut *dst;
+    uint8_t op_params[64];
+    uint32_t op_params_size; /* initialised prefix of op_params, <= 64 */
+    uint32_t reserved;       /* must be 0 */
+    int32_t *index_out;      /* NULL when absent */
+} emel_generic_request;
+
+/* Dispatch in the reference machine's order (sm.rs:318-426, guards
+ * actor.rs:2655-2983):
+ *   1. the operation's maintained F32 route (generic.rs:848-1262) passes ->
+ *      executed on the device (formulas generic.rs:1264-2055);
+ *   2. else the request validates (GenericRequest::validate, :769-789) but a
+ *      maintained operation's predicate fails -> EMEL_ERR_INVALID_SHAPE;
+ *   3. else the request validates -> EMEL_ERR_UNSUPPORTED_OPERATION;
+ *   4. else EMEL_ERR_INVALID_SHAPE.
+ * Routed on the device: dup, add, sub, mul, div, add1, scale, clamp,
+ * leaky_relu, silu_back, cumsum, repeat, repeat_back, concat, diag,
+ * diag_mask_inf/zero, soft_max, soft_max_back, norm, rms_norm, rms_norm_back,
+ * l2_norm, count_equal, fill, arange, sum, mean, argmax, sqr, sqrt, unary
+ * (abs, neg, tanh, elu, relu, gelu, silu, exp), mul_mat (F32 and F16) and
+ * mul_mat_argmax.  Divergences, each reported before anything is enqueued:
+ *   - log / sin / cos pass their route in the reference but return
+ *     EMEL_ERR_UNSUPPORTED_OPERATION (no bit-exact glibc logf/sinf/cosf);
+ *   - views the reference reads byte-wise but that are not element-aligned
+ *     (an F32 data pointer or stride not a multiple of 4), and destinations
+ *     whose elements may overlap one another, are
+ *     EMEL_ERR_UNSUPPORTED_OPERATION;
+ *   - a routed request whose last element extends past data_bytes (the
+ *     reference checks one byte and then panics reading four) is
+ *     EMEL_ERR_INVALID_SHAPE;
+ *   - dst overlapping a source (impossible for Rust's borrowed slices) is
+ *     EMEL_ERR_INVALID_ARGUMENT, except dst being exactly a source view for
+ *     the per-element and per-row routes.
+ * A NULL request, an operation code >= 95, a subop or dtype code outside its
+ * wire range, op_params_size > 64 or reserved != 0 (none representable in
+ * the reference's types) is EMEL_ERR_INVALID_ARGUMENT. */
+emel_status emel_generic_dispatch(const emel_generic_request *request, emel_stream stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -38,7 +38,10 @@ enum {
     ORC_SHAPE_MISMATCH = 2,
     ORC_INVALID_PARAMETERS = 3,
     ORC_UNEXPECTED_EVENT = 4,
-    ORC_INVALID_SHAPE = 9, /* root Error::InvalidShape */
+    ORC_INVALID_ARGUMENT = 8,        /* a value no reference type can hold */
+    ORC_INVALID_SHAPE = 9,           /* root Error::InvalidShape */
+    ORC_UNSUPPORTED_OPERATION = 10,  /* root Error::UnsupportedOperation */
+    ORC_PANIC = 99,                  /* the reference's guard passes and its executor panics */
 };
 
 enum { ORC_ADD = 0, ORC_SUB = 1, ORC_MUL = 2, ORC_DIV = 3 };
@@ -83,6 +86,27 @@ int orc_op_power(int sqrt_, const orc_view *in, const orc_view *out);
 enum { ORC_REGLU = 0, ORC_GEGLU = 1, ORC_SWIGLU = 2, ORC_SWIGLU_OAI = 3, ORC_GEGLU_ERF = 4, ORC_GEGLU_QUICK = 5 };
 int orc_op_glu(int subop, const float *input, uint64_t input_len, float *output, uint64_t output_len);
 float orc_glu_gate(int subop, float gate); /* the gate function alone (not SwiGluOai) */
+
+/* The generic wire envelope (generic.rs, sm.rs:318-426), in
+ * emel_oracle_generic.c.  Same layout as emel_generic_request in
+ * include/emel_hip.h, with host pointers.  Returns ORC_OK, ORC_INVALID_SHAPE,
+ * ORC_UNSUPPORTED_OPERATION or ORC_PANIC (a passed guard whose executor
+ * reads or writes a partial last element). */
+typedef struct orc_generic_request {
+    uint32_t operation;
+    uint32_t unary_subop;
+    uint32_t glu_subop;
+    uint32_t pool_subop;
+    const orc_view *src0;
+    const orc_view *src1;
+    const orc_view *src2;
+    const orc_view *dst;
+    uint8_t op_params[64];
+    uint32_t op_params_size;
+    uint32_t reserved;
+    int32_t *index_out;
+} orc_generic_request;
+int orc_generic(const orc_generic_request *request);
 
 /* Scalar helpers (unary.rs:522-600, quant.rs:287-300). */
 float orc_silu(float x);

@@ -184,3 +184,53 @@ def silu_scalar(x: float) -> float: return float(lib().orc_silu(x))
 def gelu_scalar(x: float) -> float: return float(lib().orc_gelu(x))
 def fp32_to_fp16(x: float) -> int: return int(lib().orc_fp32_to_fp16(x))
 def fp16_to_f32(h: int) -> float: return float(lib().orc_fp16_to_f32(h))
+
+
+# generic wire envelope --------------------------------------------------------
+
+UNSUPPORTED_OPERATION, INVALID_ARGUMENT, PANIC = 10, 8, 99
+
+
+class OGenericRequest(ctypes.Structure):
+    """orc_generic_request (the emel_generic_request layout, host pointers)."""
+
+    _fields_ = [
+        ("operation", ctypes.c_uint32),
+        ("unary_subop", ctypes.c_uint32),
+        ("glu_subop", ctypes.c_uint32),
+        ("pool_subop", ctypes.c_uint32),
+        ("src0", ctypes.POINTER(OView)),
+        ("src1", ctypes.POINTER(OView)),
+        ("src2", ctypes.POINTER(OView)),
+        ("dst", ctypes.POINTER(OView)),
+        ("op_params", ctypes.c_uint8 * 64),
+        ("op_params_size", ctypes.c_uint32),
+        ("reserved", ctypes.c_uint32),
+        ("index_out", ctypes.c_void_p),
+    ]
+
+
+def generic(operation: int, src0=None, src1=None, src2=None, dst=None, params: bytes = b"",
+            params_size: int | None = None, unary: int = 0, index_out: np.ndarray | None = None) -> int:
+    """orc_generic over OView arguments; params are the op_params bytes
+    (params_size defaults to their length); index_out is a 1-element int32
+    host array or None."""
+    r = OGenericRequest()
+    r.operation = int(operation)
+    r.unary_subop = int(unary)
+    r.glu_subop = 0
+    r.pool_subop = 1
+    for name, v in (("src0", src0), ("src1", src1), ("src2", src2), ("dst", dst)):
+        if v is not None:
+            setattr(r, name, ctypes.pointer(v))
+    raw = bytes(params).ljust(64, b"\0")
+    ctypes.memmove(r.op_params, raw, 64)
+    r.op_params_size = len(params) if params_size is None else int(params_size)
+    r.reserved = 0
+    if index_out is not None:
+        assert index_out.dtype == np.int32 and index_out.size >= 1
+        r.index_out = index_out.ctypes.data
+    L = lib()
+    L.orc_generic.argtypes = [ctypes.POINTER(OGenericRequest)]
+    L.orc_generic.restype = ctypes.c_int
+    return int(L.orc_generic(ctypes.byref(r)))

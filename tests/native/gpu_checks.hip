@@ -90,6 +90,16 @@ __global__ void k_sqrtf(uint64_t lo, uint64_t hi)
     if (bad) atomicAdd(&g_bad, bad);
 }
 
+// f64 square root and quotient as the generic norms compute them
+// (__builtin_sqrt, operator /); the host compares with IEEE results.
+__global__ void k_f64_ops(const double *x, const double *y, double *sq, double *dv, uint64_t n)
+{
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < n; i += 256ull * gridDim.x) {
+        sq[i] = __builtin_sqrt(x[i]);
+        dv[i] = x[i] / y[i];
+    }
+}
+
 template <class Launch>
 uint64_t run(Launch launch)
 {
@@ -124,6 +134,28 @@ uint64_t gpu_check_expf_nonpos(void)
 uint64_t gpu_check_sqrtf(void)
 {
     return run([] { k_sqrtf<<<8192, 256>>>(0, 1ull << 32); });
+}
+
+// sq[i] = sqrt(x[i]), dv[i] = x[i] / y[i] on the device, n doubles of host
+// memory in and out.  Returns 0, or UINT64_MAX on a HIP error.
+uint64_t gpu_f64_ops(const double *x, const double *y, double *sq, double *dv, uint64_t n)
+{
+    double *d = nullptr;
+    const uint64_t bytes = n * sizeof(double);
+    if (hipMalloc(&d, 4 * bytes) != hipSuccess) return UINT64_MAX;
+    uint64_t rc = 0;
+    if (hipMemcpy(d, x, bytes, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(d + n, y, bytes, hipMemcpyHostToDevice) != hipSuccess) {
+        rc = UINT64_MAX;
+    } else {
+        k_f64_ops<<<1024, 256>>>(d, d + n, d + 2 * n, d + 3 * n, n);
+        if (hipGetLastError() != hipSuccess || hipDeviceSynchronize() != hipSuccess ||
+            hipMemcpy(sq, d + 2 * n, bytes, hipMemcpyDeviceToHost) != hipSuccess ||
+            hipMemcpy(dv, d + 3 * n, bytes, hipMemcpyDeviceToHost) != hipSuccess)
+            rc = UINT64_MAX;
+    }
+    (void)hipFree(d);
+    return rc;
 }
 
 } // extern "C"

@@ -5,10 +5,13 @@ the GPU itself (tests/native/gpu_checks.hip):
   hardware f16 -> f32 widening   == the reference's fp16_to_f32 (all 65536)
   emel_expf_nonpos              == emel_expf for every x <= 0 and NaN
   __builtin_sqrtf               correctly rounded for every input (power.rs)
+  f64 sqrt and division         IEEE results on 2^23 random doubles (the generic
+                                norms' f64 scale), compared with numpy on the host
 """
 import ctypes
 from pathlib import Path
 
+import numpy as np
 import pytest
 
 pytestmark = pytest.mark.gpu
@@ -31,3 +34,24 @@ def checks(gpu):
                                   "gpu_check_sqrtf"])
 def test_exhaustive_on_gpu(checks, name):
     assert getattr(checks, name)() == 0
+
+
+def test_f64_sqrt_and_division_are_ieee(checks):
+    g = np.random.Generator(np.random.PCG64(64))
+    n = 1 << 23
+    x = g.integers(0, 1 << 63, n, dtype=np.uint64).view(np.float64).copy()  # positive, every exponent
+    y = g.integers(0, 1 << 64, n, dtype=np.uint64, endpoint=False).view(np.float64).copy()
+    x[:8] = [0.0, -0.0, np.inf, 1.0, 2.0, 5e-324, 1.7976931348623157e308, 0.25]
+    sq = np.empty_like(x)
+    dv = np.empty_like(x)
+    P = ctypes.POINTER(ctypes.c_double)
+    checks.gpu_f64_ops.restype = ctypes.c_uint64
+    checks.gpu_f64_ops.argtypes = [P, P, P, P, ctypes.c_uint64]
+    assert checks.gpu_f64_ops(x.ctypes.data_as(P), y.ctypes.data_as(P), sq.ctypes.data_as(P),
+                              dv.ctypes.data_as(P), n) == 0
+    with np.errstate(all="ignore"):
+        want_sq = np.sqrt(x)
+        want_dv = x / y
+    for got, want, what in ((sq, want_sq, "sqrt"), (dv, want_dv, "division")):
+        same = (got.view(np.uint64) == want.view(np.uint64)) | (np.isnan(got) & np.isnan(want))
+        assert same.all(), (what, int((~same).sum()), x[~same][:4], got[~same][:4], want[~same][:4])
