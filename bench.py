@@ -20,7 +20,7 @@ step's bytes).  The CPU baseline times the C oracle (a single-threaded
 restatement of the reference's CPU path) on a bounded sample of the same
 workload.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--ops a,b] [--no-cpu] [--no-copy] [--pcie]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--ops a,b] [--no-cpu] [--no-copy] [--pcie] [--no-gather]
 """
 from __future__ import annotations
 
@@ -298,6 +298,74 @@ def pcie_inclusive(suite, host, stream, reps=5):
             "note": "inputs copied in from and the output copied out to pinned host memory around each launch"}
 
 
+GATHER_VOCAB, GATHER_DIM, GATHER_TOKENS = 32000, 4096, 512
+# format -> (dtype code, bytes per source row, event class name)
+GATHER_FORMATS = {
+    "f32": (0, GATHER_DIM * 4, "OpGetRows"),
+    "f16": (1, GATHER_DIM * 2, "OpGetRowsF16"),
+    "bf16": (30, GATHER_DIM * 2, "OpGetRowsBf16"),
+    "q8_0": (8, GATHER_DIM // 32 * 34, "OpGetRowsQ8_0"),
+    "q4_0": (2, GATHER_DIM // 32 * 18, "OpGetRowsQ4_0"),
+    "q4_k": (12, GATHER_DIM // 256 * 144, "OpGetRowsQ4K"),
+}
+
+
+def gather_ops(suite, stream, reps):
+    """Embedding lookups (get_rows.rs): GATHER_TOKENS ids into a
+    [GATHER_DIM, GATHER_VOCAB] table of each source format, f32 output.
+    Each call is timed on its own between HIP events: it includes the
+    reference's index guard, which copies the ids to the host and waits, so
+    these are per-call times, not kernel times (rocprof gives those)."""
+    torch, eh = suite.torch, suite.eh
+    g = rng(21)
+    ids = torch.from_numpy(g.integers(0, GATHER_VOCAB, GATHER_TOKENS).astype(np.int32)).to("cuda:0")
+    out = torch.empty(GATHER_DIM * GATHER_TOKENS, dtype=torch.float32, device="cuda:0")
+    dne = [GATHER_DIM, GATHER_TOKENS, 1, 1]
+    dst = eh.TensorViewMut(out, eh.Layout(eh.DType.F32, dne, dense_nb(dne)))
+    idx = eh.IndexView(ids, [GATHER_TOKENS, 1, 1])
+    res = {}
+    for fmt, (code, row_bytes, cls) in GATHER_FORMATS.items():
+        sne = [GATHER_DIM, GATHER_VOCAB, 1, 1]
+        nbytes = row_bytes * GATHER_VOCAB
+        if code == 0:
+            table = torch.randn(GATHER_DIM * GATHER_VOCAB, device="cuda:0")
+            lay = eh.Layout(code, sne, dense_nb(sne))
+        elif code in (1, 30):
+            table = torch.randn(GATHER_DIM * GATHER_VOCAB, device="cuda:0").to(
+                torch.float16 if code == 1 else torch.bfloat16)
+            lay = eh.Layout(code, sne, dense_nb(sne, 2))
+        else:
+            raw = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device="cuda:0")
+            scales = (torch.rand(nbytes // 2, device="cuda:0") * 0.01).to(torch.float16).view(torch.uint8)
+            per_block = 144 if code == 12 else (34 if code == 8 else 18)
+            blocks = raw.view(-1, per_block)
+            hdr = 4 if code == 12 else 2
+            blocks[:, :hdr] = scales[: blocks.shape[0] * hdr].view(-1, hdr)
+            table = raw
+            lay = eh.Layout.packed(code, sne)
+        ev = getattr(eh, cls)(eh.TensorView(table, lay), idx, dst)
+        times = []
+        with torch.cuda.stream(stream):
+            for i in range(reps + 2):
+                a = torch.cuda.Event(enable_timing=True)
+                b = torch.cuda.Event(enable_timing=True)
+                a.record(stream)
+                st = suite.kernel.process_event(ev)
+                b.record(stream)
+                b.synchronize()
+                if st != eh.Status.OK:
+                    raise RuntimeError(f"get_rows {fmt}: {st.name}: {eh.last_error()}")
+                if i >= 2:
+                    times.append(a.elapsed_time(b))
+        us = float(np.median(times)) * 1e3
+        alg = GATHER_TOKENS * (row_bytes + GATHER_DIM * 4 + 4)
+        res[f"get_rows_{fmt}"] = {"config": f"{GATHER_TOKENS} ids into a [{GATHER_DIM},{GATHER_VOCAB}] {fmt} table",
+                                  "alg_bytes": alg, "call_us": round(us, 2),
+                                  "GB/s_per_call": round(alg / (us * 1e-6) / 1e9, 1)}
+        del table, ev
+    return res
+
+
 def cpu_baseline(host, budget_s=20.0):
     """Single-threaded oracle on a bounded sample of each op's workload:
     the same code path the reference's CPU kernels take (view decode,
@@ -391,6 +459,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-copy", action="store_true", help="skip the same-size copy reference per op")
     ap.add_argument("--pcie", action="store_true", help="also time soft_max_ext with host-resident tensors")
+    ap.add_argument("--no-gather", action="store_true", help="skip the get_rows embedding lookups")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -516,6 +585,10 @@ def main():
         except (ValueError, KeyError):
             pass
 
+    gather = None
+    if not args.no_gather and not args.ops:
+        gather = gather_ops(suite, stream, max(10, min(args.steps, 50)))
+
     pcie = None
     if args.pcie and "soft_max_ext" in names:
         pcie = pcie_inclusive(suite, host, stream)
@@ -552,6 +625,7 @@ def main():
                    "wall_s": round(wall, 3)},
         "per_op": per_op,
         "extra_ops": extra_ops,
+        "gather_ops": gather,
         "roofline": roof,
         "cpu_baseline": cpu,
         "pcie_inclusive": pcie,

@@ -15,6 +15,7 @@
 #include <mutex>
 #include <string>
 #include <utility>
+#include <vector>
 
 #include "launch.hpp"
 
@@ -949,6 +950,338 @@ emel_status emel_op_argmax_rows(const emel_tensor_view *src, const emel_tensor_v
         return fail(EMEL_ERR_INVALID_VIEW, "argmax_rows view failed validation");
     if (!rows_dst(*src, *dst)) return fail(EMEL_ERR_SHAPE_MISMATCH, "argmax_rows dst must be [1, ne1, ne2, ne3]");
     return reduce(emel::RedOp::ArgmaxRows, *src, *dst, stream);
+}
+
+// ---- row gather (get_rows.rs) -------------------------------------------------
+
+namespace {
+
+// IndexView::new / with_strides (get_rows.rs:54-136): metadata, count and
+// the byte span its reads cover.
+struct IndexInfo {
+    bool valid = false; // metadata_valid && span_valid (:154-157)
+    uint64_t count = 0;
+    uint64_t st[3] = {0, 0, 0}; // byte strides read through
+    uint64_t span = 0;          // bytes from data to the end of the last index
+};
+
+IndexInfo index_info(const emel_index_view &v)
+{
+    IndexInfo out;
+    bool inferred = true;
+    bool allow_implicit = false;
+    if (v.explicit_strides == 0 || v.nb[0] == 0) {
+        allow_implicit = v.explicit_strides != 0;
+        out.st[0] = 4;
+        for (int d = 1; d < 3; ++d) {
+            const u128 s = static_cast<u128>(out.st[d - 1]) * v.ne[d - 1];
+            if (s > static_cast<u128>(UINT64_MAX)) {
+                inferred = false;
+                out.st[d] = 0;
+            } else {
+                out.st[d] = static_cast<uint64_t>(s);
+            }
+        }
+    } else {
+        for (int d = 0; d < 3; ++d) out.st[d] = v.nb[d];
+    }
+    uint64_t count = 1;
+    bool zero = false, shape_ok = true, strides_ok = inferred;
+    for (int d = 0; d < 3; ++d) {
+        const uint64_t extent = v.ne[d], stride = out.st[d];
+        if (extent > 1 && stride == 0 && !allow_implicit) strides_ok = false;
+        if (stride != 0 && (stride < 4 || stride % 4 != 0)) strides_ok = false;
+        if (extent == 0) {
+            zero = true;
+        } else if (!zero) {
+            const u128 c = static_cast<u128>(count) * extent;
+            if (c > static_cast<u128>(UINT64_MAX)) {
+                shape_ok = false;
+                count = 0;
+            } else {
+                count = static_cast<uint64_t>(c);
+            }
+        }
+    }
+    if (zero) count = 0;
+    bool span_ok = false;
+    if (strides_ok && shape_ok) {
+        if (zero) {
+            span_ok = true;
+        } else {
+            u128 max_offset = 0;
+            span_ok = true;
+            for (int d = 0; d < 3 && span_ok; ++d) {
+                const u128 c = static_cast<u128>(v.ne[d] - 1) * out.st[d];
+                if (max_offset > ~static_cast<u128>(0) - c) span_ok = false;
+                else max_offset += c;
+            }
+            if (span_ok) {
+                const u128 cap = static_cast<u128>(v.len) * 4;
+                span_ok = max_offset + 4 <= cap;
+                out.span = static_cast<uint64_t>(max_offset + 4);
+            }
+        }
+    }
+    out.valid = strides_ok && shape_ok && span_ok;
+    out.count = out.valid ? count : 0;
+    return out;
+}
+
+// Layout::is_dense_contiguous_for (tensor_view.rs:297-314): the given nb.
+template <class V>
+bool dense_for(const V &v, uint32_t dtype, uint64_t elem)
+{
+    if (v.dtype != dtype) return false;
+    u128 expect = elem;
+    for (int d = 0; d < 4; ++d) {
+        if (v.nb[d] != expect) return false;
+        expect *= v.ne[d];
+        if (expect > static_cast<u128>(UINT64_MAX)) return false;
+    }
+    return true;
+}
+
+// The F32 metadata a no-op (empty index) route checks (get_rows.rs:920-943,
+// :883-904); elem 2 for BF16 (:1076-1097).
+bool empty_source_valid(const emel_tensor_view &s, uint32_t dtype, uint64_t elem, bool f32_bytes)
+{
+    if (s.dtype != dtype || s.ne[0] == 0 || s.ne[1] == 0) return false;
+    if (f32_bytes) {
+        if (s.nb[0] != 0 && (s.nb[0] < 4 || s.nb[0] % 4 != 0)) return false;
+    } else if (s.nb[0] != 0 && s.nb[0] != elem) {
+        return false;
+    }
+    if (s.nb[0] != 0)
+        for (int d = 0; d < 4; ++d)
+            if (s.ne[d] > 1 && s.nb[d] == 0) return false;
+    return true;
+}
+
+// ByteTensorView::validate (tensor_view.rs:588-645).
+bool byte_view_valid(const emel_tensor_view &s)
+{
+    uint64_t count;
+    if (s.dtype != EMEL_DTYPE_F32 || !element_count(s, count)) return false;
+    if (s.nb[0] != 0) {
+        if (s.nb[0] < 4 || s.nb[0] % 4 != 0) return false;
+        for (int d = 0; d < 4; ++d)
+            if (s.ne[d] > 1 && s.nb[d] == 0) return false;
+    }
+    uint64_t st[4];
+    if (!effective_f32_strides(s, st)) return false;
+    u128 max_offset = 0;
+    for (int d = 1; d < 4; ++d) max_offset += static_cast<u128>(s.ne[d] - 1) * st[d];
+    return max_offset + static_cast<u128>(s.ne[0]) * 4 <= static_cast<u128>(s.data_bytes);
+}
+
+// Effective strides of a 2-byte source (nb[0] == 0: row-major).
+bool half_strides(const emel_tensor_view &s, uint64_t st[4])
+{
+    if (s.nb[0] != 0) {
+        for (int d = 0; d < 4; ++d) st[d] = s.nb[d];
+        return true;
+    }
+    u128 x = 2;
+    st[0] = 2;
+    for (int d = 1; d < 4; ++d) {
+        x *= s.ne[d - 1];
+        if (x > static_cast<u128>(UINT64_MAX)) return false;
+        st[d] = static_cast<uint64_t>(x);
+    }
+    return true;
+}
+
+bool half_span_ok(const emel_tensor_view &s, const uint64_t st[4])
+{
+    u128 max_offset = 0;
+    for (int d = 0; d < 4; ++d) {
+        const u128 c = static_cast<u128>(s.ne[d] - 1) * st[d];
+        if (max_offset > ~static_cast<u128>(0) - c) return false;
+        max_offset += c;
+    }
+    return max_offset + 2 <= static_cast<u128>(s.data_bytes / 2) * 2;
+}
+
+// F16View::validate (f16_matmul.rs:49-90).
+bool f16_view_valid(const emel_tensor_view &s)
+{
+    uint64_t st[4], count;
+    if (!half_strides(s, st) || s.dtype != EMEL_DTYPE_F16 || !element_count(s, count)) return false;
+    for (int d = 0; d < 4; ++d)
+        if (s.ne[d] > 1 && (st[d] < 2 || st[d] % 2 != 0)) return false;
+    return half_span_ok(s, st);
+}
+
+constexpr uint32_t kDtypeBf16 = 30, kDtypeQ4_0 = 2, kDtypeQ8_0 = 8, kDtypeQ4K = 12;
+
+// Bf16View::validate (get_rows.rs:302-343).
+bool bf16_view_valid(const emel_tensor_view &s)
+{
+    uint64_t st[4], count;
+    if (s.dtype != kDtypeBf16 || !element_count(s, count) || !half_strides(s, st)) return false;
+    if (s.nb[0] != 0)
+        for (int d = 0; d < 4; ++d)
+            if ((s.ne[d] > 1 && s.nb[d] == 0) || (s.nb[d] != 0 && (s.nb[d] < 2 || s.nb[d] % 2 != 0))) return false;
+    return half_span_ok(s, st);
+}
+
+// PackedRowView::validate (tensor_view.rs:487-532).
+bool packed_view_valid(const emel_tensor_view &s, uint32_t code, uint64_t block_values, uint64_t block_bytes)
+{
+    if (s.dtype != code) return false;
+    for (int d = 0; d < 4; ++d)
+        if (s.ne[d] == 0) return false;
+    if (s.ne[0] % block_values != 0 || s.nb[0] != 1) return false;
+    const u128 row = static_cast<u128>(s.ne[0] / block_values) * block_bytes;
+    const u128 rs2 = row * s.ne[1];
+    const u128 rs3 = rs2 * s.ne[2];
+    if (rs3 > static_cast<u128>(UINT64_MAX) || row == 0) return false;
+    if (s.nb[1] != row || s.nb[2] != rs2 || s.nb[3] != rs3) return false;
+    u128 max_offset = 0;
+    for (int d = 1; d < 4; ++d) max_offset += static_cast<u128>(s.ne[d] - 1) * s.nb[d];
+    return max_offset + row <= static_cast<u128>(s.data_bytes);
+}
+
+enum class GrKind { F32, F32Bytes, F16, Bf16, Q4_0, Q8_0, Q4K };
+
+emel_status get_rows(GrKind kind, const emel_tensor_view *src, const emel_index_view *idx,
+                     const emel_tensor_view_mut *dst, emel_stream stream)
+{
+    if (!src || !idx || !dst) return fail(EMEL_ERR_INVALID_ARGUMENT, "null view");
+    if (idx->reserved != 0 || src->reserved != 0 || dst->reserved != 0)
+        return fail(EMEL_ERR_INVALID_ARGUMENT, "reserved fields must be 0");
+    // Pointers no Rust slice of the element type can hold.
+    const uintptr_t sp = reinterpret_cast<uintptr_t>(src->data);
+    if ((reinterpret_cast<uintptr_t>(idx->data) & 3u) || (reinterpret_cast<uintptr_t>(dst->data) & 3u) ||
+        (kind == GrKind::F32 && (sp & 3u)) || ((kind == GrKind::F16 || kind == GrKind::Bf16) && (sp & 1u)))
+        return fail(EMEL_ERR_INVALID_ARGUMENT, "data pointer not aligned to its element type");
+
+    const IndexInfo ix = index_info(*idx);
+    const uint64_t n = ix.count;
+    const emel_tensor_view &s = *src;
+    // views_valid* (get_rows.rs:855-1091)
+    bool dst_ok;
+    if (n == 0) dst_ok = dense_for(*dst, EMEL_DTYPE_F32, 4);
+    else dst_ok = valid_f32(*dst, false) && dense_for(*dst, EMEL_DTYPE_F32, 4);
+    bool src_ok = false;
+    switch (kind) {
+    case GrKind::F32: src_ok = n == 0 ? empty_source_valid(s, EMEL_DTYPE_F32, 4, false) : valid_f32(s, true); break;
+    case GrKind::F32Bytes: src_ok = n == 0 ? empty_source_valid(s, EMEL_DTYPE_F32, 4, true) : byte_view_valid(s); break;
+    case GrKind::F16: src_ok = f16_view_valid(s); if (n == 0) dst_ok = valid_f32(*dst, false) && dense_for(*dst, EMEL_DTYPE_F32, 4); break;
+    case GrKind::Bf16: src_ok = n == 0 ? empty_source_valid(s, kDtypeBf16, 2, false) : bf16_view_valid(s); break;
+    case GrKind::Q4_0: src_ok = packed_view_valid(s, kDtypeQ4_0, 32, 18); break;
+    case GrKind::Q8_0: src_ok = packed_view_valid(s, kDtypeQ8_0, 32, 34); break;
+    case GrKind::Q4K: src_ok = packed_view_valid(s, kDtypeQ4K, 256, 144); break;
+    }
+    if (!ix.valid || !src_ok || !dst_ok) return fail(EMEL_ERR_INVALID_VIEW, "get_rows view failed validation");
+    // shape_valid (get_rows.rs:966-975)
+    if (!(s.ne[0] > 0 && s.ne[1] > 0 && dst->ne[0] == s.ne[0] && dst->ne[1] == idx->ne[0] &&
+          dst->ne[2] == idx->ne[1] && dst->ne[3] == idx->ne[2] && s.ne[2] == idx->ne[1] && s.ne[3] == idx->ne[2]))
+        return fail(EMEL_ERR_SHAPE_MISMATCH, "get_rows shapes differ");
+    // source_stride_valid (get_rows.rs:961-964), the F32 route only
+    if (kind == GrKind::F32 && !(s.nb[0] == 0 || (s.nb[0] >= 4 && s.nb[0] % 4 == 0)))
+        return fail(EMEL_ERR_UNSUPPORTED_SOURCE_STRIDE, "get_rows source element stride");
+    // dst must not overlap what the gather reads (impossible for Rust's borrows)
+    if (n > 0) {
+        const auto d = byte_range(*dst, 4);
+        auto hit = [&](uintptr_t lo, uint64_t bytes) { return lo < d.second && d.first < lo + bytes; };
+        if (hit(sp, s.data_bytes) || hit(reinterpret_cast<uintptr_t>(idx->data), ix.span))
+            return fail(EMEL_ERR_INVALID_VIEW, "dst overlaps the source or the indices");
+    }
+    emel_status st = ensure_device();
+    if (st != EMEL_OK) return st;
+    if (n == 0) {
+        g_last_error.clear();
+        return EMEL_OK; // the reference's loops run zero times
+    }
+    // indices_valid (get_rows.rs:1239-1250): every index in [0, src.ne1),
+    // read from a host copy of the index span.
+    const hipStream_t hs = as_stream(stream);
+    std::vector<int32_t> host((ix.span + 3) / 4);
+    hipError_t e = hipMemcpyAsync(host.data(), idx->data, ix.span, hipMemcpyDeviceToHost, hs);
+    if (e == hipSuccess) e = hipStreamSynchronize(hs);
+    if (e != hipSuccess) return hip_fail(e, "copying the indices to the host");
+    const uint64_t es[3] = {ix.st[0] / 4, ix.st[1] / 4, ix.st[2] / 4};
+    for (uint64_t k = 0; k < n; ++k) {
+        const uint64_t i0 = k % idx->ne[0], rem = k / idx->ne[0];
+        const uint64_t i1 = rem % idx->ne[1], i2 = rem / idx->ne[1];
+        const int32_t row = host[i0 * es[0] + i1 * es[1] + i2 * es[2]];
+        if (row < 0 || static_cast<uint64_t>(row) >= s.ne[1])
+            return fail(EMEL_ERR_INDEX_OUT_OF_BOUNDS, "get_rows index " + std::to_string(row) + " at ordinal " +
+                                                          std::to_string(k) + " is outside the source rows");
+    }
+    emel::GetRowsArgs a{};
+    switch (kind) {
+    case GrKind::F32: a.kind = emel::RowSrc::F32; break;
+    case GrKind::F32Bytes: a.kind = emel::RowSrc::F32Bytes; break;
+    case GrKind::F16: a.kind = emel::RowSrc::F16; break;
+    case GrKind::Bf16: a.kind = emel::RowSrc::Bf16; break;
+    case GrKind::Q4_0: a.kind = emel::RowSrc::Q4_0; break;
+    case GrKind::Q8_0: a.kind = emel::RowSrc::Q8_0; break;
+    case GrKind::Q4K: a.kind = emel::RowSrc::Q4K; break;
+    }
+    a.src = s.data;
+    uint64_t stv[4] = {s.nb[0], s.nb[1], s.nb[2], s.nb[3]};
+    if (kind == GrKind::F32 || kind == GrKind::F32Bytes) effective_f32_strides(s, stv);
+    else if (kind == GrKind::F16 || kind == GrKind::Bf16) half_strides(s, stv);
+    for (int d = 0; d < 4; ++d) {
+        a.src_ne[d] = s.ne[d];
+        a.src_st[d] = static_cast<int64_t>(s.ne[d] > 1 ? stv[d] : 0); // a singleton's stride never moves
+    }
+    a.idx = idx->data;
+    for (int d = 0; d < 3; ++d) {
+        a.idx_ne[d] = idx->ne[d];
+        a.idx_st[d] = static_cast<int64_t>(idx->ne[d] > 1 ? es[d] : 0);
+    }
+    a.dst = static_cast<float *>(dst->data);
+    a.rows = n;
+    a.cols = s.ne[0];
+    return launched(emel::launch_get_rows(a, hs));
+}
+
+} // namespace
+
+emel_status emel_op_get_rows(const emel_tensor_view *src, const emel_index_view *indices,
+                             const emel_tensor_view_mut *dst, emel_stream stream)
+{
+    return get_rows(GrKind::F32, src, indices, dst, stream);
+}
+
+emel_status emel_op_get_rows_f32_bytes(const emel_tensor_view *src, const emel_index_view *indices,
+                                       const emel_tensor_view_mut *dst, emel_stream stream)
+{
+    return get_rows(GrKind::F32Bytes, src, indices, dst, stream);
+}
+
+emel_status emel_op_get_rows_f16(const emel_tensor_view *src, const emel_index_view *indices,
+                                 const emel_tensor_view_mut *dst, emel_stream stream)
+{
+    return get_rows(GrKind::F16, src, indices, dst, stream);
+}
+
+emel_status emel_op_get_rows_bf16(const emel_tensor_view *src, const emel_index_view *indices,
+                                  const emel_tensor_view_mut *dst, emel_stream stream)
+{
+    return get_rows(GrKind::Bf16, src, indices, dst, stream);
+}
+
+emel_status emel_op_get_rows_q4_0(const emel_tensor_view *src, const emel_index_view *indices,
+                                  const emel_tensor_view_mut *dst, emel_stream stream)
+{
+    return get_rows(GrKind::Q4_0, src, indices, dst, stream);
+}
+
+emel_status emel_op_get_rows_q8_0(const emel_tensor_view *src, const emel_index_view *indices,
+                                  const emel_tensor_view_mut *dst, emel_stream stream)
+{
+    return get_rows(GrKind::Q8_0, src, indices, dst, stream);
+}
+
+emel_status emel_op_get_rows_q4_k(const emel_tensor_view *src, const emel_index_view *indices,
+                                  const emel_tensor_view_mut *dst, emel_stream stream)
+{
+    return get_rows(GrKind::Q4K, src, indices, dst, stream);
 }
 
 // ---- generic wire envelope (generic.rs, guards actor.rs:2448-2983) ----------

@@ -150,4 +150,23 @@ struct GenMatArgs {
 
 hipError_t launch_generic_mul_mat(const GenMatArgs &args, hipStream_t stream);
 
+// ---- row gather (getrows.hip) -------------------------------------------------
+
+enum class RowSrc : uint32_t { F32 = 0, F32Bytes, F16, Bf16, Q4_0, Q8_0, Q4K };
+
+struct GetRowsArgs {
+    RowSrc kind;
+    const void *src;
+    uint64_t src_ne[4];
+    int64_t src_st[4];    // effective byte strides (unused for packed sources)
+    const int32_t *idx;
+    uint64_t idx_ne[3];
+    int64_t idx_st[3];    // element strides
+    float *dst;           // dense [cols, rows]
+    uint64_t rows;        // index count
+    uint64_t cols;        // src.ne[0]
+};
+
+hipError_t launch_get_rows(const GetRowsArgs &args, hipStream_t stream);
+
 } // namespace emel

@@ -4,6 +4,8 @@ include/emel_hip.h, with a Python mirror of emel-kernels' operator API.
 """
 from .abi import BinaryOp, DType, GenericOp, GluSubOp, Status, UnarySubOp, device_count, last_error, load
 from .generic import GenericEvent, GenericRequest, OpParams
+from .get_rows import (IndexView, OpGetRows, OpGetRowsBf16, OpGetRowsF16, OpGetRowsF32Bytes, OpGetRowsQ4_0,
+                       OpGetRowsQ4K, OpGetRowsQ8_0)
 from .kernel import (
     DenseOpAdd,
     DenseOpDiv,
@@ -48,5 +50,6 @@ __all__ = [
     "OpUnary", "OpSilu", "OpGelu", "OpGlu", "OpSwiglu", "OpScale", "OpRmsNorm", "OpRmsNormMul", "OpNorm",
     "OpSoftMax", "OpSoftMaxExt", "OpSumRows", "OpSum", "OpMean", "OpArgmax", "OpArgmaxRows",
     "OpSqr", "OpSqrt", "DenseOpDup", "DenseOpAdd", "DenseOpSub", "DenseOpMul", "DenseOpDiv", "DenseOpSqr",
-    "DenseOpSqrt",
+    "DenseOpSqrt", "IndexView", "OpGetRows", "OpGetRowsF32Bytes", "OpGetRowsF16", "OpGetRowsBf16", "OpGetRowsQ4_0",
+    "OpGetRowsQ8_0", "OpGetRowsQ4K",
 ]

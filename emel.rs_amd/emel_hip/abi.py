@@ -26,6 +26,8 @@ class Status(enum.IntEnum):
     INVALID_ARGUMENT = 8
     INVALID_SHAPE = 9
     UNSUPPORTED_OPERATION = 10
+    INDEX_OUT_OF_BOUNDS = 11
+    UNSUPPORTED_SOURCE_STRIDE = 12
 
 
 class DType(enum.IntEnum):
@@ -33,7 +35,11 @@ class DType(enum.IntEnum):
 
     F32 = 0
     F16 = 1
+    Q4_0 = 2
+    Q8_0 = 8
+    Q4_K = 12
     I32 = 26
+    BF16 = 30
 
 
 class UnarySubOp(enum.IntEnum):
@@ -217,6 +223,19 @@ class CGenericRequest(ctypes.Structure):
     ]
 
 
+class CIndexView(ctypes.Structure):
+    """emel_index_view: an int32 index tensor (IndexView, get_rows.rs:42-196)."""
+
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("len", ctypes.c_uint64),
+        ("ne", ctypes.c_uint64 * 3),
+        ("nb", ctypes.c_uint64 * 3),
+        ("explicit_strides", ctypes.c_uint32),
+        ("reserved", ctypes.c_uint32),
+    ]
+
+
 _V = ctypes.POINTER(CView)
 _S = ctypes.c_void_p
 _ST = ctypes.c_int
@@ -266,6 +285,8 @@ SIGNATURES = {
     "emel_stream_synchronize": [_S],
     "emel_release_workspaces": [],
     "emel_generic_dispatch": [ctypes.POINTER(CGenericRequest), _S],
+    **{f"emel_op_get_rows{suffix}": [_V, ctypes.POINTER(CIndexView), _V, _S]
+       for suffix in ("", "_f32_bytes", "_f16", "_bf16", "_q4_0", "_q8_0", "_q4_k")},
 }
 
 _lib = None

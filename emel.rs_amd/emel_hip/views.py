@@ -15,7 +15,9 @@ from typing import Sequence
 
 from .abi import CView, DType
 
-_ELEM = {DType.F32: 4, DType.F16: 2, DType.I32: 4}
+_ELEM = {DType.F32: 4, DType.F16: 2, DType.I32: 4, DType.BF16: 2}
+# Packed formats: (values per block, bytes per block) (quant.rs:13-17, quant_more.rs:38-48).
+_PACKED = {DType.Q4_0: (32, 18), DType.Q8_0: (32, 34), DType.Q4_K: (256, 144)}
 
 
 @dataclass(frozen=True)
@@ -46,6 +48,15 @@ class Layout:
         nb = [_ELEM.get(int(dtype), 4)]
         for d in range(1, 4):
             nb.append(nb[-1] * int(ne[d - 1]))
+        return Layout(dtype, ne, nb)
+
+    @staticmethod
+    def packed(dtype: int, ne: Sequence[int]) -> "Layout":
+        """Packed quantized rows: nb = [1, row bytes, ...] as PackedRowView
+        requires (tensor_view.rs:487-532)."""
+        values, block_bytes = _PACKED[DType(int(dtype))]
+        row = (int(ne[0]) // values) * block_bytes
+        nb = [1, row, row * int(ne[1]), row * int(ne[1]) * int(ne[2])]
         return Layout(dtype, ne, nb)
 
     def permuted(self, axes: Sequence[int]) -> "Layout":

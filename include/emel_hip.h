@@ -57,7 +57,9 @@ typedef enum emel_status {
     EMEL_ERR_DEVICE = 7,             /* a HIP runtime call failed */
     EMEL_ERR_INVALID_ARGUMENT = 8,   /* a required pointer argument is NULL */
     EMEL_ERR_INVALID_SHAPE = 9,      /* root Error::InvalidShape (actor.rs:88-101): dense-slice events */
-    EMEL_ERR_UNSUPPORTED_OPERATION = 10 /* root Error::UnsupportedOperation */
+    EMEL_ERR_UNSUPPORTED_OPERATION = 10, /* root Error::UnsupportedOperation */
+    EMEL_ERR_INDEX_OUT_OF_BOUNDS = 11,   /* GetRowsError::IndexOutOfBounds (get_rows.rs:520-535) */
+    EMEL_ERR_UNSUPPORTED_SOURCE_STRIDE = 12 /* GetRowsError::UnsupportedSourceStride */
 } emel_status;
 
 /* Wire dtype codes, DType::from_code (tensor_view.rs:111-158). */
@@ -283,6 +285,58 @@ emel_status emel_op_argmax(const emel_tensor_view *src, const emel_tensor_view_m
  * column 0 yields 0, exactly as the sequential strict-> scan). */
 emel_status emel_op_argmax_rows(const emel_tensor_view *src, const emel_tensor_view_mut *dst,
                                 emel_stream stream);
+
+/* ---- row gather -----------------------------------------------------------------
+ * get_rows::OpGetRows / OpGetRowsF32Bytes / OpGetRowsF16 / OpGetRowsBf16 /
+ * OpGetRowsQ4_0 / OpGetRowsQ8_0 / OpGetRowsQ4K::new(source, indices,
+ * destination) (get_rows.rs:219-510; guards :855-1452; actions :1453-2003):
+ * dst row (i0, i1, i2) = source row indices[i0, i1, i2] of batch (i1, i2),
+ * converted to f32.  dst is dense F32 [src.ne0, idx.ne0, idx.ne1, idx.ne2];
+ * src.ne2 == idx.ne1 and src.ne3 == idx.ne2.
+ *
+ * The index tensor mirrors IndexView (get_rows.rs:42-196): int32 values,
+ * three extents, byte strides.  explicit_strides == 0 is IndexView::new
+ * (row-major); 1 is IndexView::with_strides (nb[0] == 0 still selects
+ * row-major).  len counts int32 elements at data (the Rust slice length).
+ * data is a device pointer like every view's.
+ *
+ * The reference checks every index against the source row count before
+ * writing anything.  To keep that contract, a call whose views and shapes
+ * pass copies the index span to the host on `stream` and waits for it
+ * (the only entry points that synchronise; they cannot be captured into a
+ * HIP graph).  Statuses: INVALID_VIEW, SHAPE_MISMATCH,
+ * UNSUPPORTED_SOURCE_STRIDE (F32 only), INDEX_OUT_OF_BOUNDS, in the
+ * reference's guard order. */
+typedef struct emel_index_view {
+    const int32_t *data;
+    uint64_t len;     /* int32 elements at data */
+    uint64_t ne[3];
+    uint64_t nb[3];   /* byte strides (explicit_strides == 1) */
+    uint32_t explicit_strides;
+    uint32_t reserved; /* must be 0 */
+} emel_index_view;
+
+/* F32 source: rows located by nb[1..3]; each row copies ne0 contiguous
+ * floats from its start (the pinned memcpy, whatever nb[0] is). */
+emel_status emel_op_get_rows(const emel_tensor_view *src, const emel_index_view *indices,
+                             const emel_tensor_view_mut *dst, emel_stream stream);
+/* F32 source read byte-wise: outer byte strides need not be multiples of 4. */
+emel_status emel_op_get_rows_f32_bytes(const emel_tensor_view *src, const emel_index_view *indices,
+                                       const emel_tensor_view_mut *dst, emel_stream stream);
+/* F16 / BF16 sources (dtype 1 / 30), element-strided, widened exactly. */
+emel_status emel_op_get_rows_f16(const emel_tensor_view *src, const emel_index_view *indices,
+                                 const emel_tensor_view_mut *dst, emel_stream stream);
+emel_status emel_op_get_rows_bf16(const emel_tensor_view *src, const emel_index_view *indices,
+                                  const emel_tensor_view_mut *dst, emel_stream stream);
+/* Packed quantized sources (dtype 2 / 8 / 12, nb = [1, row bytes, ...]):
+ * Q4_0 and Q8_0 blocks of 32 values (quant.rs:71-206), Q4_K blocks of 256
+ * (quant_more.rs:402-469, scale/min unpacking :952-961). */
+emel_status emel_op_get_rows_q4_0(const emel_tensor_view *src, const emel_index_view *indices,
+                                  const emel_tensor_view_mut *dst, emel_stream stream);
+emel_status emel_op_get_rows_q8_0(const emel_tensor_view *src, const emel_index_view *indices,
+                                  const emel_tensor_view_mut *dst, emel_stream stream);
+emel_status emel_op_get_rows_q4_k(const emel_tensor_view *src, const emel_index_view *indices,
+                                  const emel_tensor_view_mut *dst, emel_stream stream);
 
 /* ---- generic wire envelope ----------------------------------------------------
  * event::GenericEvent::new(GenericRequest::new(operation, src0, src1, src2,

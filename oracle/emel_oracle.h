@@ -41,6 +41,8 @@ enum {
     ORC_INVALID_ARGUMENT = 8,        /* a value no reference type can hold */
     ORC_INVALID_SHAPE = 9,           /* root Error::InvalidShape */
     ORC_UNSUPPORTED_OPERATION = 10,  /* root Error::UnsupportedOperation */
+    ORC_INDEX_OUT_OF_BOUNDS = 11,    /* GetRowsError::IndexOutOfBounds */
+    ORC_UNSUPPORTED_SOURCE_STRIDE = 12, /* GetRowsError::UnsupportedSourceStride */
     ORC_PANIC = 99,                  /* the reference's guard passes and its executor panics */
 };
 
@@ -107,6 +109,19 @@ typedef struct orc_generic_request {
     int32_t *index_out;
 } orc_generic_request;
 int orc_generic(const orc_generic_request *request);
+
+/* Row gather (get_rows.rs), in emel_oracle_getrows.c.  The index view has
+ * the emel_index_view layout of include/emel_hip.h with a host pointer. */
+typedef struct orc_index_view {
+    const int32_t *data;
+    uint64_t len; /* int32 elements */
+    uint64_t ne[3];
+    uint64_t nb[3];
+    uint32_t explicit_strides;
+    uint32_t reserved;
+} orc_index_view;
+enum { ORC_GR_F32 = 0, ORC_GR_F32_BYTES, ORC_GR_F16, ORC_GR_BF16, ORC_GR_Q4_0, ORC_GR_Q8_0, ORC_GR_Q4_K };
+int orc_get_rows(int kind, const orc_view *src, const orc_index_view *indices, const orc_view *dst);
 
 /* Scalar helpers (unary.rs:522-600, quant.rs:287-300). */
 float orc_silu(float x);

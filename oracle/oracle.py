@@ -234,3 +234,44 @@ def generic(operation: int, src0=None, src1=None, src2=None, dst=None, params: b
     L.orc_generic.argtypes = [ctypes.POINTER(OGenericRequest)]
     L.orc_generic.restype = ctypes.c_int
     return int(L.orc_generic(ctypes.byref(r)))
+
+
+# row gather -------------------------------------------------------------------
+
+INDEX_OUT_OF_BOUNDS, UNSUPPORTED_SOURCE_STRIDE = 11, 12
+GR_F32, GR_F32_BYTES, GR_F16, GR_BF16, GR_Q4_0, GR_Q8_0, GR_Q4_K = range(7)
+
+
+class OIndexView(ctypes.Structure):
+    """orc_index_view (the emel_index_view layout, host pointer)."""
+
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("len", ctypes.c_uint64),
+        ("ne", ctypes.c_uint64 * 3),
+        ("nb", ctypes.c_uint64 * 3),
+        ("explicit_strides", ctypes.c_uint32),
+        ("reserved", ctypes.c_uint32),
+    ]
+
+
+def index_view(arr: np.ndarray, ne, nb=None, length: int | None = None) -> OIndexView:
+    """IndexView::new(arr, ne) when nb is None, else IndexView::with_strides."""
+    assert arr.dtype == np.int32 and arr.flags["C_CONTIGUOUS"]
+    v = OIndexView()
+    v.data = arr.ctypes.data if arr.size else 0
+    v.len = arr.size if length is None else int(length)
+    for d in range(3):
+        v.ne[d] = int(ne[d])
+        v.nb[d] = 0 if nb is None else int(nb[d])
+    v.explicit_strides = 0 if nb is None else 1
+    v.reserved = 0
+    v._arr = arr
+    return v
+
+
+def get_rows(kind: int, src: OView, idx: OIndexView, dst: OView) -> int:
+    L = lib()
+    L.orc_get_rows.argtypes = [ctypes.c_int, ctypes.POINTER(OView), ctypes.POINTER(OIndexView), ctypes.POINTER(OView)]
+    L.orc_get_rows.restype = ctypes.c_int
+    return int(L.orc_get_rows(kind, ctypes.byref(src), ctypes.byref(idx), ctypes.byref(dst)))

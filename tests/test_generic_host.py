@@ -286,3 +286,89 @@ def test_struct_layout():
     assert ctypes.sizeof(CGenericRequest) == 128
     assert CGenericRequest.op_params.offset == 48
     assert CGenericRequest.index_out.offset == 120
+
+
+# ---- row gather: host-side classification against the oracle ---------------------------
+
+
+def test_get_rows_classification_matches_the_oracle():
+    """Views, shapes and strides are classified on the host before the index
+    check, which needs the device: an oracle OK or INDEX_OUT_OF_BOUNDS is
+    KERNEL_UNAVAILABLE here."""
+    from emel_hip.abi import CIndexView
+
+    g = np.random.Generator(np.random.PCG64(77))
+    lib = eh.load()
+    kinds = [(orc.GR_F32, 0, "emel_op_get_rows", 4), (orc.GR_F32_BYTES, 0, "emel_op_get_rows_f32_bytes", 4),
+             (orc.GR_F16, 1, "emel_op_get_rows_f16", 2), (orc.GR_BF16, 30, "emel_op_get_rows_bf16", 2),
+             (orc.GR_Q4_0, 2, "emel_op_get_rows_q4_0", 0), (orc.GR_Q8_0, 8, "emel_op_get_rows_q8_0", 0),
+             (orc.GR_Q4_K, 12, "emel_op_get_rows_q4_k", 0)]
+    seen = {}
+    for trial in range(3000):
+        kind, dtype, fn, elem = kinds[trial % len(kinds)]
+        cols = {2: 32, 8: 32, 12: 256}.get(dtype, int(g.integers(1, 5)))
+        rows = int(g.integers(1, 4))
+        ine = [int(g.integers(0, 3)), int(g.integers(1, 3)), int(g.integers(1, 3))]
+        sne = [cols, rows, ine[1], ine[2]]
+        if dtype in (2, 8, 12):
+            bv, bb = {2: (32, 18), 8: (32, 34), 12: (256, 144)}[dtype]
+            row = cols // bv * bb
+            snb = [1, row, row * rows, row * rows * ine[1]]
+        else:
+            snb = [elem]
+            for d in range(1, 4):
+                snb.append(snb[-1] * sne[d - 1])
+        dne = [cols, ine[0], ine[1], ine[2]]
+        dnb = [4, 4 * dne[0], 4 * dne[0] * dne[1], 4 * dne[0] * dne[1] * dne[2]]
+        inb = None
+        idx_len = int(np.prod(ine))
+        # mutations
+        m = int(g.integers(0, 10))
+        if m == 0:
+            sne[int(g.integers(0, 4))] = int(g.integers(0, 4))
+        elif m == 1:
+            snb[int(g.integers(0, 4))] = int(g.choice([0, 1, 2, 3, 4, 6, 8, 9]))
+        elif m == 2:
+            snb[0] = 0
+        elif m == 3:
+            dne[int(g.integers(0, 4))] = int(g.integers(0, 4))
+        elif m == 4:
+            dnb[int(g.integers(0, 4))] = int(g.choice([0, 4, 8]))
+        elif m == 5:
+            inb = [int(g.choice([0, 2, 4, 8, 12])) for _ in range(3)]
+        elif m == 6:
+            idx_len = max(0, idx_len - int(g.integers(1, 3)))
+        elif m == 7:
+            ine[int(g.integers(0, 3))] = int(g.integers(0, 4))
+        src_span = 1
+        for d in range(4):
+            src_span += max(sne[d] - 1, 0) * snb[d]
+        src_bytes = max(src_span + 8, cols * 4 + 8) if m != 8 else max(src_span - 2, 0)
+        src = np.zeros(max(src_bytes, 8) // 4 + 4, np.float32)
+        count = int(np.prod(dne))
+        out = np.zeros(max(count, 1) + 4, np.float32)
+        idx = np.zeros(max(idx_len, 1), np.int32)
+        want = orc.get_rows(kind, orc.view(src, sne, snb, dtype, src_bytes),
+                            orc.index_view(idx[:idx_len] if idx_len else np.zeros(0, np.int32), ine, inb, idx_len),
+                            orc.view(out, dne, dnb, 0, 4 * count))
+        cs, cd = CView(), CView()
+        for v, arr, ne, nb, dt, nbytes in ((cs, src, sne, snb, dtype, src_bytes), (cd, out, dne, dnb, 0, 4 * count)):
+            v.data = arr.ctypes.data
+            v.data_bytes = nbytes
+            v.dtype = dt
+            v.reserved = 0
+            for d in range(4):
+                v.ne[d] = ne[d]
+                v.nb[d] = nb[d]
+        ci = CIndexView()
+        ci.data = idx.ctypes.data
+        ci.len = idx_len
+        for d in range(3):
+            ci.ne[d] = ine[d]
+            ci.nb[d] = 0 if inb is None else inb[d]
+        ci.explicit_strides = 0 if inb is None else 1
+        got = getattr(lib, fn)(ctypes.byref(cs), ctypes.byref(ci), ctypes.byref(cd), None)
+        expect = KERNEL_UNAVAILABLE if want in (OK, orc.INDEX_OUT_OF_BOUNDS) else want
+        assert got == expect, (trial, kind, want, got, sne, snb, ine, inb, idx_len, dne, dnb, src_bytes)
+        seen[want] = seen.get(want, 0) + 1
+    assert {OK, orc.INVALID_VIEW, orc.SHAPE_MISMATCH} <= set(seen), seen
