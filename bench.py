@@ -313,56 +313,97 @@ GATHER_FORMATS = {
 def gather_ops(suite, stream, reps):
     """Embedding lookups (get_rows.rs): GATHER_TOKENS ids into a
     [GATHER_DIM, GATHER_VOCAB] table of each source format, f32 output.
-    Each call is timed on its own between HIP events: it includes the
-    reference's index guard, which copies the ids to the host and waits, so
-    these are per-call times, not kernel times (rocprof gives those)."""
+    call_us: one call between HIP events with device-resident ids (the
+    index guard copies them to the host and waits); call_us_host_ids: the
+    same with host-resident ids (checked in place, passed by value);
+    kernel_us: a captured graph of back-to-back host-id calls cycling through
+    table / output / id copies totalling >= ROTATE_BYTES, so rows come from
+    HBM as in a decode step whose other layers flushed the caches."""
     torch, eh = suite.torch, suite.eh
     g = rng(21)
-    ids = torch.from_numpy(g.integers(0, GATHER_VOCAB, GATHER_TOKENS).astype(np.int32)).to("cuda:0")
-    out = torch.empty(GATHER_DIM * GATHER_TOKENS, dtype=torch.float32, device="cuda:0")
     dne = [GATHER_DIM, GATHER_TOKENS, 1, 1]
-    dst = eh.TensorViewMut(out, eh.Layout(eh.DType.F32, dne, dense_nb(dne)))
-    idx = eh.IndexView(ids, [GATHER_TOKENS, 1, 1])
+    sne = [GATHER_DIM, GATHER_VOCAB, 1, 1]
     res = {}
     for fmt, (code, row_bytes, cls) in GATHER_FORMATS.items():
-        sne = [GATHER_DIM, GATHER_VOCAB, 1, 1]
-        nbytes = row_bytes * GATHER_VOCAB
-        if code == 0:
-            table = torch.randn(GATHER_DIM * GATHER_VOCAB, device="cuda:0")
-            lay = eh.Layout(code, sne, dense_nb(sne))
-        elif code in (1, 30):
-            table = torch.randn(GATHER_DIM * GATHER_VOCAB, device="cuda:0").to(
-                torch.float16 if code == 1 else torch.bfloat16)
-            lay = eh.Layout(code, sne, dense_nb(sne, 2))
-        else:
-            raw = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device="cuda:0")
-            scales = (torch.rand(nbytes // 2, device="cuda:0") * 0.01).to(torch.float16).view(torch.uint8)
-            per_block = 144 if code == 12 else (34 if code == 8 else 18)
-            blocks = raw.view(-1, per_block)
-            hdr = 4 if code == 12 else 2
-            blocks[:, :hdr] = scales[: blocks.shape[0] * hdr].view(-1, hdr)
-            table = raw
-            lay = eh.Layout.packed(code, sne)
-        ev = getattr(eh, cls)(eh.TensorView(table, lay), idx, dst)
-        times = []
+        table_bytes = row_bytes * GATHER_VOCAB
+        out_bytes = GATHER_DIM * GATHER_TOKENS * 4
+        copies = max(2, -(-ROTATE_BYTES // (table_bytes + out_bytes)))
+        evs_host, keep = [], []
+        ev_dev = None
+        for c in range(copies):
+            if code == 0:
+                table = torch.randn(GATHER_DIM * GATHER_VOCAB, device="cuda:0")
+                lay = eh.Layout(code, sne, dense_nb(sne))
+            elif code in (1, 30):
+                table = torch.randn(GATHER_DIM * GATHER_VOCAB, device="cuda:0").to(
+                    torch.float16 if code == 1 else torch.bfloat16)
+                lay = eh.Layout(code, sne, dense_nb(sne, 2))
+            else:
+                raw = torch.randint(0, 256, (table_bytes,), dtype=torch.uint8, device="cuda:0")
+                per_block = 144 if code == 12 else (34 if code == 8 else 18)
+                blocks = raw.view(-1, per_block)
+                hdr = 4 if code == 12 else 2
+                scales = (torch.rand(blocks.shape[0] * hdr // 2, device="cuda:0") * 0.01).to(torch.float16)
+                blocks[:, :hdr] = scales.view(torch.uint8).view(-1, hdr)
+                table = raw
+                lay = eh.Layout.packed(code, sne)
+            out = torch.empty(GATHER_DIM * GATHER_TOKENS, dtype=torch.float32, device="cuda:0")
+            ids_host = g.integers(0, GATHER_VOCAB, GATHER_TOKENS).astype(np.int32)
+            dst = eh.TensorViewMut(out, eh.Layout(eh.DType.F32, dne, dense_nb(dne)))
+            evs_host.append(getattr(eh, cls)(eh.TensorView(table, lay), eh.IndexView(ids_host, [GATHER_TOKENS, 1, 1]),
+                                             dst))
+            if c == 0:
+                ids_dev = torch.from_numpy(ids_host).to("cuda:0")
+                ev_dev = getattr(eh, cls)(eh.TensorView(table, lay), eh.IndexView(ids_dev, [GATHER_TOKENS, 1, 1]),
+                                          dst)
+                keep.append(ids_dev)
+            keep += [table, out, ids_host]
+
+        def call(e):
+            st = suite.kernel.process_event(e)
+            if st != eh.Status.OK:
+                raise RuntimeError(f"get_rows {fmt}: {st.name}: {eh.last_error()}")
+
+        def per_call(e):
+            times = []
+            with torch.cuda.stream(stream):
+                for i in range(reps + 2):
+                    a = torch.cuda.Event(enable_timing=True)
+                    b = torch.cuda.Event(enable_timing=True)
+                    a.record(stream)
+                    call(e)
+                    b.record(stream)
+                    b.synchronize()
+                    if i >= 2:
+                        times.append(a.elapsed_time(b))
+            return float(np.median(times)) * 1e3
+
+        us = per_call(ev_dev)
+        us_host = per_call(evs_host[0])
+        n = max(reps, copies)
         with torch.cuda.stream(stream):
-            for i in range(reps + 2):
-                a = torch.cuda.Event(enable_timing=True)
-                b = torch.cuda.Event(enable_timing=True)
-                a.record(stream)
-                st = suite.kernel.process_event(ev)
-                b.record(stream)
-                b.synchronize()
-                if st != eh.Status.OK:
-                    raise RuntimeError(f"get_rows {fmt}: {st.name}: {eh.last_error()}")
-                if i >= 2:
-                    times.append(a.elapsed_time(b))
-        us = float(np.median(times)) * 1e3
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr, stream=stream):
+                for i in range(n):
+                    call(evs_host[i % copies])
+            stream.synchronize()
+            gr.replay()
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            for _ in range(3):
+                gr.replay()
+            b.record(stream)
+            b.synchronize()
+            kus = a.elapsed_time(b) * 1e3 / (3 * n)
         alg = GATHER_TOKENS * (row_bytes + GATHER_DIM * 4 + 4)
         res[f"get_rows_{fmt}"] = {"config": f"{GATHER_TOKENS} ids into a [{GATHER_DIM},{GATHER_VOCAB}] {fmt} table",
-                                  "alg_bytes": alg, "call_us": round(us, 2),
-                                  "GB/s_per_call": round(alg / (us * 1e-6) / 1e9, 1)}
-        del table, ev
+                                  "alg_bytes": alg, "call_us": round(us, 2), "call_us_host_ids": round(us_host, 2),
+                                  "kernel_us": round(kus, 3), "GB/s": round(alg / (kus * 1e-6) / 1e9, 1),
+                                  "frac_of_peak": round(alg / (kus * 1e-6) / 1e9 / PEAK_GBS, 4),
+                                  "rotation": f"{copies} table/output/id copies"}
+        del gr, evs_host, ev_dev, keep
+        torch.cuda.empty_cache()
     return res
 
 

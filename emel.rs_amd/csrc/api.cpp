@@ -279,6 +279,32 @@ emel_status workspace_for(hipStream_t stream, uint64_t bytes, void **out)
     return EMEL_OK;
 }
 
+// Per-(device, stream) pinned host staging for index copies to the host.
+std::map<std::pair<int, hipStream_t>, Workspace> g_staging;
+
+emel_status staging_for(hipStream_t stream, uint64_t bytes, void **out)
+{
+    *out = nullptr;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    std::lock_guard<std::mutex> lock(g_mutex);
+    Workspace &w = g_staging[{dev, stream}];
+    if (w.bytes < bytes) {
+        if (w.ptr) {
+            (void)hipHostFree(w.ptr); // callers wait for their copy before returning
+            w.ptr = nullptr;
+            w.bytes = 0;
+        }
+        const uint64_t size = bytes < (uint64_t{1} << 16) ? (uint64_t{1} << 16) : bytes;
+        e = hipHostMalloc(&w.ptr, size, hipHostMallocDefault);
+        if (e != hipSuccess) return hip_fail(e, "hipHostMalloc(staging)");
+        w.bytes = size;
+    }
+    *out = w.ptr;
+    return EMEL_OK;
+}
+
 emel_status launched(hipError_t e)
 {
     if (e != hipSuccess) return hip_fail(e, "kernel launch");
@@ -571,6 +597,8 @@ emel_status emel_release_workspaces(void)
     hipError_t e = hipDeviceSynchronize();
     for (auto &kv : g_workspaces) (void)hipFree(kv.second.ptr);
     g_workspaces.clear();
+    for (auto &kv : g_staging) (void)hipHostFree(kv.second.ptr);
+    g_staging.clear();
     return e == hipSuccess ? EMEL_OK : hip_fail(e, "hipDeviceSynchronize");
 }
 
@@ -1149,8 +1177,8 @@ emel_status get_rows(GrKind kind, const emel_tensor_view *src, const emel_index_
                      const emel_tensor_view_mut *dst, emel_stream stream)
 {
     if (!src || !idx || !dst) return fail(EMEL_ERR_INVALID_ARGUMENT, "null view");
-    if (idx->reserved != 0 || src->reserved != 0 || dst->reserved != 0)
-        return fail(EMEL_ERR_INVALID_ARGUMENT, "reserved fields must be 0");
+    if (idx->on_host > 1 || src->reserved != 0 || dst->reserved != 0)
+        return fail(EMEL_ERR_INVALID_ARGUMENT, "on_host must be 0 or 1 and reserved fields 0");
     // Pointers no Rust slice of the element type can hold.
     const uintptr_t sp = reinterpret_cast<uintptr_t>(src->data);
     if ((reinterpret_cast<uintptr_t>(idx->data) & 3u) || (reinterpret_cast<uintptr_t>(dst->data) & 3u) ||
@@ -1186,7 +1214,7 @@ emel_status get_rows(GrKind kind, const emel_tensor_view *src, const emel_index_
     if (n > 0) {
         const auto d = byte_range(*dst, 4);
         auto hit = [&](uintptr_t lo, uint64_t bytes) { return lo < d.second && d.first < lo + bytes; };
-        if (hit(sp, s.data_bytes) || hit(reinterpret_cast<uintptr_t>(idx->data), ix.span))
+        if (hit(sp, s.data_bytes) || (!idx->on_host && hit(reinterpret_cast<uintptr_t>(idx->data), ix.span)))
             return fail(EMEL_ERR_INVALID_VIEW, "dst overlaps the source or the indices");
     }
     emel_status st = ensure_device();
@@ -1196,20 +1224,29 @@ emel_status get_rows(GrKind kind, const emel_tensor_view *src, const emel_index_
         return EMEL_OK; // the reference's loops run zero times
     }
     // indices_valid (get_rows.rs:1239-1250): every index in [0, src.ne1),
-    // read from a host copy of the index span.
+    // read from host memory (on_host) or from a host copy of the index span.
     const hipStream_t hs = as_stream(stream);
-    std::vector<int32_t> host((ix.span + 3) / 4);
-    hipError_t e = hipMemcpyAsync(host.data(), idx->data, ix.span, hipMemcpyDeviceToHost, hs);
-    if (e == hipSuccess) e = hipStreamSynchronize(hs);
-    if (e != hipSuccess) return hip_fail(e, "copying the indices to the host");
+    const int32_t *hp = idx->data;
+    if (!idx->on_host) {
+        void *stage = nullptr;
+        st = staging_for(hs, ix.span, &stage);
+        if (st != EMEL_OK) return st;
+        hipError_t e = hipMemcpyAsync(stage, idx->data, ix.span, hipMemcpyDeviceToHost, hs);
+        if (e == hipSuccess) e = hipStreamSynchronize(hs);
+        if (e != hipSuccess) return hip_fail(e, "copying the indices to the host");
+        hp = static_cast<const int32_t *>(stage);
+    }
     const uint64_t es[3] = {ix.st[0] / 4, ix.st[1] / 4, ix.st[2] / 4};
+    std::vector<int32_t> compact;
+    if (idx->on_host) compact.resize(n);
     for (uint64_t k = 0; k < n; ++k) {
         const uint64_t i0 = k % idx->ne[0], rem = k / idx->ne[0];
         const uint64_t i1 = rem % idx->ne[1], i2 = rem / idx->ne[1];
-        const int32_t row = host[i0 * es[0] + i1 * es[1] + i2 * es[2]];
+        const int32_t row = hp[i0 * es[0] + i1 * es[1] + i2 * es[2]];
         if (row < 0 || static_cast<uint64_t>(row) >= s.ne[1])
             return fail(EMEL_ERR_INDEX_OUT_OF_BOUNDS, "get_rows index " + std::to_string(row) + " at ordinal " +
                                                           std::to_string(k) + " is outside the source rows");
+        if (idx->on_host) compact[k] = row;
     }
     emel::GetRowsArgs a{};
     switch (kind) {
@@ -1229,15 +1266,33 @@ emel_status get_rows(GrKind kind, const emel_tensor_view *src, const emel_index_
         a.src_ne[d] = s.ne[d];
         a.src_st[d] = static_cast<int64_t>(s.ne[d] > 1 ? stv[d] : 0); // a singleton's stride never moves
     }
-    a.idx = idx->data;
-    for (int d = 0; d < 3; ++d) {
-        a.idx_ne[d] = idx->ne[d];
-        a.idx_st[d] = static_cast<int64_t>(idx->ne[d] > 1 ? es[d] : 0);
-    }
+    for (int d = 0; d < 3; ++d) a.idx_ne[d] = idx->ne[d];
     a.dst = static_cast<float *>(dst->data);
     a.rows = n;
     a.cols = s.ne[0];
-    return launched(emel::launch_get_rows(a, hs));
+    if (!idx->on_host) {
+        a.idx = idx->data;
+        for (int d = 0; d < 3; ++d) a.idx_st[d] = static_cast<int64_t>(idx->ne[d] > 1 ? es[d] : 0);
+        return launched(emel::launch_get_rows(a, nullptr, hs));
+    }
+    if (n <= emel::kInlineIndices && emel::get_rows_row_kernels(a)) {
+        emel::IdxInline ii{};
+        std::memcpy(ii.v, compact.data(), n * sizeof(int32_t));
+        return launched(emel::launch_get_rows(a, &ii, hs));
+    }
+    // More indices than the arguments carry: upload the checked values in
+    // ordinal order and read them row-major.
+    void *ws = nullptr;
+    st = workspace_for(hs, n * sizeof(int32_t), &ws);
+    if (st != EMEL_OK) return st;
+    hipError_t e = hipMemcpyAsync(ws, compact.data(), n * sizeof(int32_t), hipMemcpyHostToDevice, hs);
+    if (e == hipSuccess) e = hipStreamSynchronize(hs); // the host vector goes away on return
+    if (e != hipSuccess) return hip_fail(e, "uploading the indices");
+    a.idx = static_cast<const int32_t *>(ws);
+    a.idx_st[0] = 1;
+    a.idx_st[1] = static_cast<int64_t>(idx->ne[0]);
+    a.idx_st[2] = static_cast<int64_t>(idx->ne[0] * idx->ne[1]);
+    return launched(emel::launch_get_rows(a, nullptr, hs));
 }
 
 } // namespace

@@ -5,9 +5,14 @@
 //
 // A pure gather: each output value is a copy or the decode of one packed
 // block, so the bound is HBM (read the selected rows, write the output).
-// One work item per output float4 (F32), per output value (F32 with a
-// misaligned row, F16, BF16), per 32-value block (Q4_0, Q8_0) or per
-// 64-value quarter block (Q4_K); items are walked grid-stride.
+//   k_gr_row_*  one workgroup per destination row (and per 4096-float4 chunk
+//               of very wide rows): the row's index is a uniform load, and
+//               each lane produces one float4 of output per step: 128-bit
+//               loads for F32 / F16 / BF16 rows, 16-bit (Q4_0, Q8_0) or
+//               32-bit (Q4_K) loads for packed blocks.  Indices come from
+//               device memory or from the launch arguments (host-checked).
+//   k_rows_*    the fallback for misaligned or odd-width rows: one work item
+//               per value (per block for packed rows), grid-stride.
 #include "common.hpp"
 #include "launch.hpp"
 #include "libm_replica.hpp"
@@ -34,6 +39,36 @@ __device__ __forceinline__ RowRef row_ref(const GetRowsArgs &a, uint64_t r)
     const uint64_t i2 = rem / a.idx_ne[1];
     const int32_t v = a.idx[static_cast<int64_t>(i0) * a.idx_st[0] + static_cast<int64_t>(i1) * a.idx_st[1] +
                             static_cast<int64_t>(i2) * a.idx_st[2]];
+    return RowRef{static_cast<uint64_t>(static_cast<uint32_t>(v)), i1, i2};
+}
+
+// Index sources of the one-workgroup-per-row kernels: device memory read
+// through the index strides, or the host-checked values in the arguments.
+struct IdxDevice {
+    __device__ __forceinline__ int32_t get(const GetRowsArgs &a, uint64_t, uint64_t i0, uint64_t i1,
+                                           uint64_t i2) const
+    {
+        return a.idx[static_cast<int64_t>(i0) * a.idx_st[0] + static_cast<int64_t>(i1) * a.idx_st[1] +
+                     static_cast<int64_t>(i2) * a.idx_st[2]];
+    }
+};
+
+struct IdxArgs {
+    IdxInline ix;
+    __device__ __forceinline__ int32_t get(const GetRowsArgs &, uint64_t r, uint64_t, uint64_t, uint64_t) const
+    {
+        return ix.v[r];
+    }
+};
+
+template <class IX>
+__device__ __forceinline__ RowRef row_ref_ix(const GetRowsArgs &a, const IX &src, uint64_t r)
+{
+    const uint64_t i0 = r % a.idx_ne[0];
+    const uint64_t rem = r / a.idx_ne[0];
+    const uint64_t i1 = rem % a.idx_ne[1];
+    const uint64_t i2 = rem / a.idx_ne[1];
+    const int32_t v = src.get(a, r, i0, i1, i2);
     return RowRef{static_cast<uint64_t>(static_cast<uint32_t>(v)), i1, i2};
 }
 
@@ -229,6 +264,170 @@ __global__ __launch_bounds__(kBlock) void k_rows_q4k(GetRowsArgs a, uint64_t ite
     }
 }
 
+// ---- one workgroup per destination row ----------------------------------------------
+// The row's index is then a uniform (scalar) load, and the row streams with
+// one 128-bit store per lane per step.  blockIdx.y splits very wide rows
+// into chunks of kGrChunk float4.
+
+constexpr uint32_t kGrBlock = 256;
+constexpr uint64_t kGrChunk = 4096; // float4 per (row, chunk) workgroup
+
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint4 ld_nt_u4(const void *p)
+{
+    const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// hardware widening (exact for every non-NaN half), NaN payloads kept as the
+// reference's bit-level conversion does
+__device__ __forceinline__ float f16_exact(uint32_t h)
+{
+    const float w = hw_fp16_to_f32(static_cast<uint16_t>(h));
+    const bool nan = (h & 0x7c00u) == 0x7c00u && (h & 0x3ffu) != 0;
+    return nan ? bits_to_f32(((h & 0x8000u) << 16) | 0x7f800000u | ((h & 0x3ffu) << 13)) : w;
+}
+
+struct RowSpan {
+    uint64_t r, v0, v1; // destination row, float4 range [v0, v1)
+};
+
+__device__ __forceinline__ RowSpan row_span(uint64_t n4)
+{
+    const uint64_t v0 = static_cast<uint64_t>(blockIdx.y) * kGrChunk;
+    const uint64_t v1 = v0 + kGrChunk < n4 ? v0 + kGrChunk : n4;
+    return RowSpan{blockIdx.x, v0, v1};
+}
+
+// F32, 16-byte aligned row bases, cols % 4 == 0.
+template <class IX>
+__global__ __launch_bounds__(kGrBlock) void k_gr_row_f32(GetRowsArgs a, IX ix)
+{
+    const uint64_t n4 = a.cols / 4;
+    const RowSpan sp = row_span(n4);
+    const RowRef rr = row_ref_ix(a, ix, sp.r);
+    const float4 *src = reinterpret_cast<const float4 *>(static_cast<const char *>(a.src) + row_base(a, rr));
+    float4 *dst = reinterpret_cast<float4 *>(a.dst) + sp.r * n4;
+    uint64_t v = sp.v0 + threadIdx.x;
+    for (; v + 3 * kGrBlock < sp.v1; v += 4 * kGrBlock) {
+        const float4 x0 = ld_nt(src + v), x1 = ld_nt(src + v + kGrBlock);
+        const float4 x2 = ld_nt(src + v + 2 * kGrBlock), x3 = ld_nt(src + v + 3 * kGrBlock);
+        dst[v] = x0;
+        dst[v + kGrBlock] = x1;
+        dst[v + 2 * kGrBlock] = x2;
+        dst[v + 3 * kGrBlock] = x3;
+    }
+    for (; v < sp.v1; v += kGrBlock) dst[v] = ld_nt(src + v);
+}
+
+// F16 / BF16 with unit element stride, 16-byte aligned row bases, cols % 8 == 0:
+// eight halves per lane per step, widened, two 128-bit stores.
+template <bool BF16, class IX>
+__global__ __launch_bounds__(kGrBlock) void k_gr_row_half(GetRowsArgs a, IX ix)
+{
+    const uint64_t n4 = a.cols / 4;
+    const RowSpan sp = row_span(n4);
+    const RowRef rr = row_ref_ix(a, ix, sp.r);
+    const char *src = static_cast<const char *>(a.src) + row_base(a, rr);
+    float4 *dst = reinterpret_cast<float4 *>(a.dst) + sp.r * n4;
+    // the chunk bounds are even numbers of float4, so pairs never straddle one
+    for (uint64_t p = sp.v0 / 2 + threadIdx.x; 2 * p < sp.v1; p += kGrBlock) {
+        const uint4 h = ld_nt_u4(src + 16 * p);
+        const uint32_t w[4] = {h.x, h.y, h.z, h.w};
+        float f[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if constexpr (BF16) {
+                f[2 * i] = bits_to_f32(w[i] << 16);
+                f[2 * i + 1] = bits_to_f32(w[i] & 0xffff0000u);
+            } else {
+                f[2 * i] = f16_exact(w[i] & 0xffffu);
+                f[2 * i + 1] = f16_exact(w[i] >> 16);
+            }
+        }
+        dst[2 * p] = make_float4(f[0], f[1], f[2], f[3]);
+        dst[2 * p + 1] = make_float4(f[4], f[5], f[6], f[7]);
+    }
+}
+
+__device__ __forceinline__ uint32_t ld_u32_via_u16(const unsigned char *p)
+{
+    const uint16_t *q = reinterpret_cast<const uint16_t *>(p);
+    return static_cast<uint32_t>(q[0]) | (static_cast<uint32_t>(q[1]) << 16);
+}
+
+// Packed rows, one float4 of output per lane: Q8_0 / Q4_0 blocks give 8
+// float4 (lane j of a block reads quant bytes 4(j&3).. with two 16-bit loads,
+// the table base being 2-byte aligned); Q4_K blocks give 64 float4 (32-bit
+// loads, the table base being 4-byte aligned).
+template <RowSrc K, class IX>
+__global__ __launch_bounds__(kGrBlock) void k_gr_row_q(GetRowsArgs a, IX ix)
+{
+    const uint64_t n4 = a.cols / 4;
+    const RowSpan sp = row_span(n4);
+    const RowRef rr = row_ref_ix(a, ix, sp.r);
+    const uint64_t row = (rr.i2 * a.src_ne[2] + rr.i1) * a.src_ne[1] + rr.index;
+    float4 *dst = reinterpret_cast<float4 *>(a.dst) + sp.r * n4;
+    if constexpr (K == RowSrc::Q8_0 || K == RowSrc::Q4_0) {
+        constexpr uint64_t kBytes = K == RowSrc::Q8_0 ? kQ80Bytes : kQ40Bytes;
+        const unsigned char *base = static_cast<const unsigned char *>(a.src) + row * (a.cols / kQBlock) * kBytes;
+        for (uint64_t v = sp.v0 + threadIdx.x; v < sp.v1; v += kGrBlock) {
+            const uint64_t b = v / 8;
+            const uint32_t j = static_cast<uint32_t>(v % 8);
+            const unsigned char *blk = base + b * kBytes;
+            const float d = hw_fp16_to_f32(*reinterpret_cast<const uint16_t *>(blk));
+            float4 o;
+            if constexpr (K == RowSrc::Q8_0) {
+                const uint32_t q = ld_u32_via_u16(blk + 2 + 4 * j);
+                o.x = static_cast<float>(static_cast<int8_t>(q & 0xffu)) * d;
+                o.y = static_cast<float>(static_cast<int8_t>((q >> 8) & 0xffu)) * d;
+                o.z = static_cast<float>(static_cast<int8_t>((q >> 16) & 0xffu)) * d;
+                o.w = static_cast<float>(static_cast<int8_t>(q >> 24)) * d;
+            } else {
+                const uint32_t q = ld_u32_via_u16(blk + 2 + 4 * (j & 3u));
+                const uint32_t s = j < 4 ? 0u : 4u; // low nibbles for outputs 0..15, high for 16..31
+                o.x = (static_cast<float>((q >> s) & 0xfu) - 8.0f) * d;
+                o.y = (static_cast<float>((q >> (8 + s)) & 0xfu) - 8.0f) * d;
+                o.z = (static_cast<float>((q >> (16 + s)) & 0xfu) - 8.0f) * d;
+                o.w = (static_cast<float>((q >> (24 + s)) & 0xfu) - 8.0f) * d;
+            }
+            dst[v] = o;
+        }
+    } else {
+        const unsigned char *base = static_cast<const unsigned char *>(a.src) + row * (a.cols / kQ4KValues) * kQ4KBytes;
+        for (uint64_t v = sp.v0 + threadIdx.x; v < sp.v1; v += kGrBlock) {
+            const uint64_t b = v / 64;
+            const uint32_t k = static_cast<uint32_t>(v % 64);
+            const uint32_t q = k / 16, t = k % 16;
+            const unsigned char *blk = base + b * kQ4KBytes;
+            const uint32_t *w = reinterpret_cast<const uint32_t *>(blk);
+            const uint32_t hdr = w[0];
+            const uint32_t sw[3] = {w[1], w[2], w[3]}; // the 12 scale bytes
+            auto sbyte = [&](uint32_t i) { return (sw[i >> 2] >> (8 * (i & 3u))) & 0xffu; };
+            const uint32_t sj = 2 * q + (t < 8 ? 0u : 1u);
+            uint32_t sc, mn;
+            if (sj < 4) {
+                sc = sbyte(sj) & 0x3fu;
+                mn = sbyte(sj + 4) & 0x3fu;
+            } else {
+                sc = (sbyte(sj + 4) & 0x0fu) | ((sbyte(sj - 4) >> 6) << 4);
+                mn = (sbyte(sj + 4) >> 4) | ((sbyte(sj) >> 6) << 4);
+            }
+            const float dx = hw_fp16_to_f32(static_cast<uint16_t>(hdr & 0xffffu)) * static_cast<float>(sc);
+            const float mx = hw_fp16_to_f32(static_cast<uint16_t>(hdr >> 16)) * static_cast<float>(mn);
+            const uint32_t qw = w[(16 + 32 * q + 4 * (t & 7u)) / 4];
+            const uint32_t s = t < 8 ? 0u : 4u;
+            float4 o;
+            o.x = dx * static_cast<float>((qw >> s) & 0xfu) - mx;
+            o.y = dx * static_cast<float>((qw >> (8 + s)) & 0xfu) - mx;
+            o.z = dx * static_cast<float>((qw >> (16 + s)) & 0xfu) - mx;
+            o.w = dx * static_cast<float>((qw >> (24 + s)) & 0xfu) - mx;
+            dst[v] = o;
+        }
+    }
+}
+
 uint32_t grid_for(uint64_t items)
 {
     uint64_t blocks = (items + kBlock - 1) / kBlock;
@@ -239,12 +438,70 @@ uint32_t grid_for(uint64_t items)
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+enum class RowKernel { None, F32, F16, Bf16, Q4_0, Q8_0, Q4K };
+
+// The one-workgroup-per-row kernel for these arguments, if its alignment
+// and size conditions hold.
+RowKernel row_kernel(const GetRowsArgs &a)
+{
+    const uint64_t n4 = a.cols / 4;
+    const uint64_t chunks = (n4 + kGrChunk - 1) / kGrChunk;
+    if (!(a.rows >= 1 && a.rows <= 0x7fffffffull && chunks >= 1 && chunks <= 65535 && a.cols % 4 == 0 &&
+          aligned16(a.dst)))
+        return RowKernel::None;
+    auto rows16 = [&]() {
+        if (!aligned16(a.src)) return false;
+        for (int d = 1; d < 4; ++d)
+            if (a.src_st[d] % 16 != 0) return false;
+        return true;
+    };
+    const uintptr_t sp = reinterpret_cast<uintptr_t>(a.src);
+    switch (a.kind) {
+    case RowSrc::F32: return rows16() ? RowKernel::F32 : RowKernel::None;
+    case RowSrc::F16:
+    case RowSrc::Bf16:
+        if (a.cols % 8 == 0 && a.src_st[0] == 2 && rows16())
+            return a.kind == RowSrc::F16 ? RowKernel::F16 : RowKernel::Bf16;
+        return RowKernel::None;
+    case RowSrc::Q4_0: return (sp & 1u) == 0 ? RowKernel::Q4_0 : RowKernel::None;
+    case RowSrc::Q8_0: return (sp & 1u) == 0 ? RowKernel::Q8_0 : RowKernel::None;
+    case RowSrc::Q4K: return (sp & 3u) == 0 ? RowKernel::Q4K : RowKernel::None;
+    default: return RowKernel::None;
+    }
+}
+
+template <class IX>
+hipError_t launch_row_kernel(RowKernel k, const GetRowsArgs &a, const IX &ix, hipStream_t s)
+{
+    const uint64_t chunks = (a.cols / 4 + kGrChunk - 1) / kGrChunk;
+    const dim3 grid(static_cast<uint32_t>(a.rows), static_cast<uint32_t>(chunks));
+    switch (k) {
+    case RowKernel::F32: k_gr_row_f32<IX><<<grid, kGrBlock, 0, s>>>(a, ix); break;
+    case RowKernel::F16: k_gr_row_half<false, IX><<<grid, kGrBlock, 0, s>>>(a, ix); break;
+    case RowKernel::Bf16: k_gr_row_half<true, IX><<<grid, kGrBlock, 0, s>>>(a, ix); break;
+    case RowKernel::Q4_0: k_gr_row_q<RowSrc::Q4_0, IX><<<grid, kGrBlock, 0, s>>>(a, ix); break;
+    case RowKernel::Q8_0: k_gr_row_q<RowSrc::Q8_0, IX><<<grid, kGrBlock, 0, s>>>(a, ix); break;
+    case RowKernel::Q4K: k_gr_row_q<RowSrc::Q4K, IX><<<grid, kGrBlock, 0, s>>>(a, ix); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 } // namespace
 
-hipError_t launch_get_rows(const GetRowsArgs &a, hipStream_t s)
+bool get_rows_row_kernels(const GetRowsArgs &a) { return row_kernel(a) != RowKernel::None; }
+
+hipError_t launch_get_rows(const GetRowsArgs &a, const IdxInline *inline_idx, hipStream_t s)
 {
     if (a.rows == 0 || a.cols == 0) return hipSuccess;
+    const RowKernel rk = row_kernel(a);
+    if (inline_idx) {
+        if (rk == RowKernel::None || a.rows > kInlineIndices) return hipErrorInvalidValue;
+        return launch_row_kernel(rk, a, IdxArgs{*inline_idx}, s);
+    }
+    if (rk != RowKernel::None) return launch_row_kernel(rk, a, IdxDevice{}, s);
     const bool dst16 = aligned16(a.dst);
+
     switch (a.kind) {
     case RowSrc::F32: {
         // Every row base 16-byte aligned: the base pointer and the strides of

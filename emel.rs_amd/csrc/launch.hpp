@@ -167,6 +167,17 @@ struct GetRowsArgs {
     uint64_t cols;        // src.ne[0]
 };
 
-hipError_t launch_get_rows(const GetRowsArgs &args, hipStream_t stream);
+// Host-checked indices carried in the launch arguments (destination row r
+// reads v[r]); matches EMEL_GET_ROWS_INLINE_INDICES.
+constexpr uint32_t kInlineIndices = 512;
+struct IdxInline {
+    int32_t v[kInlineIndices];
+};
+
+// Whether launch_get_rows takes the one-workgroup-per-row kernels for these
+// arguments (the only ones that read inline indices).
+bool get_rows_row_kernels(const GetRowsArgs &args);
+// inline_idx: NULL reads args.idx from device memory.
+hipError_t launch_get_rows(const GetRowsArgs &args, const IdxInline *inline_idx, hipStream_t stream);
 
 } // namespace emel

@@ -232,7 +232,7 @@ class CIndexView(ctypes.Structure):
         ("ne", ctypes.c_uint64 * 3),
         ("nb", ctypes.c_uint64 * 3),
         ("explicit_strides", ctypes.c_uint32),
-        ("reserved", ctypes.c_uint32),
+        ("on_host", ctypes.c_uint32),
     ]
 
 

@@ -20,19 +20,32 @@ from .views import TensorView, TensorViewMut
 
 
 class IndexView:
-    """An int32 index tensor with three extents (get_rows.rs:42-196)."""
+    """An int32 index tensor with three extents (get_rows.rs:42-196).
 
-    def __init__(self, data, ne, nb=None, length: int | None = None):
+    data is a numpy int32 array or a CPU tensor (host memory: checked in
+    place and passed to the kernel by value), a GPU tensor (device memory:
+    copied back once for the check), or a raw pointer with `length` and
+    `on_host`."""
+
+    def __init__(self, data, ne, nb=None, length: int | None = None, on_host: bool | None = None):
         self._keep = data
         if isinstance(data, int):
-            if length is None:
-                raise ValueError("a raw device pointer needs its length in int32 elements")
+            if length is None or on_host is None:
+                raise ValueError("a raw pointer needs its length in int32 elements and its location")
             self.ptr = data
             self.len = int(length)
-        else:
+            self.on_host = bool(on_host)
+        elif hasattr(data, "__array_interface__"):  # numpy
+            if data.dtype.name != "int32" or not data.flags["C_CONTIGUOUS"]:
+                raise ValueError("host indices are a C-contiguous int32 array")
+            self.ptr = int(data.__array_interface__["data"][0])
+            self.len = data.size if length is None else int(length)
+            self.on_host = True
+        else:  # torch tensor
             self.ptr = int(data.data_ptr())
             avail = int(data.untyped_storage().nbytes()) // 4 - int(data.storage_offset())
             self.len = avail if length is None else int(length)
+            self.on_host = not data.is_cuda
         self.ne = [int(x) for x in ne]
         self.nb = None if nb is None else [int(x) for x in nb]
         if len(self.ne) != 3 or (self.nb is not None and len(self.nb) != 3):
@@ -50,7 +63,7 @@ class IndexView:
             v.ne[d] = self.ne[d]
             v.nb[d] = 0 if self.nb is None else self.nb[d]
         v.explicit_strides = 0 if self.nb is None else 1
-        v.reserved = 0
+        v.on_host = 1 if self.on_host else 0
         return v
 
 

@@ -298,22 +298,27 @@ emel_status emel_op_argmax_rows(const emel_tensor_view *src, const emel_tensor_v
  * three extents, byte strides.  explicit_strides == 0 is IndexView::new
  * (row-major); 1 is IndexView::with_strides (nb[0] == 0 still selects
  * row-major).  len counts int32 elements at data (the Rust slice length).
- * data is a device pointer like every view's.
  *
  * The reference checks every index against the source row count before
- * writing anything.  To keep that contract, a call whose views and shapes
- * pass copies the index span to the host on `stream` and waits for it
- * (the only entry points that synchronise; they cannot be captured into a
- * HIP graph).  Statuses: INVALID_VIEW, SHAPE_MISMATCH,
- * UNSUPPORTED_SOURCE_STRIDE (F32 only), INDEX_OUT_OF_BOUNDS, in the
- * reference's guard order. */
+ * writing anything, and so does every call here, on the host:
+ *   on_host == 1: data is host memory, as the reference's &[i32] is.  The
+ *     indices are checked in place; up to EMEL_GET_ROWS_INLINE_INDICES of
+ *     them then travel to the kernel inside its launch arguments (the call
+ *     is asynchronous and can be captured into a HIP graph, which then
+ *     replays the indices it was captured with); more are uploaded, and the
+ *     call waits for that copy.
+ *   on_host == 0: data is device memory.  The call copies the index span
+ *     to the host on `stream` and waits for it before checking.
+ * Statuses: INVALID_VIEW, SHAPE_MISMATCH, UNSUPPORTED_SOURCE_STRIDE (F32
+ * only), INDEX_OUT_OF_BOUNDS, in the reference's guard order. */
+#define EMEL_GET_ROWS_INLINE_INDICES 512u
 typedef struct emel_index_view {
     const int32_t *data;
     uint64_t len;     /* int32 elements at data */
     uint64_t ne[3];
     uint64_t nb[3];   /* byte strides (explicit_strides == 1) */
     uint32_t explicit_strides;
-    uint32_t reserved; /* must be 0 */
+    uint32_t on_host; /* 1: data is host memory; 0: device memory */
 } emel_index_view;
 
 /* F32 source: rows located by nb[1..3]; each row copies ne0 contiguous

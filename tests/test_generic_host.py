@@ -367,6 +367,7 @@ def test_get_rows_classification_matches_the_oracle():
             ci.ne[d] = ine[d]
             ci.nb[d] = 0 if inb is None else inb[d]
         ci.explicit_strides = 0 if inb is None else 1
+        ci.on_host = int(trial % 2)  # host-resident and device-resident indices classify alike before the check
         got = getattr(lib, fn)(ctypes.byref(cs), ctypes.byref(ci), ctypes.byref(cd), None)
         expect = KERNEL_UNAVAILABLE if want in (OK, orc.INDEX_OUT_OF_BOUNDS) else want
         assert got == expect, (trial, kind, want, got, sne, snb, ine, inb, idx_len, dne, dnb, src_bytes)

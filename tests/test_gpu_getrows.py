@@ -40,7 +40,7 @@ class Gather:
         self.kernel = eh.Kernel()
 
     def __call__(self, kind, src, sne, snb, sdtype, idx, ine, inb=None, dne=None, fill=9.0, src_bytes=None,
-                 compare=True):
+                 compare=True, offset=0):
         torch = self.torch
         print(f"get_rows kind={kind} src ne={sne} nb={snb} idx ne={ine} nb={inb}", flush=True)
         dne = dne if dne is not None else [sne[0], ine[0], ine[1], ine[2]]
@@ -50,7 +50,10 @@ class Gather:
         sbytes = src.nbytes if src_bytes is None else src_bytes
         want = orc.get_rows(kind, orc.view(src, sne, snb, sdtype, sbytes), orc.index_view(idx, ine, inb),
                             orc.view(host_out, dne, dense(dne), F32, 4 * count))
-        dsrc = torch.from_numpy(src.view(np.uint8).copy()).to(self.gpu)
+        # offset: the table starts that many bytes into its allocation (misaligned bases)
+        raw = np.zeros(src.nbytes + 16, np.uint8)
+        raw[offset:offset + src.nbytes] = src.view(np.uint8)
+        dsrc = torch.from_numpy(raw).to(self.gpu)[offset:]
         didx = torch.from_numpy(idx.copy() if idx.size else np.zeros(1, np.int32)).to(self.gpu)
         dout = torch.full((max(count, 1),), fill, dtype=torch.float32, device=self.gpu)
         ev = EVENTS[kind](eh.TensorView(dsrc, eh.Layout(sdtype, sne, snb), sbytes),
@@ -61,6 +64,15 @@ class Gather:
         if compare:
             assert int(got) == want, (kind, want, got, eh.last_error())
             assert_bits_equal(result, host_out[:count], f"get_rows kind {kind}")
+            # the same request with host-resident indices (checked in place, passed by value or uploaded)
+            dout.fill_(fill)
+            hidx = idx.copy() if idx.size else np.zeros(1, np.int32)
+            ev = EVENTS[kind](eh.TensorView(dsrc, eh.Layout(sdtype, sne, snb), sbytes),
+                              eh.IndexView(hidx, ine, inb, length=idx.size),
+                              eh.TensorViewMut(dout, eh.Layout(F32, dne, dense(dne)), 4 * count))
+            got_h = self.kernel.process_event(ev)
+            assert int(got_h) == want, (kind, "host indices", want, got_h, eh.last_error())
+            assert_bits_equal(dout.cpu().numpy()[:count], host_out[:count], f"get_rows kind {kind}, host indices")
         return want, got, result
 
 
@@ -187,3 +199,27 @@ def test_rejections_and_empty_indices(gather):
     want, got, out = gather(orc.GR_Q4_0, random_packed(1, Q4_0, [32, 2, 1, 1]), [32, 2, 1, 1], [2, 18, 36, 36],
                             Q4_0, [0], [1, 1, 1], compare=False)
     assert want == orc.INVALID_VIEW and got == eh.Status.INVALID_VIEW and (out == 9.0).all()
+
+
+def test_misaligned_tables_take_the_element_kernels(gather):
+    g = rng(15)
+    for kind, code in ((orc.GR_Q4_0, Q4_0), (orc.GR_Q8_0, Q8_0), (orc.GR_Q4_K, Q4_K)):
+        sne = [PACK[code][0] * 2, 20, 1, 1]
+        src = random_packed(30 + code, code, sne)
+        for off in (1, 2):
+            gather(kind, src, sne, packed_nb(code, sne), code, g.integers(0, 20, 9).astype(np.int32), [9, 1, 1],
+                   offset=off)
+    sne = [64, 20, 1, 1]
+    h = g.integers(0, 65536, 64 * 20, dtype=np.uint32).astype(np.uint16)
+    gather(orc.GR_F16, h, sne, dense(sne, 2), F16, g.integers(0, 20, 9).astype(np.int32), [9, 1, 1], offset=2)
+    f = g.standard_normal(64 * 20).astype(np.float32)
+    gather(orc.GR_F32, f, sne, dense(sne), F32, g.integers(0, 20, 9).astype(np.int32), [9, 1, 1], offset=4)
+
+
+def test_more_host_indices_than_the_arguments_carry(gather):
+    g = rng(16)
+    sne = [256, 1000, 1, 1]
+    for kind, code, src in ((orc.GR_F32, F32, f32_table(17, sne)),
+                            (orc.GR_Q4_K, Q4_K, random_packed(18, Q4_K, sne))):
+        nb = dense(sne) if code == F32 else packed_nb(code, sne)
+        gather(kind, src, sne, nb, code, g.integers(0, 1000, 700).astype(np.int32), [700, 1, 1])
