@@ -505,6 +505,9 @@ const char *emel_status_string(emel_status s)
     case EMEL_ERR_INVALID_ARGUMENT: return "invalid argument";
     case EMEL_ERR_INVALID_SHAPE: return "invalid kernel shape";
     case EMEL_ERR_UNSUPPORTED_OPERATION: return "unsupported operation";
+    case EMEL_ERR_INDEX_OUT_OF_BOUNDS: return "index out of bounds";
+    case EMEL_ERR_UNSUPPORTED_SOURCE_STRIDE: return "unsupported source stride";
+    case EMEL_ERR_INVALID_REQUEST: return "invalid request";
     }
     return "unknown status";
 }
@@ -1928,4 +1931,170 @@ emel_status emel_generic_dispatch(const emel_generic_request *request, emel_stre
         return fail(EMEL_ERR_INVALID_SHAPE, "the operation's maintained route rejects the request");
     if (valid) return fail(EMEL_ERR_UNSUPPORTED_OPERATION, "no maintained route for this operation");
     return fail(EMEL_ERR_INVALID_SHAPE, "the request failed validation");
+}
+
+// ---- emel-logits: native sampler and candidate validator --------------------------
+
+namespace {
+
+constexpr uint64_t kParkMillerModulus = 2147483647u; // sampler/sm.rs:22
+constexpr uint64_t kParkMillerMultiplier = 16807u;   // sampler/sm.rs:23
+
+// state * 16807^steps mod (2^31 - 1): the state after `steps` draws.
+uint32_t park_miller_advance(uint32_t state, uint64_t steps)
+{
+    uint64_t r = state % kParkMillerModulus, b = kParkMillerMultiplier;
+    while (steps) {
+        if (steps & 1) r = r * b % kParkMillerModulus;
+        b = b * b % kParkMillerModulus;
+        steps >>= 1;
+    }
+    return static_cast<uint32_t>(r);
+}
+
+struct ByteRange {
+    uintptr_t lo, hi;
+};
+ByteRange span_of(const void *p, uint64_t rows, uint64_t stride, uint64_t width, uint64_t elem)
+{
+    const uintptr_t lo = reinterpret_cast<uintptr_t>(p);
+    return ByteRange{lo, lo + ((rows - 1) * stride + width) * elem};
+}
+bool pairwise_disjoint(const ByteRange *r, int n)
+{
+    for (int i = 0; i < n; ++i)
+        for (int j = i + 1; j < n; ++j)
+            if (r[i].lo < r[j].hi && r[j].lo < r[i].hi) return false;
+    return true;
+}
+
+// rows of `width` elements, `stride` apart, inside a buffer of `len` elements
+bool rows_fit(uint64_t rows, uint64_t stride, uint64_t width, uint64_t len)
+{
+    if (rows > 1 && stride < width) return false; // rows of one call never share elements
+    const u128 need = static_cast<u128>(rows - 1) * stride + width;
+    return need <= len;
+}
+
+} // namespace
+
+emel_status emel_sample_temperature_top_k_rows(const emel_sample_temperature_top_k_request *req,
+                                               const emel_sample_rows *rows, emel_stream stream)
+{
+    if (!req || !rows) return fail(EMEL_ERR_INVALID_ARGUMENT, "null request");
+    if (req->reserved != 0) return fail(EMEL_ERR_INVALID_ARGUMENT, "reserved must be 0");
+    const uint64_t nrows = rows->rows;
+    if (nrows == 0 || nrows > 0xffffffffull) return fail(EMEL_ERR_INVALID_ARGUMENT, "row count outside [1, 2^32)");
+    if (!req->random_state) return fail(EMEL_ERR_INVALID_ARGUMENT, "null random_state");
+    const uint64_t card = req->card, top_k = req->top_k;
+    const float temperature = req->temperature;
+    // guard_temperature_valid (sampler/sm.rs:729-747), for every row
+    bool valid = card > 0 && top_k > 0 && top_k <= card && std::isfinite(temperature) && temperature > 0.0f &&
+                 rows_fit(nrows, rows->logits_stride, card, req->logits_len) &&
+                 rows_fit(nrows, rows->sorted_stride, card, req->sorted_indices_len) &&
+                 rows_fit(nrows, rows->top_stride, top_k, req->top_probabilities_len) &&
+                 rows_fit(nrows, rows->top_stride, top_k, req->top_indices_len);
+    for (uint64_t r = 0; valid && r < nrows; ++r) valid = req->random_state[r] % kParkMillerModulus != 0;
+    if (!valid) return fail(EMEL_ERR_INVALID_REQUEST, "sampler request failed its guard");
+    if (!req->logits || !req->sorted_indices || !req->top_probabilities || !req->top_indices ||
+        !req->selected_token_out || !req->selected_score_out)
+        return fail(EMEL_ERR_INVALID_ARGUMENT, "null buffer");
+    // limits of this implementation (indices are i32 in the reference's outputs)
+    if (card > 0x7fffffffull) return fail(EMEL_ERR_INVALID_ARGUMENT, "card beyond i32 indices");
+    const ByteRange spans[7] = {
+        span_of(req->logits, nrows, rows->logits_stride, card, 4),
+        span_of(req->sorted_indices, nrows, rows->sorted_stride, card, 4),
+        span_of(req->top_probabilities, nrows, rows->top_stride, top_k, 4),
+        span_of(req->top_indices, nrows, rows->top_stride, top_k, 4),
+        span_of(req->selected_token_out, nrows, 1, 1, 4),
+        span_of(req->selected_score_out, nrows, 1, 1, 4),
+        req->status_out ? span_of(req->status_out, nrows, 1, 1, 4) : ByteRange{0, 0},
+    };
+    if (!pairwise_disjoint(spans, req->status_out ? 7 : 6))
+        return fail(EMEL_ERR_INVALID_ARGUMENT, "sampler buffers overlap");
+    const uintptr_t misaligned = reinterpret_cast<uintptr_t>(req->logits) | reinterpret_cast<uintptr_t>(req->sorted_indices) |
+                                 reinterpret_cast<uintptr_t>(req->top_probabilities) |
+                                 reinterpret_cast<uintptr_t>(req->top_indices) |
+                                 reinterpret_cast<uintptr_t>(req->selected_token_out) |
+                                 reinterpret_cast<uintptr_t>(req->selected_score_out) |
+                                 reinterpret_cast<uintptr_t>(req->status_out);
+    if (misaligned & 3u) return fail(EMEL_ERR_INVALID_ARGUMENT, "sampler buffers must be 4-byte aligned");
+    emel_status s = ensure_device();
+    if (s != EMEL_OK) return s;
+    emel::SamplerArgs a{};
+    a.rows = static_cast<uint32_t>(nrows);
+    a.card = card;
+    a.top_k = static_cast<uint32_t>(top_k);
+    a.scale = 1.0f / temperature; // effect_scale_temperature (sm.rs:766), f32
+    a.logits = req->logits;
+    a.logits_ld = static_cast<int64_t>(rows->logits_stride);
+    a.sorted = req->sorted_indices;
+    a.sorted_ld = static_cast<int64_t>(rows->sorted_stride);
+    a.top_p = req->top_probabilities;
+    a.top_i = req->top_indices;
+    a.top_ld = static_cast<int64_t>(rows->top_stride);
+    a.selected = req->selected_token_out;
+    a.score = req->selected_score_out;
+    a.status = req->status_out;
+    a.states = req->random_state;
+    s = workspace_for(as_stream(stream), emel::sampler_workspace_bytes(a.rows, card, a.top_k), &a.workspace);
+    if (s != EMEL_OK) return s;
+    const hipError_t e = emel::launch_sampler(a, as_stream(stream));
+    if (e != hipSuccess) return hip_fail(e, "sampler launch");
+    // effect_select_top_k (sm.rs:821-847) leaves the state after top_k draws
+    for (uint64_t r = 0; r < nrows; ++r) req->random_state[r] = park_miller_advance(req->random_state[r], top_k);
+    return launched(hipSuccess);
+}
+
+emel_status emel_sample_temperature_top_k(const emel_sample_temperature_top_k_request *req, emel_stream stream)
+{
+    if (!req) return fail(EMEL_ERR_INVALID_ARGUMENT, "null request");
+    const emel_sample_rows one{1, req->card, req->card, req->top_k};
+    return emel_sample_temperature_top_k_rows(req, &one, stream);
+}
+
+emel_status emel_sample_preselected(uint64_t vocab_size, int32_t selected_token, int32_t *token_out)
+{
+    if (!token_out) return fail(EMEL_ERR_INVALID_ARGUMENT, "null output");
+    // guard_preselected_valid (sampler/sm.rs:685-695)
+    if (!(vocab_size > 0 && selected_token >= 0 && static_cast<uint64_t>(selected_token) < vocab_size))
+        return fail(EMEL_ERR_INVALID_REQUEST, "preselected token outside the vocabulary");
+    *token_out = selected_token;
+    g_last_error.clear();
+    return EMEL_OK;
+}
+
+emel_status emel_logits_validator_build(const float *logits, uint64_t logits_len, int32_t vocab_size,
+                                        int32_t *candidate_ids, uint64_t candidate_ids_len, float *candidate_scores,
+                                        uint64_t candidate_scores_len, int32_t candidate_capacity,
+                                        int32_t *candidate_count_out, int32_t *error_out, emel_stream stream)
+{
+    if (!candidate_count_out || !error_out) return fail(EMEL_ERR_INVALID_ARGUMENT, "null output");
+    // begin_build, then valid_request (validator/sm.rs)
+    *candidate_count_out = 0;
+    *error_out = EMEL_VALIDATOR_NONE;
+    const auto fits = [&](uint64_t len) { return len <= 0x7fffffffull && static_cast<int64_t>(len) >= vocab_size; };
+    if (!(vocab_size > 0 && candidate_capacity >= vocab_size && fits(logits_len) && fits(candidate_ids_len) &&
+          fits(candidate_scores_len))) {
+        *candidate_count_out = 0;
+        *error_out = EMEL_VALIDATOR_INVALID_REQUEST;
+        return fail(EMEL_ERR_INVALID_REQUEST, "validator request failed its guard");
+    }
+    if (!logits || !candidate_ids || !candidate_scores) return fail(EMEL_ERR_INVALID_ARGUMENT, "null buffer");
+    const uint64_t n = static_cast<uint64_t>(vocab_size);
+    const ByteRange spans[3] = {span_of(logits, 1, 0, n, 4), span_of(candidate_ids, 1, 0, n, 4),
+                                span_of(candidate_scores, 1, 0, n, 4)};
+    if (!pairwise_disjoint(spans, 3)) return fail(EMEL_ERR_INVALID_ARGUMENT, "validator buffers overlap");
+    if ((reinterpret_cast<uintptr_t>(logits) | reinterpret_cast<uintptr_t>(candidate_ids) |
+         reinterpret_cast<uintptr_t>(candidate_scores)) & 3u)
+        return fail(EMEL_ERR_INVALID_ARGUMENT, "validator buffers must be 4-byte aligned");
+    emel_status s = ensure_device();
+    if (s != EMEL_OK) return s;
+    void *ws = nullptr;
+    s = workspace_for(as_stream(stream), emel::validator_workspace_bytes(n), &ws);
+    if (s != EMEL_OK) return s;
+    const hipError_t e = emel::launch_validator(logits, n, candidate_ids, candidate_scores, ws, as_stream(stream));
+    if (e != hipSuccess) return hip_fail(e, "validator launch");
+    *candidate_count_out = vocab_size; // execute_build
+    return launched(hipSuccess);
 }

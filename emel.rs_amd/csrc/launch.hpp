@@ -180,4 +180,35 @@ bool get_rows_row_kernels(const GetRowsArgs &args);
 // inline_idx: NULL reads args.idx from device memory.
 hipError_t launch_get_rows(const GetRowsArgs &args, const IdxInline *inline_idx, hipStream_t stream);
 
+// ---- logits sampler and validator (sampler.hip) -------------------------------
+
+// rows independent SampleTemperatureTopK requests over row-strided buffers
+// (strides in elements); the host has checked every guard.
+struct SamplerArgs {
+    uint32_t rows;
+    uint64_t card;
+    uint32_t top_k;
+    float scale; // 1.0f / temperature
+    float *logits;
+    int64_t logits_ld;
+    int32_t *sorted;
+    int64_t sorted_ld;
+    float *top_p;
+    int32_t *top_i;
+    int64_t top_ld;
+    int32_t *selected;    // rows
+    float *score;         // rows
+    int32_t *status;      // rows, may be null: 0 or EMEL_ERR_INVALID_REQUEST (result guard)
+    const uint32_t *states; // host: rows start states
+    void *workspace;      // sampler_workspace_bytes
+};
+
+uint64_t sampler_workspace_bytes(uint32_t rows, uint64_t card, uint32_t top_k);
+hipError_t launch_sampler(const SamplerArgs &args, hipStream_t stream);
+
+// Validator Build: ids[i] = i and scores[i] = logits[i] - max for i < n.
+uint64_t validator_workspace_bytes(uint64_t n);
+hipError_t launch_validator(const float *logits, uint64_t n, int32_t *ids, float *scores, void *workspace,
+                            hipStream_t stream);
+
 } // namespace emel

@@ -17,6 +17,9 @@
 //                a degree-5 rational correction term, no contraction.
 //   emel_tanhf   fdlibm s_tanhf.c: tanh(x) = 1 - 2/(expm1(2|x|)+2) for
 //                |x| >= 1, -t/(t+2) with t = expm1(-2|x|) below.
+//   emel_logf    ARM optimized-routines logf (math/logf.c, in glibc since
+//                2.28): a 16-entry (1/c, log c) table and a cubic in
+//                r = z/c - 1, in double (emel-logits' sampler, f32::ln).
 //
 // The table holds the correctly rounded doubles of 2^(i/32).  glibc stores
 // them with i << 47 subtracted and forms 2^(k/32) as tab[k % 32] + (k << 47)
@@ -250,6 +253,60 @@ __host__ __device__ __forceinline__ float emel_tanhf(float x)
         z = 1.0f - 1.0e-30f; // 1 with inexact
     }
     return negative ? -z : z;
+}
+
+// logf, ARM optimized-routines design (math/logf.c, glibc's logf since
+// 2.28).  x = 2^k z with z in [0x1.66p-1, 0x1.66p0) (the offset 0x3f330000
+// centres the interval on 1); the top 4 mantissa bits of z pick one of 16
+// subintervals with a centre c, stored as invc ~ 1/c (chosen so that
+// z * invc - 1 is exact in double) and logc = log(c).  Then
+// log(x) = k ln2 + logc + log1p(r), r = z invc - 1, with log1p(r) ~ r + A2 r^2
+// + A1 r^3 + A0 r^4 (A0..A2 a minimax fit on the subinterval range),
+// evaluated in double and rounded once.  Special inputs: log(1) = 0 exactly,
+// log(+-0) = -inf, log(+inf) = +inf, negative or NaN -> NaN, subnormals are
+// normalised first.  The reference reaches it through Rust f32::ln
+// (emel-logits sampler.rs select step: -uniform.ln()).
+static constexpr double kLogfInvc[16] = {
+    0x1.661ec79f8f3bep+0, 0x1.571ed4aaf883dp+0, 0x1.49539f0f010bp+0,  0x1.3c995b0b80385p+0,
+    0x1.30d190c8864a5p+0, 0x1.25e227b0b8eap+0,  0x1.1bb4a4a1a343fp+0, 0x1.12358f08ae5bap+0,
+    0x1.0953f419900a7p+0, 0x1p+0,               0x1.e608cfd9a47acp-1, 0x1.ca4b31f026aap-1,
+    0x1.b2036576afce6p-1, 0x1.9c2d163a1aa2dp-1, 0x1.886e6037841edp-1, 0x1.767dcf5534862p-1,
+};
+static constexpr double kLogfLogc[16] = {
+    -0x1.57bf7808caadep-2, -0x1.2bef0a7c06ddbp-2, -0x1.01eae7f513a67p-2, -0x1.b31d8a68224e9p-3,
+    -0x1.6574f0ac07758p-3, -0x1.1aa2bc79c81p-3,   -0x1.a4e76ce8c0e5ep-4, -0x1.1973c5a611cccp-4,
+    -0x1.252f438e10c1ep-5, 0x0p+0,                0x1.aa5aa5df25984p-5,  0x1.c5e53aa362eb4p-4,
+    0x1.526e57720db08p-3,  0x1.bc2860d22477p-3,   0x1.1058bc8a07ee1p-2,  0x1.4043057b6ee09p-2,
+};
+
+__host__ __device__ __forceinline__ float emel_logf(float x)
+{
+    constexpr double kA0 = -0x1.00ea348b88334p-2;
+    constexpr double kA1 = 0x1.5575b0be00b6ap-2;
+    constexpr double kA2 = -0x1.ffffef20a4123p-2;
+    constexpr double kLn2 = 0x1.62e42fefa39efp-1;
+    uint32_t ix = f32_to_bits(x);
+    if (ix == 0x3f800000u) return 0.0f;
+    if (ix - 0x00800000u >= 0x7f800000u - 0x00800000u) {
+        // below the normal range, infinite or NaN
+        if (ix * 2u == 0u) return -__builtin_inff();
+        if (ix == 0x7f800000u) return x;
+        if ((ix & 0x80000000u) || ix * 2u >= 0xff000000u) return (x - x) / (x - x);
+        ix = f32_to_bits(x * 0x1p23f); // subnormal: normalise
+        ix -= 23u << 23;
+    }
+    const uint32_t tmp = ix - 0x3f330000u;
+    const uint32_t i = (tmp >> (23 - 4)) % 16u;
+    const int32_t k = static_cast<int32_t>(tmp) >> 23;
+    const uint32_t iz = ix - (tmp & (0x1ffu << 23));
+    const double z = static_cast<double>(bits_to_f32(iz));
+    const double r = z * kLogfInvc[i] - 1.0;
+    const double y0 = kLogfLogc[i] + static_cast<double>(k) * kLn2;
+    const double r2 = r * r;
+    double y = kA1 * r + kA2;
+    y = kA0 * r2 + y;
+    y = y * r2 + (y0 + r);
+    return static_cast<float>(y);
 }
 
 // fp32 -> binary16 bits with the reference helper's arithmetic

@@ -1,0 +1,985 @@
+// sampler.hip -- gfx950 kernels for emel-logits' native temperature/top-k
+// sampler (Sampler::sample_temperature_top_k, crates/emel-logits/src/
+// sampler/sm.rs:380-392, effects :759-847) and its candidate validator
+// (Validator::process_event(Build), crates/emel-logits/src/validator/sm.rs).
+//
+// A request is one row of `card` logits; a launch serves `rows` independent
+// requests.  Per row, as the reference computes it:
+//   v = x * (1/T)                          (f32, in place)
+//   m = max over v, NaN ignored            (f32::max fold from -inf)
+//   e = expf(v - m)                        (glibc expf, in place)
+//   S = e_0 + e_1 + ... sequentially, f32  (the rounding of every step kept)
+//   p = e / S                              (in place: the caller's logits end as p)
+//   rank by p descending (f32::total_cmp), keep the first top_k
+//   race_j = p_j / -logf(u_j), u_j from the Park-Miller sequence; the first
+//   maximal race wins.
+//
+// Kernels, in launch order (the same sequence for every request; rows that
+// finish a stage early skip the later ones):
+//   k_smp_max     (row, chunk) workgroups: chunk maxima of v.
+//   k_smp_exp     (row, chunk): e written in place.
+//   k_smp_sum     one 1024-thread workgroup per row: the exact sequential sum
+//                 through integer units per binade (seqsum.hpp).
+//   k_smp_div     (row, chunk): p written in place, plus the histogram of the
+//                 top 11 bits of p's total-order key.
+//   k_smp_pick / k_smp_refine
+//                 radix selection of the top_k-th key: 11, 11, 10 key bits.
+//                 A row stops as soon as every key at or above its current
+//                 prefix fits the kCap candidates one workgroup sorts; at
+//                 32 bits the threshold key T is exact.
+//   k_smp_ties    (row, chunk): elements equal to T per chunk (exact rows).
+//   k_smp_collect (row, chunk): candidates (key, index) into a per-row list:
+//                 every key >= prefix, or every key > T plus the lowest-index
+//                 ties at T up to top_k.
+//   k_smp_rank    one workgroup per row: sort of the candidates in LDS
+//                 (bitonic, key descending then index ascending), the ranked
+//                 outputs, then the race selection.
+// Lists longer than kCap (top_k > kCap) are sorted as kCap tiles
+// (k_smp_tile_sort), merged pairwise (k_smp_merge), and finished by
+// k_smp_finish.
+//
+// Ties of p: the reference sorts with sort_unstable_by, which leaves the
+// order of equal probabilities unspecified; here they rank by ascending
+// index, the order the CPU oracle uses.
+#include <type_traits>
+
+#include "common.hpp"
+#include "launch.hpp"
+#include "libm_replica.hpp"
+#include "seqsum.hpp"
+
+namespace emel {
+namespace {
+
+constexpr uint32_t kCap = 8192;          // candidates sorted in LDS by one workgroup
+constexpr uint32_t kRankThreads = 1024;
+constexpr uint32_t kSumThreads = 1024;
+constexpr uint32_t kSumPer = 16;         // elements per thread and tile of k_smp_sum
+constexpr uint32_t kBins = 2048;         // 11-bit radix digits
+constexpr uint32_t kNone = 0xffffffffu;
+constexpr uint32_t kModulus = 2147483647u;   // sampler/sm.rs:22
+constexpr uint64_t kMultiplier = 16807u;     // sampler/sm.rs:23
+constexpr int32_t kInvalidRequest = 13;      // EMEL_ERR_INVALID_REQUEST
+
+// Per-row selection state (workspace).
+struct RowSel {
+    float total;      // the sequential sum S
+    uint32_t mode;    // 0 open, 1 collect keys >= prefix, 2 collect keys > T + ties
+    uint32_t prefix;  // resolved top `depth` bits of the key (T when depth == 32)
+    uint32_t depth;
+    uint32_t need;    // elements still to take from the prefix region
+    uint32_t above;   // elements whose key prefix is greater (all taken)
+    uint32_t count;   // candidates collected
+    uint32_t written; // collect cursor
+};
+
+struct SmpGeo {
+    uint32_t rows;
+    uint32_t chunks;
+    uint64_t card;
+    uint64_t chunk_cols; // multiple of 4
+    int64_t ld;          // logits row stride, elements
+    uint32_t vec;        // 16-byte aligned rows: float4 paths
+    uint32_t top_k;
+    float scale;
+    uint32_t cand_ld;    // candidate slots per row
+};
+
+struct SmpWs {
+    float *part;   // rows * chunks chunk maxima
+    RowSel *sel;   // rows
+    uint32_t *hist; // rows * kBins
+    uint32_t *ties; // rows * chunks
+    uint64_t *cand; // rows * cand_ld
+    uint64_t *cand2; // rows * cand_ld (merge ping-pong, top_k > kCap)
+};
+
+// f32::total_cmp as an unsigned key (larger key = later in total order).
+__device__ __forceinline__ uint32_t total_key(float f)
+{
+    const uint32_t b = f32_to_bits(f);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float from_key(uint32_t k)
+{
+    return bits_to_f32((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+// Sort word: key descending, then index ascending, as one descending u64.
+__device__ __forceinline__ uint64_t cand_word(uint32_t key, uint32_t idx)
+{
+    return (static_cast<uint64_t>(key) << 32) | static_cast<uint64_t>(~idx);
+}
+
+__device__ __forceinline__ uint32_t mulmod(uint32_t a, uint32_t b)
+{
+    return static_cast<uint32_t>((static_cast<uint64_t>(a) * b) % kModulus);
+}
+__device__ __forceinline__ uint32_t powmod(uint64_t e)
+{
+    uint32_t r = 1, b = static_cast<uint32_t>(kMultiplier);
+    while (e) {
+        if (e & 1) r = mulmod(r, b);
+        b = mulmod(b, b);
+        e >>= 1;
+    }
+    return r;
+}
+
+// Visits the columns [c0, c1) of one row, in increasing order per thread:
+// float4 steps when the row is 16-byte aligned, then a scalar tail.
+// f(float &v, uint64_t col) may modify v; `write` stores it back.
+template <bool WRITE, class F>
+__device__ __forceinline__ void visit(const SmpGeo &g, float *row, uint64_t c0, uint64_t c1, F f)
+{
+    uint64_t c = c0;
+    if (g.vec) {
+        float4 *r4 = reinterpret_cast<float4 *>(row);
+        const uint64_t v1 = c1 / 4;
+        for (uint64_t v = c0 / 4 + threadIdx.x; v < v1; v += blockDim.x) {
+            float4 q = r4[v];
+            f(q.x, 4 * v);
+            f(q.y, 4 * v + 1);
+            f(q.z, 4 * v + 2);
+            f(q.w, 4 * v + 3);
+            if constexpr (WRITE) r4[v] = q;
+        }
+        c = v1 * 4 > c0 ? v1 * 4 : c0;
+    }
+    for (uint64_t k = c + threadIdx.x; k < c1; k += blockDim.x) {
+        float v = row[k];
+        f(v, k);
+        if constexpr (WRITE) row[k] = v;
+    }
+}
+
+__device__ __forceinline__ void chunk_range(const SmpGeo &g, uint32_t chunk, uint64_t &c0, uint64_t &c1)
+{
+    c0 = static_cast<uint64_t>(chunk) * g.chunk_cols;
+    c1 = c0 + g.chunk_cols < g.card ? c0 + g.chunk_cols : g.card;
+}
+
+// Block reduction of a float maximum (NaN-free operands), 256 threads.
+__device__ __forceinline__ float block_max256(float v)
+{
+    __shared__ float s[kBlock / kWave];
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+        const float o = __shfl_xor(v, off, kWave);
+        v = o > v ? o : v;
+    }
+    if (threadIdx.x % kWave == 0) s[threadIdx.x / kWave] = v;
+    __syncthreads();
+    float r = s[0];
+    for (int w = 1; w < kBlock / kWave; ++w) r = s[w] > r ? s[w] : r;
+    return r;
+}
+
+// ---- stage 1: chunk maxima of v = x * scale ---------------------------------
+
+__global__ __launch_bounds__(kBlock) void k_smp_max(SmpGeo g, float *logits, SmpWs w)
+{
+    const uint32_t row = blockIdx.x / g.chunks, chunk = blockIdx.x % g.chunks;
+    float *x = logits + static_cast<int64_t>(row) * g.ld;
+    if (chunk == 0) {
+        // fresh per-row state for this call
+        for (uint32_t b = threadIdx.x; b < kBins; b += blockDim.x) w.hist[static_cast<uint64_t>(row) * kBins + b] = 0;
+        if (threadIdx.x == 0) {
+            RowSel s{};
+            s.need = g.top_k;
+            w.sel[row] = s;
+        }
+    }
+    uint64_t c0, c1;
+    chunk_range(g, chunk, c0, c1);
+    const float scale = g.scale;
+    float m = -__builtin_inff();
+    visit<false>(g, x, c0, c1, [&](float &v, uint64_t) {
+        const float s = v * scale;
+        m = s > m ? s : m; // f32::max: a NaN operand is never taken
+    });
+    m = block_max256(m);
+    if (threadIdx.x == 0) w.part[blockIdx.x] = m;
+}
+
+__device__ __forceinline__ float row_max(const SmpGeo &g, const SmpWs &w, uint32_t row)
+{
+    float m = -__builtin_inff();
+    for (uint32_t c = threadIdx.x; c < g.chunks; c += blockDim.x) {
+        const float p = w.part[static_cast<uint64_t>(row) * g.chunks + c];
+        m = p > m ? p : m;
+    }
+    return block_max256(m);
+}
+
+// ---- stage 2: e = expf(v - m) in place --------------------------------------
+
+__global__ __launch_bounds__(kBlock) void k_smp_exp(SmpGeo g, float *logits, SmpWs w)
+{
+    const uint32_t row = blockIdx.x / g.chunks, chunk = blockIdx.x % g.chunks;
+    float *x = logits + static_cast<int64_t>(row) * g.ld;
+    const float m = row_max(g, w, row);
+    uint64_t c0, c1;
+    chunk_range(g, chunk, c0, c1);
+    const float scale = g.scale;
+    const ExpfConsts ec = expf_consts_in_vgprs();
+    visit<true>(g, x, c0, c1, [&](float &v, uint64_t) {
+        const float s = v * scale;
+        v = emel_expf(s - m, kExp2Table, ec);
+    });
+}
+
+// ---- stage 3: the exact sequential sum of e ----------------------------------
+//
+// One workgroup per row walks the row in tiles of kSumThreads * kSumPer
+// elements; thread t holds the kSumPer consecutive elements
+// [tile + kSumPer t, tile + kSumPer (t+1)).  A round computes every element's
+// units at the current binade, a workgroup-wide prefix sum of them, and
+// either commits the whole remaining tile (no event) or finds the first
+// event element, adds it with one f32 addition, and starts the next round
+// after it.  Each round commits at least one element, so the loop ends.
+
+__global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *logits, SmpWs w)
+{
+    constexpr uint32_t kWaves = kSumThreads / kWave;
+    constexpr uint32_t kTile = kSumThreads * kSumPer;
+    __shared__ uint32_t s_wsum[2][kWaves];  // per-wave unit totals (saturated), by round parity
+    __shared__ uint32_t s_wtie[2][kWaves];
+    __shared__ uint32_t s_first[kWaves];
+    __shared__ float s_next;
+
+    const uint32_t row = blockIdx.x;
+    const float *x = logits + static_cast<int64_t>(row) * g.ld;
+    const uint32_t t = threadIdx.x, lane = t % kWave, wave = t / kWave;
+    const uint64_t n = g.card;
+
+    uint32_t m = 0;
+    int32_t u = -149;
+    float special = 0.0f; // NaN or +inf once the running sum leaves the finite range
+    bool finite = true;
+    uint32_t parity = 0;
+
+    for (uint64_t base = 0; base < n; base += kTile) {
+        float e[kSumPer];
+        const uint64_t first_col = base + static_cast<uint64_t>(kSumPer) * t;
+        if (g.vec && first_col + kSumPer <= n) {
+            const float4 *p4 = reinterpret_cast<const float4 *>(x + first_col);
+#pragma unroll
+            for (uint32_t j = 0; j < kSumPer / 4; ++j) {
+                const float4 q = p4[j];
+                e[4 * j] = q.x;
+                e[4 * j + 1] = q.y;
+                e[4 * j + 2] = q.z;
+                e[4 * j + 3] = q.w;
+            }
+        } else {
+#pragma unroll
+            for (uint32_t j = 0; j < kSumPer; ++j) e[j] = first_col + j < n ? x[first_col + j] : 0.0f;
+        }
+        if (!finite) {
+            // +inf stays +inf unless a NaN follows; NaN stays NaN
+            bool nan = false;
+#pragma unroll
+            for (uint32_t j = 0; j < kSumPer; ++j) nan |= e[j] != e[j];
+            if (__syncthreads_or(nan)) special = __builtin_nanf("");
+            continue;
+        }
+        uint32_t start = 0; // tile-relative index of the first uncommitted element
+        while (true) {
+            uint32_t r[kSumPer];
+            uint32_t lsum = 0;
+            bool ltie = false;
+#pragma unroll
+            for (uint32_t j = 0; j < kSumPer; ++j) {
+                const uint32_t idx = kSumPer * t + j;
+                bool tie;
+                const uint32_t q = seq_units(e[j], u, tie);
+                const bool active = idx >= start;
+                r[j] = active ? q : 0u;
+                ltie |= active && tie;
+                lsum += r[j];
+            }
+            // lsum <= 16 * 2^24 = 2^28; saturate at 2^24 so the scans cannot
+            // overflow (a saturated value already marks a crossing)
+            uint32_t x_in = lsum < kSeqLimit ? lsum : kSeqLimit;
+            uint32_t incl = x_in;
+#pragma unroll
+            for (int off = 1; off < kWave; off <<= 1) {
+                const uint32_t o = __shfl_up(incl, off, kWave);
+                if (lane >= static_cast<uint32_t>(off)) incl += o;
+            }
+            const uint64_t tmask = __ballot(ltie);
+            if (lane == kWave - 1) {
+                s_wsum[parity][wave] = incl < kSeqLimit ? incl : kSeqLimit;
+                s_wtie[parity][wave] = tmask != 0;
+            }
+            __syncthreads();
+            uint32_t before = 0, total = 0, anytie = 0;
+#pragma unroll
+            for (uint32_t v = 0; v < kWaves; ++v) {
+                const uint32_t ws = s_wsum[parity][v];
+                before += v < wave ? ws : 0u;
+                total += ws;
+                anytie |= s_wtie[parity][v];
+            }
+            parity ^= 1u;
+            if (!anytie && m + total < kSeqLimit) {
+                m += total;
+                break; // tile committed
+            }
+            // first event element of this thread
+            uint32_t run = m + before + (incl - x_in); // units before this thread's first element
+            uint32_t mine = kNone;
+#pragma unroll
+            for (uint32_t j = 0; j < kSumPer; ++j) {
+                const uint32_t idx = kSumPer * t + j;
+                bool tie;
+                (void)seq_units(e[j], u, tie);
+                if (mine == kNone && idx >= start) {
+                    if (tie || run + r[j] >= kSeqLimit) mine = idx;
+                    else run += r[j];
+                }
+            }
+            const uint64_t emask = __ballot(mine != kNone);
+            const uint32_t wfirst = emask ? __shfl(mine, __builtin_ctzll(emask), kWave) : kNone;
+            if (lane == 0) s_first[wave] = wfirst;
+            __syncthreads();
+            uint32_t k = kNone;
+#pragma unroll
+            for (uint32_t v = 0; v < kWaves; ++v) k = s_first[v] < k ? s_first[v] : k;
+            if (k == kNone) break; // unreachable: a tie or a crossing has a first element
+            if (k / kSumPer == t) {
+                // every element before k adds its units exactly; k itself is
+                // one real f32 addition
+                const float before_k = seq_value(run, u);
+                float ek = e[0];
+#pragma unroll
+                for (uint32_t j = 1; j < kSumPer; ++j) ek = (k % kSumPer == j) ? e[j] : ek;
+                s_next = before_k + ek;
+            }
+            __syncthreads();
+            // s_next and s_first are rewritten only after the next round's
+            // first barrier, which every thread reaches after this read
+            const float sn = s_next;
+            if (!(sn < __builtin_inff())) { // NaN or +inf
+                special = sn;
+                finite = false;
+                // the rest of this tile can only turn +inf into NaN
+                bool nan = false;
+#pragma unroll
+                for (uint32_t j = 0; j < kSumPer; ++j) nan |= (kSumPer * t + j > k) && e[j] != e[j];
+                if (__syncthreads_or(nan)) special = __builtin_nanf("");
+                break;
+            }
+            const SeqState st = seq_state(sn);
+            m = st.m;
+            u = st.u;
+            start = k + 1;
+            if (start >= kTile) break;
+        }
+    }
+    if (t == 0) w.sel[row].total = finite ? seq_value(m, u) : special;
+}
+
+// ---- stage 4: p = e / S in place, first radix digit -------------------------
+
+// Adds the LDS histogram of a workgroup to the row's global histogram.
+__device__ __forceinline__ void flush_hist(uint32_t *s_hist, uint32_t nbins, uint32_t *dst)
+{
+    __syncthreads();
+    for (uint32_t b = threadIdx.x; b < nbins; b += blockDim.x) {
+        const uint32_t c = s_hist[b];
+        if (c) atomicAdd(dst + b, c);
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void k_smp_div(SmpGeo g, float *logits, SmpWs w)
+{
+    __shared__ uint32_t s_hist[kBins];
+    const uint32_t row = blockIdx.x / g.chunks, chunk = blockIdx.x % g.chunks;
+    float *x = logits + static_cast<int64_t>(row) * g.ld;
+    for (uint32_t b = threadIdx.x; b < kBins; b += blockDim.x) s_hist[b] = 0;
+    __syncthreads();
+    // S >= 1 (the maximal element contributes expf(0) = 1) or NaN: the
+    // reciprocal form is the correctly rounded quotient (div_by_recip)
+    const double recip = 1.0 / static_cast<double>(w.sel[row].total);
+    uint64_t c0, c1;
+    chunk_range(g, chunk, c0, c1);
+    visit<true>(g, x, c0, c1, [&](float &v, uint64_t) {
+        v = div_by_recip(v, recip);
+        atomicAdd(&s_hist[total_key(v) >> 21], 1u);
+    });
+    flush_hist(s_hist, kBins, w.hist + static_cast<uint64_t>(row) * kBins);
+}
+
+
+// ---- stages 5-6: radix selection of the top_k-th key ------------------------
+
+// Inclusive prefix sum over a 256-thread workgroup (uses s_tmp[4]).
+__device__ __forceinline__ uint32_t block_incl_scan256(uint32_t v, uint32_t *s_tmp, uint32_t &total)
+{
+    const uint32_t lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        const uint32_t o = __shfl_up(v, off, kWave);
+        if (lane >= static_cast<uint32_t>(off)) v += o;
+    }
+    if (lane == kWave - 1) s_tmp[wave] = v;
+    __syncthreads();
+    uint32_t before = 0;
+    total = 0;
+#pragma unroll
+    for (uint32_t w = 0; w < kBlock / kWave; ++w) {
+        before += w < wave ? s_tmp[w] : 0u;
+        total += s_tmp[w];
+    }
+    return v + before;
+}
+
+// pass = 0, 1, 2 (digits of 11, 11, 10 bits): picks the threshold digit b
+// from the histogram of the row's open prefix region -- the digit with
+// greater(b) < need <= greater(b) + count(b), greater(b) counting the
+// higher digits -- then clears the histogram for the next pass.
+__global__ __launch_bounds__(kBlock) void k_smp_pick(SmpWs w, uint32_t pass)
+{
+    __shared__ uint32_t s_tmp[kBlock / kWave];
+    __shared__ uint32_t s_pick[3];
+    const uint32_t row = blockIdx.x;
+    const RowSel sel = w.sel[row];
+    if (sel.mode != 0) return;
+    const uint32_t bits = pass == 2 ? 10u : 11u;
+    const uint32_t per = (1u << bits) / kBlock; // 8 or 4 bins per thread
+    uint32_t *h = w.hist + static_cast<uint64_t>(row) * kBins;
+    uint32_t mine[kBins / kBlock];
+    uint32_t local = 0;
+    for (uint32_t i = 0; i < per; ++i) {
+        mine[i] = h[threadIdx.x * per + i];
+        local += mine[i];
+    }
+    uint32_t total;
+    const uint32_t incl = block_incl_scan256(local, s_tmp, total);
+    uint32_t cum = total - incl; // elements in higher threads' (higher) digits
+    for (int i = static_cast<int>(per) - 1; i >= 0; --i) {
+        if (cum < sel.need && sel.need <= cum + mine[i]) {
+            s_pick[0] = threadIdx.x * per + static_cast<uint32_t>(i);
+            s_pick[1] = cum;
+            s_pick[2] = mine[i];
+        }
+        cum += mine[i];
+    }
+    for (uint32_t i = 0; i < per; ++i) h[threadIdx.x * per + i] = 0;
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    RowSel n = sel;
+    n.prefix = (sel.prefix << bits) | s_pick[0];
+    n.depth = sel.depth + bits;
+    n.above = sel.above + s_pick[1];
+    n.need = sel.need - s_pick[1];
+    if (n.above + s_pick[2] <= kCap) {
+        n.mode = 1; // every key whose top `depth` bits are >= prefix
+        n.count = n.above + s_pick[2];
+    } else if (n.depth == 32) {
+        n.mode = 2; // keys > T, then the lowest-index `need` keys == T
+        n.count = n.above + n.need;
+    }
+    w.sel[row] = n;
+}
+
+// pass = 1, 2: histogram of the next digit over the open prefix region.
+__global__ __launch_bounds__(kBlock) void k_smp_refine(SmpGeo g, float *logits, SmpWs w, uint32_t pass)
+{
+    __shared__ uint32_t s_hist[kBins];
+    const uint32_t row = blockIdx.x / g.chunks, chunk = blockIdx.x % g.chunks;
+    const RowSel sel = w.sel[row];
+    if (sel.mode != 0) return;
+    const uint32_t bits = pass == 2 ? 10u : 11u;
+    const uint32_t nbins = 1u << bits;
+    const uint32_t dshift = 32u - sel.depth; // depth is 11 or 22 here
+    const uint32_t shift = dshift - bits;
+    for (uint32_t b = threadIdx.x; b < nbins; b += blockDim.x) s_hist[b] = 0;
+    __syncthreads();
+    float *x = logits + static_cast<int64_t>(row) * g.ld;
+    uint64_t c0, c1;
+    chunk_range(g, chunk, c0, c1);
+    const uint32_t prefix = sel.prefix;
+    visit<false>(g, x, c0, c1, [&](float &v, uint64_t) {
+        const uint32_t key = total_key(v);
+        if ((key >> dshift) == prefix) atomicAdd(&s_hist[(key >> shift) & (nbins - 1)], 1u);
+    });
+    flush_hist(s_hist, nbins, w.hist + static_cast<uint64_t>(row) * kBins);
+}
+
+// ---- stage 7: ties at the exact threshold, per chunk ------------------------
+
+__global__ __launch_bounds__(kBlock) void k_smp_ties(SmpGeo g, float *logits, SmpWs w)
+{
+    __shared__ uint32_t s_tmp[kBlock / kWave];
+    const uint32_t row = blockIdx.x / g.chunks, chunk = blockIdx.x % g.chunks;
+    const RowSel sel = w.sel[row];
+    if (sel.mode != 2) return;
+    float *x = logits + static_cast<int64_t>(row) * g.ld;
+    uint64_t c0, c1;
+    chunk_range(g, chunk, c0, c1);
+    uint32_t c = 0;
+    visit<false>(g, x, c0, c1, [&](float &v, uint64_t) { c += total_key(v) == sel.prefix ? 1u : 0u; });
+    uint32_t total;
+    (void)block_incl_scan256(c, s_tmp, total);
+    if (threadIdx.x == 0) w.ties[blockIdx.x] = total;
+}
+
+// ---- stage 8: candidates ------------------------------------------------------
+
+__device__ __forceinline__ void push_cand(const SmpGeo &g, const SmpWs &w, uint32_t row, uint32_t key, uint64_t col)
+{
+    const uint32_t slot = atomicAdd(&w.sel[row].written, 1u);
+    // the selection counted exactly `count` <= cand_ld candidates; the bound
+    // only keeps a miscount from writing outside the row's list
+    if (slot < g.cand_ld) w.cand[static_cast<uint64_t>(row) * g.cand_ld + slot] = cand_word(key, static_cast<uint32_t>(col));
+}
+
+__global__ __launch_bounds__(kBlock) void k_smp_collect(SmpGeo g, float *logits, SmpWs w)
+{
+    __shared__ uint32_t s_tmp[2][kBlock / kWave];
+    const uint32_t row = blockIdx.x / g.chunks, chunk = blockIdx.x % g.chunks;
+    const RowSel sel = w.sel[row];
+    float *x = logits + static_cast<int64_t>(row) * g.ld;
+    uint64_t c0, c1;
+    chunk_range(g, chunk, c0, c1);
+    if (sel.mode == 1) {
+        const uint32_t dshift = 32u - sel.depth;
+        const uint64_t prefix = sel.prefix;
+        visit<false>(g, x, c0, c1, [&](float &v, uint64_t col) {
+            const uint32_t key = total_key(v);
+            if ((static_cast<uint64_t>(key) >> dshift) >= prefix) push_cand(g, w, row, key, col);
+        });
+        return;
+    }
+    // mode 2: keys > T, and the ties at T in column order until `need` are taken
+    const uint32_t T = sel.prefix;
+    uint32_t tie_base = 0;
+    for (uint32_t c = threadIdx.x; c < chunk; c += blockDim.x) tie_base += w.ties[static_cast<uint64_t>(row) * g.chunks + c];
+    {
+        uint32_t tb;
+        (void)block_incl_scan256(tie_base, s_tmp[0], tb);
+        tie_base = tb;
+    }
+    __syncthreads();
+    if (tie_base >= sel.need) {
+        visit<false>(g, x, c0, c1, [&](float &v, uint64_t col) {
+            const uint32_t key = total_key(v);
+            if (key > T) push_cand(g, w, row, key, col);
+        });
+        return;
+    }
+    // ordered steps of 4 consecutive columns per thread
+    uint32_t par = 1;
+    for (uint64_t blk = c0; blk < c1; blk += 4 * kBlock) {
+        const uint64_t col0 = blk + 4 * static_cast<uint64_t>(threadIdx.x);
+        float v[4];
+        uint32_t mine = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            v[j] = col0 + j < c1 ? x[col0 + j] : -__builtin_nanf("");
+            mine += (col0 + j < c1 && total_key(v[j]) == T) ? 1u : 0u;
+        }
+        uint32_t total;
+        const uint32_t incl = block_incl_scan256(mine, s_tmp[par], total);
+        par ^= 1u;
+        uint32_t rank = tie_base + incl - mine;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (col0 + j >= c1) break;
+            const uint32_t key = total_key(v[j]);
+            if (key > T) {
+                push_cand(g, w, row, key, col0 + j);
+            } else if (key == T) {
+                if (rank < sel.need) push_cand(g, w, row, key, col0 + j);
+                ++rank;
+            }
+        }
+        tie_base += total;
+    }
+}
+
+// ---- stage 9: ranking and selection -----------------------------------------
+
+struct SmpOut {
+    int32_t *sorted;
+    float *top_p;
+    int32_t *top_i;
+    int64_t sorted_ld, top_ld;
+    int32_t *selected;
+    float *score;
+    int32_t *status; // may be null
+};
+
+constexpr uint32_t kStatesInline = 512;
+struct SmpStates {
+    uint32_t v[kStatesInline]; // start states of rows [row0, row0 + kStatesInline)
+};
+
+// Race selection over the ranked slots j < top_k (sampler/sm.rs:821-847):
+// slot j draws state_j = s0 * 16807^(j+1) mod (2^31 - 1), u_j = state_j as
+// f32 / 2^31 (2147483647 as f32 is 2^31), race_j = p_j / -ln(u_j); the
+// first slot with the greatest race (strict >, starting from -inf) wins.
+template <class P, class I>
+__device__ void select_slots(const SmpGeo &g, uint32_t row, uint32_t s0, P prob, I index, const SmpOut &o)
+{
+    __shared__ float s_v[kRankThreads / kWave];
+    __shared__ uint32_t s_i[kRankThreads / kWave];
+    float best = -__builtin_inff();
+    uint32_t bslot = kNone;
+    uint32_t pw = powmod(threadIdx.x + 1);
+    const uint32_t stride = powmod(blockDim.x);
+    for (uint32_t j = threadIdx.x; j < g.top_k; j += blockDim.x) {
+        const uint32_t state = mulmod(s0, pw);
+        const float uniform = static_cast<float>(state) * 0x1p-31f;
+        const float race = prob(j) / -emel_logf(uniform);
+        if (race > -__builtin_inff() && (race > best || (race == best && j < bslot))) {
+            best = race;
+            bslot = j;
+        }
+        pw = mulmod(pw, stride);
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(best, off, kWave);
+        const uint32_t oi = __shfl_xor(bslot, off, kWave);
+        if (oi != kNone && (ov > best || (ov == best && oi < bslot) || bslot == kNone)) {
+            best = ov;
+            bslot = oi;
+        }
+    }
+    if (threadIdx.x % kWave == 0) {
+        s_v[threadIdx.x / kWave] = best;
+        s_i[threadIdx.x / kWave] = bslot;
+    }
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    for (uint32_t v = 1; v < blockDim.x / kWave; ++v) {
+        const float ov = s_v[v];
+        const uint32_t oi = s_i[v];
+        if (oi != kNone && (bslot == kNone || ov > best || (ov == best && oi < bslot))) {
+            best = ov;
+            bslot = oi;
+        }
+    }
+    const int32_t selected = bslot == kNone ? -1 : index(bslot);
+    const float score = bslot == kNone ? -__builtin_inff() : best;
+    o.selected[row] = selected;
+    o.score[row] = score;
+    const bool valid = selected >= 0 && static_cast<uint64_t>(selected) < g.card && __builtin_isfinite(score);
+    if (o.status) o.status[row] = valid ? 0 : kInvalidRequest;
+}
+
+__device__ __forceinline__ void write_ranked(const SmpGeo &g, const SmpOut &o, uint32_t row, uint32_t j, uint64_t word)
+{
+    const uint32_t idx = ~static_cast<uint32_t>(word);
+    const float p = from_key(static_cast<uint32_t>(word >> 32));
+    o.top_p[static_cast<int64_t>(row) * o.top_ld + j] = p;
+    o.top_i[static_cast<int64_t>(row) * o.top_ld + j] = static_cast<int32_t>(idx);
+    o.sorted[static_cast<int64_t>(row) * o.sorted_ld + j] = static_cast<int32_t>(idx);
+}
+
+// Bitonic sort, descending, of s[0, n) (n a power of two).
+__device__ __forceinline__ void lds_sort_desc(uint64_t *s, uint32_t n)
+{
+    for (uint32_t size = 2; size <= n; size <<= 1) {
+        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+            for (uint32_t t = threadIdx.x; t < n / 2; t += blockDim.x) {
+                const uint32_t i = 2 * t - (t & (stride - 1));
+                const uint32_t j = i + stride;
+                const bool desc = (i & size) == 0;
+                const uint64_t a = s[i], b = s[j];
+                if ((a < b) == desc) {
+                    s[i] = b;
+                    s[j] = a;
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// Candidate lists of at most kCap: one workgroup sorts a row in LDS.
+__global__ __launch_bounds__(kRankThreads) void k_smp_rank(SmpGeo g, SmpWs w, SmpOut o, SmpStates st, uint32_t row0)
+{
+    __shared__ uint64_t s_c[kCap];
+    const uint32_t row = row0 + blockIdx.x;
+    const uint32_t count = w.sel[row].count; // top_k <= count <= kCap here
+    const uint32_t n = count < kCap ? count : kCap;
+    uint32_t np = 2;
+    while (np < n || np < g.top_k) np <<= 1;
+    const uint64_t *c = w.cand + static_cast<uint64_t>(row) * g.cand_ld;
+    for (uint32_t i = threadIdx.x; i < np; i += blockDim.x) s_c[i] = i < n ? c[i] : 0ull;
+    __syncthreads();
+    lds_sort_desc(s_c, np);
+    for (uint32_t j = threadIdx.x; j < g.top_k; j += blockDim.x) write_ranked(g, o, row, j, s_c[j]);
+    select_slots(
+        g, row, st.v[blockIdx.x], [&](uint32_t j) { return from_key(static_cast<uint32_t>(s_c[j] >> 32)); },
+        [&](uint32_t j) { return static_cast<int32_t>(~static_cast<uint32_t>(s_c[j])); }, o);
+}
+
+// Longer lists (top_k > kCap, so count == top_k): sorted kCap tiles ...
+__global__ __launch_bounds__(kRankThreads) void k_smp_tile_sort(SmpGeo g, SmpWs w, uint32_t tiles)
+{
+    __shared__ uint64_t s_c[kCap];
+    const uint32_t row = blockIdx.x / tiles, tile = blockIdx.x % tiles;
+    const uint32_t n = w.sel[row].count;
+    const uint32_t b0 = tile * kCap;
+    if (b0 >= n) return;
+    const uint32_t len = n - b0 < kCap ? n - b0 : kCap;
+    uint32_t np = 2;
+    while (np < len) np <<= 1;
+    uint64_t *c = w.cand + static_cast<uint64_t>(row) * g.cand_ld + b0;
+    for (uint32_t i = threadIdx.x; i < np; i += blockDim.x) s_c[i] = i < len ? c[i] : 0ull;
+    __syncthreads();
+    lds_sort_desc(s_c, np);
+    for (uint32_t i = threadIdx.x; i < len; i += blockDim.x) c[i] = s_c[i];
+}
+
+// ... merged pairwise (runs of `width` into runs of 2 width), kMergePer
+// outputs per thread located by a merge-path search ...
+constexpr uint32_t kMergePer = 8;
+__global__ __launch_bounds__(kBlock) void k_smp_merge(SmpGeo g, SmpWs w, const uint64_t *src, uint64_t *dst,
+                                                      uint32_t width, uint32_t blocks_per_row)
+{
+    const uint32_t row = blockIdx.x / blocks_per_row;
+    const uint32_t n = w.sel[row].count;
+    const uint64_t o = (static_cast<uint64_t>(blockIdx.x % blocks_per_row) * kBlock + threadIdx.x) * kMergePer;
+    if (o >= n) return;
+    const uint64_t *s = src + static_cast<uint64_t>(row) * g.cand_ld;
+    uint64_t *d = dst + static_cast<uint64_t>(row) * g.cand_ld;
+    const uint64_t a0 = o / (2ull * width) * (2ull * width);
+    const uint64_t la = n - a0 < width ? n - a0 : width;
+    const uint64_t b0 = a0 + la;
+    const uint64_t lb = n - b0 < width ? n - b0 : (b0 >= n ? 0 : width);
+    const uint64_t *A = s + a0, *B = s + b0;
+    const uint64_t diag = o - a0;
+    uint64_t lo = diag > lb ? diag - lb : 0, hi = diag < la ? diag : la;
+    while (lo < hi) {
+        const uint64_t mid = (lo + hi) / 2;
+        if (A[mid] > B[diag - mid - 1]) lo = mid + 1;
+        else hi = mid;
+    }
+    uint64_t i = lo, j = diag - lo;
+    const uint64_t end = o + kMergePer < a0 + la + lb ? o + kMergePer : a0 + la + lb;
+    for (uint64_t k = o; k < end; ++k) {
+        const bool takeA = j >= lb || (i < la && A[i] > B[j]);
+        d[k] = takeA ? A[i++] : B[j++];
+    }
+}
+
+// ... and finished from the sorted list.
+__global__ __launch_bounds__(kRankThreads) void k_smp_finish(SmpGeo g, const uint64_t *sorted, SmpOut o,
+                                                             SmpStates st, uint32_t row0)
+{
+    const uint32_t row = row0 + blockIdx.x;
+    const uint64_t *c = sorted + static_cast<uint64_t>(row) * g.cand_ld;
+    for (uint32_t j = threadIdx.x; j < g.top_k; j += blockDim.x) write_ranked(g, o, row, j, c[j]);
+    select_slots(
+        g, row, st.v[blockIdx.x], [&](uint32_t j) { return from_key(static_cast<uint32_t>(c[j] >> 32)); },
+        [&](uint32_t j) { return static_cast<int32_t>(~static_cast<uint32_t>(c[j])); }, o);
+}
+
+// ---- validator: candidate ids and logits - max -------------------------------
+
+struct ValArgs {
+    const float *logits;
+    int32_t *ids;
+    float *scores;
+    uint64_t n;
+    uint64_t chunk_cols;
+    uint32_t chunks;
+    uint32_t vec;
+};
+
+// Chunk (value, lowest index) maxima, NaN never a candidate (argmax_merge).
+__global__ __launch_bounds__(kBlock) void k_val_max(ValArgs a, uint64_t *part)
+{
+    __shared__ float s_v[kBlock / kWave];
+    __shared__ uint32_t s_i[kBlock / kWave];
+    const uint64_t c0 = static_cast<uint64_t>(blockIdx.x) * a.chunk_cols;
+    const uint64_t c1 = c0 + a.chunk_cols < a.n ? c0 + a.chunk_cols : a.n;
+    float bv = -__builtin_inff();
+    uint32_t bi = kNone;
+    for (uint64_t k = c0 + threadIdx.x; k < c1; k += blockDim.x) argmax_merge(bv, bi, a.logits[k], static_cast<uint32_t>(k));
+    wave_argmax(bv, bi);
+    if (threadIdx.x % kWave == 0) {
+        s_v[threadIdx.x / kWave] = bv;
+        s_i[threadIdx.x / kWave] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    for (int v = 1; v < kBlock / kWave; ++v) argmax_merge(s_v[0], s_i[0], s_v[v], s_i[v]);
+    part[blockIdx.x] = (static_cast<uint64_t>(s_i[0]) << 32) | f32_to_bits(s_v[0]);
+}
+
+// execute_build (validator/sm.rs): maximum starts at logits[0] and moves on
+// strictly greater values, so it is the first maximal element (== compares
+// -0 and +0 equal), or logits[0] itself when that is NaN.
+__global__ __launch_bounds__(kBlock) void k_val_write(ValArgs a, const uint64_t *part)
+{
+    __shared__ float s_m;
+    if (threadIdx.x < kWave) {
+        float bv = -__builtin_inff();
+        uint32_t bi = kNone;
+        for (uint32_t c = threadIdx.x; c < a.chunks; c += kWave) {
+            const uint64_t q = part[c];
+            argmax_merge(bv, bi, bits_to_f32(static_cast<uint32_t>(q)), static_cast<uint32_t>(q >> 32));
+        }
+        wave_argmax(bv, bi);
+        if (threadIdx.x == 0) {
+            const float first = a.logits[0];
+            s_m = first != first ? first : bv;
+        }
+    }
+    __syncthreads();
+    const float m = s_m;
+    const uint64_t c0 = static_cast<uint64_t>(blockIdx.x) * a.chunk_cols;
+    const uint64_t c1 = c0 + a.chunk_cols < a.n ? c0 + a.chunk_cols : a.n;
+    for (uint64_t k = c0 + threadIdx.x; k < c1; k += blockDim.x) {
+        a.ids[k] = static_cast<int32_t>(k);
+        a.scores[k] = a.logits[k] - m;
+    }
+}
+
+constexpr uint32_t kTargetBlocks = 2048;
+constexpr uint64_t kMinChunkCols = 4 * kBlock;
+
+void plan_chunks(uint32_t rows, uint64_t card, uint64_t &chunk_cols, uint32_t &chunks)
+{
+    const uint64_t want = (kTargetBlocks + rows - 1) / rows;
+    uint64_t c = (card + want - 1) / want;
+    if (c < kMinChunkCols) c = kMinChunkCols;
+    c = (c + 3) & ~uint64_t{3};
+    chunk_cols = c;
+    chunks = static_cast<uint32_t>((card + c - 1) / c);
+}
+
+uint64_t align256(uint64_t b) { return (b + 255) & ~uint64_t{255}; }
+
+struct WsLayout {
+    uint64_t part, sel, hist, ties, cand, cand2, total;
+};
+
+WsLayout layout(uint32_t rows, uint32_t chunks, uint64_t cand_ld, bool merge)
+{
+    WsLayout l{};
+    l.part = 0;
+    l.sel = l.part + align256(uint64_t{rows} * chunks * sizeof(float));
+    l.hist = l.sel + align256(uint64_t{rows} * sizeof(RowSel));
+    l.ties = l.hist + align256(uint64_t{rows} * kBins * sizeof(uint32_t));
+    l.cand = l.ties + align256(uint64_t{rows} * chunks * sizeof(uint32_t));
+    l.cand2 = l.cand + align256(uint64_t{rows} * cand_ld * sizeof(uint64_t));
+    l.total = merge ? l.cand2 + align256(uint64_t{rows} * cand_ld * sizeof(uint64_t)) : l.cand2;
+    return l;
+}
+
+} // namespace
+
+uint64_t sampler_workspace_bytes(uint32_t rows, uint64_t card, uint32_t top_k)
+{
+    uint64_t chunk_cols;
+    uint32_t chunks;
+    plan_chunks(rows, card, chunk_cols, chunks);
+    const uint64_t cand_ld = top_k > kCap ? top_k : kCap;
+    return layout(rows, chunks, cand_ld, top_k > kCap).total;
+}
+
+hipError_t launch_sampler(const SamplerArgs &a, hipStream_t s)
+{
+    if (a.rows == 0 || a.card == 0 || a.top_k == 0 || a.top_k > a.card || a.card > 0x7fffffffull || !a.workspace)
+        return hipErrorInvalidValue;
+    SmpGeo g{};
+    g.rows = a.rows;
+    g.card = a.card;
+    plan_chunks(a.rows, a.card, g.chunk_cols, g.chunks);
+    g.ld = a.logits_ld;
+    g.vec = (reinterpret_cast<uintptr_t>(a.logits) % 16 == 0) && (a.rows == 1 || a.logits_ld % 4 == 0);
+    g.top_k = a.top_k;
+    g.scale = a.scale;
+    g.cand_ld = a.top_k > kCap ? a.top_k : kCap;
+    const bool merge = a.top_k > kCap;
+    const WsLayout l = layout(a.rows, g.chunks, g.cand_ld, merge);
+    char *base = static_cast<char *>(a.workspace);
+    SmpWs w{};
+    w.part = reinterpret_cast<float *>(base + l.part);
+    w.sel = reinterpret_cast<RowSel *>(base + l.sel);
+    w.hist = reinterpret_cast<uint32_t *>(base + l.hist);
+    w.ties = reinterpret_cast<uint32_t *>(base + l.ties);
+    w.cand = reinterpret_cast<uint64_t *>(base + l.cand);
+    w.cand2 = reinterpret_cast<uint64_t *>(base + l.cand2);
+
+    const dim3 grid(a.rows * g.chunks);
+    k_smp_max<<<grid, kBlock, 0, s>>>(g, a.logits, w);
+    k_smp_exp<<<grid, kBlock, 0, s>>>(g, a.logits, w);
+    k_smp_sum<<<a.rows, kSumThreads, 0, s>>>(g, a.logits, w);
+    k_smp_div<<<grid, kBlock, 0, s>>>(g, a.logits, w);
+    k_smp_pick<<<a.rows, kBlock, 0, s>>>(w, 0);
+    k_smp_refine<<<grid, kBlock, 0, s>>>(g, a.logits, w, 1);
+    k_smp_pick<<<a.rows, kBlock, 0, s>>>(w, 1);
+    k_smp_refine<<<grid, kBlock, 0, s>>>(g, a.logits, w, 2);
+    k_smp_pick<<<a.rows, kBlock, 0, s>>>(w, 2);
+    k_smp_ties<<<grid, kBlock, 0, s>>>(g, a.logits, w);
+    k_smp_collect<<<grid, kBlock, 0, s>>>(g, a.logits, w);
+
+    SmpOut o{};
+    o.sorted = a.sorted;
+    o.sorted_ld = a.sorted_ld;
+    o.top_p = a.top_p;
+    o.top_i = a.top_i;
+    o.top_ld = a.top_ld;
+    o.selected = a.selected;
+    o.score = a.score;
+    o.status = a.status;
+
+    const uint64_t *sorted = w.cand;
+    if (merge) {
+        const uint32_t tiles = (a.top_k + kCap - 1) / kCap;
+        k_smp_tile_sort<<<a.rows * tiles, kRankThreads, 0, s>>>(g, w, tiles);
+        const uint32_t per_block = kBlock * kMergePer;
+        const uint32_t bpr = (a.top_k + per_block - 1) / per_block;
+        uint64_t *src = w.cand, *dst = w.cand2;
+        for (uint32_t width = kCap; width < a.top_k; width *= 2) {
+            k_smp_merge<<<a.rows * bpr, kBlock, 0, s>>>(g, w, src, dst, width, bpr);
+            uint64_t *t = src;
+            src = dst;
+            dst = t;
+        }
+        sorted = src;
+    }
+    for (uint32_t r0 = 0; r0 < a.rows; r0 += kStatesInline) {
+        const uint32_t nr = a.rows - r0 < kStatesInline ? a.rows - r0 : kStatesInline;
+        SmpStates st{};
+        for (uint32_t i = 0; i < nr; ++i) st.v[i] = a.states[r0 + i];
+        if (merge) k_smp_finish<<<nr, kRankThreads, 0, s>>>(g, sorted, o, st, r0);
+        else k_smp_rank<<<nr, kRankThreads, 0, s>>>(g, w, o, st, r0);
+    }
+    return hipGetLastError();
+}
+
+uint64_t validator_workspace_bytes(uint64_t n)
+{
+    uint64_t chunk_cols;
+    uint32_t chunks;
+    plan_chunks(1, n, chunk_cols, chunks);
+    return uint64_t{chunks} * sizeof(uint64_t);
+}
+
+hipError_t launch_validator(const float *logits, uint64_t n, int32_t *ids, float *scores, void *workspace,
+                            hipStream_t s)
+{
+    if (n == 0 || n > 0x7fffffffull || !workspace) return hipErrorInvalidValue;
+    ValArgs a{};
+    a.logits = logits;
+    a.ids = ids;
+    a.scores = scores;
+    a.n = n;
+    plan_chunks(1, n, a.chunk_cols, a.chunks);
+    uint64_t *part = static_cast<uint64_t *>(workspace);
+    k_val_max<<<a.chunks, kBlock, 0, s>>>(a, part);
+    k_val_write<<<a.chunks, kBlock, 0, s>>>(a, part);
+    return hipGetLastError();
+}
+
+} // namespace emel

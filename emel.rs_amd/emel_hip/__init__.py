@@ -41,6 +41,7 @@ from .kernel import (
     OpSwiglu,
     OpUnary,
 )
+from .sampler import Build, SamplePreselected, Sampler, SampleTemperatureTopK, Validator
 from .views import Layout, TensorView, TensorViewMut
 
 __all__ = [
@@ -51,5 +52,5 @@ __all__ = [
     "OpSoftMax", "OpSoftMaxExt", "OpSumRows", "OpSum", "OpMean", "OpArgmax", "OpArgmaxRows",
     "OpSqr", "OpSqrt", "DenseOpDup", "DenseOpAdd", "DenseOpSub", "DenseOpMul", "DenseOpDiv", "DenseOpSqr",
     "DenseOpSqrt", "IndexView", "OpGetRows", "OpGetRowsF32Bytes", "OpGetRowsF16", "OpGetRowsBf16", "OpGetRowsQ4_0",
-    "OpGetRowsQ8_0", "OpGetRowsQ4K",
+    "OpGetRowsQ8_0", "OpGetRowsQ4K", "Sampler", "SampleTemperatureTopK", "SamplePreselected", "Validator", "Build",
 ]

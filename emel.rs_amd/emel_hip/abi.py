@@ -28,6 +28,7 @@ class Status(enum.IntEnum):
     UNSUPPORTED_OPERATION = 10
     INDEX_OUT_OF_BOUNDS = 11
     UNSUPPORTED_SOURCE_STRIDE = 12
+    INVALID_REQUEST = 13
 
 
 class DType(enum.IntEnum):
@@ -236,6 +237,40 @@ class CIndexView(ctypes.Structure):
     ]
 
 
+class CSampleRequest(ctypes.Structure):
+    """emel_sample_temperature_top_k_request (SampleTemperatureTopK, emel-logits sampler/sm.rs:148-195)."""
+
+    _fields_ = [
+        ("card", ctypes.c_uint64),
+        ("temperature", ctypes.c_float),
+        ("reserved", ctypes.c_uint32),
+        ("top_k", ctypes.c_uint64),
+        ("logits", ctypes.c_void_p),
+        ("logits_len", ctypes.c_uint64),
+        ("sorted_indices", ctypes.c_void_p),
+        ("sorted_indices_len", ctypes.c_uint64),
+        ("top_probabilities", ctypes.c_void_p),
+        ("top_probabilities_len", ctypes.c_uint64),
+        ("top_indices", ctypes.c_void_p),
+        ("top_indices_len", ctypes.c_uint64),
+        ("random_state", ctypes.c_void_p),
+        ("selected_token_out", ctypes.c_void_p),
+        ("selected_score_out", ctypes.c_void_p),
+        ("status_out", ctypes.c_void_p),
+    ]
+
+
+class CSampleRows(ctypes.Structure):
+    """emel_sample_rows: a batch of independent sampler requests."""
+
+    _fields_ = [
+        ("rows", ctypes.c_uint64),
+        ("logits_stride", ctypes.c_uint64),
+        ("sorted_stride", ctypes.c_uint64),
+        ("top_stride", ctypes.c_uint64),
+    ]
+
+
 _V = ctypes.POINTER(CView)
 _S = ctypes.c_void_p
 _ST = ctypes.c_int
@@ -287,6 +322,12 @@ SIGNATURES = {
     "emel_generic_dispatch": [ctypes.POINTER(CGenericRequest), _S],
     **{f"emel_op_get_rows{suffix}": [_V, ctypes.POINTER(CIndexView), _V, _S]
        for suffix in ("", "_f32_bytes", "_f16", "_bf16", "_q4_0", "_q8_0", "_q4_k")},
+    "emel_sample_temperature_top_k": [ctypes.POINTER(CSampleRequest), _S],
+    "emel_sample_temperature_top_k_rows": [ctypes.POINTER(CSampleRequest), ctypes.POINTER(CSampleRows), _S],
+    "emel_sample_preselected": [ctypes.c_uint64, ctypes.c_int32, ctypes.POINTER(ctypes.c_int32)],
+    "emel_logits_validator_build": [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int32, ctypes.c_void_p,
+                                    ctypes.c_uint64, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int32,
+                                    ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32), _S],
 }
 
 _lib = None

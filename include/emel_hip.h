@@ -59,7 +59,9 @@ typedef enum emel_status {
     EMEL_ERR_INVALID_SHAPE = 9,      /* root Error::InvalidShape (actor.rs:88-101): dense-slice events */
     EMEL_ERR_UNSUPPORTED_OPERATION = 10, /* root Error::UnsupportedOperation */
     EMEL_ERR_INDEX_OUT_OF_BOUNDS = 11,   /* GetRowsError::IndexOutOfBounds (get_rows.rs:520-535) */
-    EMEL_ERR_UNSUPPORTED_SOURCE_STRIDE = 12 /* GetRowsError::UnsupportedSourceStride */
+    EMEL_ERR_UNSUPPORTED_SOURCE_STRIDE = 12, /* GetRowsError::UnsupportedSourceStride */
+    EMEL_ERR_INVALID_REQUEST = 13 /* emel-logits SamplerError::InvalidRequest / ValidatorError::InvalidRequest
+                                     (crates/emel-logits/src/sampler/sm.rs:41-52, validator/sm.rs:15-21) */
 } emel_status;
 
 /* Wire dtype codes, DType::from_code (tensor_view.rs:111-158). */
@@ -426,6 +428,103 @@ typedef struct emel_generic_request {
  * wire range, op_params_size > 64 or reserved != 0 (none representable in
  * the reference's types) is EMEL_ERR_INVALID_ARGUMENT. */
 emel_status emel_generic_dispatch(const emel_generic_request *request, emel_stream stream);
+
+/* ---- emel-logits: native sampler and candidate validator ----------------------
+ * crates/emel-logits/src/sampler/sm.rs and validator/sm.rs (paths below are
+ * relative to crates/emel-logits/src/).  Buffers are device memory unless
+ * marked HOST.  Lengths are element counts, the Rust slice lengths the
+ * reference's guards read. */
+
+/* Sampler::sample_temperature_top_k(SampleTemperatureTopK::new(card,
+ * temperature, top_k, logits, sorted_indices, top_probabilities,
+ * top_indices, random_state, selected_token_out, selected_score_out))
+ * (sampler/sm.rs:148-195, :380-392).
+ *
+ * Guard (guard_temperature_valid, sm.rs:729-747): card > 0, 0 < top_k <=
+ * card, temperature finite and > 0, logits_len and sorted_indices_len >=
+ * card, top_probabilities_len and top_indices_len >= top_k, random_state
+ * not a multiple of 2^31 - 1.  A failed guard is EMEL_ERR_INVALID_REQUEST
+ * with nothing written.  Otherwise, in order (sm.rs:759-847):
+ *   logits[i] *= 1/temperature; softmax in place (f32::max fold, expf,
+ *   a sequential f32 sum -- reproduced exactly --, division);
+ *   top_probabilities / top_indices = the top_k probabilities and their
+ *   indices, descending by f32::total_cmp (equal probabilities by ascending
+ *   index: the reference's sort_unstable leaves their order unspecified);
+ *   slot j draws the (j+1)-th Park-Miller state (x16807 mod 2^31 - 1) and
+ *   races top_probabilities[j] / -ln(state / 2^31); the first maximal race
+ *   gives selected_token_out and selected_score_out.
+ * random_state (HOST) is updated to the state after top_k draws before the
+ * call returns.  sorted_indices is the reference's sort scratch: its first
+ * top_k entries receive the ranked indices, the rest is not written.
+ * The result guard (guard_temperature_result_valid, sm.rs:849-858: token in
+ * [0, card) and score finite) is evaluated on the device and written to
+ * status_out (EMEL_OK or EMEL_ERR_INVALID_REQUEST) when status_out is not
+ * NULL; the outputs are written either way, as in the reference.
+ * After the guard, NULL buffers, overlapping buffers, pointers that are not
+ * 4-byte aligned and card > 2^31 - 1 are EMEL_ERR_INVALID_ARGUMENT (a NULL
+ * request or random_state before it). */
+typedef struct emel_sample_temperature_top_k_request {
+    uint64_t card;
+    float temperature;
+    uint32_t reserved; /* must be 0 */
+    uint64_t top_k;
+    float *logits;                  uint64_t logits_len;            /* in place: probabilities on return */
+    int32_t *sorted_indices;        uint64_t sorted_indices_len;
+    float *top_probabilities;       uint64_t top_probabilities_len;
+    int32_t *top_indices;           uint64_t top_indices_len;
+    uint32_t *random_state;         /* HOST, read and updated */
+    int32_t *selected_token_out;
+    float *selected_score_out;
+    int32_t *status_out;            /* may be NULL */
+} emel_sample_temperature_top_k_request;
+
+emel_status emel_sample_temperature_top_k(const emel_sample_temperature_top_k_request *request, emel_stream stream);
+
+/* `rows` independent requests in one call (a batch of sequences sampled at
+ * once): row r uses logits + r*logits_stride, sorted_indices +
+ * r*sorted_stride, top_probabilities / top_indices + r*top_stride,
+ * random_state[r], selected_token_out[r], selected_score_out[r] and
+ * status_out[r].  The lengths in the request are the whole buffers'; every
+ * row must fit (strides >= card resp. top_k).  The guard covers every row:
+ * one failing row rejects the call. */
+typedef struct emel_sample_rows {
+    uint64_t rows;
+    uint64_t logits_stride;
+    uint64_t sorted_stride;
+    uint64_t top_stride;
+} emel_sample_rows;
+
+emel_status emel_sample_temperature_top_k_rows(const emel_sample_temperature_top_k_request *request,
+                                               const emel_sample_rows *rows, emel_stream stream);
+
+/* Sampler::sample_preselected(SamplePreselected::new(vocab_size,
+ * selected_token)) (sampler/sm.rs:129-146, :366-378, guard :685-695):
+ * host-only; writes *token_out (HOST) on success. */
+emel_status emel_sample_preselected(uint64_t vocab_size, int32_t selected_token, int32_t *token_out);
+
+/* ValidatorError (validator/sm.rs:15-21) discriminants, as *error_out. */
+typedef enum emel_validator_error {
+    EMEL_VALIDATOR_NONE = 0,
+    EMEL_VALIDATOR_INVALID_REQUEST = 1,
+    EMEL_VALIDATOR_BACKEND_ERROR = 2,
+    EMEL_VALIDATOR_INTERNAL_ERROR = 3,
+    EMEL_VALIDATOR_UNTRACKED = 4
+} emel_validator_error;
+
+/* Validator::process_event(Build::new(logits, vocab_size, candidate_ids,
+ * candidate_scores, candidate_capacity, candidate_count_out, error_out))
+ * (validator/sm.rs:33-66, :170-230).  candidate_count_out and error_out are
+ * HOST scalars: reset to 0 / NONE, then on a failed guard (vocab_size > 0,
+ * candidate_capacity >= vocab_size, each slice length >= vocab_size and
+ * below 2^31) 0 / INVALID_REQUEST with EMEL_ERR_INVALID_REQUEST.  Otherwise
+ * candidate_ids[i] = i and candidate_scores[i] = logits[i] - max for
+ * i < vocab_size, where max starts at logits[0] and moves on strictly
+ * greater values; *candidate_count_out = vocab_size. */
+emel_status emel_logits_validator_build(const float *logits, uint64_t logits_len, int32_t vocab_size,
+                                        int32_t *candidate_ids, uint64_t candidate_ids_len,
+                                        float *candidate_scores, uint64_t candidate_scores_len,
+                                        int32_t candidate_capacity, int32_t *candidate_count_out,
+                                        int32_t *error_out, emel_stream stream);
 
 #ifdef __cplusplus
 }

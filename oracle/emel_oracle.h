@@ -43,6 +43,7 @@ enum {
     ORC_UNSUPPORTED_OPERATION = 10,  /* root Error::UnsupportedOperation */
     ORC_INDEX_OUT_OF_BOUNDS = 11,    /* GetRowsError::IndexOutOfBounds */
     ORC_UNSUPPORTED_SOURCE_STRIDE = 12, /* GetRowsError::UnsupportedSourceStride */
+    ORC_INVALID_REQUEST = 13,        /* emel-logits SamplerError / ValidatorError::InvalidRequest */
     ORC_PANIC = 99,                  /* the reference's guard passes and its executor panics */
 };
 
@@ -124,6 +125,19 @@ enum { ORC_GR_F32 = 0, ORC_GR_F32_BYTES, ORC_GR_F16, ORC_GR_BF16, ORC_GR_Q4_0, O
 int orc_get_rows(int kind, const orc_view *src, const orc_index_view *indices, const orc_view *dst);
 
 /* Scalar helpers (unary.rs:522-600, quant.rs:287-300). */
+/* emel-logits (emel_oracle_sampler.c): the native temperature/top-k
+ * sampler and the candidate validator, host slices. */
+uint32_t orc_park_miller_next(uint32_t state);
+float orc_sampler_softmax(float *values, uint64_t card);
+int orc_sample_temperature_top_k(uint64_t card, float temperature, uint64_t top_k, float *logits,
+                                 uint64_t logits_len, int32_t *sorted_indices, uint64_t sorted_len,
+                                 float *top_probabilities, uint64_t top_probabilities_len, int32_t *top_indices,
+                                 uint64_t top_indices_len, uint32_t *random_state, int32_t *selected_token_out,
+                                 float *selected_score_out);
+int orc_validator_build(const float *logits, uint64_t logits_len, int32_t vocab_size, int32_t *candidate_ids,
+                        uint64_t ids_len, float *candidate_scores, uint64_t scores_len, int32_t candidate_capacity,
+                        int32_t *candidate_count_out, int32_t *error_out);
+
 float orc_silu(float x);
 float orc_gelu(float x);
 uint16_t orc_fp32_to_fp16(float x);

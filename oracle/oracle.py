@@ -275,3 +275,69 @@ def get_rows(kind: int, src: OView, idx: OIndexView, dst: OView) -> int:
     L.orc_get_rows.argtypes = [ctypes.c_int, ctypes.POINTER(OView), ctypes.POINTER(OIndexView), ctypes.POINTER(OView)]
     L.orc_get_rows.restype = ctypes.c_int
     return int(L.orc_get_rows(kind, ctypes.byref(src), ctypes.byref(idx), ctypes.byref(dst)))
+
+
+# ---- emel-logits sampler and validator (emel_oracle_sampler.c) ----------------
+
+INVALID_REQUEST = 13
+
+
+def _sampler_lib():
+    L = lib()
+    if not getattr(L, "_sampler_sigs", False):
+        L.orc_park_miller_next.argtypes = [ctypes.c_uint32]
+        L.orc_park_miller_next.restype = ctypes.c_uint32
+        L.orc_sampler_softmax.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_uint64]
+        L.orc_sampler_softmax.restype = ctypes.c_float
+        L.orc_sample_temperature_top_k.argtypes = [
+            ctypes.c_uint64, ctypes.c_float, ctypes.c_uint64,
+            ctypes.POINTER(ctypes.c_float), ctypes.c_uint64, ctypes.POINTER(ctypes.c_int32), ctypes.c_uint64,
+            ctypes.POINTER(ctypes.c_float), ctypes.c_uint64, ctypes.POINTER(ctypes.c_int32), ctypes.c_uint64,
+            ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_float)]
+        L.orc_sample_temperature_top_k.restype = ctypes.c_int
+        L.orc_validator_build.argtypes = [
+            ctypes.POINTER(ctypes.c_float), ctypes.c_uint64, ctypes.c_int32, ctypes.POINTER(ctypes.c_int32),
+            ctypes.c_uint64, ctypes.POINTER(ctypes.c_float), ctypes.c_uint64, ctypes.c_int32,
+            ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32)]
+        L.orc_validator_build.restype = ctypes.c_int
+        L._sampler_sigs = True
+    return L
+
+
+def _ptr(a: np.ndarray, ctype):
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(ctypes.POINTER(ctype))
+
+
+def park_miller_next(state: int) -> int:
+    return int(_sampler_lib().orc_park_miller_next(state))
+
+
+def sampler_softmax(values: np.ndarray) -> float:
+    """In place over a float32 array; returns the sequential f32 sum."""
+    return float(_sampler_lib().orc_sampler_softmax(_ptr(values, ctypes.c_float), values.size))
+
+
+def sample_temperature_top_k(card, temperature, top_k, logits, sorted_indices, top_probabilities, top_indices,
+                             random_state, selected, score, lens=None):
+    """Sampler::sample_temperature_top_k over numpy buffers (modified in place).
+    random_state / selected / score are 1-element uint32 / int32 / float32
+    arrays.  lens overrides the (logits, sorted, top_p, top_i) lengths."""
+    if lens is None:
+        lens = (logits.size, sorted_indices.size, top_probabilities.size, top_indices.size)
+    return int(_sampler_lib().orc_sample_temperature_top_k(
+        card, ctypes.c_float(temperature), top_k, _ptr(logits, ctypes.c_float), lens[0],
+        _ptr(sorted_indices, ctypes.c_int32), lens[1], _ptr(top_probabilities, ctypes.c_float), lens[2],
+        _ptr(top_indices, ctypes.c_int32), lens[3], _ptr(random_state, ctypes.c_uint32),
+        _ptr(selected, ctypes.c_int32), _ptr(score, ctypes.c_float)))
+
+
+def validator_build(logits, vocab_size, ids, scores, capacity, count_out, error_out, lens=None):
+    """Validator::process_event(Build) over numpy buffers; count_out and
+    error_out are 1-element int32 arrays (error: 0 None, 1 InvalidRequest)."""
+    if lens is None:
+        lens = (logits.size, ids.size, scores.size)
+    return int(_sampler_lib().orc_validator_build(
+        _ptr(logits, ctypes.c_float), lens[0], vocab_size, _ptr(ids, ctypes.c_int32), lens[1],
+        _ptr(scores, ctypes.c_float), lens[2], capacity, _ptr(count_out, ctypes.c_int32),
+        _ptr(error_out, ctypes.c_int32)))

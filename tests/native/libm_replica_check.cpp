@@ -3,14 +3,19 @@
 // Compiles the product's device math (emel.rs_amd/csrc/libm_replica.hpp) for
 // the host CPU and counts, over a range of f32 bit patterns, the inputs on
 // which it differs from an independent checker:
-//   expf / expm1f / tanhf  -> the host glibc (what Rust std calls, and so
+//   expf / expm1f / tanhf / logf
+//                          -> the host glibc (what Rust std calls, and so
 //                             what the reference's CPU path computes);
 //   fp32 -> fp16           -> the compiler's _Float16 conversion (IEEE
 //                             round-to-nearest-even);
-//   fp16 -> fp32           -> the compiler's _Float16 widening (exact).
+//   fp16 -> fp32           -> the compiler's _Float16 widening (exact);
+//   seqsum.hpp             -> a plain sequential f32 loop: the host
+//                             emulation of k_smp_sum's rounds (units per
+//                             binade, events, restarts) must give its bits.
 // NaN results count as equal when both are NaN.  Ranges are split over
 // `threads` threads.
 #include "libm_replica.hpp"
+#include "seqsum.hpp"
 
 #include <cmath>
 #include <cstdint>
@@ -46,6 +51,132 @@ bool differ(float a, float b)
 
 } // namespace
 
+// The round structure of k_smp_sum (sampler.hip) on the host: tiles of
+// threads * per elements; a round commits the rest of the tile when no
+// element is an event, else commits up to the first event and adds that
+// element with one f32 addition.  Exact (unsaturated) prefix sums.
+float seqsum_blocked(const float *e, uint64_t n, uint32_t threads, uint32_t per)
+{
+    uint32_t m = 0;
+    int32_t u = -149;
+    bool finite = true;
+    float special = 0.0f;
+    const uint64_t tile = static_cast<uint64_t>(threads) * per;
+    std::vector<float> ev(tile);
+    std::vector<uint32_t> r(tile);
+    std::vector<uint8_t> tie(tile);
+    for (uint64_t base = 0; base < n; base += tile) {
+        for (uint64_t i = 0; i < tile; ++i) ev[i] = base + i < n ? e[base + i] : 0.0f;
+        if (!finite) {
+            for (uint64_t i = 0; i < tile; ++i)
+                if (std::isnan(ev[i])) special = std::nanf("");
+            continue;
+        }
+        uint64_t start = 0;
+        while (true) {
+            uint64_t total = 0;
+            bool anytie = false;
+            for (uint64_t i = 0; i < tile; ++i) {
+                bool t;
+                const uint32_t q = emel::seq_units(ev[i], u, t);
+                r[i] = i >= start ? q : 0u;
+                tie[i] = i >= start && t;
+                total += r[i];
+                anytie |= tie[i] != 0;
+            }
+            if (!anytie && m + total < emel::kSeqLimit) {
+                m += static_cast<uint32_t>(total);
+                break;
+            }
+            uint64_t run = m, k = tile;
+            for (uint64_t i = start; i < tile; ++i) {
+                if (tie[i] || run + r[i] >= emel::kSeqLimit) {
+                    k = i;
+                    break;
+                }
+                run += r[i];
+            }
+            if (k == tile) return std::nanf("0x7e57"); // cannot happen: flag it
+            const float sn = emel::seq_value(static_cast<uint32_t>(run), u) + ev[k];
+            if (!(sn < INFINITY)) {
+                special = sn;
+                finite = false;
+                for (uint64_t i = k + 1; i < tile; ++i)
+                    if (std::isnan(ev[i])) special = std::nanf("");
+                break;
+            }
+            const emel::SeqState st = emel::seq_state(sn);
+            m = st.m;
+            u = st.u;
+            start = k + 1;
+            if (start >= tile) break;
+        }
+    }
+    return finite ? emel::seq_value(m, u) : special;
+}
+
+static uint64_t splitmix(uint64_t &z)
+{
+    uint64_t x = (z += 0x9e3779b97f4a7c15ull);
+    x = (x ^ (x >> 30)) * 0xbf58476d1ce4e5b9ull;
+    x = (x ^ (x >> 27)) * 0x94d049bb133111ebull;
+    return x ^ (x >> 31);
+}
+
+// Addend families: 0 softmax-like (expf of N(0,2) - 8, mostly < 1),
+// 1 dyadic values k * 2^j (many exact ties), 2 tiny and subnormal values
+// with zeros, 3 values of every magnitude up to 2^30, 4 family 0 with one
+// NaN or +inf planted.
+static void fill_case(uint64_t &z, int family, std::vector<float> &e)
+{
+    for (float &v : e) {
+        const uint64_t x = splitmix(z);
+        switch (family) {
+        case 0:
+        case 4: {
+            const double u1 = ((x >> 11) + 0.5) * 0x1p-53, u2 = (splitmix(z) >> 11) * 0x1p-53;
+            const double g = std::sqrt(-2.0 * std::log(u1)) * std::cos(6.283185307179586 * u2);
+            v = expf(static_cast<float>(2.0 * g - 8.0));
+            break;
+        }
+        case 1: v = std::ldexp(static_cast<float>(x % 17), -static_cast<int>((x >> 8) % 40)); break;
+        case 2: v = (x & 3) == 0 ? 0.0f : emel::bits_to_f32(static_cast<uint32_t>((x >> 8) % 0x01000000u)); break;
+        default: v = std::ldexp(static_cast<float>((x >> 40) | 1), static_cast<int>((x >> 8) % 60) - 54); break;
+        }
+    }
+    if (family == 4 && !e.empty()) {
+        const uint64_t x = splitmix(z);
+        e[x % e.size()] = (x >> 63) ? std::nanf("") : INFINITY;
+    }
+}
+
+extern "C" float seqsum_blocked_f(const float *e, uint64_t n, uint32_t threads, uint32_t per)
+{
+    return seqsum_blocked(e, n, threads, per);
+}
+
+// Random cases of each family and length up to max_n; tile shapes
+// (threads, per) of the kernel (1024, 16) and small ones that force many
+// rounds.  Counts results whose bits differ from the sequential loop.
+extern "C" uint64_t check_seqsum(uint64_t seed, int cases, uint64_t max_n)
+{
+    uint64_t z = seed, bad = 0;
+    const uint32_t shapes[3][2] = {{1024, 16}, {4, 2}, {64, 1}};
+    for (int c = 0; c < cases; ++c) {
+        const int family = c % 5;
+        const uint64_t n = 1 + splitmix(z) % max_n;
+        std::vector<float> e(n);
+        fill_case(z, family, e);
+        float want = 0.0f;
+        for (float v : e) want += v;
+        for (const auto &sh : shapes) {
+            const float got = seqsum_blocked(e.data(), n, sh[0], sh[1]);
+            if (differ(got, want)) ++bad;
+        }
+    }
+    return bad;
+}
+
 extern "C" {
 
 uint64_t check_expf(uint64_t lo, uint64_t hi, int threads)
@@ -69,6 +200,14 @@ uint64_t check_tanhf(uint64_t lo, uint64_t hi, int threads)
     return count_range(lo, hi, threads, [](uint32_t u) {
         const float x = emel::bits_to_f32(u);
         return differ(emel::emel_tanhf(x), tanhf(x));
+    });
+}
+
+uint64_t check_logf(uint64_t lo, uint64_t hi, int threads)
+{
+    return count_range(lo, hi, threads, [](uint32_t u) {
+        const float x = emel::bits_to_f32(u);
+        return differ(emel::emel_logf(x), logf(x));
     });
 }
 

@@ -2,7 +2,8 @@
 for the host by tests/native/libm_replica_check.cpp, against independent
 checkers over ALL 2^32 float inputs:
 
-  expf, expm1f, tanhf  == the host glibc (Rust std's f32::exp/exp_m1/tanh on
+  expf, expm1f, tanhf, logf
+                       == the host glibc (Rust std's f32::exp/exp_m1/tanh/ln on
                           x86_64-linux-gnu, i.e. what the reference computes);
   fp32 -> fp16         == IEEE round-to-nearest-even (_Float16 conversion);
   fp16 -> fp32         == exact widening;
@@ -28,7 +29,7 @@ def chk():
     if not LIB.exists():
         pytest.fail(f"{LIB} missing: run __graft_entry__.build()")
     L = ctypes.CDLL(str(LIB))
-    for n in ("check_expf", "check_expm1f", "check_tanhf", "check_fp32_to_fp16", "check_gelu_table"):
+    for n in ("check_expf", "check_expm1f", "check_tanhf", "check_logf", "check_fp32_to_fp16", "check_gelu_table"):
         getattr(L, n).restype = ctypes.c_uint64
         getattr(L, n).argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int]
     L.check_fp16_to_f32.restype = ctypes.c_uint64
@@ -38,7 +39,7 @@ def chk():
     return L
 
 
-@pytest.mark.parametrize("fn", ["check_expf", "check_expm1f", "check_tanhf", "check_fp32_to_fp16", "check_gelu_table"])
+@pytest.mark.parametrize("fn", ["check_expf", "check_expm1f", "check_tanhf", "check_logf", "check_fp32_to_fp16", "check_gelu_table"])
 def test_exhaustive(chk, fn):
     assert getattr(chk, fn)(0, 1 << 32, THREADS) == 0
 
@@ -79,3 +80,18 @@ def test_replica_matches_oracle_scalars(chk):
         x = float(x)
         assert np.float32(chk.replica_silu(x)).view(np.uint32) == np.float32(orc.silu_scalar(x)).view(np.uint32), x
         assert np.float32(chk.replica_gelu(x)).view(np.uint32) == np.float32(orc.gelu_scalar(x)).view(np.uint32), x
+
+
+def test_exact_sequential_sum_rounds(chk):
+    """The round structure of the sampler's exact sequential f32 sum
+    (seqsum.hpp, k_smp_sum): integer units per binade, with ties, binade
+    crossings, NaN and +inf taken as single f32 additions, must give the
+    bits of a plain sequential f32 loop.  Families: softmax-like values,
+    dyadic values full of exact ties, zeros and subnormals, every magnitude,
+    planted NaN / +inf; tiles of the kernel's shape (1024 x 16) and of small
+    shapes that force many rounds.  Ignoring ties or letting a binade run to
+    2^25 units makes this check fail (1275 and 4950 mismatching cases)."""
+    chk.check_seqsum.restype = ctypes.c_uint64
+    chk.check_seqsum.argtypes = [ctypes.c_uint64, ctypes.c_int, ctypes.c_uint64]
+    assert chk.check_seqsum(1, 2000, 300) == 0
+    assert chk.check_seqsum(2, 40, 200_000) == 0
