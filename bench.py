@@ -407,6 +407,96 @@ def gather_ops(suite, stream, reps):
     return res
 
 
+SAMPLER_VOCAB, SAMPLER_ROWS = 151936, 64
+SAMPLER_CASES = [(0.8, 40), (1.0, 8192)]  # (temperature, top_k)
+
+
+def sampler_ops(suite, stream, reps):
+    """emel-logits' native temperature/top-k sampler (sampler/sm.rs) over
+    config 5's logits: SAMPLER_ROWS sequences of a SAMPLER_VOCAB vocabulary,
+    N(0,1), sampled in one batched call.  The call rewrites the logits in
+    place (they end as probabilities), so every timed call reads a fresh
+    copy: kernel_us comes from a captured graph of back-to-back calls over
+    `copies` buffers refreshed before each replay, outside the timing.
+    alg_bytes: logits read once and probabilities written once (the outputs
+    per row are a few hundred bytes).  The CPU side is timed in
+    cpu_baseline (sampler_rows_per_s)."""
+    torch, eh = suite.torch, suite.eh
+    import ctypes
+
+    from emel_hip.abi import CSampleRows
+
+    lib = eh.load()
+    g = rng(31)
+    card, rows = SAMPLER_VOCAB, SAMPLER_ROWS
+    host = g.standard_normal((rows, card), dtype=np.float64).astype(np.float32)
+    pristine = torch.from_numpy(host.reshape(-1)).to("cuda:0")
+    alg = 2 * rows * card * 4
+    copies = max(2, -(-ROTATE_BYTES // (rows * card * 4)))
+    res = {}
+    for temperature, top_k in SAMPLER_CASES:
+        bufs = [pristine.clone() for _ in range(copies)]
+        srt = torch.empty(rows * card, dtype=torch.int32, device="cuda:0")
+        tp = torch.empty(rows * top_k, device="cuda:0")
+        ti = torch.empty(rows * top_k, dtype=torch.int32, device="cuda:0")
+        sel = torch.empty(rows, dtype=torch.int32, device="cuda:0")
+        sc = torch.empty(rows, device="cuda:0")
+        states = np.array(g.integers(1, 2147483647, rows), np.uint32)
+        cr = CSampleRows(rows, card, card, top_k)
+        reqs = [eh.SampleTemperatureTopK(card, temperature, top_k, b, srt, tp, ti, states, sel, sc).c() for b in bufs]
+
+        def call(i):
+            st = lib.emel_sample_temperature_top_k_rows(ctypes.byref(reqs[i % copies]), ctypes.byref(cr),
+                                                        ctypes.c_void_p(stream.cuda_stream))
+            if st != 0:
+                raise RuntimeError(f"sampler: {eh.Status(st).name}: {eh.last_error()}")
+
+        def refresh():
+            for b in bufs:
+                b.copy_(pristine)
+
+        with torch.cuda.stream(stream):
+            refresh()
+            times = []
+            for i in range(reps + 2):
+                refresh()
+                a = torch.cuda.Event(enable_timing=True)
+                b = torch.cuda.Event(enable_timing=True)
+                a.record(stream)
+                call(0)
+                b.record(stream)
+                b.synchronize()
+                if i >= 2:
+                    times.append(a.elapsed_time(b))
+            call_us = float(np.median(times)) * 1e3
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr, stream=stream):
+                for i in range(copies):
+                    call(i)
+            stream.synchronize()
+            ktimes = []
+            for _ in range(3):
+                refresh()
+                stream.synchronize()
+                a = torch.cuda.Event(enable_timing=True)
+                b = torch.cuda.Event(enable_timing=True)
+                a.record(stream)
+                gr.replay()
+                b.record(stream)
+                b.synchronize()
+                ktimes.append(a.elapsed_time(b) * 1e3 / copies)
+            kus = float(np.median(ktimes))
+        res[f"sample_t{temperature}_k{top_k}"] = {
+            "config": f"{rows} rows x {card} logits, temperature {temperature}, top_k {top_k}",
+            "alg_bytes": alg, "call_us": round(call_us, 2), "kernel_us": round(kus, 2),
+            "GB/s": round(alg / (kus * 1e-6) / 1e9, 1), "frac_of_peak": round(alg / (kus * 1e-6) / 1e9 / PEAK_GBS, 4),
+            "rows_per_s": round(rows / (kus * 1e-6), 1),
+            "rotation": f"{copies} logits copies refreshed before each replay"}
+        del gr, bufs, reqs
+        torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(host, budget_s=20.0):
     """Single-threaded oracle on a bounded sample of each op's workload:
     the same code path the reference's CPU kernels take (view decode,
@@ -472,7 +562,24 @@ def cpu_baseline(host, budget_s=20.0):
         per_op[name] = {"GB/s": nbytes / t / 1e9, "ms": t * 1e3}
         total_bytes += nbytes
         total_s += t
-    return total_bytes / total_s / 1e9, per_op
+    # the emel-logits sampler (not a step op): the oracle on 2 rows of the
+    # bench's sampler workload, per SAMPLER_CASES entry
+    sampler = {}
+    sg = rng(31)
+    rows = sg.standard_normal((2, SAMPLER_VOCAB), dtype=np.float64).astype(np.float32)
+    for temperature, top_k in SAMPLER_CASES:
+        t0 = time.perf_counter()
+        for r in range(2):
+            st = orc.sample_temperature_top_k(SAMPLER_VOCAB, temperature, top_k, rows[r].copy(),
+                                              np.zeros(SAMPLER_VOCAB, np.int32), np.zeros(top_k, np.float32),
+                                              np.zeros(top_k, np.int32), np.array([7], np.uint32),
+                                              np.zeros(1, np.int32), np.zeros(1, np.float32))
+            if st != orc.OK:
+                raise RuntimeError(f"oracle sampler failed: {st}")
+        t = (time.perf_counter() - t0) / 2
+        sampler[f"sample_t{temperature}_k{top_k}"] = {"rows_per_s": round(1.0 / t, 2),
+                                                      "GB/s": 2 * SAMPLER_VOCAB * 4 / t / 1e9}
+    return total_bytes / total_s / 1e9, per_op, sampler
 
 
 def host_facts():
@@ -501,6 +608,7 @@ def main():
     ap.add_argument("--no-copy", action="store_true", help="skip the same-size copy reference per op")
     ap.add_argument("--pcie", action="store_true", help="also time soft_max_ext with host-resident tensors")
     ap.add_argument("--no-gather", action="store_true", help="skip the get_rows embedding lookups")
+    ap.add_argument("--no-sampler", action="store_true", help="skip the emel-logits sampler")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -630,18 +738,24 @@ def main():
     if not args.no_gather and not args.ops:
         gather = gather_ops(suite, stream, max(10, min(args.steps, 50)))
 
+    sampler = None
+    if not args.no_sampler and not args.ops:
+        sampler = sampler_ops(suite, stream, max(5, min(args.steps, 20)))
+
     pcie = None
     if args.pcie and "soft_max_ext" in names:
         pcie = pcie_inclusive(suite, host, stream)
 
     cpu = None
     if not args.no_cpu and not args.ops:
-        cpu_gbs, cpu_ops = cpu_baseline(host)
+        cpu_gbs, cpu_ops, cpu_sampler = cpu_baseline(host)
         facts = host_facts()
         cpu = {"value": round(cpu_gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
                "sample": "C oracle (single-threaded restatement of the reference CPU path) on 1/8 of every "
-                         "op's rows/heads, median of 3, algorithmic bytes / time",
-               "host": facts, "per_op": {k: round(v["GB/s"], 3) for k, v in cpu_ops.items()}}
+                         "op's rows/heads, median of 3, algorithmic bytes / time; sampler: 2 rows of its workload",
+               "host": facts, "per_op": {k: round(v["GB/s"], 3) for k, v in cpu_ops.items()},
+               "sampler": {k: {"rows_per_s": v["rows_per_s"], "GB/s": round(v["GB/s"], 4)}
+                           for k, v in cpu_sampler.items()}}
 
     out = {
         "metric": METRIC,
@@ -667,6 +781,7 @@ def main():
         "per_op": per_op,
         "extra_ops": extra_ops,
         "gather_ops": gather,
+        "sampler_ops": sampler,
         "roofline": roof,
         "cpu_baseline": cpu,
         "pcie_inclusive": pcie,

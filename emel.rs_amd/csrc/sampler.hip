@@ -54,7 +54,6 @@ namespace {
 constexpr uint32_t kCap = 8192;          // candidates sorted in LDS by one workgroup
 constexpr uint32_t kRankThreads = 1024;
 constexpr uint32_t kSumThreads = 1024;
-constexpr uint32_t kSumPer = 16;         // elements per thread and tile of k_smp_sum
 constexpr uint32_t kBins = 2048;         // 11-bit radix digits
 constexpr uint32_t kNone = 0xffffffffu;
 constexpr uint32_t kModulus = 2147483647u;   // sampler/sm.rs:22
@@ -230,154 +229,225 @@ __global__ __launch_bounds__(kBlock) void k_smp_exp(SmpGeo g, float *logits, Smp
 
 // ---- stage 3: the exact sequential sum of e ----------------------------------
 //
-// One workgroup per row walks the row in tiles of kSumThreads * kSumPer
-// elements; thread t holds the kSumPer consecutive elements
-// [tile + kSumPer t, tile + kSumPer (t+1)).  A round computes every element's
-// units at the current binade, a workgroup-wide prefix sum of them, and
-// either commits the whole remaining tile (no event) or finds the first
-// event element, adds it with one f32 addition, and starts the next round
-// after it.  Each round commits at least one element, so the loop ends.
+// One workgroup per row walks the row in tiles; thread t holds PER
+// consecutive elements [tile + PER t, tile + PER (t+1)).  A round computes
+// every element's units at the current binade and a workgroup-wide prefix
+// sum of them, and either commits the rest of the tile (no event) or finds
+// the first event element, adds it with one f32 addition, and starts the
+// next round after it.  Each round commits at least one element, so the
+// rounds end.  The running sum crosses most binades early in a row (it
+// roughly doubles whenever the element count doubles), so the first tiles
+// are small (PER = 1, 2, 4, 8): a round over them is cheap.  From then on
+// tiles hold 16 elements per thread, and the next tile's loads are issued
+// before the current tile's rounds.
 
-__global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *logits, SmpWs w)
+struct SumState {
+    uint32_t m;
+    int32_t u;
+    uint32_t parity;
+    bool finite;
+    float special; // NaN or +inf once the running sum leaves the finite range
+};
+
+struct SumShared {
+    uint32_t wsum[2][kSumThreads / kWave]; // per-wave units (saturated) | tie flag << 31, by round parity
+    uint32_t first[kSumThreads / kWave];   // per-wave first event element
+    float next[kSumThreads / kWave];       // the sum after that element
+};
+
+template <uint32_t PER>
+__device__ __forceinline__ void load_tile(const SmpGeo &g, const float *x, uint64_t base, float (&e)[PER])
 {
-    constexpr uint32_t kWaves = kSumThreads / kWave;
-    constexpr uint32_t kTile = kSumThreads * kSumPer;
-    __shared__ uint32_t s_wsum[2][kWaves];  // per-wave unit totals (saturated), by round parity
-    __shared__ uint32_t s_wtie[2][kWaves];
-    __shared__ uint32_t s_first[kWaves];
-    __shared__ float s_next;
-
-    const uint32_t row = blockIdx.x;
-    const float *x = logits + static_cast<int64_t>(row) * g.ld;
-    const uint32_t t = threadIdx.x, lane = t % kWave, wave = t / kWave;
-    const uint64_t n = g.card;
-
-    uint32_t m = 0;
-    int32_t u = -149;
-    float special = 0.0f; // NaN or +inf once the running sum leaves the finite range
-    bool finite = true;
-    uint32_t parity = 0;
-
-    for (uint64_t base = 0; base < n; base += kTile) {
-        float e[kSumPer];
-        const uint64_t first_col = base + static_cast<uint64_t>(kSumPer) * t;
-        if (g.vec && first_col + kSumPer <= n) {
-            const float4 *p4 = reinterpret_cast<const float4 *>(x + first_col);
+    const uint64_t c = base + static_cast<uint64_t>(PER) * threadIdx.x;
+    if constexpr (PER % 4 == 0) {
+        if (g.vec && c + PER <= g.card) {
+            const float4 *p4 = reinterpret_cast<const float4 *>(x + c);
 #pragma unroll
-            for (uint32_t j = 0; j < kSumPer / 4; ++j) {
+            for (uint32_t j = 0; j < PER / 4; ++j) {
                 const float4 q = p4[j];
                 e[4 * j] = q.x;
                 e[4 * j + 1] = q.y;
                 e[4 * j + 2] = q.z;
                 e[4 * j + 3] = q.w;
             }
-        } else {
-#pragma unroll
-            for (uint32_t j = 0; j < kSumPer; ++j) e[j] = first_col + j < n ? x[first_col + j] : 0.0f;
-        }
-        if (!finite) {
-            // +inf stays +inf unless a NaN follows; NaN stays NaN
-            bool nan = false;
-#pragma unroll
-            for (uint32_t j = 0; j < kSumPer; ++j) nan |= e[j] != e[j];
-            if (__syncthreads_or(nan)) special = __builtin_nanf("");
-            continue;
-        }
-        uint32_t start = 0; // tile-relative index of the first uncommitted element
-        while (true) {
-            uint32_t r[kSumPer];
-            uint32_t lsum = 0;
-            bool ltie = false;
-#pragma unroll
-            for (uint32_t j = 0; j < kSumPer; ++j) {
-                const uint32_t idx = kSumPer * t + j;
-                bool tie;
-                const uint32_t q = seq_units(e[j], u, tie);
-                const bool active = idx >= start;
-                r[j] = active ? q : 0u;
-                ltie |= active && tie;
-                lsum += r[j];
-            }
-            // lsum <= 16 * 2^24 = 2^28; saturate at 2^24 so the scans cannot
-            // overflow (a saturated value already marks a crossing)
-            uint32_t x_in = lsum < kSeqLimit ? lsum : kSeqLimit;
-            uint32_t incl = x_in;
-#pragma unroll
-            for (int off = 1; off < kWave; off <<= 1) {
-                const uint32_t o = __shfl_up(incl, off, kWave);
-                if (lane >= static_cast<uint32_t>(off)) incl += o;
-            }
-            const uint64_t tmask = __ballot(ltie);
-            if (lane == kWave - 1) {
-                s_wsum[parity][wave] = incl < kSeqLimit ? incl : kSeqLimit;
-                s_wtie[parity][wave] = tmask != 0;
-            }
-            __syncthreads();
-            uint32_t before = 0, total = 0, anytie = 0;
-#pragma unroll
-            for (uint32_t v = 0; v < kWaves; ++v) {
-                const uint32_t ws = s_wsum[parity][v];
-                before += v < wave ? ws : 0u;
-                total += ws;
-                anytie |= s_wtie[parity][v];
-            }
-            parity ^= 1u;
-            if (!anytie && m + total < kSeqLimit) {
-                m += total;
-                break; // tile committed
-            }
-            // first event element of this thread
-            uint32_t run = m + before + (incl - x_in); // units before this thread's first element
-            uint32_t mine = kNone;
-#pragma unroll
-            for (uint32_t j = 0; j < kSumPer; ++j) {
-                const uint32_t idx = kSumPer * t + j;
-                bool tie;
-                (void)seq_units(e[j], u, tie);
-                if (mine == kNone && idx >= start) {
-                    if (tie || run + r[j] >= kSeqLimit) mine = idx;
-                    else run += r[j];
-                }
-            }
-            const uint64_t emask = __ballot(mine != kNone);
-            const uint32_t wfirst = emask ? __shfl(mine, __builtin_ctzll(emask), kWave) : kNone;
-            if (lane == 0) s_first[wave] = wfirst;
-            __syncthreads();
-            uint32_t k = kNone;
-#pragma unroll
-            for (uint32_t v = 0; v < kWaves; ++v) k = s_first[v] < k ? s_first[v] : k;
-            if (k == kNone) break; // unreachable: a tie or a crossing has a first element
-            if (k / kSumPer == t) {
-                // every element before k adds its units exactly; k itself is
-                // one real f32 addition
-                const float before_k = seq_value(run, u);
-                float ek = e[0];
-#pragma unroll
-                for (uint32_t j = 1; j < kSumPer; ++j) ek = (k % kSumPer == j) ? e[j] : ek;
-                s_next = before_k + ek;
-            }
-            __syncthreads();
-            // s_next and s_first are rewritten only after the next round's
-            // first barrier, which every thread reaches after this read
-            const float sn = s_next;
-            if (!(sn < __builtin_inff())) { // NaN or +inf
-                special = sn;
-                finite = false;
-                // the rest of this tile can only turn +inf into NaN
-                bool nan = false;
-#pragma unroll
-                for (uint32_t j = 0; j < kSumPer; ++j) nan |= (kSumPer * t + j > k) && e[j] != e[j];
-                if (__syncthreads_or(nan)) special = __builtin_nanf("");
-                break;
-            }
-            const SeqState st = seq_state(sn);
-            m = st.m;
-            u = st.u;
-            start = k + 1;
-            if (start >= kTile) break;
+            return;
         }
     }
-    if (t == 0) w.sel[row].total = finite ? seq_value(m, u) : special;
+#pragma unroll
+    for (uint32_t j = 0; j < PER; ++j) e[j] = c + j < g.card ? x[c + j] : 0.0f;
+}
+
+template <uint32_t PER>
+__device__ __forceinline__ void sum_tile(const float (&e)[PER], SumState &s, SumShared &sh)
+{
+    constexpr uint32_t kWaves = kSumThreads / kWave;
+    constexpr uint32_t kTile = kSumThreads * PER;
+    const uint32_t t = threadIdx.x, lane = t % kWave, wave = t / kWave;
+    if (!s.finite) {
+        // +inf stays +inf unless a NaN follows; NaN stays NaN
+        bool nan = false;
+#pragma unroll
+        for (uint32_t j = 0; j < PER; ++j) nan |= e[j] != e[j];
+        if (__syncthreads_or(nan)) s.special = __builtin_nanf("");
+        return;
+    }
+    uint32_t start = 0; // tile-relative index of the first uncommitted element
+    while (true) {
+        // units are not kept: the no-event path needs only their sum, and
+        // an event round recomputes them (fewer live registers)
+        uint32_t ties = 0; // bit j: element j is a tie
+        uint32_t lsum = 0;
+        if (start == 0) {
+#pragma unroll
+            for (uint32_t j = 0; j < PER; ++j) {
+                bool tie;
+                lsum += seq_units(e[j], s.u, tie);
+                ties |= static_cast<uint32_t>(tie) << j;
+            }
+        } else { // elements before start are committed
+#pragma unroll
+            for (uint32_t j = 0; j < PER; ++j) {
+                bool tie;
+                const uint32_t q = seq_units(e[j], s.u, tie);
+                const bool active = PER * t + j >= start;
+                lsum += active ? q : 0u;
+                ties |= static_cast<uint32_t>(active && tie) << j;
+            }
+        }
+        // lsum <= PER * 2^24; saturate at 2^24 so the scans cannot overflow
+        // (a saturated value already marks a crossing)
+        const uint32_t x_in = lsum < kSeqLimit ? lsum : kSeqLimit;
+        uint32_t incl = x_in;
+#pragma unroll
+        for (int off = 1; off < kWave; off <<= 1) {
+            const uint32_t o = __shfl_up(incl, off, kWave);
+            if (lane >= static_cast<uint32_t>(off)) incl += o;
+        }
+        const bool wtie = __ballot(ties != 0) != 0;
+        if (lane == kWave - 1) sh.wsum[s.parity][wave] = (incl < kSeqLimit ? incl : kSeqLimit) | (wtie ? 0x80000000u : 0u);
+        __syncthreads();
+        uint32_t before = 0, total = 0, anytie = 0;
+#pragma unroll
+        for (uint32_t v = 0; v < kWaves; ++v) {
+            const uint32_t ws = sh.wsum[s.parity][v];
+            before += v < wave ? (ws & 0x7fffffffu) : 0u;
+            total += ws & 0x7fffffffu;
+            anytie |= ws >> 31;
+        }
+        s.parity ^= 1u;
+        if (!anytie && s.m + total < kSeqLimit) {
+            s.m += total;
+            return; // tile committed
+        }
+        // this thread's first event element, and the sum just before it
+        uint32_t run = s.m + before + (incl - x_in);
+        uint32_t mine = kNone;
+        float ek = 0.0f;
+#pragma unroll
+        for (uint32_t j = 0; j < PER; ++j) {
+            if (mine == kNone && PER * t + j >= start) {
+                bool tie;
+                const uint32_t q = seq_units(e[j], s.u, tie);
+                if (tie || run + q >= kSeqLimit) {
+                    mine = PER * t + j;
+                    ek = e[j];
+                } else {
+                    run += q;
+                }
+            }
+        }
+        // the wave's first event (its lowest lane with one) adds it and
+        // publishes both the position and the new sum
+        const uint64_t emask = __ballot(mine != kNone);
+        if (emask && lane == static_cast<uint32_t>(__builtin_ctzll(emask))) {
+            sh.first[wave] = mine;
+            sh.next[wave] = seq_value(run, s.u) + ek;
+        } else if (!emask && lane == 0) {
+            sh.first[wave] = kNone;
+        }
+        __syncthreads();
+        uint32_t k = kNone;
+        float sn = 0.0f;
+#pragma unroll
+        for (uint32_t v = 0; v < kWaves; ++v) {
+            const uint32_t f = sh.first[v];
+            if (f < k) {
+                k = f;
+                sn = sh.next[v];
+            }
+        }
+        // sh.first / sh.next are rewritten only after the next round's first
+        // barrier, which every thread reaches after these reads
+        if (k == kNone) return; // unreachable: a tie or a crossing has a first element
+        if (!(sn < __builtin_inff())) { // NaN or +inf
+            s.special = sn;
+            s.finite = false;
+            bool nan = false;
+#pragma unroll
+            for (uint32_t j = 0; j < PER; ++j) nan |= (PER * t + j > k) && e[j] != e[j];
+            if (__syncthreads_or(nan)) s.special = __builtin_nanf("");
+            return;
+        }
+        const SeqState st = seq_state(sn);
+        s.m = st.m;
+        s.u = st.u;
+        start = k + 1;
+        if (start >= kTile) return;
+    }
+}
+
+__global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *logits, SmpWs w)
+{
+    __shared__ SumShared sh;
+    const uint32_t row = blockIdx.x;
+    const float *x = logits + static_cast<int64_t>(row) * g.ld;
+    const uint64_t n = g.card;
+    SumState s{0u, -149, 0u, true, 0.0f};
+    uint64_t base = 0;
+    // warm-up tiles of 1, 2, 4 and 8 elements per thread
+    {
+        float e[1];
+        load_tile<1>(g, x, base, e);
+        sum_tile<1>(e, s, sh);
+        base += kSumThreads;
+    }
+    if (base < n) {
+        float e[2];
+        load_tile<2>(g, x, base, e);
+        sum_tile<2>(e, s, sh);
+        base += 2 * kSumThreads;
+    }
+    if (base < n) {
+        float e[4];
+        load_tile<4>(g, x, base, e);
+        sum_tile<4>(e, s, sh);
+        base += 4 * kSumThreads;
+    }
+    if (base < n) {
+        float e[8];
+        load_tile<8>(g, x, base, e);
+        sum_tile<8>(e, s, sh);
+        base += 8 * kSumThreads;
+    }
+    // steady state: 16 per thread, the next tile in flight
+    constexpr uint64_t kTile = 16ull * kSumThreads;
+    if (base < n) {
+        float a[16], b[16];
+        load_tile<16>(g, x, base, a);
+        while (true) {
+            const bool more = base + kTile < n;
+            if (more) load_tile<16>(g, x, base + kTile, b);
+            sum_tile<16>(a, s, sh);
+            base += kTile;
+            if (!more) break;
+            const bool more2 = base + kTile < n;
+            if (more2) load_tile<16>(g, x, base + kTile, a);
+            sum_tile<16>(b, s, sh);
+            base += kTile;
+            if (!more2) break;
+        }
+    }
+    if (threadIdx.x == 0) w.sel[row].total = s.finite ? seq_value(s.m, s.u) : s.special;
 }
 
 // ---- stage 4: p = e / S in place, first radix digit -------------------------
@@ -527,76 +597,92 @@ __global__ __launch_bounds__(kBlock) void k_smp_ties(SmpGeo g, float *logits, Sm
 }
 
 // ---- stage 8: candidates ------------------------------------------------------
-
-__device__ __forceinline__ void push_cand(const SmpGeo &g, const SmpWs &w, uint32_t row, uint32_t key, uint64_t col)
-{
-    const uint32_t slot = atomicAdd(&w.sel[row].written, 1u);
-    // the selection counted exactly `count` <= cand_ld candidates; the bound
-    // only keeps a miscount from writing outside the row's list
-    if (slot < g.cand_ld) w.cand[static_cast<uint64_t>(row) * g.cand_ld + slot] = cand_word(key, static_cast<uint32_t>(col));
-}
+//
+// Steps of 4 consecutive columns per thread (1024 per workgroup): each step
+// counts its candidates, one workgroup prefix sum places them, and one atomic
+// per step that has any reserves their slots in the row's list.  The order
+// of the list is irrelevant (it is sorted next); the count is exact.
 
 __global__ __launch_bounds__(kBlock) void k_smp_collect(SmpGeo g, float *logits, SmpWs w)
 {
     __shared__ uint32_t s_tmp[2][kBlock / kWave];
+    __shared__ uint32_t s_base;
     const uint32_t row = blockIdx.x / g.chunks, chunk = blockIdx.x % g.chunks;
     const RowSel sel = w.sel[row];
     float *x = logits + static_cast<int64_t>(row) * g.ld;
+    uint64_t *list = w.cand + static_cast<uint64_t>(row) * g.cand_ld;
     uint64_t c0, c1;
     chunk_range(g, chunk, c0, c1);
-    if (sel.mode == 1) {
-        const uint32_t dshift = 32u - sel.depth;
-        const uint64_t prefix = sel.prefix;
-        visit<false>(g, x, c0, c1, [&](float &v, uint64_t col) {
-            const uint32_t key = total_key(v);
-            if ((static_cast<uint64_t>(key) >> dshift) >= prefix) push_cand(g, w, row, key, col);
-        });
-        return;
-    }
-    // mode 2: keys > T, and the ties at T in column order until `need` are taken
+    const bool exact = sel.mode == 2;
     const uint32_t T = sel.prefix;
+    const uint32_t dshift = 32u - sel.depth;
+    // mode 2: ties at T in the chunks before this one
     uint32_t tie_base = 0;
-    for (uint32_t c = threadIdx.x; c < chunk; c += blockDim.x) tie_base += w.ties[static_cast<uint64_t>(row) * g.chunks + c];
-    {
-        uint32_t tb;
-        (void)block_incl_scan256(tie_base, s_tmp[0], tb);
-        tie_base = tb;
+    if (exact) {
+        uint32_t mine = 0;
+        for (uint32_t c = threadIdx.x; c < chunk; c += blockDim.x) mine += w.ties[static_cast<uint64_t>(row) * g.chunks + c];
+        (void)block_incl_scan256(mine, s_tmp[0], tie_base);
+        __syncthreads();
     }
-    __syncthreads();
-    if (tie_base >= sel.need) {
-        visit<false>(g, x, c0, c1, [&](float &v, uint64_t col) {
-            const uint32_t key = total_key(v);
-            if (key > T) push_cand(g, w, row, key, col);
-        });
-        return;
-    }
-    // ordered steps of 4 consecutive columns per thread
     uint32_t par = 1;
     for (uint64_t blk = c0; blk < c1; blk += 4 * kBlock) {
         const uint64_t col0 = blk + 4 * static_cast<uint64_t>(threadIdx.x);
-        float v[4];
-        uint32_t mine = 0;
+        uint32_t key[4];
+        bool in[4];
+        if (g.vec && col0 + 4 <= c1) {
+            const float4 q = *reinterpret_cast<const float4 *>(x + col0);
+            key[0] = total_key(q.x);
+            key[1] = total_key(q.y);
+            key[2] = total_key(q.z);
+            key[3] = total_key(q.w);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            v[j] = col0 + j < c1 ? x[col0 + j] : -__builtin_nanf("");
-            mine += (col0 + j < c1 && total_key(v[j]) == T) ? 1u : 0u;
-        }
-        uint32_t total;
-        const uint32_t incl = block_incl_scan256(mine, s_tmp[par], total);
-        par ^= 1u;
-        uint32_t rank = tie_base + incl - mine;
+            for (int j = 0; j < 4; ++j) in[j] = true;
+        } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            if (col0 + j >= c1) break;
-            const uint32_t key = total_key(v[j]);
-            if (key > T) {
-                push_cand(g, w, row, key, col0 + j);
-            } else if (key == T) {
-                if (rank < sel.need) push_cand(g, w, row, key, col0 + j);
-                ++rank;
+            for (int j = 0; j < 4; ++j) {
+                in[j] = col0 + j < c1;
+                key[j] = in[j] ? total_key(x[col0 + j]) : 0u;
             }
         }
-        tie_base += total;
+        bool take[4];
+        if (!exact) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) take[j] = in[j] && (key[j] >> dshift) >= T;
+        } else {
+            // ties at T are taken in column order while fewer than `need` precede them
+            uint32_t nt = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) nt += (in[j] && key[j] == T) ? 1u : 0u;
+            uint32_t step_ties;
+            const uint32_t incl = block_incl_scan256(nt, s_tmp[par], step_ties);
+            par ^= 1u;
+            uint32_t rank = tie_base + incl - nt;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const bool tie = in[j] && key[j] == T;
+                take[j] = (in[j] && key[j] > T) || (tie && rank < sel.need);
+                rank += tie ? 1u : 0u;
+            }
+            tie_base += step_ties;
+        }
+        uint32_t nc = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) nc += take[j] ? 1u : 0u;
+        uint32_t step_total;
+        const uint32_t cincl = block_incl_scan256(nc, s_tmp[par], step_total);
+        par ^= 1u;
+        if (step_total == 0) continue; // uniform
+        if (threadIdx.x == 0) s_base = atomicAdd(&w.sel[row].written, step_total);
+        __syncthreads();
+        uint32_t slot = s_base + cincl - nc;
+        __syncthreads(); // s_base is rewritten by the next step
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            // the selection counted exactly `count` <= cand_ld candidates; the
+            // bound only keeps a miscount from writing outside the row's list
+            if (take[j] && slot < g.cand_ld) list[slot] = cand_word(key[j], static_cast<uint32_t>(col0 + j));
+            slot += take[j] ? 1u : 0u;
+        }
     }
 }
 

@@ -55,17 +55,22 @@ bool differ(float a, float b)
 // threads * per elements; a round commits the rest of the tile when no
 // element is an event, else commits up to the first event and adds that
 // element with one f32 addition.  Exact (unsaturated) prefix sums.
+// per == 0 selects k_smp_sum's schedule: tiles of threads * {1, 2, 4, 8}
+// elements, then threads * 16 to the end.
 float seqsum_blocked(const float *e, uint64_t n, uint32_t threads, uint32_t per)
 {
     uint32_t m = 0;
     int32_t u = -149;
     bool finite = true;
     float special = 0.0f;
-    const uint64_t tile = static_cast<uint64_t>(threads) * per;
-    std::vector<float> ev(tile);
-    std::vector<uint32_t> r(tile);
-    std::vector<uint8_t> tie(tile);
-    for (uint64_t base = 0; base < n; base += tile) {
+    const uint64_t max_tile = static_cast<uint64_t>(threads) * (per ? per : 16);
+    std::vector<float> ev(max_tile);
+    std::vector<uint32_t> r(max_tile);
+    std::vector<uint8_t> tie(max_tile);
+    uint32_t warm = 0;
+    for (uint64_t base = 0, tile = 0; base < n; base += tile) {
+        tile = static_cast<uint64_t>(threads) * (per ? per : (warm < 4 ? (1u << warm) : 16u));
+        ++warm;
         for (uint64_t i = 0; i < tile; ++i) ev[i] = base + i < n ? e[base + i] : 0.0f;
         if (!finite) {
             for (uint64_t i = 0; i < tile; ++i)
@@ -161,7 +166,7 @@ extern "C" float seqsum_blocked_f(const float *e, uint64_t n, uint32_t threads, 
 extern "C" uint64_t check_seqsum(uint64_t seed, int cases, uint64_t max_n)
 {
     uint64_t z = seed, bad = 0;
-    const uint32_t shapes[3][2] = {{1024, 16}, {4, 2}, {64, 1}};
+    const uint32_t shapes[4][2] = {{1024, 0}, {1024, 16}, {4, 2}, {64, 1}};
     for (int c = 0; c < cases; ++c) {
         const int family = c % 5;
         const uint64_t n = 1 + splitmix(z) % max_n;

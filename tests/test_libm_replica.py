@@ -88,8 +88,9 @@ def test_exact_sequential_sum_rounds(chk):
     crossings, NaN and +inf taken as single f32 additions, must give the
     bits of a plain sequential f32 loop.  Families: softmax-like values,
     dyadic values full of exact ties, zeros and subnormals, every magnitude,
-    planted NaN / +inf; tiles of the kernel's shape (1024 x 16) and of small
-    shapes that force many rounds.  Ignoring ties or letting a binade run to
+    planted NaN / +inf; the kernel's tile schedule (1024 threads, 1, 2, 4,
+    8 then 16 elements each), fixed 1024 x 16 tiles, and small shapes that
+    force many rounds.  Ignoring ties or letting a binade run to
     2^25 units makes this check fail (1275 and 4950 mismatching cases)."""
     chk.check_seqsum.restype = ctypes.c_uint64
     chk.check_seqsum.argtypes = [ctypes.c_uint64, ctypes.c_int, ctypes.c_uint64]
