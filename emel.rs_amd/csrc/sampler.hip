@@ -17,9 +17,13 @@
 // Kernels, in launch order (the same sequence for every request; rows that
 // finish a stage early skip the later ones):
 //   k_smp_max     (row, chunk) workgroups: chunk maxima of v.
-//   k_smp_exp     (row, chunk): e written in place.
-//   k_smp_sum     one 1024-thread workgroup per row: the exact sequential sum
-//                 through integer units per binade (seqsum.hpp).
+//   k_smp_exp     (row, chunk): e written in place, and the chunk's f64 sum.
+//   k_smp_seg     (row, chunk): the chunk's exact contribution in units of
+//                 the binade its f64 prefix predicts.
+//   k_smp_sum     one workgroup per row: the exact sequential sum
+//                 (seqsum.hpp), taking a chunk's predicted contribution when
+//                 the exact state confirms it, walking the other chunks from
+//                 LDS.
 //   k_smp_div     (row, chunk): p written in place, plus the histogram of the
 //                 top 11 bits of p's total-order key.
 //   k_smp_pick / k_smp_refine
@@ -53,7 +57,6 @@ namespace {
 
 constexpr uint32_t kCap = 8192;          // candidates sorted in LDS by one workgroup
 constexpr uint32_t kRankThreads = 1024;
-constexpr uint32_t kSumThreads = 1024;
 constexpr uint32_t kBins = 2048;         // 11-bit radix digits
 constexpr uint32_t kNone = 0xffffffffu;
 constexpr uint32_t kModulus = 2147483647u;   // sampler/sm.rs:22
@@ -84,8 +87,22 @@ struct SmpGeo {
     uint32_t cand_ld;    // candidate slots per row
 };
 
+// A sub-chunk's contribution to the row's exact sum, computed ahead of the
+// walk at a predicted binade (k_smp_seg): units (+1 when `tie` and the
+// running units plus `par` are odd) of 2^u, when ok.
+constexpr uint32_t kSub = 1024;  // elements per sub-chunk (one walk round)
+constexpr uint32_t kMaxSub = 64; // sub-chunks a chunk predicts; later ones are walked
+struct SegInfo {
+    uint32_t units; // saturates at 2^25: the walk rejects anything >= 2^24
+    int32_t u;
+    uint32_t flags; // bit 0 ok, bit 1 one tie, bit 2 its parity, bit 3 empty slot
+    uint32_t pad;
+};
+
 struct SmpWs {
     float *part;   // rows * chunks chunk maxima
+    double *psum;  // rows * chunks f64 sums of e per chunk (binade prediction)
+    SegInfo *seg;  // rows * chunks * subs per chunk
     RowSel *sel;   // rows
     uint32_t *hist; // rows * kBins
     uint32_t *ties; // rows * chunks
@@ -173,6 +190,19 @@ __device__ __forceinline__ float block_max256(float v)
     return r;
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave (DPP: row shifts within
+// rows of 16 lanes, then the row broadcasts of lanes 15 and 31).
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v)
+{
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x111, 0xf, 0xf, true)); // row_shr:1
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x112, 0xf, 0xf, true)); // row_shr:2
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x114, 0xf, 0xf, true)); // row_shr:4
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x118, 0xf, 0xf, true)); // row_shr:8
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x142, 0xa, 0xf, false)); // row_bcast:15
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x143, 0xc, 0xf, false)); // row_bcast:31
+    return v;
+}
+
 // ---- stage 1: chunk maxima of v = x * scale ---------------------------------
 
 __global__ __launch_bounds__(kBlock) void k_smp_max(SmpGeo g, float *logits, SmpWs w)
@@ -221,82 +251,188 @@ __global__ __launch_bounds__(kBlock) void k_smp_exp(SmpGeo g, float *logits, Smp
     chunk_range(g, chunk, c0, c1);
     const float scale = g.scale;
     const ExpfConsts ec = expf_consts_in_vgprs();
+    double acc = 0.0;
     visit<true>(g, x, c0, c1, [&](float &v, uint64_t) {
         const float s = v * scale;
         v = emel_expf(s - m, kExp2Table, ec);
+        acc += static_cast<double>(v);
     });
+    // f64 chunk sum: only a prediction of where the exact sum's binades
+    // change (k_smp_seg); never part of a result
+    __shared__ double s_acc[kBlock / kWave];
+    acc = wave_sum(acc);
+    if (threadIdx.x % kWave == 0) s_acc[threadIdx.x / kWave] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) w.psum[blockIdx.x] = (s_acc[0] + s_acc[1]) + (s_acc[2] + s_acc[3]);
 }
 
-// ---- stage 3: the exact sequential sum of e ----------------------------------
+// ---- stage 2b: chunk contributions at a predicted binade --------------------
 //
-// One workgroup per row walks the row in tiles; thread t holds PER
-// consecutive elements [tile + PER t, tile + PER (t+1)).  A round computes
-// every element's units at the current binade and a workgroup-wide prefix
-// sum of them, and either commits the rest of the tile (no event) or finds
-// the first event element, adds it with one f32 addition, and starts the
-// next round after it.  Each round commits at least one element, so the
-// rounds end.  The running sum crosses most binades early in a row (it
-// roughly doubles whenever the element count doubles), so the first tiles
-// are small (PER = 1, 2, 4, 8): a round over them is cheap.  From then on
-// tiles hold 16 elements per thread, and the next tile's loads are issued
-// before the current tile's rounds.
+// The exact running sum at the start of chunk c is the f64 prefix P of the
+// chunk sums up to the accumulated rounding of the steps before it: each
+// step rounds by at most 2^-24 of the running sum, which never decreases,
+// so the true value lies within P (1 +- (c0 2^-24 + 2^-30)) -- and likewise
+// at the chunk's end.  When both bounds share one binade, the chunk adds a
+// whole number of units of that binade; this kernel counts them.  The walk
+// (k_smp_sum) takes the count only after checking, on the exact state, that
+// the binade is the predicted one and that the units fit below 2^24: the
+// bound steers the work, the checks decide correctness.
 
-struct SumState {
-    uint32_t m;
-    int32_t u;
-    uint32_t parity;
-    bool finite;
-    float special; // NaN or +inf once the running sum leaves the finite range
-};
-
-struct SumShared {
-    uint32_t wsum[2][kSumThreads / kWave]; // per-wave units (saturated) | tie flag << 31, by round parity
-    uint32_t first[kSumThreads / kWave];   // per-wave first event element
-    float next[kSumThreads / kWave];       // the sum after that element
-};
-
-template <uint32_t PER>
-__device__ __forceinline__ void load_tile(const SmpGeo &g, const float *x, uint64_t base, float (&e)[PER])
+__device__ __forceinline__ uint32_t subs_per_chunk(const SmpGeo &g)
 {
-    const uint64_t c = base + static_cast<uint64_t>(PER) * threadIdx.x;
-    if constexpr (PER % 4 == 0) {
-        if (g.vec && c + PER <= g.card) {
-            const float4 *p4 = reinterpret_cast<const float4 *>(x + c);
+    return static_cast<uint32_t>((g.chunk_cols + kSub - 1) / kSub);
+}
+
+// One 256-thread workgroup per (row, chunk); wave w predicts sub-chunks
+// w, w + 4, ... from its 16 elements per lane.  A sub-chunk with one tie is
+// still usable: the tie rounds its sum to an even number of units, so it
+// adds q or q + 1 units depending on the parity of the units before it,
+// recorded as `par`.
+__global__ __launch_bounds__(kBlock) void k_smp_seg(SmpGeo g, float *logits, SmpWs w)
+{
+    __shared__ double s_red[kBlock / kWave];
+    __shared__ double s_sub[kMaxSub];
+    const uint32_t row = blockIdx.x / g.chunks, chunk = blockIdx.x % g.chunks;
+    const uint32_t lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    double pre = 0.0;
+    for (uint32_t c = threadIdx.x; c < chunk; c += blockDim.x) pre += w.psum[static_cast<uint64_t>(row) * g.chunks + c];
+    pre = wave_sum(pre);
+    if (lane == 0) s_red[wave] = pre;
+    __syncthreads();
+    const double P = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+    uint64_t c0, c1;
+    chunk_range(g, chunk, c0, c1);
+    const uint32_t spc = subs_per_chunk(g);
+    const uint32_t nsub = static_cast<uint32_t>((c1 - c0 + kSub - 1) / kSub);
+    const uint32_t npred = nsub < kMaxSub ? nsub : kMaxSub;
+    SegInfo *out = w.seg + (static_cast<uint64_t>(row) * g.chunks + chunk) * spc;
+    const float *x = logits + static_cast<int64_t>(row) * g.ld;
+    auto load16 = [&](uint32_t k, float (&e)[16]) {
+        const uint64_t first = c0 + static_cast<uint64_t>(k) * kSub + 16 * lane;
+        if (g.vec && first + 16 <= c1) {
+            const float4 *p4 = reinterpret_cast<const float4 *>(x + first);
 #pragma unroll
-            for (uint32_t j = 0; j < PER / 4; ++j) {
+            for (uint32_t j = 0; j < 4; ++j) {
                 const float4 q = p4[j];
                 e[4 * j] = q.x;
                 e[4 * j + 1] = q.y;
                 e[4 * j + 2] = q.z;
                 e[4 * j + 3] = q.w;
             }
-            return;
-        }
-    }
+        } else {
 #pragma unroll
-    for (uint32_t j = 0; j < PER; ++j) e[j] = c + j < g.card ? x[c + j] : 0.0f;
+            for (uint32_t j = 0; j < 16; ++j) e[j] = first + j < c1 ? x[first + j] : 0.0f;
+        }
+    };
+    // pass A: f64 sum of every sub-chunk
+    for (uint32_t k = wave; k < npred; k += kBlock / kWave) {
+        float e[16];
+        load16(k, e);
+        double acc = 0.0;
+#pragma unroll
+        for (uint32_t j = 0; j < 16; ++j) acc += static_cast<double>(e[j]);
+        acc = wave_sum(acc);
+        if (lane == 0) s_sub[k] = acc;
+    }
+    __syncthreads();
+    // slots past the chunk's last sub-chunk (only in a shorter last chunk)
+    // are empty: they add nothing, whatever the state
+    for (uint32_t k = nsub + threadIdx.x; k < spc; k += blockDim.x) out[k] = SegInfo{0, 0, 8u, 0};
+    // pass B: the prediction per sub-chunk
+    for (uint32_t k = wave; k < nsub; k += kBlock / kWave) {
+        SegInfo info{0, 0, 0, 0};
+        const uint64_t a0 = c0 + static_cast<uint64_t>(k) * kSub;
+        const uint64_t a1 = a0 + kSub < c1 ? a0 + kSub : c1;
+        if (k < npred) {
+            double Pk = P;
+            for (uint32_t i = 0; i < k; ++i) Pk += s_sub[i];
+            const double lo = Pk * (1.0 - (static_cast<double>(a0) * 0x1p-24 + 0x1p-30));
+            const double hi = (Pk + s_sub[k]) * (1.0 + (static_cast<double>(a1) * 0x1p-24 + 0x1p-30));
+            int elo = 0, ehi = 0;
+            (void)__builtin_frexp(lo, &elo);
+            (void)__builtin_frexp(hi, &ehi);
+            // normal f32 range, both bounds in one binade [2^(elo-1), 2^elo)
+            if (lo >= 0x1p-126 && hi < 0x1p127 && lo <= hi && elo == ehi) { // uniform
+                const int32_t u = elo - 1 - 23;
+                float e[16];
+                load16(k, e);
+                uint32_t lsum = 0, ties = 0, tq = 0, tbefore = 0;
+#pragma unroll
+                for (uint32_t j = 0; j < 16; ++j) {
+                    bool tie;
+                    const uint32_t r = seq_units(e[j], u, tie);
+                    // a tie counts its lower neighbour q here (r is q or q + 1)
+                    const uint32_t q = tie ? static_cast<uint32_t>(__builtin_floorf(__builtin_ldexpf(e[j], -u))) : r;
+                    if (tie && ties == 0) {
+                        tq = q;
+                        tbefore = lsum;
+                    }
+                    ties += tie ? 1u : 0u;
+                    lsum += q;
+                    lsum = lsum < (1u << 25) ? lsum : (1u << 25);
+                }
+                const uint32_t incl = wave_incl_scan(lsum < kSeqLimit ? lsum : kSeqLimit);
+                const uint32_t total = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), kWave - 1));
+                const uint64_t tmask = __ballot(ties != 0);
+                uint32_t nties = 0;
+                for (uint64_t m = tmask; m; m &= m - 1) {
+                    nties += static_cast<uint32_t>(
+                        __builtin_amdgcn_readlane(static_cast<int>(ties), __builtin_ctzll(m)));
+                }
+                info.units = total;
+                info.u = u;
+                if (nties == 0) {
+                    info.flags = 1u;
+                } else if (nties == 1) {
+                    const int tl = __builtin_ctzll(tmask);
+                    const uint32_t excl = incl - (lsum < kSeqLimit ? lsum : kSeqLimit);
+                    const uint32_t before = excl + tbefore; // units before the tie element
+                    const uint32_t par = (before + tq) & 1u;
+                    info.flags = 1u | 2u | (static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(par), tl)) << 2);
+                }
+            }
+        }
+        if (lane == 0) out[k] = info;
+    }
 }
 
+// ---- stage 3: the exact sequential sum of e ----------------------------------
+//
+// One wave per row walks the row's chunks in order.  A chunk whose
+// predicted contribution (k_smp_seg) holds on the exact state -- the same
+// binade, no tie, and the units stay below 2^24, so no element inside it
+// can cross (units never decrease) -- is added in one step.  Any other
+// chunk is walked element by element in tiles of 64 lanes x 4 elements: a
+// round computes the tile's units at the current binade and their wave
+// prefix sum, and either commits the rest of the tile (no event) or finds
+// the first event element, adds it with one f32 addition and starts the
+// next round after it.  Each round commits at least one element, so the
+// rounds end.  Eight tiles are in flight ahead of the one being summed.
+
+struct SumState {
+    uint32_t m;
+    int32_t u;
+    bool finite;
+    float special; // NaN or +inf once the running sum leaves the finite range
+};
+
+// The rounds over one tile of PER * 64 elements (this lane's PER consecutive
+// ones in e).
 template <uint32_t PER>
-__device__ __forceinline__ void sum_tile(const float (&e)[PER], SumState &s, SumShared &sh)
+__device__ __forceinline__ void sum_tile(const float (&e)[PER], SumState &s, uint32_t start = 0)
 {
-    constexpr uint32_t kWaves = kSumThreads / kWave;
-    constexpr uint32_t kTile = kSumThreads * PER;
-    const uint32_t t = threadIdx.x, lane = t % kWave, wave = t / kWave;
+    const uint32_t lane = threadIdx.x % kWave;
     if (!s.finite) {
         // +inf stays +inf unless a NaN follows; NaN stays NaN
         bool nan = false;
 #pragma unroll
         for (uint32_t j = 0; j < PER; ++j) nan |= e[j] != e[j];
-        if (__syncthreads_or(nan)) s.special = __builtin_nanf("");
+        if (__ballot(nan)) s.special = __builtin_nanf("");
         return;
     }
-    uint32_t start = 0; // tile-relative index of the first uncommitted element
+    // start: tile-relative index of the first uncommitted element
     while (true) {
-        // units are not kept: the no-event path needs only their sum, and
-        // an event round recomputes them (fewer live registers)
-        uint32_t ties = 0; // bit j: element j is a tie
-        uint32_t lsum = 0;
+        uint32_t lsum = 0, ties = 0;
         if (start == 0) {
 #pragma unroll
             for (uint32_t j = 0; j < PER; ++j) {
@@ -308,143 +444,204 @@ __device__ __forceinline__ void sum_tile(const float (&e)[PER], SumState &s, Sum
 #pragma unroll
             for (uint32_t j = 0; j < PER; ++j) {
                 bool tie;
-                const uint32_t q = seq_units(e[j], s.u, tie);
-                const bool active = PER * t + j >= start;
-                lsum += active ? q : 0u;
+                const uint32_t r = seq_units(e[j], s.u, tie);
+                const bool active = PER * lane + j >= start;
+                lsum += active ? r : 0u;
                 ties |= static_cast<uint32_t>(active && tie) << j;
             }
         }
-        // lsum <= PER * 2^24; saturate at 2^24 so the scans cannot overflow
-        // (a saturated value already marks a crossing)
+        // lsum <= PER * 2^24; saturated at 2^24 the scan cannot overflow (a
+        // saturated value already marks a crossing)
         const uint32_t x_in = lsum < kSeqLimit ? lsum : kSeqLimit;
-        uint32_t incl = x_in;
-#pragma unroll
-        for (int off = 1; off < kWave; off <<= 1) {
-            const uint32_t o = __shfl_up(incl, off, kWave);
-            if (lane >= static_cast<uint32_t>(off)) incl += o;
-        }
-        const bool wtie = __ballot(ties != 0) != 0;
-        if (lane == kWave - 1) sh.wsum[s.parity][wave] = (incl < kSeqLimit ? incl : kSeqLimit) | (wtie ? 0x80000000u : 0u);
-        __syncthreads();
-        uint32_t before = 0, total = 0, anytie = 0;
-#pragma unroll
-        for (uint32_t v = 0; v < kWaves; ++v) {
-            const uint32_t ws = sh.wsum[s.parity][v];
-            before += v < wave ? (ws & 0x7fffffffu) : 0u;
-            total += ws & 0x7fffffffu;
-            anytie |= ws >> 31;
-        }
-        s.parity ^= 1u;
+        const uint32_t incl = wave_incl_scan(x_in);
+        const uint32_t total = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), kWave - 1));
+        const bool anytie = __ballot(ties != 0) != 0;
         if (!anytie && s.m + total < kSeqLimit) {
             s.m += total;
             return; // tile committed
         }
-        // this thread's first event element, and the sum just before it
-        uint32_t run = s.m + before + (incl - x_in);
+        // this lane's first event element and the units just before it
+        uint32_t run = s.m + (incl - x_in);
         uint32_t mine = kNone;
         float ek = 0.0f;
 #pragma unroll
         for (uint32_t j = 0; j < PER; ++j) {
-            if (mine == kNone && PER * t + j >= start) {
+            if (mine == kNone && PER * lane + j >= start) {
                 bool tie;
-                const uint32_t q = seq_units(e[j], s.u, tie);
-                if (tie || run + q >= kSeqLimit) {
-                    mine = PER * t + j;
+                const uint32_t r = seq_units(e[j], s.u, tie);
+                if (tie || run + r >= kSeqLimit) {
+                    mine = PER * lane + j;
                     ek = e[j];
                 } else {
-                    run += q;
+                    run += r;
                 }
             }
         }
-        // the wave's first event (its lowest lane with one) adds it and
-        // publishes both the position and the new sum
         const uint64_t emask = __ballot(mine != kNone);
-        if (emask && lane == static_cast<uint32_t>(__builtin_ctzll(emask))) {
-            sh.first[wave] = mine;
-            sh.next[wave] = seq_value(run, s.u) + ek;
-        } else if (!emask && lane == 0) {
-            sh.first[wave] = kNone;
-        }
-        __syncthreads();
-        uint32_t k = kNone;
-        float sn = 0.0f;
-#pragma unroll
-        for (uint32_t v = 0; v < kWaves; ++v) {
-            const uint32_t f = sh.first[v];
-            if (f < k) {
-                k = f;
-                sn = sh.next[v];
-            }
-        }
-        // sh.first / sh.next are rewritten only after the next round's first
-        // barrier, which every thread reaches after these reads
-        if (k == kNone) return; // unreachable: a tie or a crossing has a first element
+        if (emask == 0) return; // unreachable: a tie or a crossing has a first element
+        const int fl = __builtin_ctzll(emask);
+        const uint32_t k = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(mine), fl));
+        const uint32_t run_k = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(run), fl));
+        const float e_k = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ek), fl));
+        const float sn = seq_value(run_k, s.u) + e_k; // the event element: one f32 addition
         if (!(sn < __builtin_inff())) { // NaN or +inf
             s.special = sn;
             s.finite = false;
             bool nan = false;
 #pragma unroll
-            for (uint32_t j = 0; j < PER; ++j) nan |= (PER * t + j > k) && e[j] != e[j];
-            if (__syncthreads_or(nan)) s.special = __builtin_nanf("");
+            for (uint32_t j = 0; j < PER; ++j) nan |= (PER * lane + j > k) && e[j] != e[j];
+            if (__ballot(nan)) s.special = __builtin_nanf("");
             return;
         }
         const SeqState st = seq_state(sn);
         s.m = st.m;
         s.u = st.u;
         start = k + 1;
-        if (start >= kTile) return;
+        if (start >= PER * kWave) return;
     }
 }
 
-__global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *logits, SmpWs w)
+constexpr uint32_t kPer = kSub / kWave; // 16 elements per lane and round of the walk
+constexpr uint32_t kHead = 512;          // a row's first elements, added one by one
+
+// One 256-thread workgroup per row; every wave keeps the same state.  The
+// sub-chunks' predictions are read a batch at a time (lane i of every wave
+// holds sub-chunk kb + i's).  A sub-chunk whose predicted contribution holds
+// on the exact state -- the same binade, and the units (its one tie
+// resolved by the current parity) stay below 2^24, so no element inside it
+// can cross (units never decrease) -- is added in one step.  Any other
+// sub-chunk is staged in LDS by the whole workgroup (one load latency) and
+// walked by wave 0: one round, plus one per event.
+__global__ __launch_bounds__(kBlock) void k_smp_sum(SmpGeo g, const float *logits, SmpWs w)
 {
-    __shared__ SumShared sh;
+    __shared__ float4 s_stage[kSub / 4];
+    __shared__ uint32_t s_state[4];
     const uint32_t row = blockIdx.x;
+    const uint32_t lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
     const float *x = logits + static_cast<int64_t>(row) * g.ld;
-    const uint64_t n = g.card;
-    SumState s{0u, -149, 0u, true, 0.0f};
-    uint64_t base = 0;
-    // warm-up tiles of 1, 2, 4 and 8 elements per thread
-    {
-        float e[1];
-        load_tile<1>(g, x, base, e);
-        sum_tile<1>(e, s, sh);
-        base += kSumThreads;
-    }
-    if (base < n) {
-        float e[2];
-        load_tile<2>(g, x, base, e);
-        sum_tile<2>(e, s, sh);
-        base += 2 * kSumThreads;
-    }
-    if (base < n) {
-        float e[4];
-        load_tile<4>(g, x, base, e);
-        sum_tile<4>(e, s, sh);
-        base += 4 * kSumThreads;
-    }
-    if (base < n) {
-        float e[8];
-        load_tile<8>(g, x, base, e);
-        sum_tile<8>(e, s, sh);
-        base += 8 * kSumThreads;
-    }
-    // steady state: 16 per thread, the next tile in flight
-    constexpr uint64_t kTile = 16ull * kSumThreads;
-    if (base < n) {
-        float a[16], b[16];
-        load_tile<16>(g, x, base, a);
-        while (true) {
-            const bool more = base + kTile < n;
-            if (more) load_tile<16>(g, x, base + kTile, b);
-            sum_tile<16>(a, s, sh);
-            base += kTile;
-            if (!more) break;
-            const bool more2 = base + kTile < n;
-            if (more2) load_tile<16>(g, x, base + kTile, a);
-            sum_tile<16>(b, s, sh);
-            base += kTile;
-            if (!more2) break;
+    const uint32_t spc = subs_per_chunk(g);
+    const uint64_t card4 = g.card & ~uint64_t{3};
+    SumState s{0u, -149, true, 0.0f};
+    bool nan_final = false;
+    // The row's predictions form one list of chunks * spc slots; they are
+    // read 64 at a time (lane i holds slot base + i), the next batch in
+    // flight while this one is used.
+    const uint32_t nslots = g.chunks * spc;
+    const SegInfo *seg = w.seg + static_cast<uint64_t>(row) * nslots;
+    SegInfo nxt{0, 0, 8u, 0};
+    if (lane < nslots) nxt = seg[lane];
+    for (uint32_t kb = 0; kb < nslots && !nan_final; kb += kWave) {
+        const SegInfo mine = nxt;
+        if (kb + kWave + lane < nslots) nxt = seg[kb + kWave + lane];
+        const uint32_t nb = nslots - kb < kWave ? nslots - kb : kWave;
+        {
+            uint32_t i = 0; // next slot of the batch
+            while (i < nb) {
+                // Take the run of slots from i on that need no decision: empty
+                // ones, and usable tie-free sub-chunks in the current binade,
+                // their units below 2^24 -- one wave prefix sum finds where
+                // the run ends.
+                bool fail = false;
+                uint32_t add = 0;
+                if (lane >= i && lane < nb) {
+                    const bool empty = (mine.flags & 8u) != 0;
+                    const bool easy = empty || (s.finite && (mine.flags & 3u) == 1u && mine.u == s.u);
+                    add = easy && !empty ? mine.units : 0u;
+                    fail = !easy;
+                }
+                const uint32_t incl = wave_incl_scan(add < kSeqLimit ? add : kSeqLimit);
+                fail = fail || (lane >= i && lane < nb && static_cast<uint64_t>(s.m) + incl >= kSeqLimit);
+                const uint64_t fmask = __ballot(fail);
+                const uint32_t f = fmask ? static_cast<uint32_t>(__builtin_ctzll(fmask)) : nb;
+                if (f > i) s.m += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), f - 1));
+                if (f >= nb) break;
+                i = f + 1;
+                // slot f on its own: a usable sub-chunk with one tie adds its
+                // units plus the tie's parity correction
+                const uint32_t units = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(mine.units), f));
+                const int32_t u = __builtin_amdgcn_readlane(mine.u, f);
+                const uint32_t flags = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(mine.flags), f));
+                const uint64_t addf = static_cast<uint64_t>(units) + ((flags & 2u) ? ((s.m + (flags >> 2)) & 1u) : 0u);
+                if (s.finite && (flags & 1u) && u == s.u && static_cast<uint64_t>(s.m) + addf < kSeqLimit) {
+                    s.m += static_cast<uint32_t>(addf);
+                    continue;
+                }
+                if (!s.finite && s.special != s.special) { // NaN is final
+                    nan_final = true;
+                    break;
+                }
+                // stage the sub-chunk: one float4 (or four floats) per thread
+                const uint32_t slot = kb + f;
+                uint64_t c0, c1;
+                chunk_range(g, slot / spc, c0, c1);
+                const uint64_t a0 = c0 + static_cast<uint64_t>(slot % spc) * kSub;
+                const uint64_t a1 = a0 + kSub < c1 ? a0 + kSub : c1;
+                const uint32_t n = static_cast<uint32_t>(a1 - a0);
+                float *st = reinterpret_cast<float *>(s_stage);
+                const uint32_t q = threadIdx.x; // kSub / 4 == kBlock
+                if (g.vec && a1 <= card4) {     // a0 is a multiple of 4: whole float4s
+                    if (4 * q < n) s_stage[q] = reinterpret_cast<const float4 *>(x + a0)[q];
+                } else {
+#pragma unroll
+                    for (uint32_t j = 0; j < 4; ++j) st[4 * q + j] = 4 * q + j < n ? x[a0 + 4 * q + j] : 0.0f;
+                }
+                __syncthreads();
+                if (wave == 0) {
+                    // The first elements of a row come with a binade crossing or
+                    // a tie every few elements (the sum is still comparable to
+                    // its addends), each of which would cost a round: lane 0
+                    // adds them one by one, the reference's own arithmetic.
+                    uint32_t head = 0;
+                    if (a0 == 0 && s.finite && s.m == 0) {
+                        head = n < kHead ? n : kHead;
+                        float acc = seq_value(s.m, s.u);
+                        if (lane == 0) {
+#pragma unroll 8
+                            for (uint32_t j = 0; j < head; ++j) acc += st[j];
+                        }
+                        acc = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, acc)));
+                        if (!(acc < __builtin_inff())) {
+                            s.finite = false;
+                            s.special = acc;
+                        } else {
+                            const SeqState h = seq_state(acc);
+                            s.m = h.m;
+                            s.u = h.u;
+                        }
+                    }
+                    if (head < kSub) {
+                        float e[kPer];
+                        const uint32_t cc = kPer * lane;
+                        if (cc + kPer <= n) {
+#pragma unroll
+                            for (uint32_t j = 0; j < kPer / 4; ++j) {
+                                const float4 v = s_stage[cc / 4 + j];
+                                e[4 * j] = v.x;
+                                e[4 * j + 1] = v.y;
+                                e[4 * j + 2] = v.z;
+                                e[4 * j + 3] = v.w;
+                            }
+                        } else {
+#pragma unroll
+                            for (uint32_t j = 0; j < kPer; ++j) e[j] = cc + j < n ? st[cc + j] : 0.0f;
+                        }
+                        sum_tile<kPer>(e, s, head); // the head's elements are committed
+                    }
+                }
+                // wave 0's state to every wave
+                if (threadIdx.x == 0) {
+                    s_state[0] = s.m;
+                    s_state[1] = static_cast<uint32_t>(s.u);
+                    s_state[2] = s.finite;
+                    s_state[3] = f32_to_bits(s.special);
+                }
+                __syncthreads();
+                s.m = s_state[0];
+                s.u = static_cast<int32_t>(s_state[1]);
+                s.finite = s_state[2] != 0;
+                s.special = bits_to_f32(s_state[3]);
+                __syncthreads(); // the stage and s_state are rewritten by the next walk
+            }
         }
     }
     if (threadIdx.x == 0) w.sel[row].total = s.finite ? seq_value(s.m, s.u) : s.special;
@@ -945,14 +1142,17 @@ void plan_chunks(uint32_t rows, uint64_t card, uint64_t &chunk_cols, uint32_t &c
 uint64_t align256(uint64_t b) { return (b + 255) & ~uint64_t{255}; }
 
 struct WsLayout {
-    uint64_t part, sel, hist, ties, cand, cand2, total;
+    uint64_t part, psum, seg, sel, hist, ties, cand, cand2, total;
 };
 
-WsLayout layout(uint32_t rows, uint32_t chunks, uint64_t cand_ld, bool merge)
+WsLayout layout(uint32_t rows, uint32_t chunks, uint64_t chunk_cols, uint64_t cand_ld, bool merge)
 {
+    const uint64_t spc = (chunk_cols + kSub - 1) / kSub;
     WsLayout l{};
     l.part = 0;
-    l.sel = l.part + align256(uint64_t{rows} * chunks * sizeof(float));
+    l.psum = l.part + align256(uint64_t{rows} * chunks * sizeof(float));
+    l.seg = l.psum + align256(uint64_t{rows} * chunks * sizeof(double));
+    l.sel = l.seg + align256(uint64_t{rows} * chunks * spc * sizeof(SegInfo));
     l.hist = l.sel + align256(uint64_t{rows} * sizeof(RowSel));
     l.ties = l.hist + align256(uint64_t{rows} * kBins * sizeof(uint32_t));
     l.cand = l.ties + align256(uint64_t{rows} * chunks * sizeof(uint32_t));
@@ -969,7 +1169,7 @@ uint64_t sampler_workspace_bytes(uint32_t rows, uint64_t card, uint32_t top_k)
     uint32_t chunks;
     plan_chunks(rows, card, chunk_cols, chunks);
     const uint64_t cand_ld = top_k > kCap ? top_k : kCap;
-    return layout(rows, chunks, cand_ld, top_k > kCap).total;
+    return layout(rows, chunks, chunk_cols, cand_ld, top_k > kCap).total;
 }
 
 hipError_t launch_sampler(const SamplerArgs &a, hipStream_t s)
@@ -986,10 +1186,12 @@ hipError_t launch_sampler(const SamplerArgs &a, hipStream_t s)
     g.scale = a.scale;
     g.cand_ld = a.top_k > kCap ? a.top_k : kCap;
     const bool merge = a.top_k > kCap;
-    const WsLayout l = layout(a.rows, g.chunks, g.cand_ld, merge);
+    const WsLayout l = layout(a.rows, g.chunks, g.chunk_cols, g.cand_ld, merge);
     char *base = static_cast<char *>(a.workspace);
     SmpWs w{};
     w.part = reinterpret_cast<float *>(base + l.part);
+    w.psum = reinterpret_cast<double *>(base + l.psum);
+    w.seg = reinterpret_cast<SegInfo *>(base + l.seg);
     w.sel = reinterpret_cast<RowSel *>(base + l.sel);
     w.hist = reinterpret_cast<uint32_t *>(base + l.hist);
     w.ties = reinterpret_cast<uint32_t *>(base + l.ties);
@@ -999,7 +1201,8 @@ hipError_t launch_sampler(const SamplerArgs &a, hipStream_t s)
     const dim3 grid(a.rows * g.chunks);
     k_smp_max<<<grid, kBlock, 0, s>>>(g, a.logits, w);
     k_smp_exp<<<grid, kBlock, 0, s>>>(g, a.logits, w);
-    k_smp_sum<<<a.rows, kSumThreads, 0, s>>>(g, a.logits, w);
+    k_smp_seg<<<grid, kBlock, 0, s>>>(g, a.logits, w);
+    k_smp_sum<<<a.rows, kBlock, 0, s>>>(g, a.logits, w);
     k_smp_div<<<grid, kBlock, 0, s>>>(g, a.logits, w);
     k_smp_pick<<<a.rows, kBlock, 0, s>>>(w, 0);
     k_smp_refine<<<grid, kBlock, 0, s>>>(g, a.logits, w, 1);

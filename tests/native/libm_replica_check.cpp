@@ -51,73 +51,157 @@ bool differ(float a, float b)
 
 } // namespace
 
-// The round structure of k_smp_sum (sampler.hip) on the host: tiles of
-// threads * per elements; a round commits the rest of the tile when no
-// element is an event, else commits up to the first event and adds that
-// element with one f32 addition.  Exact (unsaturated) prefix sums.
-// per == 0 selects k_smp_sum's schedule: tiles of threads * {1, 2, 4, 8}
-// elements, then threads * 16 to the end.
-float seqsum_blocked(const float *e, uint64_t n, uint32_t threads, uint32_t per)
-{
+// The sampler's exact sum (sampler.hip: k_smp_seg + k_smp_sum) on the host.
+struct EmuState {
     uint32_t m = 0;
     int32_t u = -149;
     bool finite = true;
     float special = 0.0f;
-    const uint64_t max_tile = static_cast<uint64_t>(threads) * (per ? per : 16);
-    std::vector<float> ev(max_tile);
-    std::vector<uint32_t> r(max_tile);
-    std::vector<uint8_t> tie(max_tile);
-    uint32_t warm = 0;
-    for (uint64_t base = 0, tile = 0; base < n; base += tile) {
-        tile = static_cast<uint64_t>(threads) * (per ? per : (warm < 4 ? (1u << warm) : 16u));
-        ++warm;
-        for (uint64_t i = 0; i < tile; ++i) ev[i] = base + i < n ? e[base + i] : 0.0f;
-        if (!finite) {
-            for (uint64_t i = 0; i < tile; ++i)
-                if (std::isnan(ev[i])) special = std::nanf("");
-            continue;
+};
+
+// One tile of `tile` elements through k_smp_sum's rounds: a round commits the
+// rest of the tile when no element is an event, else commits up to the
+// first event and adds that element with one f32 addition.  Exact
+// (unsaturated) prefix sums.
+static void emu_tile(const float *ev, uint64_t tile, EmuState &s, std::vector<uint32_t> &r,
+                     std::vector<uint8_t> &tie)
+{
+    if (!s.finite) {
+        for (uint64_t i = 0; i < tile; ++i)
+            if (std::isnan(ev[i])) s.special = std::nanf("");
+        return;
+    }
+    uint64_t start = 0;
+    while (true) {
+        uint64_t total = 0;
+        bool anytie = false;
+        for (uint64_t i = 0; i < tile; ++i) {
+            bool t;
+            const uint32_t q = emel::seq_units(ev[i], s.u, t);
+            r[i] = i >= start ? q : 0u;
+            tie[i] = i >= start && t;
+            total += r[i];
+            anytie |= tie[i] != 0;
         }
-        uint64_t start = 0;
-        while (true) {
-            uint64_t total = 0;
-            bool anytie = false;
-            for (uint64_t i = 0; i < tile; ++i) {
-                bool t;
-                const uint32_t q = emel::seq_units(ev[i], u, t);
-                r[i] = i >= start ? q : 0u;
-                tie[i] = i >= start && t;
-                total += r[i];
-                anytie |= tie[i] != 0;
-            }
-            if (!anytie && m + total < emel::kSeqLimit) {
-                m += static_cast<uint32_t>(total);
+        if (!anytie && s.m + total < emel::kSeqLimit) {
+            s.m += static_cast<uint32_t>(total);
+            return;
+        }
+        uint64_t run = s.m, k = tile;
+        for (uint64_t i = start; i < tile; ++i) {
+            if (tie[i] || run + r[i] >= emel::kSeqLimit) {
+                k = i;
                 break;
             }
-            uint64_t run = m, k = tile;
-            for (uint64_t i = start; i < tile; ++i) {
-                if (tie[i] || run + r[i] >= emel::kSeqLimit) {
-                    k = i;
-                    break;
-                }
-                run += r[i];
-            }
-            if (k == tile) return std::nanf("0x7e57"); // cannot happen: flag it
-            const float sn = emel::seq_value(static_cast<uint32_t>(run), u) + ev[k];
-            if (!(sn < INFINITY)) {
-                special = sn;
-                finite = false;
-                for (uint64_t i = k + 1; i < tile; ++i)
-                    if (std::isnan(ev[i])) special = std::nanf("");
-                break;
-            }
-            const emel::SeqState st = emel::seq_state(sn);
-            m = st.m;
-            u = st.u;
-            start = k + 1;
-            if (start >= tile) break;
+            run += r[i];
+        }
+        if (k == tile) { // cannot happen: flag it
+            s.finite = false;
+            s.special = std::nanf("0x7e57");
+            return;
+        }
+        const float sn = emel::seq_value(static_cast<uint32_t>(run), s.u) + ev[k];
+        if (!(sn < INFINITY)) {
+            s.special = sn;
+            s.finite = false;
+            for (uint64_t i = k + 1; i < tile; ++i)
+                if (std::isnan(ev[i])) s.special = std::nanf("");
+            return;
+        }
+        const emel::SeqState st = emel::seq_state(sn);
+        s.m = st.m;
+        s.u = st.u;
+        start = k + 1;
+        if (start >= tile) return;
+    }
+}
+
+// Walks [c0, c1) in tiles of lanes * 16 elements (k_smp_sum: 64 lanes).
+// At the start of a row the first `head` elements are added one by one.
+static void emu_walk(const float *e, uint64_t c0, uint64_t c1, uint32_t lanes, EmuState &s, uint64_t head = 512)
+{
+    const uint64_t tile = 16ull * lanes;
+    std::vector<float> ev(tile);
+    std::vector<uint32_t> r(tile);
+    std::vector<uint8_t> tie(tile);
+    uint64_t skip = 0;
+    if (c0 == 0 && s.finite && s.m == 0) {
+        skip = std::min(head, c1 - c0);
+        float acc = emel::seq_value(s.m, s.u);
+        for (uint64_t i = 0; i < skip; ++i) acc += e[c0 + i];
+        if (!(acc < INFINITY)) {
+            s.finite = false;
+            s.special = acc;
+        } else {
+            const emel::SeqState h = emel::seq_state(acc);
+            s.m = h.m;
+            s.u = h.u;
         }
     }
-    return finite ? emel::seq_value(m, u) : special;
+    for (uint64_t base = c0; base < c1; base += tile) {
+        for (uint64_t i = 0; i < tile; ++i) ev[i] = base + i < c1 && base + i >= c0 + skip ? e[base + i] : 0.0f;
+        emu_tile(ev.data(), tile, s, r, tie);
+    }
+}
+
+// chunk == 0: the whole range is walked (no predictions).  Otherwise
+// chunks of `chunk` elements split into sub-chunks of `sub`: k_smp_seg's
+// prediction per sub-chunk (f64 prefix of chunk and sub-chunk sums, the
+// rounding bound, units at the predicted binade, one tie resolved by
+// parity) and k_smp_sum's checks on the exact state; a sub-chunk that is
+// not taken is walked alone.  *jumped counts sub-chunks taken in one step.
+float seqsum_chunked(const float *e, uint64_t n, uint32_t lanes, uint64_t chunk, uint64_t sub, uint64_t *jumped)
+{
+    EmuState s;
+    if (jumped) *jumped = 0;
+    if (chunk == 0) {
+        emu_walk(e, 0, n, lanes, s);
+        return s.finite ? emel::seq_value(s.m, s.u) : s.special;
+    }
+    double pre = 0.0;
+    for (uint64_t c0 = 0; c0 < n; c0 += chunk) {
+        const uint64_t c1 = std::min(n, c0 + chunk);
+        double Pk = pre;
+        for (uint64_t a0 = c0; a0 < c1; a0 += sub) {
+            const uint64_t a1 = std::min(c1, a0 + sub);
+            double ssum = 0.0;
+            for (uint64_t i = a0; i < a1; ++i) ssum += static_cast<double>(e[i]);
+            const double lo = Pk * (1.0 - (static_cast<double>(a0) * 0x1p-24 + 0x1p-30));
+            const double hi = (Pk + ssum) * (1.0 + (static_cast<double>(a1) * 0x1p-24 + 0x1p-30));
+            Pk += ssum;
+            int elo = 0, ehi = 0;
+            std::frexp(lo, &elo);
+            std::frexp(hi, &ehi);
+            bool ok = lo >= 0x1p-126 && hi < 0x1p127 && lo <= hi && elo == ehi;
+            const int32_t u = elo - 24;
+            uint64_t units = 0;
+            int ties = 0;
+            uint32_t par = 0;
+            if (ok) {
+                for (uint64_t i = a0; i < a1; ++i) {
+                    bool t;
+                    uint32_t q = emel::seq_units(e[i], u, t);
+                    if (t) {
+                        q = static_cast<uint32_t>(std::floor(std::ldexp(e[i], -u)));
+                        if (ties == 0) par = static_cast<uint32_t>((units + q) & 1u);
+                        ++ties;
+                    }
+                    units += q;
+                }
+                if (ties > 1) ok = false;
+            }
+            const uint64_t add = units + (ties == 1 ? ((s.m + par) & 1u) : 0u);
+            if (s.finite && ok && u == s.u && s.m + add < emel::kSeqLimit) {
+                s.m += static_cast<uint32_t>(add);
+                if (jumped) ++*jumped;
+                continue;
+            }
+            if (!s.finite && std::isnan(s.special)) break;
+            emu_walk(e, a0, a1, lanes, s);
+        }
+        pre = Pk;
+    }
+    return s.finite ? emel::seq_value(s.m, s.u) : s.special;
 }
 
 static uint64_t splitmix(uint64_t &z)
@@ -155,18 +239,22 @@ static void fill_case(uint64_t &z, int family, std::vector<float> &e)
     }
 }
 
-extern "C" float seqsum_blocked_f(const float *e, uint64_t n, uint32_t threads, uint32_t per)
+extern "C" float seqsum_chunked_f(const float *e, uint64_t n, uint32_t lanes, uint64_t chunk, uint64_t sub,
+                                  uint64_t *jumped)
 {
-    return seqsum_blocked(e, n, threads, per);
+    return seqsum_chunked(e, n, lanes, chunk, sub, jumped);
 }
 
-// Random cases of each family and length up to max_n; tile shapes
-// (threads, per) of the kernel (1024, 16) and small ones that force many
-// rounds.  Counts results whose bits differ from the sequential loop.
+// Random cases of each family and length up to max_n, through the walk
+// alone (the kernel's 64 lanes and a small 4) and through sub-chunk
+// predictions (config 5's 4748-element chunks of 1024-element sub-chunks,
+// and small shapes).  Counts results whose bits differ from the sequential
+// loop.
 extern "C" uint64_t check_seqsum(uint64_t seed, int cases, uint64_t max_n)
 {
     uint64_t z = seed, bad = 0;
-    const uint32_t shapes[4][2] = {{1024, 0}, {1024, 16}, {4, 2}, {64, 1}};
+    const uint64_t shapes[6][3] = {{64, 0, 0}, {4, 0, 0}, {64, 4748, 1024}, {4, 100, 64}, {64, 1024, 1024},
+                                   {4, 300, 300}};
     for (int c = 0; c < cases; ++c) {
         const int family = c % 5;
         const uint64_t n = 1 + splitmix(z) % max_n;
@@ -175,7 +263,7 @@ extern "C" uint64_t check_seqsum(uint64_t seed, int cases, uint64_t max_n)
         float want = 0.0f;
         for (float v : e) want += v;
         for (const auto &sh : shapes) {
-            const float got = seqsum_blocked(e.data(), n, sh[0], sh[1]);
+            const float got = seqsum_chunked(e.data(), n, static_cast<uint32_t>(sh[0]), sh[1], sh[2], nullptr);
             if (differ(got, want)) ++bad;
         }
     }

@@ -83,16 +83,36 @@ def test_replica_matches_oracle_scalars(chk):
 
 
 def test_exact_sequential_sum_rounds(chk):
-    """The round structure of the sampler's exact sequential f32 sum
-    (seqsum.hpp, k_smp_sum): integer units per binade, with ties, binade
-    crossings, NaN and +inf taken as single f32 additions, must give the
-    bits of a plain sequential f32 loop.  Families: softmax-like values,
-    dyadic values full of exact ties, zeros and subnormals, every magnitude,
-    planted NaN / +inf; the kernel's tile schedule (1024 threads, 1, 2, 4,
-    8 then 16 elements each), fixed 1024 x 16 tiles, and small shapes that
-    force many rounds.  Ignoring ties or letting a binade run to
-    2^25 units makes this check fail (1275 and 4950 mismatching cases)."""
+    """The sampler's exact sequential f32 sum (seqsum.hpp; sampler.hip's
+    k_smp_seg and k_smp_sum) emulated on the host: integer units per binade,
+    ties, binade crossings, NaN and +inf taken as single f32 additions, and
+    chunk contributions predicted from f64 chunk sums and taken only when
+    the exact state confirms them.  It must give the bits of a plain
+    sequential f32 loop.  Families: softmax-like values, dyadic values full
+    of exact ties, zeros and subnormals, every magnitude, planted NaN / +inf;
+    the walk alone (64 lanes, as the kernel, and 4) and with predictions
+    (config 5's 4748-element chunks, 100- and 1024-element chunks).  Ignoring ties, or
+    letting a binade run to 2^25 units, makes this check fail."""
     chk.check_seqsum.restype = ctypes.c_uint64
     chk.check_seqsum.argtypes = [ctypes.c_uint64, ctypes.c_int, ctypes.c_uint64]
     assert chk.check_seqsum(1, 2000, 300) == 0
     assert chk.check_seqsum(2, 40, 200_000) == 0
+
+
+def test_exact_sum_predictions_are_taken(chk):
+    """On a config-5-like row (softmax of N(0,1) logits / 0.8 over 151,936
+    tokens) most sub-chunks are taken from their prediction in one step: the
+    walk is left with the sub-chunks where the binade changes."""
+    import numpy as np
+
+    chk.seqsum_chunked_f.restype = ctypes.c_float
+    chk.seqsum_chunked_f.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_uint64, ctypes.c_uint32,
+                                     ctypes.c_uint64, ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64)]
+    g = np.random.Generator(np.random.PCG64(5))
+    v = (g.standard_normal(151936) / 0.8).astype(np.float32)
+    e = np.exp((v - v.max()).astype(np.float64)).astype(np.float32)
+    jumped = ctypes.c_uint64(0)
+    got = chk.seqsum_chunked_f(e.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), e.size, 64, 4748, 1024,
+                               ctypes.byref(jumped))
+    assert np.float32(got) == np.cumsum(e, dtype=np.float32)[-1]
+    assert jumped.value >= 140, jumped.value  # of 160 sub-chunks
