@@ -141,9 +141,11 @@ __device__ __forceinline__ uint32_t powmod(uint64_t e)
     return r;
 }
 
-// Visits the columns [c0, c1) of one row, in increasing order per thread:
-// float4 steps when the row is 16-byte aligned, then a scalar tail.
-// f(float &v, uint64_t col) may modify v; `write` stores it back.
+// Visits the columns [c0, c1) of one row: float4 steps when the row is
+// 16-byte aligned (four loads in flight per thread before any is used),
+// then a scalar tail.  The order of the visits is unspecified: callers
+// only reduce order-independently or write elementwise.
+// f(float &v, uint64_t col) may modify v; WRITE stores it back.
 template <bool WRITE, class F>
 __device__ __forceinline__ void visit(const SmpGeo &g, float *row, uint64_t c0, uint64_t c1, F f)
 {
@@ -151,12 +153,27 @@ __device__ __forceinline__ void visit(const SmpGeo &g, float *row, uint64_t c0, 
     if (g.vec) {
         float4 *r4 = reinterpret_cast<float4 *>(row);
         const uint64_t v1 = c1 / 4;
-        for (uint64_t v = c0 / 4 + threadIdx.x; v < v1; v += blockDim.x) {
+        const uint64_t bs = blockDim.x;
+        uint64_t v = c0 / 4 + threadIdx.x;
+        auto apply = [&](float4 &q, uint64_t vi) {
+            f(q.x, 4 * vi);
+            f(q.y, 4 * vi + 1);
+            f(q.z, 4 * vi + 2);
+            f(q.w, 4 * vi + 3);
+        };
+        for (; v + 3 * bs < v1; v += 4 * bs) {
+            float4 q[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) q[j] = r4[v + j * bs];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                apply(q[j], v + j * bs);
+                if constexpr (WRITE) r4[v + j * bs] = q[j];
+            }
+        }
+        for (; v < v1; v += bs) {
             float4 q = r4[v];
-            f(q.x, 4 * v);
-            f(q.y, 4 * v + 1);
-            f(q.z, 4 * v + 2);
-            f(q.w, 4 * v + 3);
+            apply(q, v);
             if constexpr (WRITE) r4[v] = q;
         }
         c = v1 * 4 > c0 ? v1 * 4 : c0;
