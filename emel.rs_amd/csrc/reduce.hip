@@ -110,26 +110,23 @@ __device__ __forceinline__ void accumulate(const RedGeo &g, const float *x, int6
 }
 
 // Writes the row result from its combined (sum | (value, index)) word.
+// argmax: `first` is the row's column 0 (a NaN there makes the result 0).
 template <RedOp OP>
-__device__ __forceinline__ void write_result(const RedGeo &g, const float *x, void *dst, uint32_t row, uint64_t packed)
+__device__ __forceinline__ void write_result(const RedGeo &g, float first, void *dst, uint32_t row, uint64_t packed)
 {
     constexpr bool kArg = Acc<OP>::kArg;
     uint32_t i1 = 0, i2 = 0, i3 = 0;
-    int64_t base = 0;
     if (g.mode != kModeOrdinal) {
         const uint32_t t = g.ne1.div(row);
         i1 = row - t * g.ne1.d;
         i3 = g.ne2.div(t);
         i2 = t - i3 * g.ne2.d;
-        base = static_cast<int64_t>(i1) * g.x_st[1] + static_cast<int64_t>(i2) * g.x_st[2] +
-               static_cast<int64_t>(i3) * g.x_st[3];
     }
     const int64_t doff = static_cast<int64_t>(i1) * g.d_st[1] + static_cast<int64_t>(i2) * g.d_st[2] +
                          static_cast<int64_t>(i3) * g.d_st[3];
     if constexpr (kArg) {
         const ArgPart p = __builtin_bit_cast(ArgPart, packed);
         // column 0 NaN: the sequential scan never replaces it
-        const float first = g.mode == kModeOrdinal ? x[ordinal_offset(g, 0)] : x[base];
         const uint64_t idx = (first != first || p.i == 0xffffffffu) ? 0 : p.i;
         const float fidx = static_cast<float>(idx); // the reference stores the index as f32
         if constexpr (OP == RedOp::ArgmaxRows) static_cast<int32_t *>(dst)[doff] = static_cast<int32_t>(fidx);
@@ -170,6 +167,13 @@ __global__ __launch_bounds__(kBlock) void k_reduce(RedGeo g, const float *x, voi
     const uint64_t c0 = static_cast<uint64_t>(chunk) * g.chunk_cols;
     const uint64_t c1 = c0 + g.chunk_cols < g.ncols ? c0 + g.chunk_cols : g.ncols;
 
+    // argmax: the row's column 0, read by the chunk-0 workgroup while its
+    // range loads are in flight (a NaN there decides the row)
+    float first = 0.0f;
+    if constexpr (kArg) {
+        if (chunk == 0 && threadIdx.x == 0) first = g.mode == kModeOrdinal ? x[ordinal_offset(g, 0)] : x[base];
+    }
+
     double sum = 0.0;
     float bv = -__builtin_inff();
     uint32_t bi = 0xffffffffu; // "no candidate": loses every tie on index
@@ -191,19 +195,24 @@ __global__ __launch_bounds__(kBlock) void k_reduce(RedGeo g, const float *x, voi
     if constexpr (kArg) {
         for (int w = 1; w < kBlock / kWave; ++w) argmax_merge(s_v[0], s_i[0], s_v[w], s_i[w]);
         packed = __builtin_bit_cast(uint64_t, ArgPart{s_v[0], s_i[0]});
+        // Split rows: a NaN in column 0 makes chunk 0's partial (+inf, 0),
+        // which every other partial loses to (greater value, or equal value
+        // and higher index), so the combined index is 0.
+        if (g.chunks > 1 && chunk == 0 && first != first)
+            packed = __builtin_bit_cast(uint64_t, ArgPart{__builtin_inff(), 0u});
     } else {
         double t = s_sum[0];
         for (int w = 1; w < kBlock / kWave; ++w) t += s_sum[w];
         packed = __builtin_bit_cast(uint64_t, t);
     }
-    if (g.chunks == 1) write_result<OP>(g, x, dst, row, packed);
+    if (g.chunks == 1) write_result<OP>(g, first, dst, row, packed);
     else part[blockIdx.x] = packed;
 }
 
 // Pass 2: one wave per row combines the row's partials (lane l takes
 // chunks l, l+64, ...; then a fixed butterfly) and writes the result.
 template <RedOp OP>
-__global__ __launch_bounds__(kBlock) void k_reduce_finish(RedGeo g, const float *x, void *dst, const uint64_t *part)
+__global__ __launch_bounds__(kBlock) void k_reduce_finish(RedGeo g, void *dst, const uint64_t *part)
 {
     constexpr bool kArg = Acc<OP>::kArg;
     const uint32_t row = blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave;
@@ -229,7 +238,8 @@ __global__ __launch_bounds__(kBlock) void k_reduce_finish(RedGeo g, const float 
         tsum = wave_sum(tsum);
         packed = __builtin_bit_cast(uint64_t, tsum);
     }
-    if (lane == 0) write_result<OP>(g, x, dst, row, packed);
+    // column 0 was folded into chunk 0's partial by pass 1
+    if (lane == 0) write_result<OP>(g, 0.0f, dst, row, packed);
 }
 
 constexpr uint32_t kTargetBlocks = 2048; // 8 workgroups per CU on 256 CUs
@@ -313,7 +323,7 @@ hipError_t launch_reduce(const RedArgs &a, hipStream_t s)
     auto run = [&](auto op_tag) {
         constexpr RedOp OP = decltype(op_tag)::value;
         k_reduce<OP><<<grid, kBlock, 0, s>>>(g, x, a.dst, part);
-        if (g.chunks > 1) k_reduce_finish<OP><<<fgrid, kBlock, 0, s>>>(g, x, a.dst, part);
+        if (g.chunks > 1) k_reduce_finish<OP><<<fgrid, kBlock, 0, s>>>(g, a.dst, part);
     };
     switch (a.op) {
     case RedOp::SumRows: run(std::integral_constant<RedOp, RedOp::SumRows>{}); break;

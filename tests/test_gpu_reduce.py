@@ -70,6 +70,29 @@ def test_argmax_rows_nan_inf_ties(gpu):
     assert list(got) == [0, 40000, 0, 49999, 0, 123, 0, 0]
 
 
+def test_argmax_column0_nan_in_split_rows(gpu):
+    # rows long enough to be split across workgroups: a NaN in column 0 must
+    # decide the row even against a later +inf in another chunk
+    cols, rows = 151936, 4
+    x, where = planted_logits(cols, rows, 271)
+    x = x.reshape(rows, cols)
+    x[0, 0] = np.nan; x[0, 70000] = np.inf      # -> 0
+    x[1, 0] = np.nan                             # -> 0
+    x[2, 1] = np.nan; x[2, 100000] = np.inf     # -> 100000
+    x[3, 0] = -np.inf                            # -> the planted maximum
+    got = run_argmax_rows(gpu, x.reshape(-1), [cols, rows, 1, 1])
+    assert list(got) == [0, 0, 100000, where[3]]
+    # the whole-tensor argmax, dense and through the ordinal decode (a
+    # transposed view whose ordinal 0 is still x[0, 0])
+    for ne, nb in (([cols * rows, 1, 1, 1], None), ([rows, cols, 1, 1], [4 * cols, 4, 4 * cols * rows, 4 * cols * rows])):
+        a = Pair(x.reshape(-1), ne, nb).to(gpu)
+        o = Pair(np.full(1, -7, np.float32), [1, 1, 1, 1]).to(gpu)
+        assert eh.Kernel().process_event(eh.OpArgmax(a.pview(), o.pview(mut=True))) == eh.Status.OK, eh.last_error()
+        want = np.full(1, -7, np.float32)
+        assert orc.argmax(a.oview(), orc.view(want, [1, 1, 1, 1])) == orc.OK
+        assert want[0] == 0.0 and o.result()[0] == want[0], (o.result(), want)
+
+
 def test_argmax_rows_strided(gpu):
     cols, rows, pad = 999, 6, 1024
     x = normal(211, pad * rows * 2)
