@@ -120,3 +120,24 @@ def test_rejections_run_on_the_host_before_any_device_work():
     A3 = hv(np.ones(3, np.float32), [3, 1, 1, 1])
     assert lib.emel_op_add(r(A3), r(A3), r(O), None) == eh.Status.KERNEL_UNAVAILABLE
     assert (o == 9.0).all()
+
+
+def test_plain_c_caller_compiles_links_and_runs(tmp_path):
+    """include/emel_hip.h is valid strict C99 and a C program links the
+    library with no C++ or Python around it (what a Rust, cgo or JNI binding
+    does); on this host it runs the host-only entry points and sees the
+    accepted op reported as KERNEL_UNAVAILABLE, never run on the CPU."""
+    import subprocess
+
+    import __graft_entry__ as ge
+
+    if not (ge.PKG / "emel_hip" / "libemel_hip.so").exists():
+        pytest.skip("libemel_hip.so is not built")
+    exe = tmp_path / "c_caller"
+    r = subprocess.run(ge.c_caller_command(exe, str(ge.PKG / "emel_hip")), capture_output=True, text=True)
+    assert r.returncode == 0, r.stdout + r.stderr
+    import torch
+
+    mode = "gpu" if torch.cuda.is_available() else "cpu"
+    r = subprocess.run([str(exe), mode], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and f"c_caller {mode}: ok" in r.stdout, r.stdout + r.stderr
