@@ -279,7 +279,10 @@ static constexpr double kLogfLogc[16] = {
     0x1.526e57720db08p-3,  0x1.bc2860d22477p-3,   0x1.1058bc8a07ee1p-2,  0x1.4043057b6ee09p-2,
 };
 
-__host__ __device__ __forceinline__ float emel_logf(float x)
+// `invc` / `logc` are kLogfInvc / kLogfLogc or copies of them (kernels stage
+// them in LDS).
+__host__ __device__ __forceinline__ float emel_logf(float x, const double *invc = kLogfInvc,
+                                                    const double *logc = kLogfLogc)
 {
     constexpr double kA0 = -0x1.00ea348b88334p-2;
     constexpr double kA1 = 0x1.5575b0be00b6ap-2;
@@ -300,8 +303,8 @@ __host__ __device__ __forceinline__ float emel_logf(float x)
     const int32_t k = static_cast<int32_t>(tmp) >> 23;
     const uint32_t iz = ix - (tmp & (0x1ffu << 23));
     const double z = static_cast<double>(bits_to_f32(iz));
-    const double r = z * kLogfInvc[i] - 1.0;
-    const double y0 = kLogfLogc[i] + static_cast<double>(k) * kLn2;
+    const double r = z * invc[i] - 1.0;
+    const double y0 = logc[i] + static_cast<double>(k) * kLn2;
     const double r2 = r * r;
     double y = kA1 * r + kA2;
     y = kA0 * r2 + y;

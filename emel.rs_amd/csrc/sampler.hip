@@ -126,20 +126,37 @@ __device__ __forceinline__ uint64_t cand_word(uint32_t key, uint32_t idx)
     return (static_cast<uint64_t>(key) << 32) | static_cast<uint64_t>(~idx);
 }
 
-__device__ __forceinline__ uint32_t mulmod(uint32_t a, uint32_t b)
+// a * b mod (2^31 - 1) for a < 2^32, b < 2^31: since 2^31 == 1 (mod 2^31 - 1),
+// folding the high bits onto the low ones twice leaves r < 2 (2^31 - 1), and
+// one conditional subtraction gives the remainder.
+__host__ __device__ __forceinline__ constexpr uint32_t mulmod(uint32_t a, uint32_t b)
 {
-    return static_cast<uint32_t>((static_cast<uint64_t>(a) * b) % kModulus);
+    const uint64_t x = static_cast<uint64_t>(a) * b;
+    uint64_t r = (x & kModulus) + (x >> 31);
+    r = (r & kModulus) + (r >> 31);
+    return static_cast<uint32_t>(r >= kModulus ? r - kModulus : r);
 }
-__device__ __forceinline__ uint32_t powmod(uint64_t e)
+
+// 16807^(t+1) mod (2^31 - 1) for t < kRankThreads: the Park-Miller draw
+// multiplier of slot t (state_j = s0 16807^(j+1)); slot t + m kRankThreads
+// multiplies by kPmStride^m more.
+struct PmPowers {
+    uint32_t v[kRankThreads];
+};
+constexpr PmPowers make_pm_powers()
 {
-    uint32_t r = 1, b = static_cast<uint32_t>(kMultiplier);
-    while (e) {
-        if (e & 1) r = mulmod(r, b);
-        b = mulmod(b, b);
-        e >>= 1;
+    PmPowers p{};
+    uint32_t x = 1;
+    for (uint32_t t = 0; t < kRankThreads; ++t) {
+        x = mulmod(x, static_cast<uint32_t>(kMultiplier));
+        p.v[t] = x;
     }
-    return r;
+    return p;
 }
+static constexpr PmPowers kPmPowers = make_pm_powers();
+constexpr uint32_t kPmStride = kPmPowers.v[kRankThreads - 1]; // 16807^kRankThreads
+static_assert(kPmPowers.v[0] == 16807u && kPmPowers.v[1] == 282475249u && kPmPowers.v[2] == 1622650073u,
+              "Park-Miller powers: 16807, 16807^2, 16807^3 mod 2^31 - 1");
 
 // Visits the columns [c0, c1) of one row: float4 steps when the row is
 // 16-byte aligned (four loads in flight per thread before any is used),
@@ -926,19 +943,24 @@ __device__ void select_slots(const SmpGeo &g, uint32_t row, uint32_t s0, P prob,
 {
     __shared__ float s_v[kRankThreads / kWave];
     __shared__ uint32_t s_i[kRankThreads / kWave];
+    __shared__ double s_invc[16], s_logc[16]; // logf's table, read per lane
+    if (threadIdx.x < 16) {
+        s_invc[threadIdx.x] = kLogfInvc[threadIdx.x];
+        s_logc[threadIdx.x] = kLogfLogc[threadIdx.x];
+    }
+    __syncthreads();
     float best = -__builtin_inff();
     uint32_t bslot = kNone;
-    uint32_t pw = powmod(threadIdx.x + 1);
-    const uint32_t stride = powmod(blockDim.x);
-    for (uint32_t j = threadIdx.x; j < g.top_k; j += blockDim.x) {
+    uint32_t pw = kPmPowers.v[threadIdx.x]; // launched with kRankThreads threads
+    for (uint32_t j = threadIdx.x; j < g.top_k; j += kRankThreads) {
         const uint32_t state = mulmod(s0, pw);
         const float uniform = static_cast<float>(state) * 0x1p-31f;
-        const float race = prob(j) / -emel_logf(uniform);
+        const float race = prob(j) / -emel_logf(uniform, s_invc, s_logc);
         if (race > -__builtin_inff() && (race > best || (race == best && j < bslot))) {
             best = race;
             bslot = j;
         }
-        pw = mulmod(pw, stride);
+        pw = mulmod(pw, kPmStride);
     }
 #pragma unroll
     for (int off = kWave / 2; off > 0; off >>= 1) {
@@ -980,24 +1002,106 @@ __device__ __forceinline__ void write_ranked(const SmpGeo &g, const SmpOut &o, u
     o.sorted[static_cast<int64_t>(row) * o.sorted_ld + j] = static_cast<int32_t>(idx);
 }
 
-// Bitonic sort, descending, of s[0, n) (n a power of two).
-__device__ __forceinline__ void lds_sort_desc(uint64_t *s, uint32_t n)
+// Sort, descending, of s[0, n), for n a power of two with
+// kSortPer <= n <= kSortPer * blockDim.x.  Thread t sorts the run
+// s[t kSortPer, (t + 1) kSortPer) in registers (a bitonic network), then
+// sorted runs of length L merge pairwise into runs of 2 L, log2(n /
+// kSortPer) rounds: thread t produces kSortPer consecutive outputs of its
+// pair's merged run, finds where they start in the two runs with a
+// merge-path binary search, merges them in registers, and writes them back
+// once every thread has read.  Words are distinct except the zero padding,
+// whose copies are interchangeable; an exhausted run reads as 0.
+constexpr uint32_t kSortPer = 8;
+static_assert(kCap == kSortPer * kRankThreads, "one workgroup sorts kCap words");
+
+__device__ __forceinline__ void sort_regs_desc(uint64_t (&v)[kSortPer])
 {
-    for (uint32_t size = 2; size <= n; size <<= 1) {
+#pragma unroll
+    for (uint32_t size = 2; size <= kSortPer; size <<= 1) {
+#pragma unroll
         for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
-            for (uint32_t t = threadIdx.x; t < n / 2; t += blockDim.x) {
-                const uint32_t i = 2 * t - (t & (stride - 1));
-                const uint32_t j = i + stride;
-                const bool desc = (i & size) == 0;
-                const uint64_t a = s[i], b = s[j];
-                if ((a < b) == desc) {
-                    s[i] = b;
-                    s[j] = a;
+#pragma unroll
+            for (uint32_t i = 0; i < kSortPer; ++i) {
+                const uint32_t j = i ^ stride;
+                if (j > i) {
+                    const bool swap = (v[i] < v[j]) == ((i & size) == 0);
+                    const uint64_t a = v[i], b = v[j];
+                    v[i] = swap ? b : a;
+                    v[j] = swap ? a : b;
                 }
             }
-            __syncthreads();
         }
     }
+}
+
+__device__ void lds_sort_desc(uint64_t *s, uint32_t n)
+{
+    const uint32_t t = threadIdx.x;
+    const bool act = t * kSortPer < n;
+    uint64_t v[kSortPer];
+    if (act) {
+#pragma unroll
+        for (uint32_t r = 0; r < kSortPer; ++r) v[r] = s[t * kSortPer + r];
+        sort_regs_desc(v);
+    }
+    for (uint32_t len = kSortPer; len < n; len <<= 1) {
+        if (act) {
+#pragma unroll
+            for (uint32_t r = 0; r < kSortPer; ++r) s[t * kSortPer + r] = v[r];
+        }
+        __syncthreads();
+        if (act) {
+            const uint32_t per_pair = 2 * len / kSortPer; // threads per merged run
+            const uint64_t *A = s + (t / per_pair) * 2 * len, *B = A + len;
+            const uint32_t d = (t % per_pair) * kSortPer; // outputs before this thread's
+            // i = how many of the first d outputs come from A
+            uint32_t lo = d > len ? d - len : 0, hi = d < len ? d : len;
+            while (lo < hi) {
+                const uint32_t mid = (lo + hi) >> 1;
+                if (A[mid] > B[d - 1 - mid]) lo = mid + 1;
+                else hi = mid;
+            }
+            uint32_t i = lo, j = d - lo;
+            uint64_t a = A[i < len ? i : len - 1], b = B[j < len ? j : len - 1];
+            a = i < len ? a : 0ull;
+            b = j < len ? b : 0ull;
+#pragma unroll
+            for (uint32_t r = 0; r < kSortPer; ++r) {
+                const bool take_a = a > b;
+                v[r] = take_a ? a : b;
+                i += take_a ? 1u : 0u;
+                j += take_a ? 0u : 1u;
+                const uint64_t na = A[i < len ? i : len - 1], nb = B[j < len ? j : len - 1];
+                a = i < len ? na : 0ull;
+                b = j < len ? nb : 0ull;
+            }
+        }
+        __syncthreads(); // every read of this round precedes the next writes
+    }
+    if (act) {
+#pragma unroll
+        for (uint32_t r = 0; r < kSortPer; ++r) s[t * kSortPer + r] = v[r];
+    }
+    __syncthreads();
+}
+
+// Stages the words c[0, n) into s[0, np) (np <= kCap, zeros after n), all
+// of a thread's kSortPer global loads issued before its first LDS store.
+// Lanes past n read c[0] (inside the row's list) and store zero.
+__device__ __forceinline__ void stage_words(uint64_t *s, const uint64_t *c, uint32_t n, uint32_t np)
+{
+    uint64_t q[kSortPer];
+#pragma unroll
+    for (uint32_t r = 0; r < kSortPer; ++r) {
+        const uint32_t i = threadIdx.x + r * kRankThreads;
+        q[r] = c[i < n ? i : 0];
+    }
+#pragma unroll
+    for (uint32_t r = 0; r < kSortPer; ++r) {
+        const uint32_t i = threadIdx.x + r * kRankThreads;
+        if (i < np) s[i] = i < n ? q[r] : 0ull;
+    }
+    __syncthreads();
 }
 
 // Candidate lists of at most kCap: one workgroup sorts a row in LDS.
@@ -1007,11 +1111,9 @@ __global__ __launch_bounds__(kRankThreads) void k_smp_rank(SmpGeo g, SmpWs w, Sm
     const uint32_t row = row0 + blockIdx.x;
     const uint32_t count = w.sel[row].count; // top_k <= count <= kCap here
     const uint32_t n = count < kCap ? count : kCap;
-    uint32_t np = 2;
+    uint32_t np = kSortPer;
     while (np < n || np < g.top_k) np <<= 1;
-    const uint64_t *c = w.cand + static_cast<uint64_t>(row) * g.cand_ld;
-    for (uint32_t i = threadIdx.x; i < np; i += blockDim.x) s_c[i] = i < n ? c[i] : 0ull;
-    __syncthreads();
+    stage_words(s_c, w.cand + static_cast<uint64_t>(row) * g.cand_ld, n, np);
     lds_sort_desc(s_c, np);
     for (uint32_t j = threadIdx.x; j < g.top_k; j += blockDim.x) write_ranked(g, o, row, j, s_c[j]);
     select_slots(
@@ -1028,11 +1130,10 @@ __global__ __launch_bounds__(kRankThreads) void k_smp_tile_sort(SmpGeo g, SmpWs 
     const uint32_t b0 = tile * kCap;
     if (b0 >= n) return;
     const uint32_t len = n - b0 < kCap ? n - b0 : kCap;
-    uint32_t np = 2;
+    uint32_t np = kSortPer;
     while (np < len) np <<= 1;
     uint64_t *c = w.cand + static_cast<uint64_t>(row) * g.cand_ld + b0;
-    for (uint32_t i = threadIdx.x; i < np; i += blockDim.x) s_c[i] = i < len ? c[i] : 0ull;
-    __syncthreads();
+    stage_words(s_c, c, len, np);
     lds_sort_desc(s_c, np);
     for (uint32_t i = threadIdx.x; i < len; i += blockDim.x) c[i] = s_c[i];
 }
@@ -1075,7 +1176,20 @@ __global__ __launch_bounds__(kRankThreads) void k_smp_finish(SmpGeo g, const uin
 {
     const uint32_t row = row0 + blockIdx.x;
     const uint64_t *c = sorted + static_cast<uint64_t>(row) * g.cand_ld;
-    for (uint32_t j = threadIdx.x; j < g.top_k; j += blockDim.x) write_ranked(g, o, row, j, c[j]);
+    // kSortPer loads in flight per thread before the ranked stores
+    for (uint32_t j0 = 0; j0 < g.top_k; j0 += kSortPer * kRankThreads) {
+        uint64_t q[kSortPer];
+#pragma unroll
+        for (uint32_t r = 0; r < kSortPer; ++r) {
+            const uint32_t j = j0 + threadIdx.x + r * kRankThreads;
+            q[r] = c[j < g.top_k ? j : 0];
+        }
+#pragma unroll
+        for (uint32_t r = 0; r < kSortPer; ++r) {
+            const uint32_t j = j0 + threadIdx.x + r * kRankThreads;
+            if (j < g.top_k) write_ranked(g, o, row, j, q[r]);
+        }
+    }
     select_slots(
         g, row, st.v[blockIdx.x], [&](uint32_t j) { return from_key(static_cast<uint32_t>(c[j] >> 32)); },
         [&](uint32_t j) { return static_cast<int32_t>(~static_cast<uint32_t>(c[j])); }, o);
