@@ -1002,9 +1002,9 @@ __device__ __forceinline__ void write_ranked(const SmpGeo &g, const SmpOut &o, u
     o.sorted[static_cast<int64_t>(row) * o.sorted_ld + j] = static_cast<int32_t>(idx);
 }
 
-// Sort, descending, of s[0, n), for n a power of two with
-// kSortPer <= n <= kSortPer * blockDim.x.  Thread t sorts the run
-// s[t kSortPer, (t + 1) kSortPer) in registers (a bitonic network), then
+// Sort, descending, of the elements [0, n) held in s at slot(e), for n a
+// power of two with kSortPer <= n <= kSortPer * blockDim.x.  Thread t sorts
+// the run [t kSortPer, (t + 1) kSortPer) in registers (a bitonic network), then
 // sorted runs of length L merge pairwise into runs of 2 L, log2(n /
 // kSortPer) rounds: thread t produces kSortPer consecutive outputs of its
 // pair's merged run, finds where they start in the two runs with a
@@ -1013,6 +1013,12 @@ __device__ __forceinline__ void write_ranked(const SmpGeo &g, const SmpOut &o, u
 // whose copies are interchangeable; an exhausted run reads as 0.
 constexpr uint32_t kSortPer = 8;
 static_assert(kCap == kSortPer * kRankThreads, "one workgroup sorts kCap words");
+
+// LDS slot of sort element e: one pad word after every 32 (256 bytes), so
+// that lanes touching elements 8 or 4 apart (each lane's run, the merge
+// fronts) spread over the banks instead of sharing a few.
+__device__ __forceinline__ uint32_t slot(uint32_t e) { return e + (e >> 5); }
+constexpr uint32_t kCapSlots = kCap + kCap / 32;
 
 __device__ __forceinline__ void sort_regs_desc(uint64_t (&v)[kSortPer])
 {
@@ -1041,28 +1047,28 @@ __device__ void lds_sort_desc(uint64_t *s, uint32_t n)
     uint64_t v[kSortPer];
     if (act) {
 #pragma unroll
-        for (uint32_t r = 0; r < kSortPer; ++r) v[r] = s[t * kSortPer + r];
+        for (uint32_t r = 0; r < kSortPer; ++r) v[r] = s[slot(t * kSortPer + r)];
         sort_regs_desc(v);
     }
     for (uint32_t len = kSortPer; len < n; len <<= 1) {
         if (act) {
 #pragma unroll
-            for (uint32_t r = 0; r < kSortPer; ++r) s[t * kSortPer + r] = v[r];
+            for (uint32_t r = 0; r < kSortPer; ++r) s[slot(t * kSortPer + r)] = v[r];
         }
         __syncthreads();
         if (act) {
             const uint32_t per_pair = 2 * len / kSortPer; // threads per merged run
-            const uint64_t *A = s + (t / per_pair) * 2 * len, *B = A + len;
+            const uint32_t a0 = (t / per_pair) * 2 * len, b0 = a0 + len; // the two runs
             const uint32_t d = (t % per_pair) * kSortPer; // outputs before this thread's
-            // i = how many of the first d outputs come from A
+            // i = how many of the first d outputs come from run A
             uint32_t lo = d > len ? d - len : 0, hi = d < len ? d : len;
             while (lo < hi) {
                 const uint32_t mid = (lo + hi) >> 1;
-                if (A[mid] > B[d - 1 - mid]) lo = mid + 1;
+                if (s[slot(a0 + mid)] > s[slot(b0 + d - 1 - mid)]) lo = mid + 1;
                 else hi = mid;
             }
             uint32_t i = lo, j = d - lo;
-            uint64_t a = A[i < len ? i : len - 1], b = B[j < len ? j : len - 1];
+            uint64_t a = s[slot(a0 + (i < len ? i : len - 1))], b = s[slot(b0 + (j < len ? j : len - 1))];
             a = i < len ? a : 0ull;
             b = j < len ? b : 0ull;
 #pragma unroll
@@ -1071,7 +1077,8 @@ __device__ void lds_sort_desc(uint64_t *s, uint32_t n)
                 v[r] = take_a ? a : b;
                 i += take_a ? 1u : 0u;
                 j += take_a ? 0u : 1u;
-                const uint64_t na = A[i < len ? i : len - 1], nb = B[j < len ? j : len - 1];
+                const uint64_t na = s[slot(a0 + (i < len ? i : len - 1))];
+                const uint64_t nb = s[slot(b0 + (j < len ? j : len - 1))];
                 a = i < len ? na : 0ull;
                 b = j < len ? nb : 0ull;
             }
@@ -1080,12 +1087,13 @@ __device__ void lds_sort_desc(uint64_t *s, uint32_t n)
     }
     if (act) {
 #pragma unroll
-        for (uint32_t r = 0; r < kSortPer; ++r) s[t * kSortPer + r] = v[r];
+        for (uint32_t r = 0; r < kSortPer; ++r) s[slot(t * kSortPer + r)] = v[r];
     }
     __syncthreads();
 }
 
-// Stages the words c[0, n) into s[0, np) (np <= kCap, zeros after n), all
+// Stages the words c[0, n) into sort elements [0, np) of s (np <= kCap,
+// zeros after n), all
 // of a thread's kSortPer global loads issued before its first LDS store.
 // Lanes past n read c[0] (inside the row's list) and store zero.
 __device__ __forceinline__ void stage_words(uint64_t *s, const uint64_t *c, uint32_t n, uint32_t np)
@@ -1099,7 +1107,7 @@ __device__ __forceinline__ void stage_words(uint64_t *s, const uint64_t *c, uint
 #pragma unroll
     for (uint32_t r = 0; r < kSortPer; ++r) {
         const uint32_t i = threadIdx.x + r * kRankThreads;
-        if (i < np) s[i] = i < n ? q[r] : 0ull;
+        if (i < np) s[slot(i)] = i < n ? q[r] : 0ull;
     }
     __syncthreads();
 }
@@ -1107,7 +1115,7 @@ __device__ __forceinline__ void stage_words(uint64_t *s, const uint64_t *c, uint
 // Candidate lists of at most kCap: one workgroup sorts a row in LDS.
 __global__ __launch_bounds__(kRankThreads) void k_smp_rank(SmpGeo g, SmpWs w, SmpOut o, SmpStates st, uint32_t row0)
 {
-    __shared__ uint64_t s_c[kCap];
+    __shared__ uint64_t s_c[kCapSlots];
     const uint32_t row = row0 + blockIdx.x;
     const uint32_t count = w.sel[row].count; // top_k <= count <= kCap here
     const uint32_t n = count < kCap ? count : kCap;
@@ -1115,16 +1123,16 @@ __global__ __launch_bounds__(kRankThreads) void k_smp_rank(SmpGeo g, SmpWs w, Sm
     while (np < n || np < g.top_k) np <<= 1;
     stage_words(s_c, w.cand + static_cast<uint64_t>(row) * g.cand_ld, n, np);
     lds_sort_desc(s_c, np);
-    for (uint32_t j = threadIdx.x; j < g.top_k; j += blockDim.x) write_ranked(g, o, row, j, s_c[j]);
+    for (uint32_t j = threadIdx.x; j < g.top_k; j += blockDim.x) write_ranked(g, o, row, j, s_c[slot(j)]);
     select_slots(
-        g, row, st.v[blockIdx.x], [&](uint32_t j) { return from_key(static_cast<uint32_t>(s_c[j] >> 32)); },
-        [&](uint32_t j) { return static_cast<int32_t>(~static_cast<uint32_t>(s_c[j])); }, o);
+        g, row, st.v[blockIdx.x], [&](uint32_t j) { return from_key(static_cast<uint32_t>(s_c[slot(j)] >> 32)); },
+        [&](uint32_t j) { return static_cast<int32_t>(~static_cast<uint32_t>(s_c[slot(j)])); }, o);
 }
 
 // Longer lists (top_k > kCap, so count == top_k): sorted kCap tiles ...
 __global__ __launch_bounds__(kRankThreads) void k_smp_tile_sort(SmpGeo g, SmpWs w, uint32_t tiles)
 {
-    __shared__ uint64_t s_c[kCap];
+    __shared__ uint64_t s_c[kCapSlots];
     const uint32_t row = blockIdx.x / tiles, tile = blockIdx.x % tiles;
     const uint32_t n = w.sel[row].count;
     const uint32_t b0 = tile * kCap;
@@ -1135,7 +1143,7 @@ __global__ __launch_bounds__(kRankThreads) void k_smp_tile_sort(SmpGeo g, SmpWs 
     uint64_t *c = w.cand + static_cast<uint64_t>(row) * g.cand_ld + b0;
     stage_words(s_c, c, len, np);
     lds_sort_desc(s_c, np);
-    for (uint32_t i = threadIdx.x; i < len; i += blockDim.x) c[i] = s_c[i];
+    for (uint32_t i = threadIdx.x; i < len; i += blockDim.x) c[i] = s_c[slot(i)];
 }
 
 // ... merged pairwise (runs of `width` into runs of 2 width), kMergePer
