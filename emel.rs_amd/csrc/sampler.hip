@@ -26,12 +26,12 @@
 //                 LDS.
 //   k_smp_div     (row, chunk): p written in place, plus the histogram of the
 //                 top 11 bits of p's total-order key.
-//   k_smp_pick / k_smp_refine
-//                 radix selection of the top_k-th key: 11, 11, 10 key bits.
-//                 A row stops as soon as every key at or above its current
-//                 prefix fits the kCap candidates one workgroup sorts; at
-//                 32 bits the threshold key T is exact.
-//   k_smp_ties    (row, chunk): elements equal to T per chunk (exact rows).
+//   k_smp_resolve one workgroup per row: radix selection of the top_k-th
+//                 key, 11, 11, 10 key bits.  A row stops as soon as every
+//                 key at or above its current prefix fits the kCap
+//                 candidates one workgroup sorts; at 32 bits the threshold
+//                 key T is exact and the elements equal to T are counted
+//                 per chunk.
 //   k_smp_collect (row, chunk): candidates (key, index) into a per-row list:
 //                 every key >= prefix, or every key > T plus the lowest-index
 //                 ties at T up to top_k.
@@ -159,11 +159,11 @@ static_assert(kPmPowers.v[0] == 16807u && kPmPowers.v[1] == 282475249u && kPmPow
               "Park-Miller powers: 16807, 16807^2, 16807^3 mod 2^31 - 1");
 
 // Visits the columns [c0, c1) of one row: float4 steps when the row is
-// 16-byte aligned (four loads in flight per thread before any is used),
-// then a scalar tail.  The order of the visits is unspecified: callers
-// only reduce order-independently or write elementwise.
+// 16-byte aligned (U loads in flight per thread before any is used), then
+// a scalar tail.  The order of the visits is unspecified: callers only
+// reduce order-independently or write elementwise.
 // f(float &v, uint64_t col) may modify v; WRITE stores it back.
-template <bool WRITE, class F>
+template <bool WRITE, int U = 4, class F>
 __device__ __forceinline__ void visit(const SmpGeo &g, float *row, uint64_t c0, uint64_t c1, F f)
 {
     uint64_t c = c0;
@@ -178,12 +178,12 @@ __device__ __forceinline__ void visit(const SmpGeo &g, float *row, uint64_t c0, 
             f(q.z, 4 * vi + 2);
             f(q.w, 4 * vi + 3);
         };
-        for (; v + 3 * bs < v1; v += 4 * bs) {
-            float4 q[4];
+        for (; v + (U - 1) * bs < v1; v += U * bs) {
+            float4 q[U];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) q[j] = r4[v + j * bs];
+            for (int j = 0; j < U; ++j) q[j] = r4[v + j * bs];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int j = 0; j < U; ++j) {
                 apply(q[j], v + j * bs);
                 if constexpr (WRITE) r4[v + j * bs] = q[j];
             }
@@ -712,9 +712,6 @@ __global__ __launch_bounds__(kBlock) void k_smp_div(SmpGeo g, float *logits, Smp
     flush_hist(s_hist, kBins, w.hist + static_cast<uint64_t>(row) * kBins);
 }
 
-
-// ---- stages 5-6: radix selection of the top_k-th key ------------------------
-
 // Inclusive prefix sum over a 256-thread workgroup (uses s_tmp[4]).
 __device__ __forceinline__ uint32_t block_incl_scan256(uint32_t v, uint32_t *s_tmp, uint32_t &total)
 {
@@ -736,28 +733,56 @@ __device__ __forceinline__ uint32_t block_incl_scan256(uint32_t v, uint32_t *s_t
     return v + before;
 }
 
-// pass = 0, 1, 2 (digits of 11, 11, 10 bits): picks the threshold digit b
-// from the histogram of the row's open prefix region -- the digit with
-// greater(b) < need <= greater(b) + count(b), greater(b) counting the
-// higher digits -- then clears the histogram for the next pass.
-__global__ __launch_bounds__(kBlock) void k_smp_pick(SmpWs w, uint32_t pass)
+// ---- stages 5-7: the threshold, one workgroup per row ----------------------
+//
+// Digits of the total-order key, 11, 11 and 10 bits from the top.  A pick
+// finds the digit b holding the need-th largest key of the row's open
+// prefix region -- greater(b) < need <= greater(b) + count(b), greater(b)
+// counting the higher digits -- and extends the prefix by it.  The row is
+// resolved as soon as every key at or above the prefix fits the kCap
+// candidates one workgroup sorts (mode 1); at 32 bits the threshold key T
+// is exact (mode 2) and the ties at T are counted per chunk, for the
+// collect step to take the lowest-index ones.  The first digit's histogram
+// comes from k_smp_div; the later ones (rows that need them) from scans of
+// the row here, so rows resolved by the first digit cost one short launch.
+
+constexpr uint32_t kResolveThreads = 1024;
+
+// Inclusive prefix sum over a kResolveThreads workgroup (s_tmp: one word
+// per wave).
+__device__ __forceinline__ uint32_t block_incl_scan1024(uint32_t v, uint32_t *s_tmp, uint32_t &total)
 {
-    __shared__ uint32_t s_tmp[kBlock / kWave];
-    __shared__ uint32_t s_pick[3];
-    const uint32_t row = blockIdx.x;
-    const RowSel sel = w.sel[row];
-    if (sel.mode != 0) return;
-    const uint32_t bits = pass == 2 ? 10u : 11u;
-    const uint32_t per = (1u << bits) / kBlock; // 8 or 4 bins per thread
-    uint32_t *h = w.hist + static_cast<uint64_t>(row) * kBins;
-    uint32_t mine[kBins / kBlock];
+    const uint32_t lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    v = wave_incl_scan(v);
+    if (lane == kWave - 1) s_tmp[wave] = v;
+    __syncthreads();
+    uint32_t before = 0;
+    total = 0;
+#pragma unroll
+    for (uint32_t w = 0; w < kResolveThreads / kWave; ++w) {
+        const uint32_t x = s_tmp[w];
+        before += w < wave ? x : 0u;
+        total += x;
+    }
+    __syncthreads(); // s_tmp may be rewritten after this
+    return v + before;
+}
+
+// The pick over hist[0, 2^bits), bins in increasing key order; returns the
+// advanced selection (the same in every thread).
+__device__ RowSel pick_digit(const RowSel &sel, const uint32_t *hist, uint32_t bits, uint32_t *s_tmp,
+                             uint32_t *s_pick)
+{
+    const uint32_t per = (1u << bits) / kResolveThreads; // 2 or 1 bins per thread
+    uint32_t mine[kBins / kResolveThreads] = {};
     uint32_t local = 0;
     for (uint32_t i = 0; i < per; ++i) {
-        mine[i] = h[threadIdx.x * per + i];
+        mine[i] = hist[threadIdx.x * per + i];
         local += mine[i];
     }
+    if (threadIdx.x == 0) s_pick[0] = s_pick[1] = s_pick[2] = 0;
     uint32_t total;
-    const uint32_t incl = block_incl_scan256(local, s_tmp, total);
+    const uint32_t incl = block_incl_scan1024(local, s_tmp, total); // its barriers order s_pick's reset
     uint32_t cum = total - incl; // elements in higher threads' (higher) digits
     for (int i = static_cast<int>(per) - 1; i >= 0; --i) {
         if (cum < sel.need && sel.need <= cum + mine[i]) {
@@ -767,9 +792,7 @@ __global__ __launch_bounds__(kBlock) void k_smp_pick(SmpWs w, uint32_t pass)
         }
         cum += mine[i];
     }
-    for (uint32_t i = 0; i < per; ++i) h[threadIdx.x * per + i] = 0;
     __syncthreads();
-    if (threadIdx.x != 0) return;
     RowSel n = sel;
     n.prefix = (sel.prefix << bits) | s_pick[0];
     n.depth = sel.depth + bits;
@@ -782,49 +805,49 @@ __global__ __launch_bounds__(kBlock) void k_smp_pick(SmpWs w, uint32_t pass)
         n.mode = 2; // keys > T, then the lowest-index `need` keys == T
         n.count = n.above + n.need;
     }
-    w.sel[row] = n;
+    __syncthreads(); // s_pick is read by every thread before the next pick
+    return n;
 }
 
-// pass = 1, 2: histogram of the next digit over the open prefix region.
-__global__ __launch_bounds__(kBlock) void k_smp_refine(SmpGeo g, float *logits, SmpWs w, uint32_t pass)
+__global__ __launch_bounds__(kResolveThreads) void k_smp_resolve(SmpGeo g, float *logits, SmpWs w)
 {
-    __shared__ uint32_t s_hist[kBins];
-    const uint32_t row = blockIdx.x / g.chunks, chunk = blockIdx.x % g.chunks;
-    const RowSel sel = w.sel[row];
-    if (sel.mode != 0) return;
-    const uint32_t bits = pass == 2 ? 10u : 11u;
-    const uint32_t nbins = 1u << bits;
-    const uint32_t dshift = 32u - sel.depth; // depth is 11 or 22 here
-    const uint32_t shift = dshift - bits;
-    for (uint32_t b = threadIdx.x; b < nbins; b += blockDim.x) s_hist[b] = 0;
-    __syncthreads();
+    __shared__ uint32_t s_hist[kBins]; // digit histogram; later the per-chunk tie counts
+    __shared__ uint32_t s_tmp[kResolveThreads / kWave];
+    __shared__ uint32_t s_pick[3];
+    const uint32_t row = blockIdx.x;
+    RowSel sel = w.sel[row];
+    if (sel.mode != 0) return; // uniform
+    sel = pick_digit(sel, w.hist + static_cast<uint64_t>(row) * kBins, 11, s_tmp, s_pick);
     float *x = logits + static_cast<int64_t>(row) * g.ld;
-    uint64_t c0, c1;
-    chunk_range(g, chunk, c0, c1);
-    const uint32_t prefix = sel.prefix;
-    visit<false>(g, x, c0, c1, [&](float &v, uint64_t) {
-        const uint32_t key = total_key(v);
-        if ((key >> dshift) == prefix) atomicAdd(&s_hist[(key >> shift) & (nbins - 1)], 1u);
-    });
-    flush_hist(s_hist, nbins, w.hist + static_cast<uint64_t>(row) * kBins);
-}
-
-// ---- stage 7: ties at the exact threshold, per chunk ------------------------
-
-__global__ __launch_bounds__(kBlock) void k_smp_ties(SmpGeo g, float *logits, SmpWs w)
-{
-    __shared__ uint32_t s_tmp[kBlock / kWave];
-    const uint32_t row = blockIdx.x / g.chunks, chunk = blockIdx.x % g.chunks;
-    const RowSel sel = w.sel[row];
-    if (sel.mode != 2) return;
-    float *x = logits + static_cast<int64_t>(row) * g.ld;
-    uint64_t c0, c1;
-    chunk_range(g, chunk, c0, c1);
-    uint32_t c = 0;
-    visit<false>(g, x, c0, c1, [&](float &v, uint64_t) { c += total_key(v) == sel.prefix ? 1u : 0u; });
-    uint32_t total;
-    (void)block_incl_scan256(c, s_tmp, total);
-    if (threadIdx.x == 0) w.ties[blockIdx.x] = total;
+    for (uint32_t pass = 1; pass <= 2 && sel.mode == 0; ++pass) {
+        const uint32_t bits = pass == 2 ? 10u : 11u;
+        const uint32_t nbins = 1u << bits;
+        const uint32_t dshift = 32u - sel.depth; // depth is 11 or 22 here
+        const uint32_t shift = dshift - bits;
+        const uint32_t prefix = sel.prefix;
+        for (uint32_t b = threadIdx.x; b < nbins; b += blockDim.x) s_hist[b] = 0;
+        __syncthreads();
+        visit<false>(g, x, 0, g.card, [&](float &v, uint64_t) {
+            const uint32_t key = total_key(v);
+            if ((key >> dshift) == prefix) atomicAdd(&s_hist[(key >> shift) & (nbins - 1)], 1u);
+        });
+        __syncthreads();
+        sel = pick_digit(sel, s_hist, bits, s_tmp, s_pick);
+    }
+    if (sel.mode == 2) {
+        // chunks <= kBins (launch_sampler checks it)
+        for (uint32_t c = threadIdx.x; c < g.chunks; c += blockDim.x) s_hist[c] = 0;
+        __syncthreads();
+        const uint32_t t_key = sel.prefix;
+        const uint32_t cc = static_cast<uint32_t>(g.chunk_cols);
+        visit<false>(g, x, 0, g.card, [&](float &v, uint64_t col) {
+            if (total_key(v) == t_key) atomicAdd(&s_hist[static_cast<uint32_t>(col) / cc], 1u);
+        });
+        __syncthreads();
+        for (uint32_t c = threadIdx.x; c < g.chunks; c += blockDim.x)
+            w.ties[static_cast<uint64_t>(row) * g.chunks + c] = s_hist[c];
+    }
+    if (threadIdx.x == 0) w.sel[row] = sel;
 }
 
 // ---- stage 8: candidates ------------------------------------------------------
@@ -1319,6 +1342,7 @@ hipError_t launch_sampler(const SamplerArgs &a, hipStream_t s)
     g.rows = a.rows;
     g.card = a.card;
     plan_chunks(a.rows, a.card, g.chunk_cols, g.chunks);
+    if (g.chunks > kBins) return hipErrorInvalidValue; // k_smp_resolve counts ties per chunk in kBins words
     g.ld = a.logits_ld;
     g.vec = (reinterpret_cast<uintptr_t>(a.logits) % 16 == 0) && (a.rows == 1 || a.logits_ld % 4 == 0);
     g.top_k = a.top_k;
@@ -1343,12 +1367,7 @@ hipError_t launch_sampler(const SamplerArgs &a, hipStream_t s)
     k_smp_seg<<<grid, kBlock, 0, s>>>(g, a.logits, w);
     k_smp_sum<<<a.rows, kBlock, 0, s>>>(g, a.logits, w);
     k_smp_div<<<grid, kBlock, 0, s>>>(g, a.logits, w);
-    k_smp_pick<<<a.rows, kBlock, 0, s>>>(w, 0);
-    k_smp_refine<<<grid, kBlock, 0, s>>>(g, a.logits, w, 1);
-    k_smp_pick<<<a.rows, kBlock, 0, s>>>(w, 1);
-    k_smp_refine<<<grid, kBlock, 0, s>>>(g, a.logits, w, 2);
-    k_smp_pick<<<a.rows, kBlock, 0, s>>>(w, 2);
-    k_smp_ties<<<grid, kBlock, 0, s>>>(g, a.logits, w);
+    k_smp_resolve<<<a.rows, kResolveThreads, 0, s>>>(g, a.logits, w);
     k_smp_collect<<<grid, kBlock, 0, s>>>(g, a.logits, w);
 
     SmpOut o{};
