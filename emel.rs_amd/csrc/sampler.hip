@@ -466,21 +466,26 @@ __device__ __forceinline__ void sum_tile(const float (&e)[PER], SumState &s, uin
     }
     // start: tile-relative index of the first uncommitted element
     while (true) {
+        // this round's units at the current binade (0 for committed
+        // elements), kept for the event search below
+        uint32_t r[PER];
         uint32_t lsum = 0, ties = 0;
         if (start == 0) {
 #pragma unroll
             for (uint32_t j = 0; j < PER; ++j) {
                 bool tie;
-                lsum += seq_units(e[j], s.u, tie);
+                r[j] = seq_units(e[j], s.u, tie);
+                lsum += r[j];
                 ties |= static_cast<uint32_t>(tie) << j;
             }
         } else { // elements before start are committed
 #pragma unroll
             for (uint32_t j = 0; j < PER; ++j) {
                 bool tie;
-                const uint32_t r = seq_units(e[j], s.u, tie);
+                const uint32_t q = seq_units(e[j], s.u, tie);
                 const bool active = PER * lane + j >= start;
-                lsum += active ? r : 0u;
+                r[j] = active ? q : 0u;
+                lsum += r[j];
                 ties |= static_cast<uint32_t>(active && tie) << j;
             }
         }
@@ -501,13 +506,11 @@ __device__ __forceinline__ void sum_tile(const float (&e)[PER], SumState &s, uin
 #pragma unroll
         for (uint32_t j = 0; j < PER; ++j) {
             if (mine == kNone && PER * lane + j >= start) {
-                bool tie;
-                const uint32_t r = seq_units(e[j], s.u, tie);
-                if (tie || run + r >= kSeqLimit) {
+                if (((ties >> j) & 1u) || run + r[j] >= kSeqLimit) {
                     mine = PER * lane + j;
                     ek = e[j];
                 } else {
-                    run += r;
+                    run += r[j];
                 }
             }
         }
@@ -564,6 +567,24 @@ __global__ __launch_bounds__(kBlock) void k_smp_sum(SmpGeo g, const float *logit
     const SegInfo *seg = w.seg + static_cast<uint64_t>(row) * nslots;
     SegInfo nxt{0, 0, 8u, 0};
     if (lane < nslots) nxt = seg[lane];
+    // A sub-chunk's elements, one float4 (or four floats) per thread; every
+    // address is clamped into the sub-chunk, so the loads are unconditional.
+    auto load_slot = [&](uint32_t slot, float4 &v, uint32_t &n) {
+        uint64_t c0, c1;
+        chunk_range(g, slot / spc, c0, c1);
+        const uint64_t a0 = c0 + static_cast<uint64_t>(slot % spc) * kSub;
+        const uint64_t a1 = a0 + kSub < c1 ? a0 + kSub : c1;
+        n = static_cast<uint32_t>(a1 - a0); // 1 .. kSub
+        const uint32_t q = threadIdx.x;
+        if (g.vec && a1 <= card4) { // a0 is a multiple of 4: whole float4s
+            v = reinterpret_cast<const float4 *>(x + a0)[4 * q < n ? q : 0u];
+        } else {
+            float t[4];
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j) t[j] = x[a0 + (4 * q + j < n ? 4 * q + j : 0u)];
+            v = make_float4(t[0], t[1], t[2], t[3]);
+        }
+    };
     for (uint32_t kb = 0; kb < nslots && !nan_final; kb += kWave) {
         const SegInfo mine = nxt;
         if (kb + kWave + lane < nslots) nxt = seg[kb + kWave + lane];
@@ -606,18 +627,14 @@ __global__ __launch_bounds__(kBlock) void k_smp_sum(SmpGeo g, const float *logit
                 }
                 // stage the sub-chunk: one float4 (or four floats) per thread
                 const uint32_t slot = kb + f;
-                uint64_t c0, c1;
-                chunk_range(g, slot / spc, c0, c1);
-                const uint64_t a0 = c0 + static_cast<uint64_t>(slot % spc) * kSub;
-                const uint64_t a1 = a0 + kSub < c1 ? a0 + kSub : c1;
-                const uint32_t n = static_cast<uint32_t>(a1 - a0);
-                float *st = reinterpret_cast<float *>(s_stage);
-                const uint32_t q = threadIdx.x; // kSub / 4 == kBlock
-                if (g.vec && a1 <= card4) {     // a0 is a multiple of 4: whole float4s
-                    if (4 * q < n) s_stage[q] = reinterpret_cast<const float4 *>(x + a0)[q];
-                } else {
-#pragma unroll
-                    for (uint32_t j = 0; j < 4; ++j) st[4 * q + j] = 4 * q + j < n ? x[a0 + 4 * q + j] : 0.0f;
+                float4 v;
+                uint32_t n;
+                load_slot(slot, v, n);
+                const float *st = reinterpret_cast<const float *>(s_stage);
+                {
+                    const uint32_t q = threadIdx.x; // kSub / 4 == kBlock; +0 past n
+                    s_stage[q] = make_float4(4 * q < n ? v.x : 0.0f, 4 * q + 1 < n ? v.y : 0.0f,
+                                             4 * q + 2 < n ? v.z : 0.0f, 4 * q + 3 < n ? v.w : 0.0f);
                 }
                 __syncthreads();
                 if (wave == 0) {
@@ -626,12 +643,20 @@ __global__ __launch_bounds__(kBlock) void k_smp_sum(SmpGeo g, const float *logit
                     // its addends), each of which would cost a round: lane 0
                     // adds them one by one, the reference's own arithmetic.
                     uint32_t head = 0;
-                    if (a0 == 0 && s.finite && s.m == 0) {
+                    if (slot == 0 && s.finite && s.m == 0) { // the row's first sub-chunk
                         head = n < kHead ? n : kHead;
                         float acc = seq_value(s.m, s.u);
                         if (lane == 0) {
+                            // whole float4s: past n the stage holds +0, which
+                            // leaves the (never -0) running sum unchanged
 #pragma unroll 8
-                            for (uint32_t j = 0; j < head; ++j) acc += st[j];
+                            for (uint32_t j = 0; j < (head + 3) / 4; ++j) {
+                                const float4 q4 = s_stage[j];
+                                acc += q4.x;
+                                acc += q4.y;
+                                acc += q4.z;
+                                acc += q4.w;
+                            }
                         }
                         acc = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, acc)));
                         if (!(acc < __builtin_inff())) {
