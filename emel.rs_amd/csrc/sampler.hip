@@ -432,16 +432,15 @@ __global__ __launch_bounds__(kBlock) void k_smp_seg(SmpGeo g, float *logits, Smp
 
 // ---- stage 3: the exact sequential sum of e ----------------------------------
 //
-// One wave per row walks the row's chunks in order.  A chunk whose
+// One wave per row walks the row's sub-chunks in order.  A sub-chunk whose
 // predicted contribution (k_smp_seg) holds on the exact state -- the same
-// binade, no tie, and the units stay below 2^24, so no element inside it
-// can cross (units never decrease) -- is added in one step.  Any other
-// chunk is walked element by element in tiles of 64 lanes x 4 elements: a
-// round computes the tile's units at the current binade and their wave
-// prefix sum, and either commits the rest of the tile (no event) or finds
-// the first event element, adds it with one f32 addition and starts the
-// next round after it.  Each round commits at least one element, so the
-// rounds end.  Eight tiles are in flight ahead of the one being summed.
+// binade, and the units stay below 2^24, so no element inside it can cross
+// (units never decrease) -- is added in one step.  Any other sub-chunk is
+// walked as one tile of 64 lanes x 16 elements: a round computes the
+// tile's units at the current binade and their wave prefix sum, and either
+// commits the rest of the tile (no event) or finds the first event
+// element, adds it with one f32 addition and starts the next round after
+// it.  Each round commits at least one element, so the rounds end.
 
 struct SumState {
     uint32_t m;
@@ -541,20 +540,21 @@ __device__ __forceinline__ void sum_tile(const float (&e)[PER], SumState &s, uin
 constexpr uint32_t kPer = kSub / kWave; // 16 elements per lane and round of the walk
 constexpr uint32_t kHead = 512;          // a row's first elements, added one by one
 
-// One 256-thread workgroup per row; every wave keeps the same state.  The
-// sub-chunks' predictions are read a batch at a time (lane i of every wave
-// holds sub-chunk kb + i's).  A sub-chunk whose predicted contribution holds
-// on the exact state -- the same binade, and the units (its one tie
-// resolved by the current parity) stay below 2^24, so no element inside it
-// can cross (units never decrease) -- is added in one step.  Any other
-// sub-chunk is staged in LDS by the whole workgroup (one load latency) and
-// walked by wave 0: one round, plus one per event.
-__global__ __launch_bounds__(kBlock) void k_smp_sum(SmpGeo g, const float *logits, SmpWs w)
+// One wave per row.  The sub-chunks' predictions are read a batch at a
+// time (lane i holds sub-chunk kb + i's).  A sub-chunk whose predicted
+// contribution holds on the exact state -- the same binade, and the units
+// (its one tie resolved by the current parity) stay below 2^24, so no
+// element inside it can cross (units never decrease) -- is added in one
+// step.  Any other sub-chunk is loaded straight into the walk's registers
+// (lane l holds its elements 16 l .. 16 l + 15, four 128-bit loads in
+// flight) and walked: one round, plus one per event.
+constexpr uint32_t kSumThreads = kWave;
+
+__global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *logits, SmpWs w)
 {
-    __shared__ float4 s_stage[kSub / 4];
-    __shared__ uint32_t s_state[4];
+    __shared__ float4 s_head[kHead / 4]; // the row's first elements, for lane 0's sequential adds
     const uint32_t row = blockIdx.x;
-    const uint32_t lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const uint32_t lane = threadIdx.x;
     const float *x = logits + static_cast<int64_t>(row) * g.ld;
     const uint32_t spc = subs_per_chunk(g);
     const uint64_t card4 = g.card & ~uint64_t{3};
@@ -567,143 +567,120 @@ __global__ __launch_bounds__(kBlock) void k_smp_sum(SmpGeo g, const float *logit
     const SegInfo *seg = w.seg + static_cast<uint64_t>(row) * nslots;
     SegInfo nxt{0, 0, 8u, 0};
     if (lane < nslots) nxt = seg[lane];
-    // A sub-chunk's elements, one float4 (or four floats) per thread; every
-    // address is clamped into the sub-chunk, so the loads are unconditional.
-    auto load_slot = [&](uint32_t slot, float4 &v, uint32_t &n) {
+    // A sub-chunk's elements kPer lane .. kPer lane + kPer - 1 into e (+0 past
+    // its end); every address is clamped into the sub-chunk, so the loads
+    // are unconditional.
+    auto load_slot = [&](uint32_t slot, float (&e)[kPer], uint32_t &n) {
         uint64_t c0, c1;
         chunk_range(g, slot / spc, c0, c1);
         const uint64_t a0 = c0 + static_cast<uint64_t>(slot % spc) * kSub;
         const uint64_t a1 = a0 + kSub < c1 ? a0 + kSub : c1;
         n = static_cast<uint32_t>(a1 - a0); // 1 .. kSub
-        const uint32_t q = threadIdx.x;
-        if (g.vec && a1 <= card4) { // a0 is a multiple of 4: whole float4s
-            v = reinterpret_cast<const float4 *>(x + a0)[4 * q < n ? q : 0u];
-        } else {
-            float t[4];
+        const uint32_t c = kPer * lane;
+        if (g.vec && a1 <= card4) { // a0 and n are multiples of 4: whole float4s
+            const float4 *x4 = reinterpret_cast<const float4 *>(x + a0);
+            float4 q[kPer / 4];
 #pragma unroll
-            for (uint32_t j = 0; j < 4; ++j) t[j] = x[a0 + (4 * q + j < n ? 4 * q + j : 0u)];
-            v = make_float4(t[0], t[1], t[2], t[3]);
+            for (uint32_t j = 0; j < kPer / 4; ++j) q[j] = x4[c + 4 * j < n ? c / 4 + j : 0u];
+#pragma unroll
+            for (uint32_t j = 0; j < kPer / 4; ++j) {
+                const bool in = c + 4 * j < n;
+                e[4 * j] = in ? q[j].x : 0.0f;
+                e[4 * j + 1] = in ? q[j].y : 0.0f;
+                e[4 * j + 2] = in ? q[j].z : 0.0f;
+                e[4 * j + 3] = in ? q[j].w : 0.0f;
+            }
+        } else {
+#pragma unroll
+            for (uint32_t j = 0; j < kPer; ++j) e[j] = x[a0 + (c + j < n ? c + j : 0u)];
+#pragma unroll
+            for (uint32_t j = 0; j < kPer; ++j) e[j] = c + j < n ? e[j] : 0.0f;
         }
     };
     for (uint32_t kb = 0; kb < nslots && !nan_final; kb += kWave) {
         const SegInfo mine = nxt;
         if (kb + kWave + lane < nslots) nxt = seg[kb + kWave + lane];
         const uint32_t nb = nslots - kb < kWave ? nslots - kb : kWave;
-        {
-            uint32_t i = 0; // next slot of the batch
-            while (i < nb) {
-                // Take the run of slots from i on that need no decision: empty
-                // ones, and usable tie-free sub-chunks in the current binade,
-                // their units below 2^24 -- one wave prefix sum finds where
-                // the run ends.
-                bool fail = false;
-                uint32_t add = 0;
-                if (lane >= i && lane < nb) {
-                    const bool empty = (mine.flags & 8u) != 0;
-                    const bool easy = empty || (s.finite && (mine.flags & 3u) == 1u && mine.u == s.u);
-                    add = easy && !empty ? mine.units : 0u;
-                    fail = !easy;
-                }
-                const uint32_t incl = wave_incl_scan(add < kSeqLimit ? add : kSeqLimit);
-                fail = fail || (lane >= i && lane < nb && static_cast<uint64_t>(s.m) + incl >= kSeqLimit);
-                const uint64_t fmask = __ballot(fail);
-                const uint32_t f = fmask ? static_cast<uint32_t>(__builtin_ctzll(fmask)) : nb;
-                if (f > i) s.m += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), f - 1));
-                if (f >= nb) break;
-                i = f + 1;
-                // slot f on its own: a usable sub-chunk with one tie adds its
-                // units plus the tie's parity correction
-                const uint32_t units = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(mine.units), f));
-                const int32_t u = __builtin_amdgcn_readlane(mine.u, f);
-                const uint32_t flags = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(mine.flags), f));
-                const uint64_t addf = static_cast<uint64_t>(units) + ((flags & 2u) ? ((s.m + (flags >> 2)) & 1u) : 0u);
-                if (s.finite && (flags & 1u) && u == s.u && static_cast<uint64_t>(s.m) + addf < kSeqLimit) {
-                    s.m += static_cast<uint32_t>(addf);
-                    continue;
-                }
-                if (!s.finite && s.special != s.special) { // NaN is final
-                    nan_final = true;
-                    break;
-                }
-                // stage the sub-chunk: one float4 (or four floats) per thread
-                const uint32_t slot = kb + f;
-                float4 v;
-                uint32_t n;
-                load_slot(slot, v, n);
-                const float *st = reinterpret_cast<const float *>(s_stage);
-                {
-                    const uint32_t q = threadIdx.x; // kSub / 4 == kBlock; +0 past n
-                    s_stage[q] = make_float4(4 * q < n ? v.x : 0.0f, 4 * q + 1 < n ? v.y : 0.0f,
-                                             4 * q + 2 < n ? v.z : 0.0f, 4 * q + 3 < n ? v.w : 0.0f);
-                }
-                __syncthreads();
-                if (wave == 0) {
-                    // The first elements of a row come with a binade crossing or
-                    // a tie every few elements (the sum is still comparable to
-                    // its addends), each of which would cost a round: lane 0
-                    // adds them one by one, the reference's own arithmetic.
-                    uint32_t head = 0;
-                    if (slot == 0 && s.finite && s.m == 0) { // the row's first sub-chunk
-                        head = n < kHead ? n : kHead;
-                        float acc = seq_value(s.m, s.u);
-                        if (lane == 0) {
-                            // whole float4s: past n the stage holds +0, which
-                            // leaves the (never -0) running sum unchanged
-#pragma unroll 8
-                            for (uint32_t j = 0; j < (head + 3) / 4; ++j) {
-                                const float4 q4 = s_stage[j];
-                                acc += q4.x;
-                                acc += q4.y;
-                                acc += q4.z;
-                                acc += q4.w;
-                            }
-                        }
-                        acc = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, acc)));
-                        if (!(acc < __builtin_inff())) {
-                            s.finite = false;
-                            s.special = acc;
-                        } else {
-                            const SeqState h = seq_state(acc);
-                            s.m = h.m;
-                            s.u = h.u;
-                        }
-                    }
-                    if (head < kSub) {
-                        float e[kPer];
-                        const uint32_t cc = kPer * lane;
-                        if (cc + kPer <= n) {
-#pragma unroll
-                            for (uint32_t j = 0; j < kPer / 4; ++j) {
-                                const float4 v = s_stage[cc / 4 + j];
-                                e[4 * j] = v.x;
-                                e[4 * j + 1] = v.y;
-                                e[4 * j + 2] = v.z;
-                                e[4 * j + 3] = v.w;
-                            }
-                        } else {
-#pragma unroll
-                            for (uint32_t j = 0; j < kPer; ++j) e[j] = cc + j < n ? st[cc + j] : 0.0f;
-                        }
-                        sum_tile<kPer>(e, s, head); // the head's elements are committed
-                    }
-                }
-                // wave 0's state to every wave
-                if (threadIdx.x == 0) {
-                    s_state[0] = s.m;
-                    s_state[1] = static_cast<uint32_t>(s.u);
-                    s_state[2] = s.finite;
-                    s_state[3] = f32_to_bits(s.special);
-                }
-                __syncthreads();
-                s.m = s_state[0];
-                s.u = static_cast<int32_t>(s_state[1]);
-                s.finite = s_state[2] != 0;
-                s.special = bits_to_f32(s_state[3]);
-                __syncthreads(); // the stage and s_state are rewritten by the next walk
+        uint32_t i = 0; // next slot of the batch
+        while (i < nb) {
+            // Take the run of slots from i on that need no decision: empty
+            // ones, and usable tie-free sub-chunks in the current binade,
+            // their units below 2^24 -- one wave prefix sum finds where the
+            // run ends.
+            bool fail = false;
+            uint32_t add = 0;
+            if (lane >= i && lane < nb) {
+                const bool empty = (mine.flags & 8u) != 0;
+                const bool easy = empty || (s.finite && (mine.flags & 3u) == 1u && mine.u == s.u);
+                add = easy && !empty ? mine.units : 0u;
+                fail = !easy;
             }
+            const uint32_t incl = wave_incl_scan(add < kSeqLimit ? add : kSeqLimit);
+            fail = fail || (lane >= i && lane < nb && static_cast<uint64_t>(s.m) + incl >= kSeqLimit);
+            const uint64_t fmask = __ballot(fail);
+            const uint32_t f = fmask ? static_cast<uint32_t>(__builtin_ctzll(fmask)) : nb;
+            if (f > i) s.m += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), f - 1));
+            if (f >= nb) break;
+            i = f + 1;
+            // slot f on its own: a usable sub-chunk with one tie adds its
+            // units plus the tie's parity correction
+            const uint32_t units = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(mine.units), f));
+            const int32_t u = __builtin_amdgcn_readlane(mine.u, f);
+            const uint32_t flags = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(mine.flags), f));
+            const uint64_t addf = static_cast<uint64_t>(units) + ((flags & 2u) ? ((s.m + (flags >> 2)) & 1u) : 0u);
+            if (s.finite && (flags & 1u) && u == s.u && static_cast<uint64_t>(s.m) + addf < kSeqLimit) {
+                s.m += static_cast<uint32_t>(addf);
+                continue;
+            }
+            if (!s.finite && s.special != s.special) { // NaN is final
+                nan_final = true;
+                break;
+            }
+            const uint32_t slot = kb + f;
+            float e[kPer];
+            uint32_t n;
+            load_slot(slot, e, n);
+            // The first elements of a row come with a binade crossing or a
+            // tie every few elements (the sum is still comparable to its
+            // addends), each of which would cost a round: lane 0 adds them
+            // one by one, the reference's own arithmetic.
+            uint32_t head = 0;
+            if (slot == 0 && s.finite && s.m == 0) { // the row's first sub-chunk
+                head = n < kHead ? n : kHead;
+                if (kPer * lane < kHead) {
+#pragma unroll
+                    for (uint32_t j = 0; j < kPer / 4; ++j)
+                        s_head[kPer / 4 * lane + j] =
+                            make_float4(e[4 * j], e[4 * j + 1], e[4 * j + 2], e[4 * j + 3]);
+                }
+                __syncthreads(); // one wave: orders its LDS writes before lane 0's reads
+                float acc = seq_value(s.m, s.u);
+                if (lane == 0) {
+                    // whole float4s: past n the elements are +0, which leaves
+                    // the (never -0) running sum unchanged
+#pragma unroll 8
+                    for (uint32_t j = 0; j < (head + 3) / 4; ++j) {
+                        const float4 q4 = s_head[j];
+                        acc += q4.x;
+                        acc += q4.y;
+                        acc += q4.z;
+                        acc += q4.w;
+                    }
+                }
+                acc = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, acc)));
+                if (!(acc < __builtin_inff())) {
+                    s.finite = false;
+                    s.special = acc;
+                } else {
+                    const SeqState h = seq_state(acc);
+                    s.m = h.m;
+                    s.u = h.u;
+                }
+            }
+            if (head < kSub) sum_tile<kPer>(e, s, head); // the head's elements are committed
         }
     }
-    if (threadIdx.x == 0) w.sel[row].total = s.finite ? seq_value(s.m, s.u) : s.special;
+    if (lane == 0) w.sel[row].total = s.finite ? seq_value(s.m, s.u) : s.special;
 }
 
 // ---- stage 4: p = e / S in place, first radix digit -------------------------
@@ -1390,7 +1367,7 @@ hipError_t launch_sampler(const SamplerArgs &a, hipStream_t s)
     k_smp_max<<<grid, kBlock, 0, s>>>(g, a.logits, w);
     k_smp_exp<<<grid, kBlock, 0, s>>>(g, a.logits, w);
     k_smp_seg<<<grid, kBlock, 0, s>>>(g, a.logits, w);
-    k_smp_sum<<<a.rows, kBlock, 0, s>>>(g, a.logits, w);
+    k_smp_sum<<<a.rows, kSumThreads, 0, s>>>(g, a.logits, w);
     k_smp_div<<<grid, kBlock, 0, s>>>(g, a.logits, w);
     k_smp_resolve<<<a.rows, kResolveThreads, 0, s>>>(g, a.logits, w);
     k_smp_collect<<<grid, kBlock, 0, s>>>(g, a.logits, w);
