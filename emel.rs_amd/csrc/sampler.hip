@@ -498,26 +498,32 @@ __device__ __forceinline__ void sum_tile(const float (&e)[PER], SumState &s, uin
             s.m += total;
             return; // tile committed
         }
-        // this lane's first event element and the units just before it
-        uint32_t run = s.m + (incl - x_in);
-        uint32_t mine = kNone;
+        // this lane's first event element and the units just before it,
+        // branch-free: flags past the first event are never used, and the
+        // committed elements (r = 0, no tie) cannot be events in the lane
+        // that holds the first one (its running units are still below 2^24)
+        const uint32_t base = s.m + (incl - x_in);
+        uint32_t run = base, evmask = 0;
+#pragma unroll
+        for (uint32_t j = 0; j < PER; ++j) {
+            const bool ev = ((ties >> j) & 1u) != 0u || run + r[j] >= kSeqLimit;
+            evmask |= static_cast<uint32_t>(ev) << j;
+            run += r[j];
+        }
+        const uint32_t first = evmask ? static_cast<uint32_t>(__builtin_ctz(evmask)) : PER;
+        uint32_t run_first = base;
         float ek = 0.0f;
 #pragma unroll
         for (uint32_t j = 0; j < PER; ++j) {
-            if (mine == kNone && PER * lane + j >= start) {
-                if (((ties >> j) & 1u) || run + r[j] >= kSeqLimit) {
-                    mine = PER * lane + j;
-                    ek = e[j];
-                } else {
-                    run += r[j];
-                }
-            }
+            run_first += j < first ? r[j] : 0u;
+            ek = j == first ? e[j] : ek;
         }
-        const uint64_t emask = __ballot(mine != kNone);
+        const uint64_t emask = __ballot(evmask != 0u);
         if (emask == 0) return; // unreachable: a tie or a crossing has a first element
         const int fl = __builtin_ctzll(emask);
-        const uint32_t k = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(mine), fl));
-        const uint32_t run_k = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(run), fl));
+        const uint32_t k = PER * static_cast<uint32_t>(fl) +
+                           static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(first), fl));
+        const uint32_t run_k = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(run_first), fl));
         const float e_k = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ek), fl));
         const float sn = seq_value(run_k, s.u) + e_k; // the event element: one f32 addition
         if (!(sn < __builtin_inff())) { // NaN or +inf
