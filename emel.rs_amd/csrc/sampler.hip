@@ -159,11 +159,13 @@ static_assert(kPmPowers.v[0] == 16807u && kPmPowers.v[1] == 282475249u && kPmPow
               "Park-Miller powers: 16807, 16807^2, 16807^3 mod 2^31 - 1");
 
 // Visits the columns [c0, c1) of one row: float4 steps when the row is
-// 16-byte aligned (U loads in flight per thread before any is used), then
-// a scalar tail.  The order of the visits is unspecified: callers only
-// reduce order-independently or write elementwise.
-// f(float &v, uint64_t col) may modify v; WRITE stores it back.
-template <bool WRITE, int U = 4, class F>
+// 16-byte aligned, then a scalar tail.  A step issues U loads per thread
+// before any is used; loads past the range re-read its last float4 (in
+// bounds, from cache) and are not visited, so a chunk of up to U float4 per
+// thread costs one memory round trip.  The order of the visits is
+// unspecified: callers only reduce order-independently or write
+// elementwise.  f(float &v, uint64_t col) may modify v; WRITE stores it back.
+template <bool WRITE, int U = 8, class F>
 __device__ __forceinline__ void visit(const SmpGeo &g, float *row, uint64_t c0, uint64_t c1, F f)
 {
     uint64_t c = c0;
@@ -171,27 +173,27 @@ __device__ __forceinline__ void visit(const SmpGeo &g, float *row, uint64_t c0, 
         float4 *r4 = reinterpret_cast<float4 *>(row);
         const uint64_t v1 = c1 / 4;
         const uint64_t bs = blockDim.x;
-        uint64_t v = c0 / 4 + threadIdx.x;
         auto apply = [&](float4 &q, uint64_t vi) {
             f(q.x, 4 * vi);
             f(q.y, 4 * vi + 1);
             f(q.z, 4 * vi + 2);
             f(q.w, 4 * vi + 3);
         };
-        for (; v + (U - 1) * bs < v1; v += U * bs) {
+        for (uint64_t v = c0 / 4 + threadIdx.x; v < v1; v += U * bs) {
             float4 q[U];
 #pragma unroll
-            for (int j = 0; j < U; ++j) q[j] = r4[v + j * bs];
+            for (int j = 0; j < U; ++j) {
+                const uint64_t i = v + j * bs;
+                q[j] = r4[i < v1 ? i : v1 - 1];
+            }
 #pragma unroll
             for (int j = 0; j < U; ++j) {
-                apply(q[j], v + j * bs);
-                if constexpr (WRITE) r4[v + j * bs] = q[j];
+                const uint64_t i = v + j * bs;
+                if (i < v1) {
+                    apply(q[j], i);
+                    if constexpr (WRITE) r4[i] = q[j];
+                }
             }
-        }
-        for (; v < v1; v += bs) {
-            float4 q = r4[v];
-            apply(q, v);
-            if constexpr (WRITE) r4[v] = q;
         }
         c = v1 * 4 > c0 ? v1 * 4 : c0;
     }
@@ -286,7 +288,9 @@ __global__ __launch_bounds__(kBlock) void k_smp_exp(SmpGeo g, float *logits, Smp
     const float scale = g.scale;
     const ExpfConsts ec = expf_consts_in_vgprs();
     double acc = 0.0;
-    visit<true>(g, x, c0, c1, [&](float &v, uint64_t) {
+    // 4 float4 per step: the expf replica's registers leave room for no more
+    // at full occupancy
+    visit<true, 4>(g, x, c0, c1, [&](float &v, uint64_t) {
         const float s = v * scale;
         v = emel_expf(s - m, kExp2Table, ec);
         acc += static_cast<double>(v);
@@ -1304,7 +1308,9 @@ void plan_chunks(uint32_t rows, uint64_t card, uint64_t &chunk_cols, uint32_t &c
     const uint64_t want = (kTargetBlocks + rows - 1) / rows;
     uint64_t c = (card + want - 1) / want;
     if (c < kMinChunkCols) c = kMinChunkCols;
-    c = (c + 3) & ~uint64_t{3};
+    // whole float4 steps of a workgroup: every thread of a chunk visits the
+    // same number of float4 (the last chunk of a row excepted)
+    c = (c + kMinChunkCols - 1) / kMinChunkCols * kMinChunkCols;
     chunk_cols = c;
     chunks = static_cast<uint32_t>((card + c - 1) / c);
 }
