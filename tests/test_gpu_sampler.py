@@ -122,6 +122,17 @@ def test_sizes_and_temperatures(gpu, card, top_k, temperature, sigma):
     check(gpu, x, temperature, top_k, [int(s) for s in g.integers(1, M, rows)])
 
 
+def test_many_rows_batch_the_ranking(gpu):
+    """More rows than one ranking launch takes (the start states travel in
+    the launch arguments, 512 rows a launch), for the in-LDS ranking and for
+    the tiled merge (top_k > 8192)."""
+    g = np.random.Generator(np.random.PCG64(80))
+    x = g.standard_normal((1100, 3000)).astype(np.float32)
+    check(gpu, x, 0.9, 25, [int(s) for s in g.integers(1, M, 1100)])
+    x = g.standard_normal((600, 10000)).astype(np.float32)
+    check(gpu, x, 1.0, 9000, [int(s) for s in g.integers(1, M, 600)])
+
+
 def test_unaligned_and_padded_rows(gpu):
     g = np.random.Generator(np.random.PCG64(77))
     x = g.standard_normal((4, 12345)).astype(np.float32)
