@@ -65,8 +65,12 @@ __host__ __device__ __forceinline__ float seq_value(uint32_t m, int32_t u)
 __host__ __device__ __forceinline__ uint32_t seq_units(float e, int32_t u, bool &tie)
 {
     float t = __builtin_ldexpf(e, -u);
-    t = t < 16777216.0f ? t : 16777216.0f; // also NaN -> 2^24
+    t = __builtin_fminf(t, 16777216.0f); // IEEE minNum: also NaN -> 2^24
+#if defined(__HIP_DEVICE_COMPILE__)
+    tie = __builtin_amdgcn_fractf(t) == 0.5f; // t - floor(t), exact for 0 <= t <= 2^24
+#else
     tie = (t - __builtin_floorf(t)) == 0.5f;
+#endif
     return static_cast<uint32_t>(__builtin_rintf(t));
 }
 
