@@ -18,12 +18,12 @@
 // finish a stage early skip the later ones):
 //   k_smp_max     (row, chunk) workgroups: chunk maxima of v.
 //   k_smp_exp     (row, chunk): e written in place, and the chunk's f64 sum.
-//   k_smp_seg     (row, chunk): the chunk's exact contribution in units of
-//                 the binade its f64 prefix predicts.
-//   k_smp_sum     one workgroup per row: the exact sequential sum
-//                 (seqsum.hpp), taking a chunk's predicted contribution when
-//                 the exact state confirms it, walking the other chunks from
-//                 LDS.
+//   k_smp_seg     (row, chunk): each 1024-element sub-chunk's exact
+//                 contribution in units of the binade its f64 prefix predicts.
+//   k_smp_sum     one wave per row: the exact sequential sum (seqsum.hpp),
+//                 taking a sub-chunk's predicted contribution when the exact
+//                 state confirms it, walking the other sub-chunks from
+//                 registers.
 //   k_smp_div     (row, chunk): p written in place, plus the histogram of the
 //                 top 11 bits of p's total-order key.
 //   k_smp_resolve one workgroup per row: radix selection of the top_k-th
@@ -36,8 +36,9 @@
 //                 every key >= prefix, or every key > T plus the lowest-index
 //                 ties at T up to top_k.
 //   k_smp_rank    one workgroup per row: sort of the candidates in LDS
-//                 (bitonic, key descending then index ascending), the ranked
-//                 outputs, then the race selection.
+//                 (key descending then index ascending: register runs merged
+//                 by merge path), the ranked outputs, then the race
+//                 selection.
 // Lists longer than kCap (top_k > kCap) are sorted as kCap tiles
 // (k_smp_tile_sort), merged pairwise (k_smp_merge), and finished by
 // k_smp_finish.
