@@ -137,6 +137,28 @@ def test_soft_max_ext_causal(gpu, nkv, nq, nh):
     assert np.abs(rows - 1.0).max() < 1e-5
 
 
+@pytest.mark.parametrize("nkv,nq,nh,n3,m2,m3", [
+    (20000, 3, 2, 1, 1, 1),    # rows wider than the registers hold: the streamed passes
+    (40000, 2, 2, 1, 2, 1),    # streamed, one mask per head
+    (4096, 8, 4, 1, 4, 1),     # config 4's width, one mask per head
+    (1024, 4, 6, 2, 3, 2),     # mask broadcast over dims 2 and 3 (m2 | ne2, m3 | ne3)
+])
+def test_soft_max_ext_wide_rows_and_broadcast_masks(gpu, nkv, nq, nh, n3, m2, m3):
+    x = normal(191 + nkv + m2, nkv * nq * nh * n3, 2.0)
+    g = np.random.Generator(np.random.PCG64(192 + nkv))
+    mask = (g.standard_normal(nkv * nq * m2 * m3) * 2).astype(np.float16)
+    mask[g.random(mask.size) < 0.3] = np.float16(-np.inf)
+    mask.reshape(-1, nkv)[:, 0] = 0  # keep every row alive
+    a = Pair(x, [nkv, nq, nh, n3]).to(gpu)
+    m = Pair(mask.view(np.uint16), [nkv, nq, m2, m3], dtype=orc.F16).to(gpu)
+    o = Pair(np.zeros_like(x), a.ne).to(gpu)
+    assert eh.Kernel().process_event(eh.OpSoftMaxExt(a.pview(), m.pview(), 0.5, o.pview(mut=True))) == eh.Status.OK, \
+        eh.last_error()
+    want = np.zeros_like(x)
+    assert orc.soft_max_ext(a.oview(), m.oview(), 0.5, orc.view(want, a.ne)) == orc.OK
+    assert_close_rel(o.result(), want, RTOL, "soft_max_ext wide / broadcast mask")
+
+
 def test_soft_max_ext_reduces_to_soft_max(gpu):
     # zero mask and scale 1 must give OpSoftMax's bits exactly
     nkv, nq, nh = 1024, 16, 4
