@@ -18,7 +18,7 @@
 // finish a stage early skip the later ones):
 //   k_smp_max     (row, chunk) workgroups: chunk maxima of v.
 //   k_smp_exp     (row, chunk): e written in place, and the chunk's f64 sum.
-//   k_smp_seg     (row, chunk): each 1024-element sub-chunk's exact
+//   k_smp_seg     (row, chunk): each 512-element sub-chunk's exact
 //                 contribution in units of the binade its f64 prefix predicts.
 //   k_smp_sum     one wave per row: the exact sequential sum (seqsum.hpp),
 //                 taking a sub-chunk's predicted contribution when the exact
@@ -91,7 +91,8 @@ struct SmpGeo {
 // A sub-chunk's contribution to the row's exact sum, computed ahead of the
 // walk at a predicted binade (k_smp_seg): units (+1 when `tie` and the
 // running units plus `par` are odd) of 2^u, when ok.
-constexpr uint32_t kSub = 1024;  // elements per sub-chunk (one walk round)
+constexpr uint32_t kSub = 512;   // elements per sub-chunk (one walk round)
+constexpr uint32_t kPer = kSub / kWave; // elements per lane of a sub-chunk
 constexpr uint32_t kMaxSub = 64; // sub-chunks a chunk predicts; later ones are walked
 struct SegInfo {
     uint32_t units; // saturates at 2^25: the walk rejects anything >= 2^24
@@ -323,7 +324,7 @@ __device__ __forceinline__ uint32_t subs_per_chunk(const SmpGeo &g)
 }
 
 // One 256-thread workgroup per (row, chunk); wave w predicts sub-chunks
-// w, w + 4, ... from its 16 elements per lane.  A sub-chunk with one tie is
+// w, w + 4, ... from its kPer elements per lane.  A sub-chunk with one tie is
 // still usable: the tie rounds its sum to an even number of units, so it
 // adds q or q + 1 units depending on the parity of the units before it,
 // recorded as `par`.
@@ -346,12 +347,12 @@ __global__ __launch_bounds__(kBlock) void k_smp_seg(SmpGeo g, float *logits, Smp
     const uint32_t npred = nsub < kMaxSub ? nsub : kMaxSub;
     SegInfo *out = w.seg + (static_cast<uint64_t>(row) * g.chunks + chunk) * spc;
     const float *x = logits + static_cast<int64_t>(row) * g.ld;
-    auto load16 = [&](uint32_t k, float (&e)[16]) {
-        const uint64_t first = c0 + static_cast<uint64_t>(k) * kSub + 16 * lane;
-        if (g.vec && first + 16 <= c1) {
+    auto load_sub = [&](uint32_t k, float (&e)[kPer]) {
+        const uint64_t first = c0 + static_cast<uint64_t>(k) * kSub + kPer * lane;
+        if (g.vec && first + kPer <= c1) {
             const float4 *p4 = reinterpret_cast<const float4 *>(x + first);
 #pragma unroll
-            for (uint32_t j = 0; j < 4; ++j) {
+            for (uint32_t j = 0; j < kPer / 4; ++j) {
                 const float4 q = p4[j];
                 e[4 * j] = q.x;
                 e[4 * j + 1] = q.y;
@@ -360,16 +361,16 @@ __global__ __launch_bounds__(kBlock) void k_smp_seg(SmpGeo g, float *logits, Smp
             }
         } else {
 #pragma unroll
-            for (uint32_t j = 0; j < 16; ++j) e[j] = first + j < c1 ? x[first + j] : 0.0f;
+            for (uint32_t j = 0; j < kPer; ++j) e[j] = first + j < c1 ? x[first + j] : 0.0f;
         }
     };
     // pass A: f64 sum of every sub-chunk
     for (uint32_t k = wave; k < npred; k += kBlock / kWave) {
-        float e[16];
-        load16(k, e);
+        float e[kPer];
+        load_sub(k, e);
         double acc = 0.0;
 #pragma unroll
-        for (uint32_t j = 0; j < 16; ++j) acc += static_cast<double>(e[j]);
+        for (uint32_t j = 0; j < kPer; ++j) acc += static_cast<double>(e[j]);
         acc = wave_sum(acc);
         if (lane == 0) s_sub[k] = acc;
     }
@@ -393,11 +394,11 @@ __global__ __launch_bounds__(kBlock) void k_smp_seg(SmpGeo g, float *logits, Smp
             // normal f32 range, both bounds in one binade [2^(elo-1), 2^elo)
             if (lo >= 0x1p-126 && hi < 0x1p127 && lo <= hi && elo == ehi) { // uniform
                 const int32_t u = elo - 1 - 23;
-                float e[16];
-                load16(k, e);
+                float e[kPer];
+                load_sub(k, e);
                 uint32_t lsum = 0, ties = 0, tq = 0, tbefore = 0;
 #pragma unroll
-                for (uint32_t j = 0; j < 16; ++j) {
+                for (uint32_t j = 0; j < kPer; ++j) {
                     bool tie;
                     const uint32_t r = seq_units(e[j], u, tie);
                     // a tie counts its lower neighbour q here (r is q or q + 1)
@@ -441,7 +442,7 @@ __global__ __launch_bounds__(kBlock) void k_smp_seg(SmpGeo g, float *logits, Smp
 // predicted contribution (k_smp_seg) holds on the exact state -- the same
 // binade, and the units stay below 2^24, so no element inside it can cross
 // (units never decrease) -- is added in one step.  Any other sub-chunk is
-// walked as one tile of 64 lanes x 16 elements: a round computes the
+// walked as one tile of 64 lanes x kPer elements: a round computes the
 // tile's units at the current binade and their wave prefix sum, and either
 // commits the rest of the tile (no event) or finds the first event
 // element, adds it with one f32 addition and starts the next round after
@@ -548,7 +549,6 @@ __device__ __forceinline__ void sum_tile(const float (&e)[PER], SumState &s, uin
     }
 }
 
-constexpr uint32_t kPer = kSub / kWave; // 16 elements per lane and round of the walk
 constexpr uint32_t kHead = 512;          // a row's first elements, added one by one
 
 // One wave per row.  The sub-chunks' predictions are read a batch at a
@@ -557,7 +557,7 @@ constexpr uint32_t kHead = 512;          // a row's first elements, added one by
 // (its one tie resolved by the current parity) stay below 2^24, so no
 // element inside it can cross (units never decrease) -- is added in one
 // step.  Any other sub-chunk is loaded straight into the walk's registers
-// (lane l holds its elements 16 l .. 16 l + 15, four 128-bit loads in
+// (lane l holds its elements kPer l .. kPer l + kPer - 1, 128-bit loads in
 // flight) and walked: one round, plus one per event.
 constexpr uint32_t kSumThreads = kWave;
 

@@ -246,15 +246,16 @@ extern "C" float seqsum_chunked_f(const float *e, uint64_t n, uint32_t lanes, ui
 }
 
 // Random cases of each family and length up to max_n, through the walk
-// alone (the kernel's 64 lanes and a small 4) and through sub-chunk
-// predictions (config 5's 4748-element chunks of 1024-element sub-chunks,
-// and small shapes).  Counts results whose bits differ from the sequential
+// alone (tiles of 64 x 16 and 4 x 16 elements) and through sub-chunk
+// predictions (config 5's 5120-element chunks of 512-element sub-chunks,
+// walked in tiles of 512 as the kernel does, 4748-element chunks of
+// 1024-element sub-chunks, and small shapes).  Counts results whose bits differ from the sequential
 // loop.
 extern "C" uint64_t check_seqsum(uint64_t seed, int cases, uint64_t max_n)
 {
     uint64_t z = seed, bad = 0;
-    const uint64_t shapes[6][3] = {{64, 0, 0}, {4, 0, 0}, {64, 4748, 1024}, {4, 100, 64}, {64, 1024, 1024},
-                                   {4, 300, 300}};
+    const uint64_t shapes[7][3] = {{64, 0, 0}, {4, 0, 0}, {64, 4748, 1024}, {4, 100, 64}, {64, 1024, 1024},
+                                   {4, 300, 300}, {32, 5120, 512}};
     for (int c = 0; c < cases; ++c) {
         const int family = c % 5;
         const uint64_t n = 1 + splitmix(z) % max_n;

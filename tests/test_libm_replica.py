@@ -91,7 +91,8 @@ def test_exact_sequential_sum_rounds(chk):
     sequential f32 loop.  Families: softmax-like values, dyadic values full
     of exact ties, zeros and subnormals, every magnitude, planted NaN / +inf;
     the walk alone (64 lanes, as the kernel, and 4) and with predictions
-    (config 5's 4748-element chunks, 100- and 1024-element chunks).  Ignoring ties, or
+    (config 5's 5120-element chunks of 512-element sub-chunks as the kernel
+    walks them, 4748-element chunks, 100- and 1024-element chunks).  Ignoring ties, or
     letting a binade run to 2^25 units, makes this check fail."""
     chk.check_seqsum.restype = ctypes.c_uint64
     chk.check_seqsum.argtypes = [ctypes.c_uint64, ctypes.c_int, ctypes.c_uint64]
@@ -111,8 +112,12 @@ def test_exact_sum_predictions_are_taken(chk):
     g = np.random.Generator(np.random.PCG64(5))
     v = (g.standard_normal(151936) / 0.8).astype(np.float32)
     e = np.exp((v - v.max()).astype(np.float64)).astype(np.float32)
-    jumped = ctypes.c_uint64(0)
-    got = chk.seqsum_chunked_f(e.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), e.size, 64, 4748, 1024,
-                               ctypes.byref(jumped))
-    assert np.float32(got) == np.cumsum(e, dtype=np.float32)[-1]
-    assert jumped.value >= 140, jumped.value  # of 160 sub-chunks
+    want = np.cumsum(e, dtype=np.float32)[-1]
+    # the kernel's shape: 5120-element chunks of 512-element sub-chunks
+    # (297 of them), and 4748-element chunks of 1024-element ones (160)
+    for lanes, chunk, sub, least in ((32, 5120, 512, 270), (64, 4748, 1024, 140)):
+        jumped = ctypes.c_uint64(0)
+        got = chk.seqsum_chunked_f(e.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), e.size, lanes, chunk, sub,
+                                   ctypes.byref(jumped))
+        assert np.float32(got) == want
+        assert jumped.value >= least, (sub, jumped.value)
