@@ -111,6 +111,16 @@ def test_config5_vocabulary_batch(gpu):
     check(gpu, x, 0.8, 40, states)
 
 
+@pytest.mark.parametrize("top_k,temperature", [(8192, 1.0), (1, 0.8), (4096, 0.5)])
+def test_config5_vocabulary_large_and_single_top_k(gpu, top_k, temperature):
+    """Full 151,936-token rows at the bench's second case (top_k 8192: the
+    threshold needs the later radix digits, found by row scans) and at the
+    extremes of top_k."""
+    g = np.random.Generator(np.random.PCG64(502 + top_k))
+    x = g.standard_normal((6, 151936), dtype=np.float64).astype(np.float32)
+    check(gpu, x, temperature, top_k, [int(s) for s in g.integers(1, M, 6)])
+
+
 @pytest.mark.parametrize("card,top_k,temperature,sigma", [
     (1, 1, 1.0, 1.0), (5, 5, 0.7, 1.0), (4097, 1, 1.0, 1.0), (4097, 4097, 1.0, 2.0), (100003, 64, 0.5, 1.0),
     (30000, 8192, 1.0, 1.0), (30000, 8193, 1.0, 1.0), (50000, 20000, 1.3, 1.0), (20000, 50, 0.02, 1.0),
