@@ -12,6 +12,7 @@
 #include <cmath>
 #include <cstring>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <string>
 #include <utility>
@@ -244,65 +245,139 @@ emel_status ensure_device()
     return EMEL_OK;
 }
 
-// Per-(device, stream) scratch for the split-row reductions' partials.
-// Calls on one stream run in order, so they can share one buffer; different
-// streams get different buffers.
-struct Workspace {
+// ---- per-(device, stream) scratch ------------------------------------------
+//
+// Calls on one stream run in order on the device, so they share one set of
+// scratch buffers per (device, stream).  A call holds the stream's lock from
+// its first use of that scratch until its last launch is enqueued, so calls
+// from several host threads on one stream never interleave their launch
+// sequences or their index checks.
+//   - `work`: general scratch (reduction partials, sampler state, uploaded
+//     indices); each call fully writes what it later reads.
+//   - `counters`: the reductions' per-row arrival counters.  They are zeroed
+//     when the buffer is allocated and every launch leaves them zero, so the
+//     buffer holds nothing else.
+//   - `staging`: pinned host memory for index copies back to the host.
+// A buffer that must grow is replaced, and the old one is kept until
+// emel_release_workspaces or emel_stream_destroy: a graph captured earlier
+// may still reference it.  Growth allocates and zeroes memory, which a stream
+// under capture must not do, so a call that needs it during a capture is
+// refused with EMEL_ERR_STREAM_CAPTURE before anything is enqueued.
+struct Buffer {
     void *ptr = nullptr;
     uint64_t bytes = 0;
 };
-std::map<std::pair<int, hipStream_t>, Workspace> g_workspaces;
 
-emel_status workspace_for(hipStream_t stream, uint64_t bytes, void **out)
+struct StreamState {
+    std::mutex lock;
+    Buffer work, counters, staging;
+    std::vector<void *> retired_dev, retired_host;
+};
+
+std::map<std::pair<int, hipStream_t>, std::unique_ptr<StreamState>> g_streams; // guarded by g_mutex
+
+emel_status not_capturing(hipStream_t stream, const char *what)
 {
-    *out = nullptr;
-    if (bytes == 0) return EMEL_OK;
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
-    std::lock_guard<std::mutex> lock(g_mutex);
-    Workspace &w = g_workspaces[{dev, stream}];
-    if (w.bytes < bytes) {
-        if (w.ptr) {
-            e = hipStreamSynchronize(stream); // the old buffer may still be in use
-            if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
-            (void)hipFree(w.ptr);
-            w.ptr = nullptr;
-            w.bytes = 0;
-        }
-        const uint64_t size = bytes < (uint64_t{1} << 20) ? (uint64_t{1} << 20) : bytes;
-        e = hipMalloc(&w.ptr, size);
-        if (e != hipSuccess) return hip_fail(e, "hipMalloc(workspace)");
-        w.bytes = size;
-    }
-    *out = w.ptr;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    const hipError_t e = hipStreamIsCapturing(stream, &cs);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
+    if (cs != hipStreamCaptureStatusNone)
+        return fail(EMEL_ERR_STREAM_CAPTURE, std::string(what) + " cannot run while the stream is being captured");
     return EMEL_OK;
 }
 
-// Per-(device, stream) pinned host staging for index copies to the host.
-std::map<std::pair<int, hipStream_t>, Workspace> g_staging;
-
-emel_status staging_for(hipStream_t stream, uint64_t bytes, void **out)
-{
-    *out = nullptr;
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
-    std::lock_guard<std::mutex> lock(g_mutex);
-    Workspace &w = g_staging[{dev, stream}];
-    if (w.bytes < bytes) {
-        if (w.ptr) {
-            (void)hipHostFree(w.ptr); // callers wait for their copy before returning
-            w.ptr = nullptr;
-            w.bytes = 0;
+class StreamLease {
+public:
+    emel_status acquire(hipStream_t stream)
+    {
+        int dev = 0;
+        const hipError_t e = hipGetDevice(&dev);
+        if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+        {
+            std::lock_guard<std::mutex> g(g_mutex);
+            auto &slot = g_streams[{dev, stream}];
+            if (!slot) slot.reset(new StreamState);
+            st_ = slot.get();
         }
-        const uint64_t size = bytes < (uint64_t{1} << 16) ? (uint64_t{1} << 16) : bytes;
-        e = hipHostMalloc(&w.ptr, size, hipHostMallocDefault);
-        if (e != hipSuccess) return hip_fail(e, "hipHostMalloc(staging)");
-        w.bytes = size;
+        hold_ = std::unique_lock<std::mutex>(st_->lock);
+        stream_ = stream;
+        return EMEL_OK;
     }
-    *out = w.ptr;
-    return EMEL_OK;
+
+    emel_status work(uint64_t bytes, void **out) { return device(st_->work, bytes, false, out); }
+    emel_status counters(uint64_t bytes, void **out) { return device(st_->counters, bytes, true, out); }
+
+    emel_status staging(uint64_t bytes, void **out)
+    {
+        *out = nullptr;
+        Buffer &b = st_->staging;
+        if (b.bytes < bytes) {
+            emel_status s = not_capturing(stream_, "growing the pinned index staging buffer");
+            if (s != EMEL_OK) return s;
+            void *p = nullptr;
+            const uint64_t size = grown(b.bytes, bytes, uint64_t{1} << 16);
+            const hipError_t e = hipHostMalloc(&p, size, hipHostMallocDefault);
+            if (e != hipSuccess) return hip_fail(e, "hipHostMalloc(staging)");
+            if (b.ptr) st_->retired_host.push_back(b.ptr);
+            b.ptr = p;
+            b.bytes = size;
+        }
+        *out = b.ptr;
+        return EMEL_OK;
+    }
+
+private:
+    static uint64_t grown(uint64_t have, uint64_t need, uint64_t floor)
+    {
+        uint64_t size = have * 2 > need ? have * 2 : need;
+        return size < floor ? floor : size;
+    }
+
+    emel_status device(Buffer &b, uint64_t bytes, bool zeroed, void **out)
+    {
+        *out = nullptr;
+        if (bytes == 0) return EMEL_OK;
+        if (b.bytes < bytes) {
+            emel_status s = not_capturing(stream_, "growing the stream's device scratch");
+            if (s != EMEL_OK) return s;
+            void *p = nullptr;
+            const uint64_t size = grown(b.bytes, bytes, uint64_t{1} << 20);
+            hipError_t e = hipMalloc(&p, size);
+            if (e != hipSuccess) return hip_fail(e, "hipMalloc(scratch)");
+            if (zeroed) {
+                e = hipMemsetAsync(p, 0, size, stream_); // ordered before this call's launches
+                if (e != hipSuccess) {
+                    (void)hipFree(p);
+                    return hip_fail(e, "hipMemsetAsync(scratch)");
+                }
+            }
+            if (b.ptr) st_->retired_dev.push_back(b.ptr);
+            b.ptr = p;
+            b.bytes = size;
+        }
+        *out = b.ptr;
+        return EMEL_OK;
+    }
+
+    StreamState *st_ = nullptr;
+    std::unique_lock<std::mutex> hold_;
+    hipStream_t stream_ = nullptr;
+};
+
+// Frees every buffer of `st` (the caller has synchronised the device or the
+// stream).
+void free_state(StreamState &st)
+{
+    for (Buffer *b : {&st.work, &st.counters}) {
+        if (b->ptr) (void)hipFree(b->ptr);
+        *b = Buffer{};
+    }
+    if (st.staging.ptr) (void)hipHostFree(st.staging.ptr);
+    st.staging = Buffer{};
+    for (void *p : st.retired_dev) (void)hipFree(p);
+    for (void *p : st.retired_host) (void)hipHostFree(p);
+    st.retired_dev.clear();
+    st.retired_host.clear();
 }
 
 emel_status launched(hipError_t e)
@@ -436,9 +511,14 @@ emel_status reduce(emel::RedOp op, const emel_tensor_view &src, const emel_tenso
     args.dst_view = operand(dst, 4);
     if (dst.dtype == EMEL_DTYPE_I32)
         for (int d = 0; d < 4; ++d) args.dst_view.st[d] = static_cast<int64_t>(dst.nb[d] / 4);
-    const uint64_t bytes = emel::reduce_workspace_bytes(args);
-    s = workspace_for(as_stream(stream), bytes, &args.workspace);
-    if (s != EMEL_OK) return s;
+    args.scratch = emel::reduce_scratch_bytes(args);
+    StreamLease lease;
+    if (args.scratch.partials) {
+        s = lease.acquire(as_stream(stream));
+        if (s == EMEL_OK) s = lease.work(args.scratch.partials, &args.partials);
+        if (s == EMEL_OK) s = lease.counters(args.scratch.counters, &args.counters);
+        if (s != EMEL_OK) return s;
+    }
     const hipError_t e = emel::launch_reduce(args, as_stream(stream));
     if (e == hipErrorInvalidValue) return fail(EMEL_ERR_INTERNAL, "reduction size outside the supported range");
     return launched(e);
@@ -508,6 +588,7 @@ const char *emel_status_string(emel_status s)
     case EMEL_ERR_INDEX_OUT_OF_BOUNDS: return "index out of bounds";
     case EMEL_ERR_UNSUPPORTED_SOURCE_STRIDE: return "unsupported source stride";
     case EMEL_ERR_INVALID_REQUEST: return "invalid request";
+    case EMEL_ERR_STREAM_CAPTURE: return "not capturable: the stream is being captured";
     }
     return "unknown status";
 }
@@ -574,11 +655,11 @@ emel_status emel_stream_destroy(emel_stream stream)
 {
     {
         std::lock_guard<std::mutex> lock(g_mutex);
-        for (auto it = g_workspaces.begin(); it != g_workspaces.end();) {
+        for (auto it = g_streams.begin(); it != g_streams.end();) {
             if (it->first.second == as_stream(stream)) {
                 (void)hipStreamSynchronize(as_stream(stream));
-                (void)hipFree(it->second.ptr);
-                it = g_workspaces.erase(it);
+                free_state(*it->second);
+                it = g_streams.erase(it);
             } else {
                 ++it;
             }
@@ -598,10 +679,8 @@ emel_status emel_release_workspaces(void)
 {
     std::lock_guard<std::mutex> lock(g_mutex);
     hipError_t e = hipDeviceSynchronize();
-    for (auto &kv : g_workspaces) (void)hipFree(kv.second.ptr);
-    g_workspaces.clear();
-    for (auto &kv : g_staging) (void)hipHostFree(kv.second.ptr);
-    g_staging.clear();
+    for (auto &kv : g_streams) free_state(*kv.second);
+    g_streams.clear();
     return e == hipSuccess ? EMEL_OK : hip_fail(e, "hipDeviceSynchronize");
 }
 
@@ -1230,9 +1309,15 @@ emel_status get_rows(GrKind kind, const emel_tensor_view *src, const emel_index_
     // read from host memory (on_host) or from a host copy of the index span.
     const hipStream_t hs = as_stream(stream);
     const int32_t *hp = idx->data;
+    // Held through the index check and the launch: another host thread on
+    // this stream cannot refill the staging copy or the uploaded indices.
+    StreamLease lease;
     if (!idx->on_host) {
+        st = not_capturing(hs, "get_rows with device-resident indices (copied back and checked on the host)");
+        if (st == EMEL_OK) st = lease.acquire(hs);
+        if (st != EMEL_OK) return st;
         void *stage = nullptr;
-        st = staging_for(hs, ix.span, &stage);
+        st = lease.staging(ix.span, &stage);
         if (st != EMEL_OK) return st;
         hipError_t e = hipMemcpyAsync(stage, idx->data, ix.span, hipMemcpyDeviceToHost, hs);
         if (e == hipSuccess) e = hipStreamSynchronize(hs);
@@ -1285,8 +1370,11 @@ emel_status get_rows(GrKind kind, const emel_tensor_view *src, const emel_index_
     }
     // More indices than the arguments carry: upload the checked values in
     // ordinal order and read them row-major.
+    st = not_capturing(hs, "get_rows with more host indices than the launch arguments carry (uploaded and awaited)");
+    if (st == EMEL_OK) st = lease.acquire(hs);
+    if (st != EMEL_OK) return st;
     void *ws = nullptr;
-    st = workspace_for(hs, n * sizeof(int32_t), &ws);
+    st = lease.work(n * sizeof(int32_t), &ws);
     if (st != EMEL_OK) return st;
     hipError_t e = hipMemcpyAsync(ws, compact.data(), n * sizeof(int32_t), hipMemcpyHostToDevice, hs);
     if (e == hipSuccess) e = hipStreamSynchronize(hs); // the host vector goes away on return
@@ -1875,13 +1963,17 @@ emel_status gen_execute(const GenReq &q, Route route, int concat_axis, emel_stre
     }
     case Route::L2Norm: {
         void *ws = nullptr;
-        s = workspace_for(hs, emel::generic_workspace_bytes(emel::GenWork::L2Norm), &ws);
+        StreamLease lease;
+        s = lease.acquire(hs);
+        if (s == EMEL_OK) s = lease.work(emel::generic_workspace_bytes(emel::GenWork::L2Norm), &ws);
         if (s != EMEL_OK) return s;
         return launched(emel::launch_generic_l2_norm(gview(*q.s0), gview(dst), ws, hs));
     }
     case Route::CountEqual: {
         void *ws = nullptr;
-        s = workspace_for(hs, emel::generic_workspace_bytes(emel::GenWork::CountEqual), &ws);
+        StreamLease lease;
+        s = lease.acquire(hs);
+        if (s == EMEL_OK) s = lease.work(emel::generic_workspace_bytes(emel::GenWork::CountEqual), &ws);
         if (s != EMEL_OK) return s;
         return launched(emel::launch_generic_count_equal(gview(*q.s0), gview(*q.s1), static_cast<float *>(dmut.data),
                                                          ws, hs));
@@ -1897,8 +1989,10 @@ emel_status gen_execute(const GenReq &q, Route route, int concat_axis, emel_stre
         a.f16 = route == Route::MulMatF16;
         a.argmax = route == Route::MulMatArgmax;
         a.index_out = q.r.index_out;
+        StreamLease lease;
         if (a.argmax) {
-            s = workspace_for(hs, emel::generic_workspace_bytes(emel::GenWork::MulMatArgmax), &a.workspace);
+            s = lease.acquire(hs);
+            if (s == EMEL_OK) s = lease.work(emel::generic_workspace_bytes(emel::GenWork::MulMatArgmax), &a.workspace);
             if (s != EMEL_OK) return s;
         }
         return launched(emel::launch_generic_mul_mat(a, hs));
@@ -2037,7 +2131,12 @@ emel_status emel_sample_temperature_top_k_rows(const emel_sample_temperature_top
     a.score = req->selected_score_out;
     a.status = req->status_out;
     a.states = req->random_state;
-    s = workspace_for(as_stream(stream), emel::sampler_workspace_bytes(a.rows, card, a.top_k), &a.workspace);
+    // The draws advance the host-resident random_state when the call is
+    // enqueued; a replayed graph would redraw from the captured states.
+    s = not_capturing(as_stream(stream), "the sampler (its random_state advances on the host)");
+    StreamLease lease;
+    if (s == EMEL_OK) s = lease.acquire(as_stream(stream));
+    if (s == EMEL_OK) s = lease.work(emel::sampler_workspace_bytes(a.rows, card, a.top_k), &a.workspace);
     if (s != EMEL_OK) return s;
     const hipError_t e = emel::launch_sampler(a, as_stream(stream));
     if (e != hipSuccess) return hip_fail(e, "sampler launch");
@@ -2091,7 +2190,9 @@ emel_status emel_logits_validator_build(const float *logits, uint64_t logits_len
     emel_status s = ensure_device();
     if (s != EMEL_OK) return s;
     void *ws = nullptr;
-    s = workspace_for(as_stream(stream), emel::validator_workspace_bytes(n), &ws);
+    StreamLease lease;
+    s = lease.acquire(as_stream(stream));
+    if (s == EMEL_OK) s = lease.work(emel::validator_workspace_bytes(n), &ws);
     if (s != EMEL_OK) return s;
     const hipError_t e = emel::launch_validator(logits, n, candidate_ids, candidate_scores, ws, as_stream(stream));
     if (e != hipSuccess) return hip_fail(e, "validator launch");

@@ -80,17 +80,27 @@ hipError_t launch_rows(const RowArgs &args, hipStream_t stream);
 
 enum class RedOp : uint32_t { SumRows = 0, ArgmaxRows = 1, Sum = 2, Mean = 3, Argmax = 4 };
 
+// Scratch of a split-row reduction (both 0 when every row is reduced by a
+// single workgroup).  `partials` holds per-chunk partial words, rewritten by
+// every launch.  `counters` holds per-row arrival counters: they must be
+// zero before the first launch on that memory and every launch leaves them
+// zero again, so the counters buffer may hold nothing else.
+struct RedScratch {
+    uint64_t partials;
+    uint64_t counters;
+};
+
 struct RedArgs {
     RedOp op;
     Operand x;     // source
     void *dst;     // f32 (sums, mean, argmax index) or i32 (ArgmaxRows)
     Operand dst_view; // destination view (strided writes for SumRows)
-    void *workspace;  // per-stream scratch, see reduce_workspace_bytes
+    void *partials;   // at least scratch.partials bytes
+    void *counters;   // at least scratch.counters bytes, zero at rest
+    RedScratch scratch;
 };
 
-// Bytes of scratch the reduction needs for its per-chunk partials (0 when
-// every row is reduced by a single workgroup).
-uint64_t reduce_workspace_bytes(const RedArgs &args);
+RedScratch reduce_scratch_bytes(const RedArgs &args);
 hipError_t launch_reduce(const RedArgs &args, hipStream_t stream);
 
 // ---- generic-envelope routes (generic.hip) ---------------------------------

@@ -2,16 +2,33 @@
 // per-row argmax (one OpArgmax per row, reductions.rs:715-730) and the
 // whole-tensor sum / mean / argmax (reductions.rs:670-730).
 //
-// Long rows (the 151,936-wide logits rows) are split into `chunks` column
-// ranges, one workgroup each, so the grid fills all 256 CUs.  Each
-// workgroup reduces its range (f64 sums; (value, index) maxima) and writes
-// one partial; a second kernel with one wave per row combines the row's
-// partials in a fixed tree order.  The kernel boundary makes the partials
-// visible across XCDs without in-kernel fences: an agent-scope fence costs
-// an L2 write-back and invalidate per workgroup on gfx950, and a single pass
-// that hands partials over through agent-scope atomics measured 1.3-3.6x
-// slower than the second launch (contention on the per-row counter).
-// Results are deterministic run to run.
+// One launch.  Long rows (the 151,936-wide logits rows) are split into
+// `chunks` column ranges, one workgroup each, so the grid fills all 256 CUs.
+// Each workgroup reduces its range (f64 sums; (value, index) maxima) and
+// publishes one partial word; the last workgroup of a row to finish merges
+// the row's partials and writes the result.
+//
+// The hand-over uses agent-scope relaxed atomics only, no fences:
+//   - a partial is stored with an agent-scope store (global_store ... sc1,
+//     written through to the coherence point every XCD reads from), and
+//     `s_waitcnt vmcnt(0)` waits for its acknowledgement;
+//   - then the workgroup adds 1 to its row's arrival counter (agent-scope
+//     atomic add with return).  The workgroup that sees count - 1 is last:
+//     every other partial of the row was acknowledged before its writer's
+//     increment, which came before this one;
+//   - the last workgroup reads the partials with agent-scope loads (sc1,
+//     served from the coherence point), merges them in a fixed lane order
+//     (so the result does not depend on which workgroup came last), writes
+//     the result and stores 0 back into the counter for the next launch.
+// This is the release/acquire pair with the L2 write-back and invalidate
+// left out: every value handed over is itself written and read at the
+// coherence point, so nothing else needs to be made visible.
+//
+// Counters live on separate cache lines (a line sees about 32 increments
+// per launch): increments of one line are serialised at the coherence
+// point, and 64 row counters packed into 256 bytes measured 2x slower.  A
+// row with more than 64 chunks merges in two levels: groups of up to 64
+// chunks, then the groups.
 //
 // argmax keeps the reference's sequential strict-> scan semantics: the
 // winner is the lowest index among the maximal non-NaN values, NaNs never
@@ -30,9 +47,21 @@ struct ArgPart {
     uint32_t i;
 };
 
+constexpr uint32_t kMaxGroup = kWave;          // chunks merged by one wave
+constexpr uint32_t kMaxChunks = kMaxGroup * kMaxGroup;
+constexpr uint32_t kLineWords = 64;            // 256 bytes of u32 counters
+#ifndef RED_BATCH
+constexpr int kRedBatch = 5;                   // float4 loads in flight per thread
+#else
+constexpr int kRedBatch = RED_BATCH;
+#endif
+
 struct RedGeo {
     uint32_t rows;
-    uint32_t chunks;
+    uint32_t chunks;      // chunks per row
+    uint32_t groups;      // first-level groups per row (1: one level)
+    uint32_t group_size;  // chunks per group (<= 64)
+    uint32_t cstride;     // first-level counter stride, in u32 words
     uint64_t ncols;       // columns per row (whole tensor: the element count)
     uint64_t chunk_cols;  // columns per chunk (a multiple of 4 when vectorized)
     FastDiv ne1, ne2;     // row -> (i1, i2, i3)
@@ -40,6 +69,9 @@ struct RedGeo {
     int64_t d_st[4];
     uint64_t ne[4];       // source extents (ordinal mode)
     uint32_t mode;        // 0: float4 rows, 1: scalar rows (x_st[0]), 2: ordinal decode (rows == 1)
+    // scratch layout: byte offsets of the two partial arrays in the partials
+    // buffer, and of the two counter arrays in the counters buffer
+    uint64_t off_part1, off_part2, off_cnt1, off_cnt2;
 };
 
 enum : uint32_t { kModeVec = 0, kModeScalar = 1, kModeOrdinal = 2 };
@@ -60,10 +92,12 @@ struct Acc {
     static constexpr bool kArg = OP == RedOp::ArgmaxRows || OP == RedOp::Argmax;
 };
 
-// Per-thread accumulation over [c0, c1) of row r.
+// Per-thread accumulation over [c0, c1) of row r.  `first` receives the
+// first element the thread reads (for thread 0 of the row's chunk 0: column
+// 0, which the argmax NaN rule needs).
 template <RedOp OP>
 __device__ __forceinline__ void accumulate(const RedGeo &g, const float *x, int64_t base, uint64_t c0, uint64_t c1,
-                                           double &sum, float &bv, uint32_t &bi)
+                                           double &sum, float &bv, uint32_t &bi, float &first)
 {
     constexpr bool kArg = Acc<OP>::kArg;
     auto take = [&](float v, uint64_t c) {
@@ -77,42 +111,56 @@ __device__ __forceinline__ void accumulate(const RedGeo &g, const float *x, int6
         }
     };
     if (g.mode == kModeVec) {
-        const float4 *x4 = reinterpret_cast<const float4 *>(x + base);
-        auto take4 = [&](const float4 &q, uint64_t c) {
-            if constexpr (kArg) {
-                take(q.x, c);
-                take(q.y, c + 1);
-                take(q.z, c + 2);
-                take(q.w, c + 3);
-            } else {
-                sum += (static_cast<double>(q.x) + static_cast<double>(q.y)) +
-                       (static_cast<double>(q.z) + static_cast<double>(q.w));
+        // The range is read through a buffer descriptor bounded to it: a
+        // load past its end returns zeros without touching memory.  Each
+        // batch issues kBatch non-temporal 128-bit loads per thread
+        // unconditionally (one round trip; no lane-dependent branches, which
+        // would serialise the loads), then takes the in-range ones.  Zeros
+        // leave a sum unchanged: a partial sum that starts at +0.0 is never
+        // -0.0.
+        constexpr int kBatch = kRedBatch;
+        const uint32_t nvec = static_cast<uint32_t>((c1 - c0) / 4);
+        const BufRsrc r = buffer_rsrc(x + base + c0, nvec * 16u);
+        for (uint32_t v0 = 0; v0 < nvec; v0 += kBatch * kBlock) {
+            float4 q[kBatch];
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j) q[j] = ld_buf_nt(r, (v0 + j * kBlock + threadIdx.x) * 16u);
+            if (v0 == 0) first = q[0].x;
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j) {
+                const uint32_t k = v0 + j * kBlock + threadIdx.x;
+                if constexpr (kArg) {
+                    if (k < nvec) {
+                        const uint64_t c = c0 + 4 * k;
+                        take(q[j].x, c);
+                        take(q[j].y, c + 1);
+                        take(q[j].z, c + 2);
+                        take(q[j].w, c + 3);
+                    }
+                } else {
+                    sum += (static_cast<double>(q[j].x) + static_cast<double>(q[j].y)) +
+                           (static_cast<double>(q[j].z) + static_cast<double>(q[j].w));
+                }
             }
-        };
-        // kUnroll non-temporal loads in flight per thread (each byte is read
-        // once), then taken in column order
-        constexpr int kUnroll = 4;
-        const uint64_t vend = c1 / 4;
-        uint64_t v = c0 / 4 + threadIdx.x;
-        for (; v + (kUnroll - 1) * kBlock < vend; v += kUnroll * kBlock) {
-            float4 q[kUnroll];
-#pragma unroll
-            for (int j = 0; j < kUnroll; ++j) q[j] = ld_nt(x4 + v + j * kBlock);
-#pragma unroll
-            for (int j = 0; j < kUnroll; ++j) take4(q[j], 4 * (v + j * kBlock));
         }
-        for (; v < vend; v += kBlock) take4(ld_nt(x4 + v), 4 * v);
     } else if (g.mode == kModeScalar) {
-        for (uint64_t c = c0 + threadIdx.x; c < c1; c += kBlock) take(x[base + static_cast<int64_t>(c) * g.x_st[0]], c);
+        for (uint64_t c = c0 + threadIdx.x; c < c1; c += kBlock) {
+            const float v = x[base + static_cast<int64_t>(c) * g.x_st[0]];
+            if (c == c0 + threadIdx.x) first = v;
+            take(v, c);
+        }
     } else {
-        for (uint64_t c = c0 + threadIdx.x; c < c1; c += kBlock) take(x[ordinal_offset(g, c)], c);
+        for (uint64_t c = c0 + threadIdx.x; c < c1; c += kBlock) {
+            const float v = x[ordinal_offset(g, c)];
+            if (c == c0 + threadIdx.x) first = v;
+            take(v, c);
+        }
     }
 }
 
 // Writes the row result from its combined (sum | (value, index)) word.
-// argmax: `first` is the row's column 0 (a NaN there makes the result 0).
 template <RedOp OP>
-__device__ __forceinline__ void write_result(const RedGeo &g, float first, void *dst, uint32_t row, uint64_t packed)
+__device__ __forceinline__ void write_result(const RedGeo &g, void *dst, uint32_t row, uint64_t packed)
 {
     constexpr bool kArg = Acc<OP>::kArg;
     uint32_t i1 = 0, i2 = 0, i3 = 0;
@@ -126,9 +174,8 @@ __device__ __forceinline__ void write_result(const RedGeo &g, float first, void 
                          static_cast<int64_t>(i3) * g.d_st[3];
     if constexpr (kArg) {
         const ArgPart p = __builtin_bit_cast(ArgPart, packed);
-        // column 0 NaN: the sequential scan never replaces it
-        const uint64_t idx = (first != first || p.i == 0xffffffffu) ? 0 : p.i;
-        const float fidx = static_cast<float>(idx); // the reference stores the index as f32
+        const uint64_t idx = p.i == 0xffffffffu ? 0 : p.i; // no candidate: every value was NaN or -inf
+        const float fidx = static_cast<float>(idx);         // the reference stores the index as f32
         if constexpr (OP == RedOp::ArgmaxRows) static_cast<int32_t *>(dst)[doff] = static_cast<int32_t>(fidx);
         else static_cast<float *>(dst)[doff] = fidx;
     } else {
@@ -140,10 +187,48 @@ __device__ __forceinline__ void write_result(const RedGeo &g, float first, void 
     }
 }
 
-// Pass 1: workgroup (row, chunk) reduces its column range.  With one chunk
-// per row it writes the result; otherwise it writes its partial word.
+// Merges n <= 64 partial words across the wave: lane l contributes `own`
+// when l == self, else the word at slots[l] (read at the coherence point).
+// Returns the merged word, uniform.
 template <RedOp OP>
-__global__ __launch_bounds__(kBlock) void k_reduce(RedGeo g, const float *x, void *dst, uint64_t *part)
+__device__ __forceinline__ uint64_t merge_slots(const uint64_t *slots, uint32_t n, uint32_t self, uint64_t own)
+{
+    constexpr bool kArg = Acc<OP>::kArg;
+    const uint32_t lane = threadIdx.x % kWave;
+    uint64_t q = own;
+    if (lane < n && lane != self) q = __hip_atomic_load(slots + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if constexpr (kArg) {
+        const ArgPart p = __builtin_bit_cast(ArgPart, q);
+        float v = lane < n ? p.v : -__builtin_inff();
+        uint32_t i = lane < n ? p.i : 0xffffffffu;
+        wave_argmax_dpp(v, i);
+        return __builtin_bit_cast(uint64_t, ArgPart{v, i});
+    } else {
+        const double t = wave_sum_dpp(lane < n ? __builtin_bit_cast(double, q) : 0.0);
+        return __builtin_bit_cast(uint64_t, t);
+    }
+}
+
+// Publishes `packed` into `slot` and counts the arrival; true for the last of
+// `n` arrivals (uniform).  Lane 0 does the memory operations.
+__device__ __forceinline__ bool arrive(uint64_t *slot, uint32_t *counter, uint32_t n, uint64_t packed)
+{
+    uint32_t prev = 0;
+    if (threadIdx.x == 0) {
+        __hip_atomic_store(slot, packed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // the partial is at the coherence point
+        prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    prev = __builtin_amdgcn_readfirstlane(prev);
+    if (prev != n - 1) return false;
+    if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
+}
+
+// Workgroup (row, chunk) reduces its column range; with one chunk per row it
+// writes the result, otherwise it hands its partial over (see above).
+template <RedOp OP>
+__global__ __launch_bounds__(kBlock) void k_reduce(RedGeo g, const float *x, void *dst, char *parts, char *counts)
 {
     constexpr bool kArg = Acc<OP>::kArg;
     __shared__ double s_sum[kBlock / kWave];
@@ -167,83 +252,68 @@ __global__ __launch_bounds__(kBlock) void k_reduce(RedGeo g, const float *x, voi
     const uint64_t c0 = static_cast<uint64_t>(chunk) * g.chunk_cols;
     const uint64_t c1 = c0 + g.chunk_cols < g.ncols ? c0 + g.chunk_cols : g.ncols;
 
-    // argmax: the row's column 0, read by the chunk-0 workgroup while its
-    // range loads are in flight (a NaN there decides the row)
-    float first = 0.0f;
-    if constexpr (kArg) {
-        if (chunk == 0 && threadIdx.x == 0) first = g.mode == kModeOrdinal ? x[ordinal_offset(g, 0)] : x[base];
-    }
-
     double sum = 0.0;
     float bv = -__builtin_inff();
     uint32_t bi = 0xffffffffu; // "no candidate": loses every tie on index
-    accumulate<OP>(g, x, base, c0, c1, sum, bv, bi);
+    float first = 0.0f;        // thread 0 of chunk 0: the row's column 0
+    accumulate<OP>(g, x, base, c0, c1, sum, bv, bi, first);
 
     if constexpr (kArg) {
-        wave_argmax(bv, bi);
+        wave_argmax_dpp(bv, bi);
         if (lane == 0) {
             s_v[wave] = bv;
             s_i[wave] = bi;
         }
     } else {
-        sum = wave_sum(sum);
+        sum = wave_sum_dpp(sum);
         if (lane == 0) s_sum[wave] = sum;
     }
     __syncthreads();
-    if (threadIdx.x != 0) return;
+    if (wave != 0) return;
+    // wave 0 alone from here on: the partial is uniform across it
     uint64_t packed;
     if constexpr (kArg) {
-        for (int w = 1; w < kBlock / kWave; ++w) argmax_merge(s_v[0], s_i[0], s_v[w], s_i[w]);
-        packed = __builtin_bit_cast(uint64_t, ArgPart{s_v[0], s_i[0]});
-        // Split rows: a NaN in column 0 makes chunk 0's partial (+inf, 0),
-        // which every other partial loses to (greater value, or equal value
-        // and higher index), so the combined index is 0.
-        if (g.chunks > 1 && chunk == 0 && first != first)
-            packed = __builtin_bit_cast(uint64_t, ArgPart{__builtin_inff(), 0u});
-    } else {
-        double t = s_sum[0];
-        for (int w = 1; w < kBlock / kWave; ++w) t += s_sum[w];
-        packed = __builtin_bit_cast(uint64_t, t);
-    }
-    if (g.chunks == 1) write_result<OP>(g, first, dst, row, packed);
-    else part[blockIdx.x] = packed;
-}
-
-// Pass 2: one wave per row combines the row's partials (lane l takes
-// chunks l, l+64, ...; then a fixed butterfly) and writes the result.
-template <RedOp OP>
-__global__ __launch_bounds__(kBlock) void k_reduce_finish(RedGeo g, void *dst, const uint64_t *part)
-{
-    constexpr bool kArg = Acc<OP>::kArg;
-    const uint32_t row = blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave;
-    const uint32_t lane = threadIdx.x % kWave;
-    if (row >= g.rows) return;
-    double tsum = 0.0;
-    float tv = -__builtin_inff();
-    uint32_t ti = 0xffffffffu;
-    for (uint32_t c = lane; c < g.chunks; c += kWave) {
-        const uint64_t q = part[static_cast<uint64_t>(row) * g.chunks + c];
-        if constexpr (kArg) {
-            const ArgPart p = __builtin_bit_cast(ArgPart, q);
-            argmax_merge(tv, ti, p.v, p.i);
-        } else {
-            tsum += __builtin_bit_cast(double, q);
+        float v = s_v[0];
+        uint32_t i = s_i[0];
+        for (int w = 1; w < kBlock / kWave; ++w) argmax_merge(v, i, s_v[w], s_i[w]);
+        // A NaN in column 0 decides the row: chunk 0's partial becomes
+        // (+inf, 0), which every other candidate loses to (equal value and a
+        // higher index, or a lower value).
+        first = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, first))); // thread 0
+        if (chunk == 0 && first != first) {
+            v = __builtin_inff();
+            i = 0;
         }
-    }
-    uint64_t packed;
-    if constexpr (kArg) {
-        wave_argmax(tv, ti);
-        packed = __builtin_bit_cast(uint64_t, ArgPart{tv, ti});
+        packed = __builtin_bit_cast(uint64_t, ArgPart{v, i});
     } else {
-        tsum = wave_sum(tsum);
-        packed = __builtin_bit_cast(uint64_t, tsum);
+        packed = __builtin_bit_cast(uint64_t, (s_sum[0] + s_sum[1]) + (s_sum[2] + s_sum[3]));
     }
-    // column 0 was folded into chunk 0's partial by pass 1
-    if (lane == 0) write_result<OP>(g, 0.0f, dst, row, packed);
+    if (g.chunks == 1) {
+        if (lane == 0) write_result<OP>(g, dst, row, packed);
+        return;
+    }
+    uint64_t *part1 = reinterpret_cast<uint64_t *>(parts + g.off_part1);
+    uint32_t *cnt1 = reinterpret_cast<uint32_t *>(counts + g.off_cnt1);
+    const uint32_t grp = chunk / g.group_size;
+    const uint32_t gfirst = grp * g.group_size;
+    const uint32_t gn = g.chunks - gfirst < g.group_size ? g.chunks - gfirst : g.group_size;
+    uint64_t *gslots = part1 + static_cast<uint64_t>(row) * g.chunks + gfirst;
+    if (!arrive(gslots + (chunk - gfirst), cnt1 + (static_cast<uint64_t>(row) * g.groups + grp) * g.cstride, gn, packed))
+        return;
+    packed = merge_slots<OP>(gslots, gn, chunk - gfirst, packed);
+    if (g.groups > 1) {
+        uint64_t *rslots = reinterpret_cast<uint64_t *>(parts + g.off_part2) + static_cast<uint64_t>(row) * g.groups;
+        uint32_t *cnt2 = reinterpret_cast<uint32_t *>(counts + g.off_cnt2) + static_cast<uint64_t>(row) * kLineWords;
+        if (!arrive(rslots + grp, cnt2, g.groups, packed)) return;
+        packed = merge_slots<OP>(rslots, g.groups, grp, packed);
+    }
+    if (lane == 0) write_result<OP>(g, dst, row, packed);
 }
 
 constexpr uint32_t kTargetBlocks = 2048; // 8 workgroups per CU on 256 CUs
 constexpr uint64_t kMinChunkCols = 4 * kBlock; // one float4 per thread at least
+
+uint64_t align256(uint64_t b) { return (b + 255) & ~uint64_t{255}; }
 
 bool plan(const RedArgs &a, RedGeo &g)
 {
@@ -293,22 +363,47 @@ bool plan(const RedArgs &a, RedGeo &g)
     uint64_t want = (kTargetBlocks + g.rows - 1) / g.rows;
     uint64_t chunk = (g.ncols + want - 1) / want;
     if (chunk < kMinChunkCols) chunk = kMinChunkCols;
+    const uint64_t min_for_cap = (g.ncols + kMaxChunks - 1) / kMaxChunks;
+    if (chunk < min_for_cap) chunk = min_for_cap;
     chunk = (chunk + 3) & ~uint64_t{3};
     uint64_t chunks = (g.ncols + chunk - 1) / chunk;
     if (chunks == 0) chunks = 1;
-    if (static_cast<uint64_t>(g.rows) * chunks > 0x7fffffffull) return false;
+    if (chunks > kMaxChunks || static_cast<uint64_t>(g.rows) * chunks > 0x7fffffffull) return false;
     g.chunks = static_cast<uint32_t>(chunks);
     g.chunk_cols = chunk;
+    if (g.mode == kModeVec && chunk * 4 > 0x7fffffffull) g.mode = kModeScalar; // buffer offsets are 32-bit
+    g.groups = (g.chunks + kMaxGroup - 1) / kMaxGroup;
+    g.group_size = (g.chunks + g.groups - 1) / g.groups;
+    // first-level counters: about 32 increments per 128-byte line
+    uint32_t cs = 1;
+    while (cs < g.group_size && cs < kLineWords) cs <<= 1;
+    g.cstride = cs;
+    if (g.chunks > 1) {
+        const uint64_t rows = g.rows;
+        g.off_part1 = 0;
+        g.off_part2 = align256(rows * g.chunks * sizeof(uint64_t));
+        g.off_cnt1 = 0;
+        g.off_cnt2 = align256(rows * g.groups * g.cstride * sizeof(uint32_t));
+    }
     return true;
+}
+
+RedScratch scratch_bytes(const RedGeo &g)
+{
+    RedScratch r{0, 0};
+    if (g.chunks <= 1) return r;
+    r.partials = g.off_part2 + (g.groups > 1 ? align256(uint64_t{g.rows} * g.groups * sizeof(uint64_t)) : 0);
+    r.counters = g.off_cnt2 + (g.groups > 1 ? align256(uint64_t{g.rows} * kLineWords * sizeof(uint32_t)) : 0);
+    return r;
 }
 
 } // namespace
 
-uint64_t reduce_workspace_bytes(const RedArgs &a)
+RedScratch reduce_scratch_bytes(const RedArgs &a)
 {
     RedGeo g;
-    if (!plan(a, g) || g.chunks == 1) return 0;
-    return static_cast<uint64_t>(g.rows) * g.chunks * sizeof(uint64_t);
+    if (!plan(a, g)) return RedScratch{0, 0};
+    return scratch_bytes(g);
 }
 
 hipError_t launch_reduce(const RedArgs &a, hipStream_t s)
@@ -316,14 +411,15 @@ hipError_t launch_reduce(const RedArgs &a, hipStream_t s)
     RedGeo g;
     if (!plan(a, g)) return hipErrorInvalidValue;
     const float *x = static_cast<const float *>(a.x.data);
-    uint64_t *part = static_cast<uint64_t *>(a.workspace);
-    if (g.chunks > 1 && !part) return hipErrorInvalidValue;
+    const RedScratch need = scratch_bytes(g);
+    char *parts = static_cast<char *>(a.partials);
+    char *counts = static_cast<char *>(a.counters);
+    if (need.partials > a.scratch.partials || need.counters > a.scratch.counters) return hipErrorInvalidValue;
+    if (g.chunks > 1 && (!parts || !counts)) return hipErrorInvalidValue;
     const dim3 grid(g.rows * g.chunks);
-    const dim3 fgrid((g.rows + (kBlock / kWave) - 1) / (kBlock / kWave));
     auto run = [&](auto op_tag) {
         constexpr RedOp OP = decltype(op_tag)::value;
-        k_reduce<OP><<<grid, kBlock, 0, s>>>(g, x, a.dst, part);
-        if (g.chunks > 1) k_reduce_finish<OP><<<fgrid, kBlock, 0, s>>>(g, a.dst, part);
+        k_reduce<OP><<<grid, kBlock, 0, s>>>(g, x, a.dst, parts, counts);
     };
     switch (a.op) {
     case RedOp::SumRows: run(std::integral_constant<RedOp, RedOp::SumRows>{}); break;

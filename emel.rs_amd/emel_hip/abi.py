@@ -29,6 +29,7 @@ class Status(enum.IntEnum):
     INDEX_OUT_OF_BOUNDS = 11
     UNSUPPORTED_SOURCE_STRIDE = 12
     INVALID_REQUEST = 13
+    STREAM_CAPTURE = 14
 
 
 class DType(enum.IntEnum):

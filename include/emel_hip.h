@@ -60,8 +60,10 @@ typedef enum emel_status {
     EMEL_ERR_UNSUPPORTED_OPERATION = 10, /* root Error::UnsupportedOperation */
     EMEL_ERR_INDEX_OUT_OF_BOUNDS = 11,   /* GetRowsError::IndexOutOfBounds (get_rows.rs:520-535) */
     EMEL_ERR_UNSUPPORTED_SOURCE_STRIDE = 12, /* GetRowsError::UnsupportedSourceStride */
-    EMEL_ERR_INVALID_REQUEST = 13 /* emel-logits SamplerError::InvalidRequest / ValidatorError::InvalidRequest
-                                     (crates/emel-logits/src/sampler/sm.rs:41-52, validator/sm.rs:15-21) */
+    EMEL_ERR_INVALID_REQUEST = 13, /* emel-logits SamplerError::InvalidRequest / ValidatorError::InvalidRequest
+                                      (crates/emel-logits/src/sampler/sm.rs:41-52, validator/sm.rs:15-21) */
+    EMEL_ERR_STREAM_CAPTURE = 14   /* the call would allocate, synchronise or advance host state while its
+                                      stream is being captured into a HIP graph (no reference counterpart) */
 } emel_status;
 
 /* Wire dtype codes, DType::from_code (tensor_view.rs:111-158). */
