@@ -497,7 +497,8 @@ emel_status rows(const emel::RowArgs &args, const emel_tensor_view &in, const em
     return launched(emel::launch_rows(args, as_stream(stream)));
 }
 
-emel_status reduce(emel::RedOp op, const emel_tensor_view &src, const emel_tensor_view_mut &dst, emel_stream stream)
+emel_status reduce(emel::RedOp op, const emel_tensor_view &src, const emel_tensor_view_mut &dst, emel_stream stream,
+                   bool static_scratch = false)
 {
     if (!overlap_ok(dst, 4, src, 4) || dst.data == src.data)
         return fail(EMEL_ERR_INVALID_VIEW, "dst overlaps the source");
@@ -513,7 +514,13 @@ emel_status reduce(emel::RedOp op, const emel_tensor_view &src, const emel_tenso
         for (int d = 0; d < 4; ++d) args.dst_view.st[d] = static_cast<int64_t>(dst.nb[d] / 4);
     args.scratch = emel::reduce_scratch_bytes(args);
     StreamLease lease;
-    if (args.scratch.partials) {
+    if (static_scratch) {
+        const hipError_t e = emel::reduce_static_scratch(args, as_stream(stream));
+        if (e == hipErrorOutOfMemory)
+            return fail(EMEL_ERR_INVALID_PARAMETERS, "the reduction needs more scratch than the allocation-free "
+                                                     "entry point's static 64 KiB partials / 64 KiB counters");
+        if (e != hipSuccess) return hip_fail(e, "setting up the static reduction scratch");
+    } else if (args.scratch.partials) {
         s = lease.acquire(as_stream(stream));
         if (s == EMEL_OK) s = lease.work(args.scratch.partials, &args.partials);
         if (s == EMEL_OK) s = lease.counters(args.scratch.counters, &args.counters);
@@ -1060,6 +1067,18 @@ emel_status emel_op_argmax_rows(const emel_tensor_view *src, const emel_tensor_v
         return fail(EMEL_ERR_INVALID_VIEW, "argmax_rows view failed validation");
     if (!rows_dst(*src, *dst)) return fail(EMEL_ERR_SHAPE_MISMATCH, "argmax_rows dst must be [1, ne1, ne2, ne3]");
     return reduce(emel::RedOp::ArgmaxRows, *src, *dst, stream);
+}
+
+// The same op with its partials and arrival counters in the device's static
+// scratch (reduce.hip): no allocation, no synchronisation, no host state.
+emel_status emel_op_argmax_rows_no_alloc(const emel_tensor_view *src, const emel_tensor_view_mut *dst,
+                                         emel_stream stream)
+{
+    if (!src || !dst) return fail(EMEL_ERR_INVALID_ARGUMENT, "null view");
+    if (!valid_f32(*src, false) || !valid_i32(*dst))
+        return fail(EMEL_ERR_INVALID_VIEW, "argmax_rows view failed validation");
+    if (!rows_dst(*src, *dst)) return fail(EMEL_ERR_SHAPE_MISMATCH, "argmax_rows dst must be [1, ne1, ne2, ne3]");
+    return reduce(emel::RedOp::ArgmaxRows, *src, *dst, stream, true);
 }
 
 // ---- row gather (get_rows.rs) -------------------------------------------------

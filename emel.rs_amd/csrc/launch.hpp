@@ -101,6 +101,11 @@ struct RedArgs {
 };
 
 RedScratch reduce_scratch_bytes(const RedArgs &args);
+// Points args' scratch at the device's static reduction scratch (128 KiB,
+// shared by every call on the device; set up on the device's first call).
+// hipErrorOutOfMemory when the plan needs more than it holds.  Allocates
+// nothing.
+hipError_t reduce_static_scratch(RedArgs &args, hipStream_t stream);
 hipError_t launch_reduce(const RedArgs &args, hipStream_t stream);
 
 // ---- generic-envelope routes (generic.hip) ---------------------------------

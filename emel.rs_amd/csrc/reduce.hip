@@ -34,6 +34,7 @@
 // winner is the lowest index among the maximal non-NaN values, NaNs never
 // win, and a NaN in column 0 makes the result 0 (nothing compares greater
 // than the initial NaN).
+#include <mutex>
 #include <type_traits>
 
 #include "common.hpp"
@@ -397,7 +398,63 @@ RedScratch scratch_bytes(const RedGeo &g)
     return r;
 }
 
+// ---- the allocation-free entry point's scratch -------------------------------
+//
+// One array per device, in the code object's zero-initialised data: the
+// first 64 KiB hold arrival counters, the next 64 KiB partials.  Every plan
+// above needs at most 24 KiB of counters and 32 KiB of partials (rows below
+// 2048 split into at most 2048 + rows chunks in total; more rows need no
+// scratch).  In host code `scratch` names a host-side stand-in: the device
+// address comes from hipGetSymbolAddress, once per device.
+constexpr uint64_t kStaticCounterBytes = 64u << 10;
+constexpr uint64_t kStaticPartialBytes = 64u << 10;
+static __device__ __align__(256) unsigned char scratch[kStaticCounterBytes + kStaticPartialBytes];
+
+__global__ __launch_bounds__(kBlock) void k_clear_words(uint32_t *p, uint32_t n)
+{
+    const uint32_t i = blockIdx.x * kBlock + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_static_lock;
+char *g_static_base[kMaxDevices]; // device address of `scratch`, per device (null until set up)
+
 } // namespace
+
+hipError_t reduce_static_scratch(RedArgs &a, hipStream_t stream)
+{
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    char *base = nullptr;
+    {
+        std::lock_guard<std::mutex> g(g_static_lock);
+        if (!g_static_base[dev]) {
+            // set-up on this device's first call, with the device current
+            void *ptr = nullptr;
+            e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+            if (e != hipSuccess) return e;
+            if (!ptr) return hipErrorInvalidSymbol;
+            // The counters must start at zero (launches leave them zero).  A
+            // fill kernel, not a memset node, so a captured first call
+            // replays correctly.
+            constexpr uint32_t words = kStaticCounterBytes / 4;
+            k_clear_words<<<(words + kBlock - 1) / kBlock, kBlock, 0, stream>>>(static_cast<uint32_t *>(ptr), words);
+            e = hipGetLastError();
+            if (e != hipSuccess) return e;
+            g_static_base[dev] = static_cast<char *>(ptr);
+        }
+        base = g_static_base[dev];
+    }
+    const RedScratch need = reduce_scratch_bytes(a);
+    if (need.counters > kStaticCounterBytes || need.partials > kStaticPartialBytes) return hipErrorOutOfMemory;
+    a.counters = base;
+    a.partials = base + kStaticCounterBytes;
+    a.scratch = RedScratch{kStaticPartialBytes, kStaticCounterBytes};
+    return hipSuccess;
+}
 
 RedScratch reduce_scratch_bytes(const RedArgs &a)
 {

@@ -308,6 +308,7 @@ SIGNATURES = {
     "emel_op_mean": [_V, _V, _S],
     "emel_op_argmax": [_V, _V, _S],
     "emel_op_argmax_rows": [_V, _V, _S],
+    "emel_op_argmax_rows_no_alloc": [_V, _V, _S],
     "emel_validate_view": [_V, ctypes.c_int32],
     "emel_validate_normalization_view": [_V],
     "emel_device_count": [ctypes.POINTER(ctypes.c_int32)],

@@ -289,6 +289,19 @@ emel_status emel_op_argmax(const emel_tensor_view *src, const emel_tensor_view_m
  * column 0 yields 0, exactly as the sequential strict-> scan). */
 emel_status emel_op_argmax_rows(const emel_tensor_view *src, const emel_tensor_view_mut *dst,
                                 emel_stream stream);
+/* emel_op_argmax_rows without any allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same guards, statuses and results as emel_op_argmax_rows;
+ * the split-row partials and arrival counters live in a static 128 KiB
+ * per-device array (64 KiB counters, 64 KiB partials), set up on the
+ * device's first call.  Every shape argmax_rows accepts fits; a plan that
+ * did not would return EMEL_ERR_INVALID_PARAMETERS.  All calls on one
+ * device share that array: calls that overlap on the device (concurrent
+ * streams, or graphs replayed concurrently) race and must be serialised by
+ * the caller. */
+emel_status emel_op_argmax_rows_no_alloc(const emel_tensor_view *src, const emel_tensor_view_mut *dst,
+                                         emel_stream stream);
 
 /* ---- row gather -----------------------------------------------------------------
  * get_rows::OpGetRows / OpGetRowsF32Bytes / OpGetRowsF16 / OpGetRowsBf16 /
