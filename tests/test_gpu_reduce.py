@@ -9,7 +9,7 @@ import pytest
 
 import emel_hip as eh
 import oracle as orc
-from helpers import Pair, normal
+from helpers import Pair, assert_close_rel, normal
 
 pytestmark = pytest.mark.gpu
 
@@ -161,3 +161,35 @@ def test_repeated_launches_reuse_workspace(gpu):
     import torch
     torch.cuda.synchronize()
     assert (o.result() == where).all()
+
+
+def test_sum_rows_non_finite(gpu):
+    # f64 accumulation: NaN anywhere -> NaN; +inf and -inf -> NaN; one sign of
+    # inf -> inf; finite values whose f64 sum exceeds the f32 range -> inf
+    # when rounded; the order of the f64 tree cannot change these.
+    for cols in (151936, 4096, 37):
+        g = np.random.Generator(np.random.PCG64(431 + cols))
+        rows = []
+        def base():
+            return g.standard_normal(cols).astype(np.float32)
+        r = base(); r[0] = np.nan; rows.append(r)
+        r = base(); r[cols // 2] = np.nan; r[1] = np.inf; rows.append(r)
+        r = base(); r[cols // 3] = np.inf; rows.append(r)
+        r = base(); r[cols // 3] = np.inf; r[-1] = -np.inf; rows.append(r)
+        r = base(); r[-1] = -np.inf; rows.append(r)
+        rows.append(np.full(cols, np.float32(3e38)))
+        rows.append(np.full(cols, np.float32(-3e38)))
+        r = np.full(cols, np.float32(3e38)); r[::2] = np.float32(-3e38); rows.append(r)
+        rows.append(base())
+        x = np.concatenate(rows)
+        n = len(rows)
+        a = Pair(x, [cols, n, 1, 1]).to(gpu)
+        o = Pair(np.zeros(n, np.float32), [1, n, 1, 1]).to(gpu)
+        assert eh.Kernel().process_event(eh.OpSumRows(a.pview(), o.pview(mut=True))) == eh.Status.OK, eh.last_error()
+        want = np.zeros(n, np.float32)
+        assert orc.sum_rows(a.oview(), orc.view(want, o.ne)) == orc.OK
+        got = o.result()
+        assert np.isnan(want[0]) and np.isnan(want[3]) and want[2] == np.inf and want[4] == -np.inf
+        assert_close_rel(got, want, 1e-5, f"sum_rows non-finite, {cols} columns",
+                         atol=1e-12 * float(np.abs(x[np.isfinite(x)].astype(np.float64)).sum()))
+        assert (np.isnan(got) == np.isnan(want)).all()

@@ -200,3 +200,105 @@ def test_rows_in_place(gpu):
         want = x.copy()
         assert fn(orc.view(x, a.ne), orc.view(want, a.ne)) == orc.OK
         assert_close_rel(a.result(), want, RTOL, "in place")
+
+
+# ---- non-finite inputs --------------------------------------------------------
+#
+# The reference seeds a row's max with column 0 and scans with a strict >
+# (reductions.rs:565-601), so a NaN anywhere in a row, or a +inf, makes every
+# exp(x - max) of that row NaN or the sum NaN: the whole row is NaN.  A row
+# that is entirely -inf has max -inf, and exp(-inf - -inf) = exp(NaN) makes
+# it NaN too.  -inf entries among finite ones give exp(-inf) = 0.  The GPU's
+# max ignores NaN; the rows still agree because the NaN reaches the sum.
+
+def special_rows(cols, seed):
+    """One row per case, N(0, 4) elsewhere."""
+    g = np.random.Generator(np.random.PCG64(seed))
+    rows = []
+    def base():
+        return (g.standard_normal(cols) * 2).astype(np.float32)
+    r = base(); r[0] = np.nan; rows.append(r)                           # NaN at column 0
+    r = base(); r[cols // 2] = np.nan; rows.append(r)                   # NaN mid-row
+    r = base(); r[-1] = np.nan; r[0] = -np.inf; rows.append(r)          # NaN last, -inf first
+    r = base(); r[cols // 3] = np.inf; rows.append(r)                   # one +inf
+    r = base(); r[0] = np.inf; r[-1] = np.inf; rows.append(r)           # two +inf
+    r = base(); r[g.random(cols) < 0.5] = -np.inf; r[cols // 2] = 1.0; rows.append(r)  # -inf among finite
+    rows.append(np.full(cols, -np.inf, np.float32))                     # all -inf
+    r = base(); r[1 % cols] = np.inf; r[0] = -np.inf; rows.append(r)    # +inf and -inf
+    r = base(); r[:] = np.float32(3e38); rows.append(r)                 # large equal values
+    r = base(); r[0] = np.float32(1e-45); rows.append(r)                # a subnormal
+    rows.append(base())                                                 # ordinary row
+    return np.concatenate(rows).astype(np.float32), len(rows)
+
+
+@pytest.mark.parametrize("cols", [4096, 256, 20000, 37, 1])
+def test_soft_max_non_finite(gpu, cols):
+    # 4096: one workgroup per row in registers; 256: one wave per row;
+    # 20000: streamed passes; 37: the general (unvectorized) kernel; 1: one column
+    x, rows = special_rows(cols, 401 + cols)
+    a = Pair(x, [cols, rows, 1, 1]).to(gpu)
+    o = Pair(np.zeros_like(x), a.ne).to(gpu)
+    assert eh.Kernel().process_event(eh.OpSoftMax(a.pview(), o.pview(mut=True))) == eh.Status.OK, eh.last_error()
+    want = np.zeros_like(x)
+    assert orc.soft_max(a.oview(), orc.view(want, a.ne)) == orc.OK
+    got = o.result()
+    assert np.isnan(want.reshape(rows, cols)[0]).all()  # the rule above, as the oracle states it
+    assert_close_rel(got, want, RTOL, f"soft_max non-finite, {cols} columns")
+    assert (np.isnan(got) == np.isnan(want)).all()
+
+
+@pytest.mark.parametrize("nkv,nq,nh", [(4096, 8, 2), (512, 16, 3), (20000, 6, 2), (37, 6, 2)])
+def test_soft_max_ext_fully_masked_and_non_finite(gpu, nkv, nq, nh):
+    g = np.random.Generator(np.random.PCG64(411 + nkv))
+    x = (g.standard_normal(nkv * nq * nh) * 2).astype(np.float32)
+    xr = x.reshape(nh, nq, nkv)
+    xr[0, 1, nkv // 2] = np.nan        # NaN score
+    xr[1, 2, 0] = np.inf               # +inf score at column 0
+    xr[0, 3, -1] = -np.inf             # -inf score
+    mask = np.zeros((nq, nkv), np.float16)
+    mask[g.random(mask.shape) < 0.4] = np.float16(-np.inf)
+    mask[0, :] = np.float16(-np.inf)   # query row 0 fully masked in every head
+    mask[4, 0] = np.float16(np.inf)    # +inf in the mask
+    mask[5, :] = np.float16(65504.0)   # largest finite half
+    a = Pair(x, [nkv, nq, nh, 1]).to(gpu)
+    m = Pair(mask.reshape(-1).view(np.uint16), [nkv, nq, 1, 1], dtype=orc.F16).to(gpu)
+    o = Pair(np.zeros_like(x), a.ne).to(gpu)
+    scale = float(np.float32(1.0 / np.sqrt(128.0)))
+    assert eh.Kernel().process_event(eh.OpSoftMaxExt(a.pview(), m.pview(), scale, o.pview(mut=True))) == eh.Status.OK, \
+        eh.last_error()
+    want = np.zeros_like(x)
+    assert orc.soft_max_ext(a.oview(), m.oview(), scale, orc.view(want, a.ne)) == orc.OK
+    got = o.result()
+    assert np.isnan(want.reshape(nh, nq, nkv)[:, 0]).all()  # fully masked rows are NaN
+    assert_close_rel(got, want, RTOL, "soft_max_ext fully masked / non-finite")
+    assert (np.isnan(got) == np.isnan(want)).all()
+
+
+@pytest.mark.parametrize("cols", [4096, 256, 20000, 37])
+def test_rms_norm_non_finite(gpu, cols):
+    # x*x overflows f32 (sum +inf, scale 0: finite x -> 0, inf x -> NaN), NaN
+    # and inf elements, an all-zero row (scale 1/sqrt(eps)), subnormals
+    g = np.random.Generator(np.random.PCG64(421 + cols))
+    rows = []
+    def base():
+        return g.standard_normal(cols).astype(np.float32)
+    r = base(); r[cols // 2] = np.float32(1e20); rows.append(r)
+    r = base(); r[0] = np.inf; rows.append(r)
+    r = base(); r[-1] = -np.inf; rows.append(r)
+    r = base(); r[cols // 3] = np.nan; rows.append(r)
+    rows.append(np.zeros(cols, np.float32))
+    rows.append(np.full(cols, np.float32(1e-40)))
+    r = base(); r[:] = np.float32(3e38); rows.append(r)
+    rows.append(base())
+    x = np.concatenate(rows)
+    n = len(rows)
+    for ev, fn, what in ((lambda v, o: eh.OpRmsNorm(v, o, 1e-5), lambda a, o: orc.rms_norm(a, o, 1e-5), "rms_norm"),
+                         (lambda v, o: eh.OpNorm(v, o, 1e-5), lambda a, o: orc.norm(a, o, 1e-5), "norm")):
+        a = Pair(x, [cols, n, 1, 1]).to(gpu)
+        o = Pair(np.zeros_like(x), a.ne).to(gpu)
+        assert eh.Kernel().process_event(ev(a.pview(), o.pview(mut=True))) == eh.Status.OK, eh.last_error()
+        want = np.zeros_like(x)
+        assert fn(a.oview(), orc.view(want, a.ne)) == orc.OK
+        got = o.result()
+        assert_close_rel(got, want, RTOL, f"{what} non-finite, {cols} columns", atol=1e-30)
+        assert (np.isnan(got) == np.isnan(want)).all(), what
