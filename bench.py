@@ -21,6 +21,11 @@ restatement of the reference's CPU path) on a bounded sample of the same
 workload.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--ops a,b] [--no-cpu] [--no-copy] [--pcie] [--no-gather]
+                    [--no-sampler] [--launches N]
+
+--launches N only launches each op (and the calibration copy) N times, for
+rocprofv3 counter runs; config.launch_floor_us is the per-launch time of
+back-to-back launches that move almost no bytes.
 """
 from __future__ import annotations
 
@@ -416,8 +421,9 @@ def sampler_ops(suite, stream, reps):
     config 5's logits: SAMPLER_ROWS sequences of a SAMPLER_VOCAB vocabulary,
     N(0,1), sampled in one batched call.  The call rewrites the logits in
     place (they end as probabilities), so every timed call reads a fresh
-    copy: kernel_us comes from a captured graph of back-to-back calls over
-    `copies` buffers refreshed before each replay, outside the timing.
+    copy: kernel_us comes from back-to-back eager calls over `copies` buffers
+    refreshed before each series, outside the timing (the sampler refuses
+    graph capture: its random_state advances on the host).
     alg_bytes: logits read once and probabilities written once (the outputs
     per row are a few hundred bytes).  The CPU side is timed in
     cpu_baseline (sampler_rows_per_s)."""
@@ -469,11 +475,9 @@ def sampler_ops(suite, stream, reps):
                 if i >= 2:
                     times.append(a.elapsed_time(b))
             call_us = float(np.median(times)) * 1e3
-            gr = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(gr, stream=stream):
-                for i in range(copies):
-                    call(i)
-            stream.synchronize()
+            # back-to-back eager calls (the sampler is not capturable: its
+            # random_state advances on the host); the host enqueues ahead of
+            # the device, so the span between the events is device time
             ktimes = []
             for _ in range(3):
                 refresh()
@@ -481,7 +485,8 @@ def sampler_ops(suite, stream, reps):
                 a = torch.cuda.Event(enable_timing=True)
                 b = torch.cuda.Event(enable_timing=True)
                 a.record(stream)
-                gr.replay()
+                for i in range(copies):
+                    call(i)
                 b.record(stream)
                 b.synchronize()
                 ktimes.append(a.elapsed_time(b) * 1e3 / copies)
@@ -492,7 +497,7 @@ def sampler_ops(suite, stream, reps):
             "GB/s": round(alg / (kus * 1e-6) / 1e9, 1), "frac_of_peak": round(alg / (kus * 1e-6) / 1e9 / PEAK_GBS, 4),
             "rows_per_s": round(rows / (kus * 1e-6), 1),
             "rotation": f"{copies} logits copies refreshed before each replay"}
-        del gr, bufs, reqs
+        del bufs, reqs
         torch.cuda.empty_cache()
     return res
 
@@ -582,6 +587,40 @@ def cpu_baseline(host, budget_s=20.0):
     return total_bytes / total_s / 1e9, per_op, sampler
 
 
+def profile_launches(host, stream, names, count):
+    """Eager launches only, for counter collection: each op `count` times on
+    rotating buffer sets (cold data), one op after another."""
+    import torch
+
+    suite = GpuSuite(host, stream, names)
+    with torch.cuda.stream(stream):
+        for n in names:
+            for i in range(count):
+                suite.launch(n, i)
+            stream.synchronize()
+            print(f"profile: {n} x{count}", flush=True)
+
+
+def launch_floor(suite, capture, timed, reps=200):
+    """Per-launch time of back-to-back dependent launches that do almost no
+    work (OpScale over one float4), replayed from a graph: the fixed cost
+    every launch pays before its bytes move."""
+    torch, eh = suite.torch, suite.eh
+    src = torch.zeros(4, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty(4, dtype=torch.float32, device="cuda:0")
+    lay = eh.Layout.contiguous(eh.DType.F32, [4, 1, 1, 1])
+    ev = eh.OpScale(eh.TensorView(src, lay), eh.TensorViewMut(dst, lay), 1.0)
+
+    def launch(i):
+        if suite.kernel.process_event(ev) != eh.Status.OK:
+            raise RuntimeError(f"launch floor: {eh.last_error()}")
+
+    launch(0)
+    g = capture(lambda: [launch(i) for i in range(reps)])
+    g.replay()
+    return timed(lambda i: g.replay(), 3) / (3 * reps) * 1e3
+
+
 def host_facts():
     model = "unknown"
     try:
@@ -609,6 +648,9 @@ def main():
     ap.add_argument("--pcie", action="store_true", help="also time soft_max_ext with host-resident tensors")
     ap.add_argument("--no-gather", action="store_true", help="skip the get_rows embedding lookups")
     ap.add_argument("--no-sampler", action="store_true", help="skip the emel-logits sampler")
+    ap.add_argument("--launches", type=int, default=0,
+                    help="profiling mode: launch every selected op and the 256 MiB calibration copy this many times "
+                         "(eagerly, cycling buffer sets), then exit without timing; for rocprofv3 --pmc runs")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -630,6 +672,9 @@ def main():
 
     host = config_inputs()
     stream = torch.cuda.Stream()
+    if args.launches > 0:
+        profile_launches(host, stream, names + extra + ["copy"], args.launches)
+        return
     suite = GpuSuite(host, stream, names + extra)
 
     with torch.cuda.stream(stream):
@@ -702,6 +747,15 @@ def main():
         if not args.no_copy:
             copy_ms = copy_ceilings(suite, [info[n][1] for n in names + extra if n != "copy"], args.steps, capture,
                                     timed)
+        floor_us = launch_floor(suite, capture, timed)
+
+    traffic = {}
+    traffic_file = ROOT / "profiles" / "traffic.json"
+    if traffic_file.exists():
+        try:
+            traffic = json.loads(traffic_file.read_text())
+        except ValueError:
+            traffic = {}
 
     def op_entry(n):
         cfg, nbytes = info[n]
@@ -713,6 +767,13 @@ def main():
             cus = copy_ms[nbytes] * 1e3
             e["copy_us"] = round(cus, 3)
             e["frac_of_copy"] = round(cus / us, 4)
+        t = traffic.get(n)
+        if isinstance(t, dict) and "hbm_bytes_per_launch" in t:
+            # rocprof FETCH_SIZE + WRITE_SIZE per launch (scaled by the calibration
+            # copy), its ratio to the algorithmic bytes, and the rate at this time
+            e["traffic"] = t["hbm_bytes_per_launch"]
+            e["traffic_ratio"] = round(t["hbm_bytes_per_launch"] / nbytes, 4)
+            e["traffic_GB/s"] = round(t["hbm_bytes_per_launch"] / (us * 1e-6) / 1e9, 1)
         return e
 
     per_op = {n: op_entry(n) for n in names}
@@ -725,14 +786,9 @@ def main():
     roof = {"kernel": dom, "bound": "hbm", "achieved": measured[dom]["GB/s"], "peak": PEAK_GBS, "unit": "GB/s",
             "frac": round(measured[dom]["GB/s"] / PEAK_GBS, 4), "traffic": None,
             "alg_bytes_per_launch": info[dom][1], "avg_launch_us": measured[dom]["us"]}
-    traffic_file = ROOT / "profiles" / "traffic.json"
-    if traffic_file.exists():
-        try:
-            t = json.loads(traffic_file.read_text()).get(dom)
-            if t:
-                roof["traffic"] = t["hbm_bytes_per_launch"]
-        except (ValueError, KeyError):
-            pass
+    t = traffic.get(dom)
+    if isinstance(t, dict) and "hbm_bytes_per_launch" in t:
+        roof["traffic"] = t["hbm_bytes_per_launch"]
 
     gather = None
     if not args.no_gather and not args.ops:
@@ -777,7 +833,8 @@ def main():
                    "buffer_policy": "step: >=1 GB of other ops moves between two launches of one op; per op: "
                                     "back-to-back launches cycle through >=1 GiB of distinct buffer sets "
                                     "(Infinity Cache is 256 MB)",
-                   "wall_s": round(wall, 3)},
+                   "wall_s": round(wall, 3),
+                   "launch_floor_us": round(floor_us, 3)},
         "per_op": per_op,
         "extra_ops": extra_ops,
         "gather_ops": gather,
