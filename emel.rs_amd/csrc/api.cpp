@@ -770,6 +770,58 @@ emel_status emel_op_gelu(const emel_tensor_view *in, const emel_tensor_view_mut 
     return unary_event(emel::Ew::Gelu, in, out, s);
 }
 
+// The 21 typed unary events, keyed by the UnarySubOp wire code of the
+// formula each applies (unary.rs:72-92, formulas :472-610).  Xielu (17) has
+// no typed event.
+emel_status emel_op_unary_event(uint32_t event, const emel_tensor_view *in, const emel_tensor_view_mut *out,
+                                emel_stream s)
+{
+    emel::Ew fn;
+    switch (event) {
+    case EMEL_UNARY_ABS: fn = emel::Ew::Abs; break;
+    case EMEL_UNARY_SGN: fn = emel::Ew::Sgn; break;
+    case EMEL_UNARY_NEG: fn = emel::Ew::Neg; break;
+    case EMEL_UNARY_STEP: fn = emel::Ew::Step; break;
+    case EMEL_UNARY_TANH: fn = emel::Ew::Tanh; break;
+    case EMEL_UNARY_ELU: fn = emel::Ew::Elu; break;
+    case EMEL_UNARY_RELU: fn = emel::Ew::Relu; break;
+    case EMEL_UNARY_SIGMOID: fn = emel::Ew::Sigmoid; break;
+    case EMEL_UNARY_GELU: fn = emel::Ew::Gelu; break;
+    case EMEL_UNARY_GELU_QUICK: fn = emel::Ew::GeluQuick; break;
+    case EMEL_UNARY_SILU: fn = emel::Ew::Silu; break;
+    case EMEL_UNARY_HARDSWISH: fn = emel::Ew::Hardswish; break;
+    case EMEL_UNARY_HARDSIGMOID: fn = emel::Ew::Hardsigmoid; break;
+    case EMEL_UNARY_EXP: fn = emel::Ew::Exp; break;
+    case EMEL_UNARY_EXPM1: fn = emel::Ew::Expm1; break;
+    case EMEL_UNARY_SOFTPLUS: fn = emel::Ew::Softplus; break;
+    case EMEL_UNARY_GELU_ERF: fn = emel::Ew::GeluErf; break;
+    case EMEL_UNARY_FLOOR: fn = emel::Ew::Floor; break;
+    case EMEL_UNARY_CEIL: fn = emel::Ew::Ceil; break;
+    case EMEL_UNARY_ROUND: fn = emel::Ew::Round; break;
+    case EMEL_UNARY_TRUNC: fn = emel::Ew::Trunc; break;
+    default: return fail(EMEL_ERR_UNEXPECTED_EVENT, "no typed unary event has this code");
+    }
+    return unary_event(fn, in, out, s);
+}
+
+// reductions::OpLog / OpSin / OpCos (reductions.rs:45-90, guards :508-517,
+// effects :640-668): views valid, equal element counts, elementwise by
+// ordinal; ReductionError's InvalidView / ShapeMismatch.
+emel_status emel_op_log(const emel_tensor_view *in, const emel_tensor_view_mut *out, emel_stream s)
+{
+    return unary_event(emel::Ew::Log, in, out, s);
+}
+
+emel_status emel_op_sin(const emel_tensor_view *in, const emel_tensor_view_mut *out, emel_stream s)
+{
+    return unary_event(emel::Ew::Sin, in, out, s);
+}
+
+emel_status emel_op_cos(const emel_tensor_view *in, const emel_tensor_view_mut *out, emel_stream s)
+{
+    return unary_event(emel::Ew::Cos, in, out, s);
+}
+
 emel_status emel_op_swiglu(const emel_tensor_view *gate, const emel_tensor_view *up, const emel_tensor_view_mut *out,
                            emel_stream stream)
 {
@@ -1720,7 +1772,7 @@ bool unary_subop_routed(uint32_t s)
 
 enum class Route {
     None, Dup, Binary, Scalar, Clamp, SiluBack, Cumsum, Repeat, RepeatBack, Concat, Diag, DiagMask, SoftMaxBack,
-    RmsNormBack, L2Norm, CountEqual, Fill, Arange, MulMatF32, MulMatF16, MulMatArgmax, Power, Unsupported, Reduce,
+    RmsNormBack, L2Norm, CountEqual, Fill, Arange, MulMatF32, MulMatF16, MulMatArgmax, Power, Math, Reduce,
     SoftMax, Norm, Unary
 };
 
@@ -1757,7 +1809,7 @@ Route gen_route(const GenReq &q, int &concat_axis)
         return matmul_f16_valid(q) ? Route::MulMatF16 : Route::None;
     case kMulMatArgmax: return matmul_argmax_valid(q) ? Route::MulMatArgmax : Route::None;
     case kSqr: case kSqrt: return pair_valid(q) ? Route::Power : Route::None;
-    case kLog: case kSin: case kCos: return pair_valid(q) ? Route::Unsupported : Route::None;
+    case kLog: case kSin: case kCos: return pair_valid(q) ? Route::Math : Route::None;
     case kSum: case kMean: case kArgmax: return reduce_valid(q) ? Route::Reduce : Route::None;
     case kSoftMax: return pair_valid(q) ? Route::SoftMax : Route::None;
     case kNorm: case kRmsNorm: return norm_valid(q) ? Route::Norm : Route::None;
@@ -1789,8 +1841,8 @@ bool alias_ok(Route r)
     switch (r) {
     case Route::Dup: case Route::Binary: case Route::Scalar: case Route::Clamp: case Route::SiluBack:
     case Route::Cumsum: case Route::Repeat: case Route::RepeatBack: case Route::DiagMask: case Route::SoftMaxBack:
-    case Route::RmsNormBack: case Route::L2Norm: case Route::Power: case Route::SoftMax: case Route::Norm:
-    case Route::Unary:
+    case Route::RmsNormBack: case Route::L2Norm: case Route::Power: case Route::Math: case Route::SoftMax:
+    case Route::Norm: case Route::Unary:
         return true;
     default:
         return false;
@@ -1861,8 +1913,6 @@ emel::Ew unary_generic_fn(uint32_t s)
 emel_status gen_execute(const GenReq &q, Route route, int concat_axis, emel_stream stream)
 {
     const uint32_t op = q.r.operation;
-    if (route == Route::Unsupported)
-        return fail(EMEL_ERR_UNSUPPORTED_OPERATION, "log/sin/cos have no bit-exact device replica");
     const GView &dst = *q.d;
     const emel_tensor_view_mut &dmut = *q.r.dst;
     const GView *used[3] = {nullptr, nullptr, nullptr};
@@ -1927,6 +1977,9 @@ emel_status gen_execute(const GenReq &q, Route route, int concat_axis, emel_stre
     case Route::Power:
         return elementwise(op == kSqr ? emel::Ew::Sqr : emel::Ew::Sqrt, q.s0, pair_addr(*q.s0, dmut), nullptr,
                            emel::Addr::SameCoords, &dmut, 0.0f, stream);
+    case Route::Math: // f32::ln / sin / cos (generic.rs), the glibc replicas
+        return elementwise(op == kLog ? emel::Ew::Log : op == kSin ? emel::Ew::Sin : emel::Ew::Cos, q.s0,
+                           pair_addr(*q.s0, dmut), nullptr, emel::Addr::SameCoords, &dmut, 0.0f, stream);
     case Route::Unary:
         return elementwise(unary_generic_fn(q.r.unary_subop), q.s0, pair_addr(*q.s0, dmut), nullptr,
                            emel::Addr::SameCoords, &dmut, 0.0f, stream);

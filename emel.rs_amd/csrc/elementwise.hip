@@ -1,8 +1,9 @@
 // elementwise.hip -- gfx950 kernels for the elementwise family:
 // equal-count binary add/sub/mul/div (binary.rs:383-424), row broadcast
 // (broadcast.rs:352-390), 4-D modulo broadcast (OpRepeat + binary,
-// generic.rs:1641-1665), unary abs/neg/tanh/elu/relu/sigmoid/gelu/silu/exp
-// (unary.rs:472-606), scale (activation.rs:366-377), fused SwiGLU, the six
+// generic.rs:1641-1665), the 21 typed unary events (unary.rs:472-610),
+// log / sin / cos (reductions.rs:640-668), scale (activation.rs:366-377),
+// fused SwiGLU, the six
 // OpGlu gates (glu.rs:103-141, :258-270), copy (event.rs:133-165) and square
 // / square root (power.rs:315-360).
 //
@@ -171,6 +172,33 @@ __device__ __forceinline__ float silu_back(float x, float grad, const ExpCtx &t)
     return grad * (sg * (1.0f + x * (1.0f - sg)));
 }
 EMEL_FN(SiluBack, true, true, silu_back(a, b, t))
+// The remaining typed unary events (unary.rs:472-610), every operation
+// rounded separately as the reference writes it.
+// f32::signum: +-1 with the sign of a (both zeros included), NaN for NaN.
+EMEL_FN(Sgn, false, false, a != a ? a : __builtin_copysignf(1.0f, a))
+EMEL_FN(Step, false, false, a > 0.0f ? 1.0f : 0.0f)
+EMEL_FN(GeluQuick, false, false, 0.5f * a * (1.0f + emel_tanhf(0.7978846f * a * (1.0f + 0.044715f * a * a))))
+// (x + 3).clamp(0, 6): NaN passes through
+__device__ __forceinline__ float clamp06(float v)
+{
+    v = v < 0.0f ? 0.0f : v;
+    return v > 6.0f ? 6.0f : v;
+}
+EMEL_FN(Hardswish, false, false, a * clamp06(a + 3.0f) / 6.0f)
+EMEL_FN(Hardsigmoid, false, false, clamp06(a + 3.0f) / 6.0f)
+EMEL_FN(Expm1, false, false, emel_expm1f(a))
+// exp(x).ln_1p(): two glibc calls, each rounded to f32
+EMEL_FN(Softplus, true, false, emel_log1pf(emel_expf(a, t.tab, t.c)))
+EMEL_FN(GeluErf, true, false, glu_gelu_erf(a, t))
+EMEL_FN(Floor, false, false, __builtin_floorf(a))
+EMEL_FN(Ceil, false, false, __builtin_ceilf(a))
+// f32::round: halfway cases away from zero
+EMEL_FN(Round, false, false, __builtin_roundf(a))
+EMEL_FN(Trunc, false, false, __builtin_truncf(a))
+// reductions.rs:640-668: f32::ln / sin / cos, glibc logf / sinf / cosf
+EMEL_FN(Log, false, false, emel_logf(a))
+EMEL_FN(Sin, false, false, emel_sinf(a))
+EMEL_FN(Cos, false, false, emel_cosf(a))
 #undef EMEL_FN
 
 template <Ew OP>
@@ -611,6 +639,21 @@ hipError_t launch_elementwise(const EwArgs &args, hipStream_t stream)
     case Ew::Clamp: return launch_op<Ew::Clamp>(args, stream);
     case Ew::GeluGeneric: return launch_op<Ew::GeluGeneric>(args, stream);
     case Ew::SiluBack: return launch_op<Ew::SiluBack>(args, stream);
+    case Ew::Sgn: return launch_op<Ew::Sgn>(args, stream);
+    case Ew::Step: return launch_op<Ew::Step>(args, stream);
+    case Ew::GeluQuick: return launch_op<Ew::GeluQuick>(args, stream);
+    case Ew::Hardswish: return launch_op<Ew::Hardswish>(args, stream);
+    case Ew::Hardsigmoid: return launch_op<Ew::Hardsigmoid>(args, stream);
+    case Ew::Expm1: return launch_op<Ew::Expm1>(args, stream);
+    case Ew::Softplus: return launch_op<Ew::Softplus>(args, stream);
+    case Ew::GeluErf: return launch_op<Ew::GeluErf>(args, stream);
+    case Ew::Floor: return launch_op<Ew::Floor>(args, stream);
+    case Ew::Ceil: return launch_op<Ew::Ceil>(args, stream);
+    case Ew::Round: return launch_op<Ew::Round>(args, stream);
+    case Ew::Trunc: return launch_op<Ew::Trunc>(args, stream);
+    case Ew::Log: return launch_op<Ew::Log>(args, stream);
+    case Ew::Sin: return launch_op<Ew::Sin>(args, stream);
+    case Ew::Cos: return launch_op<Ew::Cos>(args, stream);
     }
     return hipErrorInvalidValue;
 }

@@ -26,7 +26,10 @@ enum class Ew : uint32_t {
     Swiglu,                                                        // fused
     GluRe, GluGe, GluSwi, GluSwiOai, GluGeErf, GluGeQuick,        // OpGlu: a = values, b = gates
     Copy, Sqr, Sqrt,                                               // dup and power.rs
-    Add1, LeakyRelu, Clamp, GeluGeneric, SiluBack                  // generic envelope (generic.rs)
+    Add1, LeakyRelu, Clamp, GeluGeneric, SiluBack,                 // generic envelope (generic.rs)
+    Sgn, Step, GeluQuick, Hardswish, Hardsigmoid, Expm1, Softplus,  // the other typed unary events (unary.rs)
+    GeluErf, Floor, Ceil, Round, Trunc,
+    Log, Sin, Cos                                                  // reductions.rs OpLog / OpSin / OpCos
 };
 
 // The scalar parameters an elementwise functor reads: x is Scale's factor,

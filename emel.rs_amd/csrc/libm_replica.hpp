@@ -417,4 +417,196 @@ __host__ __device__ __forceinline__ float gelu_finish(float x, float q, uint32_t
     return y;
 }
 
+// ---- sinf / cosf ---------------------------------------------------------------
+//
+// ARM optimized-routines sinf / cosf (math/sinf.c, math/cosf.c and
+// math/sincosf.h; in glibc since 2.28, whose x86_64 build selects a variant
+// compiled with FMA, so every a + b*c of the source is one fused operation
+// here).  The argument is widened to double.  |x| < 0x1p-12 returns x (sin)
+// or 1 (cos); |x| below 0x1p-1 <= pi/4 (the top-12-bit test) evaluates the
+// polynomial directly; |x| < 120 reduces by pi/2 with one fused
+// multiply-subtract (the quadrant from a 2^24-scaled 2/pi product and an
+// integer shift); larger finite |x| reduce with a 4/pi table of 192 bits and
+// a 32x96-bit integer product; infinities and NaN give NaN.  The quadrant
+// selects the sine or cosine polynomial and, through a sign table and a
+// second coefficient set with the cosine negated, the result's sign.
+struct SinCosCoeffs {
+    double c0, c1, c2, c3, c4; // cosine: c0 + c1 x^2 + ... (c0 = +1 or -1)
+    double s1, s2, s3;         // sine: x + s1 x^3 + s2 x^5 + s3 x^7
+};
+__host__ __device__ __forceinline__ SinCosCoeffs sincos_coeffs(bool negated_cos)
+{
+    const double m = negated_cos ? -1.0 : 1.0;
+    return SinCosCoeffs{m * 0x1p0, m * -0x1.ffffffd0c621cp-2, m * 0x1.55553e1068f19p-5, m * -0x1.6c087e89a359dp-10,
+                        m * 0x1.99343027bf8c3p-16, -0x1.555545995a603p-3, 0x1.1107605230bc4p-7,
+                        -0x1.994eb3774cf24p-13};
+}
+
+// 4/pi to 192 bits, 8 new bits per entry (entry i holds bits 8i-24 .. 8i+7).
+static constexpr uint32_t kInvPio4[24] = {
+    0xa2u,       0xa2f9u,     0xa2f983u,   0xa2f9836eu, 0xf9836e4eu, 0x836e4e44u, 0x6e4e4415u, 0x4e441529u,
+    0x441529fcu, 0x1529fc27u, 0x29fc2757u, 0xfc2757d1u, 0x2757d1f5u, 0x57d1f534u, 0xd1f534ddu, 0xf534ddc0u,
+    0x34ddc0dbu, 0xddc0db62u, 0xc0db6295u, 0xdb629599u, 0x6295993cu, 0x95993c43u, 0x993c4390u, 0x3c439041u,
+};
+
+// sinf_poly: the sine polynomial for an even quadrant, the cosine one for an
+// odd quadrant; x2 = x*x.
+__host__ __device__ __forceinline__ float sincosf_poly(double x, double x2, const SinCosCoeffs &p, int n)
+{
+    if ((n & 1) == 0) {
+        const double x3 = x * x2;
+        const double s1 = __builtin_fma(x2, p.s3, p.s2);
+        const double x7 = x3 * x2;
+        const double s = __builtin_fma(x3, p.s1, x);
+        return static_cast<float>(__builtin_fma(x7, s1, s));
+    }
+    const double x4 = x2 * x2;
+    const double c2 = __builtin_fma(x2, p.c4, p.c3);
+    const double c1 = __builtin_fma(x2, p.c1, p.c0);
+    const double x6 = x4 * x2;
+    const double c = __builtin_fma(x4, p.c2, c1);
+    return static_cast<float>(__builtin_fma(x6, c2, c));
+}
+
+__host__ __device__ __forceinline__ uint32_t abstop12(float x) { return (f32_to_bits(x) >> 20) & 0x7ffu; }
+
+// |x| < 120: x - n*pi/2 with n the nearest quadrant (2/pi prescaled by 2^24).
+__host__ __device__ __forceinline__ double sincosf_reduce_fast(double x, int &n)
+{
+    const double r = x * 0x1.45F306DC9C883p+23;
+    n = (static_cast<int32_t>(r) + 0x800000) >> 24;
+    return __builtin_fma(-static_cast<double>(n), 0x1.921FB54442D18p0, x);
+}
+
+// Finite |x| >= 120 (bits xi, sign ignored): the exact 2.62 fixed-point
+// product with 4/pi, rounded to the nearest quadrant.
+__host__ __device__ __forceinline__ double sincosf_reduce_large(uint32_t xi, int &np)
+{
+    const uint32_t *arr = &kInvPio4[(xi >> 26) & 15u];
+    const int shift = static_cast<int>((xi >> 23) & 7u);
+    xi = (xi & 0xffffffu) | 0x800000u;
+    xi <<= shift;
+    uint64_t res0 = static_cast<uint32_t>(xi * arr[0]); // low 32 bits only
+    const uint64_t res1 = static_cast<uint64_t>(xi) * arr[4];
+    const uint64_t res2 = static_cast<uint64_t>(xi) * arr[8];
+    res0 = (res2 >> 32) | (res0 << 32);
+    res0 += res1;
+    const uint64_t n = (res0 + (uint64_t{1} << 61)) >> 62;
+    res0 -= n << 62;
+    np = static_cast<int>(n);
+    return static_cast<double>(static_cast<int64_t>(res0)) * 0x1.921FB54442D18p-62; // 2 pi 2^-64
+}
+
+// want_cos selects cosf; sinf otherwise.
+__host__ __device__ __forceinline__ float emel_sincosf(float y, bool want_cos)
+{
+    // the quadrant sign table {1, -1, -1, 1}, without an indexed array
+    auto quadrant_sign = [](int q) { return ((q + 1) & 2) ? -1.0 : 1.0; };
+    const uint32_t top = abstop12(y);
+    double x = static_cast<double>(y);
+    if (top < abstop12(0x1.921FB6p-1f)) {
+        if (top < abstop12(0x1p-12f)) return want_cos ? 1.0f : y;
+        return sincosf_poly(x, x * x, sincos_coeffs(false), want_cos ? 1 : 0);
+    }
+    if (top < abstop12(120.0f)) {
+        int n;
+        x = sincosf_reduce_fast(x, n);
+        const double s = quadrant_sign(n);
+        return sincosf_poly(x * s, x * x, sincos_coeffs((n & 2) != 0), want_cos ? n ^ 1 : n);
+    }
+    if (top < abstop12(__builtin_inff())) {
+        const uint32_t xi = f32_to_bits(y);
+        const int sign = static_cast<int>(xi >> 31);
+        int n;
+        x = sincosf_reduce_large(xi, n);
+        const double s = quadrant_sign(n + sign);
+        return sincosf_poly(x * s, x * x, sincos_coeffs(((n + sign) & 2) != 0), want_cos ? n ^ 1 : n);
+    }
+    return (y - y) / (y - y); // NaN for infinities and NaN
+}
+
+__host__ __device__ __forceinline__ float emel_sinf(float x) { return emel_sincosf(x, false); }
+__host__ __device__ __forceinline__ float emel_cosf(float x) { return emel_sincosf(x, true); }
+
+// ---- log1pf --------------------------------------------------------------------
+//
+// fdlibm s_log1pf.c (glibc sysdeps/ieee754/flt-32, not contracted): 1 + x =
+// 2^k (1 + f) with a correction term c for the rounding of 1 + x, then
+// log(1 + f) = f - hfsq + s (hfsq + R(s^2)), s = f / (2 + f), in float.
+__host__ __device__ __forceinline__ float emel_log1pf(float x)
+{
+    constexpr float kLn2Hi = 6.9313812256e-01f; // 0x3f317180
+    constexpr float kLn2Lo = 9.0580006145e-06f; // 0x3717f7d1
+    constexpr float kTwo25 = 3.355443200e+07f;  // 0x4c000000
+    constexpr float kLp1 = 6.6666668653e-01f;   // 0x3f2aaaab
+    constexpr float kLp2 = 4.0000000596e-01f;   // 0x3ecccccd
+    constexpr float kLp3 = 2.8571429849e-01f;   // 0x3e924925
+    constexpr float kLp4 = 2.2222198546e-01f;   // 0x3e638e29
+    constexpr float kLp5 = 1.8183572590e-01f;   // 0x3e3a3325
+    constexpr float kLp6 = 1.5313838422e-01f;   // 0x3e1cd04f
+    constexpr float kLp7 = 1.4798198640e-01f;   // 0x3e178897
+    const int32_t hx = static_cast<int32_t>(f32_to_bits(x));
+    const int32_t ax = hx & 0x7fffffff;
+    int32_t k = 1, hu = 0;
+    float f = 0.0f, c = 0.0f;
+    if (hx < 0x3ed413d7) {       // x < 0.41422
+        if (ax >= 0x3f800000) {  // x <= -1
+            if (x == -1.0f) return -kTwo25 / (x - x); // -inf
+            return (x - x) / (x - x);                  // NaN
+        }
+        if (ax < 0x31000000) {   // |x| < 2^-29
+            if (ax < 0x24800000) return x;
+            return x - x * x * 0.5f;
+        }
+        if (hx > 0 || hx <= static_cast<int32_t>(0xbe95f61fu)) { // -0.2929 < x < 0.41422
+            k = 0;
+            f = x;
+            hu = 1;
+        }
+    } else if (hx >= 0x7f800000) {
+        return x + x;
+    }
+    if (k != 0) {
+        float u;
+        if (hx < 0x5a000000) {
+            u = 1.0f + x;
+            hu = static_cast<int32_t>(f32_to_bits(u));
+            k = (hu >> 23) - 127;
+            c = (k > 0) ? 1.0f - (u - x) : x - (u - 1.0f); // correction term
+            c /= u;
+        } else {
+            u = x;
+            hu = static_cast<int32_t>(f32_to_bits(u));
+            k = (hu >> 23) - 127;
+            c = 0.0f;
+        }
+        hu &= 0x007fffff;
+        if (hu < 0x3504f7) {
+            u = bits_to_f32(static_cast<uint32_t>(hu) | 0x3f800000u); // normalize u
+        } else {
+            k += 1;
+            u = bits_to_f32(static_cast<uint32_t>(hu) | 0x3f000000u); // normalize u/2
+            hu = (0x00800000 - hu) >> 2;
+        }
+        f = u - 1.0f;
+    }
+    const float hfsq = 0.5f * f * f;
+    const float fk = static_cast<float>(k);
+    if (hu == 0) { // |f| < 2^-20
+        if (f == 0.0f) {
+            if (k == 0) return 0.0f;
+            c += fk * kLn2Lo;
+            return fk * kLn2Hi + c;
+        }
+        const float R = hfsq * (1.0f - 0.66666666666666666f * f);
+        if (k == 0) return f - R;
+        return fk * kLn2Hi - ((R - (fk * kLn2Lo + c)) - f);
+    }
+    const float s = f / (2.0f + f);
+    const float z = s * s;
+    const float R = z * (kLp1 + z * (kLp2 + z * (kLp3 + z * (kLp4 + z * (kLp5 + z * (kLp6 + z * kLp7))))));
+    if (k == 0) return f - (hfsq - s * (hfsq + R));
+    return fk * kLn2Hi - ((hfsq - (s * (hfsq + R) + (fk * kLn2Lo + c))) - f);
+}
+
 } // namespace emel

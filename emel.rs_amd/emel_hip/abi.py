@@ -308,6 +308,10 @@ SIGNATURES = {
     "emel_op_mean": [_V, _V, _S],
     "emel_op_argmax": [_V, _V, _S],
     "emel_op_argmax_rows": [_V, _V, _S],
+    "emel_op_unary_event": [ctypes.c_uint32, _V, _V, _S],
+    "emel_op_log": [_V, _V, _S],
+    "emel_op_sin": [_V, _V, _S],
+    "emel_op_cos": [_V, _V, _S],
     "emel_op_argmax_rows_no_alloc": [_V, _V, _S],
     "emel_validate_view": [_V, ctypes.c_int32],
     "emel_validate_normalization_view": [_V],

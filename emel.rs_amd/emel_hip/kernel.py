@@ -134,6 +134,81 @@ class OpSilu:
 
 
 @dataclass
+class OpUnaryEvent:
+    """One of the 21 typed unary events (unary.rs:72-92), keyed by the
+    UnarySubOp code of its formula; the named classes below build it."""
+
+    event: int
+    input: TensorView
+    output: TensorViewMut
+
+    def _call(self, lib, s):
+        return lib.emel_op_unary_event(int(self.event), _p(self.input), _p(self.output), s)
+
+
+def _typed_unary(name, code):
+    def make(input, output):
+        return OpUnaryEvent(code, input, output)
+    make.__name__ = name
+    make.__doc__ = f"unary::{name}::new(input, output) (unary.rs:72-92): UnarySubOp {code.name}."
+    return make
+
+
+OpAbs = _typed_unary("OpAbs", UnarySubOp.ABS)
+OpSgn = _typed_unary("OpSgn", UnarySubOp.SGN)
+OpNeg = _typed_unary("OpNeg", UnarySubOp.NEG)
+OpStep = _typed_unary("OpStep", UnarySubOp.STEP)
+OpTanh = _typed_unary("OpTanh", UnarySubOp.TANH)
+OpElu = _typed_unary("OpElu", UnarySubOp.ELU)
+OpRelu = _typed_unary("OpRelu", UnarySubOp.RELU)
+OpSigmoid = _typed_unary("OpSigmoid", UnarySubOp.SIGMOID)
+OpGeluQuick = _typed_unary("OpGeluQuick", UnarySubOp.GELU_QUICK)
+OpHardswish = _typed_unary("OpHardswish", UnarySubOp.HARDSWISH)
+OpHardsigmoid = _typed_unary("OpHardsigmoid", UnarySubOp.HARDSIGMOID)
+OpExp = _typed_unary("OpExp", UnarySubOp.EXP)
+OpExpm1 = _typed_unary("OpExpm1", UnarySubOp.EXPM1)
+OpSoftplus = _typed_unary("OpSoftplus", UnarySubOp.SOFTPLUS)
+OpGeluErf = _typed_unary("OpGeluErf", UnarySubOp.GELU_ERF)
+OpFloor = _typed_unary("OpFloor", UnarySubOp.FLOOR)
+OpCeil = _typed_unary("OpCeil", UnarySubOp.CEIL)
+OpRound = _typed_unary("OpRound", UnarySubOp.ROUND)
+OpTrunc = _typed_unary("OpTrunc", UnarySubOp.TRUNC)
+
+
+@dataclass
+class OpLog:
+    """reductions::OpLog::new(src, dst) (reductions.rs:45-58, :640-648)."""
+
+    src: TensorView
+    dst: TensorViewMut
+
+    def _call(self, lib, s):
+        return lib.emel_op_log(_p(self.src), _p(self.dst), s)
+
+
+@dataclass
+class OpSin:
+    """reductions::OpSin::new(src, dst) (reductions.rs:60-73, :650-658)."""
+
+    src: TensorView
+    dst: TensorViewMut
+
+    def _call(self, lib, s):
+        return lib.emel_op_sin(_p(self.src), _p(self.dst), s)
+
+
+@dataclass
+class OpCos:
+    """reductions::OpCos::new(src, dst) (reductions.rs:75-88, :660-668)."""
+
+    src: TensorView
+    dst: TensorViewMut
+
+    def _call(self, lib, s):
+        return lib.emel_op_cos(_p(self.src), _p(self.dst), s)
+
+
+@dataclass
 class OpGelu:
     """unary::OpGelu::new(input, output) (unary.rs:80)."""
 

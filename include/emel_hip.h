@@ -73,17 +73,33 @@ typedef enum emel_dtype {
     EMEL_DTYPE_I32 = 26
 } emel_dtype;
 
-/* Unary wire subop codes, UnarySubOp (unary.rs:101-146). */
+/* Unary wire subop codes, UnarySubOp (unary.rs:101-146).  OpUnary and the
+ * generic envelope accept eight of them (abs, neg, tanh, elu, relu, gelu,
+ * silu, exp); emel_op_unary_event takes every code that has a typed event
+ * (all but XIELU). */
 typedef enum emel_unary_subop {
     EMEL_UNARY_ABS = 0,
+    EMEL_UNARY_SGN = 1,
     EMEL_UNARY_NEG = 2,
+    EMEL_UNARY_STEP = 3,
     EMEL_UNARY_TANH = 4,
     EMEL_UNARY_ELU = 5,
     EMEL_UNARY_RELU = 6,
     EMEL_UNARY_SIGMOID = 7,
     EMEL_UNARY_GELU = 8,
+    EMEL_UNARY_GELU_QUICK = 9,
     EMEL_UNARY_SILU = 10,
-    EMEL_UNARY_EXP = 13
+    EMEL_UNARY_HARDSWISH = 11,
+    EMEL_UNARY_HARDSIGMOID = 12,
+    EMEL_UNARY_EXP = 13,
+    EMEL_UNARY_EXPM1 = 14,
+    EMEL_UNARY_SOFTPLUS = 15,
+    EMEL_UNARY_GELU_ERF = 16,
+    EMEL_UNARY_XIELU = 17,
+    EMEL_UNARY_FLOOR = 18,
+    EMEL_UNARY_CEIL = 19,
+    EMEL_UNARY_ROUND = 20,
+    EMEL_UNARY_TRUNC = 21
 } emel_unary_subop;
 
 /* GLU wire subop codes, GluSubOp (glu.rs:22-37). */
@@ -194,6 +210,25 @@ emel_status emel_op_silu(const emel_tensor_view *in, const emel_tensor_view_mut 
 /* unary::OpGelu::new(input, output) (unary.rs:80, formula :522-586):
  * fp16-rounded tanh approximation with tanhf bit-identical to glibc's. */
 emel_status emel_op_gelu(const emel_tensor_view *in, const emel_tensor_view_mut *out, emel_stream stream);
+/* The typed unary events unary::{OpAbs, OpSgn, OpNeg, OpStep, OpTanh, OpElu,
+ * OpRelu, OpSigmoid, OpGelu, OpGeluQuick, OpSilu, OpHardswish,
+ * OpHardsigmoid, OpExp, OpExpm1, OpSoftplus, OpGeluErf, OpFloor, OpCeil,
+ * OpRound, OpTrunc}::new(input, output) (unary.rs:72-92), selected by the
+ * UnarySubOp code of their formula (unary.rs:472-610): event is an
+ * emel_unary_subop other than EMEL_UNARY_XIELU, which has no typed event
+ * (EMEL_ERR_UNEXPECTED_EVENT).  Guards (impl_unary_context, unary.rs:702-728):
+ * both views valid, else INVALID_VIEW; equal element counts, else
+ * SHAPE_MISMATCH; applied by logical ordinal.  exp, expm1, tanh and ln_1p are
+ * bit-identical to glibc's expf, expm1f, tanhf and log1pf. */
+emel_status emel_op_unary_event(uint32_t event, const emel_tensor_view *in, const emel_tensor_view_mut *out,
+                                emel_stream stream);
+/* reductions::{OpLog, OpSin, OpCos}::new(src, dst) (reductions.rs:45-90,
+ * guards :508-517, effects :640-668): f32::ln / sin / cos elementwise by
+ * ordinal, bit-identical to glibc's logf / sinf / cosf.  Views valid, else
+ * INVALID_VIEW; equal element counts, else SHAPE_MISMATCH. */
+emel_status emel_op_log(const emel_tensor_view *in, const emel_tensor_view_mut *out, emel_stream stream);
+emel_status emel_op_sin(const emel_tensor_view *in, const emel_tensor_view_mut *out, emel_stream stream);
+emel_status emel_op_cos(const emel_tensor_view *in, const emel_tensor_view_mut *out, emel_stream stream);
 /* Fused SwiGLU: the reference chain OpSilu(gate) then equal-count OpMul by
  * up (unary.rs:595-600, binary.rs:411-424) in one pass, keeping both f32
  * roundings.  The three views have identical shapes. */

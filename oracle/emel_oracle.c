@@ -251,8 +251,13 @@ float orc_fp16_to_f32(uint16_t h)
 /* ------------------------------------------------------------------ */
 
 /* Wire subop codes, unary.rs:101-146. */
-enum { SUB_ABS = 0, SUB_NEG = 2, SUB_TANH = 4, SUB_ELU = 5, SUB_RELU = 6, SUB_SIGMOID = 7,
-       SUB_GELU = 8, SUB_SILU = 10, SUB_EXP = 13 };
+enum { SUB_ABS = 0, SUB_SGN = 1, SUB_NEG = 2, SUB_STEP = 3, SUB_TANH = 4, SUB_ELU = 5, SUB_RELU = 6,
+       SUB_SIGMOID = 7, SUB_GELU = 8, SUB_GELU_QUICK = 9, SUB_SILU = 10, SUB_HARDSWISH = 11,
+       SUB_HARDSIGMOID = 12, SUB_EXP = 13, SUB_EXPM1 = 14, SUB_SOFTPLUS = 15, SUB_GELU_ERF = 16,
+       SUB_XIELU = 17, SUB_FLOOR = 18, SUB_CEIL = 19, SUB_ROUND = 20, SUB_TRUNC = 21 };
+/* Not wire codes: the reductions.rs elementwise events, routed through the
+ * same loop. */
+enum { MATH_LOG = 100, MATH_SIN = 101, MATH_COS = 102 };
 
 /* SiluFormula, unary.rs:595-600: value / (1 + exp(-value)). */
 float orc_silu(float x) { return x / (1.0f + expf(-x)); }
@@ -267,27 +272,62 @@ float orc_gelu(float value)
     return orc_fp16_to_f32(orc_fp32_to_fp16(a));
 }
 
+/* f32::clamp(self, 0.0, 6.0): below min -> min, then above max -> max; NaN
+ * passes through. */
+static float clamp06(float v)
+{
+    if (v < 0.0f) v = 0.0f;
+    if (v > 6.0f) v = 6.0f;
+    return v;
+}
+
+/* GeluErfFormula, unary.rs:567-581 (Abramowitz-Stegun erf, separate
+ * roundings). */
+static float gelu_erf(float value)
+{
+    const float sign = value < 0.0f ? -1.0f : 1.0f;
+    const float x = fabsf(value) / 1.41421356237309504880f; /* core::f32::consts::SQRT_2 */
+    const float t = 1.0f / (1.0f + 0.3275911f * x);
+    const float polynomial =
+        (((((1.0614054f * t - 1.4531521f) * t) + 1.4214138f) * t - 0.28449672f) * t + 0.2548296f) * t;
+    const float erf = sign * (1.0f - polynomial * expf(-x * x));
+    return 0.5f * value * (1.0f + erf);
+}
+
 static float apply_unary(int subop, float x)
 {
-    switch (subop) { /* unary.rs:472-520, 595-606 */
+    switch (subop) { /* unary.rs:472-610 */
     case SUB_ABS: return fabsf(x);
+    case SUB_SGN: return isnan(x) ? x : copysignf(1.0f, x); /* f32::signum: +-0 -> +-1 */
     case SUB_NEG: return -x;
+    case SUB_STEP: return x > 0.0f ? 1.0f : 0.0f;
     case SUB_TANH: return tanhf(x);
     case SUB_ELU: return x >= 0.0f ? x : expm1f(x);
-    case SUB_RELU: return fmaxf(x, 0.0f); /* f32::max: NaN -> 0; the sign of max(-0, +0) is unpinned by the reference, glibc gives +0 */
+    case SUB_RELU: return rust_maxf(x, 0.0f); /* f32::max: any NaN -> 0; the sign of max(-0, +0) is unpinned by the reference, +0 here */
     case SUB_SIGMOID: return 1.0f / (1.0f + expf(-x));
     case SUB_GELU: return orc_gelu(x);
+    case SUB_GELU_QUICK: return 0.5f * x * (1.0f + tanhf(0.7978846f * x * (1.0f + 0.044715f * x * x)));
     case SUB_SILU: return orc_silu(x);
+    case SUB_HARDSWISH: return x * clamp06(x + 3.0f) / 6.0f;
+    case SUB_HARDSIGMOID: return clamp06(x + 3.0f) / 6.0f;
+    case SUB_EXPM1: return expm1f(x);
+    case SUB_SOFTPLUS: return log1pf(expf(x)); /* value.exp().ln_1p() */
+    case SUB_GELU_ERF: return gelu_erf(x);
+    case SUB_FLOOR: return floorf(x);
+    case SUB_CEIL: return ceilf(x);
+    case SUB_ROUND: return roundf(x); /* halfway away from zero */
+    case SUB_TRUNC: return truncf(x);
+    case MATH_LOG: return logf(x); /* reductions.rs:640-668 */
+    case MATH_SIN: return sinf(x);
+    case MATH_COS: return cosf(x);
     default: return expf(x);
     }
 }
 
-/* Subops the dedicated events implement in this restatement. */
+/* Codes with a typed event (unary.rs:72-92): every wire code but XIELU. */
 static int unary_known(int subop)
 {
-    return subop == SUB_ABS || subop == SUB_NEG || subop == SUB_TANH || subop == SUB_ELU ||
-           subop == SUB_RELU || subop == SUB_SIGMOID || subop == SUB_GELU || subop == SUB_SILU ||
-           subop == SUB_EXP;
+    return subop >= SUB_ABS && subop <= SUB_TRUNC && subop != SUB_XIELU;
 }
 
 static void unary_execute(int subop, const orc_view *in, const orc_view *out)
@@ -307,6 +347,20 @@ int orc_op_unary_event(int subop, const orc_view *in, const orc_view *out)
     unary_execute(subop, in, out);
     return ORC_OK;
 }
+
+/* reductions::OpLog / OpSin / OpCos (reductions.rs:45-90): guard_unary_*
+ * (:508-517) -- both views valid, else InvalidView; equal counts, else
+ * ShapeMismatch -- then f32::ln / sin / cos by ordinal (:640-668). */
+static int math_event(int which, const orc_view *in, const orc_view *out)
+{
+    if (orc_layout_validate(in, 0) || orc_layout_validate(out, 0)) return ORC_INVALID_VIEW;
+    if (count_or_zero(in) != count_or_zero(out)) return ORC_SHAPE_MISMATCH;
+    unary_execute(which, in, out);
+    return ORC_OK;
+}
+int orc_op_log(const orc_view *in, const orc_view *out) { return math_event(MATH_LOG, in, out); }
+int orc_op_sin(const orc_view *in, const orc_view *out) { return math_event(MATH_SIN, in, out); }
+int orc_op_cos(const orc_view *in, const orc_view *out) { return math_event(MATH_COS, in, out); }
 
 /* OpUnary{subop}, unary.rs:985-1027: only eight subops are accepted and every
  * failed guard (subop, view or shape) reports UnexpectedEvent. */
@@ -683,7 +737,7 @@ int orc_swiglu(const orc_view *gate, const orc_view *up, const orc_view *out)
 /* OpGlu (glu.rs:22-160, :243-282)                                     */
 /* ------------------------------------------------------------------ */
 
-/* Gate functions, glu.rs:103-129: relu = f32::max(x, 0) (glibc fmaxf),
+/* Gate functions, glu.rs:103-129: relu = f32::max(x, 0) (rust_maxf),
  * silu = x / (1 + exp(-x)), gelu_tanh = 0.5 x (1 + tanh(0.7978846 x
  * (1 + 0.044715 x x))), gelu_quick = x (1 / (1 + exp(-1.702 x))), gelu_erf:
  * the Abramowitz-Stegun 7.1.26 polynomial with exp(-x x).  Every product
@@ -691,7 +745,7 @@ int orc_swiglu(const orc_view *gate, const orc_view *up, const orc_view *out)
 float orc_glu_gate(int subop, float g)
 {
     switch (subop) {
-    case ORC_REGLU: return fmaxf(g, 0.0f);
+    case ORC_REGLU: return rust_maxf(g, 0.0f);
     case ORC_GEGLU: return 0.5f * g * (1.0f + tanhf(0.7978846f * g * (1.0f + 0.044715f * g * g)));
     case ORC_SWIGLU: return orc_silu(g);
     case ORC_GEGLU_QUICK: return g * (1.0f / (1.0f + expf(-1.702f * g)));
@@ -719,8 +773,8 @@ int orc_op_glu(int subop, const float *input, uint64_t input_len, float *output,
     const float *values = input, *gates = input + n;
     for (uint64_t i = 0; i < n; i++) {
         if (subop == ORC_SWIGLU_OAI) {
-            const float g = fminf(gates[i], 7.0f);
-            const float v = fminf(values[i], 7.0f);
+            const float g = rust_minf(gates[i], 7.0f);
+            const float v = rust_minf(values[i], 7.0f);
             output[i] = orc_silu(1.702f * g) / 1.702f * (v + 1.0f);
         } else {
             output[i] = values[i] * orc_glu_gate(subop, gates[i]);

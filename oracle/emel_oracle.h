@@ -15,6 +15,7 @@
 #ifndef EMEL_ORACLE_H
 #define EMEL_ORACLE_H
 
+#include <math.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -57,7 +58,10 @@ int orc_normalization_view_valid(const orc_view *v);
 int orc_op_binary(int op, const orc_view *lhs, const orc_view *rhs, const orc_view *dst);
 int orc_op_broadcast_row(int op, const orc_view *src0, const orc_view *src1, const orc_view *dst);
 int orc_op_unary(int subop, const orc_view *in, const orc_view *out);       /* OpUnary */
-int orc_op_unary_event(int subop, const orc_view *in, const orc_view *out); /* OpSilu/OpGelu/... */
+int orc_op_unary_event(int subop, const orc_view *in, const orc_view *out); /* the 21 typed unary events */
+int orc_op_log(const orc_view *in, const orc_view *out);                    /* reductions::OpLog */
+int orc_op_sin(const orc_view *in, const orc_view *out);                    /* reductions::OpSin */
+int orc_op_cos(const orc_view *in, const orc_view *out);                    /* reductions::OpCos */
 int orc_op_scale(const orc_view *in, const orc_view *out, float scale);
 int orc_op_rms_norm(const orc_view *in, const orc_view *out, float eps);
 int orc_op_norm(const orc_view *in, const orc_view *out, float eps);
@@ -123,6 +127,14 @@ typedef struct orc_index_view {
 } orc_index_view;
 enum { ORC_GR_F32 = 0, ORC_GR_F32_BYTES, ORC_GR_F16, ORC_GR_BF16, ORC_GR_Q4_0, ORC_GR_Q8_0, ORC_GR_Q4_K };
 int orc_get_rows(int kind, const orc_view *src, const orc_index_view *indices, const orc_view *dst);
+
+/* Rust f32::max / f32::min.  They lower to LLVM maxnum / minnum, which on
+ * x86_64 return the other operand whenever one is NaN, signaling NaN
+ * included; glibc fmaxf / fminf instead return a quieted NaN for a
+ * signaling operand (IEEE 754-2008 maxNum).  Equal operands (+0 and -0)
+ * are left to fmaxf / fminf: their sign is not pinned by the reference. */
+static inline float rust_maxf(float a, float b) { return a != a ? b : (b != b ? a : fmaxf(a, b)); }
+static inline float rust_minf(float a, float b) { return a != a ? b : (b != b ? a : fminf(a, b)); }
 
 /* Scalar helpers (unary.rs:522-600, quant.rs:287-300). */
 /* emel-logits (emel_oracle_sampler.c): the native temperature/top-k

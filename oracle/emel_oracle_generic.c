@@ -393,7 +393,7 @@ static float unary_value(int code, float v)
     case U_NEG: return -v;
     case U_TANH: return tanhf(v);
     case U_ELU: return v > 0.0f ? v : expm1f(v);
-    case U_RELU: return fmaxf(v, 0.0f); /* f32::max, as the typed OpUnary */
+    case U_RELU: return rust_maxf(v, 0.0f); /* f32::max, as the typed OpUnary */
     case U_GELU: return 0.5f * v * (1.0f + tanhf(0.7978846f * fmaf(0.044715f * v * v, v, v)));
     case U_SILU: return v / (1.0f + expf(-v));
     case U_EXP: return expf(v);
@@ -639,7 +639,7 @@ static void x_softmax(const orc_generic_request *r)
     const uint64_t w = r->src0->ne[0], rows = g_count(r->src0) / w;
     for (uint64_t row = 0; row < rows; row++) {
         float mx = -INFINITY;
-        for (uint64_t c = 0; c < w; c++) mx = fmaxf(mx, g_rd(r->src0, row * w + c));
+        for (uint64_t c = 0; c < w; c++) mx = rust_maxf(mx, g_rd(r->src0, row * w + c)); /* generic.rs:1970 */
         float sum = 0.0f;
         for (uint64_t c = 0; c < w; c++) {
             const float e = expf(g_rd(r->src0, row * w + c) - mx);

@@ -65,6 +65,9 @@ _SIG = {
     "orc_op_broadcast_row": [ctypes.c_int, _P, _P, _P],
     "orc_op_unary": [ctypes.c_int, _P, _P],
     "orc_op_unary_event": [ctypes.c_int, _P, _P],
+    "orc_op_log": [_P, _P],
+    "orc_op_sin": [_P, _P],
+    "orc_op_cos": [_P, _P],
     "orc_op_scale": [_P, _P, ctypes.c_float],
     "orc_op_rms_norm": [_P, _P, ctypes.c_float],
     "orc_op_norm": [_P, _P, ctypes.c_float],
@@ -134,6 +137,9 @@ def binary(op, lhs, rhs, dst): return call("orc_op_binary", op, lhs, rhs, dst)
 def broadcast_row(op, src0, src1, dst): return call("orc_op_broadcast_row", op, src0, src1, dst)
 def unary(subop, src, dst): return call("orc_op_unary", subop, src, dst)
 def unary_event(subop, src, dst): return call("orc_op_unary_event", subop, src, dst)
+def log(src, dst): return call("orc_op_log", src, dst)
+def sin(src, dst): return call("orc_op_sin", src, dst)
+def cos(src, dst): return call("orc_op_cos", src, dst)
 def scale(src, dst, s): return call("orc_op_scale", src, dst, ctypes.c_float(s))
 def rms_norm(src, dst, eps): return call("orc_op_rms_norm", src, dst, ctypes.c_float(eps))
 def norm(src, dst, eps): return call("orc_op_norm", src, dst, ctypes.c_float(eps))

@@ -3,7 +3,7 @@
 // Compiles the product's device math (emel.rs_amd/csrc/libm_replica.hpp) for
 // the host CPU and counts, over a range of f32 bit patterns, the inputs on
 // which it differs from an independent checker:
-//   expf / expm1f / tanhf / logf
+//   expf / expm1f / tanhf / logf / sinf / cosf / log1pf
 //                          -> the host glibc (what Rust std calls, and so
 //                             what the reference's CPU path computes);
 //   fp32 -> fp16           -> the compiler's _Float16 conversion (IEEE
@@ -302,6 +302,30 @@ uint64_t check_logf(uint64_t lo, uint64_t hi, int threads)
     return count_range(lo, hi, threads, [](uint32_t u) {
         const float x = emel::bits_to_f32(u);
         return differ(emel::emel_logf(x), logf(x));
+    });
+}
+
+uint64_t check_sinf(uint64_t lo, uint64_t hi, int threads)
+{
+    return count_range(lo, hi, threads, [](uint32_t u) {
+        const float x = emel::bits_to_f32(u);
+        return differ(emel::emel_sinf(x), sinf(x));
+    });
+}
+
+uint64_t check_cosf(uint64_t lo, uint64_t hi, int threads)
+{
+    return count_range(lo, hi, threads, [](uint32_t u) {
+        const float x = emel::bits_to_f32(u);
+        return differ(emel::emel_cosf(x), cosf(x));
+    });
+}
+
+uint64_t check_log1pf(uint64_t lo, uint64_t hi, int threads)
+{
+    return count_range(lo, hi, threads, [](uint32_t u) {
+        const float x = emel::bits_to_f32(u);
+        return differ(emel::emel_log1pf(x), log1pf(x));
     });
 }
 

@@ -188,8 +188,6 @@ def expected_product(want, req):
     if want not in (OK, orc.PANIC):
         return want
     op = req["op"]
-    if op in (G.LOG, G.SIN, G.COS):
-        return UNSUPPORTED
     used = [req["d"]]
     if op not in (G.FILL, G.ARANGE):
         used.append(req["s0"])

@@ -3,8 +3,8 @@ oracle's restatement of generic.rs, through the C ABI.
 
 Bit-exact for every route except sum and mean, whose f64 accumulation runs
 as a parallel tree on the device (relative 1e-6 on the f32 result).  The
-documented divergences are asserted explicitly: log/sin/cos and self-
-overlapping destinations are UNSUPPORTED_OPERATION, a partial last element
+documented divergences are asserted explicitly: self-overlapping
+destinations are UNSUPPORTED_OPERATION, a partial last element
 (the reference panics) is INVALID_SHAPE, dst overlapping a source is
 INVALID_ARGUMENT."""
 import struct
@@ -339,12 +339,26 @@ def test_rejections_match_the_oracle_and_leave_dst(run):
     assert (d3.result() == 3.0).all()
 
 
+def test_log_sin_cos_routes(run):
+    # f32::ln / sin / cos through the glibc replicas: bit-exact, strided too
+    g = np.random.Generator(np.random.PCG64(94))
+    vals = np.concatenate([g.uniform(-1e4, 1e4, 700), g.standard_normal(200) * 3, [0.0, -0.0, 1.0, -1.0, np.inf,
+                           -np.inf, np.nan, 1e-40, 3e38, 120.0, -120.0, 1e9]]).astype(np.float32)
+    n = vals.size
+    for op in (G.LOG, G.SIN, G.COS):
+        x = run.pair(vals, [n, 1, 1, 1])
+        d = run.pair(np.full(n, 3.0, np.float32), [n, 1, 1, 1])
+        want, got = run(op, x, None, None, d)
+        assert want == orc.OK and got == eh.Status.OK, (G(op).name, want, got)
+        xs = run.pair(np.repeat(vals, 2), [n // 4, 4, 1, 1], [8, 8 * (n // 4), 8 * n, 8 * n])
+        ds = run.pair(np.full(n, 3.0, np.float32), [4, n // 4, 1, 1])
+        want, got = run(op, xs, None, None, ds)
+        assert want == orc.OK and got == eh.Status.OK, (G(op).name, want, got)
+
+
 def test_divergences(run):
     x = run.pair(uniform(91, 16, 0.5, 2.0), [16, 1, 1, 1])
     d = run.pair(np.full(16, 3.0, np.float32), [16, 1, 1, 1])
-    for op in (G.LOG, G.SIN, G.COS):
-        want, got = run(op, x, None, None, d, compare=False)
-        assert want == orc.OK and got == eh.Status.UNSUPPORTED_OPERATION
     short = run.pair(uniform(92, 16), [16, 1, 1, 1], data_bytes=62)  # last element 2 bytes short
     want, got = run(G.DUP, short, None, None, d)
     assert want == orc.PANIC and got == eh.Status.INVALID_SHAPE

@@ -2,9 +2,10 @@
 for the host by tests/native/libm_replica_check.cpp, against independent
 checkers over ALL 2^32 float inputs:
 
-  expf, expm1f, tanhf, logf
-                       == the host glibc (Rust std's f32::exp/exp_m1/tanh/ln on
-                          x86_64-linux-gnu, i.e. what the reference computes);
+  expf, expm1f, tanhf, logf, sinf, cosf, log1pf
+                       == the host glibc (Rust std's f32::exp/exp_m1/tanh/ln/
+                          sin/cos/ln_1p on x86_64-linux-gnu, i.e. what the
+                          reference computes);
   fp32 -> fp16         == IEEE round-to-nearest-even (_Float16 conversion);
   fp16 -> fp32         == exact widening;
   GELU by table        == the formula (the kernels' saturation thresholds
@@ -29,7 +30,8 @@ def chk():
     if not LIB.exists():
         pytest.fail(f"{LIB} missing: run __graft_entry__.build()")
     L = ctypes.CDLL(str(LIB))
-    for n in ("check_expf", "check_expm1f", "check_tanhf", "check_logf", "check_fp32_to_fp16", "check_gelu_table"):
+    for n in ("check_expf", "check_expm1f", "check_tanhf", "check_logf", "check_sinf", "check_cosf", "check_log1pf",
+              "check_fp32_to_fp16", "check_gelu_table"):
         getattr(L, n).restype = ctypes.c_uint64
         getattr(L, n).argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int]
     L.check_fp16_to_f32.restype = ctypes.c_uint64
@@ -39,7 +41,8 @@ def chk():
     return L
 
 
-@pytest.mark.parametrize("fn", ["check_expf", "check_expm1f", "check_tanhf", "check_logf", "check_fp32_to_fp16", "check_gelu_table"])
+@pytest.mark.parametrize("fn", ["check_expf", "check_expm1f", "check_tanhf", "check_logf", "check_sinf", "check_cosf",
+                                "check_log1pf", "check_fp32_to_fp16", "check_gelu_table"])
 def test_exhaustive(chk, fn):
     assert getattr(chk, fn)(0, 1 << 32, THREADS) == 0
 
