@@ -596,6 +596,8 @@ const char *emel_status_string(emel_status s)
     case EMEL_ERR_UNSUPPORTED_SOURCE_STRIDE: return "unsupported source stride";
     case EMEL_ERR_INVALID_REQUEST: return "invalid request";
     case EMEL_ERR_STREAM_CAPTURE: return "not capturable: the stream is being captured";
+    case EMEL_ERR_INVALID_OFFSET: return "invalid offset";
+    case EMEL_ERR_ZERO_NORM: return "zero norm";
     }
     return "unknown status";
 }
@@ -2270,4 +2272,233 @@ emel_status emel_logits_validator_build(const float *logits, uint64_t logits_len
     if (e != hipSuccess) return hip_fail(e, "validator launch");
     *candidate_count_out = vocab_size; // execute_build
     return launched(hipSuccess);
+}
+
+// ---- the remaining typed events of activation.rs, elementwise.rs, diag.rs and
+// ---- group_norm.rs -------------------------------------------------------------
+
+namespace {
+
+// activation.rs views_valid + same_shape (:168-175): Layout::validate on both,
+// then equal extents.
+emel_status activation_guard(const emel_tensor_view *in, const emel_tensor_view_mut *out)
+{
+    if (!in || !out) return fail(EMEL_ERR_INVALID_ARGUMENT, "null view");
+    if (!valid_f32(*in, false) || !valid_f32(*out, false))
+        return fail(EMEL_ERR_INVALID_VIEW, "activation view failed validation");
+    if (!same_ne(*in, *out)) return fail(EMEL_ERR_SHAPE_MISMATCH, "activation shapes differ");
+    return EMEL_OK;
+}
+
+// diag.rs square_side (:107-120).
+bool square_side(uint64_t len, uint64_t &side)
+{
+    if (len == 0) return false;
+    const uint64_t r = static_cast<uint64_t>(std::sqrt(static_cast<double>(len)));
+    for (uint64_t s = r > 2 ? r - 2 : 0; s <= r + 2; ++s)
+        if (static_cast<u128>(s) * s == len) {
+            side = s;
+            return true;
+        }
+    return false;
+}
+
+// A validated F32 view as the generic kernels' operand (element strides).
+template <class V>
+emel::GView gview_of(const V &v)
+{
+    const Operand o = operand(v, 4);
+    emel::GView g{};
+    g.data = o.data;
+    for (int d = 0; d < 4; ++d) {
+        g.ne[d] = o.ne[d];
+        g.st[d] = o.st[d];
+    }
+    return g;
+}
+
+emel::GView dense_gview(const float *p, uint64_t n0, uint64_t n1)
+{
+    emel::GView v{};
+    v.data = const_cast<float *>(p);
+    v.ne[0] = n0;
+    v.ne[1] = n1;
+    v.ne[2] = v.ne[3] = 1;
+    v.st[0] = 1;
+    v.st[1] = static_cast<int64_t>(n0);
+    v.st[2] = v.st[3] = static_cast<int64_t>(n0 * n1);
+    return v;
+}
+
+// Exact aliasing (output == input) is allowed: every element is read before
+// its own write.  Any other overlap is refused.
+bool slices_ok(const float *in, uint64_t in_len, const float *out, uint64_t out_len)
+{
+    const uintptr_t a0 = reinterpret_cast<uintptr_t>(in), a1 = a0 + in_len * 4;
+    const uintptr_t b0 = reinterpret_cast<uintptr_t>(out), b1 = b0 + out_len * 4;
+    return a1 <= b0 || b1 <= a0 || (a0 == b0 && in_len == out_len);
+}
+
+emel_status diag_mask(emel::GenOrd which, const float *input, uint64_t input_len, float *output, uint64_t output_len,
+                      int32_t n_past, emel_stream stream)
+{
+    uint64_t side = 0;
+    // mask_valid (diag.rs:122-124)
+    if (!(n_past >= 0 && input_len == output_len && square_side(input_len, side)))
+        return fail(EMEL_ERR_INVALID_SHAPE, "diag mask needs a non-empty square slice and n_past >= 0");
+    if (!input || !output) return fail(EMEL_ERR_INVALID_ARGUMENT, "null slice");
+    if (!slices_ok(input, input_len, output, output_len)) return fail(EMEL_ERR_INVALID_ARGUMENT, "slices overlap");
+    emel_status s = ensure_device();
+    if (s != EMEL_OK) return s;
+    emel::GenOrdArgs a{};
+    a.op = which;
+    a.a = dense_gview(input, side, side);
+    a.y = dense_gview(output, side, side);
+    a.n_past = static_cast<uint64_t>(n_past);
+    return launched(emel::launch_generic_ordinal(a, as_stream(stream)));
+}
+
+} // namespace
+
+emel_status emel_op_clamp(const emel_tensor_view *in, const emel_tensor_view_mut *out, float min, float max,
+                          emel_stream stream)
+{
+    emel_status s = activation_guard(in, out);
+    if (s != EMEL_OK) return s;
+    return elementwise(emel::Ew::ClampStd, in, emel::Addr::SameCoords, nullptr, emel::Addr::SameCoords, out, min,
+                       stream, max);
+}
+
+emel_status emel_op_leaky_relu(const emel_tensor_view *in, const emel_tensor_view_mut *out, float negative_slope,
+                               emel_stream stream)
+{
+    emel_status s = activation_guard(in, out);
+    if (s != EMEL_OK) return s;
+    return elementwise(emel::Ew::LeakyRelu, in, emel::Addr::SameCoords, nullptr, emel::Addr::SameCoords, out,
+                       negative_slope, stream);
+}
+
+emel_status emel_op_silu_back(const emel_tensor_view *in, const emel_tensor_view *gradient,
+                              const emel_tensor_view_mut *out, emel_stream stream)
+{
+    if (!in || !gradient || !out) return fail(EMEL_ERR_INVALID_ARGUMENT, "null view");
+    // three_views_valid / three_views_same_shape (activation.rs:176-190)
+    if (!valid_f32(*in, false) || !valid_f32(*gradient, false) || !valid_f32(*out, false))
+        return fail(EMEL_ERR_INVALID_VIEW, "silu_back view failed validation");
+    if (!same_ne(*in, *gradient) || !same_ne(*in, *out))
+        return fail(EMEL_ERR_SHAPE_MISMATCH, "silu_back shapes differ");
+    return elementwise(emel::Ew::SiluBack, in, emel::Addr::SameCoords, gradient, emel::Addr::SameCoords, out, 0.0f,
+                       stream);
+}
+
+emel_status emel_op_add1(const emel_tensor_view *src, float scalar, const emel_tensor_view_mut *dst, emel_stream stream)
+{
+    if (!src || !dst) return fail(EMEL_ERR_INVALID_ARGUMENT, "null view");
+    // valid_pair / same_shape (elementwise.rs:203-209)
+    if (!valid_f32(*src, false) || !valid_f32(*dst, false))
+        return fail(EMEL_ERR_INVALID_VIEW, "add1 view failed validation");
+    if (!same_ne(*src, *dst)) return fail(EMEL_ERR_SHAPE_MISMATCH, "add1 shapes differ");
+    return elementwise(emel::Ew::Add1, src, emel::Addr::SameCoords, nullptr, emel::Addr::SameCoords, dst, scalar,
+                       stream);
+}
+
+emel_status emel_op_acc(const emel_tensor_view *base, const emel_tensor_view *update, const emel_tensor_view_mut *dst,
+                        uint64_t offset, emel_stream stream)
+{
+    if (!base || !update || !dst) return fail(EMEL_ERR_INVALID_ARGUMENT, "null view");
+    // guard order of the machine (elementwise.rs:110-116, :227-243)
+    const bool pair = valid_f32(*base, false) && valid_f32(*dst, false) && valid_f32(*update, false);
+    if (pair && !same_ne(*base, *dst)) return fail(EMEL_ERR_SHAPE_MISMATCH, "acc base and dst shapes differ");
+    const bool views = pair && dense_for(*base, EMEL_DTYPE_F32, 4) && dense_for(*update, EMEL_DTYPE_F32, 4) &&
+                       dense_for(*dst, EMEL_DTYPE_F32, 4);
+    if (!views) return fail(EMEL_ERR_INVALID_VIEW, "acc views must be valid dense F32");
+    const uint64_t n = count_or_zero(*dst), nu = count_or_zero(*update);
+    if (!(offset <= n && nu <= n - offset)) return fail(EMEL_ERR_INVALID_OFFSET, "acc update extends past dst");
+    if (!overlap_ok(*dst, 4, *base, 4) || !overlap_ok(*dst, 4, *update, 4) || dst->data == update->data)
+        return fail(EMEL_ERR_INVALID_VIEW, "dst overlaps the update or partially overlaps the base");
+    emel_status s = ensure_device();
+    if (s != EMEL_OK) return s;
+    return launched(emel::launch_acc(static_cast<const float *>(base->data), static_cast<const float *>(update->data),
+                                     static_cast<float *>(dst->data), n, offset, nu, as_stream(stream)));
+}
+
+emel_status emel_op_diag(const float *input, uint64_t input_len, float *output, uint64_t output_len,
+                         emel_stream stream)
+{
+    // OpDiag::side (diag.rs:57-64)
+    if (input_len == 0 || static_cast<u128>(input_len) * input_len != output_len)
+        return fail(EMEL_ERR_INVALID_SHAPE, "diag needs a non-empty input and an n*n output");
+    if (!input || !output) return fail(EMEL_ERR_INVALID_ARGUMENT, "null slice");
+    if (!slices_ok(input, input_len, output, output_len) || input == output)
+        return fail(EMEL_ERR_INVALID_ARGUMENT, "slices overlap");
+    emel_status s = ensure_device();
+    if (s != EMEL_OK) return s;
+    emel::GenOrdArgs a{};
+    a.op = emel::GenOrd::Diag;
+    a.a = dense_gview(input, input_len, 1);
+    a.y = dense_gview(output, input_len, input_len);
+    return launched(emel::launch_generic_ordinal(a, as_stream(stream)));
+}
+
+emel_status emel_op_diag_mask_inf(const float *input, uint64_t input_len, float *output, uint64_t output_len,
+                                  int32_t n_past, emel_stream stream)
+{
+    return diag_mask(emel::GenOrd::DiagMaskInf, input, input_len, output, output_len, n_past, stream);
+}
+
+emel_status emel_op_diag_mask_zero(const float *input, uint64_t input_len, float *output, uint64_t output_len,
+                                   int32_t n_past, emel_stream stream)
+{
+    return diag_mask(emel::GenOrd::DiagMaskZero, input, input_len, output, output_len, n_past, stream);
+}
+
+emel_status emel_op_group_norm(const emel_tensor_view *in, const emel_tensor_view_mut *out, uint64_t groups,
+                               float epsilon, emel_stream stream)
+{
+    if (!in || !out) return fail(EMEL_ERR_INVALID_ARGUMENT, "null view");
+    // the machine's guard order (group_norm.rs:179-196, :205-226)
+    if (!valid_normalization(*in) || !valid_normalization(*out))
+        return fail(EMEL_ERR_INVALID_VIEW, "group_norm view failed validation");
+    if (!same_ne(*in, *out)) return fail(EMEL_ERR_SHAPE_MISMATCH, "group_norm shapes differ");
+    if (!(groups != 0 && in->ne[2] % groups == 0 && std::isfinite(epsilon) && epsilon >= 0.0f))
+        return fail(EMEL_ERR_INVALID_PARAMETERS, "groups must divide the channels; epsilon finite and >= 0");
+    if (!overlap_ok(*out, 4, *in, 4)) return fail(EMEL_ERR_INVALID_VIEW, "dst partially overlaps the source");
+    if (!elements_disjoint(*out, 4)) return fail(EMEL_ERR_INVALID_VIEW, "dst elements overlap one another");
+    if (groups > 0x7fffffffull) return fail(EMEL_ERR_INVALID_PARAMETERS, "too many groups");
+    emel_status s = ensure_device();
+    if (s != EMEL_OK) return s;
+    const hipError_t e = emel::launch_group_norm(operand(*in, 4), operand(*out, 4), static_cast<uint32_t>(groups),
+                                                 epsilon, as_stream(stream));
+    if (e == hipErrorInvalidValue) return fail(EMEL_ERR_INTERNAL, "group_norm group size outside the supported range");
+    return launched(e);
+}
+
+emel_status emel_op_l2_norm(const emel_tensor_view *in, const emel_tensor_view_mut *out, emel_stream stream)
+{
+    if (!in || !out) return fail(EMEL_ERR_INVALID_ARGUMENT, "null view");
+    if (!valid_normalization(*in) || !valid_normalization(*out))
+        return fail(EMEL_ERR_INVALID_VIEW, "l2_norm view failed validation");
+    if (!same_ne(*in, *out)) return fail(EMEL_ERR_SHAPE_MISMATCH, "l2_norm shapes differ");
+    if (!overlap_ok(*out, 4, *in, 4)) return fail(EMEL_ERR_INVALID_VIEW, "dst partially overlaps the source");
+    if (!elements_disjoint(*out, 4)) return fail(EMEL_ERR_INVALID_VIEW, "dst elements overlap one another");
+    emel_status s = ensure_device();
+    if (s != EMEL_OK) return s;
+    // guard_l2_norm_valid needs the sum (group_norm.rs:252-260): it is formed on
+    // the device, read back, and checked before anything is written.
+    const hipStream_t hs = as_stream(stream);
+    s = not_capturing(hs, "l2_norm (its ZeroNorm guard reads the sum back)");
+    StreamLease lease;
+    if (s == EMEL_OK) s = lease.acquire(hs);
+    void *ws = nullptr, *stage = nullptr;
+    if (s == EMEL_OK) s = lease.work(2 * sizeof(float), &ws);
+    if (s == EMEL_OK) s = lease.staging(2 * sizeof(float), &stage);
+    if (s != EMEL_OK) return s;
+    const emel::GView x = gview_of(*in), y = gview_of(*out);
+    hipError_t e = emel::launch_generic_l2_sum(x, ws, hs);
+    if (e == hipSuccess) e = hipMemcpyAsync(stage, ws, 2 * sizeof(float), hipMemcpyDeviceToHost, hs);
+    if (e == hipSuccess) e = hipStreamSynchronize(hs);
+    if (e != hipSuccess) return hip_fail(e, "l2_norm sum");
+    const float sum = static_cast<const float *>(stage)[1];
+    if (!(sum > 0.0f)) return fail(EMEL_ERR_ZERO_NORM, "l2_norm: the sum of squares is not positive");
+    return launched(emel::launch_generic_l2_apply(x, y, ws, hs));
 }

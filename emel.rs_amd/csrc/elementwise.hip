@@ -199,6 +199,9 @@ EMEL_FN(Trunc, false, false, __builtin_truncf(a))
 EMEL_FN(Log, false, false, emel_logf(a))
 EMEL_FN(Sin, false, false, emel_sinf(a))
 EMEL_FN(Cos, false, false, emel_cosf(a))
+// OpClamp (activation.rs:403-421): std::clamp's comparisons, min first; NaN
+// passes through, and min > max yields min below it
+EMEL_FN(ClampStd, false, false, a < s ? s : (a > s2 ? s2 : a))
 #undef EMEL_FN
 
 template <Ew OP>
@@ -639,6 +642,7 @@ hipError_t launch_elementwise(const EwArgs &args, hipStream_t stream)
     case Ew::Clamp: return launch_op<Ew::Clamp>(args, stream);
     case Ew::GeluGeneric: return launch_op<Ew::GeluGeneric>(args, stream);
     case Ew::SiluBack: return launch_op<Ew::SiluBack>(args, stream);
+    case Ew::ClampStd: return launch_op<Ew::ClampStd>(args, stream);
     case Ew::Sgn: return launch_op<Ew::Sgn>(args, stream);
     case Ew::Step: return launch_op<Ew::Step>(args, stream);
     case Ew::GeluQuick: return launch_op<Ew::GeluQuick>(args, stream);
@@ -656,6 +660,31 @@ hipError_t launch_elementwise(const EwArgs &args, hipStream_t stream)
     case Ew::Cos: return launch_op<Ew::Cos>(args, stream);
     }
     return hipErrorInvalidValue;
+}
+
+// ---- OpAcc (elementwise.rs:262-277) -------------------------------------------
+
+namespace {
+__global__ __launch_bounds__(kBlock) void k_acc(const float *base, const float *update, float *dst, uint64_t count,
+                                                 uint64_t offset, uint64_t n_update)
+{
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kBlock;
+    for (uint64_t k = static_cast<uint64_t>(blockIdx.x) * kBlock + threadIdx.x; k < count; k += stride) {
+        float v = base[k];
+        if (k >= offset && k - offset < n_update) v = v + update[k - offset]; // no +0.0 outside the update
+        dst[k] = v;
+    }
+}
+} // namespace
+
+hipError_t launch_acc(const float *base, const float *update, float *dst, uint64_t count, uint64_t offset,
+                      uint64_t n_update, hipStream_t stream)
+{
+    if (count == 0) return hipSuccess;
+    uint64_t blocks = (count + kBlock - 1) / kBlock;
+    if (blocks > 65536) blocks = 65536;
+    k_acc<<<dim3(static_cast<uint32_t>(blocks)), kBlock, 0, stream>>>(base, update, dst, count, offset, n_update);
+    return hipGetLastError();
 }
 
 } // namespace emel

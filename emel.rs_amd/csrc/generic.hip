@@ -279,6 +279,7 @@ __global__ __launch_bounds__(64) void k_l2_sum(GView xv, uint64_t count, float *
         w.next(xv);
     }
     scale_out[0] = 1.0f / __builtin_sqrtf(sum);
+    scale_out[1] = sum;
 }
 
 __global__ __launch_bounds__(kBlock) void k_l2_apply(GView xv, GView yv, uint64_t count, const float *scale)
@@ -528,6 +529,22 @@ hipError_t launch_generic_l2_norm(const GView &x, const GView &y, void *workspac
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     k_l2_apply<<<grid_for(count, kBlock, 65536), kBlock, 0, s>>>(x, y, count, scale);
+    return hipGetLastError();
+}
+
+hipError_t launch_generic_l2_sum(const GView &x, void *workspace, hipStream_t s)
+{
+    uint64_t count = 1;
+    for (int d = 0; d < 4; ++d) count *= x.ne[d];
+    k_l2_sum<<<1, 64, 0, s>>>(x, count, static_cast<float *>(workspace));
+    return hipGetLastError();
+}
+
+hipError_t launch_generic_l2_apply(const GView &x, const GView &y, const void *workspace, hipStream_t s)
+{
+    uint64_t count = 1;
+    for (int d = 0; d < 4; ++d) count *= x.ne[d];
+    k_l2_apply<<<grid_for(count, kBlock, 65536), kBlock, 0, s>>>(x, y, count, static_cast<const float *>(workspace));
     return hipGetLastError();
 }
 

@@ -29,7 +29,8 @@ enum class Ew : uint32_t {
     Add1, LeakyRelu, Clamp, GeluGeneric, SiluBack,                 // generic envelope (generic.rs)
     Sgn, Step, GeluQuick, Hardswish, Hardsigmoid, Expm1, Softplus,  // the other typed unary events (unary.rs)
     GeluErf, Floor, Ceil, Round, Trunc,
-    Log, Sin, Cos                                                  // reductions.rs OpLog / OpSin / OpCos
+    Log, Sin, Cos,                                                 // reductions.rs OpLog / OpSin / OpCos
+    ClampStd                                                       // activation.rs OpClamp (std::clamp order)
 };
 
 // The scalar parameters an elementwise functor reads: x is Scale's factor,
@@ -60,6 +61,11 @@ struct EwArgs {
 
 hipError_t launch_elementwise(const EwArgs &args, hipStream_t stream);
 
+// OpAcc over dense buffers (elementwise.rs:262-277): dst[k] = base[k], plus
+// update[k - offset] for offset <= k < offset + n_update (one f32 addition).
+hipError_t launch_acc(const float *base, const float *update, float *dst, uint64_t count, uint64_t offset,
+                      uint64_t n_update, hipStream_t stream);
+
 // ---- row kernels (rows.hip) --------------------------------------------
 
 enum class RowOp : uint32_t { RmsNorm = 0, RmsNormMul = 1, Norm = 2, SoftMax = 3, SoftMaxExt = 4 };
@@ -78,6 +84,10 @@ struct RowArgs {
 };
 
 hipError_t launch_rows(const RowArgs &args, hipStream_t stream);
+
+// OpGroupNorm (group_norm.rs:197-241): x and y share extents [W, H, C, B];
+// group g of batch b is channels [g C/groups, (g+1) C/groups).
+hipError_t launch_group_norm(const Operand &x, const Operand &y, uint32_t groups, float eps, hipStream_t stream);
 
 // ---- reductions (reduce.hip) ---------------------------------------------
 
@@ -154,6 +164,10 @@ enum class GenWork : uint32_t { L2Norm = 0, CountEqual, MulMatArgmax };
 uint64_t generic_workspace_bytes(GenWork which);
 
 hipError_t launch_generic_l2_norm(const GView &x, const GView &y, void *workspace, hipStream_t stream);
+// The two halves of l2_norm: the sequential f32 sum of squares (workspace[1])
+// and its scale 1/sqrt(sum) (workspace[0]); then y = x * scale.
+hipError_t launch_generic_l2_sum(const GView &x, void *workspace, hipStream_t stream);
+hipError_t launch_generic_l2_apply(const GView &x, const GView &y, const void *workspace, hipStream_t stream);
 hipError_t launch_generic_count_equal(const GView &a, const GView &b, float *dst, void *workspace,
                                       hipStream_t stream);
 

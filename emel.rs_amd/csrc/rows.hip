@@ -628,4 +628,87 @@ hipError_t launch_rows(const RowArgs &a, hipStream_t s)
     return hipGetLastError();
 }
 
+// ---- OpGroupNorm (group_norm.rs:197-241) -----------------------------------------
+//
+// One workgroup per (batch, group).  The group's W*H*(C/groups) elements are
+// visited three times -- f64 sum, f64 sum of the squared f32-centered
+// values, then (x - mean) * scale -- at their (column, row, channel, batch)
+// offsets, so any element strides work; the later passes hit L2.  The f64
+// sums run as a tree instead of the reference's sequential loop, the same
+// trade as rms_norm.
+
+namespace {
+
+struct GroupGeo {
+    uint32_t groups;
+    uint32_t cpg;          // channels per group
+    uint64_t n;            // elements per group
+    FastDiv w, wh;         // W and W*H
+    int64_t x_st[4], y_st[4];
+};
+
+__device__ __forceinline__ double block_sum4(double v, double *lds)
+{
+    v = wave_sum_dpp(v);
+    const uint32_t wave = threadIdx.x / kWave;
+    if (threadIdx.x % kWave == 0) lds[wave] = v;
+    __syncthreads();
+    const double t = (lds[0] + lds[1]) + (lds[2] + lds[3]);
+    __syncthreads(); // lds is reused by the next reduction
+    return t;
+}
+
+__global__ __launch_bounds__(kBlock) void k_group_norm(GroupGeo g, const float *x, float *y, float eps)
+{
+    static_assert(kBlock == 4 * kWave, "block_sum4 combines four waves");
+    __shared__ double lds[kBlock / kWave];
+    const uint32_t b = blockIdx.x / g.groups;
+    const uint32_t grp = blockIdx.x - b * g.groups;
+    const uint32_t ch0 = grp * g.cpg;
+    auto offset = [&](const int64_t *st, uint32_t e) {
+        const uint32_t c = g.wh.div(e);
+        const uint32_t rem = e - c * g.wh.d;
+        const uint32_t row = g.w.div(rem);
+        const uint32_t col = rem - row * g.w.d;
+        return static_cast<int64_t>(col) * st[0] + static_cast<int64_t>(row) * st[1] +
+               static_cast<int64_t>(ch0 + c) * st[2] + static_cast<int64_t>(b) * st[3];
+    };
+    const uint32_t n = static_cast<uint32_t>(g.n);
+    double sum = 0.0;
+    for (uint32_t e = threadIdx.x; e < n; e += kBlock) sum += static_cast<double>(x[offset(g.x_st, e)]);
+    sum = block_sum4(sum, lds);
+    const float mean = static_cast<float>(sum / static_cast<double>(g.n));
+    double var = 0.0;
+    for (uint32_t e = threadIdx.x; e < n; e += kBlock) {
+        const float c = x[offset(g.x_st, e)] - mean;
+        var += static_cast<double>(c) * static_cast<double>(c);
+    }
+    var = block_sum4(var, lds);
+    const float scale = 1.0f / __builtin_sqrtf(static_cast<float>(var / static_cast<double>(g.n)) + eps);
+    for (uint32_t e = threadIdx.x; e < n; e += kBlock) y[offset(g.y_st, e)] = (x[offset(g.x_st, e)] - mean) * scale;
+}
+
+} // namespace
+
+hipError_t launch_group_norm(const Operand &x, const Operand &y, uint32_t groups, float eps, hipStream_t s)
+{
+    const uint64_t w = x.ne[0], h = x.ne[1], c = x.ne[2], bt = x.ne[3];
+    if (groups == 0 || c % groups != 0) return hipErrorInvalidValue;
+    GroupGeo g{};
+    g.groups = groups;
+    g.cpg = static_cast<uint32_t>(c / groups);
+    g.n = w * h * g.cpg;
+    const uint64_t blocks = static_cast<uint64_t>(groups) * bt;
+    if (w * h >= 0xffffffffull || g.n >= 0xffffffffull || blocks >= 0x7fffffffull) return hipErrorInvalidValue;
+    g.w = FastDiv(static_cast<uint32_t>(w));
+    g.wh = FastDiv(static_cast<uint32_t>(w * h));
+    for (int d = 0; d < 4; ++d) {
+        g.x_st[d] = x.st[d];
+        g.y_st[d] = y.st[d];
+    }
+    k_group_norm<<<dim3(static_cast<uint32_t>(blocks)), kBlock, 0, s>>>(g, static_cast<const float *>(x.data),
+                                                                         static_cast<float *>(y.data), eps);
+    return hipGetLastError();
+}
+
 } // namespace emel

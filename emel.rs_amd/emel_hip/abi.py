@@ -30,6 +30,8 @@ class Status(enum.IntEnum):
     UNSUPPORTED_SOURCE_STRIDE = 12
     INVALID_REQUEST = 13
     STREAM_CAPTURE = 14
+    INVALID_OFFSET = 15
+    ZERO_NORM = 16
 
 
 class DType(enum.IntEnum):
@@ -312,6 +314,16 @@ SIGNATURES = {
     "emel_op_log": [_V, _V, _S],
     "emel_op_sin": [_V, _V, _S],
     "emel_op_cos": [_V, _V, _S],
+    "emel_op_clamp": [_V, _V, ctypes.c_float, ctypes.c_float, _S],
+    "emel_op_leaky_relu": [_V, _V, ctypes.c_float, _S],
+    "emel_op_silu_back": [_V, _V, _V, _S],
+    "emel_op_add1": [_V, ctypes.c_float, _V, _S],
+    "emel_op_acc": [_V, _V, _V, ctypes.c_uint64, _S],
+    "emel_op_diag": [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_uint64, _S],
+    "emel_op_diag_mask_inf": [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int32, _S],
+    "emel_op_diag_mask_zero": [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int32, _S],
+    "emel_op_group_norm": [_V, _V, ctypes.c_uint64, ctypes.c_float, _S],
+    "emel_op_l2_norm": [_V, _V, _S],
     "emel_op_argmax_rows_no_alloc": [_V, _V, _S],
     "emel_validate_view": [_V, ctypes.c_int32],
     "emel_validate_normalization_view": [_V],

@@ -504,3 +504,130 @@ class Kernel:
             if sync != Status.OK:
                 return sync
         return status
+
+
+# ---- typed events of activation.rs, elementwise.rs, diag.rs, group_norm.rs ----
+
+@dataclass
+class OpClamp:
+    """activation::OpClamp::new(input, output, min, max) (activation.rs:78-96)."""
+
+    input: TensorView
+    output: TensorViewMut
+    min: float
+    max: float
+
+    def _call(self, lib, s):
+        return lib.emel_op_clamp(_p(self.input), _p(self.output), self.min, self.max, s)
+
+
+@dataclass
+class OpLeakyRelu:
+    """activation::OpLeakyRelu::new(input, output, negative_slope) (activation.rs:118-140)."""
+
+    input: TensorView
+    output: TensorViewMut
+    negative_slope: float
+
+    def _call(self, lib, s):
+        return lib.emel_op_leaky_relu(_p(self.input), _p(self.output), self.negative_slope, s)
+
+
+@dataclass
+class OpSiluBack:
+    """activation::OpSiluBack::new(input, gradient, output) (activation.rs:98-116)."""
+
+    input: TensorView
+    gradient: TensorView
+    output: TensorViewMut
+
+    def _call(self, lib, s):
+        return lib.emel_op_silu_back(_p(self.input), _p(self.gradient), _p(self.output), s)
+
+
+@dataclass
+class OpAdd1:
+    """elementwise::OpAdd1::new(src, scalar, dst) (elementwise.rs:51-62)."""
+
+    src: TensorView
+    scalar: float
+    dst: TensorViewMut
+
+    def _call(self, lib, s):
+        return lib.emel_op_add1(_p(self.src), self.scalar, _p(self.dst), s)
+
+
+@dataclass
+class OpAcc:
+    """elementwise::OpAcc::new(base, update, dst, offset) (elementwise.rs:64-80)."""
+
+    base: TensorView
+    update: TensorView
+    dst: TensorViewMut
+    offset: int
+
+    def _call(self, lib, s):
+        return lib.emel_op_acc(_p(self.base), _p(self.update), _p(self.dst), self.offset, s)
+
+
+@dataclass
+class OpDiag:
+    """diag::OpDiag::new(input, output) (diag.rs:38-65): device tensors as slices."""
+
+    input: object
+    output: object
+    input_len: int | None = None
+    output_len: int | None = None
+
+    def _call(self, lib, s):
+        ip, il = _slice(self.input, self.input_len)
+        op, ol = _slice(self.output, self.output_len)
+        return lib.emel_op_diag(ip, il, op, ol, s)
+
+
+@dataclass
+class OpDiagMaskInf:
+    """diag::OpDiagMaskInf::new(input, output, n_past) (diag.rs:67-85)."""
+
+    input: object
+    output: object
+    n_past: int
+    input_len: int | None = None
+    output_len: int | None = None
+    _fn = "emel_op_diag_mask_inf"
+
+    def _call(self, lib, s):
+        ip, il = _slice(self.input, self.input_len)
+        op, ol = _slice(self.output, self.output_len)
+        return getattr(lib, self._fn)(ip, il, op, ol, self.n_past, s)
+
+
+@dataclass
+class OpDiagMaskZero(OpDiagMaskInf):
+    """diag::OpDiagMaskZero::new(input, output, n_past) (diag.rs:87-105)."""
+
+    _fn = "emel_op_diag_mask_zero"
+
+
+@dataclass
+class OpGroupNorm:
+    """group_norm::OpGroupNorm::new(input, output, groups, epsilon) (group_norm.rs:49-66)."""
+
+    input: TensorView
+    output: TensorViewMut
+    groups: int
+    epsilon: float
+
+    def _call(self, lib, s):
+        return lib.emel_op_group_norm(_p(self.input), _p(self.output), self.groups, self.epsilon, s)
+
+
+@dataclass
+class OpL2Norm:
+    """group_norm::OpL2Norm::new(input, output) (group_norm.rs:68-78)."""
+
+    input: TensorView
+    output: TensorViewMut
+
+    def _call(self, lib, s):
+        return lib.emel_op_l2_norm(_p(self.input), _p(self.output), s)

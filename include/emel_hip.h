@@ -62,8 +62,10 @@ typedef enum emel_status {
     EMEL_ERR_UNSUPPORTED_SOURCE_STRIDE = 12, /* GetRowsError::UnsupportedSourceStride */
     EMEL_ERR_INVALID_REQUEST = 13, /* emel-logits SamplerError::InvalidRequest / ValidatorError::InvalidRequest
                                       (crates/emel-logits/src/sampler/sm.rs:41-52, validator/sm.rs:15-21) */
-    EMEL_ERR_STREAM_CAPTURE = 14   /* the call would allocate, synchronise or advance host state while its
+    EMEL_ERR_STREAM_CAPTURE = 14,  /* the call would allocate, synchronise or advance host state while its
                                       stream is being captured into a HIP graph (no reference counterpart) */
+    EMEL_ERR_INVALID_OFFSET = 15,  /* ElementwiseError::InvalidOffset (elementwise.rs:20-27): OpAcc */
+    EMEL_ERR_ZERO_NORM = 16        /* GroupNormError::ZeroNorm (group_norm.rs:15-23): OpL2Norm */
 } emel_status;
 
 /* Wire dtype codes, DType::from_code (tensor_view.rs:111-158). */
@@ -324,6 +326,61 @@ emel_status emel_op_argmax(const emel_tensor_view *src, const emel_tensor_view_m
  * column 0 yields 0, exactly as the sequential strict-> scan). */
 emel_status emel_op_argmax_rows(const emel_tensor_view *src, const emel_tensor_view_mut *dst,
                                 emel_stream stream);
+/* ---- typed events of activation.rs, elementwise.rs, diag.rs, group_norm.rs ---- */
+
+/* activation::OpClamp::new(input, output, min, max) (activation.rs:78-96,
+ * effect :403-421): std::clamp's comparisons -- below min gives min, else
+ * above max gives max, NaN passes through.  activation::OpLeakyRelu::new(
+ * input, output, negative_slope) (:118-140): x < 0 ? x * slope : x.
+ * activation::OpSiluBack::new(input, gradient, output) (:98-116, :467-480):
+ * gradient * s (1 + x (1 - s)), s = 1 / (1 + expf(-x)).  Guards: views valid,
+ * else INVALID_VIEW; identical extents, else SHAPE_MISMATCH. */
+emel_status emel_op_clamp(const emel_tensor_view *in, const emel_tensor_view_mut *out, float min, float max,
+                          emel_stream stream);
+emel_status emel_op_leaky_relu(const emel_tensor_view *in, const emel_tensor_view_mut *out, float negative_slope,
+                               emel_stream stream);
+emel_status emel_op_silu_back(const emel_tensor_view *in, const emel_tensor_view *gradient,
+                              const emel_tensor_view_mut *out, emel_stream stream);
+/* elementwise::OpAdd1::new(src, scalar, dst) (elementwise.rs:51-62, :262-271):
+ * dst = src + scalar; views valid, identical extents. */
+emel_status emel_op_add1(const emel_tensor_view *src, float scalar, const emel_tensor_view_mut *dst,
+                         emel_stream stream);
+/* elementwise::OpAcc::new(base, update, dst, offset) (elementwise.rs:64-80,
+ * guards :216-243, effect :273-288): dst = base, then dst[offset + i] +=
+ * update[i].  base and dst identical extents (SHAPE_MISMATCH); all three dense
+ * F32 (INVALID_VIEW); offset + count(update) <= count(dst) (INVALID_OFFSET).
+ * dst may be base itself. */
+emel_status emel_op_acc(const emel_tensor_view *base, const emel_tensor_view *update, const emel_tensor_view_mut *dst,
+                        uint64_t offset, emel_stream stream);
+/* diag::OpDiag::new(input, output) (diag.rs:38-65, :332-344): output (n*n,
+ * zeroed) gets input on its diagonal; input_len > 0 and output_len == n*n,
+ * else INVALID_SHAPE.  diag::OpDiagMaskInf / OpDiagMaskZero::new(input,
+ * output, n_past) (:67-105, :144-160): a square matrix copied with -inf / 0
+ * where column > row + n_past; n_past >= 0, equal lengths, a square length,
+ * else INVALID_SHAPE.  The slices are device memory; the masks may run in
+ * place. */
+emel_status emel_op_diag(const float *input, uint64_t input_len, float *output, uint64_t output_len,
+                         emel_stream stream);
+emel_status emel_op_diag_mask_inf(const float *input, uint64_t input_len, float *output, uint64_t output_len,
+                                  int32_t n_past, emel_stream stream);
+emel_status emel_op_diag_mask_zero(const float *input, uint64_t input_len, float *output, uint64_t output_len,
+                                   int32_t n_past, emel_stream stream);
+/* group_norm::OpGroupNorm::new(input, output, groups, epsilon)
+ * (group_norm.rs:49-66, guards :179-196, run_group_norm :205-241): per batch
+ * and group of C/groups channels of a [W, H, C, B] view, mean and variance of
+ * the group's f32 elements summed in f64, y = (x - mean) / sqrt(var + eps).
+ * INVALID_VIEW (normalization_view_valid), SHAPE_MISMATCH, INVALID_PARAMETERS
+ * (groups 0 or not dividing C, epsilon negative or not finite).  Within 1e-5
+ * of the sequential f64 sums. */
+emel_status emel_op_group_norm(const emel_tensor_view *in, const emel_tensor_view_mut *out, uint64_t groups,
+                               float epsilon, emel_stream stream);
+/* group_norm::OpL2Norm::new(input, output) (group_norm.rs:68-78, :244-268):
+ * y = x / sqrt(sum of x*x), the sum sequential in f32 over the whole view.
+ * A sum that is not positive is EMEL_ERR_ZERO_NORM with nothing written: the
+ * call reads the sum back and waits for it, so it cannot be captured
+ * (EMEL_ERR_STREAM_CAPTURE). */
+emel_status emel_op_l2_norm(const emel_tensor_view *in, const emel_tensor_view_mut *out, emel_stream stream);
+
 /* emel_op_argmax_rows without any allocation.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid

@@ -831,3 +831,184 @@ int orc_slice_power(int sqrt_, const float *in, uint64_t in_len, float *out, uin
     return s;
 }
 
+
+/* ------------------------------------------------------------------ */
+/* Typed events of activation.rs, elementwise.rs, diag.rs and          */
+/* group_norm.rs                                                       */
+/* ------------------------------------------------------------------ */
+
+/* activation.rs views_valid + same_shape (:168-175). */
+static int activation_guard(const orc_view *in, const orc_view *out)
+{
+    if (orc_layout_validate(in, 0) || orc_layout_validate(out, 0)) return ORC_INVALID_VIEW;
+    if (!same_ne(in, out)) return ORC_SHAPE_MISMATCH;
+    return ORC_OK;
+}
+
+/* effect_clamp_execute (activation.rs:403-421): std::clamp's comparisons. */
+int orc_op_clamp(const orc_view *in, const orc_view *out, float min, float max)
+{
+    int s = activation_guard(in, out);
+    if (s) return s;
+    rview a = resolve(in), o = resolve(out);
+    for (uint64_t k = 0; k < a.count; k++) {
+        const float v = rd(&a, k);
+        wr(&o, k, v < min ? min : (v > max ? max : v));
+    }
+    return ORC_OK;
+}
+
+/* effect_leaky_relu_execute (activation.rs:507-520). */
+int orc_op_leaky_relu(const orc_view *in, const orc_view *out, float slope)
+{
+    int s = activation_guard(in, out);
+    if (s) return s;
+    rview a = resolve(in), o = resolve(out);
+    for (uint64_t k = 0; k < a.count; k++) {
+        const float v = rd(&a, k);
+        wr(&o, k, v < 0.0f ? v * slope : v);
+    }
+    return ORC_OK;
+}
+
+/* guard_silu_back_* (activation.rs:435-465), effect (:467-480). */
+int orc_op_silu_back(const orc_view *in, const orc_view *grad, const orc_view *out)
+{
+    if (orc_layout_validate(in, 0) || orc_layout_validate(grad, 0) || orc_layout_validate(out, 0))
+        return ORC_INVALID_VIEW;
+    if (!same_ne(in, grad) || !same_ne(in, out)) return ORC_SHAPE_MISMATCH;
+    rview a = resolve(in), g = resolve(grad), o = resolve(out);
+    for (uint64_t k = 0; k < a.count; k++) {
+        const float x = rd(&a, k);
+        const float sigmoid = 1.0f / (1.0f + expf(-x));
+        const float derivative = sigmoid * (1.0f + x * (1.0f - sigmoid));
+        wr(&o, k, rd(&g, k) * derivative);
+    }
+    return ORC_OK;
+}
+
+/* elementwise.rs guard_add1_* (:216-226), effect (:262-271). */
+int orc_op_add1(const orc_view *src, float scalar, const orc_view *dst)
+{
+    if (orc_layout_validate(src, 0) || orc_layout_validate(dst, 0)) return ORC_INVALID_VIEW;
+    if (!same_ne(src, dst)) return ORC_SHAPE_MISMATCH;
+    rview a = resolve(src), o = resolve(dst);
+    for (uint64_t k = 0; k < a.count; k++) wr(&o, k, rd(&a, k) + scalar);
+    return ORC_OK;
+}
+
+/* Layout::is_dense_contiguous (tensor_view.rs:281-314). */
+static int dense_contiguous(const orc_view *v)
+{
+    if (v->dtype != DT_F32) return 0;
+    unsigned __int128 expect = 4;
+    for (int d = 0; d < 4; d++) {
+        if (v->nb[d] != expect) return 0;
+        expect *= v->ne[d];
+    }
+    return 1;
+}
+
+/* OpAcc: the machine tries guard_acc_valid, _shape_invalid, _offset_invalid,
+ * _view_invalid in that order (elementwise.rs:110-116, :227-243); effect
+ * (:273-288). */
+int orc_op_acc(const orc_view *base, const orc_view *update, const orc_view *dst, uint64_t offset)
+{
+    const int pair = !orc_layout_validate(base, 0) && !orc_layout_validate(dst, 0) && !orc_layout_validate(update, 0);
+    const int views = pair && same_ne(base, dst) && dense_contiguous(base) && dense_contiguous(update) &&
+                      dense_contiguous(dst);
+    const uint64_t n = count_or_zero(dst), nu = count_or_zero(update);
+    const int offset_ok = offset <= n && nu <= n - offset;
+    if (views && offset_ok) {
+        rview b = resolve(base), u = resolve(update), o = resolve(dst);
+        for (uint64_t k = 0; k < b.count; k++) wr(&o, k, rd(&b, k));
+        for (uint64_t k = 0; k < u.count; k++) wr(&o, offset + k, rd(&o, offset + k) + rd(&u, k));
+        return ORC_OK;
+    }
+    if (pair && !same_ne(base, dst)) return ORC_SHAPE_MISMATCH;
+    if (views && !offset_ok) return ORC_INVALID_OFFSET;
+    return ORC_INVALID_VIEW;
+}
+
+/* diag.rs: square_side (:107-120), OpDiag::side (:57-64), apply_mask
+ * (:144-160), effect_diag (:332-344).  Slices, lengths in floats. */
+static int square_side(uint64_t len, uint64_t *side)
+{
+    if (len == 0) return 0;
+    uint64_t s = 1;
+    while (s * s < len) s++;
+    if (s * s != len) return 0;
+    *side = s;
+    return 1;
+}
+
+int orc_op_diag(const float *in, uint64_t in_len, float *out, uint64_t out_len)
+{
+    if (in_len == 0 || (unsigned __int128)in_len * in_len != out_len) return ORC_INVALID_SHAPE;
+    for (uint64_t k = 0; k < out_len; k++) out[k] = 0.0f;
+    for (uint64_t i = 0; i < in_len; i++) out[i * in_len + i] = in[i];
+    return ORC_OK;
+}
+
+int orc_op_diag_mask(int inf, const float *in, uint64_t in_len, float *out, uint64_t out_len, int32_t n_past)
+{
+    uint64_t side = 0;
+    if (!(n_past >= 0 && in_len == out_len && square_side(in_len, &side))) return ORC_INVALID_SHAPE;
+    const float masked = inf ? -INFINITY : 0.0f;
+    for (uint64_t row = 0; row < side; row++)
+        for (uint64_t col = 0; col < side; col++) {
+            const uint64_t index = row * side + col;
+            out[index] = col > row + (uint64_t)n_past ? masked : in[index];
+        }
+    return ORC_OK;
+}
+
+/* group_norm.rs: guards (:179-196), run_group_norm (:205-241). */
+int orc_op_group_norm(const orc_view *in, const orc_view *out, uint64_t groups, float eps)
+{
+    if (!orc_normalization_view_valid(in) || !orc_normalization_view_valid(out)) return ORC_INVALID_VIEW;
+    if (!same_ne(in, out)) return ORC_SHAPE_MISMATCH;
+    if (!(groups != 0 && in->ne[2] != 0 && in->ne[2] % groups == 0 && isfinite(eps) && eps >= 0.0f))
+        return ORC_INVALID_PARAMETERS;
+    rview a = resolve(in), o = resolve(out);
+    const uint64_t w = in->ne[0], h = in->ne[1], c = in->ne[2], b = in->ne[3], cpg = c / groups;
+    const uint64_t count = w * h * cpg;
+    for (uint64_t bt = 0; bt < b; bt++)
+        for (uint64_t g = 0; g < groups; g++) {
+            const uint64_t ch0 = g * cpg;
+            double sum = 0.0;
+            for (uint64_t ch = ch0; ch < ch0 + cpg; ch++)
+                for (uint64_t r = 0; r < h; r++)
+                    for (uint64_t col = 0; col < w; col++) sum += (double)rd(&a, col + w * (r + h * (ch + c * bt)));
+            const float mean = (float)(sum / (double)count);
+            double var = 0.0;
+            for (uint64_t ch = ch0; ch < ch0 + cpg; ch++)
+                for (uint64_t r = 0; r < h; r++)
+                    for (uint64_t col = 0; col < w; col++) {
+                        const float cen = rd(&a, col + w * (r + h * (ch + c * bt))) - mean;
+                        var += (double)cen * (double)cen;
+                    }
+            const float scale = 1.0f / sqrtf((float)(var / (double)count) + eps);
+            for (uint64_t ch = ch0; ch < ch0 + cpg; ch++)
+                for (uint64_t r = 0; r < h; r++)
+                    for (uint64_t col = 0; col < w; col++) {
+                        const uint64_t k = col + w * (r + h * (ch + c * bt));
+                        wr(&o, k, (rd(&a, k) - mean) * scale);
+                    }
+        }
+    return ORC_OK;
+}
+
+/* OpL2Norm: guards (:252-260, :290-305), run_l2_norm (:262-268). */
+int orc_op_l2_norm(const orc_view *in, const orc_view *out)
+{
+    if (!orc_normalization_view_valid(in) || !orc_normalization_view_valid(out)) return ORC_INVALID_VIEW;
+    if (!same_ne(in, out)) return ORC_SHAPE_MISMATCH;
+    rview a = resolve(in), o = resolve(out);
+    float sum = 0.0f;
+    for (uint64_t k = 0; k < a.count; k++) sum += rd(&a, k) * rd(&a, k);
+    if (!(sum > 0.0f)) return ORC_ZERO_NORM;
+    const float scale = 1.0f / sqrtf(sum);
+    for (uint64_t k = 0; k < a.count; k++) wr(&o, k, rd(&a, k) * scale);
+    return ORC_OK;
+}

@@ -45,6 +45,8 @@ enum {
     ORC_INDEX_OUT_OF_BOUNDS = 11,    /* GetRowsError::IndexOutOfBounds */
     ORC_UNSUPPORTED_SOURCE_STRIDE = 12, /* GetRowsError::UnsupportedSourceStride */
     ORC_INVALID_REQUEST = 13,        /* emel-logits SamplerError / ValidatorError::InvalidRequest */
+    ORC_INVALID_OFFSET = 15,         /* ElementwiseError::InvalidOffset */
+    ORC_ZERO_NORM = 16,              /* GroupNormError::ZeroNorm */
     ORC_PANIC = 99,                  /* the reference's guard passes and its executor panics */
 };
 
@@ -62,6 +64,16 @@ int orc_op_unary_event(int subop, const orc_view *in, const orc_view *out); /* t
 int orc_op_log(const orc_view *in, const orc_view *out);                    /* reductions::OpLog */
 int orc_op_sin(const orc_view *in, const orc_view *out);                    /* reductions::OpSin */
 int orc_op_cos(const orc_view *in, const orc_view *out);                    /* reductions::OpCos */
+/* activation.rs, elementwise.rs, diag.rs, group_norm.rs typed events. */
+int orc_op_clamp(const orc_view *in, const orc_view *out, float min, float max);
+int orc_op_leaky_relu(const orc_view *in, const orc_view *out, float slope);
+int orc_op_silu_back(const orc_view *in, const orc_view *grad, const orc_view *out);
+int orc_op_add1(const orc_view *src, float scalar, const orc_view *dst);
+int orc_op_acc(const orc_view *base, const orc_view *update, const orc_view *dst, uint64_t offset);
+int orc_op_diag(const float *in, uint64_t in_len, float *out, uint64_t out_len);
+int orc_op_diag_mask(int inf, const float *in, uint64_t in_len, float *out, uint64_t out_len, int32_t n_past);
+int orc_op_group_norm(const orc_view *in, const orc_view *out, uint64_t groups, float eps);
+int orc_op_l2_norm(const orc_view *in, const orc_view *out);
 int orc_op_scale(const orc_view *in, const orc_view *out, float scale);
 int orc_op_rms_norm(const orc_view *in, const orc_view *out, float eps);
 int orc_op_norm(const orc_view *in, const orc_view *out, float eps);

@@ -17,6 +17,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libemel_oracle.so"
 
 OK, INVALID_VIEW, SHAPE_MISMATCH, INVALID_PARAMETERS, UNEXPECTED_EVENT = 0, 1, 2, 3, 4
 INVALID_SHAPE = 9
+INVALID_OFFSET, ZERO_NORM = 15, 16
 ADD, SUB, MUL, DIV = 0, 1, 2, 3
 F32, F16, I32 = 0, 1, 26
 
@@ -68,6 +69,15 @@ _SIG = {
     "orc_op_log": [_P, _P],
     "orc_op_sin": [_P, _P],
     "orc_op_cos": [_P, _P],
+    "orc_op_clamp": [_P, _P, ctypes.c_float, ctypes.c_float],
+    "orc_op_leaky_relu": [_P, _P, ctypes.c_float],
+    "orc_op_silu_back": [_P, _P, _P],
+    "orc_op_add1": [_P, ctypes.c_float, _P],
+    "orc_op_acc": [_P, _P, _P, ctypes.c_uint64],
+    "orc_op_diag": [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_uint64],
+    "orc_op_diag_mask": [ctypes.c_int, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int32],
+    "orc_op_group_norm": [_P, _P, ctypes.c_uint64, ctypes.c_float],
+    "orc_op_l2_norm": [_P, _P],
     "orc_op_scale": [_P, _P, ctypes.c_float],
     "orc_op_rms_norm": [_P, _P, ctypes.c_float],
     "orc_op_norm": [_P, _P, ctypes.c_float],
@@ -140,6 +150,21 @@ def unary_event(subop, src, dst): return call("orc_op_unary_event", subop, src, 
 def log(src, dst): return call("orc_op_log", src, dst)
 def sin(src, dst): return call("orc_op_sin", src, dst)
 def cos(src, dst): return call("orc_op_cos", src, dst)
+def clamp(src, dst, lo, hi): return call("orc_op_clamp", src, dst, ctypes.c_float(lo), ctypes.c_float(hi))
+def leaky_relu(src, dst, slope): return call("orc_op_leaky_relu", src, dst, ctypes.c_float(slope))
+def silu_back(src, grad, dst): return call("orc_op_silu_back", src, grad, dst)
+def add1(src, scalar, dst): return call("orc_op_add1", src, ctypes.c_float(scalar), dst)
+def acc(base, update, dst, offset): return call("orc_op_acc", base, update, dst, ctypes.c_uint64(offset))
+def group_norm(src, dst, groups, eps): return call("orc_op_group_norm", src, dst, ctypes.c_uint64(groups), ctypes.c_float(eps))
+def l2_norm(src, dst): return call("orc_op_l2_norm", src, dst)
+
+
+def diag(inp: np.ndarray, out: np.ndarray) -> int:
+    return int(lib().orc_op_diag(inp.ctypes.data, inp.size, out.ctypes.data, out.size))
+
+
+def diag_mask(inf: bool, inp: np.ndarray, out: np.ndarray, n_past: int) -> int:
+    return int(lib().orc_op_diag_mask(int(inf), inp.ctypes.data, inp.size, out.ctypes.data, out.size, n_past))
 def scale(src, dst, s): return call("orc_op_scale", src, dst, ctypes.c_float(s))
 def rms_norm(src, dst, eps): return call("orc_op_rms_norm", src, dst, ctypes.c_float(eps))
 def norm(src, dst, eps): return call("orc_op_norm", src, dst, ctypes.c_float(eps))
