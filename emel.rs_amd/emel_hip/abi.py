@@ -200,11 +200,11 @@ class CView(ctypes.Structure):
 
     _fields_ = [
         ("data", ctypes.c_void_p),
-        ("data_bytes", ctypes.c_uint64),
         ("dtype", ctypes.c_uint32),
         ("reserved", ctypes.c_uint32),
         ("ne", ctypes.c_uint64 * 4),
         ("nb", ctypes.c_uint64 * 4),
+        ("data_bytes", ctypes.c_uint64),
     ]
 
 

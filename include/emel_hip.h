@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define EMEL_HIP_ABI_VERSION 1u
+#define EMEL_HIP_ABI_VERSION 2u
 
 /* Status codes.  One code per variant of the reference's typed errors:
  * BinaryError / BroadcastError / UnaryError / ReductionError /
@@ -121,22 +121,26 @@ typedef enum emel_binary_op {
     EMEL_BINARY_DIV = 3
 } emel_binary_op;
 
+/* The first 80 bytes are the pinned C++ tensor_view {data, type, ne, nb}
+ * (tools/emel-kernel-binary-reference/main.cpp:14-30, with its 4-byte dtype
+ * enum padded to 8): a view in that format becomes this one by setting
+ * reserved to 0 and appending data_bytes. */
 typedef struct emel_tensor_view {
     const void *data;
-    uint64_t data_bytes;
     uint32_t dtype;
     uint32_t reserved; /* must be 0 */
     uint64_t ne[4];
     uint64_t nb[4];
+    uint64_t data_bytes;
 } emel_tensor_view;
 
 typedef struct emel_tensor_view_mut {
     void *data;
-    uint64_t data_bytes;
     uint32_t dtype;
     uint32_t reserved; /* must be 0 */
     uint64_t ne[4];
     uint64_t nb[4];
+    uint64_t data_bytes;
 } emel_tensor_view_mut;
 
 typedef void *emel_stream; /* hipStream_t */

@@ -25,11 +25,11 @@ extern "C" {
 /* Same memory layout as emel_tensor_view in include/emel_hip.h. */
 typedef struct orc_view {
     void *data;          /* host pointer */
-    uint64_t data_bytes; /* bytes owned at data (Rust slice len * 4) */
     uint32_t dtype;      /* wire dtype code: F32=0, F16=1, I32=26 */
     uint32_t reserved;
     uint64_t ne[4];
     uint64_t nb[4];
+    uint64_t data_bytes; /* bytes owned at data (Rust slice len * 4) */
 } orc_view;
 
 /* Status codes: identical numbering to emel_status in include/emel_hip.h. */

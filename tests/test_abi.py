@@ -31,15 +31,17 @@ def test_every_declared_symbol_is_exported():
 
 def test_abi_version_and_status_strings():
     lib = eh.load()
-    assert lib.emel_abi_version() == 1
+    assert lib.emel_abi_version() == 2
     for s in eh.Status:
         assert lib.emel_status_string(int(s)).decode()
 
 
 def test_struct_layout_matches_header():
-    # emel_tensor_view: pointer, u64, u32, u32, u64[4], u64[4]
-    assert ctypes.sizeof(CView) == 8 + 8 + 4 + 4 + 32 + 32
-    assert CView.ne.offset == 24 and CView.nb.offset == 56
+    # emel_tensor_view: pointer, u32 dtype, u32 reserved, u64[4], u64[4], u64 data_bytes -- the pinned
+    # C++ tensor_view {data, type, ne, nb} (80 bytes) followed by data_bytes
+    assert ctypes.sizeof(CView) == 8 + 4 + 4 + 32 + 32 + 8
+    assert CView.dtype.offset == 8 and CView.ne.offset == 16 and CView.nb.offset == 48
+    assert CView.data_bytes.offset == 80
 
 
 def random_layouts(seed, count):
