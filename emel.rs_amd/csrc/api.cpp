@@ -382,6 +382,9 @@ void free_state(StreamState &st)
 
 emel_status launched(hipError_t e)
 {
+    if (e == hipErrorStreamCaptureUnsupported)
+        return fail(EMEL_ERR_STREAM_CAPTURE, "a step the call needs is not permitted while the stream is being "
+                                             "captured (the first GELU on a device builds its table and waits)");
     if (e != hipSuccess) return hip_fail(e, "kernel launch");
     g_last_error.clear();
     return EMEL_OK;
@@ -1296,13 +1299,11 @@ bool f16_view_valid(const emel_tensor_view &s)
     return half_span_ok(s, st);
 }
 
-constexpr uint32_t kDtypeBf16 = 30, kDtypeQ4_0 = 2, kDtypeQ8_0 = 8, kDtypeQ4K = 12;
-
 // Bf16View::validate (get_rows.rs:302-343).
 bool bf16_view_valid(const emel_tensor_view &s)
 {
     uint64_t st[4], count;
-    if (s.dtype != kDtypeBf16 || !element_count(s, count) || !half_strides(s, st)) return false;
+    if (s.dtype != EMEL_DTYPE_BF16 || !element_count(s, count) || !half_strides(s, st)) return false;
     if (s.nb[0] != 0)
         for (int d = 0; d < 4; ++d)
             if ((s.ne[d] > 1 && s.nb[d] == 0) || (s.nb[d] != 0 && (s.nb[d] < 2 || s.nb[d] % 2 != 0))) return false;
@@ -1352,10 +1353,10 @@ emel_status get_rows(GrKind kind, const emel_tensor_view *src, const emel_index_
     case GrKind::F32: src_ok = n == 0 ? empty_source_valid(s, EMEL_DTYPE_F32, 4, false) : valid_f32(s, true); break;
     case GrKind::F32Bytes: src_ok = n == 0 ? empty_source_valid(s, EMEL_DTYPE_F32, 4, true) : byte_view_valid(s); break;
     case GrKind::F16: src_ok = f16_view_valid(s); if (n == 0) dst_ok = valid_f32(*dst, false) && dense_for(*dst, EMEL_DTYPE_F32, 4); break;
-    case GrKind::Bf16: src_ok = n == 0 ? empty_source_valid(s, kDtypeBf16, 2, false) : bf16_view_valid(s); break;
-    case GrKind::Q4_0: src_ok = packed_view_valid(s, kDtypeQ4_0, 32, 18); break;
-    case GrKind::Q8_0: src_ok = packed_view_valid(s, kDtypeQ8_0, 32, 34); break;
-    case GrKind::Q4K: src_ok = packed_view_valid(s, kDtypeQ4K, 256, 144); break;
+    case GrKind::Bf16: src_ok = n == 0 ? empty_source_valid(s, EMEL_DTYPE_BF16, 2, false) : bf16_view_valid(s); break;
+    case GrKind::Q4_0: src_ok = packed_view_valid(s, EMEL_DTYPE_Q4_0, 32, 18); break;
+    case GrKind::Q8_0: src_ok = packed_view_valid(s, EMEL_DTYPE_Q8_0, 32, 34); break;
+    case GrKind::Q4K: src_ok = packed_view_valid(s, EMEL_DTYPE_Q4_K, 256, 144); break;
     }
     if (!ix.valid || !src_ok || !dst_ok) return fail(EMEL_ERR_INVALID_VIEW, "get_rows view failed validation");
     // shape_valid (get_rows.rs:966-975)

@@ -82,6 +82,12 @@ hipError_t device_info(hipStream_t stream, bool need_gelu, DeviceInfo &out)
         if (d.cus <= 0) d.cus = 1;
     }
     if (need_gelu && !d.gelu_ready) {
+        // Building the table ends with a wait, which a stream under capture
+        // cannot do: the first GELU on a device must run eagerly.
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        e = hipStreamIsCapturing(stream, &cs);
+        if (e != hipSuccess) return e;
+        if (cs != hipStreamCaptureStatusNone) return hipErrorStreamCaptureUnsupported;
         k_gelu_table<<<dim3((kGeluTableHalfs + kBlock - 1) / kBlock), kBlock, 0, stream>>>();
         e = hipGetLastError();
         if (e == hipSuccess) e = hipStreamSynchronize(stream); // visible to every stream from now on

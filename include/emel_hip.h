@@ -68,11 +68,17 @@ typedef enum emel_status {
     EMEL_ERR_ZERO_NORM = 16        /* GroupNormError::ZeroNorm (group_norm.rs:15-23): OpL2Norm */
 } emel_status;
 
-/* Wire dtype codes, DType::from_code (tensor_view.rs:111-158). */
+/* Wire dtype codes, DType::from_code (crates/emel-kernels/src/any/
+ * tensor_view.rs:111-158): the codes some entry point of this library reads.
+ * Views of any other code (0..255) are carried and validated, never read. */
 typedef enum emel_dtype {
     EMEL_DTYPE_F32 = 0,
     EMEL_DTYPE_F16 = 1,
-    EMEL_DTYPE_I32 = 26
+    EMEL_DTYPE_Q4_0 = 2,
+    EMEL_DTYPE_Q8_0 = 8,
+    EMEL_DTYPE_Q4_K = 12,
+    EMEL_DTYPE_I32 = 26,
+    EMEL_DTYPE_BF16 = 30
 } emel_dtype;
 
 /* Unary wire subop codes, UnarySubOp (unary.rs:101-146).  OpUnary and the
@@ -520,11 +526,10 @@ typedef struct emel_generic_request {
  * Routed on the device: dup, add, sub, mul, div, add1, scale, clamp,
  * leaky_relu, silu_back, cumsum, repeat, repeat_back, concat, diag,
  * diag_mask_inf/zero, soft_max, soft_max_back, norm, rms_norm, rms_norm_back,
- * l2_norm, count_equal, fill, arange, sum, mean, argmax, sqr, sqrt, unary
- * (abs, neg, tanh, elu, relu, gelu, silu, exp), mul_mat (F32 and F16) and
- * mul_mat_argmax.  Divergences, each reported before anything is enqueued:
- *   - log / sin / cos pass their route in the reference but return
- *     EMEL_ERR_UNSUPPORTED_OPERATION (no bit-exact glibc logf/sinf/cosf);
+ * l2_norm, count_equal, fill, arange, sum, mean, argmax, sqr, sqrt, log, sin,
+ * cos (glibc-exact logf/sinf/cosf), unary (abs, neg, tanh, elu, relu, gelu,
+ * silu, exp), mul_mat (F32 and F16) and mul_mat_argmax.  Divergences, each
+ * reported before anything is enqueued:
  *   - views the reference reads byte-wise but that are not element-aligned
  *     (an F32 data pointer or stride not a multiple of 4), and destinations
  *     whose elements may overlap one another, are
