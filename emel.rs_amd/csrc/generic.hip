@@ -6,8 +6,9 @@
 // depends on the order of its additions, so each kernel gives one lane the
 // reference's whole loop for its unit of independent work, in the
 // reference's order:
-//   k_gen_rows      one lane per row: cumsum, soft_max (f32 sum), norm and
-//                   rms_norm (f64 sums, f64 scale), soft_max_back, rms_norm_back;
+//   k_gen_rows      one lane per row: cumsum, norm and rms_norm (f64 sums,
+//                   f64 scale), soft_max_back, rms_norm_back (soft_max uses
+//                   the typed strided path's exact sequential-sum kernel);
 //   k_gen_ord       one lane per destination element: fill, arange, diag,
 //                   diag_mask_inf/zero, concat, repeat_back (the source
 //                   elements of one target summed in source-ordinal order);
@@ -74,11 +75,6 @@ __device__ __forceinline__ int64_t coords_offset(const GView &v, const uint64_t 
 template <GenRow OP>
 __global__ __launch_bounds__(kRowBlock) void k_gen_rows(GenRowArgs a)
 {
-    __shared__ uint64_t lds[32];
-    if constexpr (OP == GenRow::SoftMax) {
-        if (threadIdx.x < 32) lds[threadIdx.x] = kExp2Table[threadIdx.x];
-        __syncthreads();
-    }
     const uint64_t r = static_cast<uint64_t>(blockIdx.x) * kRowBlock + threadIdx.x;
     if (r >= a.rows) return;
     const float *x = static_cast<const float *>(a.x.data);
@@ -96,30 +92,6 @@ __global__ __launch_bounds__(kRowBlock) void k_gen_rows(GenRowArgs a)
             y[y0.off] = sum;
             x0.next(a.x);
             y0.next(a.y);
-        }
-    } else if constexpr (OP == GenRow::SoftMax) { // generic.rs:1948-1986
-        const ExpfConsts ec = expf_consts_in_vgprs();
-        Walk xi = x0;
-        float mx = -__builtin_inff(); // f32::max from -inf: NaN never replaces it
-        for (uint64_t c = 0; c < w; ++c) {
-            const float v = x[xi.off];
-            if (v > mx) mx = v;
-            xi.next(a.x);
-        }
-        xi = x0;
-        Walk yi = y0;
-        float sum = 0.0f;
-        for (uint64_t c = 0; c < w; ++c) {
-            const float e = emel_expf(x[xi.off] - mx, lds, ec);
-            y[yi.off] = e;
-            sum += e;
-            xi.next(a.x);
-            yi.next(a.y);
-        }
-        yi = y0;
-        for (uint64_t c = 0; c < w; ++c) {
-            y[yi.off] = y[yi.off] / sum;
-            yi.next(a.y);
         }
     } else if constexpr (OP == GenRow::Norm || OP == GenRow::RmsNorm) { // generic.rs:1988-2055
         Walk xi = x0;
@@ -482,7 +454,11 @@ hipError_t launch_generic_rows(const GenRowArgs &a, hipStream_t s)
     const dim3 grid(static_cast<uint32_t>(blocks));
     switch (a.op) {
     case GenRow::Cumsum: k_gen_rows<GenRow::Cumsum><<<grid, kRowBlock, 0, s>>>(a); break;
-    case GenRow::SoftMax: k_gen_rows<GenRow::SoftMax><<<grid, kRowBlock, 0, s>>>(a); break;
+    case GenRow::SoftMax: { // generic.rs:1948-1986: the exact sequential-sum kernel of the typed strided path
+        const Operand x{a.x.data, {a.x.ne[0], a.x.ne[1], a.x.ne[2], a.x.ne[3]}, {a.x.st[0], a.x.st[1], a.x.st[2], a.x.st[3]}};
+        const Operand y{a.y.data, {a.y.ne[0], a.y.ne[1], a.y.ne[2], a.y.ne[3]}, {a.y.st[0], a.y.st[1], a.y.st[2], a.y.st[3]}};
+        return launch_softmax_seq(x, y, s);
+    }
     case GenRow::Norm: k_gen_rows<GenRow::Norm><<<grid, kRowBlock, 0, s>>>(a); break;
     case GenRow::RmsNorm: k_gen_rows<GenRow::RmsNorm><<<grid, kRowBlock, 0, s>>>(a); break;
     case GenRow::SoftMaxBack: k_gen_rows<GenRow::SoftMaxBack><<<grid, kRowBlock, 0, s>>>(a); break;

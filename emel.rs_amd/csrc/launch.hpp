@@ -85,6 +85,10 @@ struct RowArgs {
 
 hipError_t launch_rows(const RowArgs &args, hipStream_t stream);
 
+// soft_max rows of x (ne[0] columns) with the sequential f32 row sum, into y
+// (the same element count, addressed by its own ordinals).
+hipError_t launch_softmax_seq(const Operand &x, const Operand &y, hipStream_t stream);
+
 // OpGroupNorm (group_norm.rs:197-241): x and y share extents [W, H, C, B];
 // group g of batch b is channels [g C/groups, (g+1) C/groups).
 hipError_t launch_group_norm(const Operand &x, const Operand &y, uint32_t groups, float eps, hipStream_t stream);

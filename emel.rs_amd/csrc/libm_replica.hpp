@@ -20,6 +20,11 @@
 //   emel_logf    ARM optimized-routines logf (math/logf.c, in glibc since
 //                2.28): a 16-entry (1/c, log c) table and a cubic in
 //                r = z/c - 1, in double (emel-logits' sampler, f32::ln).
+//   emel_sinf, emel_cosf
+//                ARM optimized-routines sinf / cosf (math/sinf.c, cosf.c,
+//                sincosf.h, sincosf_data.c): reduction by pi/2 in double,
+//                Payne-Hanek for large inputs, even/odd polynomials.
+//   emel_log1pf  fdlibm s_log1pf.c (softplus).
 //
 // The table holds the correctly rounded doubles of 2^(i/32).  glibc stores
 // them with i << 47 subtracted and forms 2^(k/32) as tab[k % 32] + (k << 47)
@@ -29,6 +34,45 @@
 // Every function is __host__ __device__: tests build them for the CPU and
 // compare them with the host glibc over all 2^32 float inputs.  Compile
 // with -ffp-contract=off: the only fused operations are the explicit fma().
+//
+// The constants, tables and steps of the functions above are those of the
+// two published implementations named, restated in this file's own code;
+// their licences ask for these notices:
+//
+// ---- fdlibm (emel_expm1f, emel_tanhf, emel_log1pf) --------------------------
+// Copyright (C) 1993 by Sun Microsystems, Inc. All rights reserved.
+//
+// Developed at SunPro, a Sun Microsystems, Inc. business.
+// Permission to use, copy, modify, and distribute this
+// software is freely granted, provided that this notice
+// is preserved.
+//
+// (The float versions s_expm1f.c, s_tanhf.c and s_log1pf.c are the
+// conversion to float by Ian Lance Taylor, Cygnus Support.)
+//
+// ---- ARM optimized-routines (emel_expf, emel_logf, emel_sinf, emel_cosf) ---
+// Copyright (c) 2017-2018 Arm Limited.
+// SPDX-License-Identifier: MIT (the project is MIT OR Apache-2.0 WITH
+// LLVM-exception; the MIT terms are taken here):
+//
+// Permission is hereby granted, free of charge, to any person obtaining a
+// copy of this software and associated documentation files (the
+// "Software"), to deal in the Software without restriction, including
+// without limitation the rights to use, copy, modify, merge, publish,
+// distribute, sublicense, and/or sell copies of the Software, and to permit
+// persons to whom the Software is furnished to do so, subject to the
+// following conditions:
+//
+// The above copyright notice and this permission notice shall be included
+// in all copies or substantial portions of the Software.
+//
+// THE SOFTWARE IS PROVIDED "AS IS", WITHOUT WARRANTY OF ANY KIND, EXPRESS
+// OR IMPLIED, INCLUDING BUT NOT LIMITED TO THE WARRANTIES OF
+// MERCHANTABILITY, FITNESS FOR A PARTICULAR PURPOSE AND NONINFRINGEMENT. IN
+// NO EVENT SHALL THE AUTHORS OR COPYRIGHT HOLDERS BE LIABLE FOR ANY CLAIM,
+// DAMAGES OR OTHER LIABILITY, WHETHER IN AN ACTION OF CONTRACT, TORT OR
+// OTHERWISE, ARISING FROM, OUT OF OR IN CONNECTION WITH THE SOFTWARE OR THE
+// USE OR OTHER DEALINGS IN THE SOFTWARE.
 #pragma once
 
 #include <hip/hip_runtime.h>

@@ -17,6 +17,7 @@
 #include "common.hpp"
 #include "launch.hpp"
 #include "libm_replica.hpp"
+#include "seqsum.hpp"
 
 namespace emel {
 namespace {
@@ -427,13 +428,37 @@ __global__ __launch_bounds__(kBlock) void k_softmax_generic(OrdView xv, OrdView 
     }
 }
 
-// Strided soft_max (reductions.rs:603-638): the f32 sum is sequential, so
-// each lane owns a row and adds its exponentials in column order.
-__global__ __launch_bounds__(kBlock) void k_softmax_seq(OrdView xv, OrdView yv, uint64_t rows, uint64_t ncols,
-                                                         const float *x, float *y)
+// Strided soft_max (reductions.rs:603-638) and the generic envelope's
+// soft_max (generic.rs:1948-1986): the row sum is the sequential f32 sum
+// s_k = RN(s_{k-1} + e_k) in column order.  One workgroup of NT threads per
+// row:
+//   1. the row maximum, all threads (the order does not matter: NaN never
+//      wins, and a NaN or an infinity turns the row into NaN through its sum
+//      in either formulation);
+//   2. per tile of NT * SEG columns, every thread computes its e = expf(x -
+//      max) and stages it in LDS in column order; the tile is then added to
+//      the running sum exactly (seq_tile_sum below);
+//   3. y = e / sum, the correctly rounded quotient (div_by_recip, sum >= 1).
+// Column c of row r is ordinal r * ncols + c of each view; x has ncols ==
+// ne[0], so its offset is the row's offset plus c * st[0].  y shares that
+// form when its ne[0] is ncols (kYRow), else its ordinal is decoded.
+// Rows of at most kSeqShort columns take one lane each instead: the
+// reference's own loop, short enough that a workgroup per row would idle.
+constexpr uint64_t kSeqShort = 64;
+
+__device__ __forceinline__ int64_t row_offset(const OrdView &v, uint64_t r)
 {
-    __shared__ uint64_t lds[32];
-    if (threadIdx.x < 32) lds[threadIdx.x] = kExp2Table[threadIdx.x];
+    const uint64_t i1 = r % v.ne[1];
+    const uint64_t q = r / v.ne[1];
+    return static_cast<int64_t>(i1) * v.st[1] + static_cast<int64_t>(q % v.ne[2]) * v.st[2] +
+           static_cast<int64_t>(q / v.ne[2]) * v.st[3];
+}
+
+__global__ __launch_bounds__(kBlock) void k_softmax_lane(OrdView xv, OrdView yv, uint64_t rows, uint64_t ncols,
+                                                          const float *x, float *y)
+{
+    __shared__ uint64_t tab[32];
+    if (threadIdx.x < 32) tab[threadIdx.x] = kExp2Table[threadIdx.x];
     __syncthreads();
     const uint64_t r = static_cast<uint64_t>(blockIdx.x) * kBlock + threadIdx.x;
     if (r >= rows) return;
@@ -445,7 +470,7 @@ __global__ __launch_bounds__(kBlock) void k_softmax_seq(OrdView xv, OrdView yv, 
     }
     float sum = 0.0f;
     for (uint64_t c = 0; c < ncols; ++c) {
-        const float e = emel_expf_nonpos(x[ord_index(xv, base + c)] - mx, lds);
+        const float e = emel_expf_nonpos(x[ord_index(xv, base + c)] - mx, tab);
         y[ord_index(yv, base + c)] = e;
         sum += e;
     }
@@ -453,6 +478,309 @@ __global__ __launch_bounds__(kBlock) void k_softmax_seq(OrdView xv, OrdView yv, 
     for (uint64_t c = 0; c < ncols; ++c) {
         const int64_t o = ord_index(yv, base + c);
         y[o] = div_by_recip(y[o], recip);
+    }
+}
+
+// The exact sequential sum of one staged tile (seqsum.hpp), in two steps.
+//
+// Predict, all threads: thread t owns the tile's addends SEG t .. SEG t +
+// SEG - 1 (segment t).  The running sum before them is within
+// seq_rel_bound of the exact value s_prev + (f64 prefix of the tile),
+// s_prev being the exact running sum before the tile.  When that interval,
+// widened to the end of the segment, lies in one binade [2^(E-1), 2^E) and
+// no addend is a rounding tie on its grid 2^u (u = E - 24), every addition
+// inside the segment adds round(e / 2^u) units: the segment is predictable
+// and its contribution is an integer.  Its units are scanned over the
+// tile, and the unpredictable segments are listed in order.
+//
+// Combine, wave 0: between two unpredictable segments lies a run of
+// predictable ones, all in one binade (the running sum is monotone and
+// consecutive intervals overlap), so the run adds the difference of two
+// scanned unit counts at once -- checked against the exact state, with a
+// fallback that adds the whole tile one addend at a time.  Each
+// unpredictable segment is added one f32 addition at a time, the
+// reference's own arithmetic, and the state restarts from the result.  A
+// row takes one walk per binade crossing and per segment holding a tie.
+constexpr int32_t kNoGrid = -1000; // u of an unpredictable segment
+
+// What the combine needs of the i-th unpredictable segment f, in one
+// 16-byte-aligned record: f, the scanned units before it, the grid of the
+// segments on either side of it (the last of the run before it, the first
+// of the run after it) and its own addends.  Record nfail is a sentinel
+// with f = NT, the tile's total units and the last segment's grid.
+template <uint32_t SEG>
+struct alignas(16) FailRec {
+    uint32_t f;
+    uint32_t units; // units[f]: predictable units before segment f
+    int32_t u_before; // u[f - 1] (kNoGrid for f = 0)
+    int32_t u_after;  // u[f + 1] (kNoGrid past the tile)
+    float e[SEG];
+};
+
+template <uint32_t NT, uint32_t SEG>
+struct SeqScratch {
+    int32_t u[NT]; // grid exponent per segment, kNoGrid if unpredictable
+    FailRec<SEG> rec[NT + 1];
+    uint32_t wave_units[NT / kWave];
+    uint32_t wave_fail[NT / kWave];
+    double wave_sum[NT / kWave];
+};
+
+// Adds segment g's addends to acc one by one.
+template <uint32_t SEG>
+__device__ __forceinline__ float walk_segment(const float *s_e, uint32_t g, float acc)
+{
+    const float4 *q = reinterpret_cast<const float4 *>(s_e + SEG * g);
+#pragma unroll
+    for (uint32_t j = 0; j < SEG / 4; ++j) {
+        const float4 v = q[j];
+        acc += v.x;
+        acc += v.y;
+        acc += v.z;
+        acc += v.w;
+    }
+    return acc;
+}
+
+template <uint32_t NT, uint32_t SEG>
+__device__ __forceinline__ void seq_tile_sum(const float *s_e, SeqScratch<NT, SEG> &sc, float s_prev, SumState &st)
+{
+    constexpr uint32_t NW = NT / kWave;
+    const uint32_t t = threadIdx.x;
+    const uint32_t wave = t / kWave, lane = t % kWave;
+    float e[SEG];
+#pragma unroll
+    for (uint32_t j = 0; j < SEG; j += 4) {
+        const float4 q = *reinterpret_cast<const float4 *>(&s_e[SEG * t + j]);
+        e[j] = q.x;
+        e[j + 1] = q.y;
+        e[j + 2] = q.z;
+        e[j + 3] = q.w;
+    }
+    double part[4]; // four partial sums: a short dependency chain
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) part[j] = static_cast<double>(e[j]);
+#pragma unroll
+    for (uint32_t j = 4; j < SEG; ++j) part[j % 4] += static_cast<double>(e[j]);
+    const double seg = (part[0] + part[1]) + (part[2] + part[3]);
+    const double incl = wave_incl_scan_f64(seg);
+    if (lane == kWave - 1) sc.wave_sum[wave] = incl;
+    __syncthreads();
+    // the exclusive prefix as a sum of whole segments (never incl - seg,
+    // whose cancellation error is not relative to the prefix): positive
+    // terms, so its f64 error is relative, within seq_rel_bound's slack
+    const double up = __shfl_up(incl, 1, kWave);
+    double pre = lane == 0 ? 0.0 : up;
+    for (uint32_t w = 0; w < wave; ++w) pre += sc.wave_sum[w];
+    const double base = static_cast<double>(s_prev) + pre;
+    const double lo = base * (1.0 - seq_rel_bound(static_cast<double>(SEG * t)));
+    const double hi = (base + seg) * (1.0 + seq_rel_bound(static_cast<double>(SEG * t + SEG)));
+    int elo = 0, ehi = 0;
+    (void)__builtin_frexp(lo, &elo);
+    (void)__builtin_frexp(hi, &ehi);
+    bool ok = lo >= 0x1p-126 && hi < 0x1p127 && lo <= hi && elo == ehi;
+    const int32_t u = elo - 1 - 23;
+    uint32_t units = 0;
+    if (ok) {
+#pragma unroll
+        for (uint32_t j = 0; j < SEG; ++j) {
+            bool tie;
+            units += seq_units(e[j], u, tie);
+            ok = ok && !tie;
+        }
+    }
+    units = ok ? units : 0u;
+    sc.u[t] = ok ? u : kNoGrid;
+    // scan of units and compaction of the unpredictable segments
+    const uint32_t uincl = wave_incl_scan(units);
+    const uint64_t failing = __ballot(!ok);
+    if (lane == kWave - 1) {
+        sc.wave_units[wave] = uincl;
+        sc.wave_fail[wave] = static_cast<uint32_t>(__builtin_popcountll(failing));
+    }
+    __syncthreads();
+    uint32_t ubase = 0, fbase = 0, nfail = 0, total = 0;
+#pragma unroll
+    for (uint32_t w = 0; w < NW; ++w) {
+        const uint32_t wu = sc.wave_units[w], wf = sc.wave_fail[w];
+        ubase += w < wave ? wu : 0u;
+        fbase += w < wave ? wf : 0u;
+        nfail += wf;
+        total += wu;
+    }
+    if (!ok) {
+        FailRec<SEG> &r = sc.rec[fbase + static_cast<uint32_t>(__builtin_popcountll(failing & ((uint64_t{1} << lane) - 1)))];
+        r.f = t;
+        r.units = ubase + uincl; // units contributes 0
+        r.u_before = t > 0 ? sc.u[t - 1] : kNoGrid;
+        r.u_after = t + 1 < NT ? sc.u[t + 1] : kNoGrid;
+#pragma unroll
+        for (uint32_t j = 0; j < SEG; ++j) r.e[j] = e[j];
+    }
+    if (t == NT - 1) {
+        FailRec<SEG> &r = sc.rec[nfail];
+        r.f = NT;
+        r.units = total;
+        r.u_before = sc.u[NT - 1];
+        r.u_after = kNoGrid;
+    }
+    __syncthreads();
+    if (wave != 0 || !st.finite) return;
+
+    // Wave 0 runs the combine as uniform code: every value it reads from LDS
+    // is the same in all lanes and moved to a scalar register, so the
+    // control flow is scalar; the next record is loaded while the current
+    // one is used.
+    auto uni = [](uint32_t v) { return static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v))); };
+    const uint32_t nrec = uni(nfail);
+    uint32_t m = st.m;
+    int32_t gu = st.u;     // the state's grid exponent
+    bool bad = false;      // a run failed its check against the exact state
+    uint32_t prev_f1 = 0;  // first segment after the previous record's
+    uint32_t prev_units = 0;
+    int32_t prev_after = static_cast<int32_t>(uni(static_cast<uint32_t>(sc.u[0])));
+    FailRec<SEG> cur = sc.rec[0];
+    for (uint32_t i = 0; i <= nrec; ++i) {
+        const FailRec<SEG> ahead = sc.rec[i < nrec ? i + 1 : nrec];
+        const uint32_t f = uni(cur.f);
+        if (f > prev_f1) { // the run prev_f1 .. f - 1 of predictable segments
+            const uint32_t add = uni(cur.units) - prev_units;
+            const int32_t u_last = static_cast<int32_t>(uni(static_cast<uint32_t>(cur.u_before)));
+            bad = bad || !(prev_after == gu && u_last == gu && m + add < kSeqLimit);
+            m += add;
+        }
+        if (f == NT) break;
+        // segment f, one f32 addition at a time
+        float acc = seq_value(m, gu);
+#pragma unroll
+        for (uint32_t j = 0; j < SEG; ++j) acc += cur.e[j];
+        acc = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, acc)));
+        if (!(acc < __builtin_inff())) { // NaN (the addends are at most 1: never +inf)
+            st.finite = false;
+            st.special = acc;
+            return;
+        }
+        const SeqState h = seq_state(acc);
+        m = h.m;
+        gu = h.u;
+        prev_f1 = f + 1;
+        prev_units = uni(cur.units);
+        prev_after = static_cast<int32_t>(uni(static_cast<uint32_t>(cur.u_after)));
+        cur = ahead;
+    }
+    if (!bad) {
+        st.m = m;
+        st.u = gu;
+        return;
+    }
+    // Not expected (the predictions carry a proven bound): the whole tile
+    // again from its exact starting value, one addition at a time.
+    float acc = s_prev;
+    for (uint32_t g = 0; g < NT; ++g) acc = walk_segment<SEG>(s_e, g, acc);
+    acc = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, acc)));
+    if (!(acc < __builtin_inff())) {
+        st.finite = false;
+        st.special = acc;
+        return;
+    }
+    const SeqState h = seq_state(acc);
+    st.m = h.m;
+    st.u = h.u;
+}
+
+// kOneTile: the row fits one tile (ncols <= NT * SEG), so each thread keeps
+// its exponentials in registers across the walk and writes y once.  Every
+// pass issues a thread's SEG loads before using any of them (a store to y
+// between loads would otherwise wait for each load in turn: x and y may be
+// the same memory).
+template <uint32_t NT, uint32_t SEG, bool kYRow, bool kOneTile>
+__global__ __launch_bounds__(NT) void k_softmax_seq(OrdView xv, OrdView yv, uint64_t ncols, const float *x, float *y)
+{
+    constexpr uint32_t TILE = NT * SEG;
+    constexpr uint32_t NW = NT / kWave;
+    __shared__ uint64_t tab[32];
+    __shared__ __align__(16) float s_e[TILE];
+    __shared__ SeqScratch<NT, SEG> s_seq;
+    __shared__ float s_red[NW];
+    __shared__ float s_total;
+    if (threadIdx.x < 32) tab[threadIdx.x] = kExp2Table[threadIdx.x];
+    const uint32_t wave = threadIdx.x / kWave;
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint64_t r = blockIdx.x;
+    const int64_t xrow = row_offset(xv, r);
+    const int64_t yrow = kYRow ? row_offset(yv, r) : 0;
+    const int64_t xs0 = xv.st[0], ys0 = yv.st[0];
+    auto yoff = [&](uint64_t c) { return kYRow ? yrow + static_cast<int64_t>(c) * ys0 : ord_index(yv, r * ncols + c); };
+    // column j of this thread in the tile at t0 (clamped to the tile's first
+    // column past its end: the loads stay unconditional and in bounds)
+    auto col = [&](uint64_t t0, uint32_t n, uint32_t j) {
+        const uint32_t c = threadIdx.x + NT * j;
+        return t0 + (c < n ? c : 0u);
+    };
+    auto tile_n = [&](uint64_t t0) { return ncols - t0 < TILE ? static_cast<uint32_t>(ncols - t0) : TILE; };
+
+    // 1. maximum (NaN never wins; NaN and infinities reach the sum instead)
+    float v[SEG];
+    float mx = -__builtin_inff();
+    for (uint64_t t0 = 0; t0 < ncols; t0 += TILE) {
+        const uint32_t n = tile_n(t0);
+#pragma unroll
+        for (uint32_t j = 0; j < SEG; ++j) v[j] = x[xrow + static_cast<int64_t>(col(t0, n, j)) * xs0];
+#pragma unroll
+        for (uint32_t j = 0; j < SEG; ++j) mx = threadIdx.x + NT * j < n ? __builtin_fmaxf(mx, v[j]) : mx;
+    }
+    mx = wave_max_dpp(mx);
+    if (lane == 0) s_red[wave] = mx;
+    __syncthreads();
+    mx = s_red[0];
+#pragma unroll
+    for (uint32_t w = 1; w < NW; ++w) mx = __builtin_fmaxf(mx, s_red[w]);
+
+    // 2. exponentials and the sequential sum
+    SumState st{0u, -149, true, 0.0f};
+    for (uint64_t t0 = 0; t0 < ncols; t0 += TILE) {
+        const uint32_t n = tile_n(t0);
+        if constexpr (!kOneTile) {
+#pragma unroll
+            for (uint32_t j = 0; j < SEG; ++j) v[j] = x[xrow + static_cast<int64_t>(col(t0, n, j)) * xs0];
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < SEG; ++j) {
+            const uint32_t c = threadIdx.x + NT * j;
+            // +0 past the row's end adds nothing to a sum that is never -0
+            v[j] = c < n ? emel_expf_nonpos(v[j] - mx, tab) : 0.0f;
+            s_e[c] = v[j];
+            if (!kOneTile && c < n) y[yoff(t0 + c)] = v[j];
+        }
+        if (threadIdx.x == 0) s_total = st.finite ? seq_value(st.m, st.u) : st.special; // the sum before the tile
+        __syncthreads();
+        const float s_prev = s_total;
+        if (s_prev == s_prev) seq_tile_sum<NT, SEG>(s_e, s_seq, s_prev, st); // a NaN sum is final
+        __syncthreads(); // s_e, s_seq and s_total are rewritten next
+    }
+    if (threadIdx.x == 0) s_total = st.finite ? seq_value(st.m, st.u) : st.special;
+    __syncthreads();
+
+    // 3. y = e / sum (sum >= 1, or NaN)
+    const double recip = 1.0 / static_cast<double>(s_total);
+    if constexpr (kOneTile) {
+        const uint32_t n = static_cast<uint32_t>(ncols);
+#pragma unroll
+        for (uint32_t j = 0; j < SEG; ++j) {
+            const uint32_t c = threadIdx.x + NT * j;
+            if (c < n) y[yoff(c)] = div_by_recip(v[j], recip);
+        }
+    } else {
+        for (uint64_t t0 = 0; t0 < ncols; t0 += TILE) {
+            const uint32_t n = tile_n(t0);
+#pragma unroll
+            for (uint32_t j = 0; j < SEG; ++j) v[j] = y[yoff(col(t0, n, j))];
+#pragma unroll
+            for (uint32_t j = 0; j < SEG; ++j) {
+                const uint32_t c = threadIdx.x + NT * j;
+                if (c < n) y[yoff(t0 + c)] = div_by_recip(v[j], recip);
+            }
+        }
     }
 }
 
@@ -486,6 +814,24 @@ OrdView ord_view(const Operand &p)
     }
     return v;
 }
+
+template <uint32_t NT, uint32_t SEG>
+void launch_softmax_seq_nt(const Operand &x, const Operand &y, uint64_t rows, hipStream_t s)
+{
+    const uint64_t ncols = x.ne[0];
+    const float *xp = static_cast<const float *>(x.data);
+    float *yp = static_cast<float *>(y.data);
+    const dim3 grid(static_cast<uint32_t>(rows));
+    const bool one = ncols <= NT * SEG;
+    if (y.ne[0] == ncols) {
+        if (one) k_softmax_seq<NT, SEG, true, true><<<grid, NT, 0, s>>>(ord_view(x), ord_view(y), ncols, xp, yp);
+        else k_softmax_seq<NT, SEG, true, false><<<grid, NT, 0, s>>>(ord_view(x), ord_view(y), ncols, xp, yp);
+    } else {
+        if (one) k_softmax_seq<NT, SEG, false, true><<<grid, NT, 0, s>>>(ord_view(x), ord_view(y), ncols, xp, yp);
+        else k_softmax_seq<NT, SEG, false, false><<<grid, NT, 0, s>>>(ord_view(x), ord_view(y), ncols, xp, yp);
+    }
+}
+
 
 template <RowOp OP, int NW, int NV, bool FULL>
 void launch_vec(const RowGeo &g, const RowArgs &a, const MaskGeo &mg, hipStream_t s)
@@ -526,6 +872,30 @@ void launch_vec_nv(const RowGeo &g, const RowArgs &a, const MaskGeo &mg, hipStre
 
 } // namespace
 
+hipError_t launch_softmax_seq(const Operand &x, const Operand &y, hipStream_t s)
+{
+    const uint64_t ncols = x.ne[0];
+    uint64_t count = 1;
+    for (int d = 0; d < 4; ++d) count *= x.ne[d];
+    if (count == 0 || ncols == 0) return hipSuccess;
+    const uint64_t rows = count / ncols;
+    if (ncols <= kSeqShort) {
+        const uint64_t blocks = (rows + kBlock - 1) / kBlock;
+        if (blocks > 0x7fffffffull) return hipErrorInvalidValue;
+        k_softmax_lane<<<dim3(static_cast<uint32_t>(blocks)), kBlock, 0, s>>>(
+            ord_view(x), ord_view(y), rows, ncols, static_cast<const float *>(x.data), static_cast<float *>(y.data));
+        return hipGetLastError();
+    }
+    if (rows > 0x7fffffffull) return hipErrorInvalidValue; // one workgroup per row
+    // (threads, addends per segment) by row width, measured on MI355X: one
+    // tile covers rows up to 4096 columns, wider rows stream tiles of 4096
+    if (ncols <= 512) launch_softmax_seq_nt<64, 8>(x, y, rows, s);
+    else if (ncols <= 1024) launch_softmax_seq_nt<64, 16>(x, y, rows, s);
+    else if (ncols <= 2048) launch_softmax_seq_nt<256, 8>(x, y, rows, s);
+    else launch_softmax_seq_nt<512, 8>(x, y, rows, s);
+    return hipGetLastError();
+}
+
 hipError_t launch_rows(const RowArgs &a, hipStream_t s)
 {
     const bool soft = a.op == RowOp::SoftMax || a.op == RowOp::SoftMaxExt;
@@ -536,13 +906,7 @@ hipError_t launch_rows(const RowArgs &a, hipStream_t s)
     const uint64_t rows = count / ncols;
 
     // The strided soft_max keeps the reference's sequential f32 sum.
-    if (a.op == RowOp::SoftMax && !a.dense_sum) {
-        const uint64_t blocks = (rows + kBlock - 1) / kBlock;
-        k_softmax_seq<<<dim3(static_cast<uint32_t>(blocks)), kBlock, 0, s>>>(
-            ord_view(a.x), ord_view(a.y), rows, ncols, static_cast<const float *>(a.x.data),
-            static_cast<float *>(a.y.data));
-        return hipGetLastError();
-    }
+    if (a.op == RowOp::SoftMax && !a.dense_sum) return launch_softmax_seq(a.x, a.y, s);
 
     // Vectorized rows: contiguous dim 0, 16-byte aligned row starts, and the
     // destination row r holding the same columns as the source row r.

@@ -29,6 +29,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "common.hpp"
 #include "libm_replica.hpp"
 
 namespace emel {
@@ -72,6 +73,160 @@ __host__ __device__ __forceinline__ uint32_t seq_units(float e, int32_t u, bool 
     tie = (t - __builtin_floorf(t)) == 0.5f;
 #endif
     return static_cast<uint32_t>(__builtin_rintf(t));
+}
+
+
+// Inclusive prefix sum over the 64 lanes of a wave (DPP: row shifts within
+// rows of 16 lanes, then the row broadcasts of lanes 15 and 31).
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v)
+{
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x111, 0xf, 0xf, true)); // row_shr:1
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x112, 0xf, 0xf, true)); // row_shr:2
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x114, 0xf, 0xf, true)); // row_shr:4
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x118, 0xf, 0xf, true)); // row_shr:8
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x142, 0xa, 0xf, false)); // row_bcast:15
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x143, 0xc, 0xf, false)); // row_bcast:31
+    return v;
+}
+
+// The same scan over doubles (each DPP step moves both halves).
+template <int CTRL, int ROW_MASK, bool BOUND>
+__device__ __forceinline__ double dpp_shift_f64(double v)
+{
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = static_cast<uint32_t>(
+        __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(b)), CTRL, ROW_MASK, 0xf, BOUND));
+    const uint32_t hi = static_cast<uint32_t>(
+        __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(b >> 32)), CTRL, ROW_MASK, 0xf, BOUND));
+    return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+__device__ __forceinline__ double wave_incl_scan_f64(double v)
+{
+    v += dpp_shift_f64<0x111, 0xf, true>(v);
+    v += dpp_shift_f64<0x112, 0xf, true>(v);
+    v += dpp_shift_f64<0x114, 0xf, true>(v);
+    v += dpp_shift_f64<0x118, 0xf, true>(v);
+    v += dpp_shift_f64<0x142, 0xa, false>(v);
+    v += dpp_shift_f64<0x143, 0xc, false>(v);
+    return v;
+}
+
+// Relative distance, either way, between a running f32 sum after `a`
+// roundings of non-negative addends (starting from an exact value) and the
+// exact sum: each rounding scales by (1 + d) with |d| < 2^-24, so the ratio
+// lies in [(1 - 2^-24)^a, (1 + 2^-24)^a], inside [1 - a 2^-24, 1 + a 2^-24 +
+// (a 2^-24)^2] (Bernoulli's inequality; e^x <= 1 + x + x^2 for x <= 1).
+// 2^-30 covers the f64 rounding of the predicted sums (up to 2^22 terms).
+// Past 2^22 roundings it returns 1, which makes every prediction fail.
+__host__ __device__ __forceinline__ double seq_rel_bound(double a)
+{
+    const double au = a * 0x1p-24;
+    return au <= 0.25 ? au * (1.0 + au) + 0x1p-30 : 1.0;
+}
+
+// ---- one wave walks a tile of its addends ----------------------------------
+
+// The running sum of a walk: m units of 2^u while finite.
+struct SumState {
+    uint32_t m;
+    int32_t u;
+    bool finite;
+    float special; // NaN or +inf once the running sum leaves the finite range
+};
+
+// The rounds over one tile of PER * 64 elements (this lane's PER consecutive
+// ones in e).
+template <uint32_t PER>
+__device__ __forceinline__ void sum_tile(const float (&e)[PER], SumState &s, uint32_t start = 0)
+{
+    const uint32_t lane = threadIdx.x % kWave;
+    if (!s.finite) {
+        // +inf stays +inf unless a NaN follows; NaN stays NaN
+        bool nan = false;
+#pragma unroll
+        for (uint32_t j = 0; j < PER; ++j) nan |= e[j] != e[j];
+        if (__ballot(nan)) s.special = __builtin_nanf("");
+        return;
+    }
+    // start: tile-relative index of the first uncommitted element
+    while (true) {
+        // this round's units at the current binade (0 for committed
+        // elements), kept for the event search below
+        uint32_t r[PER];
+        uint32_t lsum = 0, ties = 0;
+        if (start == 0) {
+#pragma unroll
+            for (uint32_t j = 0; j < PER; ++j) {
+                bool tie;
+                r[j] = seq_units(e[j], s.u, tie);
+                lsum += r[j];
+                ties |= static_cast<uint32_t>(tie) << j;
+            }
+        } else { // elements before start are committed
+#pragma unroll
+            for (uint32_t j = 0; j < PER; ++j) {
+                bool tie;
+                const uint32_t q = seq_units(e[j], s.u, tie);
+                const bool active = PER * lane + j >= start;
+                r[j] = active ? q : 0u;
+                lsum += r[j];
+                ties |= static_cast<uint32_t>(active && tie) << j;
+            }
+        }
+        // lsum <= PER * 2^24; saturated at 2^24 the scan cannot overflow (a
+        // saturated value already marks a crossing)
+        const uint32_t x_in = lsum < kSeqLimit ? lsum : kSeqLimit;
+        const uint32_t incl = wave_incl_scan(x_in);
+        const uint32_t total = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), kWave - 1));
+        const bool anytie = __ballot(ties != 0) != 0;
+        if (!anytie && s.m + total < kSeqLimit) {
+            s.m += total;
+            return; // tile committed
+        }
+        // this lane's first event element and the units just before it,
+        // branch-free: flags past the first event are never used, and the
+        // committed elements (r = 0, no tie) cannot be events in the lane
+        // that holds the first one (its running units are still below 2^24)
+        const uint32_t base = s.m + (incl - x_in);
+        uint32_t run = base, evmask = 0;
+#pragma unroll
+        for (uint32_t j = 0; j < PER; ++j) {
+            const bool ev = ((ties >> j) & 1u) != 0u || run + r[j] >= kSeqLimit;
+            evmask |= static_cast<uint32_t>(ev) << j;
+            run += r[j];
+        }
+        const uint32_t first = evmask ? static_cast<uint32_t>(__builtin_ctz(evmask)) : PER;
+        uint32_t run_first = base;
+        float ek = 0.0f;
+#pragma unroll
+        for (uint32_t j = 0; j < PER; ++j) {
+            run_first += j < first ? r[j] : 0u;
+            ek = j == first ? e[j] : ek;
+        }
+        const uint64_t emask = __ballot(evmask != 0u);
+        if (emask == 0) return; // unreachable: a tie or a crossing has a first element
+        const int fl = __builtin_ctzll(emask);
+        const uint32_t k = PER * static_cast<uint32_t>(fl) +
+                           static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(first), fl));
+        const uint32_t run_k = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(run_first), fl));
+        const float e_k = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ek), fl));
+        const float sn = seq_value(run_k, s.u) + e_k; // the event element: one f32 addition
+        if (!(sn < __builtin_inff())) { // NaN or +inf
+            s.special = sn;
+            s.finite = false;
+            bool nan = false;
+#pragma unroll
+            for (uint32_t j = 0; j < PER; ++j) nan |= (PER * lane + j > k) && e[j] != e[j];
+            if (__ballot(nan)) s.special = __builtin_nanf("");
+            return;
+        }
+        const SeqState st = seq_state(sn);
+        s.m = st.m;
+        s.u = st.u;
+        start = k + 1;
+        if (start >= PER * kWave) return;
+    }
 }
 
 } // namespace emel

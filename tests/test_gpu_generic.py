@@ -168,6 +168,16 @@ def test_row_routes(run, op, layout):
     assert run(op, s, None, None, d, params) == (orc.OK, eh.Status.OK)
 
 
+@pytest.mark.parametrize("ne,dne", [([300, 20, 1, 1], [600, 10, 1, 1]), ([5000, 3, 2, 1], [5000, 3, 2, 1])])
+def test_wide_softmax_permuted_and_reshaped(run, ne, dne):
+    # soft_max's exact sequential f32 sum over a workgroup per row
+    n = int(np.prod(ne))
+    x = normal(56, n) * np.float32(4)
+    x[7] = np.nan if ne[0] == 300 else x[7]
+    s = run.pair(x, ne, permuted(x, ne))
+    assert run(G.SOFT_MAX, s, None, None, run.pair(np.zeros(n, np.float32), dne)) == (orc.OK, eh.Status.OK)
+
+
 def test_wide_softmax_and_norm_rows(run):
     ne = [4096, 70, 1, 1]
     n = int(np.prod(ne))

@@ -114,6 +114,87 @@ def test_soft_max_strided_is_bit_exact(gpu):
     assert_bits_equal(o.result(), want, "strided soft_max")
 
 
+# ---- strided soft_max: the exact sequential f32 row sum -------------------------
+#
+# Any layout that is not dense row-major makes the reference sum each row's
+# exponentials one by one in f32 (reductions.rs:603-638).  The GPU reproduces
+# that sum exactly (a lane per row up to 64 columns, a workgroup per row with
+# the binade walk above that); every case is bit-exact against the oracle.
+
+def padded_pair(x, cols, rows, pad):
+    """Rows of `cols` values `pad` floats apart: not dense."""
+    buf = np.zeros((rows, cols + pad), np.float32)
+    buf[:, :cols] = x.reshape(rows, cols)
+    pitch = 4 * (cols + pad)
+    return Pair(buf.reshape(-1), [cols, rows, 1, 1], [4, pitch, pitch * rows, pitch * rows])
+
+
+def strided_soft_max(gpu, a, out_ne):
+    n = int(np.prod(a.ne))
+    o = Pair(np.zeros(n, np.float32), out_ne).to(gpu)
+    assert eh.Kernel().process_event(eh.OpSoftMax(a.to(gpu).pview(), o.pview(mut=True))) == eh.Status.OK, \
+        eh.last_error()
+    want = np.zeros(n, np.float32)
+    assert orc.soft_max(a.oview(), orc.view(want, o.ne, o.nb)) == orc.OK
+    return o.result(), want
+
+
+@pytest.mark.parametrize("cols,rows", [(4096, 512), (65, 40), (511, 7), (512, 9), (513, 5), (1024, 33),
+                                       (2048, 7), (2049, 3), (4097, 3), (20000, 4), (100000, 2), (64, 300)])
+def test_soft_max_strided_rows_bit_exact(gpu, cols, rows):
+    x = normal(700 + cols, cols * rows, 3.0)
+    got, want = strided_soft_max(gpu, padded_pair(x, cols, rows, 3), [cols, rows, 1, 1])
+    assert_bits_equal(got, want, f"strided soft_max {cols}x{rows}")
+
+
+def test_soft_max_strided_transposed_and_reshaped_dst(gpu):
+    cols, rows = 3000, 6
+    x = normal(710, cols * rows, 2.0)
+    # column-major storage: dim 0 has stride rows * 4 bytes
+    a = Pair(x.reshape(cols, rows).copy().reshape(-1), [cols, rows, 1, 1], [4 * rows, 4, 4 * cols * rows,
+                                                                           4 * cols * rows])
+    got, want = strided_soft_max(gpu, a, [cols, rows, 1, 1])
+    assert_bits_equal(got, want, "transposed soft_max")
+    # a dst of the same count but another shape: its ordinals are decoded per element
+    got, want = strided_soft_max(gpu, padded_pair(x, cols, rows, 1), [rows * 2, cols // 2, 1, 1])
+    assert_bits_equal(got, want, "soft_max into a reshaped dst")
+
+
+@pytest.mark.parametrize("cols", [4096, 20000, 300, 65, 37])
+def test_soft_max_strided_non_finite(gpu, cols):
+    x, rows = special_rows(cols, 720 + cols)
+    got, want = strided_soft_max(gpu, padded_pair(x, cols, rows, 2), [cols, rows, 1, 1])
+    assert np.isnan(want.reshape(rows, cols)[0]).all()
+    assert_bits_equal(got, want, f"strided soft_max non-finite, {cols} columns")
+
+
+# x for which glibc's expf is exactly k/8, so that, once the running sum has
+# a spacing of 1/4 (from 2^21 on), odd multiples of 1/8 are rounding ties
+# (found by searching the float neighbours of log(k/8) against glibc).
+DYADIC_EXP = {1.0: 0.0, 0.875: -0.133531391620636, 0.75: -0.28768208622932434, 0.625: -0.4700036346912384,
+              0.5: -0.6931471824645996, 0.375: -0.9808292388916016, 0.25: -1.3862943649291992,
+              0.125: -2.079441547393799}
+
+
+def test_soft_max_strided_ties_and_saturation(gpu):
+    import ctypes
+    libm = ctypes.CDLL("libm.so.6")
+    libm.expf.restype, libm.expf.argtypes = ctypes.c_float, [ctypes.c_float]
+    for value, arg in DYADIC_EXP.items():
+        assert libm.expf(arg) == value
+    g = np.random.Generator(np.random.PCG64(730))
+    cols = (1 << 21) + (1 << 18)
+    keys = np.array(list(DYADIC_EXP.values()), np.float32)
+    x = np.where(g.random(cols) < 0.9, np.float32(0.0), keys[g.integers(0, len(keys), cols)]).astype(np.float32)
+    got, want = strided_soft_max(gpu, padded_pair(x, cols, 1, 1), [cols, 1, 1, 1])
+    assert_bits_equal(got, want, "soft_max with rounding ties")
+    # 2^24 ones saturate the f32 sum: every later +1 is a tie that rounds back
+    cols = (1 << 24) + 4096
+    got, want = strided_soft_max(gpu, padded_pair(np.zeros(cols, np.float32), cols, 1, 1), [cols, 1, 1, 1])
+    assert_bits_equal(got, want, "soft_max with a saturated sum")
+    assert got[0] == np.float32(2.0 ** -24)
+
+
 def causal_mask(nkv, nq):
     k = np.arange(nkv)[None, :]
     q = np.arange(nq)[:, None]
