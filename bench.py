@@ -125,6 +125,9 @@ OPS = [
 # `value`): adjacent ops beyond the BASELINE configs' op list.
 EXTRA_OPS = [
     ("glu_swiglu", "config 2 as one OpGlu (glu.rs): [up | gate] -> silu(gate) * up", 3 * 22544384),
+    ("soft_max_dense", "OpSoftMax [4096,512], dense: f64 row sum (reductions.rs:565-601)", 2 * 8388608),
+    ("soft_max_strided", "OpSoftMax [4096,512], rows 4 floats apart: exact sequential f32 row sum "
+                         "(reductions.rs:603-638)", 2 * 8388608),
 ]
 DOMINANT = "soft_max_ext"
 COPY_BYTES = 2 * 268435456  # the calibration copy: 256 MiB read + 256 MiB written
@@ -202,6 +205,13 @@ class GpuSuite:
             "mul_broadcast_4d": ([host["c5b_src0"], host["c5b_src1"]], (128 * 64 * 32 * 8, torch.float32),
                                  lambda i, o: eh.OpBinaryBroadcast(eh.BinaryOp.MUL, V(i[0], [128, 64, 32, 8], vnb),
                                                                    V(i[1], [128, 1, 32, 1]), M(o, [128, 64, 32, 8]))),
+            "soft_max_dense": ([host["c1_src0"] * np.float32(4)], (4096 * 512, torch.float32),
+                               lambda i, o: eh.OpSoftMax(V(i[0], [4096, 512, 1, 1]), M(o, [4096, 512, 1, 1]))),
+            "soft_max_strided": ([np.pad((host["c1_src0"] * np.float32(4)).reshape(512, 4096), ((0, 0), (0, 4)))
+                                  .reshape(-1)], (4096 * 512, torch.float32),
+                                 lambda i, o: eh.OpSoftMax(V(i[0], [4096, 512, 1, 1], [4, 4 * 4100, 4 * 4100 * 512,
+                                                                                        4 * 4100 * 512]),
+                                                           M(o, [4096, 512, 1, 1]))),
             "glu_swiglu": ([np.concatenate([host["c2_up"], host["c2_gate"]])], (n2, torch.float32),
                            lambda i, o: eh.OpGlu(i[0], o, eh.GluSubOp.SWIGLU)),
             "copy": ([np.zeros(COPY_BYTES // 8, np.float32)], (COPY_BYTES // 8, torch.float32),
