@@ -408,10 +408,29 @@ __host__ __device__ __forceinline__ uint16_t emel_gelu_core_fp16(float q)
     return emel_fp32_to_fp16(approximation);
 }
 
-// SiluFormula (unary.rs:595-600).
+// SiluFormula (unary.rs:595-600): x / (1 + expf(-x)).  The argument of
+// expf is clamped to [-20, 89] and expf's main path evaluated without its
+// special-case selects, which gives the same quotient for every x:
+//   -x <= 0x1.62e42ep6: the main path is expf (above -20, glibc's main
+//   range);
+//   -x in (0x1.62e42ep6, 89] and above: the main path's value exceeds
+//   FLT_MAX by more than half an ulp and rounds to +inf, expf's overflow
+//   result, so x / inf gives -0 (and -inf / inf NaN);
+//   -x < -20: expf(-x) < 2^-28, so 1 + expf(-x) rounds to 1 either way;
+//   NaN x: the quotient is NaN whatever the clamp returns.
+// Checked against glibc over all 2^32 inputs on the host and against the
+// select-based expf on the GPU by the test suite.
+__host__ __device__ __forceinline__ float silu_exp_arg(float v)
+{
+#if defined(__HIP_DEVICE_COMPILE__)
+    return __builtin_amdgcn_fmed3f(v, -20.0f, 89.0f);
+#else
+    return __builtin_fminf(__builtin_fmaxf(v, -20.0f), 89.0f);
+#endif
+}
 __host__ __device__ __forceinline__ float emel_silu(float x, const uint64_t *tab, const ExpfConsts &c = ExpfConsts{})
 {
-    return x / (1.0f + emel_expf(-x, tab, c));
+    return x / (1.0f + expf_main_path(silu_exp_arg(-x), tab, c));
 }
 
 // GeluFormula (unary.rs:522-541): separate products, fp16 round trips on
@@ -424,38 +443,79 @@ __host__ __device__ __forceinline__ float emel_gelu(float value)
     return emel_fp16_to_f32(emel_gelu_core_fp16(q));
 }
 
-// ---- GELU by table -----------------------------------------------------------
-// For |x| < 10 the result depends only on q = fp16(x), and it saturates:
-// every fp16 q >= 3.380859375 (bits 0x42c3) gives exactly q, and every
-// q <= -5.16015625 (bits 0xc529) gives -0.0 (the product underflows fp16).
-// The table therefore holds the results for positive magnitudes below
-// 0x42c3 (slots 0 .. 0x42c2) then negative magnitudes below 0x4529 (slots
-// 0x42c3 ..): 34796 fp16 entries.  Both thresholds and the whole lookup
-// are checked against emel_gelu over all 2^32 inputs by the test suite.
+// ---- GELU by polynomial and table --------------------------------------------
+// For |x| < 10 the result depends only on q = fp16(x).  Three ranges of the
+// fp16 magnitude m of q, per sign:
+//   m below kGeluPolyPos (q >= 0) or kGeluPolyNeg (q < 0), |q| up to about
+//   0.26 / 0.30: the result equals fp16(0.5 q (1 + t (1 - t^2/3 + 2 t^4/15)))
+//   with t = 0.7978846 (q + 0.044715 q^3), tanh's degree-5 Taylor
+//   polynomial, in f32 with the formula's order of operations
+//   (gelu_poly).  Each limit is the first magnitude where that fails.
+//   saturated: every q >= 3.380859375 (bits 0x42c3) gives exactly q, and
+//   every q <= -5.16015625 (bits 0xc529) gives -0.0 (the product underflows
+//   fp16);
+//   in between: a table of the results, the positive magnitudes from
+//   kGeluPolyPos then the negative ones from kGeluPolyNeg, 7918 fp16
+//   entries (15.8 KB, small enough for every workgroup to stage in LDS).
+// The limits and the whole lookup are checked against emel_gelu over all
+// 2^32 inputs by the test suite, which also rescans each polynomial limit.
 constexpr uint32_t kGeluPosLimit = 0x42c3u;
 constexpr uint32_t kGeluNegLimit = 0x4529u;
-constexpr uint32_t kGeluEntries = kGeluPosLimit + kGeluNegLimit;
+constexpr uint32_t kGeluPolyPos = 0x342eu;
+constexpr uint32_t kGeluPolyNeg = 0x34d0u;
+constexpr uint32_t kGeluPosEntries = kGeluPosLimit - kGeluPolyPos;
+constexpr uint32_t kGeluNegEntries = kGeluNegLimit - kGeluPolyNeg;
+constexpr uint32_t kGeluEntries = kGeluPosEntries + kGeluNegEntries;
 constexpr uint32_t kGeluTableHalfs = (kGeluEntries + 7u) / 8u * 8u; // padded to 16-byte rows
 
 // fp16 bits of the q that table slot `slot` holds the result for.
 __host__ __device__ __forceinline__ uint16_t gelu_slot_key(uint32_t slot)
 {
-    return static_cast<uint16_t>(slot < kGeluPosLimit ? slot : 0x8000u | (slot - kGeluPosLimit));
+    return static_cast<uint16_t>(slot < kGeluPosEntries ? kGeluPolyPos + slot
+                                                        : 0x8000u | (kGeluPolyNeg + slot - kGeluPosEntries));
 }
 
-// Table slot of fp16 bits h, or kGeluEntries when q saturates (or is NaN).
-__host__ __device__ __forceinline__ uint32_t gelu_slot(uint16_t h)
+// Where the result for fp16 bits h comes from: table slot `slot` (table),
+// the polynomial (poly), or else saturation (or NaN).  slot is 0 outside
+// the table, so a lookup needs no further select.
+struct GeluClass {
+    uint32_t slot;
+    bool table;
+    bool poly;
+};
+__host__ __device__ __forceinline__ GeluClass gelu_class(uint16_t h)
 {
     const uint32_t mag = h & 0x7fffu;
-    if (h & 0x8000u) return mag < kGeluNegLimit ? kGeluPosLimit + mag : kGeluEntries;
-    return mag < kGeluPosLimit ? mag : kGeluEntries;
+    const bool neg = (h & 0x8000u) != 0;
+    const uint32_t lo = neg ? kGeluPolyNeg : kGeluPolyPos;
+    const uint32_t rel = mag - lo; // wraps below the table
+    const bool table = rel < (neg ? kGeluNegEntries : kGeluPosEntries);
+    return GeluClass{table ? rel + (neg ? kGeluPosEntries : 0u) : 0u, table, mag < lo};
 }
 
-// GeluFormula from the looked-up entry: x the input, q = fp16(x) widened,
-// entry the widened table value at gelu_slot (ignored when saturated).
-__host__ __device__ __forceinline__ float gelu_finish(float x, float q, uint32_t slot, float entry)
+// The f32 value whose fp16 rounding is GELU(q) for |q| in the polynomial
+// range.  On the device the value is passed through an empty asm so that
+// the compiler cannot fuse the last product into the fp16 conversion
+// (v_fma_mix adds +0.0, which loses the sign of -0 * 1, and rounds the
+// product once instead of through f32).
+__host__ __device__ __forceinline__ float gelu_poly(float q)
 {
-    float y = slot < kGeluEntries ? entry : (q < 0.0f ? -0.0f : q);
+    const float t = 0.7978846f * (q + 0.044715f * q * q * q);
+    const float t2 = t * t;
+    float r = 0.5f * q * (1.0f + t * (1.0f + t2 * (-1.0f / 3.0f + t2 * (2.0f / 15.0f))));
+#if defined(__HIP_DEVICE_COMPILE__)
+    asm("" : "+v"(r));
+#endif
+    return r;
+}
+
+// GeluFormula from the pieces: x the input, q = fp16(x) widened, c =
+// gelu_class of its bits, entry the widened table value at c.slot, poly
+// the widened fp16 rounding of gelu_poly(q); each is ignored outside its
+// range.
+__host__ __device__ __forceinline__ float gelu_finish(float x, float q, GeluClass c, float entry, float poly)
+{
+    float y = c.table ? entry : (c.poly ? poly : (q < 0.0f ? -0.0f : q));
     if (x <= -10.0f) y = 0.0f;
     if (x >= 10.0f || x != x) y = x;
     return y;

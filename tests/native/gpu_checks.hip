@@ -5,6 +5,8 @@
 //   hw_fp32_to_fp16 vs emel_fp32_to_fp16  (all 2^32 f32 inputs)
 //   hw_fp16_to_f32  vs emel_fp16_to_f32   (all 65536 f16 inputs)
 //   emel_expf_nonpos vs emel_expf         (all f32 <= 0, and NaNs)
+//   emel_silu vs x / (1 + emel_expf(-x))  (all 2^32 f32 inputs)
+//   the kernels' GELU lookup vs emel_gelu (all 2^32 f32 inputs)
 //   __builtin_sqrtf (the power.rs kernels) correctly rounded: for every
 //   positive finite x the exact squares of the two rounding midpoints
 //   around the result bracket x (exact in double: <= 52 significant bits);
@@ -56,6 +58,53 @@ __global__ void k_expf_nonpos(uint64_t lo, uint64_t hi)
         if (!(x <= 0.0f) && x == x) continue; // positive inputs are outside the contract
         const float a = emel::emel_expf_nonpos(x, tab);
         const float b = emel::emel_expf(x, tab);
+        if (emel::f32_to_bits(a) != emel::f32_to_bits(b) && !(a != a && b != b)) ++bad;
+    }
+    if (bad) atomicAdd(&g_bad, bad);
+}
+
+// emel_silu (clamped argument, no special-case selects) against the
+// SiluFormula with the select-based emel_expf.
+__global__ void k_silu(uint64_t lo, uint64_t hi)
+{
+    __shared__ uint64_t tab[32];
+    if (threadIdx.x < 32) tab[threadIdx.x] = emel::kExp2Table[threadIdx.x];
+    __syncthreads();
+    unsigned long long bad = 0;
+    for (uint64_t u = lo + blockIdx.x * 256ull + threadIdx.x; u < hi; u += 256ull * gridDim.x) {
+        const float x = emel::bits_to_f32(static_cast<uint32_t>(u));
+        const float a = emel::emel_silu(x, tab);
+        const float b = x / (1.0f + emel::emel_expf(-x, tab));
+        if (emel::f32_to_bits(a) != emel::f32_to_bits(b) && !(a != a && b != b)) ++bad;
+    }
+    if (bad) atomicAdd(&g_bad, bad);
+}
+
+// The GELU lookup of the kernels (hardware fp16 conversions, polynomial,
+// table, saturation) against the scalar GeluFormula replica.
+__device__ __align__(16) uint16_t g_gelu[emel::kGeluTableHalfs];
+
+__global__ void k_gelu_fill()
+{
+    const uint32_t slot = blockIdx.x * 256u + threadIdx.x;
+    if (slot < emel::kGeluTableHalfs)
+        g_gelu[slot] = slot < emel::kGeluEntries
+                           ? emel::emel_gelu_core_fp16(emel::emel_fp16_to_f32(emel::gelu_slot_key(slot)))
+                           : 0;
+}
+
+__global__ void k_gelu(uint64_t lo, uint64_t hi)
+{
+    unsigned long long bad = 0;
+    for (uint64_t u = lo + blockIdx.x * 256ull + threadIdx.x; u < hi; u += 256ull * gridDim.x) {
+        const float x = emel::bits_to_f32(static_cast<uint32_t>(u));
+        const uint16_t h = emel::hw_fp32_to_fp16(x);
+        const float q = emel::hw_fp16_to_f32(h);
+        const emel::GeluClass c = emel::gelu_class(h);
+        const float entry = emel::hw_fp16_to_f32(g_gelu[c.slot]);
+        const float poly = emel::hw_fp16_to_f32(emel::hw_fp32_to_fp16(emel::gelu_poly(q)));
+        const float a = emel::gelu_finish(x, q, c, entry, poly);
+        const float b = emel::emel_gelu(x);
         if (emel::f32_to_bits(a) != emel::f32_to_bits(b) && !(a != a && b != b)) ++bad;
     }
     if (bad) atomicAdd(&g_bad, bad);
@@ -129,6 +178,19 @@ uint64_t gpu_check_fp16_to_f32(void)
 uint64_t gpu_check_expf_nonpos(void)
 {
     return run([] { k_expf_nonpos<<<8192, 256>>>(0, 1ull << 32); });
+}
+
+uint64_t gpu_check_silu(void)
+{
+    return run([] { k_silu<<<8192, 256>>>(0, 1ull << 32); });
+}
+
+uint64_t gpu_check_gelu(void)
+{
+    return run([] {
+        k_gelu_fill<<<(emel::kGeluTableHalfs + 255) / 256, 256>>>();
+        k_gelu<<<8192, 256>>>(0, 1ull << 32);
+    });
 }
 
 uint64_t gpu_check_sqrtf(void)

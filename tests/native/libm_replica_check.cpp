@@ -9,6 +9,11 @@
 //   fp32 -> fp16           -> the compiler's _Float16 conversion (IEEE
 //                             round-to-nearest-even);
 //   fp16 -> fp32           -> the compiler's _Float16 widening (exact);
+//   silu                   -> x / (1 + glibc expf(-x)) (the kernels' form
+//                             clamps expf's argument instead of selecting
+//                             its special cases);
+//   GELU by polynomial and table -> the scalar formula, and each
+//                             polynomial limit rescanned;
 //   seqsum.hpp             -> a plain sequential f32 loop: the host
 //                             emulation of k_smp_sum's rounds (units per
 //                             binade, events, restarts) must give its bits.
@@ -379,7 +384,7 @@ uint64_t check_div_recip_random(uint64_t seed, uint64_t n, int threads)
     });
 }
 
-// The table-driven GELU of the kernels (gelu_slot / gelu_finish over a
+// The table-driven GELU of the kernels (gelu_class / gelu_finish over a
 // table filled like k_gelu_table) against emel_gelu for every input in
 // [lo, hi).  Also counts table slots whose key maps back to another slot.
 uint64_t check_gelu_table(uint64_t lo, uint64_t hi, int threads)
@@ -388,16 +393,43 @@ uint64_t check_gelu_table(uint64_t lo, uint64_t hi, int threads)
     uint64_t bad = 0;
     for (uint32_t slot = 0; slot < emel::kGeluEntries; ++slot) {
         const uint16_t key = emel::gelu_slot_key(slot);
-        if (emel::gelu_slot(key) != slot) ++bad;
+        const emel::GeluClass c = emel::gelu_class(key);
+        if (!c.table || c.poly || c.slot != slot) ++bad;
         tab[slot] = emel::emel_gelu_core_fp16(emel::emel_fp16_to_f32(key));
     }
     const uint16_t *t = tab.data();
     return bad + count_range(lo, hi, threads, [t](uint32_t u) {
         const float x = emel::bits_to_f32(u);
         const uint16_t h = emel::emel_fp32_to_fp16(x);
-        const uint32_t slot = emel::gelu_slot(h);
-        const float entry = emel::emel_fp16_to_f32(t[slot < emel::kGeluEntries ? slot : 0u]);
-        return differ(emel::gelu_finish(x, emel::emel_fp16_to_f32(h), slot, entry), emel::emel_gelu(x));
+        const float q = emel::emel_fp16_to_f32(h);
+        const emel::GeluClass c = emel::gelu_class(h);
+        const float entry = emel::emel_fp16_to_f32(t[c.slot]);
+        const float poly = emel::emel_fp16_to_f32(emel::emel_fp32_to_fp16(emel::gelu_poly(q)));
+        return differ(emel::gelu_finish(x, q, c, entry, poly), emel::emel_gelu(x));
+    });
+}
+
+// The first fp16 magnitude (of sign `negative`) at which fp16(gelu_poly(q))
+// differs from GeluFormula's core, scanning up from 0: the polynomial's
+// range ends exactly there (kGeluPolyPos / kGeluPolyNeg).
+uint32_t gelu_poly_first_miss(int negative)
+{
+    for (uint32_t mag = 0; mag < 0x7c00u; ++mag) {
+        const uint16_t h = static_cast<uint16_t>((negative ? 0x8000u : 0u) | mag);
+        const float q = emel::emel_fp16_to_f32(h);
+        if (emel::emel_fp32_to_fp16(emel::gelu_poly(q)) != emel::emel_gelu_core_fp16(q)) return mag;
+    }
+    return 0x7c00u;
+}
+uint32_t gelu_poly_limit(int negative) { return negative ? emel::kGeluPolyNeg : emel::kGeluPolyPos; }
+
+// emel_silu (clamped argument, expf's main path without its special-case
+// selects) against SiluFormula on the host glibc, x / (1 + expf(-x)).
+uint64_t check_silu(uint64_t lo, uint64_t hi, int threads)
+{
+    return count_range(lo, hi, threads, [](uint32_t u) {
+        const float x = emel::bits_to_f32(u);
+        return differ(emel::emel_silu(x, emel::kExp2Table), x / (1.0f + expf(-x)));
     });
 }
 

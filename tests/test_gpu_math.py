@@ -4,6 +4,9 @@ the GPU itself (tests/native/gpu_checks.hip):
   hardware f32 -> f16 conversion == the reference's fp32_to_fp16 (all 2^32)
   hardware f16 -> f32 widening   == the reference's fp16_to_f32 (all 65536)
   emel_expf_nonpos              == emel_expf for every x <= 0 and NaN
+  emel_silu (clamped expf argument) == x / (1 + emel_expf(-x)) (all 2^32)
+  GELU by polynomial and table  == emel_gelu (all 2^32), with the hardware
+                                fp16 conversions the kernels use
   __builtin_sqrtf               correctly rounded for every input (power.rs)
   f64 sqrt and division         IEEE results on 2^23 random doubles (the generic
                                 norms' f64 scale), compared with numpy on the host
@@ -24,14 +27,15 @@ def checks(gpu):
     if not LIB.exists():
         pytest.fail(f"{LIB} missing: run __graft_entry__.build()")
     L = ctypes.CDLL(str(LIB))
-    for n in ("gpu_check_fp32_to_fp16", "gpu_check_fp16_to_f32", "gpu_check_expf_nonpos", "gpu_check_sqrtf"):
+    for n in ("gpu_check_fp32_to_fp16", "gpu_check_fp16_to_f32", "gpu_check_expf_nonpos", "gpu_check_sqrtf",
+              "gpu_check_silu", "gpu_check_gelu"):
         getattr(L, n).restype = ctypes.c_uint64
         getattr(L, n).argtypes = []
     return L
 
 
 @pytest.mark.parametrize("name", ["gpu_check_fp32_to_fp16", "gpu_check_fp16_to_f32", "gpu_check_expf_nonpos",
-                                  "gpu_check_sqrtf"])
+                                  "gpu_check_sqrtf", "gpu_check_silu", "gpu_check_gelu"])
 def test_exhaustive_on_gpu(checks, name):
     assert getattr(checks, name)() == 0
 

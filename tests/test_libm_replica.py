@@ -8,8 +8,12 @@ checkers over ALL 2^32 float inputs:
                           reference computes);
   fp32 -> fp16         == IEEE round-to-nearest-even (_Float16 conversion);
   fp16 -> fp32         == exact widening;
-  GELU by table        == the formula (the kernels' saturation thresholds
-                          and compact table layout).
+  GELU by polynomial and table
+                       == the formula (the kernels' polynomial limits,
+                          saturation thresholds and compact table layout);
+  silu                 == x / (1 + glibc expf(-x)) (the kernels clamp
+                          expf's argument instead of selecting its special
+                          cases).
 
 The GPU kernels run this same code, so a GPU result can differ from the
 oracle only through the GPU's IEEE basic operations, which the GPU tests
@@ -31,7 +35,7 @@ def chk():
         pytest.fail(f"{LIB} missing: run __graft_entry__.build()")
     L = ctypes.CDLL(str(LIB))
     for n in ("check_expf", "check_expm1f", "check_tanhf", "check_logf", "check_sinf", "check_cosf", "check_log1pf",
-              "check_fp32_to_fp16", "check_gelu_table"):
+              "check_fp32_to_fp16", "check_gelu_table", "check_silu"):
         getattr(L, n).restype = ctypes.c_uint64
         getattr(L, n).argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int]
     L.check_fp16_to_f32.restype = ctypes.c_uint64
@@ -42,9 +46,24 @@ def chk():
 
 
 @pytest.mark.parametrize("fn", ["check_expf", "check_expm1f", "check_tanhf", "check_logf", "check_sinf", "check_cosf",
-                                "check_log1pf", "check_fp32_to_fp16", "check_gelu_table"])
+                                "check_log1pf", "check_fp32_to_fp16", "check_gelu_table", "check_silu"])
 def test_exhaustive(chk, fn):
     assert getattr(chk, fn)(0, 1 << 32, THREADS) == 0
+
+
+@pytest.mark.parametrize("negative", [0, 1])
+def test_gelu_polynomial_range_is_maximal(chk, negative):
+    """The kernels compute GELU by polynomial below an fp16 magnitude limit
+    per sign and look the rest up; the exhaustive table check shows the
+    polynomial right below each limit, this shows it fails at the limit, so
+    the table holds exactly the values the polynomial cannot give."""
+    chk.gelu_poly_first_miss.restype = ctypes.c_uint32
+    chk.gelu_poly_first_miss.argtypes = [ctypes.c_int]
+    chk.gelu_poly_limit.restype = ctypes.c_uint32
+    chk.gelu_poly_limit.argtypes = [ctypes.c_int]
+    limit = chk.gelu_poly_limit(negative)
+    assert chk.gelu_poly_first_miss(negative) == limit
+    assert limit == (0x34d0 if negative else 0x342e)
 
 
 def test_fp16_widening(chk):
