@@ -494,27 +494,32 @@ __global__ __launch_bounds__(kBlock) void k_softmax_lane(OrdView xv, OrdView yv,
 // tile, and the unpredictable segments are listed in order.
 //
 // Combine, wave 0: between two unpredictable segments lies a run of
-// predictable ones, all in one binade (the running sum is monotone and
-// consecutive intervals overlap), so the run adds the difference of two
-// scanned unit counts at once -- checked against the exact state, with a
-// fallback that adds the whole tile one addend at a time.  Each
+// predictable ones.  When the run lies in one binade with the running sum
+// (the grids of its first and last segments equal the state's), the run
+// adds an exact multiple of 2^u: its scanned unit count times 2^u, an f32
+// value, so one f32 addition adds the whole run exactly.  Each
 // unpredictable segment is added one f32 addition at a time, the
-// reference's own arithmetic, and the state restarts from the result.  A
-// row takes one walk per binade crossing and per segment holding a tie.
+// reference's own arithmetic.  So the combine is one flat sequence of f32
+// additions -- per unpredictable segment, its run then its addends -- with
+// each run's binade checked before and after its addition (a check that
+// fails falls back to adding the whole tile one addend at a time).  A row
+// takes SEG + 1 additions per binade crossing and per segment holding a
+// tie.  The sequence is read from LDS records, the next record loaded while
+// the current one is added: a handful of instructions per addition, where
+// a loop that rebuilt the state (m, u) per segment cost several times more.
 constexpr int32_t kNoGrid = -1000; // u of an unpredictable segment
 
-// What the combine needs of the i-th unpredictable segment f, in one
-// 16-byte-aligned record: f, the scanned units before it, the grid of the
-// segments on either side of it (the last of the run before it, the first
-// of the run after it) and its own addends.  Record nfail is a sentinel
-// with f = NT, the tile's total units and the last segment's grid.
+// The i-th unpredictable segment f in one 16-byte-aligned record: its
+// addends, the scanned units before it and the grids on either side of it
+// (the last segment of the run before it, the first of the run after it).
+// Record nfail is a sentinel: zero addends after the tile's last run.
 template <uint32_t SEG>
 struct alignas(16) FailRec {
-    uint32_t f;
-    uint32_t units; // units[f]: predictable units before segment f
-    int32_t u_before; // u[f - 1] (kNoGrid for f = 0)
-    int32_t u_after;  // u[f + 1] (kNoGrid past the tile)
-    float e[SEG];
+    float e[SEG];     // segment f's addends (+0 in the sentinel)
+    uint32_t units;   // predictable units before segment f (the tile's total in the sentinel)
+    int32_t u_before; // u[f - 1]: the run's last grid; kNoGrid when the run before f is empty
+    int32_t u_after;  // u[f + 1]: the next run's first grid; kNoGrid when it is empty
+    uint32_t pad;
 };
 
 template <uint32_t NT, uint32_t SEG>
@@ -610,7 +615,6 @@ __device__ __forceinline__ void seq_tile_sum(const float *s_e, SeqScratch<NT, SE
     }
     if (!ok) {
         FailRec<SEG> &r = sc.rec[fbase + static_cast<uint32_t>(__builtin_popcountll(failing & ((uint64_t{1} << lane) - 1)))];
-        r.f = t;
         r.units = ubase + uincl; // units contributes 0
         r.u_before = t > 0 ? sc.u[t - 1] : kNoGrid;
         r.u_after = t + 1 < NT ? sc.u[t + 1] : kNoGrid;
@@ -619,63 +623,59 @@ __device__ __forceinline__ void seq_tile_sum(const float *s_e, SeqScratch<NT, SE
     }
     if (t == NT - 1) {
         FailRec<SEG> &r = sc.rec[nfail];
-        r.f = NT;
         r.units = total;
-        r.u_before = sc.u[NT - 1];
+        r.u_before = ok ? u : kNoGrid;
         r.u_after = kNoGrid;
+#pragma unroll
+        for (uint32_t j = 0; j < SEG; ++j) r.e[j] = 0.0f;
     }
     __syncthreads();
     if (wave != 0 || !st.finite) return;
 
-    // Wave 0 runs the combine as uniform code: every value it reads from LDS
-    // is the same in all lanes and moved to a scalar register, so the
-    // control flow is scalar; the next record is loaded while the current
-    // one is used.
-    auto uni = [](uint32_t v) { return static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v))); };
-    const uint32_t nrec = uni(nfail);
-    uint32_t m = st.m;
-    int32_t gu = st.u;     // the state's grid exponent
-    bool bad = false;      // a run failed its check against the exact state
-    uint32_t prev_f1 = 0;  // first segment after the previous record's
+    // The flat walk, uniform across wave 0.  Record i's run is the
+    // segments between the previous record's segment and its own: its
+    // units are the difference of the two scanned counts, its first grid
+    // the previous record's u_after (u[0] for the first).  grid(): the
+    // exponent of the f32 spacing around a value >= +0 (2^-149 below the
+    // normal range).
+    auto grid = [](float v) {
+        const int32_t be = static_cast<int32_t>(__builtin_bit_cast(uint32_t, v) >> 23);
+        return (be > 0 ? be : 1) - 150;
+    };
+    const uint32_t nrec = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(nfail)));
+    float acc = s_prev;
+    bool bad = false;
     uint32_t prev_units = 0;
-    int32_t prev_after = static_cast<int32_t>(uni(static_cast<uint32_t>(sc.u[0])));
+    int32_t prev_after = sc.u[0];
     FailRec<SEG> cur = sc.rec[0];
     for (uint32_t i = 0; i <= nrec; ++i) {
         const FailRec<SEG> ahead = sc.rec[i < nrec ? i + 1 : nrec];
-        const uint32_t f = uni(cur.f);
-        if (f > prev_f1) { // the run prev_f1 .. f - 1 of predictable segments
-            const uint32_t add = uni(cur.units) - prev_units;
-            const int32_t u_last = static_cast<int32_t>(uni(static_cast<uint32_t>(cur.u_before)));
-            bad = bad || !(prev_after == gu && u_last == gu && m + add < kSeqLimit);
-            m += add;
-        }
-        if (f == NT) break;
-        // segment f, one f32 addition at a time
-        float acc = seq_value(m, gu);
+        const bool has_run = cur.u_before != kNoGrid;
+        const float run = has_run ? __builtin_ldexpf(static_cast<float>(cur.units - prev_units), cur.u_before) : 0.0f;
+        const float after = acc + run; // exact when the run stays in the state's binade
+        bad = bad || (has_run && !(grid(acc) == prev_after && prev_after == cur.u_before && grid(after) == cur.u_before));
+        acc = after;
 #pragma unroll
         for (uint32_t j = 0; j < SEG; ++j) acc += cur.e[j];
-        acc = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, acc)));
-        if (!(acc < __builtin_inff())) { // NaN (the addends are at most 1: never +inf)
-            st.finite = false;
-            st.special = acc;
-            return;
-        }
-        const SeqState h = seq_state(acc);
-        m = h.m;
-        gu = h.u;
-        prev_f1 = f + 1;
-        prev_units = uni(cur.units);
-        prev_after = static_cast<int32_t>(uni(static_cast<uint32_t>(cur.u_after)));
+        prev_units = cur.units;
+        prev_after = cur.u_after;
         cur = ahead;
     }
-    if (!bad) {
-        st.m = m;
-        st.u = gu;
+    acc = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, acc)));
+    if (!(acc < __builtin_inff())) { // NaN (the addends are at most 1: never +inf): final whatever the checks say
+        st.finite = false;
+        st.special = acc;
+        return;
+    }
+    if (__builtin_amdgcn_readfirstlane(static_cast<int>(bad)) == 0) {
+        const SeqState h = seq_state(acc);
+        st.m = h.m;
+        st.u = h.u;
         return;
     }
     // Not expected (the predictions carry a proven bound): the whole tile
     // again from its exact starting value, one addition at a time.
-    float acc = s_prev;
+    acc = s_prev;
     for (uint32_t g = 0; g < NT; ++g) acc = walk_segment<SEG>(s_e, g, acc);
     acc = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, acc)));
     if (!(acc < __builtin_inff())) {
