@@ -747,8 +747,13 @@ __global__ __launch_bounds__(NT) void k_softmax_seq(OrdView xv, OrdView yv, uint
 #pragma unroll
         for (uint32_t j = 0; j < SEG; ++j) {
             const uint32_t c = threadIdx.x + NT * j;
-            // +0 past the row's end adds nothing to a sum that is never -0
-            v[j] = c < n ? emel_expf_nonpos(v[j] - mx, tab) : 0.0f;
+            // +0 past the row's end adds nothing to a sum that is never -0.
+            // The exponential is computed for every lane (the clamped
+            // column is in bounds) and selected: a branch per element would
+            // serialise the table reads of the SEG exponentials.
+            float ej = emel_expf_nonpos(v[j] - mx, tab);
+            asm("" : "+v"(ej));
+            v[j] = c < n ? ej : 0.0f;
             s_e[c] = v[j];
             if (!kOneTile && c < n) y[yoff(t0 + c)] = v[j];
         }
@@ -888,11 +893,13 @@ hipError_t launch_softmax_seq(const Operand &x, const Operand &y, hipStream_t s)
     }
     if (rows > 0x7fffffffull) return hipErrorInvalidValue; // one workgroup per row
     // (threads, addends per segment) by row width, measured on MI355X: one
-    // tile covers rows up to 4096 columns, wider rows stream tiles of 4096
+    // tile covers rows up to 16384 columns, wider rows stream tiles of 16384
     if (ncols <= 512) launch_softmax_seq_nt<64, 8>(x, y, rows, s);
     else if (ncols <= 1024) launch_softmax_seq_nt<64, 16>(x, y, rows, s);
     else if (ncols <= 2048) launch_softmax_seq_nt<256, 8>(x, y, rows, s);
-    else launch_softmax_seq_nt<512, 8>(x, y, rows, s);
+    else if (ncols <= 4096) launch_softmax_seq_nt<256, 16>(x, y, rows, s);
+    else if (ncols <= 8192) launch_softmax_seq_nt<512, 16>(x, y, rows, s);
+    else launch_softmax_seq_nt<1024, 16>(x, y, rows, s);
     return hipGetLastError();
 }
 
