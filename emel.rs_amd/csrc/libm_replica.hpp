@@ -80,16 +80,19 @@
 
 namespace emel {
 
-// tab[i] = bits(2^(i/32)), the double nearest 2^(i/32), i = 0..31.
+// tab[i] = bits(2^(i/32)) - (i << 47): the double nearest 2^(i/32) with
+// i/32 taken back out of its exponent field, i = 0..31, so that adding
+// k << 47 to tab[k % 32] (the exponent field gains k / 32 and the i/32
+// cancels) gives bits(2^(k/32)) without a separate scaling.
 static constexpr uint64_t kExp2Table[32] = {
-    0x3ff0000000000000ull, 0x3ff059b0d3158574ull, 0x3ff0b5586cf9890full, 0x3ff11301d0125b51ull,
-    0x3ff172b83c7d517bull, 0x3ff1d4873168b9aaull, 0x3ff2387a6e756238ull, 0x3ff29e9df51fdee1ull,
-    0x3ff306fe0a31b715ull, 0x3ff371a7373aa9cbull, 0x3ff3dea64c123422ull, 0x3ff44e086061892dull,
-    0x3ff4bfdad5362a27ull, 0x3ff5342b569d4f82ull, 0x3ff5ab07dd485429ull, 0x3ff6247eb03a5585ull,
-    0x3ff6a09e667f3bcdull, 0x3ff71f75e8ec5f74ull, 0x3ff7a11473eb0187ull, 0x3ff82589994cce13ull,
-    0x3ff8ace5422aa0dbull, 0x3ff93737b0cdc5e5ull, 0x3ff9c49182a3f090ull, 0x3ffa5503b23e255dull,
-    0x3ffae89f995ad3adull, 0x3ffb7f76f2fb5e47ull, 0x3ffc199bdd85529cull, 0x3ffcb720dcef9069ull,
-    0x3ffd5818dcfba487ull, 0x3ffdfc97337b9b5full, 0x3ffea4afa2a490daull, 0x3fff50765b6e4540ull,
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
 };
 
 __host__ __device__ __forceinline__ float bits_to_f32(uint32_t u) { return __builtin_bit_cast(float, u); }
@@ -144,9 +147,17 @@ __host__ __device__ __forceinline__ float expf_main_path(float x, const uint64_t
     const uint64_t ki = f64_to_bits(kd);
     kd -= c.shift;
     const double r = __builtin_fma(c.inv_ln2n, xd, -kd);
-    // k is the low word of kd's bits; 2^(k/N) = 2^((k mod N)/N) * 2^floor(k/N)
-    const int32_t k = static_cast<int32_t>(static_cast<uint32_t>(ki));
-    const double s = __builtin_ldexp(bits_to_f64(tab[k & 31]), k >> 5);
+    // k is the low word of kd's bits.  2^(k/N) = tab[k mod N] + (k << 47) as
+    // 64-bit integers: the addend has no low word, so only the high word
+    // changes (by k << 15).  Exact while k / N stays inside the double
+    // exponent range, which it does for every |x| < 700; larger |x| give
+    // garbage here that the callers' range selects replace.
+    struct Words {
+        uint32_t lo, hi;
+    };
+    const uint32_t k = static_cast<uint32_t>(ki);
+    const Words tk = __builtin_bit_cast(Words, tab[k & 31]);
+    const double s = __builtin_bit_cast(double, Words{tk.lo, tk.hi + (k << 15)});
     const double z = __builtin_fma(c.c0, r, c.c1);
     const double r2 = r * r;
     double y = __builtin_fma(c.c2, r, 1.0);
