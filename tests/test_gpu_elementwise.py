@@ -189,6 +189,22 @@ def test_unary_fp16_grid(gpu, name):
     assert_bits_equal(o.result(), want, name)
 
 
+@pytest.mark.parametrize("n", [1, 3, 4, 5, 255, 1023, 1025, 262147, 2 * 2048 * 256 * 4 + 7])
+def test_heavy_unary_ragged_sizes(gpu, n):
+    """The libm-based unary formulas walk a resident grid (one float4 per
+    thread per step, a scalar tail): sizes below one float4, one short of and
+    past a workgroup, and past one resident generation of 2048 x 256 threads."""
+    x = normal(53 + n % 17, n, 8.0)
+    a = Pair(x, [n, 1, 1, 1]).to(gpu)
+    for name in ("silu", "exp", "tanh", "elu"):
+        o = Pair(np.zeros(n, np.float32), [n, 1, 1, 1]).to(gpu)
+        st = eh.Kernel().process_event(eh.OpUnary(eh.UnarySubOp(UNARY[name]), a.pview(), o.pview(mut=True)))
+        assert st == eh.Status.OK, eh.last_error()
+        want = np.zeros(n, np.float32)
+        assert orc.unary(UNARY[name], a.oview(), orc.view(want, o.ne)) == orc.OK
+        assert_bits_equal(o.result(), want, f"{name} n={n}")
+
+
 def test_exp_dense_sweep(gpu):
     # every 97th f32 bit pattern: ~44M inputs across the whole float line
     u = np.arange(0, 2 ** 32, 97, dtype=np.uint64).astype(np.uint32)
