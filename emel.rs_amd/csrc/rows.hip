@@ -722,10 +722,22 @@ __global__ __launch_bounds__(NT) void k_softmax_seq(OrdView xv, OrdView yv, uint
     // 1. maximum (NaN never wins; NaN and infinities reach the sum instead)
     float v[SEG];
     float mx = -__builtin_inff();
+    // Unit column strides (rows apart, columns contiguous: the common
+    // strided case) address a row from one uniform base with 32-bit offsets.
+    const bool unit = xs0 == 1 && (!kYRow || ys0 == 1);
     for (uint64_t t0 = 0; t0 < ncols; t0 += TILE) {
         const uint32_t n = tile_n(t0);
+        if (unit) {
+            const float *xp = x + xrow + static_cast<int64_t>(t0);
 #pragma unroll
-        for (uint32_t j = 0; j < SEG; ++j) v[j] = x[xrow + static_cast<int64_t>(col(t0, n, j)) * xs0];
+            for (uint32_t j = 0; j < SEG; ++j) {
+                const uint32_t c = threadIdx.x + NT * j;
+                v[j] = xp[c < n ? c : 0u];
+            }
+        } else {
+#pragma unroll
+            for (uint32_t j = 0; j < SEG; ++j) v[j] = x[xrow + static_cast<int64_t>(col(t0, n, j)) * xs0];
+        }
 #pragma unroll
         for (uint32_t j = 0; j < SEG; ++j) mx = threadIdx.x + NT * j < n ? __builtin_fmaxf(mx, v[j]) : mx;
     }
@@ -770,10 +782,16 @@ __global__ __launch_bounds__(NT) void k_softmax_seq(OrdView xv, OrdView yv, uint
     const double recip = 1.0 / static_cast<double>(s_total);
     if constexpr (kOneTile) {
         const uint32_t n = static_cast<uint32_t>(ncols);
+        if (unit && n == TILE) { // every column of every thread in the row: no per-element test
+            float *yp = y + yrow;
 #pragma unroll
-        for (uint32_t j = 0; j < SEG; ++j) {
-            const uint32_t c = threadIdx.x + NT * j;
-            if (c < n) y[yoff(c)] = div_by_recip(v[j], recip);
+            for (uint32_t j = 0; j < SEG; ++j) yp[threadIdx.x + NT * j] = div_by_recip(v[j], recip);
+        } else {
+#pragma unroll
+            for (uint32_t j = 0; j < SEG; ++j) {
+                const uint32_t c = threadIdx.x + NT * j;
+                if (c < n) y[yoff(c)] = div_by_recip(v[j], recip);
+            }
         }
     } else {
         for (uint64_t t0 = 0; t0 < ncols; t0 += TILE) {
