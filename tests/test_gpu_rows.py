@@ -195,6 +195,49 @@ def test_soft_max_strided_ties_and_saturation(gpu):
     assert got[0] == np.float32(2.0 ** -24)
 
 
+def exp_preimage(libm, value):
+    """A float32 x with glibc's expf(x) == value exactly, by walking the float neighbours of log(value)."""
+    x = np.float32(np.log(value))
+    for direction in (np.float32(np.inf), np.float32(-np.inf)):
+        y = x
+        for _ in range(4096):
+            if libm.expf(float(y)) == value:
+                return y
+            y = np.nextafter(y, direction)
+    raise AssertionError(f"no float32 x with expf(x) == {value}")
+
+
+def sequential_ties(e):
+    """Additions of the sequential float32 sum of e whose exact result is a rounding tie."""
+    s = np.concatenate([[np.float32(0.0)], np.cumsum(e, dtype=np.float32)[:-1]]).astype(np.float64)
+    exact = s + e.astype(np.float64)
+    ulp = np.ldexp(1.0, np.frexp(exact)[1] - 24)
+    return int(np.count_nonzero((exact > 0) & (np.mod(exact, ulp) == ulp / 2)))
+
+
+@pytest.mark.parametrize("cols", [512, 1024, 2048, 4096, 8192, 20000])
+def test_soft_max_strided_sparse_ties(gpu, cols):
+    """Rows of ones (x = 0) with a few addends 1 - 2^(k - 24): once the running sum passes 2^k they are
+    exact rounding ties, a handful per segment, next to runs of addends that are not."""
+    import ctypes
+    libm = ctypes.CDLL("libm.so.6")
+    libm.expf.restype, libm.expf.argtypes = ctypes.c_float, [ctypes.c_float]
+    top = int(np.log2(cols))
+    keys = np.array([exp_preimage(libm, 1.0 - 2.0 ** (k - 24)) for k in range(top - 3, top + 1)], np.float32)
+    g = np.random.Generator(np.random.PCG64(740 + cols))
+    rows = 6
+    x = np.zeros((rows, cols), np.float32)
+    for r in range(rows):
+        density = (1 / 64, 1 / 16, 1 / 4, 1 / 200, 1 / 32, 1 / 8)[r]
+        pick = g.random(cols) < density
+        x[r, pick] = keys[g.integers(0, len(keys), int(pick.sum()))]
+    e = np.ones((rows, cols), np.float32)  # the row max is 0: expf(x - 0)
+    e[x != 0] = np.array([libm.expf(float(v)) for v in x[x != 0]], np.float32)
+    assert sum(sequential_ties(e[r]) for r in range(rows)) >= rows * 4
+    got, want = strided_soft_max(gpu, padded_pair(x.reshape(-1), cols, rows, 2), [cols, rows, 1, 1])
+    assert_bits_equal(got, want, f"strided soft_max with sparse ties, {cols} columns")
+
+
 def causal_mask(nkv, nq):
     k = np.arange(nkv)[None, :]
     q = np.arange(nq)[:, None]
