@@ -11,7 +11,8 @@
 // arithmetic: f32-rounded squares summed in f64 (normalization.rs:343-362),
 // exp(x - max) summed in f64 (reductions.rs:565-601), divisions and square
 // roots correctly rounded.  The strided soft_max keeps the reference's
-// sequential f32 sum (reductions.rs:603-638) with one row per lane.
+// sequential f32 sum (reductions.rs:603-638), evaluated exactly by a
+// workgroup per row (one lane per row for rows of at most 64 columns).
 #include <cstdlib>
 
 #include "common.hpp"
@@ -585,14 +586,24 @@ __device__ __forceinline__ void seq_tile_sum(const float *s_e, SeqScratch<NT, SE
     (void)__builtin_frexp(hi, &ehi);
     bool ok = lo >= 0x1p-126 && hi < 0x1p127 && lo <= hi && elo == ehi;
     const int32_t u = elo - 1 - 23;
+    // seq_units of each addend, specialised to a segment in one binade:
+    // every addend is below 2^24 units there (no clamp needed, never NaN),
+    // each t - round(t) is exact, and every partial unit sum is an integer
+    // below 2^24, so four f32 partial sums hold them exactly.  A tie is
+    // |t - round(t)| == 1/2, taken from the largest distance.
     uint32_t units = 0;
     if (ok) {
+        float part[4];
+        float dist = 0.0f;
 #pragma unroll
         for (uint32_t j = 0; j < SEG; ++j) {
-            bool tie;
-            units += seq_units(e[j], u, tie);
-            ok = ok && !tie;
+            const float tj = __builtin_ldexpf(e[j], -u);
+            const float rj = __builtin_rintf(tj);
+            part[j % 4] = j < 4 ? rj : part[j % 4] + rj;
+            dist = __builtin_fmaxf(dist, __builtin_fabsf(tj - rj));
         }
+        units = static_cast<uint32_t>((part[0] + part[1]) + (part[2] + part[3]));
+        ok = dist != 0.5f;
     }
     units = ok ? units : 0u;
     sc.u[t] = ok ? u : kNoGrid;
