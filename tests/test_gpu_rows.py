@@ -27,8 +27,10 @@ def outlier_rows(x, cols, rows, seed, frac=0.01, factor=100.0):
     return x.reshape(-1)
 
 
+# (2048, 2048), (8192, 1536), (4096, 4096): one wave per row; (4096, 1535): the row range's edge
 @pytest.mark.parametrize("cols,rows", [(4096, 2048), (4096, 3), (1, 5), (3, 7), (64, 64), (1000, 9),
-                                       (8192, 4), (20000, 3)])
+                                       (8192, 4), (20000, 3), (2048, 2048), (8192, 1536), (4096, 4096),
+                                       (4096, 1535)])
 def test_rms_norm(gpu, cols, rows):
     x = outlier_rows(normal(101 + cols, cols * rows), cols, rows, 7)
     a = Pair(x, [cols, rows, 1, 1]).to(gpu)
@@ -43,8 +45,8 @@ def test_rms_norm(gpu, cols, rows):
     assert exact > 0.99, f"only {exact:.4%} bit-exact"
 
 
-def test_rms_norm_mul_config3(gpu):
-    cols, rows = 4096, 2048
+@pytest.mark.parametrize("cols,rows", [(4096, 2048), (2048, 1600), (8192, 2048), (4096, 1024)])
+def test_rms_norm_mul(gpu, cols, rows):
     x = outlier_rows(normal(111, cols * rows), cols, rows, 8)
     w = uniform(112, cols, 0.5, 1.5)
     a = Pair(x, [cols, rows, 1, 1]).to(gpu)
@@ -80,7 +82,7 @@ def test_rms_norm_strided_and_implicit(gpu):
     assert_close_rel(o.result(), want, RTOL, "implicit rms_norm")
 
 
-@pytest.mark.parametrize("cols,rows", [(4096, 64), (7, 9), (10000, 5)])
+@pytest.mark.parametrize("cols,rows", [(4096, 64), (7, 9), (10000, 5), (4096, 2048), (2048, 3000), (8192, 1600)])
 def test_norm(gpu, cols, rows):
     x = normal(131, cols * rows, 3.0) + np.float32(2.0)
     a = Pair(x, [cols, rows, 1, 1]).to(gpu)
