@@ -82,6 +82,21 @@ def test_rms_norm_strided_and_implicit(gpu):
     assert_close_rel(o.result(), want, RTOL, "implicit rms_norm")
 
 
+@pytest.mark.parametrize("op", ["rms_norm", "norm"])
+def test_norm_rows_padded_pitch(gpu, op):
+    """Rows 8 floats apart (a 16-byte-aligned pitch that is not the width) in the one-wave-per-row range."""
+    cols, rows = 4096, 2048
+    x = outlier_rows(normal(151, cols * rows, 2.0), cols, rows, 9) + np.float32(0.5)
+    a = padded_pair(x, cols, rows, 8).to(gpu)
+    o = Pair(np.zeros(cols * rows, np.float32), [cols, rows, 1, 1]).to(gpu)
+    ev = eh.OpRmsNorm if op == "rms_norm" else eh.OpNorm
+    assert eh.Kernel().process_event(ev(a.pview(), o.pview(mut=True), 1e-5)) == eh.Status.OK, eh.last_error()
+    want = np.zeros(cols * rows, np.float32)
+    fn = orc.rms_norm if op == "rms_norm" else orc.norm
+    assert fn(a.oview(), orc.view(want, o.ne), 1e-5) == orc.OK
+    assert_close_rel(o.result(), want, RTOL, f"{op} with a padded row pitch", atol=1e-6)
+
+
 @pytest.mark.parametrize("cols,rows", [(4096, 64), (7, 9), (10000, 5), (4096, 2048), (2048, 3000), (8192, 1600)])
 def test_norm(gpu, cols, rows):
     x = normal(131, cols * rows, 3.0) + np.float32(2.0)
