@@ -415,8 +415,9 @@ def test_soft_max_ext_fully_masked_and_non_finite(gpu, nkv, nq, nh):
     assert (np.isnan(got) == np.isnan(want)).all()
 
 
-@pytest.mark.parametrize("cols", [4096, 256, 20000, 37])
-def test_rms_norm_non_finite(gpu, cols):
+# (4096, 2040) and (2048, 1592): the special rows among enough plain rows for one wave per row
+@pytest.mark.parametrize("cols,extra", [(4096, 0), (256, 0), (20000, 0), (37, 0), (4096, 2040), (2048, 1592)])
+def test_rms_norm_non_finite(gpu, cols, extra):
     # x*x overflows f32 (sum +inf, scale 0: finite x -> 0, inf x -> NaN), NaN
     # and inf elements, an all-zero row (scale 1/sqrt(eps)), subnormals
     g = np.random.Generator(np.random.PCG64(421 + cols))
@@ -431,6 +432,7 @@ def test_rms_norm_non_finite(gpu, cols):
     rows.append(np.full(cols, np.float32(1e-40)))
     r = base(); r[:] = np.float32(3e38); rows.append(r)
     rows.append(base())
+    rows.extend(base() for _ in range(extra))
     x = np.concatenate(rows)
     n = len(rows)
     for ev, fn, what in ((lambda v, o: eh.OpRmsNorm(v, o, 1e-5), lambda a, o: orc.rms_norm(a, o, 1e-5), "rms_norm"),
