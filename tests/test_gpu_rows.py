@@ -27,10 +27,11 @@ def outlier_rows(x, cols, rows, seed, frac=0.01, factor=100.0):
     return x.reshape(-1)
 
 
-# (2048, 2048), (8192, 1536), (4096, 4096): one wave per row; (4096, 1535): the row range's edge
+# (2048, 2048), (8192, 1536), (4096, 4096), (2048, 1536): one wave per row; (4096, 1535), (2048, 4097):
+# just outside the row range
 @pytest.mark.parametrize("cols,rows", [(4096, 2048), (4096, 3), (1, 5), (3, 7), (64, 64), (1000, 9),
                                        (8192, 4), (20000, 3), (2048, 2048), (8192, 1536), (4096, 4096),
-                                       (4096, 1535)])
+                                       (4096, 1535), (2048, 1536), (2048, 4097)])
 def test_rms_norm(gpu, cols, rows):
     x = outlier_rows(normal(101 + cols, cols * rows), cols, rows, 7)
     a = Pair(x, [cols, rows, 1, 1]).to(gpu)
@@ -157,7 +158,8 @@ def strided_soft_max(gpu, a, out_ne):
 
 
 @pytest.mark.parametrize("cols,rows", [(4096, 512), (65, 40), (511, 7), (512, 9), (513, 5), (1024, 33),
-                                       (2048, 7), (2049, 3), (4097, 3), (20000, 4), (100000, 2), (64, 300)])
+                                       (2048, 7), (2049, 3), (4097, 3), (20000, 4), (100000, 2), (64, 300),
+                                       (1025, 3), (8192, 3), (8193, 2), (16384, 2), (16385, 2), (32768, 1)])
 def test_soft_max_strided_rows_bit_exact(gpu, cols, rows):
     x = normal(700 + cols, cols * rows, 3.0)
     got, want = strided_soft_max(gpu, padded_pair(x, cols, rows, 3), [cols, rows, 1, 1])
