@@ -162,13 +162,25 @@ __global__ __launch_bounds__(BS) void k_row_vec(RowGeo g, const float *x, float 
     __shared__ double lds_b[BS / kWave];       // second row reduction
     const uint64_t *tab = nullptr;
     ExpfConsts ec;
+    // The expf table goes to LDS.  With NW > 1, wave 0 loads it into a
+    // register ahead of the row, writes it once the row's data is in, and
+    // the max reduction's barrier orders it before use: no wave waits for
+    // the table before issuing its row loads.  With NW == 1 it is staged up
+    // front, before any wave may leave.
+    uint64_t tab_word = 0;
     if constexpr (kSoft) {
-        if (threadIdx.x < 32) lds_tab[threadIdx.x] = kExp2Table[threadIdx.x];
-        // with NW > 1 the max reduction's barrier orders the table before use
-        if constexpr (NW == 1) __syncthreads();
+        if constexpr (NW == 1) {
+            if (threadIdx.x < 32) lds_tab[threadIdx.x] = kExp2Table[threadIdx.x];
+            __syncthreads();
+        } else {
+            if (threadIdx.x < kWave) tab_word = kExp2Table[threadIdx.x % 32];
+        }
         tab = lds_tab;
         ec = expf_consts_in_vgprs();
     }
+    auto stage_table = [&]() {
+        if (threadIdx.x < 32) lds_tab[threadIdx.x] = tab_word;
+    };
     const uint32_t t = threadIdx.x % kTPR;
     uint32_t r; // uniform across the row's waves
     if constexpr (kRPB == 1) {
@@ -207,6 +219,7 @@ __global__ __launch_bounds__(BS) void k_row_vec(RowGeo g, const float *x, float 
         float4 v[NV];
 #pragma unroll
         for (int j = 0; j < NV; ++j) v[j] = in_row(j) ? load(t + kTPR * j) : make_float4(0.f, 0.f, 0.f, 0.f);
+        if constexpr (kSoft && NW > 1) stage_table();
         if constexpr (OP == RowOp::RmsNorm || OP == RowOp::RmsNormMul) {
             double acc = 0.0;
 #pragma unroll
@@ -269,6 +282,7 @@ __global__ __launch_bounds__(BS) void k_row_vec(RowGeo g, const float *x, float 
     } else {
         // streamed passes for rows wider than the register budget; the
         // intermediate passes use cached accesses so re-reads hit L2
+        if constexpr (kSoft && NW > 1) stage_table();
         if constexpr (OP == RowOp::RmsNorm || OP == RowOp::RmsNormMul) {
             double acc = 0.0;
             for (uint32_t idx = t; idx < nv; idx += kTPR) acc += sumsq4(xr[idx]);
@@ -714,9 +728,12 @@ __global__ __launch_bounds__(NT) void k_softmax_seq(OrdView xv, OrdView yv, uint
     __shared__ SeqScratch<NT, SEG> s_seq;
     __shared__ float s_red[NW];
     __shared__ float s_total;
-    if (threadIdx.x < 32) tab[threadIdx.x] = kExp2Table[threadIdx.x];
     const uint32_t wave = threadIdx.x / kWave;
     const uint32_t lane = threadIdx.x % kWave;
+    // the expf table: loaded by wave 0 ahead of the row, written to LDS once
+    // the row's maximum is formed (the barrier after it orders the table)
+    uint64_t tab_word = 0;
+    if (wave == 0) tab_word = kExp2Table[lane % 32];
     const uint64_t r = blockIdx.x;
     const int64_t xrow = row_offset(xv, r);
     const int64_t yrow = kYRow ? row_offset(yv, r) : 0;
@@ -752,6 +769,7 @@ __global__ __launch_bounds__(NT) void k_softmax_seq(OrdView xv, OrdView yv, uint
 #pragma unroll
         for (uint32_t j = 0; j < SEG; ++j) mx = threadIdx.x + NT * j < n ? __builtin_fmaxf(mx, v[j]) : mx;
     }
+    if (threadIdx.x < 32) tab[threadIdx.x] = tab_word;
     mx = wave_max_dpp(mx);
     if (lane == 0) s_red[wave] = mx;
     __syncthreads();
