@@ -239,13 +239,16 @@ __device__ __forceinline__ ExpCtx stage_table(uint64_t *lds)
 
 // ---- dense: every operand contiguous, paired by linear index -------------
 
-// Streaming policy measured on MI355X with cold buffers (a 22.5 MB and a
-// 256 MB array per operand): one float4 per thread, non-temporal loads and
-// stores, was fastest or tied for copy, mul, silu and swiglu at both sizes.
+// Streaming policy measured on MI355X with cold buffers: non-temporal loads
+// and stores, one float4 per thread for the copy (scale), swiglu and the
+// formulas.  The one-instruction binaries (add, sub, mul) stream 8 float4
+// per lane, each wave over 512 consecutive float4: fewer, fatter waves (mul
+// at [11008,512]: 11.85 against 12.5 us).  With 8 float4 per thread swiglu,
+// the row broadcast and a 541 MB copy were slower.
 template <Ew OP>
 struct Stream {
     static constexpr bool kNtLoad = true;
-    static constexpr int kVpt = 1;
+    static constexpr int kVpt = OP == Ew::Add || OP == Ew::Sub || OP == Ew::Mul ? 8 : 1;
 };
 
 template <Ew OP, int VPT>
@@ -257,11 +260,13 @@ __global__ __launch_bounds__(kBlock) void k_dense(const float *a, const float *b
     const float4 *a4 = reinterpret_cast<const float4 *>(a);
     const float4 *b4 = reinterpret_cast<const float4 *>(b);
     float4 *o4 = reinterpret_cast<float4 *>(o);
-    const uint64_t base = static_cast<uint64_t>(blockIdx.x) * (kBlock * VPT) + threadIdx.x;
+    // each wave streams VPT * 64 consecutive float4: lane l takes l, l + 64, ...
+    const uint64_t base = (static_cast<uint64_t>(blockIdx.x) * kBlock + (threadIdx.x & ~(kWave - 1u))) * VPT +
+                          threadIdx.x % kWave;
     float4 va[VPT], vb[VPT];
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-        const uint64_t i = base + static_cast<uint64_t>(j) * kBlock;
+        const uint64_t i = base + static_cast<uint64_t>(j) * kWave;
         if (i < nvec) {
             va[j] = Stream<OP>::kNtLoad ? ld_nt(a4 + i) : a4[i];
             if constexpr (Fn<OP>::kBinary) vb[j] = Stream<OP>::kNtLoad ? ld_nt(b4 + i) : b4[i];
@@ -270,7 +275,7 @@ __global__ __launch_bounds__(kBlock) void k_dense(const float *a, const float *b
     }
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-        const uint64_t i = base + static_cast<uint64_t>(j) * kBlock;
+        const uint64_t i = base + static_cast<uint64_t>(j) * kWave;
         if (i < nvec) st_nt(o4 + i, apply4<OP>(va[j], vb[j], s, tab));
     }
     const uint64_t gid = static_cast<uint64_t>(blockIdx.x) * kBlock + threadIdx.x;
@@ -595,7 +600,7 @@ hipError_t launch_op(const EwArgs &x, hipStream_t stream)
     if (kBin && ne0 % 4 == 0 && vec_ok && contiguous(x.o) && contiguous(x.a) && same_ne(x.a, x.o) &&
         x.a_addr != Addr::Ordinal && x.b.ne[0] == ne0 && x.b.ne[1] == 1 && x.b.ne[2] == 1 && x.b.ne[3] == 1 &&
         x.b.st[0] == 1 && n / 4 < 0xffffffffull && x.b_addr != Addr::Ordinal) {
-        constexpr int vpt = Stream<OP>::kVpt;
+        constexpr int vpt = 1; // more float4 per thread measured slower here
         const uint32_t nvec = static_cast<uint32_t>(n / 4);
         const uint32_t per_block = kBlock * vpt;
         const dim3 grid((nvec + per_block - 1) / per_block);

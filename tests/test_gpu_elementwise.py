@@ -53,8 +53,10 @@ def run_binary(gpu, op, a: Pair, b: Pair, o: Pair, ev=None):
     assert_bits_equal(o.result(), want, f"binary op {op}")
 
 
+# add, sub and mul stream 512 float4 per wave, 2048 per workgroup: 2049, 8191, 8196 and 24579
+# end inside a wave's and a workgroup's span
 @pytest.mark.parametrize("op", [orc.ADD, orc.SUB, orc.MUL, orc.DIV])
-@pytest.mark.parametrize("n", [1, 3, 4, 5, 255, 1023, 4097, 11008 * 512])
+@pytest.mark.parametrize("n", [1, 3, 4, 5, 255, 1023, 4097, 11008 * 512, 2049, 8191, 8196, 24579])
 def test_binary_dense(gpu, op, n):
     a = Pair(uniform(11 + n, n), [n, 1, 1, 1])
     b = Pair(uniform(17 + n, n), [n, 1, 1, 1])
