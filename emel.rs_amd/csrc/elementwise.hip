@@ -261,8 +261,9 @@ __global__ __launch_bounds__(kBlock) void k_dense(const float *a, const float *b
     const float4 *b4 = reinterpret_cast<const float4 *>(b);
     float4 *o4 = reinterpret_cast<float4 *>(o);
     // each wave streams VPT * 64 consecutive float4: lane l takes l, l + 64, ...
-    const uint64_t base = (static_cast<uint64_t>(blockIdx.x) * kBlock + (threadIdx.x & ~(kWave - 1u))) * VPT +
-                          threadIdx.x % kWave;
+    const uint64_t base = VPT == 1 ? static_cast<uint64_t>(blockIdx.x) * kBlock + threadIdx.x
+                                   : (static_cast<uint64_t>(blockIdx.x) * kBlock + (threadIdx.x & ~(kWave - 1u))) * VPT +
+                                         threadIdx.x % kWave;
     float4 va[VPT], vb[VPT];
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
