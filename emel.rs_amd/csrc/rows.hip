@@ -163,10 +163,11 @@ __global__ __launch_bounds__(BS) void k_row_vec(RowGeo g, const float *x, float 
     const uint64_t *tab = nullptr;
     ExpfConsts ec;
     // The expf table goes to LDS.  With NW > 1, wave 0 loads it into a
-    // register ahead of the row, writes it once the row's data is in, and
-    // the max reduction's barrier orders it before use: no wave waits for
-    // the table before issuing its row loads.  With NW == 1 it is staged up
-    // front, before any wave may leave.
+    // register ahead of the row and writes it once the row's loads are
+    // issued (waiting for the table load only), and the max reduction's
+    // barrier orders it before use: no wave waits for the table before
+    // issuing its row loads.  With NW == 1 it is staged up front, before
+    // any wave may leave.
     uint64_t tab_word = 0;
     if constexpr (kSoft) {
         if constexpr (NW == 1) {
@@ -730,8 +731,8 @@ __global__ __launch_bounds__(NT) void k_softmax_seq(OrdView xv, OrdView yv, uint
     __shared__ float s_total;
     const uint32_t wave = threadIdx.x / kWave;
     const uint32_t lane = threadIdx.x % kWave;
-    // the expf table: loaded by wave 0 ahead of the row, written to LDS once
-    // the row's maximum is formed (the barrier after it orders the table)
+    // the expf table: loaded by wave 0 ahead of the row, written to LDS after
+    // the row's loads (the barrier after the maximum orders the table)
     uint64_t tab_word = 0;
     if (wave == 0) tab_word = kExp2Table[lane % 32];
     const uint64_t r = blockIdx.x;
@@ -919,8 +920,8 @@ void launch_wave_rows(const RowGeo &g, const RowArgs &a, hipStream_t s)
 // streaming in passes.  Measured on MI355X: the normalisations of 1536 to
 // 4096 rows of exactly 2048, 4096 or 8192 columns run faster with one wave
 // per row in 64-thread workgroups (11.3 against 12.9 us for rms_norm at
-// [4096, 2048]; 1.5 to 3 times the 1024 SIMDs in waves, each with its whole
-// row in flight).  Fewer rows leave SIMDs idle and more rows favour four
+// [4096, 2048]; 1.5 to 4 waves per SIMD, each with its whole row in
+// flight).  Fewer rows leave SIMDs idle and more rows favour four
 // waves per row, and the softmaxes' two reductions and exponentials favour
 // four waves per row at every row count.
 template <RowOp OP>
