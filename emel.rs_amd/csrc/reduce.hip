@@ -111,14 +111,13 @@ __device__ __forceinline__ void accumulate(const RedGeo &g, const float *x, int6
             sum += static_cast<double>(v);
         }
     };
-    if (g.mode == kModeVec) {
+    if (!kArg && g.mode == kModeVec) { // argmax's vector mode is argmax_chunk_vec
         // The range is read through a buffer descriptor bounded to it: a
         // load past its end returns zeros without touching memory.  Each
         // batch issues kBatch non-temporal 128-bit loads per thread
         // unconditionally (one round trip; no lane-dependent branches, which
-        // would serialise the loads), then takes the in-range ones.  Zeros
-        // leave a sum unchanged: a partial sum that starts at +0.0 is never
-        // -0.0.
+        // would serialise the loads).  Zeros leave a sum unchanged: a partial
+        // sum that starts at +0.0 is never -0.0.
         constexpr int kBatch = kRedBatch;
         const uint32_t nvec = static_cast<uint32_t>((c1 - c0) / 4);
         const BufRsrc r = buffer_rsrc(x + base + c0, nvec * 16u);
@@ -126,23 +125,10 @@ __device__ __forceinline__ void accumulate(const RedGeo &g, const float *x, int6
             float4 q[kBatch];
 #pragma unroll
             for (int j = 0; j < kBatch; ++j) q[j] = ld_buf_nt(r, (v0 + j * kBlock + threadIdx.x) * 16u);
-            if (v0 == 0) first = q[0].x;
 #pragma unroll
-            for (int j = 0; j < kBatch; ++j) {
-                const uint32_t k = v0 + j * kBlock + threadIdx.x;
-                if constexpr (kArg) {
-                    if (k < nvec) {
-                        const uint64_t c = c0 + 4 * k;
-                        take(q[j].x, c);
-                        take(q[j].y, c + 1);
-                        take(q[j].z, c + 2);
-                        take(q[j].w, c + 3);
-                    }
-                } else {
-                    sum += (static_cast<double>(q[j].x) + static_cast<double>(q[j].y)) +
-                           (static_cast<double>(q[j].z) + static_cast<double>(q[j].w));
-                }
-            }
+            for (int j = 0; j < kBatch; ++j)
+                sum += (static_cast<double>(q[j].x) + static_cast<double>(q[j].y)) +
+                       (static_cast<double>(q[j].z) + static_cast<double>(q[j].w));
         }
     } else if (g.mode == kModeScalar) {
         for (uint64_t c = c0 + threadIdx.x; c < c1; c += kBlock) {
@@ -157,6 +143,198 @@ __device__ __forceinline__ void accumulate(const RedGeo &g, const float *x, int6
             take(v, c);
         }
     }
+}
+
+// ---- argmax over a 128-bit-vectorised chunk ----------------------------------
+//
+// The per-element form above (compare, then select value and index) is a
+// dependent chain of 3 instructions per element.  The vector path splits it:
+//   1. each lane takes the maximum of its batch's non-NaN values with a
+//      v_max3_f32 tree (independent operations, ~1 instruction per 2
+//      elements);
+//   2. the workgroup forms the chunk maximum M of those lane maxima;
+//   3. only lanes whose maximum equals M look for the first column holding
+//      a value equal to M (usually one lane per chunk).
+// This is the reference's strict-> scan: its winner is the first column
+// whose value equals the maximum of the non-NaN values (float equality, so
+// -0.0 and +0.0 tie and the earlier column wins), since every earlier value
+// is smaller and no later equal value is strictly greater.
+
+// v_max3_f32 as the instruction, without the canonicalising v_max_f32 that
+// clang puts in front of every operand of fmaxf.  In IEEE mode a quiet NaN
+// operand is ignored and a signalling one makes the result a quiet NaN;
+// lane_max rescans exactly whenever the tree yields NaN.
+__device__ __forceinline__ float max3_raw(float a, float b, float c)
+{
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
+template <int N>
+__device__ __forceinline__ float max3_tree(const float (&v)[N])
+{
+    constexpr int M = (N + 2) / 3;
+    float w[M];
+#pragma unroll
+    for (int i = 0; i < M; ++i) {
+        const float a = v[3 * i];
+        if (3 * i + 1 >= N) {
+            w[i] = a; // a lone leftover goes up a level as it is
+        } else {
+            const float b = v[3 * i + 1];
+            const float c = 3 * i + 2 < N ? v[3 * i + 2] : a;
+            w[i] = max3_raw(a, b, c);
+        }
+    }
+    if constexpr (M == 1) return w[0];
+    else return max3_tree(w);
+}
+
+template <int B>
+__device__ __forceinline__ void flatten(const float4 (&q)[B], float (&v)[4 * B])
+{
+#pragma unroll
+    for (int j = 0; j < B; ++j) {
+        v[4 * j] = q[j].x;
+        v[4 * j + 1] = q[j].y;
+        v[4 * j + 2] = q[j].z;
+        v[4 * j + 3] = q[j].w;
+    }
+}
+
+// Maximum of the lane's non-NaN values, -inf when it has none.
+template <int B>
+__device__ __forceinline__ float lane_max(const float (&v)[4 * B])
+{
+    float m = max3_tree(v);
+    if (m != m) { // a signalling NaN, or no non-NaN value at all
+        m = -__builtin_inff();
+#pragma unroll
+        for (int i = 0; i < 4 * B; ++i) m = v[i] > m ? v[i] : m;
+    }
+    return m;
+}
+
+// Position (float4 j * 4 + component) of the lane's first value equal to m,
+// or 0xffffffff.
+template <int B>
+__device__ __forceinline__ uint32_t lane_first(const float (&v)[4 * B], float m)
+{
+    uint32_t p = 0xffffffffu;
+#pragma unroll
+    for (int i = 4 * B - 1; i >= 0; --i) p = v[i] == m ? static_cast<uint32_t>(i) : p;
+    return p;
+}
+
+// Total order on non-NaN floats as signed integers (-0.0 just below +0.0).
+__device__ __forceinline__ int32_t f32_order(float f)
+{
+    const int32_t b = __builtin_bit_cast(int32_t, f);
+    return b ^ ((b >> 31) & 0x7fffffff);
+}
+
+__device__ __forceinline__ float f32_from_order(int32_t k)
+{
+    return __builtin_bit_cast(float, k ^ ((k >> 31) & 0x7fffffff));
+}
+
+__device__ __forceinline__ int32_t wave_max_dpp_i32(int32_t v)
+{
+    const auto step = [](int32_t a, int32_t b) { return a > b ? a : b; };
+    v = step(v, static_cast<int32_t>(dpp32<kDppXor1>(static_cast<uint32_t>(v))));
+    v = step(v, static_cast<int32_t>(dpp32<kDppXor2>(static_cast<uint32_t>(v))));
+    v = step(v, static_cast<int32_t>(dpp32<kDppHalfMirror>(static_cast<uint32_t>(v))));
+    v = step(v, static_cast<int32_t>(dpp32<kDppMirror>(static_cast<uint32_t>(v))));
+    const int32_t a = static_cast<int32_t>(lane_u32(static_cast<uint32_t>(v), 0));
+    const int32_t b = static_cast<int32_t>(lane_u32(static_cast<uint32_t>(v), 16));
+    const int32_t c = static_cast<int32_t>(lane_u32(static_cast<uint32_t>(v), 32));
+    const int32_t d = static_cast<int32_t>(lane_u32(static_cast<uint32_t>(v), 48));
+    return step(step(a, b), step(c, d));
+}
+
+// The (value, column) candidate of columns [c0, c0 + 4 nvec) of the row at
+// x + base, with 16-byte aligned rows; every thread of the workgroup calls
+// it.  Wave 0 returns true with the candidate in `out` (uniform); the other
+// waves return false and have nothing more to do.  `nan0` is true when the
+// chunk's first column holds a NaN.  Thread t reads float4 t, t + 256, ...
+// of each batch, like the sums.  (Measured at config 5: giving each wave a
+// contiguous quarter of the chunk, or letting the wave that holds the
+// maximum publish without the second barrier, were both 0.2 us slower.)
+__device__ __forceinline__ bool argmax_chunk_vec(const float *x, int64_t base, uint64_t c0, uint32_t nvec,
+                                                 ArgPart &out, bool &nan0)
+{
+    constexpr int kBatch = kRedBatch;
+    constexpr uint32_t kSpan = kBatch * kBlock; // float4 per batch
+    constexpr uint32_t kWaves = kBlock / kWave;
+    __shared__ int32_t s_key[kWaves];
+    __shared__ uint32_t s_col[kWaves];
+    __shared__ uint32_t s_nan0;
+    const uint32_t t = threadIdx.x;
+    const uint32_t wave = t / kWave;
+    const BufRsrc r = buffer_rsrc(x + base + c0, nvec * 16u);
+    const auto col = [&](uint32_t v0, uint32_t p) { return (v0 + (p >> 2) * kBlock + t) * 4u + (p & 3u); };
+
+    // Batches before the last, all in range: the lane's running candidate
+    // (value, chunk-relative column), replaced only by a strictly greater one.
+    float run_v = -__builtin_inff();
+    uint32_t run_c = 0xffffffffu;
+    uint32_t v0 = 0;
+    float first = 0.0f; // thread 0: column c0
+    float4 q[kBatch];
+    float v[4 * kBatch];
+    for (; v0 + kSpan < nvec; v0 += kSpan) {
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) q[j] = ld_buf_nt(r, (v0 + j * kBlock + t) * 16u);
+        if (v0 == 0) first = q[0].x;
+        flatten(q, v);
+        const float bm = lane_max<kBatch>(v);
+        if (bm > run_v) {
+            run_c = col(v0, lane_first<kBatch>(v, bm));
+            run_v = bm;
+        }
+    }
+    // The last batch.  A lane's float4 index past the chunk is clamped to its
+    // last float4 (nvec >= 1: every chunk holds a column): the duplicate
+    // cannot change the maximum, and the column it reports, computed from
+    // the unclamped index, is above that of the lane that holds the float4,
+    // so the minimum over lanes never takes it.
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) q[j] = ld_buf_nt(r, min(v0 + j * kBlock + t, nvec - 1) * 16u);
+    if (v0 == 0) first = q[0].x;
+    flatten(q, v);
+    const float bm = lane_max<kBatch>(v);
+    const float lm = bm > run_v ? bm : run_v;
+
+    // chunk maximum
+    const int32_t wk = wave_max_dpp_i32(f32_order(lm));
+    if (t % kWave == 0) s_key[wave] = wk;
+    if (t == 0) s_nan0 = first != first;
+    __syncthreads();
+    int32_t mk = s_key[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) mk = mk > s_key[w] ? mk : s_key[w];
+    const float m = f32_from_order(mk);
+
+    // first column holding it: an earlier batch's (lower) column, else the
+    // last batch's
+    uint32_t c = 0xffffffffu;
+    if (lm == m) {
+        if (run_v == m) {
+            c = run_c;
+        } else {
+            const uint32_t p = lane_first<kBatch>(v, m);
+            if (p != 0xffffffffu) c = col(v0, p);
+        }
+    }
+    c = wave_min_dpp(c);
+    if (t % kWave == 0) s_col[wave] = c;
+    __syncthreads();
+    nan0 = s_nan0 != 0;
+    if (wave != 0) return false;
+    c = min(min(s_col[0], s_col[1]), min(s_col[2], s_col[3]));
+    out = ArgPart{m, c == 0xffffffffu ? c : static_cast<uint32_t>(c0) + c};
+    return true;
 }
 
 // Writes the row result from its combined (sum | (value, index)) word.
@@ -211,18 +389,20 @@ __device__ __forceinline__ uint64_t merge_slots(const uint64_t *slots, uint32_t 
 }
 
 // Publishes `packed` into `slot` and counts the arrival; true for the last of
-// `n` arrivals (uniform).  Lane 0 does the memory operations.
+// `n` arrivals (uniform).  Lane 0 of the calling wave does the memory
+// operations.
 __device__ __forceinline__ bool arrive(uint64_t *slot, uint32_t *counter, uint32_t n, uint64_t packed)
 {
+    const bool lead = threadIdx.x % kWave == 0;
     uint32_t prev = 0;
-    if (threadIdx.x == 0) {
+    if (lead) {
         __hip_atomic_store(slot, packed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // the partial is at the coherence point
         prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     prev = __builtin_amdgcn_readfirstlane(prev);
     if (prev != n - 1) return false;
-    if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lead) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return true;
 }
 
@@ -257,31 +437,48 @@ __global__ __launch_bounds__(kBlock) void k_reduce(RedGeo g, const float *x, voi
     float bv = -__builtin_inff();
     uint32_t bi = 0xffffffffu; // "no candidate": loses every tie on index
     float first = 0.0f;        // thread 0 of chunk 0: the row's column 0
-    accumulate<OP>(g, x, base, c0, c1, sum, bv, bi, first);
-
+    bool vec_arg = false;
+    bool nan0 = false; // the chunk's first column is NaN (vector argmax)
     if constexpr (kArg) {
-        wave_argmax_dpp(bv, bi);
-        if (lane == 0) {
-            s_v[wave] = bv;
-            s_i[wave] = bi;
+        if (g.mode == kModeVec) {
+            ArgPart p;
+            if (!argmax_chunk_vec(x, base, c0, static_cast<uint32_t>((c1 - c0) / 4), p, nan0)) return;
+            bv = p.v;
+            bi = p.i;
+            vec_arg = true;
         }
-    } else {
-        sum = wave_sum_dpp(sum);
-        if (lane == 0) s_sum[wave] = sum;
     }
-    __syncthreads();
-    if (wave != 0) return;
+    if (!vec_arg) {
+        accumulate<OP>(g, x, base, c0, c1, sum, bv, bi, first);
+        if constexpr (kArg) {
+            wave_argmax_dpp(bv, bi);
+            if (lane == 0) {
+                s_v[wave] = bv;
+                s_i[wave] = bi;
+            }
+        } else {
+            sum = wave_sum_dpp(sum);
+            if (lane == 0) s_sum[wave] = sum;
+        }
+        __syncthreads();
+    }
     // wave 0 alone from here on: the partial is uniform across it
+    if (!vec_arg && wave != 0) return; // (argmax_chunk_vec returned the other waves)
     uint64_t packed;
     if constexpr (kArg) {
-        float v = s_v[0];
-        uint32_t i = s_i[0];
-        for (int w = 1; w < kBlock / kWave; ++w) argmax_merge(v, i, s_v[w], s_i[w]);
+        float v = bv;
+        uint32_t i = bi;
+        if (!vec_arg) {
+            v = s_v[0];
+            i = s_i[0];
+            for (int w = 1; w < kBlock / kWave; ++w) argmax_merge(v, i, s_v[w], s_i[w]);
+            first = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, first))); // thread 0
+            nan0 = first != first;
+        }
         // A NaN in column 0 decides the row: chunk 0's partial becomes
         // (+inf, 0), which every other candidate loses to (equal value and a
         // higher index, or a lower value).
-        first = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, first))); // thread 0
-        if (chunk == 0 && first != first) {
+        if (chunk == 0 && nan0) {
             v = __builtin_inff();
             i = 0;
         }

@@ -149,18 +149,85 @@ def test_scalar_reductions(gpu, ne, nb):
             assert abs(float(got[0]) - float(want[0])) <= 1e-5 * abs(float(want[0])) + floor, (got, want)
 
 
-def test_repeated_launches_reuse_workspace(gpu):
-    # the split-row counters are reset by each launch: results stay right
-    cols, rows = 151936, 64
-    x, where = planted_logits(cols, rows, 261)
-    a = Pair(x, [cols, rows, 1, 1]).to(gpu)
-    o = Pair(np.zeros(rows, np.int32), [1, rows, 1, 1]).to(gpu)
-    k = eh.Kernel(synchronous=False)
-    for _ in range(50):
-        assert k.process_event(eh.OpArgmaxRows(a.pview(), o.pview(mut=True))) == eh.Status.OK
+def _alternating_launches(gpu, event, oracle_fn, cols, rows, out_dtype, seeds, launches=12):
+    """Back-to-back launches, no synchronisation between them, alternating
+    between inputs that differ in every row, each into its own output.  A
+    merge that read a partial left by the previous launch (same slots, other
+    data) would give that launch's row result, so every output is checked
+    against the oracle."""
     import torch
+
+    ins = []
+    for sd in seeds:
+        x, _ = planted_logits(cols, rows, sd)
+        ins.append(Pair(x, [cols, rows, 1, 1]).to(gpu))
+    outs = [Pair(np.zeros(rows, out_dtype), [1, rows, 1, 1]).to(gpu) for _ in range(launches)]
+    k = eh.Kernel(synchronous=False)
+    for i in range(launches):
+        assert k.process_event(event(ins[i % len(ins)].pview(), outs[i].pview(mut=True))) == eh.Status.OK
     torch.cuda.synchronize()
-    assert (o.result() == where).all()
+    wants = []
+    for a in ins:
+        w = np.zeros(rows, out_dtype)
+        assert oracle_fn(a.oview(), orc.view(w, [1, rows, 1, 1])) == orc.OK
+        wants.append(w)
+    for i in range(launches):
+        got, want = outs[i].result(), wants[i % len(ins)]
+        if out_dtype == np.int32:
+            assert (got == want).all(), (i, np.flatnonzero(got != want)[:5])
+        else:
+            assert_close_rel(got, want, 1e-5, f"launch {i}", atol=1e-12 * 4 * cols)
+    return wants
+
+
+@pytest.mark.parametrize("cols,rows", [(151936, 64),   # config 5: 32 chunks per row, one merge level
+                                       (600000, 4)])   # 512 chunks per row: two merge levels
+def test_alternating_inputs_argmax_rows(gpu, cols, rows):
+    wants = _alternating_launches(gpu, eh.OpArgmaxRows, orc.argmax_rows, cols, rows, np.int32, (261, 262))
+    assert (wants[0] != wants[1]).all()  # every row's answer differs between the two inputs
+
+
+@pytest.mark.parametrize("cols,rows", [(151936, 64), (600000, 4)])
+def test_alternating_inputs_sum_rows(gpu, cols, rows):
+    wants = _alternating_launches(gpu, eh.OpSumRows, orc.sum_rows, cols, rows, np.float32, (263, 264))
+    assert (wants[0] != wants[1]).all()
+
+
+def _f32_bits(u):
+    return np.array(u, np.uint32).view(np.float32)
+
+
+@pytest.mark.parametrize("cols,rows", [(151936, 12),   # 149 chunks of 1024 columns: one batch each
+                                       (8192, 2048),   # one chunk per row, 2 batches (the second partial)
+                                       (13004, 2100),  # 3 batches, the last partial
+                                       (5124, 2048)])  # 2 batches, the last holding one float4
+def test_argmax_rows_vector_path_corners(gpu, cols, rows):
+    """The vector path's maximum tree, its search and the clamped last batch:
+    maxima in an earlier batch tied by a later one, maxima in a chunk's last
+    float4 (re-read by the lanes past the end), signalling NaNs, +-0 ties,
+    rows that are all negative, all -inf or -inf with NaNs."""
+    g = np.random.Generator(np.random.PCG64(281 + cols))
+    x = g.standard_normal(cols * rows).astype(np.float32).reshape(rows, cols)
+    snan_p, snan_n = _f32_bits(0x7F800001), _f32_bits(0xFFA00000)
+    n = 0
+    def row():
+        nonlocal n
+        n += 1
+        return x[n - 1]
+    r = row(); r[5] = 9.0; r[cols - 1] = 9.0                          # tie: first batch vs last float4 -> 5
+    r = row(); r[cols - 1] = 9.0                                       # maximum in the chunk's last column
+    r = row(); r[cols - 4] = 9.0                                       # ... its last float4's first column
+    r = row(); r[1::7] = snan_p; r[100] = 20.0                         # signalling NaNs everywhere -> 100
+    r = row(); r[:] = snan_n; r[0] = -5.0; r[cols // 2] = -1.0         # all sNaN but two values
+    r = row(); r[:] = -np.abs(r) - 1.0; r[cols - 2] = -0.5             # all negative: no zero from a pad
+    r = row(); r[:] = -1.0; r[3] = -0.0; r[cols - 1] = 0.0; r[cols // 2] = -0.0   # +-0 tie -> 3
+    r = row(); r[:] = -np.inf                                          # all -inf -> 0
+    r = row(); r[:] = np.nan; r[1] = -np.inf; r[cols - 3] = -np.inf    # NaN at 0 -> 0
+    r = row(); r[:] = np.nan; r[0] = -np.inf; r[cols - 3] = -np.inf    # -> 0
+    r = row(); r[:] = _f32_bits(0x7FC00001); r[0] = -2.0; r[cols - 1] = 1.0   # quiet NaNs -> cols-1
+    r = row(); r[1280 * 4 + 1] = 50.0; r[2 * 1280 * 4 + 7 if 2 * 1280 * 4 + 7 < cols else 0] = 50.0
+    got = run_argmax_rows(gpu, x.reshape(-1), [cols, rows, 1, 1])
+    assert list(got[[0, 1, 2, 3, 6, 7, 8, 9, 10]]) == [5, cols - 1, cols - 4, 100, 3, 0, 0, 0, cols - 1], got[:12]
 
 
 def test_sum_rows_non_finite(gpu):
