@@ -17,8 +17,8 @@ launches of that op that cycle through at least 1 GiB of distinct buffer
 sets, so those launches are cold too.  The roofline object describes the
 dominant kernel (the scaled + masked soft_max of config 4, over half of the
 step's bytes).  The CPU baseline times the C oracle (a single-threaded
-restatement of the reference's CPU path) on a bounded sample of the same
-workload.
+restatement of the reference's CPU path) on the same config tensors: one
+warm-up run, then the median of 5.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--ops a,b] [--no-cpu] [--no-copy] [--pcie] [--no-gather]
                     [--no-sampler] [--launches N]
@@ -134,6 +134,7 @@ COPY_BYTES = 2 * 268435456  # the calibration copy: 256 MiB read + 256 MiB writt
 
 
 ROTATE_BYTES = 1 << 30  # per-op timing cycles through at least this many distinct bytes
+WARM_MS = 3.0  # each per-op graph (and copy reference) runs this long before it is timed
 
 
 class GpuSuite:
@@ -245,33 +246,43 @@ class GpuSuite:
             raise RuntimeError(f"{name}: {st.name}: {self.eh.last_error()}")
 
 
-def copy_ceilings(suite, sizes, steps, capture, timed):
-    """Times OpScale(1.0) moving each algorithmic byte count (half read, half
-    written) over rotating buffer sets totalling >= ROTATE_BYTES; returns
-    {bytes: ms per launch}."""
+COPY_SHAPES = ("FLAT", "WAVE4", "WAVE8", "WALK")
+
+
+def copy_ceilings(suite, sizes, steps, capture, timed, warm):
+    """Times a bit copy moving each algorithmic byte count (half read, half
+    written) with every streaming shape of emel_stream_copy (one float4 per
+    thread; 4 or 8 float4 per lane, wave-contiguous; one resident generation
+    walking grid-stride), over rotating buffer sets totalling >=
+    ROTATE_BYTES.  Returns {bytes: {shape: ms per launch}}."""
     torch, eh = suite.torch, suite.eh
+    sid = suite.stream.cuda_stream
     out = {}
     for nbytes in sorted(set(sizes)):
         n = (nbytes // 8) // 64 * 64  # floats per side, 256-byte aligned slices
         slots = max(2, -(-ROTATE_BYTES // (8 * n)))
         src = torch.zeros(slots * n, dtype=torch.float32, device="cuda:0")
         dst = torch.empty(slots * n, dtype=torch.float32, device="cuda:0")
-        lay = eh.Layout.contiguous(eh.DType.F32, [n, 1, 1, 1])
-        evs = [eh.OpScale(eh.TensorView(src[i * n:(i + 1) * n], lay), eh.TensorViewMut(dst[i * n:(i + 1) * n], lay), 1.0)
-               for i in range(slots)]
+        s0, d0 = src.data_ptr(), dst.data_ptr()
+        res = {}
+        for shape_name in COPY_SHAPES:
+            shape = eh.CopyShape[shape_name]
 
-        def launch(i, evs=evs):
-            st = suite.kernel.process_event(evs[i % len(evs)])
-            if st != eh.Status.OK:
-                raise RuntimeError(f"copy: {st.name}: {eh.last_error()}")
+            def launch(i, shape=shape):
+                k = i % slots
+                st = eh.stream_copy(s0 + 4 * n * k, d0 + 4 * n * k, 4 * n, shape, sid)
+                if st != eh.Status.OK:
+                    raise RuntimeError(f"copy {shape.name}: {st.name}: {eh.last_error()}")
 
-        for i in range(2):
-            launch(i)
-        reps = max(steps, 20, slots)
-        g = capture(lambda reps=reps: [launch(i) for i in range(reps)])
-        g.replay()
-        out[nbytes] = timed(lambda i: g.replay(), 3) / (3 * reps) * (nbytes / (8.0 * n))
-        del g, evs, src, dst
+            for i in range(2):
+                launch(i)
+            reps = max(steps, 20, slots)
+            g = capture(lambda reps=reps, launch=launch: [launch(i) for i in range(reps)])
+            warm(g)
+            res[shape_name] = timed(lambda i: g.replay(), 3) / (3 * reps) * (nbytes / (8.0 * n))
+            del g
+        out[nbytes] = res
+        del src, dst
     return out
 
 
@@ -512,88 +523,90 @@ def sampler_ops(suite, stream, reps):
     return res
 
 
-def cpu_baseline(host, budget_s=20.0):
-    """Single-threaded oracle on a bounded sample of each op's workload:
-    the same code path the reference's CPU kernels take (view decode,
-    glibc libm), timed with a monotonic clock, median of 3 runs per op."""
+def cpu_baseline(host, runs=5, op_budget_s=30.0):
+    """The C oracle (a single-threaded restatement of the reference's CPU
+    path: view decode, glibc libm) on the exact config tensors, the same
+    host bytes bench uploads: per op one warm-up run, then `runs` timed runs
+    (the reference's own policy, snapshots/bench/kernel-elementwise-aarch64.txt:8),
+    median, monotonic clock.  An op whose runs pass op_budget_s stops early
+    and reports how many it took.  Returns (GB/s over all ops, per op,
+    sampler)."""
     import oracle as orc
 
     def v(a, ne, nb=None, dtype=None):
         return orc.view(a, ne, nb, dtype)
 
-    rows_frac = 8  # each op runs on 1/8 of its rows (or heads)
-    samples = {}
-    c1 = host["c1_src0"][: 4096 * 64]
-    samples["add_broadcast_row"] = (lambda o=np.zeros(4096 * 64, np.float32): orc.broadcast_row(
-        orc.ADD, v(c1, [4096, 64, 1, 1]), v(host["c1_src1"], [4096, 1, 1, 1]), v(o, [4096, 64, 1, 1])),
-        (8388608 + 16384 + 8388608) / rows_frac)
-    g = host["c2_gate"][: 11008 * 64]
-    u = host["c2_up"][: 11008 * 64]
-    samples["silu"] = (lambda o=np.zeros_like(g): orc.unary_event(10, v(g, [11008, 64, 1, 1]), v(o, [11008, 64, 1, 1])),
-                       2 * 22544384 / rows_frac)
-    samples["mul"] = (lambda o=np.zeros_like(g): orc.binary(orc.MUL, v(g, [11008, 64, 1, 1]), v(u, [11008, 64, 1, 1]),
-                                                            v(o, [11008, 64, 1, 1])), 3 * 22544384 / rows_frac)
-    samples["swiglu"] = (lambda o=np.zeros_like(g): orc.swiglu(v(g, [11008, 64, 1, 1]), v(u, [11008, 64, 1, 1]),
-                                                               v(o, [11008, 64, 1, 1])), 3 * 22544384 / rows_frac)
-    samples["gelu"] = (lambda o=np.zeros_like(g): orc.unary_event(8, v(g, [11008, 64, 1, 1]), v(o, [11008, 64, 1, 1])),
-                       2 * 22544384 / rows_frac)
-    x3 = host["c3_x"][: 4096 * 256]
-    samples["rms_norm"] = (lambda o=np.zeros_like(x3): orc.rms_norm(v(x3, [4096, 256, 1, 1]), v(o, [4096, 256, 1, 1]), 1e-5),
-                           2 * 33554432 / rows_frac)
-    samples["rms_norm_mul"] = (lambda o=np.zeros_like(x3): orc.rms_norm_mul(
-        v(x3, [4096, 256, 1, 1]), v(host["c3_w"], [4096, 1, 1, 1]), v(o, [4096, 256, 1, 1]), 1e-5),
-        (2 * 33554432 + 16384) / rows_frac)
-    x4 = host["c4_x"][: 4096 * 512 * 4]
+    n2 = 11008 * 512
+    g, u = host["c2_gate"], host["c2_up"]
+    x3, x4, x5 = host["c3_x"], host["c4_x"], host["c5_logits"]
     scale = float(np.float32(1.0 / np.sqrt(128.0)))
-    samples["soft_max_ext"] = (lambda o=np.zeros_like(x4): orc.soft_max_ext(
-        v(x4, [4096, 512, 4, 1]), v(host["c4_mask"], [4096, 512, 1, 1], None, orc.F16), scale, v(o, [4096, 512, 4, 1])),
-        2 * 268435456 / rows_frac + 4194304)
-    x5 = host["c5_logits"][: 151936 * 8]
-    samples["argmax_rows"] = (lambda o=np.zeros(8, np.int32): orc.argmax_rows(v(x5, [151936, 8, 1, 1]), v(o, [1, 8, 1, 1])),
-                              (38895616 + 256) / rows_frac)
-    samples["sum_rows"] = (lambda o=np.zeros(8, np.float32): orc.sum_rows(v(x5, [151936, 8, 1, 1]), v(o, [1, 8, 1, 1])),
-                           (38895616 + 256) / rows_frac)
-    s5 = host["c5b_src0"]
     snb = dense_nb([128, 32, 64, 8])
     vnb = [snb[0], snb[2], snb[1], snb[3]]
-    samples["mul_broadcast_4d"] = (lambda o=np.zeros(128 * 64 * 32 * 1, np.float32): orc.binary_bcast(
-        orc.MUL, v(s5, [128, 64, 32, 1], vnb), v(host["c5b_src1"], [128, 1, 32, 1]), v(o, [128, 64, 32, 1])),
-        (8388608 + 16384 + 8388608) / rows_frac)
+    outs = {"c1": np.zeros(4096 * 512, np.float32), "c2": np.zeros(n2, np.float32),
+            "c3": np.zeros(4096 * 2048, np.float32), "c4": np.zeros(4096 * 512 * 32, np.float32),
+            "c5i": np.zeros(64, np.int32), "c5f": np.zeros(64, np.float32), "c5b": np.zeros(128 * 64 * 32 * 8, np.float32)}
+    calls = {
+        "add_broadcast_row": lambda: orc.broadcast_row(orc.ADD, v(host["c1_src0"], [4096, 512, 1, 1]),
+                                                       v(host["c1_src1"], [4096, 1, 1, 1]), v(outs["c1"], [4096, 512, 1, 1])),
+        "silu": lambda: orc.unary_event(10, v(g, [11008, 512, 1, 1]), v(outs["c2"], [11008, 512, 1, 1])),
+        "mul": lambda: orc.binary(orc.MUL, v(g, [11008, 512, 1, 1]), v(u, [11008, 512, 1, 1]),
+                                  v(outs["c2"], [11008, 512, 1, 1])),
+        "swiglu": lambda: orc.swiglu(v(g, [11008, 512, 1, 1]), v(u, [11008, 512, 1, 1]), v(outs["c2"], [11008, 512, 1, 1])),
+        "gelu": lambda: orc.unary_event(8, v(g, [11008, 512, 1, 1]), v(outs["c2"], [11008, 512, 1, 1])),
+        "rms_norm": lambda: orc.rms_norm(v(x3, [4096, 2048, 1, 1]), v(outs["c3"], [4096, 2048, 1, 1]), 1e-5),
+        "rms_norm_mul": lambda: orc.rms_norm_mul(v(x3, [4096, 2048, 1, 1]), v(host["c3_w"], [4096, 1, 1, 1]),
+                                                 v(outs["c3"], [4096, 2048, 1, 1]), 1e-5),
+        "soft_max_ext": lambda: orc.soft_max_ext(v(x4, [4096, 512, 32, 1]),
+                                                 v(host["c4_mask"], [4096, 512, 1, 1], None, orc.F16), scale,
+                                                 v(outs["c4"], [4096, 512, 32, 1])),
+        "argmax_rows": lambda: orc.argmax_rows(v(x5, [151936, 64, 1, 1]), v(outs["c5i"], [1, 64, 1, 1])),
+        "sum_rows": lambda: orc.sum_rows(v(x5, [151936, 64, 1, 1]), v(outs["c5f"], [1, 64, 1, 1])),
+        "mul_broadcast_4d": lambda: orc.binary_bcast(orc.MUL, v(host["c5b_src0"], [128, 64, 32, 8], vnb),
+                                                     v(host["c5b_src1"], [128, 1, 32, 1]), v(outs["c5b"], [128, 64, 32, 8])),
+    }
+    alg = dict((n, b) for n, _, b in OPS)
+
+    def median_time(fn, what):
+        st = fn()  # warm-up
+        if st != orc.OK:
+            raise RuntimeError(f"oracle {what} failed: {st}")
+        times = []
+        t_op = time.monotonic()
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+            if time.monotonic() - t_op > op_budget_s:
+                break
+        return float(np.median(times)), len(times)
+
     per_op = {}
     total_bytes = 0.0
     total_s = 0.0
-    t_start = time.monotonic()
-    for name, (fn, nbytes) in samples.items():
-        times = []
-        for _ in range(3):
-            t0 = time.perf_counter()
-            st = fn()
-            times.append(time.perf_counter() - t0)
-            if st != orc.OK:
-                raise RuntimeError(f"oracle {name} failed: {st}")
-            if time.monotonic() - t_start > budget_s:
-                break
-        t = float(np.median(times))
-        per_op[name] = {"GB/s": nbytes / t / 1e9, "ms": t * 1e3}
-        total_bytes += nbytes
+    for name, fn in calls.items():
+        t, n = median_time(fn, name)
+        per_op[name] = {"GB/s": alg[name] / t / 1e9, "ns_per_op": t * 1e9, "runs": n}
+        total_bytes += alg[name]
         total_s += t
-    # the emel-logits sampler (not a step op): the oracle on 2 rows of the
-    # bench's sampler workload, per SAMPLER_CASES entry
+    # the emel-logits sampler (not a step op): the oracle over the bench's
+    # whole sampler workload (SAMPLER_ROWS rows), per SAMPLER_CASES entry
     sampler = {}
-    sg = rng(31)
-    rows = sg.standard_normal((2, SAMPLER_VOCAB), dtype=np.float64).astype(np.float32)
+    rows = rng(31).standard_normal((SAMPLER_ROWS, SAMPLER_VOCAB), dtype=np.float64).astype(np.float32)
     for temperature, top_k in SAMPLER_CASES:
-        t0 = time.perf_counter()
-        for r in range(2):
-            st = orc.sample_temperature_top_k(SAMPLER_VOCAB, temperature, top_k, rows[r].copy(),
-                                              np.zeros(SAMPLER_VOCAB, np.int32), np.zeros(top_k, np.float32),
-                                              np.zeros(top_k, np.int32), np.array([7], np.uint32),
-                                              np.zeros(1, np.int32), np.zeros(1, np.float32))
-            if st != orc.OK:
-                raise RuntimeError(f"oracle sampler failed: {st}")
-        t = (time.perf_counter() - t0) / 2
-        sampler[f"sample_t{temperature}_k{top_k}"] = {"rows_per_s": round(1.0 / t, 2),
-                                                      "GB/s": 2 * SAMPLER_VOCAB * 4 / t / 1e9}
+        def batch(temperature=temperature, top_k=top_k):
+            for r in range(SAMPLER_ROWS):
+                st = orc.sample_temperature_top_k(SAMPLER_VOCAB, temperature, top_k, rows[r].copy(),
+                                                  np.zeros(SAMPLER_VOCAB, np.int32), np.zeros(top_k, np.float32),
+                                                  np.zeros(top_k, np.int32), np.array([7], np.uint32),
+                                                  np.zeros(1, np.int32), np.zeros(1, np.float32))
+                if st != orc.OK:
+                    return st
+            return orc.OK
+
+        t, n = median_time(batch, "sampler")
+        sampler[f"sample_t{temperature}_k{top_k}"] = {"rows_per_s": round(SAMPLER_ROWS / t, 2),
+                                                      "GB/s": 2 * SAMPLER_ROWS * SAMPLER_VOCAB * 4 / t / 1e9,
+                                                      "ns_per_op": t * 1e9, "runs": n}
     return total_bytes / total_s / 1e9, per_op, sampler
 
 
@@ -710,6 +723,12 @@ def main():
             stream.synchronize()
             return g
 
+        def warm(g):
+            """Replays g for at least WARM_MS (and at least once)."""
+            once = timed(lambda i: g.replay(), 1)
+            for _ in range(int(WARM_MS / max(once, 1e-3))):
+                g.replay()
+
         def two_steps():
             for c in range(2):
                 for n in names:
@@ -742,21 +761,27 @@ def main():
         step_ms = timed(lambda i: step_graph.replay(), pairs) / (2 * pairs)
 
         # per op: a graph of back-to-back launches cycling through all of
-        # the op's buffer sets (>= ROTATE_BYTES), so each launch is cold
+        # the op's buffer sets (>= ROTATE_BYTES), so each launch is cold.
+        # The graph runs for WARM_MS before it is timed: an op timed right
+        # after soft_max_ext's 541 MB launches ran ~1 us per launch slower for
+        # about a millisecond (argmax_rows 11.2 against 9.9 us, sum_rows 10.0
+        # against 9.1 us on one box), so each op is timed in its own steady
+        # state.
         per_ms = {}
         for n in names + extra:
             reps = max(args.steps, 20, suite.copies[n])
             g = capture(lambda n=n, reps=reps: [suite.launch(n, i) for i in range(reps)])
-            g.replay()
+            warm(g)
             per_ms[n] = timed(lambda i: g.replay(), 3) / (3 * reps)
 
-        # same-size copy: scale by 1.0 over a dense f32 buffer moving the op's
-        # algorithmic bytes, launched and rotated the same way; what a plain
-        # stream achieves at that size (launch ramp and tail included)
+        # same-size copy: a bit copy moving the op's algorithmic bytes with
+        # each streaming shape, launched and rotated the same way; the fastest
+        # is what a plain stream achieves at that size (launch ramp and tail
+        # included)
         copy_ms = {}
         if not args.no_copy:
             copy_ms = copy_ceilings(suite, [info[n][1] for n in names + extra if n != "copy"], args.steps, capture,
-                                    timed)
+                                    timed, warm)
         floor_us = launch_floor(suite, capture, timed)
 
     traffic = {}
@@ -774,8 +799,12 @@ def main():
         e = {"config": cfg, "alg_bytes": nbytes, "us": round(us, 3), "GB/s": round(gbs, 1),
              "frac_of_peak": round(gbs / PEAK_GBS, 4)}
         if nbytes in copy_ms:
-            cus = copy_ms[nbytes] * 1e3
+            shapes = copy_ms[nbytes]
+            best = min(shapes, key=shapes.get)
+            cus = shapes[best] * 1e3
             e["copy_us"] = round(cus, 3)
+            e["copy_shape"] = best
+            e["copy_us_by_shape"] = {k: round(v * 1e3, 3) for k, v in shapes.items()}
             e["frac_of_copy"] = round(cus / us, 4)
         t = traffic.get(n)
         if isinstance(t, dict) and "hbm_bytes_per_launch" in t:
@@ -817,10 +846,15 @@ def main():
         cpu_gbs, cpu_ops, cpu_sampler = cpu_baseline(host)
         facts = host_facts()
         cpu = {"value": round(cpu_gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-               "sample": "C oracle (single-threaded restatement of the reference CPU path) on 1/8 of every "
-                         "op's rows/heads, median of 3, algorithmic bytes / time; sampler: 2 rows of its workload",
-               "host": facts, "per_op": {k: round(v["GB/s"], 3) for k, v in cpu_ops.items()},
-               "sampler": {k: {"rows_per_s": v["rows_per_s"], "GB/s": round(v["GB/s"], 4)}
+               "sample": "C oracle (single-threaded restatement of the reference CPU path) on the exact config "
+                         "tensors bench uploads: one warm-up run, then the median of 5 runs per op (fewer if an "
+                         "op's runs pass 30 s; 'runs' says how many); value = all ops' algorithmic bytes / the sum "
+                         "of their median times; sampler: all 64 rows of its workload",
+               "host": facts,
+               "per_op": {k: {"GB/s": round(v["GB/s"], 3), "ns_per_op": round(v["ns_per_op"]), "runs": v["runs"]}
+                          for k, v in cpu_ops.items()},
+               "sampler": {k: {"rows_per_s": v["rows_per_s"], "GB/s": round(v["GB/s"], 4),
+                               "ns_per_op": round(v["ns_per_op"]), "runs": v["runs"]}
                            for k, v in cpu_sampler.items()}}
 
     out = {
@@ -840,7 +874,7 @@ def main():
                    "launch": "one captured HIP graph of two steps replayed K/2 times (replays checked bit-exact "
                              "against eager launches); eager_ms_per_step: the same steps launched from Python",
                    "eager_ms_per_step": round(eager_step_ms, 4),
-                   "buffer_policy": "step: >=1 GB of other ops moves between two launches of one op; per op: "
+                   "buffer_policy": "step: >=1 GB of other ops moves between two launches of one op; per op (after 3 ms of warm-up replays): "
                                     "back-to-back launches cycle through >=1 GiB of distinct buffer sets "
                                     "(Infinity Cache is 256 MB)",
                    "wall_s": round(wall, 3),

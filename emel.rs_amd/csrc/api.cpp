@@ -696,6 +696,18 @@ emel_status emel_release_workspaces(void)
     return e == hipSuccess ? EMEL_OK : hip_fail(e, "hipDeviceSynchronize");
 }
 
+emel_status emel_stream_copy(const void *src, void *dst, uint64_t bytes, uint32_t shape, emel_stream stream)
+{
+    if (bytes % 16 != 0 || (reinterpret_cast<uintptr_t>(src) & 15u) != 0 || (reinterpret_cast<uintptr_t>(dst) & 15u) != 0)
+        return fail(EMEL_ERR_INVALID_ARGUMENT, "stream copy: bytes and both pointers must be multiples of 16");
+    if (bytes != 0 && (!src || !dst)) return fail(EMEL_ERR_INVALID_ARGUMENT, "stream copy: null pointer");
+    if (shape > EMEL_COPY_WALK) return fail(EMEL_ERR_INVALID_ARGUMENT, "stream copy: unknown shape");
+    const emel_status d = ensure_device();
+    if (d != EMEL_OK) return d;
+    const hipError_t e = emel::launch_stream_copy(src, dst, bytes, static_cast<emel::CopyShape>(shape), as_stream(stream));
+    return e == hipSuccess ? EMEL_OK : hip_fail(e, "stream copy launch");
+}
+
 emel_status emel_validate_view(const emel_tensor_view *view, int32_t allow_singleton_zero_stride)
 {
     if (!view) return fail(EMEL_ERR_INVALID_ARGUMENT, "null view");

@@ -23,6 +23,7 @@
 #include <cstdlib>
 #include <map>
 #include <mutex>
+#include <type_traits>
 
 #include "common.hpp"
 #include "launch.hpp"
@@ -742,6 +743,40 @@ __global__ __launch_bounds__(kBlock) void k_acc(const float *base, const float *
     }
 }
 } // namespace
+
+hipError_t launch_stream_copy(const void *src, void *dst, uint64_t bytes, CopyShape shape, hipStream_t stream)
+{
+    if (bytes == 0) return hipSuccess;
+    const float *a = static_cast<const float *>(src);
+    float *o = static_cast<float *>(dst);
+    const uint64_t nvec = bytes / 16;
+    const uint64_t n = bytes / 4;
+    auto dense = [&](auto vpt_tag) {
+        constexpr int vpt = decltype(vpt_tag)::value;
+        const uint64_t blocks = (nvec + kBlock * vpt - 1) / (kBlock * vpt);
+        if (blocks > 0x7fffffffull) return hipErrorInvalidConfiguration;
+        k_dense<Ew::Copy, vpt><<<dim3(static_cast<uint32_t>(blocks)), kBlock, 0, stream>>>(a, nullptr, o, nvec, n,
+                                                                                            Scal{0.0f, 0.0f});
+        return hipGetLastError();
+    };
+    switch (shape) {
+    case CopyShape::Flat: return dense(std::integral_constant<int, 1>{});
+    case CopyShape::Wave4: return dense(std::integral_constant<int, 4>{});
+    case CopyShape::Wave8: return dense(std::integral_constant<int, 8>{});
+    case CopyShape::Walk: {
+        DeviceInfo dev{};
+        const hipError_t e = device_info(stream, false, dev);
+        if (e != hipSuccess) return e;
+        uint64_t blocks = (nvec + kBlock - 1) / kBlock;
+        const uint64_t resident = static_cast<uint64_t>(dev.cus) * kResidentPerCu;
+        if (blocks > resident) blocks = resident;
+        k_dense_walk<Ew::Copy><<<dim3(static_cast<uint32_t>(blocks)), kBlock, 0, stream>>>(a, o, nvec, n,
+                                                                                          Scal{0.0f, 0.0f});
+        return hipGetLastError();
+    }
+    }
+    return hipErrorInvalidValue;
+}
 
 hipError_t launch_acc(const float *base, const float *update, float *dst, uint64_t count, uint64_t offset,
                       uint64_t n_update, hipStream_t stream)

@@ -66,6 +66,15 @@ hipError_t launch_elementwise(const EwArgs &args, hipStream_t stream);
 hipError_t launch_acc(const float *base, const float *update, float *dst, uint64_t count, uint64_t offset,
                       uint64_t n_update, hipStream_t stream);
 
+// Bit copy of `bytes` (a multiple of 16; both pointers 16-byte aligned) with
+// one of the streaming shapes of the dense kernels, for measuring what a
+// plain stream achieves: 0 one float4 per thread, 1 and 2 four and eight
+// float4 per lane (each wave over 256 / 512 consecutive float4), 3 one
+// resident generation walking the array grid-stride with the next float4
+// in flight.
+enum class CopyShape : uint32_t { Flat = 0, Wave4 = 1, Wave8 = 2, Walk = 3 };
+hipError_t launch_stream_copy(const void *src, void *dst, uint64_t bytes, CopyShape shape, hipStream_t stream);
+
 // ---- row kernels (rows.hip) --------------------------------------------
 
 enum class RowOp : uint32_t { RmsNorm = 0, RmsNormMul = 1, Norm = 2, SoftMax = 3, SoftMaxExt = 4 };

@@ -337,6 +337,7 @@ SIGNATURES = {
     "emel_stream_destroy": [_S],
     "emel_stream_synchronize": [_S],
     "emel_release_workspaces": [],
+    "emel_stream_copy": [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32, _S],
     "emel_generic_dispatch": [ctypes.POINTER(CGenericRequest), _S],
     **{f"emel_op_get_rows{suffix}": [_V, ctypes.POINTER(CIndexView), _V, _S]
        for suffix in ("", "_f32_bytes", "_f16", "_bf16", "_q4_0", "_q8_0", "_q4_k")},
@@ -393,3 +394,18 @@ def device_count() -> int:
     n = ctypes.c_int32(0)
     load().emel_device_count(ctypes.byref(n))
     return int(n.value)
+
+
+class CopyShape(enum.IntEnum):
+    """emel_copy_shape: the streaming shapes emel_stream_copy measures."""
+    FLAT = 0
+    WAVE4 = 1
+    WAVE8 = 2
+    WALK = 3
+
+
+def stream_copy(src_ptr: int, dst_ptr: int, nbytes: int, shape: "CopyShape", stream: int = 0) -> Status:
+    """emel_stream_copy: a bit copy of nbytes device bytes with one streaming
+    shape (a measurement reference; asynchronous on `stream`)."""
+    return Status(load().emel_stream_copy(ctypes.c_void_p(src_ptr), ctypes.c_void_p(dst_ptr), nbytes, int(shape),
+                                          ctypes.c_void_p(stream)))

@@ -249,6 +249,26 @@ impl<T: Copy> DeviceBuffer<T> {
     pub const fn as_mut_ptr(&mut self) -> *mut T {
         self.ptr
     }
+
+    /// Enqueues a bit copy of `src` into the start of this buffer with one
+    /// streaming shape (`ffi::EMEL_COPY_*`): a measurement reference for
+    /// what a plain stream achieves at this size.
+    ///
+    /// # Errors
+    /// `EMEL_ERR_INVALID_ARGUMENT` when `src` is longer than the buffer, the
+    /// byte count is not a multiple of 16 or the shape is unknown, else the
+    /// library status of the launch.
+    pub fn stream_copy_from(&mut self, src: &Self, shape: u32, stream: &Stream) -> Result<(), HipError> {
+        if src.len > self.len {
+            return Err(HipError(ffi::EMEL_ERR_INVALID_ARGUMENT));
+        }
+        // SAFETY: both device ranges hold src.byte_len() bytes and stay
+        // allocated while `self` and `src` are borrowed; the library checks
+        // alignment and the shape.
+        HipError::check(unsafe {
+            ffi::emel_stream_copy(src.ptr.cast(), self.ptr.cast(), src.byte_len() as u64, shape, stream.as_raw())
+        })
+    }
 }
 
 impl<T: Copy> Drop for DeviceBuffer<T> {

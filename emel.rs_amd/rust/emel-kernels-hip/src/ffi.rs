@@ -18,6 +18,12 @@ pub const EMEL_HIP_ABI_VERSION: u32 = 2;
 /// passed inline in the kernel arguments.
 pub const EMEL_GET_ROWS_INLINE_INDICES: u32 = 512;
 
+// ---- emel_copy_shape (emel_stream_copy, a measurement reference) ----
+pub const EMEL_COPY_FLAT: u32 = 0;
+pub const EMEL_COPY_WAVE4: u32 = 1;
+pub const EMEL_COPY_WAVE8: u32 = 2;
+pub const EMEL_COPY_WALK: u32 = 3;
+
 /// `emel_status`.
 pub type Status = i32;
 /// `emel_stream`: a `hipStream_t`; null is the default stream.
@@ -295,6 +301,7 @@ unsafe extern "C" {
     pub fn emel_stream_destroy(stream: Stream) -> Status;
     pub fn emel_stream_synchronize(stream: Stream) -> Status;
     pub fn emel_release_workspaces() -> Status;
+    pub fn emel_stream_copy(src: *const c_void, dst: *mut c_void, bytes: u64, shape: u32, stream: Stream) -> Status;
     pub fn emel_validate_view(view: *const EmelTensorView, allow_singleton_zero_stride: i32) -> Status;
     pub fn emel_validate_normalization_view(view: *const EmelTensorView) -> Status;
     pub fn emel_op_add(lhs: *const EmelTensorView, rhs: *const EmelTensorView, out: *const EmelTensorViewMut, stream: Stream) -> Status;

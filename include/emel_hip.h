@@ -170,6 +170,19 @@ emel_status emel_stream_synchronize(emel_stream stream);
 /* Releases the per-stream reduction workspaces the library holds. */
 emel_status emel_release_workspaces(void);
 
+/* Measurement reference, no counterpart in the reference: a bit copy of
+ * `bytes` device bytes (a multiple of 16, both pointers 16-byte aligned)
+ * with one of the streaming shapes the dense kernels use, so a caller can
+ * time what a plain stream achieves at a given size.  Asynchronous on
+ * `stream`. */
+typedef enum emel_copy_shape {
+    EMEL_COPY_FLAT = 0,  /* one float4 per thread */
+    EMEL_COPY_WAVE4 = 1, /* four float4 per lane, each wave over 256 consecutive float4 */
+    EMEL_COPY_WAVE8 = 2, /* eight float4 per lane, each wave over 512 consecutive float4 */
+    EMEL_COPY_WALK = 3   /* one resident generation, grid-stride, next float4 in flight */
+} emel_copy_shape;
+emel_status emel_stream_copy(const void *src, void *dst, uint64_t bytes, uint32_t shape, emel_stream stream);
+
 /* ---- view predicates (host only, no device access) -------------------- */
 
 /* Layout::validate / validate_binary (tensor_view.rs:365-447):
