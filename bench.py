@@ -128,6 +128,8 @@ EXTRA_OPS = [
     ("soft_max_dense", "OpSoftMax [4096,512], dense: f64 row sum (reductions.rs:565-601)", 2 * 8388608),
     ("soft_max_strided", "OpSoftMax [4096,512], rows 4 floats apart: exact sequential f32 row sum "
                          "(reductions.rs:603-638)", 2 * 8388608),
+    ("generic_rms_norm", "config 3 through the generic envelope (GenericEvent RMS_NORM, generic.rs:1988-2055): "
+                         "rms_norm [4096,2048] eps=1e-5, f64 scale", 2 * 33554432),
 ]
 DOMINANT = "soft_max_ext"
 COPY_BYTES = 2 * 268435456  # the calibration copy: 256 MiB read + 256 MiB written
@@ -215,6 +217,10 @@ class GpuSuite:
                                                            M(o, [4096, 512, 1, 1]))),
             "glu_swiglu": ([np.concatenate([host["c2_up"], host["c2_gate"]])], (n2, torch.float32),
                            lambda i, o: eh.OpGlu(i[0], o, eh.GluSubOp.SWIGLU)),
+            "generic_rms_norm": ([host["c3_x"]], (4096 * 2048, torch.float32),
+                                 lambda i, o: eh.GenericEvent(eh.GenericRequest(
+                                     eh.GenericOp.RMS_NORM, V(i[0], [4096, 2048, 1, 1]), None, None,
+                                     M(o, [4096, 2048, 1, 1]), eh.OpParams(np.float32(1e-5).tobytes(), 4)))),
             "copy": ([np.zeros(COPY_BYTES // 8, np.float32)], (COPY_BYTES // 8, torch.float32),
                      lambda i, o: eh.OpScale(V(i[0], [COPY_BYTES // 8, 1, 1, 1]), M(o, [COPY_BYTES // 8, 1, 1, 1]),
                                              1.0)),

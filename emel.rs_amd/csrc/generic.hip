@@ -3,12 +3,19 @@
 // (crates/emel-kernels/src/any/generic.rs:1264-2055).
 //
 // Every route here is a sequential loop in the reference whose rounding
-// depends on the order of its additions, so each kernel gives one lane the
-// reference's whole loop for its unit of independent work, in the
-// reference's order:
-//   k_gen_rows      one lane per row: cumsum, norm and rms_norm (f64 sums,
-//                   f64 scale), soft_max_back, rms_norm_back (soft_max uses
-//                   the typed strided path's exact sequential-sum kernel);
+// depends on the order of its additions, so each kernel but k_gen_norm
+// gives one lane the reference's whole loop for its unit of independent
+// work, in the reference's order:
+//   k_gen_rows      one lane per row: cumsum, soft_max_back, rms_norm_back,
+//                   and norm / rms_norm rows narrower than a wave (soft_max
+//                   uses the typed strided path's exact sequential-sum
+//                   kernel);
+//   k_gen_norm      a workgroup per row for norm and rms_norm rows of 64 or
+//                   more columns that the typed row kernels cannot take
+//                   (those run vectorisable rows with the generic arithmetic);
+//                   both sum in f64 as a fixed-order tree: within rms_norm's
+//                   1e-5 tolerance, the one route here not in the
+//                   reference's order;
 //   k_gen_ord       one lane per destination element: fill, arange, diag,
 //                   diag_mask_inf/zero, concat, repeat_back (the source
 //                   elements of one target summed in source-ordinal order);
@@ -446,6 +453,111 @@ constexpr uint32_t kMmArgmaxBlocks = 2048;
 
 } // namespace
 
+// ---- norm and rms_norm: a workgroup per row ------------------------------------------
+// generic.rs:1988-2055: per row of width = src0.ne[0] ordinals, s = sum of
+// f64(v*v) (rms) or f64(v) (norm), mean = f32(s / width); norm adds the f64
+// sum of f32(centered^2) divided by width; scale = f32(1 / sqrt(base + eps))
+// in f64; y = v * scale or (v - mean) * scale in f32.  The f64 sums run as a
+// fixed-order tree over the row's threads (parity within the 1e-5 relative
+// tolerance of rms_norm, not bit for bit against the reference's sequential
+// order); every f32 step is the reference's.  A generic row is one dim-0
+// row of src0, so its elements sit at a row base plus column * st[0]; dst
+// rows are addressed the same way when dst.ne[0] == width, else each
+// element's ordinal is decoded through dst's own extents.
+template <int BS>
+__device__ __forceinline__ double block_sum_f64(double v, double *lds)
+{
+    v = wave_sum_dpp(v);
+    if constexpr (BS == kWave) {
+        return v;
+    } else {
+        const uint32_t w = threadIdx.x / kWave;
+        __syncthreads(); // lds is reused by the next reduction
+        if (threadIdx.x % kWave == 0) lds[w] = v;
+        __syncthreads();
+        double t = lds[0];
+#pragma unroll
+        for (int i = 1; i < BS / kWave; ++i) t += lds[i];
+        return t;
+    }
+}
+
+template <bool RMS, int BS>
+__global__ __launch_bounds__(BS) void k_gen_norm(GenRowArgs a, bool dst_rows)
+{
+    __shared__ double lds[BS / kWave];
+    const uint64_t r = blockIdx.x;
+    const uint64_t w = a.width;
+    const float *x = static_cast<const float *>(a.x.data);
+    float *y = static_cast<float *>(a.y.data);
+    Walk xr, yr;
+    xr.init(a.x, r * w); // column 0 of the row
+    const int64_t sx = a.x.st[0];
+    if (dst_rows) yr.init(a.y, r * w);
+    double sum = 0.0;
+    for (uint64_t c = threadIdx.x; c < w; c += BS) {
+        const float v = x[xr.off + static_cast<int64_t>(c) * sx];
+        sum += RMS ? static_cast<double>(v * v) : static_cast<double>(v);
+    }
+    sum = block_sum_f64<BS>(sum, lds);
+    const float mean = static_cast<float>(sum / static_cast<double>(w));
+    double base = static_cast<double>(mean);
+    if constexpr (!RMS) {
+        double var = 0.0;
+        for (uint64_t c = threadIdx.x; c < w; c += BS) {
+            const float centered = x[xr.off + static_cast<int64_t>(c) * sx] - mean;
+            var += static_cast<double>(centered * centered);
+        }
+        var = block_sum_f64<BS>(var, lds);
+        base = var / static_cast<double>(w);
+    }
+    const float scale = static_cast<float>(1.0 / __builtin_sqrt(base + static_cast<double>(a.eps)));
+    for (uint64_t c = threadIdx.x; c < w; c += BS) {
+        const float v = x[xr.off + static_cast<int64_t>(c) * sx];
+        const float o = RMS ? v * scale : (v - mean) * scale;
+        int64_t yo;
+        if (dst_rows) {
+            yo = yr.off + static_cast<int64_t>(c) * a.y.st[0];
+        } else {
+            Walk e;
+            e.init(a.y, r * w + c);
+            yo = e.off;
+        }
+        y[yo] = o;
+    }
+}
+
+Operand as_operand(const GView &v)
+{
+    return Operand{v.data, {v.ne[0], v.ne[1], v.ne[2], v.ne[3]}, {v.st[0], v.st[1], v.st[2], v.st[3]}};
+}
+
+// Vectorisable rows (dim 0 contiguous, 16-byte aligned, same shapes) run on
+// the typed row kernels with the generic arithmetic (RowOp::GenRmsNorm /
+// GenNorm: rows in registers, 128-bit accesses); other layouts on
+// k_gen_norm.
+template <bool RMS>
+hipError_t launch_gen_norm(const GenRowArgs &a, hipStream_t s)
+{
+    RowArgs ra{};
+    ra.op = RMS ? RowOp::GenRmsNorm : RowOp::GenNorm;
+    ra.x = as_operand(a.x);
+    ra.y = as_operand(a.y);
+    ra.eps = a.eps;
+    const hipError_t e = launch_rows(ra, s);
+    if (e != hipErrorNotSupported) return e;
+    if (a.rows > 0x7fffffffull) return hipErrorInvalidConfiguration;
+    const bool dst_rows = a.y.ne[0] == a.width;
+    const dim3 grid(static_cast<uint32_t>(a.rows));
+    if (a.width <= 1024) k_gen_norm<RMS, kWave><<<grid, kWave, 0, s>>>(a, dst_rows);
+    else k_gen_norm<RMS, kBlock><<<grid, kBlock, 0, s>>>(a, dst_rows);
+    return hipGetLastError();
+}
+
+// Rows narrower than a wave keep one lane per row (and the reference's
+// sequential order).
+constexpr uint64_t kNormRowMin = kWave;
+
 hipError_t launch_generic_rows(const GenRowArgs &a, hipStream_t s)
 {
     if (a.rows == 0) return hipSuccess;
@@ -455,12 +567,16 @@ hipError_t launch_generic_rows(const GenRowArgs &a, hipStream_t s)
     switch (a.op) {
     case GenRow::Cumsum: k_gen_rows<GenRow::Cumsum><<<grid, kRowBlock, 0, s>>>(a); break;
     case GenRow::SoftMax: { // generic.rs:1948-1986: the exact sequential-sum kernel of the typed strided path
-        const Operand x{a.x.data, {a.x.ne[0], a.x.ne[1], a.x.ne[2], a.x.ne[3]}, {a.x.st[0], a.x.st[1], a.x.st[2], a.x.st[3]}};
-        const Operand y{a.y.data, {a.y.ne[0], a.y.ne[1], a.y.ne[2], a.y.ne[3]}, {a.y.st[0], a.y.st[1], a.y.st[2], a.y.st[3]}};
-        return launch_softmax_seq(x, y, s);
+        return launch_softmax_seq(as_operand(a.x), as_operand(a.y), s);
     }
-    case GenRow::Norm: k_gen_rows<GenRow::Norm><<<grid, kRowBlock, 0, s>>>(a); break;
-    case GenRow::RmsNorm: k_gen_rows<GenRow::RmsNorm><<<grid, kRowBlock, 0, s>>>(a); break;
+    case GenRow::Norm:
+        if (a.width >= kNormRowMin) return launch_gen_norm<false>(a, s);
+        k_gen_rows<GenRow::Norm><<<grid, kRowBlock, 0, s>>>(a);
+        break;
+    case GenRow::RmsNorm:
+        if (a.width >= kNormRowMin) return launch_gen_norm<true>(a, s);
+        k_gen_rows<GenRow::RmsNorm><<<grid, kRowBlock, 0, s>>>(a);
+        break;
     case GenRow::SoftMaxBack: k_gen_rows<GenRow::SoftMaxBack><<<grid, kRowBlock, 0, s>>>(a); break;
     case GenRow::RmsNormBack: k_gen_rows<GenRow::RmsNormBack><<<grid, kRowBlock, 0, s>>>(a); break;
     default: return hipErrorInvalidValue;

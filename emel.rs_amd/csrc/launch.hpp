@@ -77,7 +77,10 @@ hipError_t launch_stream_copy(const void *src, void *dst, uint64_t bytes, CopySh
 
 // ---- row kernels (rows.hip) --------------------------------------------
 
-enum class RowOp : uint32_t { RmsNorm = 0, RmsNormMul = 1, Norm = 2, SoftMax = 3, SoftMaxExt = 4 };
+// GenRmsNorm / GenNorm: the generic envelope's arithmetic (generic.rs:1988-2055):
+// f64 scale, and for norm the f64 sum of f32 squares of the centered values.
+enum class RowOp : uint32_t { RmsNorm = 0, RmsNormMul = 1, Norm = 2, SoftMax = 3, SoftMaxExt = 4, GenRmsNorm = 5,
+                              GenNorm = 6 };
 
 struct RowArgs {
     RowOp op;

@@ -102,6 +102,47 @@ __device__ __forceinline__ float4 exp4(float4 v, const uint64_t *t, const ExpfCo
                        emel_expf_nonpos(v.w, t, c));
 }
 
+// The scale factors of the two normalisations.  Typed events
+// (normalization.rs:316-362): k = 1 / sqrtf(mean + eps) in f32, norm's
+// variance the f64 sum of f64 products of the centered values, rounded to
+// f32 before its square root.  The generic envelope (generic.rs:2030-2040):
+// k = f32(1 / sqrt(base + eps)) in f64, norm's variance the f64 sum of f32
+// squares, kept in f64.
+template <RowOp OP>
+constexpr bool kRmsOp = OP == RowOp::RmsNorm || OP == RowOp::RmsNormMul || OP == RowOp::GenRmsNorm;
+template <RowOp OP>
+constexpr bool kNormOp = OP == RowOp::Norm || OP == RowOp::GenNorm;
+
+template <RowOp OP>
+__device__ __forceinline__ float rms_scale(float mean, float eps)
+{
+    if constexpr (OP == RowOp::GenRmsNorm)
+        return static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(mean) + static_cast<double>(eps)));
+    else
+        return 1.0f / __builtin_sqrtf(mean + eps);
+}
+
+template <RowOp OP>
+__device__ __forceinline__ double centered_sq4(float4 c)
+{
+    if constexpr (OP == RowOp::GenNorm)
+        return sumsq4(c);
+    else
+        return (static_cast<double>(c.x) * c.x + static_cast<double>(c.y) * c.y) +
+               (static_cast<double>(c.z) * c.z + static_cast<double>(c.w) * c.w);
+}
+
+template <RowOp OP>
+__device__ __forceinline__ float norm_scale(double var, uint32_t ncols, float eps)
+{
+    if constexpr (OP == RowOp::GenNorm) {
+        return static_cast<float>(1.0 / __builtin_sqrt(var / static_cast<double>(ncols) + static_cast<double>(eps)));
+    } else {
+        const float variance = static_cast<float>(var / static_cast<double>(ncols));
+        return 1.0f / __builtin_sqrtf(variance + eps);
+    }
+}
+
 // ---- vectorized rows: contiguous dim 0, ncols % 4 == 0 ------------------
 // NW waves own a row: NW = 1 puts four rows in a 256-thread workgroup (rows
 // of at most 1024 columns), NW = 4 gives each row its own workgroup.  Thread
@@ -221,14 +262,14 @@ __global__ __launch_bounds__(BS) void k_row_vec(RowGeo g, const float *x, float 
 #pragma unroll
         for (int j = 0; j < NV; ++j) v[j] = in_row(j) ? load(t + kTPR * j) : make_float4(0.f, 0.f, 0.f, 0.f);
         if constexpr (kSoft && NW > 1) stage_table();
-        if constexpr (OP == RowOp::RmsNorm || OP == RowOp::RmsNormMul) {
+        if constexpr (kRmsOp<OP>) {
             double acc = 0.0;
 #pragma unroll
             for (int j = 0; j < NV; ++j)
                 if (in_row(j)) acc += sumsq4(v[j]);
             acc = row_sum<NW>(acc, lds_a);
             const float mean = static_cast<float>(acc / static_cast<double>(g.ncols));
-            const float k = 1.0f / __builtin_sqrtf(mean + eps);
+            const float k = rms_scale<OP>(mean, eps);
 #pragma unroll
             for (int j = 0; j < NV; ++j) {
                 if (in_row(j)) {
@@ -238,7 +279,7 @@ __global__ __launch_bounds__(BS) void k_row_vec(RowGeo g, const float *x, float 
                     st_nt(yr + idx, o);
                 }
             }
-        } else if constexpr (OP == RowOp::Norm) {
+        } else if constexpr (kNormOp<OP>) {
             double acc = 0.0;
 #pragma unroll
             for (int j = 0; j < NV; ++j)
@@ -247,16 +288,10 @@ __global__ __launch_bounds__(BS) void k_row_vec(RowGeo g, const float *x, float 
             const float mean = static_cast<float>(acc / static_cast<double>(g.ncols));
             double var = 0.0;
 #pragma unroll
-            for (int j = 0; j < NV; ++j) {
-                if (in_row(j)) {
-                    const float4 c = sub4(v[j], mean);
-                    var += (static_cast<double>(c.x) * c.x + static_cast<double>(c.y) * c.y) +
-                           (static_cast<double>(c.z) * c.z + static_cast<double>(c.w) * c.w);
-                }
-            }
+            for (int j = 0; j < NV; ++j)
+                if (in_row(j)) var += centered_sq4<OP>(sub4(v[j], mean));
             var = row_sum<NW>(var, lds_b);
-            const float variance = static_cast<float>(var / static_cast<double>(g.ncols));
-            const float k = 1.0f / __builtin_sqrtf(variance + eps);
+            const float k = norm_scale<OP>(var, g.ncols, eps);
 #pragma unroll
             for (int j = 0; j < NV; ++j)
                 if (in_row(j)) st_nt(yr + t + kTPR * j, mul4(sub4(v[j], mean), k));
@@ -284,31 +319,26 @@ __global__ __launch_bounds__(BS) void k_row_vec(RowGeo g, const float *x, float 
         // streamed passes for rows wider than the register budget; the
         // intermediate passes use cached accesses so re-reads hit L2
         if constexpr (kSoft && NW > 1) stage_table();
-        if constexpr (OP == RowOp::RmsNorm || OP == RowOp::RmsNormMul) {
+        if constexpr (kRmsOp<OP>) {
             double acc = 0.0;
             for (uint32_t idx = t; idx < nv; idx += kTPR) acc += sumsq4(xr[idx]);
             acc = row_sum<NW>(acc, lds_a);
             const float mean = static_cast<float>(acc / static_cast<double>(g.ncols));
-            const float k = 1.0f / __builtin_sqrtf(mean + eps);
+            const float k = rms_scale<OP>(mean, eps);
             for (uint32_t idx = t; idx < nv; idx += kTPR) {
                 float4 o = mul4(xr[idx], k);
                 if constexpr (OP == RowOp::RmsNormMul) o = mul4(o, reinterpret_cast<const float4 *>(w)[idx]);
                 st_nt(yr + idx, o);
             }
-        } else if constexpr (OP == RowOp::Norm) {
+        } else if constexpr (kNormOp<OP>) {
             double acc = 0.0;
             for (uint32_t idx = t; idx < nv; idx += kTPR) acc += sum4(xr[idx]);
             acc = row_sum<NW>(acc, lds_a);
             const float mean = static_cast<float>(acc / static_cast<double>(g.ncols));
             double var = 0.0;
-            for (uint32_t idx = t; idx < nv; idx += kTPR) {
-                const float4 c = sub4(xr[idx], mean);
-                var += (static_cast<double>(c.x) * c.x + static_cast<double>(c.y) * c.y) +
-                       (static_cast<double>(c.z) * c.z + static_cast<double>(c.w) * c.w);
-            }
+            for (uint32_t idx = t; idx < nv; idx += kTPR) var += centered_sq4<OP>(sub4(xr[idx], mean));
             var = row_sum<NW>(var, lds_b);
-            const float variance = static_cast<float>(var / static_cast<double>(g.ncols));
-            const float k = 1.0f / __builtin_sqrtf(variance + eps);
+            const float k = norm_scale<OP>(var, g.ncols, eps);
             for (uint32_t idx = t; idx < nv; idx += kTPR) st_nt(yr + idx, mul4(sub4(xr[idx], mean), k));
         } else {
             auto load_cached = [&](uint32_t idx) {
@@ -928,7 +958,7 @@ template <RowOp OP>
 void launch_vec_nv(const RowGeo &g, const RowArgs &a, const MaskGeo &mg, hipStream_t s)
 {
     const uint32_t nv = g.ncols / 4;
-    if constexpr (OP == RowOp::RmsNorm || OP == RowOp::RmsNormMul || OP == RowOp::Norm) {
+    if constexpr (kRmsOp<OP> || kNormOp<OP>) {
         if (g.rows >= 1536 && g.rows <= 4096) {
             if (nv == 8 * kWave) return launch_wave_rows<OP, 8>(g, a, s);
             if (nv == 16 * kWave) return launch_wave_rows<OP, 16>(g, a, s);
@@ -1034,9 +1064,14 @@ hipError_t launch_rows(const RowArgs &a, hipStream_t s)
         case RowOp::Norm: launch_vec_nv<RowOp::Norm>(g, a, mg, s); break;
         case RowOp::SoftMax: launch_vec_nv<RowOp::SoftMax>(g, a, mg, s); break;
         case RowOp::SoftMaxExt: launch_vec_nv<RowOp::SoftMaxExt>(g, a, mg, s); break;
+        case RowOp::GenRmsNorm: launch_vec_nv<RowOp::GenRmsNorm>(g, a, mg, s); break;
+        case RowOp::GenNorm: launch_vec_nv<RowOp::GenNorm>(g, a, mg, s); break;
         }
         return hipGetLastError();
     }
+    // the generic envelope's norms take this path only for vectorisable
+    // rows; their caller has a kernel for every other layout
+    if (a.op == RowOp::GenRmsNorm || a.op == RowOp::GenNorm) return hipErrorNotSupported;
 
     const uint64_t blocks = (rows + (kBlock / kWave) - 1) / (kBlock / kWave);
     if (blocks > 0x7fffffffull) return hipErrorInvalidConfiguration;
