@@ -183,8 +183,9 @@ __device__ __forceinline__ float silu_back(float x, float grad, const ExpCtx &t)
 EMEL_FN(SiluBack, true, true, silu_back(a, b, t))
 // The remaining typed unary events (unary.rs:472-610), every operation
 // rounded separately as the reference writes it.
-// f32::signum: +-1 with the sign of a (both zeros included), NaN for NaN.
-EMEL_FN(Sgn, false, false, a != a ? a : __builtin_copysignf(1.0f, a))
+// f32::signum: +-1 with the sign of a (both zeros included); every NaN
+// gives f32::NAN, the quiet NaN 0x7fc00000, whatever its sign or payload.
+EMEL_FN(Sgn, false, false, a != a ? __builtin_nanf("") : __builtin_copysignf(1.0f, a))
 EMEL_FN(Step, false, false, a > 0.0f ? 1.0f : 0.0f)
 EMEL_FN(GeluQuick, false, false, 0.5f * a * (1.0f + emel_tanhf(0.7978846f * a * (1.0f + 0.044715f * a * a))))
 // (x + 3).clamp(0, 6): NaN passes through

@@ -414,7 +414,11 @@ emel_status emel_op_l2_norm(const emel_tensor_view *in, const emel_tensor_view_m
  * did not would return EMEL_ERR_INVALID_PARAMETERS.  All calls on one
  * device share that array: calls that overlap on the device (concurrent
  * streams, or graphs replayed concurrently) race and must be serialised by
- * the caller. */
+ * the caller.  A race can leave a row's arrival counter non-zero; every
+ * later call on that device then merges the wrong partials and returns
+ * wrong indices with no error, until the process ends (a new process
+ * starts with the array zeroed).  The first call on a device may be made
+ * under HIP graph capture: its set-up kernel is captured with it. */
 emel_status emel_op_argmax_rows_no_alloc(const emel_tensor_view *src, const emel_tensor_view_mut *dst,
                                          emel_stream stream);
 

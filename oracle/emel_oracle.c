@@ -298,7 +298,7 @@ static float apply_unary(int subop, float x)
 {
     switch (subop) { /* unary.rs:472-610 */
     case SUB_ABS: return fabsf(x);
-    case SUB_SGN: return isnan(x) ? x : copysignf(1.0f, x); /* f32::signum: +-0 -> +-1 */
+    case SUB_SGN: return isnan(x) ? __builtin_nanf("") : copysignf(1.0f, x); /* f32::signum: +-0 -> +-1, NaN -> f32::NAN (0x7fc00000) */
     case SUB_NEG: return -x;
     case SUB_STEP: return x > 0.0f ? 1.0f : 0.0f;
     case SUB_TANH: return tanhf(x);

@@ -9,7 +9,9 @@
 2. In a fresh process (tests/graph_capture_child.py), the calls that would
    allocate, wait or advance host state refuse a capturing stream with
    EMEL_ERR_STREAM_CAPTURE before enqueuing anything; the capture stays
-   valid, and the same calls succeed eagerly afterwards.
+   valid, and the same calls succeed eagerly afterwards.  The process's
+   first allocation-free argmax_rows call is made under that capture and
+   its replays match an eager emel_op_argmax_rows.
 """
 import json
 import subprocess
@@ -117,5 +119,9 @@ def test_refusals_under_capture_in_a_fresh_process(gpu):
         assert out[key] == cap, (key, out)
     assert out["add"] == int(eh.Status.OK), out
     assert out["state_unchanged"] and out["replay_matches"], out
+    # the first allocation-free call of the process, made under capture
+    assert out["argmax_no_alloc_first"] == int(eh.Status.OK), out
+    assert out["argmax_rows_eager"] == int(eh.Status.OK), out
+    assert out["argmax_no_alloc_matches"] and out["argmax_no_alloc_replay2"], out
     for key in ("gelu_eager", "sum_eager", "l2_norm_eager", "get_rows_eager"):
         assert out[key] == int(eh.Status.OK), (key, out)

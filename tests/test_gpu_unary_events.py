@@ -56,6 +56,17 @@ def test_typed_unary_event_bit_exact(gpu, xs, code):
     assert_bits_equal(got, want, code.name)
 
 
+def test_sgn_nan_bits(gpu):
+    # assert_bits_equal lets any NaN match any NaN; f32::signum's NaN is
+    # the one quiet NaN 0x7fc00000, checked bit for bit here
+    nans = np.array([0x7FC00000, 0xFFC00000, 0x7FC00123, 0xFFFFFFFF, 0x7F800001, 0xFF800001, 0x7FBFFFFF, 0x3F800000],
+                    np.uint32).view(np.float32)
+    got, want = run_event(gpu, lambda i, o: eh.OpUnaryEvent(U.SGN, i, o), lambda i, o: orc.unary_event(int(U.SGN), i, o),
+                          nans, [nans.size, 1, 1, 1])
+    assert (got.view(np.uint32) == want.view(np.uint32)).all(), (got.view(np.uint32), want.view(np.uint32))
+    assert (got.view(np.uint32)[:7] == 0x7FC00000).all() and got[7] == 1.0
+
+
 @pytest.mark.parametrize("name", list(MATH))
 def test_log_sin_cos_bit_exact(gpu, xs, name):
     print(f"{name}: {xs.size} values", flush=True)

@@ -66,6 +66,14 @@ def test_sign_step_rounding_closed_forms():
     assert np.isnan(ev(U.SGN, nan)).all() and ev(U.STEP, nan)[0] == 0.0
 
 
+def test_sgn_of_every_nan_is_the_canonical_nan():
+    # f32::signum returns f32::NAN (0x7fc00000) for any NaN: negative NaNs,
+    # payloads and signalling NaNs included (unary.rs:483 calls signum)
+    nans = np.array([0x7FC00000, 0xFFC00000, 0x7FC00123, 0xFFFFFFFF, 0x7F800001, 0xFF800001, 0x7FBFFFFF],
+                    np.uint32).view(np.float32)
+    assert (ev(U.SGN, nans).view(np.uint32) == 0x7FC00000).all()
+
+
 def test_hard_activations_closed_forms():
     x = grid(2)
     c = np.clip(f32ops(x + np.float32(3.0)), np.float32(0.0), np.float32(6.0))  # each op rounded to f32
