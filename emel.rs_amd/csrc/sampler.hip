@@ -16,10 +16,15 @@
 //
 // Kernels, in launch order (the same sequence for every request; rows that
 // finish a stage early skip the later ones):
-//   k_smp_max     (row, chunk) workgroups: chunk maxima of v.
-//   k_smp_exp     (row, chunk): e written in place, and the chunk's f64 sum.
-//   k_smp_seg     (row, chunk): each 512-element sub-chunk's exact
-//                 contribution in units of the binade its f64 prefix predicts.
+//   k_smp_max     (row, chunk) workgroups: chunk maxima of v; for chunks of
+//                 at most 8192 columns also each 512-element sub-chunk's
+//                 maximum and approximate sum of exp(v - that maximum).
+//   k_smp_expseg  (row, chunk), chunks of at most 8192 columns: e written
+//                 in place, and each sub-chunk's exact contribution in units
+//                 of the binade predicted from the approximate sums.
+//   k_smp_exp and k_smp_seg, wider chunks, the same in two passes: e and
+//                 the chunk's f64 sum, then the predictions from exact f64
+//                 prefixes.
 //   k_smp_sum     one wave per row: the exact sequential sum (seqsum.hpp),
 //                 taking a sub-chunk's predicted contribution when the exact
 //                 state confirms it, walking the other sub-chunks from
@@ -100,10 +105,25 @@ struct SegInfo {
     uint32_t flags; // bit 0 ok, bit 1 one tie, bit 2 its parity, bit 3 empty slot
     uint32_t pad;
 };
+// Chunks of at most kFuseSubs sub-chunks (kFuseCols columns) take the fused
+// path: k_smp_max<true> also leaves an approximate sum of exp(v - m_k) per
+// sub-chunk (m_k its maximum), and k_smp_expseg writes e and predicts each
+// sub-chunk from those sums in one pass.  Wider chunks run k_smp_max<false>,
+// k_smp_exp and k_smp_seg, which predict from exact f64 sums of e.
+constexpr uint32_t kFuseSubs = 16;
+constexpr uint32_t kFusePerWave = kFuseSubs / (kBlock / kWave);
+constexpr uint64_t kFuseCols = uint64_t{kFuseSubs} * kSub;
+static_assert(kFusePerWave * (kBlock / kWave) == kFuseSubs, "sub-chunks split evenly over the waves");
+struct SubSum {
+    float m; // maximum of v over the sub-chunk (-inf when it has none)
+    float s; // ~ sum of exp(v - m) over the sub-chunk; 0 when m is -inf
+};
 
 struct SmpWs {
     float *part;   // rows * chunks chunk maxima
-    double *psum;  // rows * chunks f64 sums of e per chunk (binade prediction)
+    double *psum;  // rows * chunks f64 sums of e per chunk (binade prediction);
+                   // fused path: ~ sums of exp(v - chunk maximum)
+    SubSum *sub;   // rows * chunks * subs per chunk (fused path)
     SegInfo *seg;  // rows * chunks * subs per chunk
     RowSel *sel;   // rows
     uint32_t *hist; // rows * kBins
@@ -212,6 +232,11 @@ __device__ __forceinline__ void chunk_range(const SmpGeo &g, uint32_t chunk, uin
     c1 = c0 + g.chunk_cols < g.card ? c0 + g.chunk_cols : g.card;
 }
 
+__device__ __forceinline__ uint32_t subs_per_chunk(const SmpGeo &g)
+{
+    return static_cast<uint32_t>((g.chunk_cols + kSub - 1) / kSub);
+}
+
 // Block reduction of a float maximum (NaN-free operands), 256 threads.
 __device__ __forceinline__ float block_max256(float v)
 {
@@ -230,6 +255,54 @@ __device__ __forceinline__ float block_max256(float v)
 
 // ---- stage 1: chunk maxima of v = x * scale ---------------------------------
 
+// The fused path's lane layout of a sub-chunk starting at column a0: lane l
+// holds columns a0 + 4 l .. a0 + 4 l + 3 and a0 + kSub / 2 + 4 l .. + 3
+// (elements 0-3 and 4-7 of its kPer), so each 128-bit load or store
+// instruction of a wave covers 1 KiB contiguously.
+constexpr uint32_t kSplit = 2; // groups of a lane's elements
+static_assert(kPer == 4 * kSplit, "one float4 per group");
+__device__ __forceinline__ uint64_t split_col(uint64_t a0, uint32_t lane, uint32_t q)
+{
+    return a0 + (q / 4) * (kSub / kSplit) + 4 * lane + (q % 4);
+}
+
+// Lane `lane`'s elements of the sub-chunk at a0 (zeros past c1, or everywhere
+// when !valid).
+__device__ __forceinline__ void load_split(const SmpGeo &g, const float *x, uint64_t a0, uint64_t c1, uint32_t lane,
+                                           bool valid, float (&v)[kPer])
+{
+#pragma unroll
+    for (uint32_t h = 0; h < kSplit; ++h) {
+        const uint64_t col = split_col(a0, lane, 4 * h);
+        if (valid && g.vec && col + 4 <= c1) {
+            // plain loads: later passes re-read these lines from cache
+            const float4 t = *reinterpret_cast<const float4 *>(x + col);
+            v[4 * h] = t.x;
+            v[4 * h + 1] = t.y;
+            v[4 * h + 2] = t.z;
+            v[4 * h + 3] = t.w;
+        } else {
+#pragma unroll
+            for (uint32_t q = 0; q < 4; ++q) v[4 * h + q] = valid && col + q < c1 ? x[col + q] : 0.0f;
+        }
+    }
+}
+
+// exp(x) for the binade predictions only, never for a result: one hardware
+// 2^x of x log2(e).  The f32 product's rounding and v_exp_f32's own error
+// leave it within about (1 + |x|) 2^-23 of exp(x).
+__device__ __forceinline__ float approx_exp(float x)
+{
+    return __builtin_amdgcn_exp2f(x * 1.44269504088896341f);
+}
+
+// FUSED (chunks of at most kFuseSubs sub-chunks) reads the chunk as
+// k_smp_expseg does, lane l of a wave holding elements kPer l .. kPer l +
+// kPer - 1 of a sub-chunk, and also leaves each sub-chunk's maximum and
+// approximate sum of exp(v - that maximum) in sub, and in psum the chunk's
+// approximate sum of exp(v - chunk maximum): k_smp_expseg's binade
+// predictions start from them.
+template <bool FUSED>
 __global__ __launch_bounds__(kBlock) void k_smp_max(SmpGeo g, float *logits, SmpWs w)
 {
     const uint32_t row = blockIdx.x / g.chunks, chunk = blockIdx.x % g.chunks;
@@ -246,13 +319,76 @@ __global__ __launch_bounds__(kBlock) void k_smp_max(SmpGeo g, float *logits, Smp
     uint64_t c0, c1;
     chunk_range(g, chunk, c0, c1);
     const float scale = g.scale;
-    float m = -__builtin_inff();
-    visit<false>(g, x, c0, c1, [&](float &v, uint64_t) {
-        const float s = v * scale;
-        m = s > m ? s : m; // f32::max: a NaN operand is never taken
-    });
-    m = block_max256(m);
-    if (threadIdx.x == 0) w.part[blockIdx.x] = m;
+    if constexpr (!FUSED) {
+        float m = -__builtin_inff();
+        visit<false>(g, x, c0, c1, [&](float &v, uint64_t) {
+            const float s = v * scale;
+            m = s > m ? s : m; // f32::max: a NaN operand is never taken
+        });
+        m = block_max256(m);
+        if (threadIdx.x == 0) w.part[blockIdx.x] = m;
+    } else {
+        const uint32_t lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+        const uint32_t spc = subs_per_chunk(g);
+        const uint32_t nsub = static_cast<uint32_t>((c1 - c0 + kSub - 1) / kSub); // <= kFuseSubs
+        float v[kFusePerWave][kPer];
+#pragma unroll
+        for (uint32_t j = 0; j < kFusePerWave; ++j) {
+            const uint32_t k = wave + (kBlock / kWave) * j;
+            load_split(g, x, c0 + static_cast<uint64_t>(k) * kSub, c1, lane, k < nsub, v[j]);
+        }
+        float wm = -__builtin_inff(); // this wave's maximum
+        float mk[kFusePerWave], sk[kFusePerWave];
+#pragma unroll
+        for (uint32_t j = 0; j < kFusePerWave; ++j) {
+            const uint32_t k = wave + (kBlock / kWave) * j;
+            mk[j] = -__builtin_inff();
+            sk[j] = 0.0f;
+            if (k >= nsub) continue; // wave-uniform
+            const uint64_t a0 = c0 + static_cast<uint64_t>(k) * kSub;
+            float m = -__builtin_inff(), a = 0.0f;
+            // only a row's last sub-chunk can end early: the others skip the
+            // per-element column checks
+            auto stats = [&](auto full_tag) {
+                constexpr bool kFull = decltype(full_tag)::value;
+                float lm = -__builtin_inff();
+#pragma unroll
+                for (uint32_t q = 0; q < kPer; ++q) {
+                    const float t = v[j][q] * scale;
+                    v[j][q] = t;
+                    const bool in = kFull || split_col(a0, lane, q) < c1;
+                    lm = in && t > lm ? t : lm; // f32::max: a NaN operand is never taken
+                }
+                m = wave_max_dpp(lm);
+                if (m > -__builtin_inff()) {
+#pragma unroll
+                    for (uint32_t q = 0; q < kPer; ++q) {
+                        const bool in = kFull || split_col(a0, lane, q) < c1;
+                        a += in ? approx_exp(v[j][q] - m) : 0.0f;
+                    }
+                }
+            };
+            if (a0 + kSub <= c1) stats(std::true_type{});
+            else stats(std::false_type{});
+            // a NaN or +inf element makes the sum NaN: every prediction from it fails
+            mk[j] = m;
+            sk[j] = static_cast<float>(wave_sum_dpp(static_cast<double>(a)));
+            if (lane == 0) w.sub[static_cast<uint64_t>(blockIdx.x) * spc + k] = SubSum{m, sk[j]};
+            wm = m > wm ? m : wm;
+        }
+        const float mc = block_max256(wm);
+        double t = 0.0;
+#pragma unroll
+        for (uint32_t j = 0; j < kFusePerWave; ++j)
+            if (sk[j] != 0.0f) t += static_cast<double>(sk[j] * approx_exp(mk[j] - mc));
+        __shared__ double s_acc[kBlock / kWave];
+        if (lane == 0) s_acc[wave] = t;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            w.part[blockIdx.x] = mc;
+            w.psum[blockIdx.x] = (s_acc[0] + s_acc[1]) + (s_acc[2] + s_acc[3]);
+        }
+    }
 }
 
 __device__ __forceinline__ float row_max(const SmpGeo &g, const SmpWs &w, uint32_t row)
@@ -305,9 +441,76 @@ __global__ __launch_bounds__(kBlock) void k_smp_exp(SmpGeo g, float *logits, Smp
 // the binade is the predicted one and that the units fit below 2^24: the
 // bound steers the work, the checks decide correctness.
 
-__device__ __forceinline__ uint32_t subs_per_chunk(const SmpGeo &g)
+
+// The prediction of one sub-chunk whose exact running sum before and after
+// lies in [lo, hi]: when both bounds share one normal f32 binade
+// [2^(b-1), 2^b), the sub-chunk's units of 2^(b-24), at most one tie and
+// that tie's parity; otherwise not usable (flags 0).  Lane l holds kPer of
+// its elements (zeros past its end) in H groups of kPer / H consecutive
+// ones, group h starting at element h kSub / H + l kPer / H: H = 1 is eight
+// consecutive elements per lane, H = 2 two float4 of a wave-contiguous
+// layout.  Called by a whole wave; the result is the same in every lane.
+template <uint32_t H>
+__device__ __forceinline__ SegInfo predict_sub(const float (&e)[kPer], double lo, double hi)
 {
-    return static_cast<uint32_t>((g.chunk_cols + kSub - 1) / kSub);
+    constexpr uint32_t G = kPer / H;
+    static_assert(G * H == kPer, "groups split a lane's elements evenly");
+    SegInfo info{0, 0, 0, 0};
+    int elo = 0, ehi = 0;
+    (void)__builtin_frexp(lo, &elo);
+    (void)__builtin_frexp(hi, &ehi);
+    // normal f32 range, both bounds in one binade [2^(elo-1), 2^elo)
+    if (!(lo >= 0x1p-126 && hi < 0x1p127 && lo <= hi && elo == ehi)) return info;
+    const int32_t u = elo - 1 - 23;
+    uint32_t gs[H], ties = 0, tq = 0, tbefore = 0, th = 0;
+#pragma unroll
+    for (uint32_t h = 0; h < H; ++h) {
+        gs[h] = 0;
+#pragma unroll
+        for (uint32_t i = 0; i < G; ++i) {
+            const float x = e[h * G + i];
+            bool tie;
+            const uint32_t r = seq_units(x, u, tie);
+            // a tie counts its lower neighbour q here (r is q or q + 1)
+            const uint32_t q = tie ? static_cast<uint32_t>(__builtin_floorf(__builtin_ldexpf(x, -u))) : r;
+            if (tie && ties == 0) {
+                tq = q;
+                tbefore = gs[h];
+                th = h;
+            }
+            ties += tie ? 1u : 0u;
+            gs[h] += q;
+            gs[h] = gs[h] < (1u << 25) ? gs[h] : (1u << 25);
+        }
+    }
+    uint32_t incl[H], total = 0, mine_excl = 0, offs = 0, tie_offs = 0;
+#pragma unroll
+    for (uint32_t h = 0; h < H; ++h) {
+        const uint32_t c = gs[h] < kSeqLimit ? gs[h] : kSeqLimit;
+        incl[h] = wave_incl_scan(c);
+        if (th == h) {
+            mine_excl = incl[h] - c; // units of this group in the lanes before
+            tie_offs = offs;         // units of the groups before
+        }
+        offs += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl[h]), kWave - 1));
+    }
+    total = offs;
+    const uint64_t tmask = __ballot(ties != 0);
+    uint32_t nties = 0;
+    for (uint64_t m = tmask; m; m &= m - 1) {
+        nties += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(ties), __builtin_ctzll(m)));
+    }
+    info.units = total;
+    info.u = u;
+    if (nties == 0) {
+        info.flags = 1u;
+    } else if (nties == 1) {
+        const int tl = __builtin_ctzll(tmask);
+        const uint32_t before = tie_offs + mine_excl + tbefore; // units before the tie element
+        const uint32_t par = (before + tq) & 1u;
+        info.flags = 1u | 2u | (static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(par), tl)) << 2);
+    }
+    return info;
 }
 
 // One 256-thread workgroup per (row, chunk); wave w predicts sub-chunks
@@ -375,51 +578,118 @@ __global__ __launch_bounds__(kBlock) void k_smp_seg(SmpGeo g, float *logits, Smp
             for (uint32_t i = 0; i < k; ++i) Pk += s_sub[i];
             const double lo = Pk * (1.0 - seq_rel_bound(static_cast<double>(a0)));
             const double hi = (Pk + s_sub[k]) * (1.0 + seq_rel_bound(static_cast<double>(a1)));
-            int elo = 0, ehi = 0;
-            (void)__builtin_frexp(lo, &elo);
-            (void)__builtin_frexp(hi, &ehi);
-            // normal f32 range, both bounds in one binade [2^(elo-1), 2^elo)
-            if (lo >= 0x1p-126 && hi < 0x1p127 && lo <= hi && elo == ehi) { // uniform
-                const int32_t u = elo - 1 - 23;
-                float e[kPer];
-                load_sub(k, e);
-                uint32_t lsum = 0, ties = 0, tq = 0, tbefore = 0;
-#pragma unroll
-                for (uint32_t j = 0; j < kPer; ++j) {
-                    bool tie;
-                    const uint32_t r = seq_units(e[j], u, tie);
-                    // a tie counts its lower neighbour q here (r is q or q + 1)
-                    const uint32_t q = tie ? static_cast<uint32_t>(__builtin_floorf(__builtin_ldexpf(e[j], -u))) : r;
-                    if (tie && ties == 0) {
-                        tq = q;
-                        tbefore = lsum;
-                    }
-                    ties += tie ? 1u : 0u;
-                    lsum += q;
-                    lsum = lsum < (1u << 25) ? lsum : (1u << 25);
-                }
-                const uint32_t incl = wave_incl_scan(lsum < kSeqLimit ? lsum : kSeqLimit);
-                const uint32_t total = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), kWave - 1));
-                const uint64_t tmask = __ballot(ties != 0);
-                uint32_t nties = 0;
-                for (uint64_t m = tmask; m; m &= m - 1) {
-                    nties += static_cast<uint32_t>(
-                        __builtin_amdgcn_readlane(static_cast<int>(ties), __builtin_ctzll(m)));
-                }
-                info.units = total;
-                info.u = u;
-                if (nties == 0) {
-                    info.flags = 1u;
-                } else if (nties == 1) {
-                    const int tl = __builtin_ctzll(tmask);
-                    const uint32_t excl = incl - (lsum < kSeqLimit ? lsum : kSeqLimit);
-                    const uint32_t before = excl + tbefore; // units before the tie element
-                    const uint32_t par = (before + tq) & 1u;
-                    info.flags = 1u | 2u | (static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(par), tl)) << 2);
-                }
-            }
+            float e[kPer];
+            load_sub(k, e);
+            info = predict_sub<1>(e, lo, hi);
         }
         if (lane == 0) out[k] = info;
+    }
+}
+
+// ---- stages 2 and 2b in one pass (chunks of at most kFuseSubs sub-chunks) ---
+//
+// e = expf(v - m) in place, as k_smp_exp computes it, and each sub-chunk's
+// prediction as k_smp_seg makes it, from the e still in registers.  The sum
+// of e before a sub-chunk, and the sub-chunk's own, come from
+// k_smp_max<true>'s approximate sums (of the chunks before this one, then
+// of this chunk's sub-chunks before it), rescaled from their maxima to the
+// row's; the bounds widen by kApproxRel for their error.  Every wave works
+// on its own: no barrier, and the next sub-chunk's loads are in flight while
+// the current one is computed.  The walk's checks on the exact state decide
+// every prediction, so an approximate sum can only cost walks.
+//
+// Relative error of those sums, bounded with a wide margin: an approximate
+// exponential is within (1 + |x|) 2^-23 of exp(x) and the exact e within
+// (1 + |x|) 2^-24 of exp(v - m) (x = v - the maximum it is taken from, so
+// |x| grows only as e shrinks); weighted by size, a sum of N terms is then
+// within (2 + ln N) 2^-23, about 2^-19 for a 151,936-token row.
+constexpr double kApproxRel = 0x1p-14;
+
+__device__ __forceinline__ double readlane_f64(double v, uint32_t l)
+{
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(b)), l));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(b >> 32)), l));
+    return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+__global__ __launch_bounds__(kBlock) void k_smp_expseg(SmpGeo g, float *logits, SmpWs w)
+{
+    const uint32_t row = blockIdx.x / g.chunks, chunk = blockIdx.x % g.chunks;
+    const uint32_t lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    float *x = logits + static_cast<int64_t>(row) * g.ld;
+    uint64_t c0, c1;
+    chunk_range(g, chunk, c0, c1);
+    const uint32_t spc = subs_per_chunk(g);
+    const uint32_t nsub = static_cast<uint32_t>((c1 - c0 + kSub - 1) / kSub); // <= kFuseSubs
+    auto sub_col = [&](uint32_t k) { return c0 + static_cast<uint64_t>(k) * kSub; };
+    // the first sub-chunk's loads go out before the row state is read
+    float cur[kPer];
+    load_split(g, x, sub_col(wave), c1, lane, wave < nsub, cur);
+    const uint64_t rbase = static_cast<uint64_t>(row) * g.chunks;
+    float m = -__builtin_inff();
+    for (uint32_t c = lane; c < g.chunks; c += kWave) {
+        const float p = w.part[rbase + c];
+        m = p > m ? p : m;
+    }
+    m = wave_max_dpp(m);
+    double pre = 0.0; // ~ sum of e over the chunks before this one
+    for (uint32_t c = lane; c < chunk; c += kWave) {
+        const double sc = w.psum[rbase + c];
+        // m = +inf makes it NaN (inf - inf), and every prediction fails
+        if (sc != 0.0) pre += sc * exp(static_cast<double>(w.part[rbase + c]) - static_cast<double>(m));
+    }
+    pre = wave_sum_dpp(pre);
+    double term = 0.0; // lane i: ~ sum of e over sub-chunk i of this chunk
+    if (lane < nsub) {
+        const SubSum ss = w.sub[(rbase + chunk) * spc + lane];
+        if (ss.s != 0.0f) term = static_cast<double>(ss.s) * exp(static_cast<double>(ss.m) - static_cast<double>(m));
+    }
+    const double incl = wave_incl_scan_f64(term);
+    SegInfo *out = w.seg + (rbase + chunk) * spc;
+    // slots past the chunk's last sub-chunk (only in a shorter last chunk)
+    // are empty: they add nothing, whatever the state
+    for (uint32_t k = nsub + threadIdx.x; k < spc; k += blockDim.x) out[k] = SegInfo{0, 0, 8u, 0};
+    const float scale = g.scale;
+    const ExpfConsts ec = expf_consts_in_vgprs();
+#pragma unroll
+    for (uint32_t j = 0; j < kFusePerWave; ++j) {
+        const uint32_t k = wave + (kBlock / kWave) * j;
+        if (k >= nsub) break; // wave-uniform
+        float nxt[kPer];
+        if (j + 1 < kFusePerWave)
+            load_split(g, x, sub_col(k + kBlock / kWave), c1, lane, k + kBlock / kWave < nsub, nxt);
+        const uint64_t a0 = sub_col(k);
+        if (a0 + kSub <= c1) { // only a row's last sub-chunk can end early
+#pragma unroll
+            for (uint32_t q = 0; q < kPer; ++q) cur[q] = emel_expf(cur[q] * scale - m, kExp2Table, ec);
+        } else {
+#pragma unroll
+            for (uint32_t q = 0; q < kPer; ++q)
+                cur[q] = split_col(a0, lane, q) < c1 ? emel_expf(cur[q] * scale - m, kExp2Table, ec) : 0.0f;
+        }
+#pragma unroll
+        for (uint32_t h = 0; h < kSplit; ++h) {
+            const uint64_t col = split_col(a0, lane, 4 * h);
+            if (g.vec && col + 4 <= c1) {
+                *reinterpret_cast<float4 *>(x + col) = make_float4(cur[4 * h], cur[4 * h + 1], cur[4 * h + 2], cur[4 * h + 3]);
+            } else {
+#pragma unroll
+                for (uint32_t q = 0; q < 4; ++q)
+                    if (col + q < c1) x[col + q] = cur[4 * h + q];
+            }
+        }
+        const double own = readlane_f64(term, k);
+        const double before = pre + (readlane_f64(incl, k) - own);
+        const uint64_t a1 = a0 + kSub < c1 ? a0 + kSub : c1;
+        const double lo = before * (1.0 - kApproxRel) * (1.0 - seq_rel_bound(static_cast<double>(a0)));
+        const double hi = (before + own) * (1.0 + kApproxRel) * (1.0 + seq_rel_bound(static_cast<double>(a1)));
+        const SegInfo info = predict_sub<kSplit>(cur, lo, hi);
+        if (lane == 0) out[k] = info;
+        if (j + 1 < kFusePerWave) {
+#pragma unroll
+            for (uint32_t q = 0; q < kPer; ++q) cur[q] = nxt[q];
+        }
     }
 }
 
@@ -1205,7 +1475,7 @@ void plan_chunks(uint32_t rows, uint64_t card, uint64_t &chunk_cols, uint32_t &c
 uint64_t align256(uint64_t b) { return (b + 255) & ~uint64_t{255}; }
 
 struct WsLayout {
-    uint64_t part, psum, seg, sel, hist, ties, cand, cand2, total;
+    uint64_t part, psum, sub, seg, sel, hist, ties, cand, cand2, total;
 };
 
 WsLayout layout(uint32_t rows, uint32_t chunks, uint64_t chunk_cols, uint64_t cand_ld, bool merge)
@@ -1214,7 +1484,8 @@ WsLayout layout(uint32_t rows, uint32_t chunks, uint64_t chunk_cols, uint64_t ca
     WsLayout l{};
     l.part = 0;
     l.psum = l.part + align256(uint64_t{rows} * chunks * sizeof(float));
-    l.seg = l.psum + align256(uint64_t{rows} * chunks * sizeof(double));
+    l.sub = l.psum + align256(uint64_t{rows} * chunks * sizeof(double));
+    l.seg = l.sub + align256(uint64_t{rows} * chunks * spc * sizeof(SubSum));
     l.sel = l.seg + align256(uint64_t{rows} * chunks * spc * sizeof(SegInfo));
     l.hist = l.sel + align256(uint64_t{rows} * sizeof(RowSel));
     l.ties = l.hist + align256(uint64_t{rows} * kBins * sizeof(uint32_t));
@@ -1255,6 +1526,7 @@ hipError_t launch_sampler(const SamplerArgs &a, hipStream_t s)
     SmpWs w{};
     w.part = reinterpret_cast<float *>(base + l.part);
     w.psum = reinterpret_cast<double *>(base + l.psum);
+    w.sub = reinterpret_cast<SubSum *>(base + l.sub);
     w.seg = reinterpret_cast<SegInfo *>(base + l.seg);
     w.sel = reinterpret_cast<RowSel *>(base + l.sel);
     w.hist = reinterpret_cast<uint32_t *>(base + l.hist);
@@ -1263,9 +1535,14 @@ hipError_t launch_sampler(const SamplerArgs &a, hipStream_t s)
     w.cand2 = reinterpret_cast<uint64_t *>(base + l.cand2);
 
     const dim3 grid(a.rows * g.chunks);
-    k_smp_max<<<grid, kBlock, 0, s>>>(g, a.logits, w);
-    k_smp_exp<<<grid, kBlock, 0, s>>>(g, a.logits, w);
-    k_smp_seg<<<grid, kBlock, 0, s>>>(g, a.logits, w);
+    if (g.chunk_cols <= kFuseCols) {
+        k_smp_max<true><<<grid, kBlock, 0, s>>>(g, a.logits, w);
+        k_smp_expseg<<<grid, kBlock, 0, s>>>(g, a.logits, w);
+    } else {
+        k_smp_max<false><<<grid, kBlock, 0, s>>>(g, a.logits, w);
+        k_smp_exp<<<grid, kBlock, 0, s>>>(g, a.logits, w);
+        k_smp_seg<<<grid, kBlock, 0, s>>>(g, a.logits, w);
+    }
     k_smp_sum<<<a.rows, kSumThreads, 0, s>>>(g, a.logits, w);
     k_smp_div<<<grid, kBlock, 0, s>>>(g, a.logits, w);
     k_smp_resolve<<<a.rows, kResolveThreads, 0, s>>>(g, a.logits, w);

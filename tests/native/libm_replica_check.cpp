@@ -149,14 +149,24 @@ static void emu_walk(const float *e, uint64_t c0, uint64_t c1, uint32_t lanes, E
     }
 }
 
+static uint64_t splitmix(uint64_t &z);
+
 // chunk == 0: the whole range is walked (no predictions).  Otherwise
 // chunks of `chunk` elements split into sub-chunks of `sub`: k_smp_seg's
 // prediction per sub-chunk (f64 prefix of chunk and sub-chunk sums, the
 // rounding bound, units at the predicted binade, one tie resolved by
 // parity) and k_smp_sum's checks on the exact state; a sub-chunk that is
 // not taken is walked alone.  *jumped counts sub-chunks taken in one step.
-float seqsum_chunked(const float *e, uint64_t n, uint32_t lanes, uint64_t chunk, uint64_t sub, uint64_t *jumped)
+// perturb > 0 stands in for k_smp_expseg's approximate sums: the prefix and
+// the sub-chunk's sum each scaled by a random factor in [1 - perturb,
+// 1 + perturb], the bounds widened by `widen` (the kernel's kApproxRel).
+float seqsum_chunked(const float *e, uint64_t n, uint32_t lanes, uint64_t chunk, uint64_t sub, uint64_t *jumped,
+                     double perturb = 0.0, double widen = 0.0, uint64_t seed = 0)
 {
+    uint64_t z = seed;
+    auto jitter = [&]() {
+        return perturb > 0.0 ? 1.0 + perturb * (2.0 * static_cast<double>(splitmix(z) >> 11) * 0x1p-53 - 1.0) : 1.0;
+    };
     EmuState s;
     if (jumped) *jumped = 0;
     if (chunk == 0) {
@@ -171,8 +181,9 @@ float seqsum_chunked(const float *e, uint64_t n, uint32_t lanes, uint64_t chunk,
             const uint64_t a1 = std::min(c1, a0 + sub);
             double ssum = 0.0;
             for (uint64_t i = a0; i < a1; ++i) ssum += static_cast<double>(e[i]);
-            const double lo = Pk * (1.0 - (static_cast<double>(a0) * 0x1p-24 + 0x1p-30));
-            const double hi = (Pk + ssum) * (1.0 + (static_cast<double>(a1) * 0x1p-24 + 0x1p-30));
+            const double pe = Pk * jitter(), se = ssum * jitter();
+            const double lo = pe * (1.0 - widen) * (1.0 - (static_cast<double>(a0) * 0x1p-24 + 0x1p-30));
+            const double hi = (pe + se) * (1.0 + widen) * (1.0 + (static_cast<double>(a1) * 0x1p-24 + 0x1p-30));
             Pk += ssum;
             int elo = 0, ehi = 0;
             std::frexp(lo, &elo);
@@ -248,6 +259,31 @@ extern "C" float seqsum_chunked_f(const float *e, uint64_t n, uint32_t lanes, ui
                                   uint64_t *jumped)
 {
     return seqsum_chunked(e, n, lanes, chunk, sub, jumped);
+}
+
+extern "C" float seqsum_approx_f(const float *e, uint64_t n, uint32_t lanes, uint64_t chunk, uint64_t sub,
+                                 double perturb, double widen, uint64_t seed, uint64_t *jumped)
+{
+    return seqsum_chunked(e, n, lanes, chunk, sub, jumped, perturb, widen, seed);
+}
+
+// check_seqsum's families through the predictions with perturbed prefixes
+// (config 5's chunk shapes): counts results whose bits differ from the
+// sequential loop.
+extern "C" uint64_t check_seqsum_approx(uint64_t seed, int cases, uint64_t max_n, double perturb, double widen)
+{
+    uint64_t z = seed, bad = 0;
+    for (int c = 0; c < cases; ++c) {
+        const int family = c % 5;
+        const uint64_t n = 1 + splitmix(z) % max_n;
+        std::vector<float> e(n);
+        fill_case(z, family, e);
+        float want = 0.0f;
+        for (float v : e) want += v;
+        for (const uint64_t chunk : {5120ull, 1024ull})
+            if (differ(seqsum_chunked(e.data(), n, 32, chunk, 512, nullptr, perturb, widen, splitmix(z)), want)) ++bad;
+    }
+    return bad;
 }
 
 // Random cases of each family and length up to max_n, through the walk

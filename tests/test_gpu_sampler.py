@@ -143,6 +143,65 @@ def test_many_rows_batch_the_ranking(gpu):
     check(gpu, x, 1.0, 9000, [int(s) for s in g.integers(1, M, 600)])
 
 
+def test_wide_chunks_take_the_three_pass_exact_sum(gpu):
+    """300 rows of 60,000 logits make 9,216-column chunks, wider than the
+    fused exp + prediction pass holds (8,192): the chunk maxima, the
+    exponentials and the predictions then run as three kernels, the
+    predictions from exact f64 chunk sums.  Narrower chunks (every other
+    case here) take the fused pass and predict from approximate sums."""
+    g = np.random.Generator(np.random.PCG64(81))
+    x = g.standard_normal((300, 60000)).astype(np.float32)
+    check(gpu, x, 0.8, 40, [int(s) for s in g.integers(1, M, 300)])
+
+
+TIE_16_32 = np.float32(-6.978456974029541)  # glibc expf: 488.5 units of 2^-19, a tie while 16 <= S < 32
+TIE_32_64 = np.float32(-6.953190326690674)  # 250.5 units of 2^-18, a tie while 32 <= S < 64
+
+
+def one_tie_rows(g, rows, card):
+    """Rows whose running sum passes 16 within the first 16 elements (logit
+    0, e = 1), then grows by about 0.5 per 512-element sub-chunk (logits in
+    [-7.6, -6.3]), with both tie logits at random places in every
+    sub-chunk: in the binades [16, 32) and [32, 64) every sub-chunk then
+    holds exactly one element that lands halfway between two units, whose
+    rounding the prediction resolves from the parity of the units before
+    it."""
+    x = g.uniform(-7.6, -6.3, (rows, card)).astype(np.float32)
+    x[:, :16] = 0.0
+    for r in range(rows):
+        for a0 in range(512, card, 512):
+            n = min(512, card - a0)
+            i, j = g.choice(n, 2, replace=False)
+            x[r, a0 + i] = TIE_16_32
+            x[r, a0 + j] = TIE_32_64
+    return x
+
+
+def test_tie_constants_are_ties():
+    """The two logits' exponentials (host glibc expf, the function the GPU
+    replica matches bit for bit) sit exactly halfway between units of their
+    binade, and on whole units of the other one."""
+    libm = ctypes.CDLL("libm.so.6")
+    libm.expf.restype = ctypes.c_float
+    libm.expf.argtypes = [ctypes.c_float]
+    a, b = np.float64(libm.expf(float(TIE_16_32))), np.float64(libm.expf(float(TIE_32_64)))
+    assert np.ldexp(a, 19) % 1 == 0.5 and np.ldexp(a, 18) % 1 == 0.25
+    assert np.ldexp(b, 18) % 1 == 0.5 and np.ldexp(b, 19) % 1 == 0.0
+
+
+def test_one_tie_per_sub_chunk(gpu):
+    """Sub-chunks predicted with exactly one tie, in both prediction paths:
+    4 rows of 40,000 (1,024-column chunks, the fused pass, lanes holding two
+    float4 of a wave-contiguous layout) and 300 rows of 60,000 (9,216-column
+    chunks, the three-kernel path, eight consecutive elements per lane).  A
+    wrong tie position or parity moves S by one unit and every p with it."""
+    g = np.random.Generator(np.random.PCG64(82))
+    x = one_tie_rows(g, 4, 40000)
+    check(gpu, x, 1.0, 40, [3, 5, 7, 9])
+    x = one_tie_rows(g, 300, 60000)
+    check(gpu, x, 1.0, 40, [int(s) for s in g.integers(1, M, 300)])
+
+
 def test_unaligned_and_padded_rows(gpu):
     g = np.random.Generator(np.random.PCG64(77))
     x = g.standard_normal((4, 12345)).astype(np.float32)

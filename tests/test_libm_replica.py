@@ -122,6 +122,41 @@ def test_exact_sequential_sum_rounds(chk):
     assert chk.check_seqsum(2, 40, 200_000) == 0
 
 
+def test_exact_sum_from_approximate_prefixes(chk):
+    """The fused path (sampler.hip's k_smp_max<true> + k_smp_expseg) predicts
+    from approximate sums, with the bounds widened by 2^-14.  Correctness
+    rests on the walk's checks alone: prefixes perturbed within that margin,
+    and far beyond it (1%, which steers many predictions to a wrong binade),
+    must still give the bits of the sequential loop.  On a config-5-like row
+    the small perturbation takes as many sub-chunks in one step as exact
+    prefixes do, and the large one fewer."""
+    import numpy as np
+
+    chk.check_seqsum_approx.restype = ctypes.c_uint64
+    chk.check_seqsum_approx.argtypes = [ctypes.c_uint64, ctypes.c_int, ctypes.c_uint64, ctypes.c_double,
+                                        ctypes.c_double]
+    assert chk.check_seqsum_approx(3, 1000, 20_000, 2.0**-16, 2.0**-14) == 0
+    assert chk.check_seqsum_approx(4, 1000, 20_000, 1e-2, 2.0**-14) == 0
+    assert chk.check_seqsum_approx(5, 1000, 20_000, 0.5, 0.0) == 0
+    chk.seqsum_approx_f.restype = ctypes.c_float
+    chk.seqsum_approx_f.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint64,
+                                    ctypes.c_uint64, ctypes.c_double, ctypes.c_double, ctypes.c_uint64,
+                                    ctypes.POINTER(ctypes.c_uint64)]
+    g = np.random.Generator(np.random.PCG64(6))
+    v = (g.standard_normal(151936) / 0.8).astype(np.float32)
+    e = np.exp((v - v.max()).astype(np.float64)).astype(np.float32)
+    want = np.cumsum(e, dtype=np.float32)[-1]
+    ptr = e.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+    taken = {}
+    for perturb, widen in ((0.0, 0.0), (2.0**-16, 2.0**-14), (1e-2, 2.0**-14)):
+        jumped = ctypes.c_uint64(0)
+        got = chk.seqsum_approx_f(ptr, e.size, 32, 5120, 512, perturb, widen, 7, ctypes.byref(jumped))
+        assert np.float32(got) == want, perturb
+        taken[perturb] = jumped.value
+    assert taken[2.0**-16] >= taken[0.0] - 2, taken
+    assert taken[1e-2] < taken[0.0], taken
+
+
 def test_exact_sum_predictions_are_taken(chk):
     """On a config-5-like row (softmax of N(0,1) logits / 0.8 over 151,936
     tokens) most sub-chunks are taken from their prediction in one step: the
