@@ -28,9 +28,13 @@
 //   k_smp_sum     one wave per row: the exact sequential sum (seqsum.hpp),
 //                 taking a sub-chunk's predicted contribution when the exact
 //                 state confirms it, walking the other sub-chunks from
-//                 registers.
+//                 registers.  A second wave finds the fast candidate
+//                 threshold p_thr: the top_k-th largest p among the row's
+//                 sub-chunk maxima (fused path, top_k <= 8192).
 //   k_smp_div     (row, chunk): p written in place, plus the histogram of the
-//                 top 11 bits of p's total-order key.
+//                 top 11 bits of p's total-order key, and the list of every
+//                 p >= p_thr.  A row whose list fits 8192 entries is ranked
+//                 from it (mode 3): resolve and collect skip it.
 //   k_smp_resolve one workgroup per row: radix selection of the top_k-th
 //                 key, 11, 11, 10 key bits.  A row stops as soon as every
 //                 key at or above its current prefix fits the kCap
@@ -72,13 +76,17 @@ constexpr int32_t kInvalidRequest = 13;      // EMEL_ERR_INVALID_REQUEST
 // Per-row selection state (workspace).
 struct RowSel {
     float total;      // the sequential sum S
-    uint32_t mode;    // 0 open, 1 collect keys >= prefix, 2 collect keys > T + ties
+    uint32_t mode;    // 0 open, 1 collect keys >= prefix, 2 collect keys > T + ties,
+                      // 3 the list k_smp_div wrote (keys >= fast_key)
     uint32_t prefix;  // resolved top `depth` bits of the key (T when depth == 32)
     uint32_t depth;
     uint32_t need;    // elements still to take from the prefix region
     uint32_t above;   // elements whose key prefix is greater (all taken)
     uint32_t count;   // candidates collected
     uint32_t written; // collect cursor
+    uint32_t fast_on;    // k_smp_div lists the keys >= fast_key
+    uint32_t fast_key;   // key of p_thr (k_smp_sum)
+    uint32_t fast_count; // keys >= fast_key found; > kCap: the radix path decides
 };
 
 struct SmpGeo {
@@ -706,31 +714,95 @@ __global__ __launch_bounds__(kBlock) void k_smp_expseg(SmpGeo g, float *logits, 
 // it.  Each round commits at least one element, so the rounds end.
 
 constexpr uint32_t kHead = 512;          // a row's first elements, added one by one
+constexpr uint32_t kFastPer = 8;         // sub-chunk maxima per lane for the fast threshold
+constexpr uint32_t kFastWg = 256;        // fast candidates a k_smp_div workgroup buffers
 
-// One wave per row.  The sub-chunks' predictions are read a batch at a
-// time (lane i holds sub-chunk kb + i's).  A sub-chunk whose predicted
-// contribution holds on the exact state -- the same binade, and the units
-// (its one tie resolved by the current parity) stay below 2^24, so no
-// element inside it can cross (units never decrease) -- is added in one
-// step.  Any other sub-chunk is loaded straight into the walk's registers
-// (lane l holds its elements kPer l .. kPer l + kPer - 1, 128-bit loads in
-// flight) and walked: one round, plus one per event.
-constexpr uint32_t kSumThreads = kWave;
+// The fast candidate threshold, by one wave.  The top_k largest sub-chunk
+// maxima are top_k distinct elements; with e_thr the top_k-th largest of
+// their e (computed as k_smp_expseg computes e), at least top_k elements
+// have e >= e_thr, so p >= p_thr = e_thr / S (the division k_smp_div uses,
+// correctly rounded and so monotone), and every element of the top_k by p
+// -- ties at the boundary included -- has p >= p_thr.  k_smp_div then lists
+// those elements directly.  Returns false when the row cannot take it
+// (three-pass chunks, top_k above kCap or above the sub-chunk count, more
+// than kFastPer sub-chunks per lane).
+__device__ bool fast_threshold(const SmpGeo &g, const SmpWs &w, uint32_t row, uint32_t nslots, uint32_t spc,
+                               uint32_t lane, uint32_t &ethr_key)
+{
+    if (!(g.chunk_cols <= kFuseCols && g.top_k <= kCap && nslots <= kWave * kFastPer)) return false;
+    const SubSum *sub = w.sub + static_cast<uint64_t>(row) * nslots;
+    float mv[kFastPer];
+    bool valid[kFastPer];
+    float M = -__builtin_inff();
+#pragma unroll
+    for (uint32_t j = 0; j < kFastPer; ++j) {
+        const uint32_t slot = lane + kWave * j;
+        valid[j] = false;
+        if (slot < nslots) {
+            uint64_t c0, c1;
+            chunk_range(g, slot / spc, c0, c1);
+            valid[j] = static_cast<uint64_t>(slot % spc) * kSub < c1 - c0; // written by k_smp_max<true>
+        }
+        mv[j] = valid[j] ? sub[slot].m : -__builtin_inff();
+        M = mv[j] > M ? mv[j] : M;
+    }
+    M = wave_max_dpp(M); // the row maximum: every element lies in a sub-chunk
+    const ExpfConsts ec = expf_consts_in_vgprs();
+    uint32_t key[kFastPer];
+    uint32_t nvalid = 0;
+#pragma unroll
+    for (uint32_t j = 0; j < kFastPer; ++j) {
+        key[j] = valid[j] ? total_key(emel_expf(mv[j] - M, kExp2Table, ec)) : 0u; // valid keys are > 0
+        nvalid += static_cast<uint32_t>(__builtin_popcountll(__ballot(valid[j])));
+    }
+    if (nvalid < g.top_k) return false;
+    // the largest t with top_k keys >= t, bit by bit from the top
+    uint32_t t = 0;
+    for (int b = 31; b >= 0; --b) {
+        const uint32_t c = t | (1u << b);
+        uint32_t n = 0;
+#pragma unroll
+        for (uint32_t j = 0; j < kFastPer; ++j) n += static_cast<uint32_t>(__builtin_popcountll(__ballot(key[j] >= c)));
+        if (n >= g.top_k) t = c;
+    }
+    ethr_key = t;
+    return true;
+}
+
+// One wave per row walks (wave 0); wave 1 computes the fast candidate
+// threshold beside it, off the walk's path.  The sub-chunks' predictions are
+// read a batch at a time (lane i holds sub-chunk kb + i's).  A sub-chunk
+// whose predicted contribution holds on the exact state -- the same binade,
+// and the units (its one tie resolved by the current parity) stay below
+// 2^24, so no element inside it can cross (units never decrease) -- is
+// added in one step.  Any other sub-chunk is loaded straight into the
+// walk's registers (lane l holds its elements kPer l .. kPer l + kPer - 1,
+// 128-bit loads in flight) and walked: one round, plus one per event.
+constexpr uint32_t kSumThreads = 2 * kWave;
 
 __global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *logits, SmpWs w)
 {
     __shared__ float4 s_head[kHead / 4]; // the row's first elements, for lane 0's sequential adds
+    __shared__ uint32_t s_fast[2];       // wave 1's threshold: taken, e_thr's key
     const uint32_t row = blockIdx.x;
-    const uint32_t lane = threadIdx.x;
+    const uint32_t lane = threadIdx.x % kWave;
     const float *x = logits + static_cast<int64_t>(row) * g.ld;
     const uint32_t spc = subs_per_chunk(g);
     const uint64_t card4 = g.card & ~uint64_t{3};
     SumState s{0u, -149, true, 0.0f};
-    bool nan_final = false;
     // The row's predictions form one list of chunks * spc slots; they are
     // read 64 at a time (lane i holds slot base + i), the next batch in
     // flight while this one is used.
     const uint32_t nslots = g.chunks * spc;
+    if (threadIdx.x >= kWave) { // wave 1
+        uint32_t ethr_key = 0;
+        const bool fast = fast_threshold(g, w, row, nslots, spc, lane, ethr_key);
+        if (lane == 0) {
+            s_fast[0] = fast ? 1u : 0u;
+            s_fast[1] = ethr_key;
+        }
+    } else { // wave 0: the walk
+    bool nan_final = false;
     const SegInfo *seg = w.seg + static_cast<uint64_t>(row) * nslots;
     SegInfo nxt{0, 0, 8u, 0};
     if (lane < nslots) nxt = seg[lane];
@@ -820,7 +892,11 @@ __global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *
                         s_head[kPer / 4 * lane + j] =
                             make_float4(e[4 * j], e[4 * j + 1], e[4 * j + 2], e[4 * j + 3]);
                 }
-                __syncthreads(); // one wave: orders its LDS writes before lane 0's reads
+                // orders this wave's LDS writes before lane 0's reads (wave 1
+                // never reaches here, so no workgroup barrier)
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
                 float acc = seq_value(s.m, s.u);
                 if (lane == 0) {
                     // whole float4s: past n the elements are +0, which leaves
@@ -847,7 +923,16 @@ __global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *
             if (head < kSub) sum_tile<kPer>(e, s, head); // the head's elements are committed
         }
     }
-    if (lane == 0) w.sel[row].total = s.finite ? seq_value(s.m, s.u) : s.special;
+    } // wave 0
+    __syncthreads(); // both waves: wave 1's threshold is in s_fast
+    if (threadIdx.x == 0) {
+        const float S = s.finite ? seq_value(s.m, s.u) : s.special;
+        w.sel[row].total = S;
+        if (s_fast[0] && s.finite) { // a NaN or +inf sum takes the radix path
+            w.sel[row].fast_key = total_key(div_by_recip(from_key(s_fast[1]), 1.0 / static_cast<double>(S)));
+            w.sel[row].fast_on = 1u;
+        }
+    }
 }
 
 // ---- stage 4: p = e / S in place, first radix digit -------------------------
@@ -862,23 +947,48 @@ __device__ __forceinline__ void flush_hist(uint32_t *s_hist, uint32_t nbins, uin
     }
 }
 
+// Rows with a fast threshold (k_smp_sum) also list every key >= fast_key:
+// buffered per workgroup in LDS, then placed with one atomic.  A workgroup
+// with more than kFastWg of them pushes the row's count past kCap, and the
+// row takes the radix path.
 __global__ __launch_bounds__(kBlock) void k_smp_div(SmpGeo g, float *logits, SmpWs w)
 {
     __shared__ uint32_t s_hist[kBins];
+    __shared__ uint64_t s_fbuf[kFastWg];
+    __shared__ uint32_t s_fcnt, s_fbase;
     const uint32_t row = blockIdx.x / g.chunks, chunk = blockIdx.x % g.chunks;
     float *x = logits + static_cast<int64_t>(row) * g.ld;
     for (uint32_t b = threadIdx.x; b < kBins; b += blockDim.x) s_hist[b] = 0;
+    if (threadIdx.x == 0) s_fcnt = 0;
     __syncthreads();
+    const RowSel sel = w.sel[row];
+    const bool fast = sel.fast_on != 0;
+    const uint32_t fkey = sel.fast_key;
     // S >= 1 (the maximal element contributes expf(0) = 1) or NaN: the
     // reciprocal form is the correctly rounded quotient (div_by_recip)
-    const double recip = 1.0 / static_cast<double>(w.sel[row].total);
+    const double recip = 1.0 / static_cast<double>(sel.total);
     uint64_t c0, c1;
     chunk_range(g, chunk, c0, c1);
-    visit<true>(g, x, c0, c1, [&](float &v, uint64_t) {
+    visit<true, 4>(g, x, c0, c1, [&](float &v, uint64_t col) {
         v = div_by_recip(v, recip);
-        atomicAdd(&s_hist[total_key(v) >> 21], 1u);
+        const uint32_t key = total_key(v);
+        atomicAdd(&s_hist[key >> 21], 1u);
+        if (fast && key >= fkey) {
+            const uint32_t i = atomicAdd(&s_fcnt, 1u);
+            if (i < kFastWg) s_fbuf[i] = cand_word(key, static_cast<uint32_t>(col));
+        }
     });
-    flush_hist(s_hist, kBins, w.hist + static_cast<uint64_t>(row) * kBins);
+    flush_hist(s_hist, kBins, w.hist + static_cast<uint64_t>(row) * kBins); // begins with a barrier
+    if (!fast) return; // uniform
+    const uint32_t n = s_fcnt;
+    if (n == 0) return; // uniform
+    if (threadIdx.x == 0) s_fbase = atomicAdd(&w.sel[row].fast_count, n <= kFastWg ? n : kCap + 1);
+    __syncthreads();
+    const uint32_t base = s_fbase;
+    uint64_t *list = w.cand + static_cast<uint64_t>(row) * g.cand_ld;
+    if (n <= kFastWg)
+        for (uint32_t i = threadIdx.x; i < n; i += blockDim.x)
+            if (base + i < kCap) list[base + i] = s_fbuf[i];
 }
 
 // Inclusive prefix sum over a 256-thread workgroup (uses s_tmp[4]).
@@ -986,6 +1096,13 @@ __global__ __launch_bounds__(kResolveThreads) void k_smp_resolve(SmpGeo g, float
     const uint32_t row = blockIdx.x;
     RowSel sel = w.sel[row];
     if (sel.mode != 0) return; // uniform
+    if (sel.fast_on && sel.fast_count <= kCap) { // uniform: k_smp_div listed the candidates
+        if (threadIdx.x == 0) {
+            w.sel[row].count = sel.fast_count; // >= top_k: the maxima behind the threshold
+            w.sel[row].mode = 3;
+        }
+        return;
+    }
     sel = pick_digit(sel, w.hist + static_cast<uint64_t>(row) * kBins, 11, s_tmp, s_pick);
     float *x = logits + static_cast<int64_t>(row) * g.ld;
     for (uint32_t pass = 1; pass <= 2 && sel.mode == 0; ++pass) {
@@ -1032,6 +1149,7 @@ __global__ __launch_bounds__(kBlock) void k_smp_collect(SmpGeo g, float *logits,
     __shared__ uint32_t s_base;
     const uint32_t row = blockIdx.x / g.chunks, chunk = blockIdx.x % g.chunks;
     const RowSel sel = w.sel[row];
+    if (sel.mode == 3) return; // uniform: listed by k_smp_div
     float *x = logits + static_cast<int64_t>(row) * g.ld;
     uint64_t *list = w.cand + static_cast<uint64_t>(row) * g.cand_ld;
     uint64_t c0, c1;

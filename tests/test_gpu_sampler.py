@@ -202,6 +202,26 @@ def test_one_tie_per_sub_chunk(gpu):
     check(gpu, x, 1.0, 40, [int(s) for s in g.integers(1, M, 300)])
 
 
+def test_fast_candidate_list_and_its_fallback(gpu):
+    """The list k_smp_div writes from the sub-chunk maxima's threshold, and
+    the radix path it falls back to, in one batched call (top_k 40 over
+    151,936 logits):
+      row 0: N(0,1) on a 0.5 grid -- dozens of p ties at the top_k-th value,
+             a few hundred candidates, ranked by index;
+      row 1: all logits equal -- every element a candidate: past 8192 the
+             radix path with its exact ties decides;
+      row 2: N(0,1);
+      row 3: 10,000 logits at 5.0 spread over the row -- the threshold is
+             their p, more than 256 candidates in one workgroup."""
+    g = np.random.Generator(np.random.PCG64(83))
+    card = 151936
+    x = g.standard_normal((4, card)).astype(np.float32)
+    x[0] = np.round(x[0] * 2) / 2
+    x[1] = 0.0
+    x[3, g.choice(card, 10000, replace=False)] = 5.0
+    check(gpu, x, 1.0, 40, [11, 13, 17, 19])
+
+
 def test_unaligned_and_padded_rows(gpu):
     g = np.random.Generator(np.random.PCG64(77))
     x = g.standard_normal((4, 12345)).astype(np.float32)
