@@ -28,9 +28,11 @@
 //   k_smp_sum     one wave per row: the exact sequential sum (seqsum.hpp),
 //                 taking a sub-chunk's predicted contribution when the exact
 //                 state confirms it, walking the other sub-chunks from
-//                 registers.  A second wave finds the fast candidate
-//                 threshold p_thr: the top_k-th largest p among the row's
-//                 sub-chunk maxima (fused path, top_k <= 8192).
+//                 registers or from LDS.  A second wave stages the
+//                 sub-chunks with unusable predictions into LDS ahead of
+//                 the walk, then finds the fast candidate threshold p_thr:
+//                 the top_k-th largest p among the row's sub-chunk maxima
+//                 (fused path, top_k <= 8192).
 //   k_smp_div     (row, chunk): p written in place, plus the histogram of the
 //                 top 11 bits of p's total-order key, and the list of every
 //                 p >= p_thr.  A row whose list fits 8192 entries is ranked
@@ -716,6 +718,7 @@ __global__ __launch_bounds__(kBlock) void k_smp_expseg(SmpGeo g, float *logits, 
 constexpr uint32_t kHead = 512;          // a row's first elements, added one by one
 constexpr uint32_t kFastPer = 8;         // sub-chunk maxima per lane for the fast threshold
 constexpr uint32_t kFastWg = 256;        // fast candidates a k_smp_div workgroup buffers
+constexpr uint32_t kStage = 24;          // walked sub-chunks k_smp_sum's second wave stages in LDS
 
 // The fast candidate threshold, by one wave.  The top_k largest sub-chunk
 // maxima are top_k distinct elements; with e_thr the top_k-th largest of
@@ -784,6 +787,12 @@ __global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *
 {
     __shared__ float4 s_head[kHead / 4]; // the row's first elements, for lane 0's sequential adds
     __shared__ uint32_t s_fast[2];       // wave 1's threshold: taken, e_thr's key
+    // wave 1 stages sub-chunks the walk will load: s_stage[i] holds slot
+    // s_slot[i] as the walk's registers hold it (float4 q of lane l at
+    // [i][q][l]); s_ready counts the staged ones (release / acquire)
+    __shared__ float4 s_stage[kStage][kPer / 4][kWave];
+    __shared__ uint32_t s_slot[kStage];
+    __shared__ uint32_t s_ready;
     const uint32_t row = blockIdx.x;
     const uint32_t lane = threadIdx.x % kWave;
     const float *x = logits + static_cast<int64_t>(row) * g.ld;
@@ -794,27 +803,22 @@ __global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *
     // read 64 at a time (lane i holds slot base + i), the next batch in
     // flight while this one is used.
     const uint32_t nslots = g.chunks * spc;
-    if (threadIdx.x >= kWave) { // wave 1
-        uint32_t ethr_key = 0;
-        const bool fast = fast_threshold(g, w, row, nslots, spc, lane, ethr_key);
-        if (lane == 0) {
-            s_fast[0] = fast ? 1u : 0u;
-            s_fast[1] = ethr_key;
-        }
-    } else { // wave 0: the walk
-    bool nan_final = false;
     const SegInfo *seg = w.seg + static_cast<uint64_t>(row) * nslots;
-    SegInfo nxt{0, 0, 8u, 0};
-    if (lane < nslots) nxt = seg[lane];
+    // A sub-chunk's element count (1 .. kSub) and first column.
+    auto slot_range = [&](uint32_t slot, uint64_t &a0) {
+        uint64_t c0, c1;
+        chunk_range(g, slot / spc, c0, c1);
+        a0 = c0 + static_cast<uint64_t>(slot % spc) * kSub;
+        const uint64_t a1 = a0 + kSub < c1 ? a0 + kSub : c1;
+        return static_cast<uint32_t>(a1 - a0);
+    };
     // A sub-chunk's elements kPer lane .. kPer lane + kPer - 1 into e (+0 past
     // its end); every address is clamped into the sub-chunk, so the loads
     // are unconditional.
     auto load_slot = [&](uint32_t slot, float (&e)[kPer], uint32_t &n) {
-        uint64_t c0, c1;
-        chunk_range(g, slot / spc, c0, c1);
-        const uint64_t a0 = c0 + static_cast<uint64_t>(slot % spc) * kSub;
-        const uint64_t a1 = a0 + kSub < c1 ? a0 + kSub : c1;
-        n = static_cast<uint32_t>(a1 - a0); // 1 .. kSub
+        uint64_t a0;
+        n = slot_range(slot, a0);
+        const uint64_t a1 = a0 + n;
         const uint32_t c = kPer * lane;
         if (g.vec && a1 <= card4) { // a0 and n are multiples of 4: whole float4s
             const float4 *x4 = reinterpret_cast<const float4 *>(x + a0);
@@ -836,6 +840,44 @@ __global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *
             for (uint32_t j = 0; j < kPer; ++j) e[j] = c + j < n ? e[j] : 0.0f;
         }
     };
+    if (threadIdx.x == 0) s_ready = 0;
+    __syncthreads();
+    if (threadIdx.x >= kWave) { // wave 1
+        // Stage, in slot order, the sub-chunks whose prediction is unusable
+        // (almost every sub-chunk the walk loads), slot 0 excepted: the walk
+        // starts there at once.  The walk takes a staged sub-chunk from LDS
+        // when it is ready and loads it itself otherwise, so it never waits.
+        uint32_t nst = 0;
+        for (uint32_t kb = 0; kb < nslots && nst < kStage; kb += kWave) {
+            const uint32_t sl = kb + lane;
+            bool need = false;
+            if (sl < nslots && sl != 0) need = (seg[sl].flags & 9u) == 0u; // neither usable nor empty
+            uint64_t m = __ballot(need);
+            while (m != 0 && nst < kStage) {
+                const uint32_t slot = kb + static_cast<uint32_t>(__builtin_ctzll(m));
+                m &= m - 1;
+                float e[kPer];
+                uint32_t n;
+                load_slot(slot, e, n);
+#pragma unroll
+                for (uint32_t q = 0; q < kPer / 4; ++q)
+                    s_stage[nst][q][lane] = make_float4(e[4 * q], e[4 * q + 1], e[4 * q + 2], e[4 * q + 3]);
+                if (lane == 0) s_slot[nst] = slot;
+                ++nst;
+                if (lane == 0) __hip_atomic_store(&s_ready, nst, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
+        }
+        uint32_t ethr_key = 0;
+        const bool fast = fast_threshold(g, w, row, nslots, spc, lane, ethr_key);
+        if (lane == 0) {
+            s_fast[0] = fast ? 1u : 0u;
+            s_fast[1] = ethr_key;
+        }
+    } else { // wave 0: the walk
+    bool nan_final = false;
+    uint32_t cur = 0; // staged sub-chunks passed
+    SegInfo nxt{0, 0, 8u, 0};
+    if (lane < nslots) nxt = seg[lane];
     for (uint32_t kb = 0; kb < nslots && !nan_final; kb += kWave) {
         const SegInfo mine = nxt;
         if (kb + kWave + lane < nslots) nxt = seg[kb + kWave + lane];
@@ -878,7 +920,22 @@ __global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *
             const uint32_t slot = kb + f;
             float e[kPer];
             uint32_t n;
-            load_slot(slot, e, n);
+            const uint32_t ready = __hip_atomic_load(&s_ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            while (cur < ready && s_slot[cur] < slot) ++cur;
+            if (cur < ready && s_slot[cur] == slot) { // staged by wave 1
+                uint64_t a0;
+                n = slot_range(slot, a0);
+#pragma unroll
+                for (uint32_t q = 0; q < kPer / 4; ++q) {
+                    const float4 v = s_stage[cur][q][lane];
+                    e[4 * q] = v.x;
+                    e[4 * q + 1] = v.y;
+                    e[4 * q + 2] = v.z;
+                    e[4 * q + 3] = v.w;
+                }
+            } else {
+                load_slot(slot, e, n);
+            }
             // The first elements of a row come with a binade crossing or a
             // tie every few elements (the sum is still comparable to its
             // addends), each of which would cost a round: lane 0 adds them
@@ -958,28 +1015,37 @@ __global__ __launch_bounds__(kBlock) void k_smp_div(SmpGeo g, float *logits, Smp
     __shared__ uint32_t s_fcnt, s_fbase;
     const uint32_t row = blockIdx.x / g.chunks, chunk = blockIdx.x % g.chunks;
     float *x = logits + static_cast<int64_t>(row) * g.ld;
-    for (uint32_t b = threadIdx.x; b < kBins; b += blockDim.x) s_hist[b] = 0;
-    if (threadIdx.x == 0) s_fcnt = 0;
-    __syncthreads();
     const RowSel sel = w.sel[row];
     const bool fast = sel.fast_on != 0;
+    if (!fast)
+        for (uint32_t b = threadIdx.x; b < kBins; b += blockDim.x) s_hist[b] = 0;
+    if (threadIdx.x == 0) s_fcnt = 0;
+    __syncthreads();
     const uint32_t fkey = sel.fast_key;
     // S >= 1 (the maximal element contributes expf(0) = 1) or NaN: the
     // reciprocal form is the correctly rounded quotient (div_by_recip)
     const double recip = 1.0 / static_cast<double>(sel.total);
     uint64_t c0, c1;
     chunk_range(g, chunk, c0, c1);
+    if (!fast) { // uniform
+        visit<true, 4>(g, x, c0, c1, [&](float &v, uint64_t) {
+            v = div_by_recip(v, recip);
+            atomicAdd(&s_hist[total_key(v) >> 21], 1u);
+        });
+        flush_hist(s_hist, kBins, w.hist + static_cast<uint64_t>(row) * kBins);
+        return;
+    }
+    // a fast row needs no histogram: should its list overflow, k_smp_resolve
+    // scans the row for the first digit
     visit<true, 4>(g, x, c0, c1, [&](float &v, uint64_t col) {
         v = div_by_recip(v, recip);
         const uint32_t key = total_key(v);
-        atomicAdd(&s_hist[key >> 21], 1u);
-        if (fast && key >= fkey) {
+        if (key >= fkey) {
             const uint32_t i = atomicAdd(&s_fcnt, 1u);
             if (i < kFastWg) s_fbuf[i] = cand_word(key, static_cast<uint32_t>(col));
         }
     });
-    flush_hist(s_hist, kBins, w.hist + static_cast<uint64_t>(row) * kBins); // begins with a barrier
-    if (!fast) return; // uniform
+    __syncthreads();
     const uint32_t n = s_fcnt;
     if (n == 0) return; // uniform
     if (threadIdx.x == 0) s_fbase = atomicAdd(&w.sel[row].fast_count, n <= kFastWg ? n : kCap + 1);
@@ -1103,8 +1169,16 @@ __global__ __launch_bounds__(kResolveThreads) void k_smp_resolve(SmpGeo g, float
         }
         return;
     }
-    sel = pick_digit(sel, w.hist + static_cast<uint64_t>(row) * kBins, 11, s_tmp, s_pick);
     float *x = logits + static_cast<int64_t>(row) * g.ld;
+    if (!sel.fast_on) {
+        sel = pick_digit(sel, w.hist + static_cast<uint64_t>(row) * kBins, 11, s_tmp, s_pick);
+    } else { // a fast row whose list overflowed: k_smp_div left no histogram
+        for (uint32_t b = threadIdx.x; b < kBins; b += blockDim.x) s_hist[b] = 0;
+        __syncthreads();
+        visit<false>(g, x, 0, g.card, [&](float &v, uint64_t) { atomicAdd(&s_hist[total_key(v) >> 21], 1u); });
+        __syncthreads();
+        sel = pick_digit(sel, s_hist, 11, s_tmp, s_pick);
+    }
     for (uint32_t pass = 1; pass <= 2 && sel.mode == 0; ++pass) {
         const uint32_t bits = pass == 2 ? 10u : 11u;
         const uint32_t nbins = 1u << bits;
