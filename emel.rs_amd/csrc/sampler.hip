@@ -347,44 +347,65 @@ __global__ __launch_bounds__(kBlock) void k_smp_max(SmpGeo g, float *logits, Smp
             const uint32_t k = wave + (kBlock / kWave) * j;
             load_split(g, x, c0 + static_cast<uint64_t>(k) * kSub, c1, lane, k < nsub, v[j]);
         }
-        float wm = -__builtin_inff(); // this wave's maximum
-        float mk[kFusePerWave], sk[kFusePerWave];
+        // per lane: its maximum lm over its elements of each sub-chunk and
+        // la = sum of exp(v - lm), so the exponentials need no wave
+        // reduction first; then per sub-chunk the wave maximum m_k and
+        // sum of la exp(lm - m_k), the four sub-chunks' reductions
+        // independent of one another
+        float lm[kFusePerWave], la[kFusePerWave];
 #pragma unroll
         for (uint32_t j = 0; j < kFusePerWave; ++j) {
             const uint32_t k = wave + (kBlock / kWave) * j;
-            mk[j] = -__builtin_inff();
-            sk[j] = 0.0f;
-            if (k >= nsub) continue; // wave-uniform
             const uint64_t a0 = c0 + static_cast<uint64_t>(k) * kSub;
-            float m = -__builtin_inff(), a = 0.0f;
+            lm[j] = -__builtin_inff();
+            la[j] = 0.0f;
             // only a row's last sub-chunk can end early: the others skip the
             // per-element column checks
             auto stats = [&](auto full_tag) {
                 constexpr bool kFull = decltype(full_tag)::value;
-                float lm = -__builtin_inff();
+                float m = -__builtin_inff(), a = 0.0f;
 #pragma unroll
                 for (uint32_t q = 0; q < kPer; ++q) {
                     const float t = v[j][q] * scale;
                     v[j][q] = t;
                     const bool in = kFull || split_col(a0, lane, q) < c1;
-                    lm = in && t > lm ? t : lm; // f32::max: a NaN operand is never taken
+                    m = in && t > m ? t : m; // f32::max: a NaN operand is never taken
                 }
-                m = wave_max_dpp(lm);
                 if (m > -__builtin_inff()) {
 #pragma unroll
                     for (uint32_t q = 0; q < kPer; ++q) {
                         const bool in = kFull || split_col(a0, lane, q) < c1;
-                        a += in ? approx_exp(v[j][q] - m) : 0.0f;
+                        a += in ? approx_exp(v[j][q] - m) : 0.0f; // a NaN or +inf makes it NaN
                     }
                 }
+                lm[j] = m;
+                la[j] = a;
             };
-            if (a0 + kSub <= c1) stats(std::true_type{});
-            else stats(std::false_type{});
-            // a NaN or +inf element makes the sum NaN: every prediction from it fails
-            mk[j] = m;
-            sk[j] = static_cast<float>(wave_sum_dpp(static_cast<double>(a)));
-            if (lane == 0) w.sub[static_cast<uint64_t>(blockIdx.x) * spc + k] = SubSum{m, sk[j]};
-            wm = m > wm ? m : wm;
+            if (k < nsub) { // wave-uniform
+                if (a0 + kSub <= c1) stats(std::true_type{});
+                else stats(std::false_type{});
+            }
+        }
+        float wm = -__builtin_inff(); // this wave's maximum
+        float mk[kFusePerWave], sk[kFusePerWave];
+#pragma unroll
+        for (uint32_t j = 0; j < kFusePerWave; ++j) mk[j] = wave_max_dpp(lm[j]);
+#pragma unroll
+        for (uint32_t j = 0; j < kFusePerWave; ++j) {
+            // every prediction from a NaN sum fails
+            const float t = la[j] != 0.0f ? la[j] * approx_exp(lm[j] - mk[j]) : 0.0f;
+            sk[j] = static_cast<float>(wave_sum_dpp(static_cast<double>(t)));
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < kFusePerWave; ++j) {
+            const uint32_t k = wave + (kBlock / kWave) * j;
+            if (k < nsub) {
+                if (lane == 0) w.sub[static_cast<uint64_t>(blockIdx.x) * spc + k] = SubSum{mk[j], sk[j]};
+                wm = mk[j] > wm ? mk[j] : wm;
+            } else {
+                mk[j] = -__builtin_inff();
+                sk[j] = 0.0f;
+            }
         }
         const float mc = block_max256(wm);
         double t = 0.0;
@@ -1477,16 +1498,15 @@ __device__ void lds_sort_desc(uint64_t *s, uint32_t n)
 }
 
 // Stages the words c[0, n) into sort elements [0, np) of s (np <= kCap,
-// zeros after n), all
-// of a thread's kSortPer global loads issued before its first LDS store.
-// Lanes past n read c[0] (inside the row's list) and store zero.
+// zeros after n), all of a thread's kSortPer global loads issued before its
+// first LDS store.
 __device__ __forceinline__ void stage_words(uint64_t *s, const uint64_t *c, uint32_t n, uint32_t np)
 {
     uint64_t q[kSortPer];
 #pragma unroll
     for (uint32_t r = 0; r < kSortPer; ++r) {
         const uint32_t i = threadIdx.x + r * kRankThreads;
-        q[r] = c[i < n ? i : 0];
+        q[r] = i < n ? c[i] : 0ull; // short lists (the fast path's) load only their words
     }
 #pragma unroll
     for (uint32_t r = 0; r < kSortPer; ++r) {
