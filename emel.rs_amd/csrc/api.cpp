@@ -696,6 +696,50 @@ emel_status emel_release_workspaces(void)
     return e == hipSuccess ? EMEL_OK : hip_fail(e, "hipDeviceSynchronize");
 }
 
+emel_status emel_stream_reserve(emel_stream stream, uint64_t work_bytes, uint64_t counter_bytes)
+{
+    const emel_status d = ensure_device();
+    if (d != EMEL_OK) return d;
+    emel_status s = not_capturing(as_stream(stream), "reserving a stream's scratch");
+    if (s != EMEL_OK) return s;
+    StreamLease lease;
+    s = lease.acquire(as_stream(stream));
+    if (s != EMEL_OK) return s;
+    void *p = nullptr;
+    s = lease.work(work_bytes, &p);
+    if (s != EMEL_OK) return s;
+    return lease.counters(counter_bytes, &p);
+}
+
+emel_status emel_stream_workspace(emel_stream stream, uint64_t *work_bytes, uint64_t *counter_bytes)
+{
+    if (!work_bytes || !counter_bytes) return fail(EMEL_ERR_INVALID_ARGUMENT, "null size pointer");
+    *work_bytes = 0;
+    *counter_bytes = 0;
+    int dev = 0;
+    const hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    // g_mutex, then the stream's lock: no thread takes them in the other
+    // order, and holding g_mutex keeps the state from being released
+    std::lock_guard<std::mutex> g(g_mutex);
+    const auto it = g_streams.find({dev, as_stream(stream)});
+    if (it == g_streams.end()) return EMEL_OK;
+    std::lock_guard<std::mutex> hold(it->second->lock);
+    *work_bytes = it->second->work.bytes;
+    *counter_bytes = it->second->counters.bytes;
+    return EMEL_OK;
+}
+
+emel_status emel_device_prepare(emel_stream stream)
+{
+    const emel_status d = ensure_device();
+    if (d != EMEL_OK) return d;
+    const emel_status s = not_capturing(as_stream(stream), "building the device's tables");
+    if (s != EMEL_OK) return s;
+    const hipError_t e = emel::prepare_device_tables(as_stream(stream));
+    return e == hipSuccess ? EMEL_OK : hip_fail(e, "building the device's tables");
+}
+
 emel_status emel_stream_copy(const void *src, void *dst, uint64_t bytes, uint32_t shape, emel_stream stream)
 {
     if (bytes % 16 != 0 || (reinterpret_cast<uintptr_t>(src) & 15u) != 0 || (reinterpret_cast<uintptr_t>(dst) & 15u) != 0)

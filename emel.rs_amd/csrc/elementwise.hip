@@ -745,6 +745,12 @@ __global__ __launch_bounds__(kBlock) void k_acc(const float *base, const float *
 }
 } // namespace
 
+hipError_t prepare_device_tables(hipStream_t stream)
+{
+    DeviceInfo d{};
+    return device_info(stream, true, d);
+}
+
 hipError_t launch_stream_copy(const void *src, void *dst, uint64_t bytes, CopyShape shape, hipStream_t stream)
 {
     if (bytes == 0) return hipSuccess;

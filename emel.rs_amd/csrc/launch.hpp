@@ -74,6 +74,9 @@ hipError_t launch_acc(const float *base, const float *update, float *dst, uint64
 // in flight.
 enum class CopyShape : uint32_t { Flat = 0, Wave4 = 1, Wave8 = 2, Walk = 3 };
 hipError_t launch_stream_copy(const void *src, void *dst, uint64_t bytes, CopyShape shape, hipStream_t stream);
+// Builds the current device's lookup tables (the GELU table) if not yet
+// built, and waits for them on `stream`.
+hipError_t prepare_device_tables(hipStream_t stream);
 
 // ---- row kernels (rows.hip) --------------------------------------------
 

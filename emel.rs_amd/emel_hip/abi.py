@@ -337,6 +337,9 @@ SIGNATURES = {
     "emel_stream_destroy": [_S],
     "emel_stream_synchronize": [_S],
     "emel_release_workspaces": [],
+    "emel_stream_reserve": [_S, ctypes.c_uint64, ctypes.c_uint64],
+    "emel_stream_workspace": [_S, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)],
+    "emel_device_prepare": [_S],
     "emel_stream_copy": [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32, _S],
     "emel_generic_dispatch": [ctypes.POINTER(CGenericRequest), _S],
     **{f"emel_op_get_rows{suffix}": [_V, ctypes.POINTER(CIndexView), _V, _S]
@@ -402,6 +405,24 @@ class CopyShape(enum.IntEnum):
     WAVE4 = 1
     WAVE8 = 2
     WALK = 3
+
+
+def stream_reserve(work_bytes: int, counter_bytes: int, stream: int = 0) -> Status:
+    """emel_stream_reserve: grows the scratch calls on `stream` share so later
+    calls needing no more allocate nothing (refused under capture)."""
+    return Status(load().emel_stream_reserve(ctypes.c_void_p(stream), work_bytes, counter_bytes))
+
+
+def stream_workspace(stream: int = 0) -> tuple:
+    """emel_stream_workspace: (status, work bytes, counter bytes) the stream holds now."""
+    w, c = ctypes.c_uint64(0), ctypes.c_uint64(0)
+    st = Status(load().emel_stream_workspace(ctypes.c_void_p(stream), ctypes.byref(w), ctypes.byref(c)))
+    return st, w.value, c.value
+
+
+def device_prepare(stream: int = 0) -> Status:
+    """emel_device_prepare: builds the current device's tables (GELU's) and waits."""
+    return Status(load().emel_device_prepare(ctypes.c_void_p(stream)))
 
 
 def stream_copy(src_ptr: int, dst_ptr: int, nbytes: int, shape: "CopyShape", stream: int = 0) -> Status:

@@ -136,6 +136,42 @@ impl Stream {
         // SAFETY: `raw` is live by construction.
         HipError::check(unsafe { ffi::emel_stream_synchronize(self.raw) })
     }
+
+    /// Grows the scratch that calls on this stream share to at least
+    /// `work_bytes` of workspace and `counter_bytes` of reduction counters,
+    /// so that later calls needing no more allocate nothing (for callers
+    /// that capture calls into HIP graphs).
+    ///
+    /// # Errors
+    /// `EMEL_ERR_STREAM_CAPTURE` while the stream is being captured, else
+    /// the library status of the allocation.
+    pub fn reserve(&self, work_bytes: u64, counter_bytes: u64) -> Result<(), HipError> {
+        // SAFETY: `raw` is live by construction.
+        HipError::check(unsafe { ffi::emel_stream_reserve(self.raw, work_bytes, counter_bytes) })
+    }
+
+    /// The (workspace, counter) bytes this stream's calls share now; after
+    /// one eager run of a workload, what to [`Stream::reserve`] for it.
+    ///
+    /// # Errors
+    /// The library status when the current device cannot be read.
+    pub fn workspace(&self) -> Result<(u64, u64), HipError> {
+        let (mut work, mut counters) = (0u64, 0u64);
+        // SAFETY: `raw` is live; both out pointers are valid.
+        HipError::check(unsafe { ffi::emel_stream_workspace(self.raw, &raw mut work, &raw mut counters) })?;
+        Ok((work, counters))
+    }
+
+    /// Builds the current device's lookup tables (GELU's) on this stream and
+    /// waits for them, so that no later call waits to build them.
+    ///
+    /// # Errors
+    /// `EMEL_ERR_STREAM_CAPTURE` while the stream is being captured, else
+    /// the library status of the build.
+    pub fn prepare_device(&self) -> Result<(), HipError> {
+        // SAFETY: `raw` is live by construction.
+        HipError::check(unsafe { ffi::emel_device_prepare(self.raw) })
+    }
 }
 
 impl Drop for Stream {

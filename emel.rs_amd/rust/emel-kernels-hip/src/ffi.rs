@@ -301,6 +301,9 @@ unsafe extern "C" {
     pub fn emel_stream_destroy(stream: Stream) -> Status;
     pub fn emel_stream_synchronize(stream: Stream) -> Status;
     pub fn emel_release_workspaces() -> Status;
+    pub fn emel_stream_reserve(stream: Stream, work_bytes: u64, counter_bytes: u64) -> Status;
+    pub fn emel_stream_workspace(stream: Stream, work_bytes: *mut u64, counter_bytes: *mut u64) -> Status;
+    pub fn emel_device_prepare(stream: Stream) -> Status;
     pub fn emel_stream_copy(src: *const c_void, dst: *mut c_void, bytes: u64, shape: u32, stream: Stream) -> Status;
     pub fn emel_validate_view(view: *const EmelTensorView, allow_singleton_zero_stride: i32) -> Status;
     pub fn emel_validate_normalization_view(view: *const EmelTensorView) -> Status;

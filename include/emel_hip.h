@@ -170,6 +170,24 @@ emel_status emel_stream_synchronize(emel_stream stream);
 /* Releases the per-stream reduction workspaces the library holds. */
 emel_status emel_release_workspaces(void);
 
+/* Set-up for dispatch that neither allocates nor waits, no counterpart in
+ * the reference (whose dispatch never allocates): for callers that capture
+ * calls into HIP graphs or run tight serving loops.
+ *   emel_stream_reserve grows the scratch that calls on `stream` share (on
+ *   the current device) to at least `work_bytes` of workspace and
+ *   `counter_bytes` of zeroed reduction counters.  Later calls on the stream
+ *   that need no more allocate nothing.  It allocates, and zeroes the
+ *   counters on the stream, so it is refused under capture
+ *   (EMEL_ERR_STREAM_CAPTURE).
+ *   emel_stream_workspace reports the sizes the stream holds now: after one
+ *   eager run of a workload they are what that workload needs, for
+ *   emel_stream_reserve in a later process.
+ *   emel_device_prepare builds the current device's lookup tables (GELU's)
+ *   and waits for them, so no later call waits to build them. */
+emel_status emel_stream_reserve(emel_stream stream, uint64_t work_bytes, uint64_t counter_bytes);
+emel_status emel_stream_workspace(emel_stream stream, uint64_t *work_bytes, uint64_t *counter_bytes);
+emel_status emel_device_prepare(emel_stream stream);
+
 /* Measurement reference, no counterpart in the reference: a bit copy of
  * `bytes` device bytes (a multiple of 16, both pointers 16-byte aligned)
  * with one of the streaming shapes the dense kernels use, so a caller can

@@ -125,3 +125,27 @@ def test_refusals_under_capture_in_a_fresh_process(gpu):
     assert out["argmax_no_alloc_matches"] and out["argmax_no_alloc_replay2"], out
     for key in ("gelu_eager", "sum_eager", "l2_norm_eager", "get_rows_eager"):
         assert out[key] == int(eh.Status.OK), (key, out)
+
+
+RESERVE_CHILD = Path(__file__).resolve().parent / "reserve_capture_child.py"
+
+
+def test_reserved_scratch_and_prepared_tables_allow_capture(gpu):
+    """emel_stream_reserve and emel_device_prepare, in a fresh process: the
+    first GELU and the first split reductions on the stream are captured
+    (without them they are refused, as the test above shows), replays equal
+    eager calls, and the reserved sizes are what the stream holds."""
+    print("child:", RESERVE_CHILD.name, flush=True)
+    r = subprocess.run([sys.executable, str(RESERVE_CHILD)], capture_output=True, text=True, timeout=180)
+    assert r.returncode == 0, r.stderr[-3000:]
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    ok, cap = int(eh.Status.OK), int(eh.Status.STREAM_CAPTURE)
+    assert out["workspace_before"] == [ok, 0, 0], out
+    assert out["prepare"] == ok and out["reserve"] == ok, out
+    st, work, counters = out["workspace_after"]
+    assert st == ok and work >= 4 << 20 and counters >= 1 << 20, out
+    assert out["captured"] == [ok, ok, ok], out
+    assert out["reserve_under_capture"] == cap, out
+    assert out["eager"] == [ok, ok, ok], out
+    assert all(out["replay_matches"].values()) and all(out["replay2_matches"].values()), out
+    assert out["workspace_end"] == out["workspace_after"], out

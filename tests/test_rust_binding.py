@@ -42,6 +42,7 @@ C_TO_RUST = {
     "const int32_t *": "*const i32",
     "int32_t *": "*mut i32",
     "uint32_t *": "*mut u32",
+    "uint64_t *": "*mut u64",
     "const char *": "*const c_char",
     "uint8_t": "u8",
     "uint32_t": "u32",
