@@ -1339,11 +1339,27 @@ struct SmpStates {
     uint32_t v[kStatesInline]; // start states of rows [row0, row0 + kStatesInline)
 };
 
+// Synchronises the T threads that run a ranking step: the whole workgroup
+// (T == kRankThreads), or wave 0 alone (T == kWave; the other waves have
+// left), whose LDS writes a fence and a wave barrier order.
+template <uint32_t T>
+__device__ __forceinline__ void group_sync()
+{
+    if constexpr (T == kWave) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    } else {
+        __syncthreads();
+    }
+}
+
 // Race selection over the ranked slots j < top_k (sampler/sm.rs:821-847):
 // slot j draws state_j = s0 * 16807^(j+1) mod (2^31 - 1), u_j = state_j as
 // f32 / 2^31 (2147483647 as f32 is 2^31), race_j = p_j / -ln(u_j); the
 // first slot with the greatest race (strict >, starting from -inf) wins.
-template <class P, class I>
+// T threads take part (see group_sync).
+template <uint32_t T, class P, class I>
 __device__ void select_slots(const SmpGeo &g, uint32_t row, uint32_t s0, P prob, I index, const SmpOut &o)
 {
     __shared__ float s_v[kRankThreads / kWave];
@@ -1353,11 +1369,11 @@ __device__ void select_slots(const SmpGeo &g, uint32_t row, uint32_t s0, P prob,
         s_invc[threadIdx.x] = kLogfInvc[threadIdx.x];
         s_logc[threadIdx.x] = kLogfLogc[threadIdx.x];
     }
-    __syncthreads();
+    group_sync<T>();
     float best = -__builtin_inff();
     uint32_t bslot = kNone;
-    uint32_t pw = kPmPowers.v[threadIdx.x]; // launched with kRankThreads threads
-    for (uint32_t j = threadIdx.x; j < g.top_k; j += kRankThreads) {
+    uint32_t pw = kPmPowers.v[threadIdx.x]; // 16807^(t+1); slot t + m T multiplies by (16807^T)^m
+    for (uint32_t j = threadIdx.x; j < g.top_k; j += T) {
         const uint32_t state = mulmod(s0, pw);
         const float uniform = static_cast<float>(state) * 0x1p-31f;
         const float race = prob(j) / -emel_logf(uniform, s_invc, s_logc);
@@ -1365,7 +1381,7 @@ __device__ void select_slots(const SmpGeo &g, uint32_t row, uint32_t s0, P prob,
             best = race;
             bslot = j;
         }
-        pw = mulmod(pw, kPmStride);
+        pw = mulmod(pw, kPmPowers.v[T - 1]);
     }
 #pragma unroll
     for (int off = kWave / 2; off > 0; off >>= 1) {
@@ -1376,13 +1392,15 @@ __device__ void select_slots(const SmpGeo &g, uint32_t row, uint32_t s0, P prob,
             bslot = oi;
         }
     }
-    if (threadIdx.x % kWave == 0) {
-        s_v[threadIdx.x / kWave] = best;
-        s_i[threadIdx.x / kWave] = bslot;
+    if constexpr (T > kWave) {
+        if (threadIdx.x % kWave == 0) {
+            s_v[threadIdx.x / kWave] = best;
+            s_i[threadIdx.x / kWave] = bslot;
+        }
+        __syncthreads();
     }
-    __syncthreads();
     if (threadIdx.x != 0) return;
-    for (uint32_t v = 1; v < blockDim.x / kWave; ++v) {
+    for (uint32_t v = 1; v < T / kWave; ++v) {
         const float ov = s_v[v];
         const uint32_t oi = s_i[v];
         if (oi != kNone && (bslot == kNone || ov > best || (ov == best && oi < bslot))) {
@@ -1445,6 +1463,7 @@ __device__ __forceinline__ void sort_regs_desc(uint64_t (&v)[kSortPer])
     }
 }
 
+template <uint32_t T>
 __device__ void lds_sort_desc(uint64_t *s, uint32_t n)
 {
     const uint32_t t = threadIdx.x;
@@ -1460,7 +1479,7 @@ __device__ void lds_sort_desc(uint64_t *s, uint32_t n)
 #pragma unroll
             for (uint32_t r = 0; r < kSortPer; ++r) s[slot(t * kSortPer + r)] = v[r];
         }
-        __syncthreads();
+        group_sync<T>();
         if (act) {
             const uint32_t per_pair = 2 * len / kSortPer; // threads per merged run
             const uint32_t a0 = (t / per_pair) * 2 * len, b0 = a0 + len; // the two runs
@@ -1488,32 +1507,33 @@ __device__ void lds_sort_desc(uint64_t *s, uint32_t n)
                 b = j < len ? nb : 0ull;
             }
         }
-        __syncthreads(); // every read of this round precedes the next writes
+        group_sync<T>(); // every read of this round precedes the next writes
     }
     if (act) {
 #pragma unroll
         for (uint32_t r = 0; r < kSortPer; ++r) s[slot(t * kSortPer + r)] = v[r];
     }
-    __syncthreads();
+    group_sync<T>();
 }
 
 // Stages the words c[0, n) into sort elements [0, np) of s (np <= kCap,
 // zeros after n), all of a thread's kSortPer global loads issued before its
 // first LDS store.
+template <uint32_t T>
 __device__ __forceinline__ void stage_words(uint64_t *s, const uint64_t *c, uint32_t n, uint32_t np)
 {
     uint64_t q[kSortPer];
 #pragma unroll
     for (uint32_t r = 0; r < kSortPer; ++r) {
-        const uint32_t i = threadIdx.x + r * kRankThreads;
+        const uint32_t i = threadIdx.x + r * T;
         q[r] = i < n ? c[i] : 0ull; // short lists (the fast path's) load only their words
     }
 #pragma unroll
     for (uint32_t r = 0; r < kSortPer; ++r) {
-        const uint32_t i = threadIdx.x + r * kRankThreads;
+        const uint32_t i = threadIdx.x + r * T;
         if (i < np) s[slot(i)] = i < n ? q[r] : 0ull;
     }
-    __syncthreads();
+    group_sync<T>();
 }
 
 // Candidate lists of at most kCap: one workgroup sorts a row in LDS.
@@ -1525,10 +1545,21 @@ __global__ __launch_bounds__(kRankThreads) void k_smp_rank(SmpGeo g, SmpWs w, Sm
     const uint32_t n = count < kCap ? count : kCap;
     uint32_t np = kSortPer;
     while (np < n || np < g.top_k) np <<= 1;
-    stage_words(s_c, w.cand + static_cast<uint64_t>(row) * g.cand_ld, n, np);
-    lds_sort_desc(s_c, np);
+    const uint64_t *list = w.cand + static_cast<uint64_t>(row) * g.cand_ld;
+    if (np <= kWave * kSortPer && g.top_k <= kWave) { // uniform: a short list (the fast path's) by wave 0 alone
+        if (threadIdx.x >= kWave) return;
+        stage_words<kWave>(s_c, list, n, np);
+        lds_sort_desc<kWave>(s_c, np);
+        if (threadIdx.x < g.top_k) write_ranked(g, o, row, threadIdx.x, s_c[slot(threadIdx.x)]);
+        select_slots<kWave>(
+            g, row, st.v[blockIdx.x], [&](uint32_t j) { return from_key(static_cast<uint32_t>(s_c[slot(j)] >> 32)); },
+            [&](uint32_t j) { return static_cast<int32_t>(~static_cast<uint32_t>(s_c[slot(j)])); }, o);
+        return;
+    }
+    stage_words<kRankThreads>(s_c, list, n, np);
+    lds_sort_desc<kRankThreads>(s_c, np);
     for (uint32_t j = threadIdx.x; j < g.top_k; j += blockDim.x) write_ranked(g, o, row, j, s_c[slot(j)]);
-    select_slots(
+    select_slots<kRankThreads>(
         g, row, st.v[blockIdx.x], [&](uint32_t j) { return from_key(static_cast<uint32_t>(s_c[slot(j)] >> 32)); },
         [&](uint32_t j) { return static_cast<int32_t>(~static_cast<uint32_t>(s_c[slot(j)])); }, o);
 }
@@ -1545,8 +1576,8 @@ __global__ __launch_bounds__(kRankThreads) void k_smp_tile_sort(SmpGeo g, SmpWs 
     uint32_t np = kSortPer;
     while (np < len) np <<= 1;
     uint64_t *c = w.cand + static_cast<uint64_t>(row) * g.cand_ld + b0;
-    stage_words(s_c, c, len, np);
-    lds_sort_desc(s_c, np);
+    stage_words<kRankThreads>(s_c, c, len, np);
+    lds_sort_desc<kRankThreads>(s_c, np);
     for (uint32_t i = threadIdx.x; i < len; i += blockDim.x) c[i] = s_c[slot(i)];
 }
 
@@ -1602,7 +1633,7 @@ __global__ __launch_bounds__(kRankThreads) void k_smp_finish(SmpGeo g, const uin
             if (j < g.top_k) write_ranked(g, o, row, j, q[r]);
         }
     }
-    select_slots(
+    select_slots<kRankThreads>(
         g, row, st.v[blockIdx.x], [&](uint32_t j) { return from_key(static_cast<uint32_t>(c[j] >> 32)); },
         [&](uint32_t j) { return static_cast<int32_t>(~static_cast<uint32_t>(c[j])); }, o);
 }
