@@ -141,6 +141,19 @@ static int check_gpu(void)
 
     STATUS(emel_set_device(0), EMEL_OK);
     STATUS(emel_stream_create(&stream), EMEL_OK);
+    {   /* scratch reserved and tables built up front (no counterpart in the reference) */
+        uint64_t work = 1, counters = 1;
+        STATUS(emel_stream_workspace(stream, &work, &counters), EMEL_OK);
+        CHECK(work == 0 && counters == 0, "fresh stream holds %llu / %llu bytes", (unsigned long long)work,
+              (unsigned long long)counters);
+        STATUS(emel_stream_reserve(stream, 3u << 20, 1u << 20), EMEL_OK);
+        STATUS(emel_stream_workspace(stream, &work, &counters), EMEL_OK);
+        CHECK(work >= (3u << 20) && counters >= (1u << 20), "reserved %llu / %llu bytes", (unsigned long long)work,
+              (unsigned long long)counters);
+        STATUS(emel_stream_workspace(stream, NULL, &counters), EMEL_ERR_INVALID_ARGUMENT);
+        STATUS(emel_device_prepare(stream), EMEL_OK);
+        printf("stream_reserve / device_prepare: ok\n");
+    }
     STATUS(emel_malloc(&dx, n * 4), EMEL_OK);
     STATUS(emel_malloc(&dy, n * 4), EMEL_OK);
     STATUS(emel_malloc(&drow, NE0 * 4), EMEL_OK);

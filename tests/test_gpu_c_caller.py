@@ -1,7 +1,8 @@
 """GPU: the plain-C caller (tests/native/c_caller.c, built by
 __graft_entry__.build()) drives the C ABI on device 0 with no Python in
 the loop: library-allocated device buffers, broadcast add, scaled + masked
-soft_max, per-row argmax, the logits validator and the sampler, each
+soft_max, per-row argmax, the logits validator and the sampler (after
+reserving the stream's scratch and building the device tables), each
 checked inside the program."""
 import subprocess
 from pathlib import Path
