@@ -630,6 +630,43 @@ def profile_launches(host, stream, names, count):
             print(f"profile: {n} x{count}", flush=True)
 
 
+def profile_sampler(host, stream, count):
+    """Eager sampler calls for counter collection: each SAMPLER_CASES case
+    `count` times over config 5's logits, a fresh copy per call."""
+    import ctypes
+
+    import torch
+
+    from emel_hip.abi import CSampleRows
+
+    suite = GpuSuite(host, stream, [])
+    eh = suite.eh
+    lib = eh.load()
+    g = rng(31)
+    card, rows = SAMPLER_VOCAB, SAMPLER_ROWS
+    pristine = torch.from_numpy(g.standard_normal((rows, card), dtype=np.float64).astype(np.float32).reshape(-1)).to(
+        "cuda:0")
+    with torch.cuda.stream(stream):
+        for temperature, top_k in SAMPLER_CASES:
+            buf = pristine.clone()
+            srt = torch.empty(rows * card, dtype=torch.int32, device="cuda:0")
+            tp = torch.empty(rows * top_k, device="cuda:0")
+            ti = torch.empty(rows * top_k, dtype=torch.int32, device="cuda:0")
+            sel = torch.empty(rows, dtype=torch.int32, device="cuda:0")
+            sc = torch.empty(rows, device="cuda:0")
+            states = np.array(g.integers(1, 2147483647, rows), np.uint32)
+            cr = CSampleRows(rows, card, card, top_k)
+            req = eh.SampleTemperatureTopK(card, temperature, top_k, buf, srt, tp, ti, states, sel, sc).c()
+            for _ in range(count):
+                buf.copy_(pristine)
+                st = lib.emel_sample_temperature_top_k_rows(ctypes.byref(req), ctypes.byref(cr),
+                                                            ctypes.c_void_p(stream.cuda_stream))
+                if st != 0:
+                    raise RuntimeError(f"sampler: {eh.Status(st).name}: {eh.last_error()}")
+            stream.synchronize()
+            print(f"profile: sampler t{temperature} k{top_k} x{count}", flush=True)
+
+
 def launch_floor(suite, capture, timed, reps=200):
     """Per-launch time of back-to-back dependent launches that do almost no
     work (OpScale over one float4), replayed from a graph: the fixed cost
@@ -679,7 +716,8 @@ def main():
     ap.add_argument("--no-sampler", action="store_true", help="skip the emel-logits sampler")
     ap.add_argument("--launches", type=int, default=0,
                     help="profiling mode: launch every selected op and the 256 MiB calibration copy this many times "
-                         "(eagerly, cycling buffer sets), then exit without timing; for rocprofv3 --pmc runs")
+                         "(eagerly, cycling buffer sets), and each sampler case as often (unless --no-sampler or "
+                         "--ops), then exit without timing; for rocprofv3 --pmc runs")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -703,6 +741,8 @@ def main():
     stream = torch.cuda.Stream()
     if args.launches > 0:
         profile_launches(host, stream, names + extra + ["copy"], args.launches)
+        if not args.no_sampler and not args.ops:
+            profile_sampler(host, stream, args.launches)
         return
     suite = GpuSuite(host, stream, names + extra)
 

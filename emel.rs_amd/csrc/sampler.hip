@@ -278,9 +278,24 @@ __device__ __forceinline__ uint64_t split_col(uint64_t a0, uint32_t lane, uint32
 
 // Lane `lane`'s elements of the sub-chunk at a0 (zeros past c1, or everywhere
 // when !valid).
+// WHOLE: test a whole sub-chunk once (wave-uniform) before the per-float4
+// tests.
+template <bool WHOLE = false>
 __device__ __forceinline__ void load_split(const SmpGeo &g, const float *x, uint64_t a0, uint64_t c1, uint32_t lane,
                                            bool valid, float (&v)[kPer])
 {
+    if (WHOLE && valid && g.vec && a0 + kSub <= c1) { // uniform: a whole sub-chunk of an aligned row
+#pragma unroll
+        for (uint32_t h = 0; h < kSplit; ++h) {
+            // plain loads: later passes re-read these lines from cache
+            const float4 t = *reinterpret_cast<const float4 *>(x + split_col(a0, lane, 4 * h));
+            v[4 * h] = t.x;
+            v[4 * h + 1] = t.y;
+            v[4 * h + 2] = t.z;
+            v[4 * h + 3] = t.w;
+        }
+        return;
+    }
 #pragma unroll
     for (uint32_t h = 0; h < kSplit; ++h) {
         const uint64_t col = split_col(a0, lane, 4 * h);
@@ -345,7 +360,7 @@ __global__ __launch_bounds__(kBlock) void k_smp_max(SmpGeo g, float *logits, Smp
 #pragma unroll
         for (uint32_t j = 0; j < kFusePerWave; ++j) {
             const uint32_t k = wave + (kBlock / kWave) * j;
-            load_split(g, x, c0 + static_cast<uint64_t>(k) * kSub, c1, lane, k < nsub, v[j]);
+            load_split<true>(g, x, c0 + static_cast<uint64_t>(k) * kSub, c1, lane, k < nsub, v[j]);
         }
         // per lane: its maximum lm over its elements of each sub-chunk and
         // la = sum of exp(v - lm), so the exponentials need no wave
@@ -389,12 +404,16 @@ __global__ __launch_bounds__(kBlock) void k_smp_max(SmpGeo g, float *logits, Smp
         float wm = -__builtin_inff(); // this wave's maximum
         float mk[kFusePerWave], sk[kFusePerWave];
 #pragma unroll
-        for (uint32_t j = 0; j < kFusePerWave; ++j) mk[j] = wave_max_dpp(lm[j]);
+        for (uint32_t j = 0; j < kFusePerWave; ++j)
+            mk[j] = wave + (kBlock / kWave) * j < nsub ? wave_max_dpp(lm[j]) : -__builtin_inff(); // uniform
 #pragma unroll
         for (uint32_t j = 0; j < kFusePerWave; ++j) {
-            // every prediction from a NaN sum fails
-            const float t = la[j] != 0.0f ? la[j] * approx_exp(lm[j] - mk[j]) : 0.0f;
-            sk[j] = static_cast<float>(wave_sum_dpp(static_cast<double>(t)));
+            sk[j] = 0.0f;
+            if (wave + (kBlock / kWave) * j < nsub) { // uniform
+                // every prediction from a NaN sum fails
+                const float t = la[j] != 0.0f ? la[j] * approx_exp(lm[j] - mk[j]) : 0.0f;
+                sk[j] = wave_sum_dpp(t); // f32 tree: within 6 2^-24, far inside kApproxRel
+            }
         }
 #pragma unroll
         for (uint32_t j = 0; j < kFusePerWave; ++j) {
@@ -633,7 +652,9 @@ __global__ __launch_bounds__(kBlock) void k_smp_seg(SmpGeo g, float *logits, Smp
 // exponential is within (1 + |x|) 2^-23 of exp(x) and the exact e within
 // (1 + |x|) 2^-24 of exp(v - m) (x = v - the maximum it is taken from, so
 // |x| grows only as e shrinks); weighted by size, a sum of N terms is then
-// within (2 + ln N) 2^-23, about 2^-19 for a 151,936-token row.
+// within (2 + ln N) 2^-23, about 2^-19 for a 151,936-token row.  The f32
+// sums inside a sub-chunk (8 terms per lane, then a six-level wave tree) and
+// the f32 stores add at most 15 2^-24 more.
 constexpr double kApproxRel = 0x1p-14;
 
 __device__ __forceinline__ double readlane_f64(double v, uint32_t l)
