@@ -512,51 +512,64 @@ __device__ __forceinline__ SegInfo predict_sub(const float (&e)[kPer], double lo
     // normal f32 range, both bounds in one binade [2^(elo-1), 2^elo)
     if (!(lo >= 0x1p-126 && hi < 0x1p127 && lo <= hi && elo == ehi)) return info;
     const int32_t u = elo - 1 - 23;
-    uint32_t gs[H], ties = 0, tq = 0, tbefore = 0, th = 0;
+    // Units of 2^u (seq_units): t = e / 2^u, floor(t) plus one when the
+    // fraction is above 1/2; a tie (fraction exactly 1/2) counts its lower
+    // neighbour here and sets its bit in tmask.
+    auto units = [&](float x, uint32_t &q, float &f) {
+        float t = __builtin_ldexpf(x, -u);
+        t = __builtin_fminf(t, 16777216.0f); // IEEE minNum: also NaN -> 2^24
+        f = __builtin_amdgcn_fractf(t);      // t - floor(t), exact for 0 <= t <= 2^24
+        q = static_cast<uint32_t>(t);        // floor for t >= 0
+    };
+    uint32_t gs[H], tmask = 0; // per group at most 8 (2^24 + 1) units: no overflow
 #pragma unroll
     for (uint32_t h = 0; h < H; ++h) {
         gs[h] = 0;
 #pragma unroll
         for (uint32_t i = 0; i < G; ++i) {
-            const float x = e[h * G + i];
-            bool tie;
-            const uint32_t r = seq_units(x, u, tie);
-            // a tie counts its lower neighbour q here (r is q or q + 1)
-            const uint32_t q = tie ? static_cast<uint32_t>(__builtin_floorf(__builtin_ldexpf(x, -u))) : r;
-            if (tie && ties == 0) {
-                tq = q;
-                tbefore = gs[h];
-                th = h;
-            }
-            ties += tie ? 1u : 0u;
-            gs[h] += q;
-            gs[h] = gs[h] < (1u << 25) ? gs[h] : (1u << 25);
+            uint32_t q;
+            float f;
+            units(e[h * G + i], q, f);
+            gs[h] += q + (f > 0.5f ? 1u : 0u);
+            tmask |= static_cast<uint32_t>(f == 0.5f) << (h * G + i);
         }
     }
-    uint32_t incl[H], total = 0, mine_excl = 0, offs = 0, tie_offs = 0;
+    uint32_t incl[H], total = 0;
 #pragma unroll
     for (uint32_t h = 0; h < H; ++h) {
-        const uint32_t c = gs[h] < kSeqLimit ? gs[h] : kSeqLimit;
-        incl[h] = wave_incl_scan(c);
-        if (th == h) {
-            mine_excl = incl[h] - c; // units of this group in the lanes before
-            tie_offs = offs;         // units of the groups before
-        }
-        offs += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl[h]), kWave - 1));
+        incl[h] = wave_incl_scan(gs[h] < kSeqLimit ? gs[h] : kSeqLimit);
+        total += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl[h]), kWave - 1));
     }
-    total = offs;
-    const uint64_t tmask = __ballot(ties != 0);
+    const uint32_t lane_ties = static_cast<uint32_t>(__builtin_popcount(tmask));
+    const uint64_t tl_mask = __ballot(tmask != 0u);
     uint32_t nties = 0;
-    for (uint64_t m = tmask; m; m &= m - 1) {
-        nties += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(ties), __builtin_ctzll(m)));
-    }
+    for (uint64_t m = tl_mask; m; m &= m - 1)
+        nties += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(lane_ties), __builtin_ctzll(m)));
     info.units = total;
     info.u = u;
     if (nties == 0) {
         info.flags = 1u;
-    } else if (nties == 1) {
-        const int tl = __builtin_ctzll(tmask);
-        const uint32_t before = tie_offs + mine_excl + tbefore; // units before the tie element
+    } else if (nties == 1) { // uniform; the tie sits in lane tl, element ti of group th
+        const int tl = __builtin_ctzll(tl_mask);
+        const uint32_t ti = tmask ? static_cast<uint32_t>(__builtin_ctz(tmask)) : 0u;
+        const uint32_t th = ti / G;
+        // units before the tie: the groups before th, this group's lanes
+        // before tl, then this lane's elements of group th before ti
+        uint32_t before = 0, tq = 0;
+#pragma unroll
+        for (uint32_t h = 0; h < H; ++h) {
+            const uint32_t tot_h = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl[h]), kWave - 1));
+            const uint32_t excl_h = incl[h] - (gs[h] < kSeqLimit ? gs[h] : kSeqLimit);
+            before += h < th ? tot_h : (h == th ? excl_h : 0u);
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < kPer; ++i) {
+            uint32_t q;
+            float f;
+            units(e[i], q, f);
+            if (i / G == th && i < ti) before += q + (f > 0.5f ? 1u : 0u);
+            if (i == ti) tq = q;
+        }
         const uint32_t par = (before + tq) & 1u;
         info.flags = 1u | 2u | (static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(par), tl)) << 2);
     }
