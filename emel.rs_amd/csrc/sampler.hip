@@ -457,6 +457,9 @@ __global__ __launch_bounds__(kBlock) void k_smp_exp(SmpGeo g, float *logits, Smp
 {
     const uint32_t row = blockIdx.x / g.chunks, chunk = blockIdx.x % g.chunks;
     float *x = logits + static_cast<int64_t>(row) * g.ld;
+    // expf's 2^(i/32) table in LDS, ordered by row_max's barrier
+    __shared__ uint64_t s_tab[32];
+    if (threadIdx.x < 32) s_tab[threadIdx.x] = kExp2Table[threadIdx.x];
     const float m = row_max(g, w, row);
     uint64_t c0, c1;
     chunk_range(g, chunk, c0, c1);
@@ -467,7 +470,7 @@ __global__ __launch_bounds__(kBlock) void k_smp_exp(SmpGeo g, float *logits, Smp
     // at full occupancy
     visit<true, 4>(g, x, c0, c1, [&](float &v, uint64_t) {
         const float s = v * scale;
-        v = emel_expf(s - m, kExp2Table, ec);
+        v = emel_expf(s - m, s_tab, ec);
         acc += static_cast<double>(v);
     });
     // f64 chunk sum: only a prediction of where the exact sum's binades
@@ -717,6 +720,13 @@ __global__ __launch_bounds__(kBlock) void k_smp_expseg(SmpGeo g, float *logits, 
     for (uint32_t k = nsub + threadIdx.x; k < spc; k += blockDim.x) out[k] = SegInfo{0, 0, 8u, 0};
     const float scale = g.scale;
     const ExpfConsts ec = expf_consts_in_vgprs();
+    // each wave's own copy of expf's 2^(i/32) table in LDS: no workgroup barrier
+    __shared__ uint64_t s_tab[kBlock / kWave][32];
+    if (lane < 32) s_tab[wave][lane] = kExp2Table[lane];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    const uint64_t *tab = s_tab[wave];
 #pragma unroll
     for (uint32_t j = 0; j < kFusePerWave; ++j) {
         const uint32_t k = wave + (kBlock / kWave) * j;
@@ -727,11 +737,11 @@ __global__ __launch_bounds__(kBlock) void k_smp_expseg(SmpGeo g, float *logits, 
         const uint64_t a0 = sub_col(k);
         if (a0 + kSub <= c1) { // only a row's last sub-chunk can end early
 #pragma unroll
-            for (uint32_t q = 0; q < kPer; ++q) cur[q] = emel_expf(cur[q] * scale - m, kExp2Table, ec);
+            for (uint32_t q = 0; q < kPer; ++q) cur[q] = emel_expf(cur[q] * scale - m, tab, ec);
         } else {
 #pragma unroll
             for (uint32_t q = 0; q < kPer; ++q)
-                cur[q] = split_col(a0, lane, q) < c1 ? emel_expf(cur[q] * scale - m, kExp2Table, ec) : 0.0f;
+                cur[q] = split_col(a0, lane, q) < c1 ? emel_expf(cur[q] * scale - m, tab, ec) : 0.0f;
         }
 #pragma unroll
         for (uint32_t h = 0; h < kSplit; ++h) {
