@@ -109,12 +109,19 @@ struct SmpGeo {
 constexpr uint32_t kSub = 512;   // elements per sub-chunk (one walk round)
 constexpr uint32_t kPer = kSub / kWave; // elements per lane of a sub-chunk
 constexpr uint32_t kMaxSub = 64; // sub-chunks a chunk predicts; later ones are walked
+// When the sub-chunk's bounds span two binades, it is counted at both: u for
+// the lower one and u + 1 for the upper one (units1 and flag bits 4-6); the
+// walk takes the count of whichever binade its exact state is in.
 struct SegInfo {
-    uint32_t units; // saturates at 2^25: the walk rejects anything >= 2^24
+    uint32_t units;  // at 2^u; large counts saturate: the walk rejects anything >= 2^24
     int32_t u;
-    uint32_t flags; // bit 0 ok, bit 1 one tie, bit 2 its parity, bit 3 empty slot
-    uint32_t pad;
+    uint32_t flags;  // bit 0 ok at 2^u, bit 1 one tie, bit 2 its parity, bit 3 empty slot,
+                     // bits 4-6 the same at 2^(u+1), bit 7 likely walked (stage it)
+    uint32_t units1; // at 2^(u+1), when bit 4 is set
 };
+constexpr uint32_t kSegEmpty = 8u;
+constexpr uint32_t kSegUpper = 4u;     // shift of the 2^(u+1) bits
+constexpr uint32_t kSegWalk = 0x80u;
 // Chunks of at most kFuseSubs sub-chunks (kFuseCols columns) take the fused
 // path: k_smp_max<true> also leaves an approximate sum of exp(v - m_k) per
 // sub-chunk (m_k its maximum), and k_smp_expseg writes e and predicts each
@@ -489,32 +496,26 @@ __global__ __launch_bounds__(kBlock) void k_smp_exp(SmpGeo g, float *logits, Smp
 // step rounds by at most 2^-24 of the running sum, which never decreases,
 // so the true value lies within P (1 +- (c0 2^-24 + 2^-30)) -- and likewise
 // at the chunk's end.  When both bounds share one binade, the chunk adds a
-// whole number of units of that binade; this kernel counts them.  The walk
-// (k_smp_sum) takes the count only after checking, on the exact state, that
-// the binade is the predicted one and that the units fit below 2^24: the
-// bound steers the work, the checks decide correctness.
+// whole number of units of that binade; when they span two, it adds a whole
+// number of units of either, unless it crosses from one into the other.
+// This kernel counts them.  The walk (k_smp_sum) takes a count only after
+// checking, on the exact state, that its binade is the state's and that
+// the units fit below 2^24: the bound steers the work, the checks decide
+// correctness.
 
 
-// The prediction of one sub-chunk whose exact running sum before and after
-// lies in [lo, hi]: when both bounds share one normal f32 binade
-// [2^(b-1), 2^b), the sub-chunk's units of 2^(b-24), at most one tie and
-// that tie's parity; otherwise not usable (flags 0).  Lane l holds kPer of
-// its elements (zeros past its end) in H groups of kPer / H consecutive
-// ones, group h starting at element h kSub / H + l kPer / H: H = 1 is eight
-// consecutive elements per lane, H = 2 two float4 of a wave-contiguous
-// layout.  Called by a whole wave; the result is the same in every lane.
+// A sub-chunk's units of 2^u (seq_units) and its tie flags (bits 0-2 of
+// SegInfo::flags: ok when it holds at most one tie, that tie, its parity).
+// Lane l holds kPer of its elements (zeros past its end) in H groups of
+// kPer / H consecutive ones, group h starting at element h kSub / H + l kPer
+// / H: H = 1 is eight consecutive elements per lane, H = 2 two float4 of a
+// wave-contiguous layout.  Called by a whole wave; the result is the same in
+// every lane.
 template <uint32_t H>
-__device__ __forceinline__ SegInfo predict_sub(const float (&e)[kPer], double lo, double hi)
+__device__ __forceinline__ void count_units(const float (&e)[kPer], int32_t u, uint32_t &units_out, uint32_t &flags_out)
 {
     constexpr uint32_t G = kPer / H;
     static_assert(G * H == kPer, "groups split a lane's elements evenly");
-    SegInfo info{0, 0, 0, 0};
-    int elo = 0, ehi = 0;
-    (void)__builtin_frexp(lo, &elo);
-    (void)__builtin_frexp(hi, &ehi);
-    // normal f32 range, both bounds in one binade [2^(elo-1), 2^elo)
-    if (!(lo >= 0x1p-126 && hi < 0x1p127 && lo <= hi && elo == ehi)) return info;
-    const int32_t u = elo - 1 - 23;
     // Units of 2^u (seq_units): t = e / 2^u, floor(t) plus one when the
     // fraction is above 1/2; a tie (fraction exactly 1/2) counts its lower
     // neighbour here and sets its bit in tmask.
@@ -548,10 +549,10 @@ __device__ __forceinline__ SegInfo predict_sub(const float (&e)[kPer], double lo
     uint32_t nties = 0;
     for (uint64_t m = tl_mask; m; m &= m - 1)
         nties += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(lane_ties), __builtin_ctzll(m)));
-    info.units = total;
-    info.u = u;
+    units_out = total;
+    flags_out = 0u;
     if (nties == 0) {
-        info.flags = 1u;
+        flags_out = 1u;
     } else if (nties == 1) { // uniform; the tie sits in lane tl, element ti of group th
         const int tl = __builtin_ctzll(tl_mask);
         const uint32_t ti = tmask ? static_cast<uint32_t>(__builtin_ctz(tmask)) : 0u;
@@ -574,8 +575,64 @@ __device__ __forceinline__ SegInfo predict_sub(const float (&e)[kPer], double lo
             if (i == ti) tq = q;
         }
         const uint32_t par = (before + tq) & 1u;
-        info.flags = 1u | 2u | (static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(par), tl)) << 2);
+        flags_out = 1u | 2u | (static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(par), tl)) << 2);
     }
+}
+
+// A steering margin, not a bound: how far predictions assume the running f32
+// sum after `a` roundings strays from the exact prefix, relatively.  Each
+// rounding moves it by at most 2^-24 of itself, either way; without a bias in
+// the rounding direction the moves mostly cancel, and their total stays near
+// sqrt(a) 2^-24 (seq_rel_bound is the worst case, a 2^-24).  A sub-chunk whose
+// range under this margin spans a binade boundary probably crosses it.
+__device__ __forceinline__ double steer_margin(double a)
+{
+    return 8.0 * __builtin_sqrt(a) * 0x1p-24;
+}
+
+// The plan of one sub-chunk's prediction, packed in 32 bits: its exact
+// running sum before and after lies in [lo, hi] (the rounding bound), and
+// probably in [wlo, whi] (the steering margin).  When both bounds lie in
+// normal f32 binades, one or two adjacent ones, it is counted at the lower
+// binade [2^(b-1), 2^b) (u = b - 24) and, for two, at the upper one: bits
+// 0-1 hold the number of binades (0: not usable), bit 2 is set when
+// [wlo, whi] spans a binade boundary (the sub-chunk probably crosses it and
+// is walked), bits 8-31 hold u + kPlanBias.
+constexpr int32_t kPlanBias = 512;
+__device__ __forceinline__ uint32_t plan_sub(double lo, double hi, double wlo, double whi)
+{
+    int elo = 0, ehi = 0, wl = 0, wh = 0;
+    (void)__builtin_frexp(lo, &elo);
+    (void)__builtin_frexp(hi, &ehi);
+    (void)__builtin_frexp(wlo, &wl);
+    (void)__builtin_frexp(whi, &wh);
+    if (!(lo >= 0x1p-126 && hi < 0x1p127 && lo <= hi && ehi - elo <= 1)) return 0u;
+    const uint32_t walk = wl != wh ? 4u : 0u;
+    return (ehi != elo ? 2u : 1u) | walk | (static_cast<uint32_t>(elo - 1 - 23 + kPlanBias) << 8);
+}
+
+// The prediction of one sub-chunk by its plan (wave-uniform): its counts at
+// one or two binades, else not usable; the likely-walked bit when the plan
+// says so or neither count is usable.
+template <uint32_t H>
+__device__ __forceinline__ SegInfo predict_sub(const float (&e)[kPer], uint32_t plan)
+{
+    SegInfo info{0, 0, kSegWalk, 0};
+    const uint32_t nb = plan & 3u;
+    if (nb == 0) return info;
+    info.u = static_cast<int32_t>(plan >> 8) - kPlanBias;
+    info.flags = 0u;
+    // one copy of the count, run once per binade: the two counts never hold
+    // registers at the same time
+#pragma nounroll
+    for (uint32_t b = 0; b < nb; ++b) {
+        uint32_t units, flags;
+        count_units<H>(e, info.u + static_cast<int32_t>(b), units, flags);
+        if (b == 0) info.units = units;
+        else info.units1 = units;
+        info.flags |= flags << (b * kSegUpper);
+    }
+    if ((plan & 4u) || (info.flags & (1u | (1u << kSegUpper))) == 0u) info.flags |= kSegWalk;
     return info;
 }
 
@@ -633,20 +690,23 @@ __global__ __launch_bounds__(kBlock) void k_smp_seg(SmpGeo g, float *logits, Smp
     __syncthreads();
     // slots past the chunk's last sub-chunk (only in a shorter last chunk)
     // are empty: they add nothing, whatever the state
-    for (uint32_t k = nsub + threadIdx.x; k < spc; k += blockDim.x) out[k] = SegInfo{0, 0, 8u, 0};
+    for (uint32_t k = nsub + threadIdx.x; k < spc; k += blockDim.x) out[k] = SegInfo{0, 0, kSegEmpty, 0};
     // pass B: the prediction per sub-chunk
     for (uint32_t k = wave; k < nsub; k += kBlock / kWave) {
-        SegInfo info{0, 0, 0, 0};
+        SegInfo info{0, 0, kSegWalk, 0}; // past kMaxSub: walked
         const uint64_t a0 = c0 + static_cast<uint64_t>(k) * kSub;
         const uint64_t a1 = a0 + kSub < c1 ? a0 + kSub : c1;
         if (k < npred) {
             double Pk = P;
             for (uint32_t i = 0; i < k; ++i) Pk += s_sub[i];
-            const double lo = Pk * (1.0 - seq_rel_bound(static_cast<double>(a0)));
-            const double hi = (Pk + s_sub[k]) * (1.0 + seq_rel_bound(static_cast<double>(a1)));
+            const double end = Pk + s_sub[k];
+            const uint32_t plan = plan_sub(Pk * (1.0 - seq_rel_bound(static_cast<double>(a0))),
+                                           end * (1.0 + seq_rel_bound(static_cast<double>(a1))),
+                                           Pk * (1.0 - steer_margin(static_cast<double>(a0))),
+                                           end * (1.0 + steer_margin(static_cast<double>(a1))));
             float e[kPer];
             load_sub(k, e);
-            info = predict_sub<1>(e, lo, hi);
+            info = predict_sub<1>(e, plan);
         }
         if (lane == 0) out[k] = info;
     }
@@ -714,10 +774,21 @@ __global__ __launch_bounds__(kBlock) void k_smp_expseg(SmpGeo g, float *logits, 
         if (ss.s != 0.0f) term = static_cast<double>(ss.s) * exp(static_cast<double>(ss.m) - static_cast<double>(m));
     }
     const double incl = wave_incl_scan_f64(term);
+    // lane i: sub-chunk i's prediction plan, from the sums before and at it
+    uint32_t plan = 0;
+    if (lane < nsub) {
+        const double before = pre + (incl - term);
+        const double end = before + term;
+        const uint64_t a0 = sub_col(lane);
+        const double a1 = static_cast<double>(a0 + kSub < c1 ? a0 + kSub : c1);
+        const double lo = before * (1.0 - kApproxRel), hi = end * (1.0 + kApproxRel);
+        plan = plan_sub(lo * (1.0 - seq_rel_bound(static_cast<double>(a0))), hi * (1.0 + seq_rel_bound(a1)),
+                        lo * (1.0 - steer_margin(static_cast<double>(a0))), hi * (1.0 + steer_margin(a1)));
+    }
     SegInfo *out = w.seg + (rbase + chunk) * spc;
     // slots past the chunk's last sub-chunk (only in a shorter last chunk)
     // are empty: they add nothing, whatever the state
-    for (uint32_t k = nsub + threadIdx.x; k < spc; k += blockDim.x) out[k] = SegInfo{0, 0, 8u, 0};
+    for (uint32_t k = nsub + threadIdx.x; k < spc; k += blockDim.x) out[k] = SegInfo{0, 0, kSegEmpty, 0};
     const float scale = g.scale;
     const ExpfConsts ec = expf_consts_in_vgprs();
     // each wave's own copy of expf's 2^(i/32) table in LDS: no workgroup barrier
@@ -754,12 +825,8 @@ __global__ __launch_bounds__(kBlock) void k_smp_expseg(SmpGeo g, float *logits, 
                     if (col + q < c1) x[col + q] = cur[4 * h + q];
             }
         }
-        const double own = readlane_f64(term, k);
-        const double before = pre + (readlane_f64(incl, k) - own);
-        const uint64_t a1 = a0 + kSub < c1 ? a0 + kSub : c1;
-        const double lo = before * (1.0 - kApproxRel) * (1.0 - seq_rel_bound(static_cast<double>(a0)));
-        const double hi = (before + own) * (1.0 + kApproxRel) * (1.0 + seq_rel_bound(static_cast<double>(a1)));
-        const SegInfo info = predict_sub<kSplit>(cur, lo, hi);
+        const SegInfo info =
+            predict_sub<kSplit>(cur, static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(plan), k)));
         if (lane == 0) out[k] = info;
         if (j + 1 < kFusePerWave) {
 #pragma unroll
@@ -916,7 +983,7 @@ __global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *
         for (uint32_t kb = 0; kb < nslots && nst < kStage; kb += kWave) {
             const uint32_t sl = kb + lane;
             bool need = false;
-            if (sl < nslots && sl != 0) need = (seg[sl].flags & 9u) == 0u; // neither usable nor empty
+            if (sl < nslots && sl != 0) need = (seg[sl].flags & (kSegWalk | kSegEmpty)) == kSegWalk;
             uint64_t m = __ballot(need);
             while (m != 0 && nst < kStage) {
                 const uint32_t slot = kb + static_cast<uint32_t>(__builtin_ctzll(m));
@@ -941,7 +1008,7 @@ __global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *
     } else { // wave 0: the walk
     bool nan_final = false;
     uint32_t cur = 0; // staged sub-chunks passed
-    SegInfo nxt{0, 0, 8u, 0};
+    SegInfo nxt{0, 0, kSegEmpty, 0};
     if (lane < nslots) nxt = seg[lane];
     for (uint32_t kb = 0; kb < nslots && !nan_final; kb += kWave) {
         const SegInfo mine = nxt;
@@ -956,9 +1023,11 @@ __global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *
             bool fail = false;
             uint32_t add = 0;
             if (lane >= i && lane < nb) {
-                const bool empty = (mine.flags & 8u) != 0;
-                const bool easy = empty || (s.finite && (mine.flags & 3u) == 1u && mine.u == s.u);
-                add = easy && !empty ? mine.units : 0u;
+                const bool empty = (mine.flags & kSegEmpty) != 0;
+                const bool lower = (mine.flags & 3u) == 1u && mine.u == s.u;
+                const bool upper = ((mine.flags >> kSegUpper) & 3u) == 1u && mine.u + 1 == s.u;
+                const bool easy = empty || (s.finite && (lower || upper));
+                add = easy && !empty ? (upper ? mine.units1 : mine.units) : 0u;
                 fail = !easy;
             }
             const uint32_t incl = wave_incl_scan(add < kSeqLimit ? add : kSeqLimit);
@@ -969,12 +1038,16 @@ __global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *
             if (f >= nb) break;
             i = f + 1;
             // slot f on its own: a usable sub-chunk with one tie adds its
-            // units plus the tie's parity correction
-            const uint32_t units = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(mine.units), f));
+            // units plus the tie's parity correction, at whichever of its
+            // binades the state is in
             const int32_t u = __builtin_amdgcn_readlane(mine.u, f);
-            const uint32_t flags = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(mine.flags), f));
+            const bool upper = u + 1 == s.u; // uniform
+            const uint32_t units = static_cast<uint32_t>(
+                __builtin_amdgcn_readlane(static_cast<int>(upper ? mine.units1 : mine.units), f));
+            const uint32_t flags =
+                static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(mine.flags), f)) >> (upper ? kSegUpper : 0u);
             const uint64_t addf = static_cast<uint64_t>(units) + ((flags & 2u) ? ((s.m + (flags >> 2)) & 1u) : 0u);
-            if (s.finite && (flags & 1u) && u == s.u && static_cast<uint64_t>(s.m) + addf < kSeqLimit) {
+            if (s.finite && (flags & 1u) && (u == s.u || upper) && static_cast<uint64_t>(s.m) + addf < kSeqLimit) {
                 s.m += static_cast<uint32_t>(addf);
                 continue;
             }

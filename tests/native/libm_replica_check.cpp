@@ -154,7 +154,8 @@ static uint64_t splitmix(uint64_t &z);
 // chunk == 0: the whole range is walked (no predictions).  Otherwise
 // chunks of `chunk` elements split into sub-chunks of `sub`: k_smp_seg's
 // prediction per sub-chunk (f64 prefix of chunk and sub-chunk sums, the
-// rounding bound, units at the predicted binade, one tie resolved by
+// rounding bound, units at the predicted binade or at both of two adjacent
+// ones, one tie resolved by
 // parity) and k_smp_sum's checks on the exact state; a sub-chunk that is
 // not taken is walked alone.  *jumped counts sub-chunks taken in one step.
 // perturb > 0 stands in for k_smp_expseg's approximate sums: the prefix and
@@ -188,8 +189,11 @@ float seqsum_chunked(const float *e, uint64_t n, uint32_t lanes, uint64_t chunk,
             int elo = 0, ehi = 0;
             std::frexp(lo, &elo);
             std::frexp(hi, &ehi);
-            bool ok = lo >= 0x1p-126 && hi < 0x1p127 && lo <= hi && elo == ehi;
-            const int32_t u = elo - 24;
+            // one binade, or two adjacent ones: a count at each
+            const bool usable = lo >= 0x1p-126 && hi < 0x1p127 && lo <= hi && ehi - elo <= 1;
+            // the count at the state's binade, when it is one of them
+            const int32_t u = s.u == elo - 24 + 1 && ehi != elo ? elo - 24 + 1 : elo - 24;
+            bool ok = usable;
             uint64_t units = 0;
             int ties = 0;
             uint32_t par = 0;
