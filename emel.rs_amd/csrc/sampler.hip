@@ -21,7 +21,9 @@
 //                 maximum and approximate sum of exp(v - that maximum).
 //   k_smp_expseg  (row, chunk), chunks of at most 8192 columns: e written
 //                 in place, and each sub-chunk's exact contribution in units
-//                 of the binade predicted from the approximate sums.
+//                 of the binade (or each of the two binades) predicted from
+//                 the approximate sums; the row's first sub-chunk is added
+//                 one by one instead, leaving the walk's starting state.
 //   k_smp_exp and k_smp_seg, wider chunks, the same in two passes: e and
 //                 the chunk's f64 sum, then the predictions from exact f64
 //                 prefixes.
@@ -29,7 +31,7 @@
 //                 taking a sub-chunk's predicted contribution when the exact
 //                 state confirms it, walking the other sub-chunks from
 //                 registers or from LDS.  A second wave stages the
-//                 sub-chunks with unusable predictions into LDS ahead of
+//                 sub-chunks that probably cross a binade into LDS ahead of
 //                 the walk, then finds the fast candidate threshold p_thr:
 //                 the top_k-th largest p among the row's sub-chunk maxima
 //                 (fused path, top_k <= 8192).
@@ -122,6 +124,11 @@ struct SegInfo {
 constexpr uint32_t kSegEmpty = 8u;
 constexpr uint32_t kSegUpper = 4u;     // shift of the 2^(u+1) bits
 constexpr uint32_t kSegWalk = 0x80u;
+// A row's first slot holds the running sum after it instead (the walk starts
+// there): units = m and u, or with kSegSpecial a NaN or +inf sum whose bits
+// are in units1.  It is also empty: the walk adds nothing for it.
+constexpr uint32_t kSegState = 0x100u;
+constexpr uint32_t kSegSpecial = 0x200u;
 // Chunks of at most kFuseSubs sub-chunks (kFuseCols columns) take the fused
 // path: k_smp_max<true> also leaves an approximate sum of exp(v - m_k) per
 // sub-chunk (m_k its maximum), and k_smp_expseg writes e and predicts each
@@ -636,6 +643,54 @@ __device__ __forceinline__ SegInfo predict_sub(const float (&e)[kPer], uint32_t 
     return info;
 }
 
+// The row's first sub-chunk, added one element at a time by lane 0: the
+// reference's own arithmetic.  At the start of a row the running sum is
+// comparable to its addends, and a binade crossing or a tie comes every few
+// elements, each of which would cost the walk a round.  Returns slot 0's
+// SegInfo: the state after it.  e is this lane's part of the sub-chunk in
+// predict_sub's layout H (+0 past the row's end, which leaves the never -0
+// running sum unchanged); s_buf is kSub floats of this wave's LDS.  Called
+// by a whole wave.
+template <uint32_t H>
+__device__ __forceinline__ SegInfo head_state(const float (&e)[kPer], float4 *s_buf)
+{
+    constexpr uint32_t G = kPer / H;
+    static_assert(G % 4 == 0, "whole float4 per group");
+    const uint32_t lane = threadIdx.x % kWave;
+#pragma unroll
+    for (uint32_t h = 0; h < H; ++h)
+#pragma unroll
+        for (uint32_t j = 0; j < G / 4; ++j)
+            s_buf[(h * (kSub / H) + lane * G) / 4 + j] =
+                make_float4(e[h * G + 4 * j], e[h * G + 4 * j + 1], e[h * G + 4 * j + 2], e[h * G + 4 * j + 3]);
+    // this wave's LDS writes before lane 0's reads
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    float acc = 0.0f;
+    if (lane == 0) {
+#pragma unroll 8
+        for (uint32_t j = 0; j < kSub / 4; ++j) {
+            const float4 q = s_buf[j];
+            acc += q.x;
+            acc += q.y;
+            acc += q.z;
+            acc += q.w;
+        }
+    }
+    acc = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, acc)));
+    SegInfo info{0, 0, kSegEmpty | kSegState, 0};
+    if (!(acc < __builtin_inff())) { // NaN or +inf
+        info.flags |= kSegSpecial;
+        info.units1 = __builtin_bit_cast(uint32_t, acc);
+    } else {
+        const SeqState st = seq_state(acc);
+        info.units = st.m;
+        info.u = st.u;
+    }
+    return info;
+}
+
 // One 256-thread workgroup per (row, chunk); wave w predicts sub-chunks
 // w, w + 4, ... from its kPer elements per lane.  A sub-chunk with one tie is
 // still usable: the tie rounds its sum to an even number of units, so it
@@ -645,6 +700,7 @@ __global__ __launch_bounds__(kBlock) void k_smp_seg(SmpGeo g, float *logits, Smp
 {
     __shared__ double s_red[kBlock / kWave];
     __shared__ double s_sub[kMaxSub];
+    __shared__ float4 s_head[kSub / 4]; // wave 0 of a row's first chunk: the head
     const uint32_t row = blockIdx.x / g.chunks, chunk = blockIdx.x % g.chunks;
     const uint32_t lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
     double pre = 0.0;
@@ -706,7 +762,8 @@ __global__ __launch_bounds__(kBlock) void k_smp_seg(SmpGeo g, float *logits, Smp
                                            end * (1.0 + steer_margin(static_cast<double>(a1))));
             float e[kPer];
             load_sub(k, e);
-            info = predict_sub<1>(e, plan);
+            // the row's first sub-chunk: the walk's starting state instead
+            info = chunk == 0 && k == 0 ? head_state<1>(e, s_head) : predict_sub<1>(e, plan);
         }
         if (lane == 0) out[k] = info;
     }
@@ -741,10 +798,58 @@ __device__ __forceinline__ double readlane_f64(double v, uint32_t l)
     return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
 }
 
+// The row maximum of v, from the chunk maxima (every lane of a wave).
+__device__ __forceinline__ float row_max_wave(const SmpGeo &g, const SmpWs &w, uint32_t row, uint32_t lane)
+{
+    const uint64_t rbase = static_cast<uint64_t>(row) * g.chunks;
+    float m = -__builtin_inff();
+    for (uint32_t c = lane; c < g.chunks; c += kWave) {
+        const float p = w.part[rbase + c];
+        m = p > m ? p : m;
+    }
+    return wave_max_dpp(m);
+}
+
+// A head workgroup of k_smp_expseg (one per row, first in the grid): its
+// first wave computes the row's first sub-chunk's e, as the (row, 0)
+// workgroup does, and adds them one by one (head_state) into slot 0.  Its
+// own workgroup, dispatched before the others, keeps this serial chain off
+// the tail of the pass.
+__device__ __forceinline__ void expseg_head(const SmpGeo &g, const float *logits, const SmpWs &w, uint32_t row,
+                                            uint64_t *tab, float4 *s_head)
+{
+    const uint32_t lane = threadIdx.x % kWave;
+    const float *x = logits + static_cast<int64_t>(row) * g.ld;
+    uint64_t c0, c1;
+    chunk_range(g, 0, c0, c1);
+    float v[kPer];
+    load_split(g, x, c0, c1, lane, true, v);
+    const float m = row_max_wave(g, w, row, lane);
+    const ExpfConsts ec = expf_consts_in_vgprs();
+    if (lane < 32) tab[lane] = kExp2Table[lane];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+#pragma unroll
+    for (uint32_t q = 0; q < kPer; ++q)
+        v[q] = split_col(c0, lane, q) < c1 ? emel_expf(v[q] * g.scale - m, tab, ec) : 0.0f;
+    const SegInfo head = head_state<kSplit>(v, s_head);
+    if (lane == 0) w.seg[static_cast<uint64_t>(row) * g.chunks * subs_per_chunk(g)] = head;
+}
+
+// Grid: g.rows head workgroups (expseg_head), then one per (row, chunk).
 __global__ __launch_bounds__(kBlock) void k_smp_expseg(SmpGeo g, float *logits, SmpWs w)
 {
-    const uint32_t row = blockIdx.x / g.chunks, chunk = blockIdx.x % g.chunks;
     const uint32_t lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    // each wave's own copy of expf's 2^(i/32) table in LDS: no workgroup barrier
+    __shared__ uint64_t s_tab[kBlock / kWave][32];
+    if (blockIdx.x < g.rows) {
+        __shared__ float4 s_head[kSub / 4];
+        if (wave == 0) expseg_head(g, logits, w, blockIdx.x, s_tab[0], s_head);
+        return;
+    }
+    const uint32_t b = blockIdx.x - g.rows;
+    const uint32_t row = b / g.chunks, chunk = b % g.chunks;
     float *x = logits + static_cast<int64_t>(row) * g.ld;
     uint64_t c0, c1;
     chunk_range(g, chunk, c0, c1);
@@ -755,12 +860,7 @@ __global__ __launch_bounds__(kBlock) void k_smp_expseg(SmpGeo g, float *logits, 
     float cur[kPer];
     load_split(g, x, sub_col(wave), c1, lane, wave < nsub, cur);
     const uint64_t rbase = static_cast<uint64_t>(row) * g.chunks;
-    float m = -__builtin_inff();
-    for (uint32_t c = lane; c < g.chunks; c += kWave) {
-        const float p = w.part[rbase + c];
-        m = p > m ? p : m;
-    }
-    m = wave_max_dpp(m);
+    const float m = row_max_wave(g, w, row, lane);
     double pre = 0.0; // ~ sum of e over the chunks before this one
     for (uint32_t c = lane; c < chunk; c += kWave) {
         const double sc = w.psum[rbase + c];
@@ -791,8 +891,6 @@ __global__ __launch_bounds__(kBlock) void k_smp_expseg(SmpGeo g, float *logits, 
     for (uint32_t k = nsub + threadIdx.x; k < spc; k += blockDim.x) out[k] = SegInfo{0, 0, kSegEmpty, 0};
     const float scale = g.scale;
     const ExpfConsts ec = expf_consts_in_vgprs();
-    // each wave's own copy of expf's 2^(i/32) table in LDS: no workgroup barrier
-    __shared__ uint64_t s_tab[kBlock / kWave][32];
     if (lane < 32) s_tab[wave][lane] = kExp2Table[lane];
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __builtin_amdgcn_wave_barrier();
@@ -827,7 +925,8 @@ __global__ __launch_bounds__(kBlock) void k_smp_expseg(SmpGeo g, float *logits, 
         }
         const SegInfo info =
             predict_sub<kSplit>(cur, static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(plan), k)));
-        if (lane == 0) out[k] = info;
+        // the row's first slot holds the head workgroup's state instead
+        if (lane == 0 && (chunk != 0 || k != 0)) out[k] = info;
         if (j + 1 < kFusePerWave) {
 #pragma unroll
             for (uint32_t q = 0; q < kPer; ++q) cur[q] = nxt[q];
@@ -847,7 +946,6 @@ __global__ __launch_bounds__(kBlock) void k_smp_expseg(SmpGeo g, float *logits, 
 // element, adds it with one f32 addition and starts the next round after
 // it.  Each round commits at least one element, so the rounds end.
 
-constexpr uint32_t kHead = 512;          // a row's first elements, added one by one
 constexpr uint32_t kFastPer = 8;         // sub-chunk maxima per lane for the fast threshold
 constexpr uint32_t kFastWg = 256;        // fast candidates a k_smp_div workgroup buffers
 constexpr uint32_t kStage = 24;          // walked sub-chunks k_smp_sum's second wave stages in LDS
@@ -917,8 +1015,7 @@ constexpr uint32_t kSumThreads = 2 * kWave;
 
 __global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *logits, SmpWs w)
 {
-    __shared__ float4 s_head[kHead / 4]; // the row's first elements, for lane 0's sequential adds
-    __shared__ uint32_t s_fast[2];       // wave 1's threshold: taken, e_thr's key
+    __shared__ uint32_t s_fast[2]; // wave 1's threshold: taken, e_thr's key
     // wave 1 stages sub-chunks the walk will load: s_stage[i] holds slot
     // s_slot[i] as the walk's registers hold it (float4 q of lane l at
     // [i][q][l]); s_ready counts the staged ones (release / acquire)
@@ -930,12 +1027,24 @@ __global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *
     const float *x = logits + static_cast<int64_t>(row) * g.ld;
     const uint32_t spc = subs_per_chunk(g);
     const uint64_t card4 = g.card & ~uint64_t{3};
-    SumState s{0u, -149, true, 0.0f};
     // The row's predictions form one list of chunks * spc slots; they are
     // read 64 at a time (lane i holds slot base + i), the next batch in
     // flight while this one is used.
     const uint32_t nslots = g.chunks * spc;
     const SegInfo *seg = w.seg + static_cast<uint64_t>(row) * nslots;
+    // the walk starts from the state after the row's first sub-chunk (its
+    // head, added one by one by the prediction pass)
+    SumState s{0u, -149, true, 0.0f};
+    {
+        const SegInfo h = seg[0];
+        if (h.flags & kSegSpecial) {
+            s.finite = false;
+            s.special = __builtin_bit_cast(float, h.units1);
+        } else {
+            s.m = h.units;
+            s.u = h.u;
+        }
+    }
     // A sub-chunk's element count (1 .. kSub) and first column.
     auto slot_range = [&](uint32_t slot, uint64_t &a0) {
         uint64_t c0, c1;
@@ -1061,8 +1170,6 @@ __global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *
             const uint32_t ready = __hip_atomic_load(&s_ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
             while (cur < ready && s_slot[cur] < slot) ++cur;
             if (cur < ready && s_slot[cur] == slot) { // staged by wave 1
-                uint64_t a0;
-                n = slot_range(slot, a0);
 #pragma unroll
                 for (uint32_t q = 0; q < kPer / 4; ++q) {
                     const float4 v = s_stage[cur][q][lane];
@@ -1074,48 +1181,7 @@ __global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *
             } else {
                 load_slot(slot, e, n);
             }
-            // The first elements of a row come with a binade crossing or a
-            // tie every few elements (the sum is still comparable to its
-            // addends), each of which would cost a round: lane 0 adds them
-            // one by one, the reference's own arithmetic.
-            uint32_t head = 0;
-            if (slot == 0 && s.finite && s.m == 0) { // the row's first sub-chunk
-                head = n < kHead ? n : kHead;
-                if (kPer * lane < kHead) {
-#pragma unroll
-                    for (uint32_t j = 0; j < kPer / 4; ++j)
-                        s_head[kPer / 4 * lane + j] =
-                            make_float4(e[4 * j], e[4 * j + 1], e[4 * j + 2], e[4 * j + 3]);
-                }
-                // orders this wave's LDS writes before lane 0's reads (wave 1
-                // never reaches here, so no workgroup barrier)
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-                __builtin_amdgcn_wave_barrier();
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-                float acc = seq_value(s.m, s.u);
-                if (lane == 0) {
-                    // whole float4s: past n the elements are +0, which leaves
-                    // the (never -0) running sum unchanged
-#pragma unroll 8
-                    for (uint32_t j = 0; j < (head + 3) / 4; ++j) {
-                        const float4 q4 = s_head[j];
-                        acc += q4.x;
-                        acc += q4.y;
-                        acc += q4.z;
-                        acc += q4.w;
-                    }
-                }
-                acc = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, acc)));
-                if (!(acc < __builtin_inff())) {
-                    s.finite = false;
-                    s.special = acc;
-                } else {
-                    const SeqState h = seq_state(acc);
-                    s.m = h.m;
-                    s.u = h.u;
-                }
-            }
-            if (head < kSub) sum_tile<kPer>(e, s, head); // the head's elements are committed
+            sum_tile<kPer>(e, s);
         }
     }
     } // wave 0
@@ -1897,7 +1963,7 @@ hipError_t launch_sampler(const SamplerArgs &a, hipStream_t s)
     const dim3 grid(a.rows * g.chunks);
     if (g.chunk_cols <= kFuseCols) {
         k_smp_max<true><<<grid, kBlock, 0, s>>>(g, a.logits, w);
-        k_smp_expseg<<<grid, kBlock, 0, s>>>(g, a.logits, w);
+        k_smp_expseg<<<dim3(a.rows + a.rows * g.chunks), kBlock, 0, s>>>(g, a.logits, w);
     } else {
         k_smp_max<false><<<grid, kBlock, 0, s>>>(g, a.logits, w);
         k_smp_exp<<<grid, kBlock, 0, s>>>(g, a.logits, w);
