@@ -1016,11 +1016,11 @@ constexpr uint32_t kSumThreads = 2 * kWave;
 __global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *logits, SmpWs w)
 {
     __shared__ uint32_t s_fast[2]; // wave 1's threshold: taken, e_thr's key
-    // wave 1 stages sub-chunks the walk will load: s_stage[i] holds slot
-    // s_slot[i] as the walk's registers hold it (float4 q of lane l at
-    // [i][q][l]); s_ready counts the staged ones (release / acquire)
+    // wave 1 stages the walk-marked sub-chunks: s_stage[i] holds the i-th
+    // of them (in slot order) as the walk's registers hold it (float4 q of
+    // lane l at [i][q][l]); s_ready counts the staged ones (release /
+    // acquire)
     __shared__ float4 s_stage[kStage][kPer / 4][kWave];
-    __shared__ uint32_t s_slot[kStage];
     __shared__ uint32_t s_ready;
     const uint32_t row = blockIdx.x;
     const uint32_t lane = threadIdx.x % kWave;
@@ -1084,10 +1084,10 @@ __global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *
     if (threadIdx.x == 0) s_ready = 0;
     __syncthreads();
     if (threadIdx.x >= kWave) { // wave 1
-        // Stage, in slot order, the sub-chunks whose prediction is unusable
-        // (almost every sub-chunk the walk loads), slot 0 excepted: the walk
-        // starts there at once.  The walk takes a staged sub-chunk from LDS
-        // when it is ready and loads it itself otherwise, so it never waits.
+        // Stage, in slot order, the sub-chunks marked as probably walked
+        // (almost every sub-chunk the walk loads).  The walk takes a staged
+        // sub-chunk from LDS when it is ready and loads it itself otherwise,
+        // so it never waits.
         uint32_t nst = 0;
         for (uint32_t kb = 0; kb < nslots && nst < kStage; kb += kWave) {
             const uint32_t sl = kb + lane;
@@ -1103,7 +1103,6 @@ __global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *
 #pragma unroll
                 for (uint32_t q = 0; q < kPer / 4; ++q)
                     s_stage[nst][q][lane] = make_float4(e[4 * q], e[4 * q + 1], e[4 * q + 2], e[4 * q + 3]);
-                if (lane == 0) s_slot[nst] = slot;
                 ++nst;
                 if (lane == 0) __hip_atomic_store(&s_ready, nst, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
             }
@@ -1116,73 +1115,90 @@ __global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *
         }
     } else { // wave 0: the walk
     bool nan_final = false;
-    uint32_t cur = 0; // staged sub-chunks passed
+    uint32_t marked = 0; // walk-marked slots before this batch: wave 1 stages them in this order
     SegInfo nxt{0, 0, kSegEmpty, 0};
     if (lane < nslots) nxt = seg[lane];
     for (uint32_t kb = 0; kb < nslots && !nan_final; kb += kWave) {
         const SegInfo mine = nxt;
         if (kb + kWave + lane < nslots) nxt = seg[kb + kWave + lane];
         const uint32_t nb = nslots - kb < kWave ? nslots - kb : kWave;
+        const uint64_t wmask =
+            __ballot(lane < nb && kb + lane != 0 && (mine.flags & (kSegWalk | kSegEmpty)) == kSegWalk);
         uint32_t i = 0; // next slot of the batch
         while (i < nb) {
             // Take the run of slots from i on that need no decision: empty
-            // ones, and usable tie-free sub-chunks in the current binade,
+            // ones, and usable sub-chunks counted at the current binade,
             // their units below 2^24 -- one wave prefix sum finds where the
             // run ends.
-            bool fail = false;
-            uint32_t add = 0;
+            bool fail = false, tie = false;
+            uint32_t add = 0, par = 0;
             if (lane >= i && lane < nb) {
                 const bool empty = (mine.flags & kSegEmpty) != 0;
-                const bool lower = (mine.flags & 3u) == 1u && mine.u == s.u;
-                const bool upper = ((mine.flags >> kSegUpper) & 3u) == 1u && mine.u + 1 == s.u;
-                const bool easy = empty || (s.finite && (lower || upper));
+                const bool upper = mine.u + 1 == s.u;
+                const uint32_t fb = mine.flags >> (upper ? kSegUpper : 0u); // the state's binade's bits
+                const bool easy = empty || (s.finite && (fb & 1u) && (upper || mine.u == s.u));
                 add = easy && !empty ? (upper ? mine.units1 : mine.units) : 0u;
+                tie = easy && !empty && (fb & 2u);
+                par = (fb >> 2) & 1u;
                 fail = !easy;
             }
-            const uint32_t incl = wave_incl_scan(add < kSeqLimit ? add : kSeqLimit);
+            const uint32_t x = add < kSeqLimit ? add : kSeqLimit;
+            uint32_t incl = wave_incl_scan(x);
+            // A slot with one tie adds one more unit when the running units
+            // before it plus its tie's parity bit are odd (round to even).
+            // Its correction moves the slots after it, so they are settled
+            // in order, on the scalar unit: at most a few per batch.
+            const uint64_t tmask = __ballot(tie);
+            if (tmask) {
+                const uint32_t excl = incl - x;
+                uint64_t cmask = 0;
+                uint32_t cacc = 0;
+                for (uint64_t m = tmask; m; m &= m - 1) {
+                    const int tl = __builtin_ctzll(m);
+                    const uint32_t c = (s.m + static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(excl), tl)) +
+                                        cacc + static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(par), tl))) &
+                                       1u;
+                    cmask |= static_cast<uint64_t>(c) << tl;
+                    cacc += c;
+                }
+                // the corrections at and before this lane
+                incl += __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(cmask >> 32),
+                                                  __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(cmask), 0u)) +
+                        static_cast<uint32_t>((cmask >> lane) & 1u);
+            }
             fail = fail || (lane >= i && lane < nb && static_cast<uint64_t>(s.m) + incl >= kSeqLimit);
             const uint64_t fmask = __ballot(fail);
             const uint32_t f = fmask ? static_cast<uint32_t>(__builtin_ctzll(fmask)) : nb;
             if (f > i) s.m += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), f - 1));
             if (f >= nb) break;
             i = f + 1;
-            // slot f on its own: a usable sub-chunk with one tie adds its
-            // units plus the tie's parity correction, at whichever of its
-            // binades the state is in
-            const int32_t u = __builtin_amdgcn_readlane(mine.u, f);
-            const bool upper = u + 1 == s.u; // uniform
-            const uint32_t units = static_cast<uint32_t>(
-                __builtin_amdgcn_readlane(static_cast<int>(upper ? mine.units1 : mine.units), f));
-            const uint32_t flags =
-                static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(mine.flags), f)) >> (upper ? kSegUpper : 0u);
-            const uint64_t addf = static_cast<uint64_t>(units) + ((flags & 2u) ? ((s.m + (flags >> 2)) & 1u) : 0u);
-            if (s.finite && (flags & 1u) && (u == s.u || upper) && static_cast<uint64_t>(s.m) + addf < kSeqLimit) {
-                s.m += static_cast<uint32_t>(addf);
-                continue;
-            }
             if (!s.finite && s.special != s.special) { // NaN is final
                 nan_final = true;
                 break;
             }
-            const uint32_t slot = kb + f;
+            // slot f is walked: from LDS when wave 1 has staged it (the
+            // staged slots are the walk-marked ones, in slot order)
             float e[kPer];
-            uint32_t n;
-            const uint32_t ready = __hip_atomic_load(&s_ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
-            while (cur < ready && s_slot[cur] < slot) ++cur;
-            if (cur < ready && s_slot[cur] == slot) { // staged by wave 1
+            bool staged = false;
+            const uint32_t sidx = marked + static_cast<uint32_t>(__builtin_popcountll(wmask & ((uint64_t{1} << f) - 1u)));
+            if ((wmask >> f) & 1u)
+                staged = sidx < __hip_atomic_load(&s_ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (staged) {
 #pragma unroll
                 for (uint32_t q = 0; q < kPer / 4; ++q) {
-                    const float4 v = s_stage[cur][q][lane];
+                    const float4 v = s_stage[sidx][q][lane];
                     e[4 * q] = v.x;
                     e[4 * q + 1] = v.y;
                     e[4 * q + 2] = v.z;
                     e[4 * q + 3] = v.w;
                 }
             } else {
-                load_slot(slot, e, n);
+                uint32_t n;
+                load_slot(kb + f, e, n);
             }
             sum_tile<kPer>(e, s);
         }
+        marked += static_cast<uint32_t>(__builtin_popcountll(wmask));
     }
     } // wave 0
     __syncthreads(); // both waves: wave 1's threshold is in s_fast

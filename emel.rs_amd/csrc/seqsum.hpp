@@ -136,9 +136,14 @@ struct SumState {
 };
 
 // The rounds over one tile of PER * 64 elements (this lane's PER consecutive
-// ones in e).
+// ones in e).  A round counts the uncommitted elements' units at the current
+// binade and scans the lane totals.  Without an event it commits them all.
+// Otherwise the first event lies in the first lane that holds a tie or whose
+// running units reach 2^24; that lane's elements are then read one by one on
+// the scalar unit up to the event, which is added with one f32 addition, and
+// the next round starts after it.
 template <uint32_t PER>
-__device__ __forceinline__ void sum_tile(const float (&e)[PER], SumState &s, uint32_t start = 0)
+__device__ __forceinline__ void sum_tile(const float (&e)[PER], SumState &s)
 {
     const uint32_t lane = threadIdx.x % kWave;
     if (!s.finite) {
@@ -149,7 +154,7 @@ __device__ __forceinline__ void sum_tile(const float (&e)[PER], SumState &s, uin
         if (__ballot(nan)) s.special = __builtin_nanf("");
         return;
     }
-    // start: tile-relative index of the first uncommitted element
+    uint32_t start = 0; // tile-relative index of the first uncommitted element
     while (true) {
         // this round's units at the current binade (0 for committed
         // elements), kept for the event search below
@@ -178,39 +183,35 @@ __device__ __forceinline__ void sum_tile(const float (&e)[PER], SumState &s, uin
         // saturated value already marks a crossing)
         const uint32_t x_in = lsum < kSeqLimit ? lsum : kSeqLimit;
         const uint32_t incl = wave_incl_scan(x_in);
-        const uint32_t total = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), kWave - 1));
-        const bool anytie = __ballot(ties != 0) != 0;
-        if (!anytie && s.m + total < kSeqLimit) {
-            s.m += total;
-            return; // tile committed
+        // lanes before the first event lane neither tie nor reach 2^24, so
+        // its running units before it are s.m plus its exclusive prefix
+        const uint64_t emask = __ballot(ties != 0u || s.m + incl >= kSeqLimit);
+        if (emask == 0) { // no event: the tile is committed
+            s.m += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), kWave - 1));
+            return;
         }
-        // this lane's first event element and the units just before it,
-        // branch-free: flags past the first event are never used, and the
-        // committed elements (r = 0, no tie) cannot be events in the lane
-        // that holds the first one (its running units are still below 2^24)
-        const uint32_t base = s.m + (incl - x_in);
-        uint32_t run = base, evmask = 0;
-#pragma unroll
-        for (uint32_t j = 0; j < PER; ++j) {
-            const bool ev = ((ties >> j) & 1u) != 0u || run + r[j] >= kSeqLimit;
-            evmask |= static_cast<uint32_t>(ev) << j;
-            run += r[j];
-        }
-        const uint32_t first = evmask ? static_cast<uint32_t>(__builtin_ctz(evmask)) : PER;
-        uint32_t run_first = base;
-        float ek = 0.0f;
-#pragma unroll
-        for (uint32_t j = 0; j < PER; ++j) {
-            run_first += j < first ? r[j] : 0u;
-            ek = j == first ? e[j] : ek;
-        }
-        const uint64_t emask = __ballot(evmask != 0u);
-        if (emask == 0) return; // unreachable: a tie or a crossing has a first element
         const int fl = __builtin_ctzll(emask);
-        const uint32_t k = PER * static_cast<uint32_t>(fl) +
-                           static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(first), fl));
-        const uint32_t run_k = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(run_first), fl));
-        const float e_k = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ek), fl));
+        uint32_t run = s.m + static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl - x_in), fl));
+        const uint32_t tl = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(ties), fl));
+        // lane fl's elements in order, on the scalar unit: the first tie, or
+        // the first element whose units reach 2^24 (committed elements add
+        // 0 units and hold no tie)
+        uint32_t k = PER * kWave, run_k = 0;
+        float e_k = 0.0f;
+#pragma unroll
+        for (uint32_t j = 0; j < PER; ++j) {
+            if (k == PER * kWave) {
+                const uint32_t rj = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(r[j]), fl));
+                if (((tl >> j) & 1u) || run + rj >= kSeqLimit) {
+                    k = PER * static_cast<uint32_t>(fl) + j;
+                    run_k = run;
+                    e_k = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e[j]), fl));
+                } else {
+                    run += rj;
+                }
+            }
+        }
+        if (k == PER * kWave) return; // unreachable: the lane holds an event
         const float sn = seq_value(run_k, s.u) + e_k; // the event element: one f32 addition
         if (!(sn < __builtin_inff())) { // NaN or +inf
             s.special = sn;
