@@ -22,8 +22,11 @@
 //   k_smp_expseg  (row, chunk), chunks of at most 8192 columns: e written
 //                 in place, and each sub-chunk's exact contribution in units
 //                 of the binade (or each of the two binades) predicted from
-//                 the approximate sums; the row's first sub-chunk is added
-//                 one by one instead, leaving the walk's starting state.
+//                 the approximate sums.  One head workgroup per row, first in
+//                 the grid, adds the row's first sub-chunk one by one (the
+//                 walk's starting state) and finds e_thr, the top_k-th
+//                 largest e among the row's sub-chunk maxima (fast candidate
+//                 list, top_k <= 8192).
 //   k_smp_exp and k_smp_seg, wider chunks, the same in two passes: e and
 //                 the chunk's f64 sum, then the predictions from exact f64
 //                 prefixes.
@@ -32,9 +35,9 @@
 //                 state confirms it, walking the other sub-chunks from
 //                 registers or from LDS.  A second wave stages the
 //                 sub-chunks that probably cross a binade into LDS ahead of
-//                 the walk, then finds the fast candidate threshold p_thr:
-//                 the top_k-th largest p among the row's sub-chunk maxima
-//                 (fused path, top_k <= 8192).
+//                 the walk, with their lane unit scans at both binades, so
+//                 that a crossing takes one step.  The walk ends with the
+//                 fast threshold p_thr = e_thr / S.
 //   k_smp_div     (row, chunk): p written in place, plus the histogram of the
 //                 top 11 bits of p's total-order key, and the list of every
 //                 p >= p_thr.  A row whose list fits 8192 entries is ranked
@@ -91,6 +94,8 @@ struct RowSel {
     uint32_t fast_on;    // k_smp_div lists the keys >= fast_key
     uint32_t fast_key;   // key of p_thr (k_smp_sum)
     uint32_t fast_count; // keys >= fast_key found; > kCap: the radix path decides
+    uint32_t ethr_on;    // e_thr found (k_smp_expseg's head workgroup)
+    uint32_t ethr_key;   // key of e_thr
 };
 
 struct SmpGeo {
@@ -129,6 +134,7 @@ constexpr uint32_t kSegWalk = 0x80u;
 // are in units1.  It is also empty: the walk adds nothing for it.
 constexpr uint32_t kSegState = 0x100u;
 constexpr uint32_t kSegSpecial = 0x200u;
+constexpr uint32_t kSegHasU = 0x400u; // u names the lower binade of a usable plan
 // Chunks of at most kFuseSubs sub-chunks (kFuseCols columns) take the fused
 // path: k_smp_max<true> also leaves an approximate sum of exp(v - m_k) per
 // sub-chunk (m_k its maximum), and k_smp_expseg writes e and predicts each
@@ -628,7 +634,7 @@ __device__ __forceinline__ SegInfo predict_sub(const float (&e)[kPer], uint32_t 
     const uint32_t nb = plan & 3u;
     if (nb == 0) return info;
     info.u = static_cast<int32_t>(plan >> 8) - kPlanBias;
-    info.flags = 0u;
+    info.flags = kSegHasU;
     // one copy of the count, run once per binade: the two counts never hold
     // registers at the same time
 #pragma nounroll
@@ -798,6 +804,62 @@ __device__ __forceinline__ double readlane_f64(double v, uint32_t l)
     return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
 }
 
+constexpr uint32_t kFastPer = 8;         // sub-chunk maxima per lane for the fast threshold
+constexpr uint32_t kFastBits = 14;       // low key bits the fast threshold leaves 0 (2^-9 of e_thr at most)
+
+// The fast candidate threshold, by one wave.  The top_k largest sub-chunk
+// maxima are top_k distinct elements; with e_thr the top_k-th largest of
+// their e (computed as k_smp_expseg computes e), at least top_k elements
+// have e >= e_thr, so p >= p_thr = e_thr / S (the division k_smp_div uses,
+// correctly rounded and so monotone), and every element of the top_k by p
+// -- ties at the boundary included -- has p >= p_thr.  k_smp_div then lists
+// those elements directly.  Returns false when the row cannot take it
+// (three-pass chunks, top_k above kCap or above the sub-chunk count, more
+// than kFastPer sub-chunks per lane).
+__device__ bool fast_threshold(const SmpGeo &g, const SmpWs &w, uint32_t row, uint32_t lane, const uint64_t *tab,
+                               uint32_t &ethr_key)
+{
+    const uint32_t spc = subs_per_chunk(g), nslots = g.chunks * spc;
+    if (!(g.chunk_cols <= kFuseCols && g.top_k <= kCap && nslots <= kWave * kFastPer)) return false;
+    const SubSum *sub = w.sub + static_cast<uint64_t>(row) * nslots;
+    // only the last chunk can hold empty slots: its first `tail` slots are written
+    const uint32_t last = (g.chunks - 1) * spc;
+    const uint32_t tail = static_cast<uint32_t>((g.card - static_cast<uint64_t>(g.chunks - 1) * g.chunk_cols + kSub - 1) / kSub);
+    float mv[kFastPer];
+    bool valid[kFastPer];
+    float M = -__builtin_inff();
+#pragma unroll
+    for (uint32_t j = 0; j < kFastPer; ++j) {
+        const uint32_t slot = lane + kWave * j;
+        valid[j] = slot < nslots && (slot < last || slot - last < tail); // written by k_smp_max<true>
+        mv[j] = valid[j] ? sub[slot].m : -__builtin_inff();
+        M = mv[j] > M ? mv[j] : M;
+    }
+    M = wave_max_dpp(M); // the row maximum: every element lies in a sub-chunk
+    const ExpfConsts ec = expf_consts_in_vgprs();
+    uint32_t key[kFastPer];
+    uint32_t nvalid = 0;
+#pragma unroll
+    for (uint32_t j = 0; j < kFastPer; ++j) {
+        key[j] = valid[j] ? total_key(emel_expf(mv[j] - M, tab, ec)) : 0u; // valid keys are > 0
+        nvalid += static_cast<uint32_t>(__builtin_popcountll(__ballot(valid[j])));
+    }
+    if (nvalid < g.top_k) return false;
+    // The largest t with top_k keys >= t, bit by bit from the top; the bits
+    // below kFastBits stay 0, which only lowers t (a lower threshold lists a
+    // few more candidates, never fewer).
+    uint32_t t = 0;
+    for (int b = 31; b >= static_cast<int>(kFastBits); --b) {
+        const uint32_t c = t | (1u << b);
+        uint32_t n = 0;
+#pragma unroll
+        for (uint32_t j = 0; j < kFastPer; ++j) n += static_cast<uint32_t>(__builtin_popcountll(__ballot(key[j] >= c)));
+        if (n >= g.top_k) t = c;
+    }
+    ethr_key = t;
+    return true;
+}
+
 // The row maximum of v, from the chunk maxima (every lane of a wave).
 __device__ __forceinline__ float row_max_wave(const SmpGeo &g, const SmpWs &w, uint32_t row, uint32_t lane)
 {
@@ -846,6 +908,18 @@ __global__ __launch_bounds__(kBlock) void k_smp_expseg(SmpGeo g, float *logits, 
     if (blockIdx.x < g.rows) {
         __shared__ float4 s_head[kSub / 4];
         if (wave == 0) expseg_head(g, logits, w, blockIdx.x, s_tab[0], s_head);
+        if (wave == 1) { // beside it: e_thr for the fast candidate list
+            if (lane < 32) s_tab[1][lane] = kExp2Table[lane];
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+            uint32_t key = 0;
+            const bool ok = fast_threshold(g, w, blockIdx.x, lane, s_tab[1], key);
+            if (lane == 0) {
+                w.sel[blockIdx.x].ethr_key = key;
+                w.sel[blockIdx.x].ethr_on = ok ? 1u : 0u;
+            }
+        }
         return;
     }
     const uint32_t b = blockIdx.x - g.rows;
@@ -946,61 +1020,9 @@ __global__ __launch_bounds__(kBlock) void k_smp_expseg(SmpGeo g, float *logits, 
 // element, adds it with one f32 addition and starts the next round after
 // it.  Each round commits at least one element, so the rounds end.
 
-constexpr uint32_t kFastPer = 8;         // sub-chunk maxima per lane for the fast threshold
 constexpr uint32_t kFastWg = 256;        // fast candidates a k_smp_div workgroup buffers
 constexpr uint32_t kStage = 24;          // walked sub-chunks k_smp_sum's second wave stages in LDS
 
-// The fast candidate threshold, by one wave.  The top_k largest sub-chunk
-// maxima are top_k distinct elements; with e_thr the top_k-th largest of
-// their e (computed as k_smp_expseg computes e), at least top_k elements
-// have e >= e_thr, so p >= p_thr = e_thr / S (the division k_smp_div uses,
-// correctly rounded and so monotone), and every element of the top_k by p
-// -- ties at the boundary included -- has p >= p_thr.  k_smp_div then lists
-// those elements directly.  Returns false when the row cannot take it
-// (three-pass chunks, top_k above kCap or above the sub-chunk count, more
-// than kFastPer sub-chunks per lane).
-__device__ bool fast_threshold(const SmpGeo &g, const SmpWs &w, uint32_t row, uint32_t nslots, uint32_t spc,
-                               uint32_t lane, uint32_t &ethr_key)
-{
-    if (!(g.chunk_cols <= kFuseCols && g.top_k <= kCap && nslots <= kWave * kFastPer)) return false;
-    const SubSum *sub = w.sub + static_cast<uint64_t>(row) * nslots;
-    float mv[kFastPer];
-    bool valid[kFastPer];
-    float M = -__builtin_inff();
-#pragma unroll
-    for (uint32_t j = 0; j < kFastPer; ++j) {
-        const uint32_t slot = lane + kWave * j;
-        valid[j] = false;
-        if (slot < nslots) {
-            uint64_t c0, c1;
-            chunk_range(g, slot / spc, c0, c1);
-            valid[j] = static_cast<uint64_t>(slot % spc) * kSub < c1 - c0; // written by k_smp_max<true>
-        }
-        mv[j] = valid[j] ? sub[slot].m : -__builtin_inff();
-        M = mv[j] > M ? mv[j] : M;
-    }
-    M = wave_max_dpp(M); // the row maximum: every element lies in a sub-chunk
-    const ExpfConsts ec = expf_consts_in_vgprs();
-    uint32_t key[kFastPer];
-    uint32_t nvalid = 0;
-#pragma unroll
-    for (uint32_t j = 0; j < kFastPer; ++j) {
-        key[j] = valid[j] ? total_key(emel_expf(mv[j] - M, kExp2Table, ec)) : 0u; // valid keys are > 0
-        nvalid += static_cast<uint32_t>(__builtin_popcountll(__ballot(valid[j])));
-    }
-    if (nvalid < g.top_k) return false;
-    // the largest t with top_k keys >= t, bit by bit from the top
-    uint32_t t = 0;
-    for (int b = 31; b >= 0; --b) {
-        const uint32_t c = t | (1u << b);
-        uint32_t n = 0;
-#pragma unroll
-        for (uint32_t j = 0; j < kFastPer; ++j) n += static_cast<uint32_t>(__builtin_popcountll(__ballot(key[j] >= c)));
-        if (n >= g.top_k) t = c;
-    }
-    ethr_key = t;
-    return true;
-}
 
 // One wave per row walks (wave 0); wave 1 computes the fast candidate
 // threshold beside it, off the walk's path.  The sub-chunks' predictions are
@@ -1011,16 +1033,124 @@ __device__ bool fast_threshold(const SmpGeo &g, const SmpWs &w, uint32_t row, ui
 // added in one step.  Any other sub-chunk is loaded straight into the
 // walk's registers (lane l holds its elements kPer l .. kPer l + kPer - 1,
 // 128-bit loads in flight) and walked: one round, plus one per event.
+// Per lane of a staged sub-chunk with a usable plan (lower binade u), left
+// by k_smp_sum's second wave: the inclusive wave scans of the lane unit
+// totals at u and at u + 1 (each total capped at 2^24, as the walk's rounds
+// cap them) and whether the lane holds a tie at u (bit 0) or u + 1 (bit 1).
+struct LaneScan {
+    uint32_t incl0, incl1, ties, pad;
+};
+
+// A lane's unit total at 2^u of its elements (capped at 2^24; NaN counts
+// 2^24) and whether one of them is a tie (seq_units).
+__device__ __forceinline__ uint32_t lane_units(const float (&e)[kPer], int32_t u, bool &tie)
+{
+    uint32_t lsum = 0;
+    float dmax = 0.0f;
+#pragma unroll
+    for (uint32_t j = 0; j < kPer; ++j) {
+        float t = __builtin_ldexpf(e[j], -u);
+        t = __builtin_fminf(t, 16777216.0f);
+        const float rt = __builtin_rintf(t);
+        lsum += static_cast<uint32_t>(rt);
+        dmax = __builtin_fmaxf(dmax, __builtin_fabsf(t - rt));
+    }
+    tie = dmax == 0.5f;
+    return lsum < kSeqLimit ? lsum : kSeqLimit;
+}
+
+// One step for a staged sub-chunk whose walk starts in its lower binade u
+// (s.u == u), from the lane scans of its LaneScan entries (ls, this lane's)
+// and its elements in LDS (st, the walk's register layout).  The first event
+// at u -- a tie, or the element whose units reach 2^24 -- lies in the first
+// lane whose tie bit is set or whose scan reaches 2^24 - m; that lane's
+// elements are spread over lanes 0-7 and resolved there, and the event is
+// added with one f32 addition.  When it is the crossing into u + 1, and the
+// rest of the sub-chunk holds no tie at u + 1 and its units there keep the
+// state below 2^24, the state after the sub-chunk follows from the scans at
+// u + 1.  Returns kStepDone with s the state after the sub-chunk, kStepEvent
+// with s the state after element k (the caller walks the elements after
+// it), or kStepNone with s unchanged (a NaN or +inf sum: the caller walks the
+// whole sub-chunk).
+constexpr uint32_t kStepDone = 0, kStepEvent = 1, kStepNone = 2;
+
+// Inclusive prefix sum over lanes 0-7 (row shifts of 1, 2, 4 inside the
+// first row of 16 lanes; the other lanes' results are not used).
+__device__ __forceinline__ uint32_t scan8(uint32_t v)
+{
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x111, 0xf, 0xf, true)); // row_shr:1
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x112, 0xf, 0xf, true)); // row_shr:2
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x114, 0xf, 0xf, true)); // row_shr:4
+    return v;
+}
+
+__device__ __forceinline__ uint32_t crossing_step(const LaneScan &lsr, const float4 (&st)[kPer / 4][kWave], int32_t u,
+                                                  SumState &s, uint32_t &k)
+{
+    static_assert(kPer == 8, "a lane's elements spread over lanes 0-7");
+    const uint32_t lane = threadIdx.x % kWave;
+    // one 128-bit LDS read
+    const uint4 lv = *reinterpret_cast<const uint4 *>(&lsr);
+    const LaneScan ls{lv.x, lv.y, lv.z, lv.w};
+    const uint64_t emask = __ballot((ls.ties & 1u) || s.m + ls.incl0 >= kSeqLimit);
+    if (emask == 0) { // no event at u: the sub-chunk adds its units
+        s.m += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(ls.incl0), kWave - 1));
+        return kStepDone;
+    }
+    const int fl = __builtin_ctzll(emask);
+    // lane fl's elements, element i in lane i (i < 8): one LDS read each
+    const uint32_t i = lane % kPer;
+    const float *stf = reinterpret_cast<const float *>(&st[0][0]);
+    const float ev = stf[((i / 4) * kWave + static_cast<uint32_t>(fl)) * 4 + (i % 4)];
+    const float ei = lane < kPer ? ev : 0.0f;
+    const uint32_t before = fl == 0 ? 0u : static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(ls.incl0), fl - 1));
+    // their units and t - rint(t) at u and at u + 1, with in-lane prefixes
+    auto units = [&](int32_t b, float &d) {
+        float t = __builtin_ldexpf(ei, -b);
+        t = __builtin_fminf(t, 16777216.0f); // also NaN -> 2^24
+        const float rt = __builtin_rintf(t);
+        d = t - rt;
+        return static_cast<uint32_t>(rt);
+    };
+    float d0, d1;
+    const uint32_t r0 = units(u, d0), r1 = units(u + 1, d1);
+    const uint32_t p0 = scan8(r0), p1 = scan8(r1);
+    const uint32_t base = s.m + before;
+    const uint64_t jmask = __ballot(lane < kPer && (__builtin_fabsf(d0) == 0.5f || base + p0 >= kSeqLimit));
+    if (jmask == 0) return kStepNone; // unreachable: lane fl holds an event
+    const int jc = __builtin_ctzll(jmask);
+    const uint32_t run_k = base + static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(p0 - r0), jc));
+    const float e_k = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ei), jc));
+    const float sn = seq_value(run_k, u) + e_k; // the event element: one f32 addition
+    if (!(sn < __builtin_inff())) return kStepNone;
+    const SeqState nx = seq_state(sn);
+    k = kPer * static_cast<uint32_t>(fl) + static_cast<uint32_t>(jc);
+    s.m = nx.m;
+    s.u = nx.u;
+    if (nx.u != u + 1) return kStepEvent;
+    // the rest at u + 1: lane fl's elements after jc, then the lanes after fl
+    const uint32_t in_lane = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(p1), kPer - 1)) -
+                             static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(p1), jc));
+    const uint32_t total1 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(ls.incl1), kWave - 1));
+    const uint32_t upto1 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(ls.incl1), fl));
+    const uint64_t t1in = __ballot(lane < kPer && __builtin_fabsf(d1) == 0.5f) >> (jc + 1);
+    const uint64_t t1out = __ballot(lane > static_cast<uint32_t>(fl) && (ls.ties & 2u));
+    const uint64_t rest = static_cast<uint64_t>(in_lane) + (total1 - upto1);
+    if (t1in != 0 || t1out != 0 || s.m + rest >= kSeqLimit) return kStepEvent;
+    s.m += static_cast<uint32_t>(rest);
+    return kStepDone;
+}
+
 constexpr uint32_t kSumThreads = 2 * kWave;
 
 __global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *logits, SmpWs w)
 {
-    __shared__ uint32_t s_fast[2]; // wave 1's threshold: taken, e_thr's key
     // wave 1 stages the walk-marked sub-chunks: s_stage[i] holds the i-th
     // of them (in slot order) as the walk's registers hold it (float4 q of
     // lane l at [i][q][l]); s_ready counts the staged ones (release /
     // acquire)
     __shared__ float4 s_stage[kStage][kPer / 4][kWave];
+    __shared__ LaneScan s_lanes[kStage][kWave]; // with a usable plan: the lane scans (crossing_step)
     __shared__ uint32_t s_ready;
     const uint32_t row = blockIdx.x;
     const uint32_t lane = threadIdx.x % kWave;
@@ -1091,11 +1221,12 @@ __global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *
         uint32_t nst = 0;
         for (uint32_t kb = 0; kb < nslots && nst < kStage; kb += kWave) {
             const uint32_t sl = kb + lane;
-            bool need = false;
-            if (sl < nslots && sl != 0) need = (seg[sl].flags & (kSegWalk | kSegEmpty)) == kSegWalk;
-            uint64_t m = __ballot(need);
+            SegInfo si{0, 0, kSegEmpty, 0};
+            if (sl < nslots && sl != 0) si = seg[sl];
+            uint64_t m = __ballot((si.flags & (kSegWalk | kSegEmpty)) == kSegWalk);
             while (m != 0 && nst < kStage) {
-                const uint32_t slot = kb + static_cast<uint32_t>(__builtin_ctzll(m));
+                const int bit = __builtin_ctzll(m);
+                const uint32_t slot = kb + static_cast<uint32_t>(bit);
                 m &= m - 1;
                 float e[kPer];
                 uint32_t n;
@@ -1103,19 +1234,23 @@ __global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *
 #pragma unroll
                 for (uint32_t q = 0; q < kPer / 4; ++q)
                     s_stage[nst][q][lane] = make_float4(e[4 * q], e[4 * q + 1], e[4 * q + 2], e[4 * q + 3]);
+                const uint32_t sf = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(si.flags), bit));
+                if (sf & kSegHasU) { // the lane scans at its two binades
+                    const int32_t su = __builtin_amdgcn_readlane(si.u, bit);
+                    bool t0, t1;
+                    const uint32_t x0 = lane_units(e, su, t0);
+                    const uint32_t x1 = lane_units(e, su + 1, t1);
+                    s_lanes[nst][lane] = LaneScan{wave_incl_scan(x0), wave_incl_scan(x1),
+                                                  static_cast<uint32_t>(t0) | (static_cast<uint32_t>(t1) << 1), 0u};
+                }
                 ++nst;
                 if (lane == 0) __hip_atomic_store(&s_ready, nst, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
             }
         }
-        uint32_t ethr_key = 0;
-        const bool fast = fast_threshold(g, w, row, nslots, spc, lane, ethr_key);
-        if (lane == 0) {
-            s_fast[0] = fast ? 1u : 0u;
-            s_fast[1] = ethr_key;
-        }
     } else { // wave 0: the walk
     bool nan_final = false;
     uint32_t marked = 0; // walk-marked slots before this batch: wave 1 stages them in this order
+    uint32_t ready = 0;  // staged slots known to be ready (s_ready only grows)
     SegInfo nxt{0, 0, kSegEmpty, 0};
     if (lane < nslots) nxt = seg[lane];
     for (uint32_t kb = 0; kb < nslots && !nan_final; kb += kWave) {
@@ -1181,16 +1316,28 @@ __global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *
             float e[kPer];
             bool staged = false;
             const uint32_t sidx = marked + static_cast<uint32_t>(__builtin_popcountll(wmask & ((uint64_t{1} << f) - 1u)));
-            if ((wmask >> f) & 1u)
-                staged = sidx < __hip_atomic_load(&s_ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if ((wmask >> f) & 1u) {
+                if (sidx >= ready) ready = __hip_atomic_load(&s_ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+                staged = sidx < ready;
+            }
             if (staged) {
+                // in its lower binade, a staged sub-chunk with lane scans
+                // crosses in one step (crossing_step)
+                const int32_t su = __builtin_amdgcn_readlane(mine.u, f);
+                const uint32_t sf = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(mine.flags), f));
+                uint32_t k = kSub;
+                uint32_t step = kStepNone;
+                if ((sf & kSegHasU) && s.finite && su == s.u) step = crossing_step(s_lanes[sidx][lane], s_stage[sidx], su, s, k);
+                if (step == kStepDone || (step == kStepEvent && k + 1 >= kSub)) continue;
+                // the elements after k when an event was taken, else all
+                const int32_t kk = step == kStepEvent ? static_cast<int32_t>(k) - static_cast<int32_t>(kPer * lane) : -1;
 #pragma unroll
                 for (uint32_t q = 0; q < kPer / 4; ++q) {
                     const float4 v = s_stage[sidx][q][lane];
-                    e[4 * q] = v.x;
-                    e[4 * q + 1] = v.y;
-                    e[4 * q + 2] = v.z;
-                    e[4 * q + 3] = v.w;
+                    e[4 * q] = static_cast<int32_t>(4 * q) <= kk ? 0.0f : v.x;
+                    e[4 * q + 1] = static_cast<int32_t>(4 * q + 1) <= kk ? 0.0f : v.y;
+                    e[4 * q + 2] = static_cast<int32_t>(4 * q + 2) <= kk ? 0.0f : v.z;
+                    e[4 * q + 3] = static_cast<int32_t>(4 * q + 3) <= kk ? 0.0f : v.w;
                 }
             } else {
                 uint32_t n;
@@ -1200,16 +1347,16 @@ __global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *
         }
         marked += static_cast<uint32_t>(__builtin_popcountll(wmask));
     }
-    } // wave 0
-    __syncthreads(); // both waves: wave 1's threshold is in s_fast
-    if (threadIdx.x == 0) {
+    if (lane == 0) {
         const float S = s.finite ? seq_value(s.m, s.u) : s.special;
         w.sel[row].total = S;
-        if (s_fast[0] && s.finite) { // a NaN or +inf sum takes the radix path
-            w.sel[row].fast_key = total_key(div_by_recip(from_key(s_fast[1]), 1.0 / static_cast<double>(S)));
+        // p_thr = e_thr / S, as k_smp_div divides (a NaN or +inf sum takes the radix path)
+        if (w.sel[row].ethr_on && s.finite) {
+            w.sel[row].fast_key = total_key(div_by_recip(from_key(w.sel[row].ethr_key), 1.0 / static_cast<double>(S)));
             w.sel[row].fast_on = 1u;
         }
     }
+    } // wave 0
 }
 
 // ---- stage 4: p = e / S in place, first radix digit -------------------------

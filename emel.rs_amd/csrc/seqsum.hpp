@@ -141,7 +141,11 @@ struct SumState {
 // Otherwise the first event lies in the first lane that holds a tie or whose
 // running units reach 2^24; that lane's elements are then read one by one on
 // the scalar unit up to the event, which is added with one f32 addition, and
-// the next round starts after it.
+// the next round starts after it.  A single wave issues these instructions
+// one at a time, so every round is kept to few of them: committed elements
+// are zeroed once per event (a zero adds no units and is no tie), and a tie
+// is found from t - rint(t), which is exactly +-1/2 for a tie and smaller
+// otherwise, one maximum per lane.
 template <uint32_t PER>
 __device__ __forceinline__ void sum_tile(const float (&e)[PER], SumState &s)
 {
@@ -154,30 +158,24 @@ __device__ __forceinline__ void sum_tile(const float (&e)[PER], SumState &s)
         if (__ballot(nan)) s.special = __builtin_nanf("");
         return;
     }
-    uint32_t start = 0; // tile-relative index of the first uncommitted element
+    float x[PER]; // e, with the committed elements zeroed
+#pragma unroll
+    for (uint32_t j = 0; j < PER; ++j) x[j] = e[j];
     while (true) {
-        // this round's units at the current binade (0 for committed
-        // elements), kept for the event search below
-        uint32_t r[PER];
-        uint32_t lsum = 0, ties = 0;
-        if (start == 0) {
+        // this round's units at the current binade (seq_units: the clamp
+        // also takes NaN to 2^24 units, an event), kept with t - rint(t)
+        // for the event search below
+        uint32_t r[PER], lsum = 0;
+        float d[PER], dmax = 0.0f;
 #pragma unroll
-            for (uint32_t j = 0; j < PER; ++j) {
-                bool tie;
-                r[j] = seq_units(e[j], s.u, tie);
-                lsum += r[j];
-                ties |= static_cast<uint32_t>(tie) << j;
-            }
-        } else { // elements before start are committed
-#pragma unroll
-            for (uint32_t j = 0; j < PER; ++j) {
-                bool tie;
-                const uint32_t q = seq_units(e[j], s.u, tie);
-                const bool active = PER * lane + j >= start;
-                r[j] = active ? q : 0u;
-                lsum += r[j];
-                ties |= static_cast<uint32_t>(active && tie) << j;
-            }
+        for (uint32_t j = 0; j < PER; ++j) {
+            float t = __builtin_ldexpf(x[j], -s.u);
+            t = __builtin_fminf(t, 16777216.0f); // IEEE minNum: also NaN -> 2^24
+            const float rt = __builtin_rintf(t);
+            d[j] = t - rt; // exact: t and rint(t) are within 1/2
+            r[j] = static_cast<uint32_t>(rt);
+            lsum += r[j];
+            dmax = __builtin_fmaxf(dmax, __builtin_fabsf(d[j]));
         }
         // lsum <= PER * 2^24; saturated at 2^24 the scan cannot overflow (a
         // saturated value already marks a crossing)
@@ -185,27 +183,27 @@ __device__ __forceinline__ void sum_tile(const float (&e)[PER], SumState &s)
         const uint32_t incl = wave_incl_scan(x_in);
         // lanes before the first event lane neither tie nor reach 2^24, so
         // its running units before it are s.m plus its exclusive prefix
-        const uint64_t emask = __ballot(ties != 0u || s.m + incl >= kSeqLimit);
+        const uint64_t emask = __ballot(dmax == 0.5f || s.m + incl >= kSeqLimit);
         if (emask == 0) { // no event: the tile is committed
             s.m += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), kWave - 1));
             return;
         }
         const int fl = __builtin_ctzll(emask);
         uint32_t run = s.m + static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl - x_in), fl));
-        const uint32_t tl = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(ties), fl));
-        // lane fl's elements in order, on the scalar unit: the first tie, or
-        // the first element whose units reach 2^24 (committed elements add
-        // 0 units and hold no tie)
+        // lane fl's elements in order, on the scalar unit: the first tie
+        // (|t - rint(t)| = 1/2), or the first element whose units reach 2^24
+        // (zeroed elements add 0 units and hold no tie)
         uint32_t k = PER * kWave, run_k = 0;
         float e_k = 0.0f;
 #pragma unroll
         for (uint32_t j = 0; j < PER; ++j) {
             if (k == PER * kWave) {
                 const uint32_t rj = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(r[j]), fl));
-                if (((tl >> j) & 1u) || run + rj >= kSeqLimit) {
+                const uint32_t dj = static_cast<uint32_t>(__builtin_amdgcn_readlane(__builtin_bit_cast(int, d[j]), fl));
+                if ((dj & 0x7fffffffu) == 0x3f000000u || run + rj >= kSeqLimit) {
                     k = PER * static_cast<uint32_t>(fl) + j;
                     run_k = run;
-                    e_k = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e[j]), fl));
+                    e_k = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x[j]), fl));
                 } else {
                     run += rj;
                 }
@@ -225,8 +223,11 @@ __device__ __forceinline__ void sum_tile(const float (&e)[PER], SumState &s)
         const SeqState st = seq_state(sn);
         s.m = st.m;
         s.u = st.u;
-        start = k + 1;
-        if (start >= PER * kWave) return;
+        if (k + 1 >= PER * kWave) return;
+        // elements up to k are committed
+        const int32_t kk = static_cast<int32_t>(k) - static_cast<int32_t>(PER * lane);
+#pragma unroll
+        for (uint32_t j = 0; j < PER; ++j) x[j] = static_cast<int32_t>(j) <= kk ? 0.0f : x[j];
     }
 }
 
