@@ -1059,9 +1059,9 @@ __device__ __forceinline__ uint32_t lane_units(const float (&e)[kPer], int32_t u
     return lsum < kSeqLimit ? lsum : kSeqLimit;
 }
 
-// One step for a staged sub-chunk whose walk starts in its lower binade u
-// (s.u == u), from the lane scans of its LaneScan entries (ls, this lane's)
-// and its elements in LDS (st, the walk's register layout).  The first event
+// One step for a sub-chunk whose walk starts in its lower binade u (s.u ==
+// u), from its lane scans (ls, this lane's) and its elements in LDS (st, the
+// walk's register layout).  The first event
 // at u -- a tie, or the element whose units reach 2^24 -- lies in the first
 // lane whose tie bit is set or whose scan reaches 2^24 - m; that lane's
 // elements are spread over lanes 0-7 and resolved there, and the event is
@@ -1084,14 +1084,11 @@ __device__ __forceinline__ uint32_t scan8(uint32_t v)
     return v;
 }
 
-__device__ __forceinline__ uint32_t crossing_step(const LaneScan &lsr, const float4 (&st)[kPer / 4][kWave], int32_t u,
+__device__ __forceinline__ uint32_t crossing_step(const LaneScan ls, const float4 (&st)[kPer / 4][kWave], int32_t u,
                                                   SumState &s, uint32_t &k)
 {
     static_assert(kPer == 8, "a lane's elements spread over lanes 0-7");
     const uint32_t lane = threadIdx.x % kWave;
-    // one 128-bit LDS read
-    const uint4 lv = *reinterpret_cast<const uint4 *>(&lsr);
-    const LaneScan ls{lv.x, lv.y, lv.z, lv.w};
     const uint64_t emask = __ballot((ls.ties & 1u) || s.m + ls.incl0 >= kSeqLimit);
     if (emask == 0) { // no event at u: the sub-chunk adds its units
         s.m += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(ls.incl0), kWave - 1));
@@ -1151,6 +1148,7 @@ __global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *
     // acquire)
     __shared__ float4 s_stage[kStage][kPer / 4][kWave];
     __shared__ LaneScan s_lanes[kStage][kWave]; // with a usable plan: the lane scans (crossing_step)
+    __shared__ float4 s_own[kPer / 4][kWave];   // wave 0: a sub-chunk it loaded, for crossing_step
     __shared__ uint32_t s_ready;
     const uint32_t row = blockIdx.x;
     const uint32_t lane = threadIdx.x % kWave;
@@ -1251,6 +1249,8 @@ __global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *
     bool nan_final = false;
     uint32_t marked = 0; // walk-marked slots before this batch: wave 1 stages them in this order
     uint32_t ready = 0;  // staged slots known to be ready (s_ready only grows)
+    uint32_t pre_slot = kNone; // prefetched into pre_e
+    float pre_e[kPer];
     SegInfo nxt{0, 0, kSegEmpty, 0};
     if (lane < nslots) nxt = seg[lane];
     for (uint32_t kb = 0; kb < nslots && !nan_final; kb += kWave) {
@@ -1259,6 +1259,11 @@ __global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *
         const uint32_t nb = nslots - kb < kWave ? nslots - kb : kWave;
         const uint64_t wmask =
             __ballot(lane < nb && kb + lane != 0 && (mine.flags & (kSegWalk | kSegEmpty)) == kSegWalk);
+        if (kb == 0 && wmask != 0) { // the first walk-marked slot: usually reached before wave 1 stages it
+            pre_slot = static_cast<uint32_t>(__builtin_ctzll(wmask));
+            uint32_t n;
+            load_slot(pre_slot, pre_e, n);
+        }
         uint32_t i = 0; // next slot of the batch
         while (i < nb) {
             // Take the run of slots from i on that need no decision: empty
@@ -1312,7 +1317,8 @@ __global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *
                 break;
             }
             // slot f is walked: from LDS when wave 1 has staged it (the
-            // staged slots are the walk-marked ones, in slot order)
+            // staged slots are the walk-marked ones, in slot order), else
+            // from the prefetch or a load of its own
             float e[kPer];
             bool staged = false;
             const uint32_t sidx = marked + static_cast<uint32_t>(__builtin_popcountll(wmask & ((uint64_t{1} << f) - 1u)));
@@ -1320,28 +1326,55 @@ __global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *
                 if (sidx >= ready) ready = __hip_atomic_load(&s_ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
                 staged = sidx < ready;
             }
+            // in its lower binade, a sub-chunk with a usable plan crosses in
+            // one step (crossing_step)
+            const int32_t su = __builtin_amdgcn_readlane(mine.u, f);
+            const uint32_t sf = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(mine.flags), f));
+            const bool one_step = (sf & kSegHasU) && s.finite && su == s.u;
+            uint32_t k = kSub;
+            uint32_t step = kStepNone;
             if (staged) {
-                // in its lower binade, a staged sub-chunk with lane scans
-                // crosses in one step (crossing_step)
-                const int32_t su = __builtin_amdgcn_readlane(mine.u, f);
-                const uint32_t sf = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(mine.flags), f));
-                uint32_t k = kSub;
-                uint32_t step = kStepNone;
-                if ((sf & kSegHasU) && s.finite && su == s.u) step = crossing_step(s_lanes[sidx][lane], s_stage[sidx], su, s, k);
-                if (step == kStepDone || (step == kStepEvent && k + 1 >= kSub)) continue;
-                // the elements after k when an event was taken, else all
-                const int32_t kk = step == kStepEvent ? static_cast<int32_t>(k) - static_cast<int32_t>(kPer * lane) : -1;
+                if (one_step) {
+                    const uint4 lv = *reinterpret_cast<const uint4 *>(&s_lanes[sidx][lane]); // one 128-bit read
+                    step = crossing_step(LaneScan{lv.x, lv.y, lv.z, lv.w}, s_stage[sidx], su, s, k);
+                }
+                if (step == kStepDone) continue;
 #pragma unroll
                 for (uint32_t q = 0; q < kPer / 4; ++q) {
                     const float4 v = s_stage[sidx][q][lane];
-                    e[4 * q] = static_cast<int32_t>(4 * q) <= kk ? 0.0f : v.x;
-                    e[4 * q + 1] = static_cast<int32_t>(4 * q + 1) <= kk ? 0.0f : v.y;
-                    e[4 * q + 2] = static_cast<int32_t>(4 * q + 2) <= kk ? 0.0f : v.z;
-                    e[4 * q + 3] = static_cast<int32_t>(4 * q + 3) <= kk ? 0.0f : v.w;
+                    e[4 * q] = v.x;
+                    e[4 * q + 1] = v.y;
+                    e[4 * q + 2] = v.z;
+                    e[4 * q + 3] = v.w;
                 }
             } else {
-                uint32_t n;
-                load_slot(kb + f, e, n);
+                if (kb + f == pre_slot) {
+#pragma unroll
+                    for (uint32_t j = 0; j < kPer; ++j) e[j] = pre_e[j];
+                } else {
+                    uint32_t n;
+                    load_slot(kb + f, e, n);
+                }
+                if (one_step) { // the lane scans here; the elements into s_own for the spread
+#pragma unroll
+                    for (uint32_t q = 0; q < kPer / 4; ++q)
+                        s_own[q][lane] = make_float4(e[4 * q], e[4 * q + 1], e[4 * q + 2], e[4 * q + 3]);
+                    bool t0, t1;
+                    const uint32_t x0 = lane_units(e, su, t0);
+                    const uint32_t x1 = lane_units(e, su + 1, t1);
+                    const LaneScan ls{wave_incl_scan(x0), wave_incl_scan(x1),
+                                      static_cast<uint32_t>(t0) | (static_cast<uint32_t>(t1) << 1), 0u};
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+                    __builtin_amdgcn_wave_barrier();
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+                    step = crossing_step(ls, s_own, su, s, k);
+                }
+            }
+            if (step == kStepDone || (step == kStepEvent && k + 1 >= kSub)) continue;
+            if (step == kStepEvent) { // the elements after k remain
+                const int32_t kk = static_cast<int32_t>(k) - static_cast<int32_t>(kPer * lane);
+#pragma unroll
+                for (uint32_t j = 0; j < kPer; ++j) e[j] = static_cast<int32_t>(j) <= kk ? 0.0f : e[j];
             }
             sum_tile<kPer>(e, s);
         }
