@@ -41,23 +41,27 @@
 //   k_smp_div     (row, chunk): p written in place, plus the histogram of the
 //                 top 11 bits of p's total-order key, and the list of every
 //                 p >= p_thr.  A row whose list fits 8192 entries is ranked
-//                 from it (mode 3): resolve and collect skip it.
-//   k_smp_resolve one workgroup per row: radix selection of the top_k-th
-//                 key, 11, 11, 10 key bits.  A row stops as soon as every
-//                 key at or above its current prefix fits the kCap
-//                 candidates one workgroup sorts; at 32 bits the threshold
-//                 key T is exact and the elements equal to T are counted
-//                 per chunk.
-//   k_smp_collect (row, chunk): candidates (key, index) into a per-row list:
-//                 every key >= prefix, or every key > T plus the lowest-index
-//                 ties at T up to top_k.
-//   k_smp_rank    one workgroup per row: sort of the candidates in LDS
-//                 (key descending then index ascending: register runs merged
-//                 by merge path), the ranked outputs, then the race
-//                 selection.
-// Lists longer than kCap (top_k > kCap) are sorted as kCap tiles
-// (k_smp_tile_sort), merged pairwise (k_smp_merge), and finished by
-// k_smp_finish.
+//                 from it.
+//   k_smp_tail    (when the fast list applies: top_k at most the row's
+//                 sub-chunk count) one 1024-thread workgroup per row, in one
+//                 launch:
+//                 - rows the fast list did not resolve: radix selection of
+//                   the top_k-th key, 11, 11, 10 key bits (the first digit
+//                   from k_smp_div's histogram, later ones from scans of the
+//                   row), stopping as soon as every key at or above the
+//                   current prefix fits the kCap candidates one workgroup
+//                   sorts; at 32 bits the threshold key T is exact.  Then the
+//                   candidate list (key, index) in column order: every key >=
+//                   prefix, or every key > T plus the lowest-index ties at T
+//                   up to top_k;
+//                 - every row: sort of the candidates in LDS (key descending
+//                   then index ascending: register runs merged by merge
+//                   path), the ranked outputs, then the race selection.
+// Otherwise the selection runs as k_smp_resolve (one workgroup per row, the
+// ties at T counted per chunk) and k_smp_collect ((row, chunk) workgroups),
+// and k_smp_rank ranks (top_k <= kCap); for top_k > kCap the list is sorted
+// as kCap tiles (k_smp_tile_sort), merged pairwise (k_smp_merge), and
+// finished by k_smp_finish.
 //
 // Ties of p: the reference sorts with sort_unstable_by, which leaves the
 // order of equal probabilities unspecified; here they rank by ascending
@@ -816,11 +820,22 @@ constexpr uint32_t kFastBits = 14;       // low key bits the fast threshold leav
 // those elements directly.  Returns false when the row cannot take it
 // (three-pass chunks, top_k above kCap or above the sub-chunk count, more
 // than kFastPer sub-chunks per lane).
+// Whether a launch's rows can take the fast list: the fused path, top_k
+// within kCap and within the row's sub-chunk count, at most kFastPer
+// sub-chunks per lane.
+__host__ __device__ inline bool fast_list_possible(const SmpGeo &g)
+{
+    const uint64_t spc = (g.chunk_cols + kSub - 1) / kSub, nslots = uint64_t{g.chunks} * spc;
+    const uint64_t last = g.card - uint64_t{g.chunks - 1} * g.chunk_cols;
+    const uint64_t nsub = uint64_t{g.chunks - 1} * spc + (last + kSub - 1) / kSub; // sub-chunks with elements
+    return g.chunk_cols <= kFuseCols && g.top_k <= kCap && nslots <= kWave * kFastPer && nsub >= g.top_k;
+}
+
 __device__ bool fast_threshold(const SmpGeo &g, const SmpWs &w, uint32_t row, uint32_t lane, const uint64_t *tab,
                                uint32_t &ethr_key)
 {
     const uint32_t spc = subs_per_chunk(g), nslots = g.chunks * spc;
-    if (!(g.chunk_cols <= kFuseCols && g.top_k <= kCap && nslots <= kWave * kFastPer)) return false;
+    if (!fast_list_possible(g)) return false;
     const SubSum *sub = w.sub + static_cast<uint64_t>(row) * nslots;
     // only the last chunk can hold empty slots: its first `tail` slots are written
     const uint32_t last = (g.chunks - 1) * spc;
@@ -1554,21 +1569,14 @@ __device__ RowSel pick_digit(const RowSel &sel, const uint32_t *hist, uint32_t b
     return n;
 }
 
-__global__ __launch_bounds__(kResolveThreads) void k_smp_resolve(SmpGeo g, float *logits, SmpWs w)
+// The radix selection of one row (mode 0, not resolved by the fast list) by
+// one 1024-thread workgroup: the first digit from k_smp_div's histogram (or
+// from a scan, for a fast row whose list overflowed), later digits from
+// scans of the row, and at an exact threshold the ties per chunk (w.ties).
+// Leaves the row's RowSel (mode 1 or 2) in w.sel and returns it.
+__device__ RowSel resolve_row(const SmpGeo &g, float *logits, const SmpWs &w, uint32_t row, RowSel sel,
+                              uint32_t *s_hist, uint32_t *s_tmp, uint32_t *s_pick)
 {
-    __shared__ uint32_t s_hist[kBins]; // digit histogram; later the per-chunk tie counts
-    __shared__ uint32_t s_tmp[kResolveThreads / kWave];
-    __shared__ uint32_t s_pick[3];
-    const uint32_t row = blockIdx.x;
-    RowSel sel = w.sel[row];
-    if (sel.mode != 0) return; // uniform
-    if (sel.fast_on && sel.fast_count <= kCap) { // uniform: k_smp_div listed the candidates
-        if (threadIdx.x == 0) {
-            w.sel[row].count = sel.fast_count; // >= top_k: the maxima behind the threshold
-            w.sel[row].mode = 3;
-        }
-        return;
-    }
     float *x = logits + static_cast<int64_t>(row) * g.ld;
     if (!sel.fast_on) {
         sel = pick_digit(sel, w.hist + static_cast<uint64_t>(row) * kBins, 11, s_tmp, s_pick);
@@ -1608,6 +1616,27 @@ __global__ __launch_bounds__(kResolveThreads) void k_smp_resolve(SmpGeo g, float
             w.ties[static_cast<uint64_t>(row) * g.chunks + c] = s_hist[c];
     }
     if (threadIdx.x == 0) w.sel[row] = sel;
+    return sel;
+}
+
+// Rows of a top_k above kCap (the merge path): k_smp_resolve, k_smp_collect
+// and the merge kernels.  Other rows take k_smp_tail.
+__global__ __launch_bounds__(kResolveThreads) void k_smp_resolve(SmpGeo g, float *logits, SmpWs w)
+{
+    __shared__ uint32_t s_hist[kBins]; // digit histogram; later the per-chunk tie counts
+    __shared__ uint32_t s_tmp[kResolveThreads / kWave];
+    __shared__ uint32_t s_pick[3];
+    const uint32_t row = blockIdx.x;
+    const RowSel sel = w.sel[row];
+    if (sel.mode != 0) return; // uniform
+    if (sel.fast_on && sel.fast_count <= kCap) { // uniform: k_smp_div listed the candidates
+        if (threadIdx.x == 0) {
+            w.sel[row].count = sel.fast_count; // >= top_k: the maxima behind the threshold
+            w.sel[row].mode = 3;
+        }
+        return;
+    }
+    (void)resolve_row(g, logits, w, row, sel, s_hist, s_tmp, s_pick);
 }
 
 // ---- stage 8: candidates ------------------------------------------------------
@@ -1916,12 +1945,13 @@ __device__ __forceinline__ void stage_words(uint64_t *s, const uint64_t *c, uint
 }
 
 // Candidate lists of at most kCap: one workgroup sorts a row in LDS.
-__global__ __launch_bounds__(kRankThreads) void k_smp_rank(SmpGeo g, SmpWs w, SmpOut o, SmpStates st, uint32_t row0)
+// The ranking of one row's candidate list (count words in w.cand) by one
+// 1024-thread workgroup: the LDS sort, the ranked outputs and the race
+// (random state s0).
+__device__ void rank_row(const SmpGeo &g, const SmpWs &w, const SmpOut &o, uint32_t s0, uint32_t row, uint32_t count,
+                         uint64_t *s_c)
 {
-    __shared__ uint64_t s_c[kCapSlots];
-    const uint32_t row = row0 + blockIdx.x;
-    const uint32_t count = w.sel[row].count; // top_k <= count <= kCap here
-    const uint32_t n = count < kCap ? count : kCap;
+    const uint32_t n = count < kCap ? count : kCap; // top_k <= count <= kCap here
     uint32_t np = kSortPer;
     while (np < n || np < g.top_k) np <<= 1;
     const uint64_t *list = w.cand + static_cast<uint64_t>(row) * g.cand_ld;
@@ -1931,7 +1961,7 @@ __global__ __launch_bounds__(kRankThreads) void k_smp_rank(SmpGeo g, SmpWs w, Sm
         lds_sort_desc<kWave>(s_c, np);
         if (threadIdx.x < g.top_k) write_ranked(g, o, row, threadIdx.x, s_c[slot(threadIdx.x)]);
         select_slots<kWave>(
-            g, row, st.v[blockIdx.x], [&](uint32_t j) { return from_key(static_cast<uint32_t>(s_c[slot(j)] >> 32)); },
+            g, row, s0, [&](uint32_t j) { return from_key(static_cast<uint32_t>(s_c[slot(j)] >> 32)); },
             [&](uint32_t j) { return static_cast<int32_t>(~static_cast<uint32_t>(s_c[slot(j)])); }, o);
         return;
     }
@@ -1939,8 +1969,114 @@ __global__ __launch_bounds__(kRankThreads) void k_smp_rank(SmpGeo g, SmpWs w, Sm
     lds_sort_desc<kRankThreads>(s_c, np);
     for (uint32_t j = threadIdx.x; j < g.top_k; j += blockDim.x) write_ranked(g, o, row, j, s_c[slot(j)]);
     select_slots<kRankThreads>(
-        g, row, st.v[blockIdx.x], [&](uint32_t j) { return from_key(static_cast<uint32_t>(s_c[slot(j)] >> 32)); },
+        g, row, s0, [&](uint32_t j) { return from_key(static_cast<uint32_t>(s_c[slot(j)] >> 32)); },
         [&](uint32_t j) { return static_cast<int32_t>(~static_cast<uint32_t>(s_c[slot(j)])); }, o);
+}
+
+// The candidate list of one row (mode 1 or 2) by one 1024-thread workgroup,
+// in column order: the selection of k_smp_collect, the ties at T taken while
+// fewer than `need` precede them.  Each thread takes 16 consecutive columns
+// per step (their four float4 loads in flight together); one workgroup
+// prefix sum per step places the candidates (and one more counts the ties).
+constexpr uint32_t kTailPer = 16;
+__device__ void collect_row(const SmpGeo &g, const float *x, uint64_t *list, const RowSel &sel, uint32_t *s_tmp)
+{
+    const bool exact = sel.mode == 2;
+    const uint32_t T = sel.prefix;
+    const uint32_t dshift = 32u - sel.depth;
+    uint32_t written = 0, ties = 0;
+    for (uint64_t blk = 0; blk < g.card; blk += kTailPer * kRankThreads) {
+        const uint64_t col0 = blk + kTailPer * static_cast<uint64_t>(threadIdx.x);
+        uint32_t key[kTailPer];
+        bool in[kTailPer];
+        if (g.vec && col0 + kTailPer <= g.card) {
+            float4 q[kTailPer / 4];
+#pragma unroll
+            for (uint32_t j = 0; j < kTailPer / 4; ++j) q[j] = *reinterpret_cast<const float4 *>(x + col0 + 4 * j);
+#pragma unroll
+            for (uint32_t j = 0; j < kTailPer / 4; ++j) {
+                key[4 * j] = total_key(q[j].x);
+                key[4 * j + 1] = total_key(q[j].y);
+                key[4 * j + 2] = total_key(q[j].z);
+                key[4 * j + 3] = total_key(q[j].w);
+            }
+#pragma unroll
+            for (uint32_t j = 0; j < kTailPer; ++j) in[j] = true;
+        } else {
+#pragma unroll
+            for (uint32_t j = 0; j < kTailPer; ++j) {
+                in[j] = col0 + j < g.card;
+                key[j] = in[j] ? total_key(x[col0 + j]) : 0u;
+            }
+        }
+        bool take[kTailPer];
+        if (!exact) {
+#pragma unroll
+            for (uint32_t j = 0; j < kTailPer; ++j) take[j] = in[j] && (key[j] >> dshift) >= T;
+        } else {
+            uint32_t nt = 0;
+#pragma unroll
+            for (uint32_t j = 0; j < kTailPer; ++j) nt += (in[j] && key[j] == T) ? 1u : 0u;
+            uint32_t step_ties;
+            const uint32_t incl = block_incl_scan1024(nt, s_tmp, step_ties);
+            uint32_t rank = ties + incl - nt;
+#pragma unroll
+            for (uint32_t j = 0; j < kTailPer; ++j) {
+                const bool tie = in[j] && key[j] == T;
+                take[j] = (in[j] && key[j] > T) || (tie && rank < sel.need);
+                rank += tie ? 1u : 0u;
+            }
+            ties += step_ties;
+        }
+        uint32_t nc = 0;
+#pragma unroll
+        for (uint32_t j = 0; j < kTailPer; ++j) nc += take[j] ? 1u : 0u;
+        uint32_t step_total;
+        const uint32_t cincl = block_incl_scan1024(nc, s_tmp, step_total);
+        uint32_t slot = written + cincl - nc;
+#pragma unroll
+        for (uint32_t j = 0; j < kTailPer; ++j) {
+            // the selection counts exactly `count` <= cand_ld candidates; the
+            // bound only keeps a miscount from writing outside the row's list
+            if (take[j] && slot < g.cand_ld) list[slot] = cand_word(key[j], static_cast<uint32_t>(col0 + j));
+            slot += take[j] ? 1u : 0u;
+        }
+        written += step_total;
+    }
+}
+
+__global__ __launch_bounds__(kRankThreads) void k_smp_rank(SmpGeo g, SmpWs w, SmpOut o, SmpStates st, uint32_t row0)
+{
+    __shared__ uint64_t s_c[kCapSlots];
+    const uint32_t row = row0 + blockIdx.x;
+    rank_row(g, w, o, st.v[blockIdx.x], row, w.sel[row].count, s_c);
+}
+
+// A launch whose rows can take the fast list: one workgroup per row
+// resolves, collects and ranks it in one launch.  A row the fast list resolved (k_smp_div listed it) goes
+// straight to the ranking; the others take the radix selection, then the
+// candidate list in column order.
+static_assert(kRankThreads == kResolveThreads, "one workgroup shape for the whole tail");
+__global__ __launch_bounds__(kRankThreads) void k_smp_tail(SmpGeo g, float *logits, SmpWs w, SmpOut o, SmpStates st,
+                                                           uint32_t row0)
+{
+    __shared__ uint64_t s_c[kCapSlots];
+    __shared__ uint32_t s_hist[kBins];
+    __shared__ uint32_t s_tmp[kRankThreads / kWave];
+    __shared__ uint32_t s_pick[3];
+    const uint32_t row = row0 + blockIdx.x;
+    const RowSel sel0 = w.sel[row];
+    uint32_t count;
+    if (sel0.fast_on && sel0.fast_count <= kCap) { // uniform: k_smp_div listed the candidates
+        count = sel0.fast_count; // >= top_k: the maxima behind the threshold
+    } else {
+        const RowSel sel = resolve_row(g, logits, w, row, sel0, s_hist, s_tmp, s_pick);
+        collect_row(g, logits + static_cast<int64_t>(row) * g.ld, w.cand + static_cast<uint64_t>(row) * g.cand_ld, sel,
+                    s_tmp);
+        count = sel.count;
+        __syncthreads(); // the list, written by the whole workgroup, is read by the ranking
+    }
+    rank_row(g, w, o, st.v[blockIdx.x], row, count, s_c);
 }
 
 // Longer lists (top_k > kCap, so count == top_k): sorted kCap tiles ...
@@ -2167,8 +2303,15 @@ hipError_t launch_sampler(const SamplerArgs &a, hipStream_t s)
     }
     k_smp_sum<<<a.rows, kSumThreads, 0, s>>>(g, a.logits, w);
     k_smp_div<<<grid, kBlock, 0, s>>>(g, a.logits, w);
-    k_smp_resolve<<<a.rows, kResolveThreads, 0, s>>>(g, a.logits, w);
-    k_smp_collect<<<grid, kBlock, 0, s>>>(g, a.logits, w);
+    // Rows resolved by the fast list need no selection: when the fast list
+    // applies, k_smp_tail selects (in one workgroup per row, for the rows it
+    // left) and ranks in one launch; otherwise every row takes the selection
+    // kernels, which spread the candidate list over (row, chunk) workgroups.
+    const bool tail = fast_list_possible(g);
+    if (!tail) {
+        k_smp_resolve<<<a.rows, kResolveThreads, 0, s>>>(g, a.logits, w);
+        k_smp_collect<<<grid, kBlock, 0, s>>>(g, a.logits, w);
+    }
 
     SmpOut o{};
     o.sorted = a.sorted;
@@ -2200,6 +2343,7 @@ hipError_t launch_sampler(const SamplerArgs &a, hipStream_t s)
         SmpStates st{};
         for (uint32_t i = 0; i < nr; ++i) st.v[i] = a.states[r0 + i];
         if (merge) k_smp_finish<<<nr, kRankThreads, 0, s>>>(g, sorted, o, st, r0);
+        else if (tail) k_smp_tail<<<nr, kRankThreads, 0, s>>>(g, a.logits, w, o, st, r0);
         else k_smp_rank<<<nr, kRankThreads, 0, s>>>(g, w, o, st, r0);
     }
     return hipGetLastError();
