@@ -57,11 +57,22 @@
 //                 - every row: sort of the candidates in LDS (key descending
 //                   then index ascending: register runs merged by merge
 //                   path), the ranked outputs, then the race selection.
-// Otherwise the selection runs as k_smp_resolve (one workgroup per row, the
-// ties at T counted per chunk) and k_smp_collect ((row, chunk) workgroups),
-// and k_smp_rank ranks (top_k <= kCap); for top_k > kCap the list is sorted
-// as kCap tiles (k_smp_tile_sort), merged pairwise (k_smp_merge), and
-// finished by k_smp_finish.
+// Otherwise, for top_k <= kCap:
+//   k_smp_bucket  (row, chunk): the first digit P1 of the threshold from
+//                 k_smp_div's histogram; the keys of a higher first digit
+//                 (all candidates) into the row's candidate list, the keys at
+//                 P1 into its bucket list, in one pass.
+//   k_smp_rank    a few 1024-thread workgroups per row: groups of whole first
+//                 digits of the candidate list, each sorted in LDS at its
+//                 known offset, and the bucket list, cut by its next digits
+//                 and sorted, after them; each races its own slots and the
+//                 row's last workgroup writes the selection.  Rows whose
+//                 bucket is too large take the radix selection from scans of
+//                 the row in one workgroup.
+// For top_k > kCap the selection runs as k_smp_resolve (one workgroup per
+// row, the ties at T counted per chunk) and k_smp_collect ((row, chunk)
+// workgroups), and the list is sorted as kCap tiles (k_smp_tile_sort),
+// merged pairwise (k_smp_merge), and finished by k_smp_finish.
 //
 // Ties of p: the reference sorts with sort_unstable_by, which leaves the
 // order of equal probabilities unspecified; here they rank by ascending
@@ -100,7 +111,17 @@ struct RowSel {
     uint32_t fast_count; // keys >= fast_key found; > kCap: the radix path decides
     uint32_t ethr_on;    // e_thr found (k_smp_expseg's head workgroup)
     uint32_t ethr_key;   // key of e_thr
+    uint32_t gdone;      // k_smp_rank: workgroups of the row finished
+    uint64_t gfill;      // k_smp_bucket: words listed, above P1 (low half) and at P1 (high half)
 };
+constexpr uint32_t kMaxGroups = 8; // k_smp_rank workgroups per row
+// One k_smp_rank workgroup's result: its greatest race_word and the token of
+// that slot.
+struct GroupBest {
+    uint64_t word;
+    uint64_t idx;
+};
+constexpr uint32_t kBucketCap = 16384; // words a row's bucket list holds (keys at the threshold's first digit)
 
 struct SmpGeo {
     uint32_t rows;
@@ -164,6 +185,8 @@ struct SmpWs {
     uint32_t *ties; // rows * chunks
     uint64_t *cand; // rows * cand_ld
     uint64_t *cand2; // rows * cand_ld (merge ping-pong, top_k > kCap)
+    uint64_t *bucket; // rows * kBucketCap (k_smp_bucket's lists; the bucket path only)
+    GroupBest *gbest; // rows * kMaxGroups (the bucket path only)
 };
 
 // f32::total_cmp as an unsigned key (larger key = later in total order).
@@ -213,6 +236,21 @@ static constexpr PmPowers kPmPowers = make_pm_powers();
 constexpr uint32_t kPmStride = kPmPowers.v[kRankThreads - 1]; // 16807^kRankThreads
 static_assert(kPmPowers.v[0] == 16807u && kPmPowers.v[1] == 282475249u && kPmPowers.v[2] == 1622650073u,
               "Park-Miller powers: 16807, 16807^2, 16807^3 mod 2^31 - 1");
+
+// 16807^n mod (2^31 - 1) by squaring: the draw state of slot j - 1 from s0
+// is s0 16807^j, so a workgroup ranking the slots from j0 starts from
+// s0 pm_power(j0).
+__host__ __device__ constexpr uint32_t pm_power(uint32_t n)
+{
+    uint32_t r = 1, b = static_cast<uint32_t>(kMultiplier);
+    for (; n; n >>= 1) {
+        if (n & 1u) r = mulmod(r, b);
+        b = mulmod(b, b);
+    }
+    return r;
+}
+static_assert(pm_power(1) == kPmPowers.v[0] && pm_power(3) == kPmPowers.v[2] && pm_power(kRankThreads) == kPmStride,
+              "pm_power agrees with the power table");
 
 // Visits the columns [c0, c1) of one row: float4 steps when the row is
 // 16-byte aligned, then a scalar tail.  A step issues U loads per thread
@@ -1573,7 +1611,7 @@ __device__ RowSel pick_digit(const RowSel &sel, const uint32_t *hist, uint32_t b
 // one 1024-thread workgroup: the first digit from k_smp_div's histogram (or
 // from a scan, for a fast row whose list overflowed), later digits from
 // scans of the row, and at an exact threshold the ties per chunk (w.ties).
-// Leaves the row's RowSel (mode 1 or 2) in w.sel and returns it.
+// Returns the row's selection (mode 1 or 2).
 __device__ RowSel resolve_row(const SmpGeo &g, float *logits, const SmpWs &w, uint32_t row, RowSel sel,
                               uint32_t *s_hist, uint32_t *s_tmp, uint32_t *s_pick)
 {
@@ -1615,12 +1653,11 @@ __device__ RowSel resolve_row(const SmpGeo &g, float *logits, const SmpWs &w, ui
         for (uint32_t c = threadIdx.x; c < g.chunks; c += blockDim.x)
             w.ties[static_cast<uint64_t>(row) * g.chunks + c] = s_hist[c];
     }
-    if (threadIdx.x == 0) w.sel[row] = sel;
     return sel;
 }
 
 // Rows of a top_k above kCap (the merge path): k_smp_resolve, k_smp_collect
-// and the merge kernels.  Other rows take k_smp_tail.
+// and the merge kernels.
 __global__ __launch_bounds__(kResolveThreads) void k_smp_resolve(SmpGeo g, float *logits, SmpWs w)
 {
     __shared__ uint32_t s_hist[kBins]; // digit histogram; later the per-chunk tie counts
@@ -1636,7 +1673,8 @@ __global__ __launch_bounds__(kResolveThreads) void k_smp_resolve(SmpGeo g, float
         }
         return;
     }
-    (void)resolve_row(g, logits, w, row, sel, s_hist, s_tmp, s_pick);
+    const RowSel r = resolve_row(g, logits, w, row, sel, s_hist, s_tmp, s_pick);
+    if (threadIdx.x == 0) w.sel[row] = r; // for k_smp_collect
 }
 
 // ---- stage 8: candidates ------------------------------------------------------
@@ -1730,6 +1768,150 @@ __global__ __launch_bounds__(kBlock) void k_smp_collect(SmpGeo g, float *logits,
     }
 }
 
+
+// ---- the bucket path: top_k <= kCap without the fast list -------------------
+//
+// The first digit P1 of the threshold (the top 11 key bits of the top_k-th
+// largest key) splits a row's keys in two: A, a higher first digit, every key
+// a candidate (fewer than top_k of them), and B, first digit P1, whose
+// largest top_k - |A| keys complete the candidates.  Ranked, A fills the
+// slots [0, |A|) and B the rest.  k_smp_bucket, one (row, chunk) workgroup
+// per chunk, picks P1 from k_smp_div's histogram (every workgroup of the row
+// alike) and lists A into the row's candidate list and B into its bucket list
+// in one pass over the row; k_smp_rank sorts them.
+
+struct FirstDigit {
+    uint32_t digit, above, inb; // P1, |A|, |B|
+};
+
+// P1 from the row's first-digit histogram by a kBlock workgroup, thread t
+// holding digits [8t, 8t + 8) in h0, h1.
+static_assert(kBins == 8 * kBlock, "two uint4 of the histogram per thread");
+__device__ FirstDigit first_digit256(uint4 h0, uint4 h1, uint32_t top_k, uint32_t *s_tmp, uint32_t *s_pick)
+{
+    constexpr uint32_t per = kBins / kBlock;
+    const uint32_t mine[per] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+    uint32_t local = 0;
+#pragma unroll
+    for (uint32_t i = 0; i < per; ++i) local += mine[i];
+    uint32_t total;
+    const uint32_t incl = block_incl_scan256(local, s_tmp, total);
+    uint32_t cum = total - incl; // keys in the higher threads' (higher) digits
+#pragma unroll
+    for (int i = per - 1; i >= 0; --i) {
+        if (cum < top_k && top_k <= cum + mine[i]) {
+            s_pick[0] = threadIdx.x * per + static_cast<uint32_t>(i);
+            s_pick[1] = cum;
+            s_pick[2] = mine[i];
+        }
+        cum += mine[i];
+    }
+    __syncthreads();
+    return FirstDigit{s_pick[0], s_pick[1], s_pick[2]};
+}
+
+// Steps of kBucketVec float4 per thread (5120 columns per workgroup: config
+// 5's chunk in one step).  The histogram's loads, then the first step's, are
+// issued before P1 is picked, so the pick overlaps the chunk's memory round
+// trip.  One prefix sum of the packed counts (A low, B high half: at most
+// 5120 each) places both lists' words, and one 64-bit atomic per step
+// reserves them.  A has fewer than top_k <= cand_ld words; B is listed when
+// it fits kBucketCap (else k_smp_rank selects from scans of the row).
+constexpr uint32_t kBucketVec = 5;
+__device__ __forceinline__ void bucket_load(const SmpGeo &g, const float *x, uint64_t col0, uint64_t c1,
+                                            float4 (&q)[kBucketVec])
+{
+#pragma unroll
+    for (uint32_t i = 0; i < kBucketVec; ++i) {
+        const uint64_t c = col0 + 4ull * kBlock * i;
+        if (g.vec && c + 4 <= c1) {
+            q[i] = *reinterpret_cast<const float4 *>(x + c);
+        } else {
+            q[i].x = c < c1 ? x[c] : 0.0f;
+            q[i].y = c + 1 < c1 ? x[c + 1] : 0.0f;
+            q[i].z = c + 2 < c1 ? x[c + 2] : 0.0f;
+            q[i].w = c + 3 < c1 ? x[c + 3] : 0.0f;
+        }
+    }
+}
+
+// Lists one step's columns [col0 + 4 kBlock i + j) of q.
+__device__ __forceinline__ void bucket_step(const SmpGeo &g, const SmpWs &w, uint32_t row, const FirstDigit &f,
+                                            const float4 (&q)[kBucketVec], uint32_t col0, uint32_t c1,
+                                            uint32_t *s_tmp, uint64_t *s_base)
+{
+    uint32_t key[4 * kBucketVec];
+#pragma unroll
+    for (uint32_t i = 0; i < kBucketVec; ++i) {
+        key[4 * i] = total_key(q[i].x);
+        key[4 * i + 1] = total_key(q[i].y);
+        key[4 * i + 2] = total_key(q[i].z);
+        key[4 * i + 3] = total_key(q[i].w);
+    }
+    uint32_t na = 0, nb = 0; // columns from c1 on (a row's last step) are not listed
+#pragma unroll
+    for (uint32_t j = 0; j < 4 * kBucketVec; ++j) {
+        const bool in = col0 + 4u * kBlock * (j / 4) + j % 4 < c1; // columns < 2^31
+        const uint32_t d = key[j] >> 21;
+        na += (in && d > f.digit) ? 1u : 0u;
+        nb += (in && d == f.digit) ? 1u : 0u;
+    }
+    uint32_t tot;
+    const uint32_t incl = block_incl_scan256(na | (nb << 16), s_tmp, tot);
+    if (tot == 0) return; // uniform
+    if (threadIdx.x == 0)
+        *s_base = atomicAdd(reinterpret_cast<unsigned long long *>(&w.sel[row].gfill),
+                            static_cast<unsigned long long>(tot & 0xffffu) |
+                                (static_cast<unsigned long long>(tot >> 16) << 32));
+    __syncthreads();
+    const uint64_t base = *s_base;
+    __syncthreads(); // s_base and s_tmp are rewritten by the next step
+    uint32_t sa = static_cast<uint32_t>(base) + (incl & 0xffffu) - na;
+    uint32_t sb = static_cast<uint32_t>(base >> 32) + (incl >> 16) - nb;
+    uint64_t *alist = w.cand + static_cast<uint64_t>(row) * g.cand_ld;
+    uint64_t *blist = w.bucket + static_cast<uint64_t>(row) * kBucketCap;
+    const bool list_b = f.inb <= kBucketCap;
+#pragma unroll
+    for (uint32_t j = 0; j < 4 * kBucketVec; ++j) {
+        const uint32_t col = col0 + 4u * kBlock * (j / 4) + j % 4;
+        const bool in = col < c1;
+        const uint32_t d = key[j] >> 21;
+        if (in && d > f.digit) {
+            if (sa < g.cand_ld) alist[sa] = cand_word(key[j], col);
+            ++sa;
+        } else if (in && d == f.digit) {
+            if (list_b && sb < kBucketCap) blist[sb] = cand_word(key[j], col);
+            ++sb;
+        }
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void k_smp_bucket(SmpGeo g, const float *logits, SmpWs w)
+{
+    __shared__ uint32_t s_tmp[kBlock / kWave];
+    __shared__ uint32_t s_pick[3];
+    __shared__ uint64_t s_base;
+    const uint32_t row = blockIdx.x / g.chunks, chunk = blockIdx.x % g.chunks;
+    const float *x = logits + static_cast<int64_t>(row) * g.ld;
+    uint64_t c0, c1;
+    chunk_range(g, chunk, c0, c1);
+    const uint4 *hist = reinterpret_cast<const uint4 *>(w.hist + static_cast<uint64_t>(row) * kBins);
+    const uint4 h0 = hist[2 * threadIdx.x], h1 = hist[2 * threadIdx.x + 1];
+    constexpr uint64_t step = 4ull * kBucketVec * kBlock;
+    {
+        float4 q[kBucketVec];
+        bucket_load(g, x, c0 + 4ull * threadIdx.x, c1, q);
+        const FirstDigit f = first_digit256(h0, h1, g.top_k, s_tmp, s_pick);
+        const uint32_t e1 = static_cast<uint32_t>(c1); // card < 2^31
+        bucket_step(g, w, row, f, q, static_cast<uint32_t>(c0) + 4u * threadIdx.x, e1, s_tmp, &s_base);
+        for (uint64_t blk = c0 + step; blk < c1; blk += step) {
+            __syncthreads(); // s_tmp: the previous step's scan is read
+            bucket_load(g, x, blk + 4ull * threadIdx.x, c1, q);
+            bucket_step(g, w, row, f, q, static_cast<uint32_t>(blk) + 4u * threadIdx.x, e1, s_tmp, &s_base);
+        }
+    }
+}
+
 // ---- stage 9: ranking and selection -----------------------------------------
 
 struct SmpOut {
@@ -1766,62 +1948,74 @@ __device__ __forceinline__ void group_sync()
 // slot j draws state_j = s0 * 16807^(j+1) mod (2^31 - 1), u_j = state_j as
 // f32 / 2^31 (2147483647 as f32 is 2^31), race_j = p_j / -ln(u_j); the
 // first slot with the greatest race (strict >, starting from -inf) wins.
-// T threads take part (see group_sync).
-template <uint32_t T, class P, class I>
-__device__ void select_slots(const SmpGeo &g, uint32_t row, uint32_t s0, P prob, I index, const SmpOut &o)
+//
+// The race word of a slot orders slots as that rule does: total_key(race)
+// above ~slot, so the greatest word holds the greatest race and, among equal
+// races, the first slot.  Races are >= +0 (p >= +0 over -ln(u) >= 0) when
+// they are not -inf or NaN, so the key order is the float order; 0 stands
+// for no slot.
+__device__ __forceinline__ uint64_t race_word(float race, uint32_t slot)
 {
-    __shared__ float s_v[kRankThreads / kWave];
-    __shared__ uint32_t s_i[kRankThreads / kWave];
+    return (static_cast<uint64_t>(total_key(race)) << 32) | static_cast<uint32_t>(~slot);
+}
+
+// The greatest race word over slots slot0 + j, j < n, whose draws start from
+// s0j = s0 16807^slot0 (slot0 + j draws s0j 16807^(j+1)); prob(j) is the
+// probability of slot slot0 + j.  T threads take part (see group_sync); the
+// result is thread 0's.
+template <uint32_t T, class P>
+__device__ uint64_t race_best(uint32_t n, uint32_t s0j, uint32_t slot0, P prob)
+{
+    __shared__ uint64_t s_w[kRankThreads / kWave];
     __shared__ double s_invc[16], s_logc[16]; // logf's table, read per lane
     if (threadIdx.x < 16) {
         s_invc[threadIdx.x] = kLogfInvc[threadIdx.x];
         s_logc[threadIdx.x] = kLogfLogc[threadIdx.x];
     }
     group_sync<T>();
-    float best = -__builtin_inff();
-    uint32_t bslot = kNone;
+    uint64_t best = 0;
     uint32_t pw = kPmPowers.v[threadIdx.x]; // 16807^(t+1); slot t + m T multiplies by (16807^T)^m
-    for (uint32_t j = threadIdx.x; j < g.top_k; j += T) {
-        const uint32_t state = mulmod(s0, pw);
+    for (uint32_t j = threadIdx.x; j < n; j += T) {
+        const uint32_t state = mulmod(s0j, pw);
         const float uniform = static_cast<float>(state) * 0x1p-31f;
         const float race = prob(j) / -emel_logf(uniform, s_invc, s_logc);
-        if (race > -__builtin_inff() && (race > best || (race == best && j < bslot))) {
-            best = race;
-            bslot = j;
-        }
+        const uint64_t wd = race > -__builtin_inff() ? race_word(race, slot0 + j) : 0ull;
+        best = wd > best ? wd : best;
         pw = mulmod(pw, kPmPowers.v[T - 1]);
     }
 #pragma unroll
     for (int off = kWave / 2; off > 0; off >>= 1) {
-        const float ov = __shfl_xor(best, off, kWave);
-        const uint32_t oi = __shfl_xor(bslot, off, kWave);
-        if (oi != kNone && (ov > best || (ov == best && oi < bslot) || bslot == kNone)) {
-            best = ov;
-            bslot = oi;
-        }
+        const uint64_t ob = static_cast<uint64_t>(__shfl_xor(static_cast<unsigned long long>(best), off, kWave));
+        best = ob > best ? ob : best;
     }
     if constexpr (T > kWave) {
-        if (threadIdx.x % kWave == 0) {
-            s_v[threadIdx.x / kWave] = best;
-            s_i[threadIdx.x / kWave] = bslot;
-        }
+        if (threadIdx.x % kWave == 0) s_w[threadIdx.x / kWave] = best;
         __syncthreads();
+        if (threadIdx.x == 0)
+            for (uint32_t v = 1; v < T / kWave; ++v) best = s_w[v] > best ? s_w[v] : best;
     }
-    if (threadIdx.x != 0) return;
-    for (uint32_t v = 1; v < T / kWave; ++v) {
-        const float ov = s_v[v];
-        const uint32_t oi = s_i[v];
-        if (oi != kNone && (bslot == kNone || ov > best || (ov == best && oi < bslot))) {
-            best = ov;
-            bslot = oi;
-        }
-    }
-    const int32_t selected = bslot == kNone ? -1 : index(bslot);
-    const float score = bslot == kNone ? -__builtin_inff() : best;
+    return best;
+}
+
+// The row's outputs from the winning race word (0: no slot); index(j) is
+// the token of ranked slot j.
+template <class I>
+__device__ __forceinline__ void write_selection(const SmpGeo &g, const SmpOut &o, uint32_t row, uint64_t best, I index)
+{
+    const int32_t selected = best ? index(~static_cast<uint32_t>(best)) : -1;
+    const float score = best ? from_key(static_cast<uint32_t>(best >> 32)) : -__builtin_inff();
     o.selected[row] = selected;
     o.score[row] = score;
     const bool valid = selected >= 0 && static_cast<uint64_t>(selected) < g.card && __builtin_isfinite(score);
     if (o.status) o.status[row] = valid ? 0 : kInvalidRequest;
+}
+
+// The race over slots j < top_k, decided in one workgroup.
+template <uint32_t T, class P, class I>
+__device__ void select_slots(const SmpGeo &g, uint32_t row, uint32_t s0, P prob, I index, const SmpOut &o)
+{
+    const uint64_t best = race_best<T>(g.top_k, s0, 0, prob);
+    if (threadIdx.x == 0) write_selection(g, o, row, best, index);
 }
 
 __device__ __forceinline__ void write_ranked(const SmpGeo &g, const SmpOut &o, uint32_t row, uint32_t j, uint64_t word)
@@ -2045,11 +2239,214 @@ __device__ void collect_row(const SmpGeo &g, const float *x, uint64_t *list, con
     }
 }
 
-__global__ __launch_bounds__(kRankThreads) void k_smp_rank(SmpGeo g, SmpWs w, SmpOut o, SmpStates st, uint32_t row0)
+// The bucket path's ranking: `groups` workgroups per row.  Groups q <
+// groups - 1 take A's first digits, digit b > P1 to group floor(cb(b)
+// (groups - 1) / |A|), cb(b) the keys of the higher digits: a group holds
+// whole digits, at most |A| < kCap keys, and its slots start at the least cb
+// of its digits.  The last group takes B from the bucket list, cut by the
+// next digits (histograms of the list, as pick_digit) when it is longer than
+// kSortDirect, and ranks B's first top_k - |A| words after A.  A row whose B
+// was not listed, or whose ties at an exact threshold exceed kCap, is
+// selected by the last group alone from scans of the row (resolve_row,
+// collect_row, in the bucket list's place) and ranked whole; the A groups'
+// slots are then written twice with the same words.  Every workgroup races
+// its own slots; the last one of the row to finish (a count per row) writes
+// the selection from the greatest race word.
+constexpr uint32_t kSortDirect = 1024;
+
+// Sorts the n words of s_c, ranks the first `out` at slots slot0 + j and
+// returns their greatest race word (thread 0's).
+template <uint32_t T>
+__device__ uint64_t rank_words(const SmpGeo &g, const SmpOut &o, uint32_t row, uint32_t s0, uint64_t *s_c, uint32_t n,
+                               uint32_t out, uint32_t slot0)
+{
+    uint32_t np = kSortPer;
+    while (np < n) np <<= 1;
+    for (uint32_t i = n + threadIdx.x; i < np; i += T) s_c[slot(i)] = 0ull;
+    group_sync<T>();
+    lds_sort_desc<T>(s_c, np);
+    for (uint32_t j = threadIdx.x; j < out; j += T) write_ranked(g, o, row, slot0 + j, s_c[slot(j)]);
+    return race_best<T>(out, mulmod(s0, pm_power(slot0)), slot0,
+                        [&](uint32_t j) { return from_key(static_cast<uint32_t>(s_c[slot(j)] >> 32)); });
+}
+
+// A workgroup's end (thread 0, holding `best`, the greatest race word of
+// the slots from slot0 ranked in s_c): its word and the token of that slot
+// go to the row's entry q, released by the count of finished workgroups;
+// the last workgroup of the row acquires the entries and writes the
+// selection from the greatest word.  Only thread 0 publishes, so one
+// device-scope release per workgroup (an L2 write-back) suffices.
+__device__ void group_finish(const SmpGeo &g, const SmpOut &o, const SmpWs &w, uint32_t row, uint32_t q,
+                             uint64_t best, const uint64_t *s_c, uint32_t slot0, uint32_t groups)
+{
+    if (threadIdx.x != 0) return;
+    GroupBest *gb = w.gbest + static_cast<uint64_t>(row) * kMaxGroups;
+    const uint64_t idx = best ? ~static_cast<uint32_t>(s_c[slot(~static_cast<uint32_t>(best) - slot0)]) : 0u;
+    __hip_atomic_store(&gb[q].word, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&gb[q].idx, idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (__hip_atomic_fetch_add(&w.sel[row].gdone, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) != groups - 1) return;
+    uint64_t b = 0, bi = 0;
+    for (uint32_t k = 0; k < groups; ++k) {
+        const uint64_t wk = __hip_atomic_load(&gb[k].word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (wk > b) {
+            b = wk;
+            bi = __hip_atomic_load(&gb[k].idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    write_selection(g, o, row, b, [&](uint32_t) { return static_cast<int32_t>(bi); });
+}
+
+// Ranks the n <= kCap words staged in s_c, on wave 0 alone when they are few.
+__device__ void rank_group(const SmpGeo &g, const SmpOut &o, const SmpWs &w, uint32_t row, uint32_t q, uint32_t s0,
+                           uint64_t *s_c, uint32_t n, uint32_t out, uint32_t slot0, uint32_t groups)
+{
+    if (n <= kWave * kSortPer) { // uniform
+        if (threadIdx.x >= kWave) return;
+        const uint64_t best = rank_words<kWave>(g, o, row, s0, s_c, n, out, slot0);
+        group_finish(g, o, w, row, q, best, s_c, slot0, groups);
+        return;
+    }
+    const uint64_t best = rank_words<kRankThreads>(g, o, row, s0, s_c, n, out, slot0);
+    group_finish(g, o, w, row, q, best, s_c, slot0, groups);
+}
+
+static_assert(kBins == 2 * kRankThreads, "two first digits per thread");
+__global__ __launch_bounds__(kRankThreads) void k_smp_rank(SmpGeo g, float *logits, SmpWs w, SmpOut o, SmpStates st,
+                                                           uint32_t row0, uint32_t groups)
 {
     __shared__ uint64_t s_c[kCapSlots];
-    const uint32_t row = row0 + blockIdx.x;
-    rank_row(g, w, o, st.v[blockIdx.x], row, w.sel[row].count, s_c);
+    __shared__ uint32_t s_hist[kBins]; // A: the group of each first digit; B: digit histograms
+    __shared__ uint32_t s_tmp[kRankThreads / kWave];
+    __shared__ uint32_t s_pick[3];
+    __shared__ uint32_t s_off, s_n;
+    const uint32_t r = blockIdx.x / groups, q = blockIdx.x % groups, ga = groups - 1;
+    const uint32_t row = row0 + r, s0 = st.v[r];
+    const uint32_t b0 = 2 * threadIdx.x, b1 = b0 + 1;
+    const uint2 h = reinterpret_cast<const uint2 *>(w.hist + static_cast<uint64_t>(row) * kBins)[threadIdx.x];
+    if (threadIdx.x == 0) {
+        s_off = kNone;
+        s_n = 0;
+    }
+    uint32_t total;
+    const uint32_t incl = block_incl_scan1024(h.x + h.y, s_tmp, total); // its barriers order the resets
+    const uint32_t cb1 = total - incl, cb0 = cb1 + h.y; // keys in the digits above b1, above b0
+    if (cb1 < g.top_k && g.top_k <= cb1 + h.y) {
+        s_pick[0] = b1;
+        s_pick[1] = cb1;
+        s_pick[2] = h.y;
+    }
+    if (cb0 < g.top_k && g.top_k <= cb0 + h.x) {
+        s_pick[0] = b0;
+        s_pick[1] = cb0;
+        s_pick[2] = h.x;
+    }
+    __syncthreads();
+    const uint32_t p1 = s_pick[0], above = s_pick[1], inb = s_pick[2];
+    const uint64_t fill = w.sel[row].gfill;
+    if (q < ga) { // A
+        const uint32_t g0 = (b0 > p1 && h.x) ? cb0 * ga / above : kNone; // a key above P1: above > 0
+        const uint32_t g1 = (b1 > p1 && h.y) ? cb1 * ga / above : kNone;
+        s_hist[b0] = g0;
+        s_hist[b1] = g1;
+        if (g0 == q) atomicMin(&s_off, cb0);
+        if (g1 == q) atomicMin(&s_off, cb1);
+        __syncthreads();
+        const uint32_t off = s_off;
+        if (off == kNone) { // uniform: no digit
+            group_finish(g, o, w, row, q, 0ull, s_c, 0, groups);
+            return;
+        }
+        const uint32_t na = above < static_cast<uint32_t>(fill) ? above : static_cast<uint32_t>(fill); // < kCap
+        const uint64_t *alist = w.cand + static_cast<uint64_t>(row) * g.cand_ld;
+        uint64_t v[kSortPer];
+#pragma unroll
+        for (uint32_t k = 0; k < kSortPer; ++k) {
+            const uint32_t i = threadIdx.x + k * kRankThreads;
+            v[k] = i < na ? alist[i] : 0ull;
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < kSortPer; ++k) {
+            const uint32_t i = threadIdx.x + k * kRankThreads;
+            if (i < na && s_hist[static_cast<uint32_t>(v[k] >> 53)] == q) {
+                const uint32_t e = atomicAdd(&s_n, 1u);
+                if (e < kCap) s_c[slot(e)] = v[k];
+            }
+        }
+        __syncthreads();
+        const uint32_t n = s_n < kCap ? s_n : kCap;
+        rank_group(g, o, w, row, q, s0, s_c, n, n, off, groups);
+        return;
+    }
+    // B: its largest need words after A's slots
+    const uint32_t need = g.top_k - above;
+    uint64_t *blist = w.bucket + static_cast<uint64_t>(row) * kBucketCap;
+    if (inb <= kBucketCap) { // uniform
+        const uint32_t nb = inb < static_cast<uint32_t>(fill >> 32) ? inb : static_cast<uint32_t>(fill >> 32);
+        RowSel bs{};
+        bs.prefix = p1;
+        bs.depth = 11;
+        bs.need = need;
+        bs.mode = 1;
+        if (nb > kSortDirect) {
+            bs.mode = 0;
+            for (uint32_t pass = 1; pass <= 2 && bs.mode == 0; ++pass) {
+                const uint32_t bits = pass == 2 ? 10u : 11u, nbins = 1u << bits;
+                const uint32_t dshift = 32u - bs.depth, shift = dshift - bits;
+                for (uint32_t b = threadIdx.x; b < nbins; b += kRankThreads) s_hist[b] = 0;
+                __syncthreads();
+                for (uint32_t i0 = 0; i0 < nb; i0 += kSortPer * kRankThreads) {
+                    uint32_t key[kSortPer];
+#pragma unroll
+                    for (uint32_t k = 0; k < kSortPer; ++k) {
+                        const uint32_t i = i0 + threadIdx.x + k * kRankThreads;
+                        key[k] = i < nb ? static_cast<uint32_t>(blist[i] >> 32) : 0u;
+                    }
+#pragma unroll
+                    for (uint32_t k = 0; k < kSortPer; ++k) {
+                        const uint32_t i = i0 + threadIdx.x + k * kRankThreads;
+                        if (i < nb && (key[k] >> dshift) == bs.prefix) atomicAdd(&s_hist[(key[k] >> shift) & (nbins - 1)], 1u);
+                    }
+                }
+                __syncthreads();
+                bs = pick_digit(bs, s_hist, bits, s_tmp, s_pick);
+            }
+        }
+        if (bs.mode == 1) { // uniform; else the ties at T exceed kCap
+            const uint32_t dshift = 32u - bs.depth;
+            for (uint32_t i0 = 0; i0 < nb; i0 += kSortPer * kRankThreads) {
+                uint64_t v[kSortPer];
+#pragma unroll
+                for (uint32_t k = 0; k < kSortPer; ++k) {
+                    const uint32_t i = i0 + threadIdx.x + k * kRankThreads;
+                    v[k] = i < nb ? blist[i] : 0ull;
+                }
+#pragma unroll
+                for (uint32_t k = 0; k < kSortPer; ++k) {
+                    const uint32_t i = i0 + threadIdx.x + k * kRankThreads;
+                    if (i < nb && (static_cast<uint32_t>(v[k] >> 32) >> dshift) >= bs.prefix) {
+                        const uint32_t e = atomicAdd(&s_n, 1u);
+                        if (e < kCap) s_c[slot(e)] = v[k];
+                    }
+                }
+            }
+            __syncthreads();
+            const uint32_t n = s_n; // bs.count <= kCap
+            if (n <= kCap) { // uniform
+                rank_group(g, o, w, row, q, s0, s_c, n, need < n ? need : n, above, groups);
+                return;
+            }
+        }
+    }
+    // the whole row from scans
+    __syncthreads(); // every thread has read s_pick, which resolve_row rewrites
+    RowSel rs{};
+    rs.need = g.top_k;
+    rs = resolve_row(g, logits, w, row, rs, s_hist, s_tmp, s_pick);
+    collect_row(g, logits + static_cast<int64_t>(row) * g.ld, blist, rs, s_tmp);
+    __syncthreads(); // the list, written by the whole workgroup, is staged next
+    const uint32_t n = rs.count < kCap ? rs.count : kCap;
+    stage_words<kRankThreads>(s_c, blist, n, n);
+    rank_group(g, o, w, row, q, s0, s_c, n, g.top_k, 0, groups);
 }
 
 // A launch whose rows can take the fast list: one workgroup per row
@@ -2233,10 +2630,38 @@ void plan_chunks(uint32_t rows, uint64_t card, uint64_t &chunk_cols, uint32_t &c
 uint64_t align256(uint64_t b) { return (b + 255) & ~uint64_t{255}; }
 
 struct WsLayout {
-    uint64_t part, psum, sub, seg, sel, hist, ties, cand, cand2, total;
+    uint64_t part, psum, sub, seg, sel, hist, ties, cand, cand2, bucket, gbest, total;
 };
 
-WsLayout layout(uint32_t rows, uint32_t chunks, uint64_t chunk_cols, uint64_t cand_ld, bool merge)
+// Geometry of a launch (what launch_sampler derives from its arguments).
+SmpGeo plan_geo(uint32_t rows, uint64_t card, uint32_t top_k)
+{
+    SmpGeo g{};
+    g.rows = rows;
+    g.card = card;
+    plan_chunks(rows, card, g.chunk_cols, g.chunks);
+    g.top_k = top_k;
+    g.cand_ld = top_k > kCap ? top_k : kCap;
+    return g;
+}
+
+// The bucket path: top_k <= kCap without the fast list.
+bool bucket_path(const SmpGeo &g) { return g.top_k <= kCap && !fast_list_possible(g); }
+
+// k_smp_rank's workgroups per row: A groups of about 1024 keys (at most
+// kMaxGroups - 1, and at most kRankWgs workgroups in all while there are
+// rows to spare), then B.
+constexpr uint32_t kRankWgs = 256;
+uint32_t rank_groups(uint32_t top_k, uint32_t rows)
+{
+    uint32_t ga = (top_k + 1023) / 1024;
+    if (ga > kMaxGroups - 1) ga = kMaxGroups - 1;
+    const uint32_t fit = rows < kRankWgs ? kRankWgs / rows : 1u; // groups that keep one wave of workgroups
+    if (ga + 1 > fit) ga = fit > 1 ? fit - 1 : 1u;
+    return ga + 1;
+}
+
+WsLayout layout(uint32_t rows, uint32_t chunks, uint64_t chunk_cols, uint64_t cand_ld, bool merge, bool bucket)
 {
     const uint64_t spc = (chunk_cols + kSub - 1) / kSub;
     WsLayout l{};
@@ -2249,7 +2674,9 @@ WsLayout layout(uint32_t rows, uint32_t chunks, uint64_t chunk_cols, uint64_t ca
     l.ties = l.hist + align256(uint64_t{rows} * kBins * sizeof(uint32_t));
     l.cand = l.ties + align256(uint64_t{rows} * chunks * sizeof(uint32_t));
     l.cand2 = l.cand + align256(uint64_t{rows} * cand_ld * sizeof(uint64_t));
-    l.total = merge ? l.cand2 + align256(uint64_t{rows} * cand_ld * sizeof(uint64_t)) : l.cand2;
+    l.bucket = merge ? l.cand2 + align256(uint64_t{rows} * cand_ld * sizeof(uint64_t)) : l.cand2;
+    l.gbest = bucket ? l.bucket + align256(uint64_t{rows} * kBucketCap * sizeof(uint64_t)) : l.bucket;
+    l.total = bucket ? l.gbest + align256(uint64_t{rows} * kMaxGroups * sizeof(GroupBest)) : l.gbest;
     return l;
 }
 
@@ -2257,29 +2684,21 @@ WsLayout layout(uint32_t rows, uint32_t chunks, uint64_t chunk_cols, uint64_t ca
 
 uint64_t sampler_workspace_bytes(uint32_t rows, uint64_t card, uint32_t top_k)
 {
-    uint64_t chunk_cols;
-    uint32_t chunks;
-    plan_chunks(rows, card, chunk_cols, chunks);
-    const uint64_t cand_ld = top_k > kCap ? top_k : kCap;
-    return layout(rows, chunks, chunk_cols, cand_ld, top_k > kCap).total;
+    const SmpGeo g = plan_geo(rows, card, top_k);
+    return layout(rows, g.chunks, g.chunk_cols, g.cand_ld, top_k > kCap, bucket_path(g)).total;
 }
 
 hipError_t launch_sampler(const SamplerArgs &a, hipStream_t s)
 {
     if (a.rows == 0 || a.card == 0 || a.top_k == 0 || a.top_k > a.card || a.card > 0x7fffffffull || !a.workspace)
         return hipErrorInvalidValue;
-    SmpGeo g{};
-    g.rows = a.rows;
-    g.card = a.card;
-    plan_chunks(a.rows, a.card, g.chunk_cols, g.chunks);
-    if (g.chunks > kBins) return hipErrorInvalidValue; // k_smp_resolve counts ties per chunk in kBins words
+    SmpGeo g = plan_geo(a.rows, a.card, a.top_k);
+    if (g.chunks > kBins) return hipErrorInvalidValue; // resolve_row counts ties per chunk in kBins words
     g.ld = a.logits_ld;
     g.vec = (reinterpret_cast<uintptr_t>(a.logits) % 16 == 0) && (a.rows == 1 || a.logits_ld % 4 == 0);
-    g.top_k = a.top_k;
     g.scale = a.scale;
-    g.cand_ld = a.top_k > kCap ? a.top_k : kCap;
-    const bool merge = a.top_k > kCap;
-    const WsLayout l = layout(a.rows, g.chunks, g.chunk_cols, g.cand_ld, merge);
+    const bool merge = a.top_k > kCap, bucket = bucket_path(g);
+    const WsLayout l = layout(a.rows, g.chunks, g.chunk_cols, g.cand_ld, merge, bucket);
     char *base = static_cast<char *>(a.workspace);
     SmpWs w{};
     w.part = reinterpret_cast<float *>(base + l.part);
@@ -2291,6 +2710,8 @@ hipError_t launch_sampler(const SamplerArgs &a, hipStream_t s)
     w.ties = reinterpret_cast<uint32_t *>(base + l.ties);
     w.cand = reinterpret_cast<uint64_t *>(base + l.cand);
     w.cand2 = reinterpret_cast<uint64_t *>(base + l.cand2);
+    w.bucket = reinterpret_cast<uint64_t *>(base + l.bucket);
+    w.gbest = reinterpret_cast<GroupBest *>(base + l.gbest);
 
     const dim3 grid(a.rows * g.chunks);
     if (g.chunk_cols <= kFuseCols) {
@@ -2305,12 +2726,16 @@ hipError_t launch_sampler(const SamplerArgs &a, hipStream_t s)
     k_smp_div<<<grid, kBlock, 0, s>>>(g, a.logits, w);
     // Rows resolved by the fast list need no selection: when the fast list
     // applies, k_smp_tail selects (in one workgroup per row, for the rows it
-    // left) and ranks in one launch; otherwise every row takes the selection
-    // kernels, which spread the candidate list over (row, chunk) workgroups.
-    const bool tail = fast_list_possible(g);
-    if (!tail) {
+    // left) and ranks in one launch.  Otherwise, up to kCap, k_smp_bucket
+    // lists the candidates by their first digit and k_smp_rank selects and
+    // ranks in groups; above kCap the selection kernels spread the
+    // candidate list over (row, chunk) workgroups for the merge sort.
+    const bool tail = !merge && !bucket;
+    if (merge) {
         k_smp_resolve<<<a.rows, kResolveThreads, 0, s>>>(g, a.logits, w);
         k_smp_collect<<<grid, kBlock, 0, s>>>(g, a.logits, w);
+    } else if (bucket) {
+        k_smp_bucket<<<grid, kBlock, 0, s>>>(g, a.logits, w);
     }
 
     SmpOut o{};
@@ -2323,6 +2748,7 @@ hipError_t launch_sampler(const SamplerArgs &a, hipStream_t s)
     o.score = a.score;
     o.status = a.status;
 
+    const uint32_t groups = rank_groups(a.top_k, a.rows);
     const uint64_t *sorted = w.cand;
     if (merge) {
         const uint32_t tiles = (a.top_k + kCap - 1) / kCap;
@@ -2344,7 +2770,7 @@ hipError_t launch_sampler(const SamplerArgs &a, hipStream_t s)
         for (uint32_t i = 0; i < nr; ++i) st.v[i] = a.states[r0 + i];
         if (merge) k_smp_finish<<<nr, kRankThreads, 0, s>>>(g, sorted, o, st, r0);
         else if (tail) k_smp_tail<<<nr, kRankThreads, 0, s>>>(g, a.logits, w, o, st, r0);
-        else k_smp_rank<<<nr, kRankThreads, 0, s>>>(g, w, o, st, r0);
+        else k_smp_rank<<<nr * groups, kRankThreads, 0, s>>>(g, a.logits, w, o, st, r0, groups);
     }
     return hipGetLastError();
 }
