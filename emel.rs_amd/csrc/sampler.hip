@@ -1963,18 +1963,26 @@ __device__ __forceinline__ uint64_t race_word(float race, uint32_t slot)
 // s0j = s0 16807^slot0 (slot0 + j draws s0j 16807^(j+1)); prob(j) is the
 // probability of slot slot0 + j.  T threads take part (see group_sync); the
 // result is thread 0's.
+// logf's table in LDS, read per lane (staged by threads 0-15; the caller
+// synchronises before use).
+struct LogfTab {
+    double invc[16], logc[16];
+};
+__device__ __forceinline__ void stage_logf(LogfTab *t)
+{
+    if (threadIdx.x < 16) {
+        t->invc[threadIdx.x] = kLogfInvc[threadIdx.x];
+        t->logc[threadIdx.x] = kLogfLogc[threadIdx.x];
+    }
+}
+
 template <uint32_t T, class P>
-__device__ uint64_t race_best(uint32_t n, uint32_t s0j, uint32_t slot0, P prob)
+__device__ uint64_t race_best(uint32_t n, uint32_t s0j, uint32_t slot0, P prob, const LogfTab *tab, uint32_t pw)
 {
     __shared__ uint64_t s_w[kRankThreads / kWave];
-    __shared__ double s_invc[16], s_logc[16]; // logf's table, read per lane
-    if (threadIdx.x < 16) {
-        s_invc[threadIdx.x] = kLogfInvc[threadIdx.x];
-        s_logc[threadIdx.x] = kLogfLogc[threadIdx.x];
-    }
-    group_sync<T>();
+    const double *s_invc = tab->invc, *s_logc = tab->logc;
     uint64_t best = 0;
-    uint32_t pw = kPmPowers.v[threadIdx.x]; // 16807^(t+1); slot t + m T multiplies by (16807^T)^m
+    // pw = 16807^(t+1) (kPmPowers.v[t]); slot t + m T multiplies by (16807^T)^m
     for (uint32_t j = threadIdx.x; j < n; j += T) {
         const uint32_t state = mulmod(s0j, pw);
         const float uniform = static_cast<float>(state) * 0x1p-31f;
@@ -2014,7 +2022,11 @@ __device__ __forceinline__ void write_selection(const SmpGeo &g, const SmpOut &o
 template <uint32_t T, class P, class I>
 __device__ void select_slots(const SmpGeo &g, uint32_t row, uint32_t s0, P prob, I index, const SmpOut &o)
 {
-    const uint64_t best = race_best<T>(g.top_k, s0, 0, prob);
+    __shared__ LogfTab s_tab;
+    const uint32_t pw = kPmPowers.v[threadIdx.x];
+    stage_logf(&s_tab);
+    group_sync<T>();
+    const uint64_t best = race_best<T>(g.top_k, s0, 0, prob, &s_tab, pw);
     if (threadIdx.x == 0) write_selection(g, o, row, best, index);
 }
 
@@ -2254,20 +2266,119 @@ __device__ void collect_row(const SmpGeo &g, const float *x, uint64_t *list, con
 // the selection from the greatest race word.
 constexpr uint32_t kSortDirect = 1024;
 
-// Sorts the n words of s_c, ranks the first `out` at slots slot0 + j and
+// Sort, descending, of the n <= kCap distinct words of s (at slot(e)) by
+// fine key bins, for one kRankThreads workgroup: the bin of a word is
+// (kmax - key) >> sh, sh the least shift that maps the words' key range onto
+// kFineBins bins, so bins run in descending key order.  An LDS atomic per
+// word counts its bin and returns the word's place among the bin's; a
+// prefix sum of the counts gives each bin's first position; the words are
+// scattered by bin into d; and a word's final position is its bin's first
+// plus the number of greater words in its bin.  Returns false, s untouched,
+// when a bin holds more than kFineMax words (many equal keys, or a key range
+// dense at this resolution): the merge sort takes those.
+constexpr uint32_t kFineBins = 4096, kFineMax = 64;
+static_assert(kFineBins == 4 * kRankThreads, "four fine bins per thread");
+__device__ __forceinline__ uint32_t block_reduce1024(uint32_t v, bool take_max, uint32_t *s_red)
+{
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+        const uint32_t o = __shfl_xor(v, off, kWave);
+        v = take_max ? (o > v ? o : v) : (o < v ? o : v);
+    }
+    if (threadIdx.x % kWave == 0) s_red[threadIdx.x / kWave] = v;
+    __syncthreads();
+    v = s_red[0];
+#pragma unroll
+    for (uint32_t w = 1; w < kRankThreads / kWave; ++w) {
+        const uint32_t o = s_red[w];
+        v = take_max ? (o > v ? o : v) : (o < v ? o : v);
+    }
+    __syncthreads(); // s_red may be rewritten after this
+    return v;
+}
+
+__device__ bool bin_sort_desc(uint64_t *s, uint32_t n, uint64_t *d, uint32_t *cnt, uint32_t *s_tmp)
+{
+    constexpr uint32_t T = kRankThreads;
+    // per word of this thread only a packed (bin, place) is kept across the
+    // barriers; the words are read again from LDS where needed
+    uint32_t kmin = 0xffffffffu, kmax = 0;
+#pragma unroll
+    for (uint32_t r = 0; r < kSortPer; ++r) {
+        const uint32_t e = threadIdx.x + r * T;
+        if (e < n) {
+            const uint32_t k = static_cast<uint32_t>(s[slot(e)] >> 32);
+            kmin = k < kmin ? k : kmin;
+            kmax = k > kmax ? k : kmax;
+        }
+    }
+    reinterpret_cast<uint4 *>(cnt)[threadIdx.x] = uint4{0u, 0u, 0u, 0u};
+    kmin = block_reduce1024(kmin, false, s_tmp); // its barriers order the zeroing
+    kmax = block_reduce1024(kmax, true, s_tmp);
+    uint32_t sh = 0;
+    while (((kmax - kmin) >> sh) >= kFineBins) ++sh;
+    uint32_t pk[kSortPer]; // bin | place in the bin << 12
+#pragma unroll
+    for (uint32_t r = 0; r < kSortPer; ++r) {
+        const uint32_t e = threadIdx.x + r * T;
+        pk[r] = kNone;
+        if (e < n) {
+            const uint32_t b = (kmax - static_cast<uint32_t>(s[slot(e)] >> 32)) >> sh;
+            pk[r] = b | (atomicAdd(&cnt[b], 1u) << 12);
+        }
+    }
+    __syncthreads();
+    const uint4 c = reinterpret_cast<const uint4 *>(cnt)[threadIdx.x];
+    uint32_t big = c.x > c.y ? c.x : c.y;
+    big = c.z > big ? c.z : big;
+    big = c.w > big ? c.w : big;
+    if (block_reduce1024(big, true, s_tmp) > kFineMax) return false; // uniform
+    const uint32_t mine = c.x + c.y + c.z + c.w;
+    uint32_t total;
+    const uint32_t first = block_incl_scan1024(mine, s_tmp, total) - mine;
+    reinterpret_cast<uint4 *>(cnt)[threadIdx.x] = uint4{first, first + c.x, first + c.x + c.y, first + c.x + c.y + c.z};
+    __syncthreads();
+#pragma unroll
+    for (uint32_t r = 0; r < kSortPer; ++r) {
+        if (pk[r] == kNone) continue;
+        const uint32_t b = pk[r] & (kFineBins - 1), at = cnt[b] + (pk[r] >> 12); // < n
+        d[at] = s[slot(threadIdx.x + r * T)];
+        pk[r] = b | (at << 12);
+    }
+    __syncthreads();
+#pragma unroll
+    for (uint32_t r = 0; r < kSortPer; ++r) {
+        if (pk[r] == kNone) continue;
+        const uint32_t b = pk[r] & (kFineBins - 1);
+        const uint32_t b0 = cnt[b], b1 = b + 1 < kFineBins ? cnt[b + 1] : n; // at most kFineMax words
+        const uint64_t word = d[pk[r] >> 12];
+        uint32_t above = 0;
+        for (uint32_t i = b0; i < b1; ++i) above += d[i] > word ? 1u : 0u;
+        s[slot(b0 + above)] = word;
+    }
+    __syncthreads();
+    return true;
+}
+
+// Sorts the n words of s_c (by fine bins when the workgroup ranks and they
+// allow, else by merges), ranks the first `out` at slots slot0 + j and
 // returns their greatest race word (thread 0's).
 template <uint32_t T>
 __device__ uint64_t rank_words(const SmpGeo &g, const SmpOut &o, uint32_t row, uint32_t s0, uint64_t *s_c, uint32_t n,
-                               uint32_t out, uint32_t slot0)
+                               uint32_t out, uint32_t slot0, uint64_t *s_d, uint32_t *s_cnt, uint32_t *s_tmp,
+                               const LogfTab *tab, uint32_t pw)
 {
-    uint32_t np = kSortPer;
-    while (np < n) np <<= 1;
-    for (uint32_t i = n + threadIdx.x; i < np; i += T) s_c[slot(i)] = 0ull;
-    group_sync<T>();
-    lds_sort_desc<T>(s_c, np);
+    if (T == kWave || !bin_sort_desc(s_c, n, s_d, s_cnt, s_tmp)) {
+        uint32_t np = kSortPer;
+        while (np < n) np <<= 1;
+        for (uint32_t i = n + threadIdx.x; i < np; i += T) s_c[slot(i)] = 0ull;
+        group_sync<T>();
+        lds_sort_desc<T>(s_c, np);
+    }
     for (uint32_t j = threadIdx.x; j < out; j += T) write_ranked(g, o, row, slot0 + j, s_c[slot(j)]);
-    return race_best<T>(out, mulmod(s0, pm_power(slot0)), slot0,
-                        [&](uint32_t j) { return from_key(static_cast<uint32_t>(s_c[slot(j)] >> 32)); });
+    return race_best<T>(
+        out, mulmod(s0, pm_power(slot0)), slot0,
+        [&](uint32_t j) { return from_key(static_cast<uint32_t>(s_c[slot(j)] >> 32)); }, tab, pw);
 }
 
 // A workgroup's end (thread 0, holding `best`, the greatest race word of
@@ -2296,17 +2407,32 @@ __device__ void group_finish(const SmpGeo &g, const SmpOut &o, const SmpWs &w, u
     write_selection(g, o, row, b, [&](uint32_t) { return static_cast<int32_t>(bi); });
 }
 
+// Appends v to s (at slot(*s_n + k)) for the lanes where take holds, one LDS
+// atomic per wave; every lane of the wave calls it.
+__device__ __forceinline__ void wave_append(bool take, uint64_t v, uint32_t *s_n, uint64_t *s)
+{
+    const uint64_t m = __ballot(take);
+    if (m == 0) return; // uniform over the wave
+    const uint32_t lane = threadIdx.x % kWave, leader = static_cast<uint32_t>(__builtin_ctzll(m));
+    uint32_t base = 0;
+    if (lane == leader) base = atomicAdd(s_n, static_cast<uint32_t>(__builtin_popcountll(m)));
+    base = __shfl(base, static_cast<int>(leader), kWave);
+    const uint32_t e = base + static_cast<uint32_t>(__builtin_popcountll(m & ((1ull << lane) - 1)));
+    if (take && e < kCap) s[slot(e)] = v;
+}
+
 // Ranks the n <= kCap words staged in s_c, on wave 0 alone when they are few.
 __device__ void rank_group(const SmpGeo &g, const SmpOut &o, const SmpWs &w, uint32_t row, uint32_t q, uint32_t s0,
-                           uint64_t *s_c, uint32_t n, uint32_t out, uint32_t slot0, uint32_t groups)
+                           uint64_t *s_c, uint32_t n, uint32_t out, uint32_t slot0, uint32_t groups, uint64_t *s_d,
+                           uint32_t *s_cnt, uint32_t *s_tmp, const LogfTab *tab, uint32_t pw)
 {
     if (n <= kWave * kSortPer) { // uniform
         if (threadIdx.x >= kWave) return;
-        const uint64_t best = rank_words<kWave>(g, o, row, s0, s_c, n, out, slot0);
+        const uint64_t best = rank_words<kWave>(g, o, row, s0, s_c, n, out, slot0, s_d, s_cnt, s_tmp, tab, pw);
         group_finish(g, o, w, row, q, best, s_c, slot0, groups);
         return;
     }
-    const uint64_t best = rank_words<kRankThreads>(g, o, row, s0, s_c, n, out, slot0);
+    const uint64_t best = rank_words<kRankThreads>(g, o, row, s0, s_c, n, out, slot0, s_d, s_cnt, s_tmp, tab, pw);
     group_finish(g, o, w, row, q, best, s_c, slot0, groups);
 }
 
@@ -2315,10 +2441,14 @@ __global__ __launch_bounds__(kRankThreads) void k_smp_rank(SmpGeo g, float *logi
                                                            uint32_t row0, uint32_t groups)
 {
     __shared__ uint64_t s_c[kCapSlots];
-    __shared__ uint32_t s_hist[kBins]; // A: the group of each first digit; B: digit histograms
+    __shared__ uint64_t s_d[kCap];          // bin_sort_desc's scatter
+    __shared__ uint32_t s_hist[kFineBins];  // A: the group of each first digit; B: digit histograms; fine bins
     __shared__ uint32_t s_tmp[kRankThreads / kWave];
     __shared__ uint32_t s_pick[3];
     __shared__ uint32_t s_off, s_n;
+    __shared__ LogfTab s_tab;
+    stage_logf(&s_tab); // ordered by the barriers before the race
+    const uint32_t pw = kPmPowers.v[threadIdx.x];
     const uint32_t r = blockIdx.x / groups, q = blockIdx.x % groups, ga = groups - 1;
     const uint32_t row = row0 + r, s0 = st.v[r];
     const uint32_t b0 = 2 * threadIdx.x, b1 = b0 + 1;
@@ -2367,14 +2497,11 @@ __global__ __launch_bounds__(kRankThreads) void k_smp_rank(SmpGeo g, float *logi
 #pragma unroll
         for (uint32_t k = 0; k < kSortPer; ++k) {
             const uint32_t i = threadIdx.x + k * kRankThreads;
-            if (i < na && s_hist[static_cast<uint32_t>(v[k] >> 53)] == q) {
-                const uint32_t e = atomicAdd(&s_n, 1u);
-                if (e < kCap) s_c[slot(e)] = v[k];
-            }
+            wave_append(i < na && s_hist[static_cast<uint32_t>(v[k] >> 53)] == q, v[k], &s_n, s_c);
         }
         __syncthreads();
         const uint32_t n = s_n < kCap ? s_n : kCap;
-        rank_group(g, o, w, row, q, s0, s_c, n, n, off, groups);
+        rank_group(g, o, w, row, q, s0, s_c, n, n, off, groups, s_d, s_hist, s_tmp, &s_tab, pw);
         return;
     }
     // B: its largest need words after A's slots
@@ -2423,16 +2550,13 @@ __global__ __launch_bounds__(kRankThreads) void k_smp_rank(SmpGeo g, float *logi
 #pragma unroll
                 for (uint32_t k = 0; k < kSortPer; ++k) {
                     const uint32_t i = i0 + threadIdx.x + k * kRankThreads;
-                    if (i < nb && (static_cast<uint32_t>(v[k] >> 32) >> dshift) >= bs.prefix) {
-                        const uint32_t e = atomicAdd(&s_n, 1u);
-                        if (e < kCap) s_c[slot(e)] = v[k];
-                    }
+                    wave_append(i < nb && (static_cast<uint32_t>(v[k] >> 32) >> dshift) >= bs.prefix, v[k], &s_n, s_c);
                 }
             }
             __syncthreads();
             const uint32_t n = s_n; // bs.count <= kCap
             if (n <= kCap) { // uniform
-                rank_group(g, o, w, row, q, s0, s_c, n, need < n ? need : n, above, groups);
+                rank_group(g, o, w, row, q, s0, s_c, n, need < n ? need : n, above, groups, s_d, s_hist, s_tmp, &s_tab, pw);
                 return;
             }
         }
@@ -2446,7 +2570,7 @@ __global__ __launch_bounds__(kRankThreads) void k_smp_rank(SmpGeo g, float *logi
     __syncthreads(); // the list, written by the whole workgroup, is staged next
     const uint32_t n = rs.count < kCap ? rs.count : kCap;
     stage_words<kRankThreads>(s_c, blist, n, n);
-    rank_group(g, o, w, row, q, s0, s_c, n, g.top_k, 0, groups);
+    rank_group(g, o, w, row, q, s0, s_c, n, g.top_k, 0, groups, s_d, s_hist, s_tmp, &s_tab, pw);
 }
 
 // A launch whose rows can take the fast list: one workgroup per row

@@ -222,6 +222,38 @@ def test_fast_candidate_list_and_its_fallback(gpu):
     check(gpu, x, 1.0, 40, [11, 13, 17, 19])
 
 
+def test_bucket_path_cases(gpu):
+    """top_k 3000 over 40,000 logits (no fast list: the bucket path), one row
+    per case of the first-digit split (A: keys above the threshold's first
+    digit, B: keys at it):
+      row 0: N(0,1);
+      row 1: all logits equal -- B is the whole row, too long to list: the
+             selection by scans of the row, ties by index;
+      row 2: 20,000 logits at 1.0 under 1,000 larger ones -- B too long;
+      row 3: 12,000 at 1.0 -- B listed, cut down to its exact threshold,
+             where the ties exceed one workgroup's sort: scans again;
+      row 4: 5,000 at 1.0 -- B cut to its exact threshold, the ties sorted
+             by index;
+      row 5: NaN -- every probability NaN, one key;
+      row 6: logits spread over [-40, 40] -- B short, sorted uncut;
+      row 7: 5,000 at the maximum -- A empty, B the top digit."""
+    g = np.random.Generator(np.random.PCG64(84))
+    card, rows = 40000, 8
+    x = g.standard_normal((rows, card)).astype(np.float32)
+    x[1] = 0.5
+    for r, n in ((2, 20000), (3, 12000), (4, 5000)):
+        x[r] -= 4.0
+        cols = g.permutation(card)
+        x[r, cols[:n]] = 1.0
+        x[r, cols[n:n + 1000]] = 3.0 + g.random(1000).astype(np.float32)
+    x[5, 123] = np.nan
+    x[6] = np.linspace(-40, 40, card, dtype=np.float32)[g.permutation(card)]
+    x[7] = np.minimum(x[7], 2.0)
+    x[7, g.choice(card, 5000, replace=False)] = 3.0
+    got, _ = check(gpu, x, 1.0, 3000, [int(s) for s in g.integers(1, M, rows)])
+    assert got[5]["sel"] == -1
+
+
 def test_unaligned_and_padded_rows(gpu):
     g = np.random.Generator(np.random.PCG64(77))
     x = g.standard_normal((4, 12345)).astype(np.float32)
