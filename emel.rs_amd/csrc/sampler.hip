@@ -57,18 +57,18 @@
 //                 - every row: sort of the candidates in LDS (key descending
 //                   then index ascending: register runs merged by merge
 //                   path), the ranked outputs, then the race selection.
-// Otherwise, for top_k <= kCap:
-//   k_smp_bucket  (row, chunk): the first digit P1 of the threshold from
-//                 k_smp_div's histogram; the keys of a higher first digit
-//                 (all candidates) into the row's candidate list, the keys at
-//                 P1 into its bucket list, in one pass.
+// Otherwise, for top_k <= kCap (the bucket path), the exponential pass also
+// counts e's first digits, k_smp_sum turns the digit holding the top_k-th
+// largest e into a bracket [blo, bhi] of p's keys, and k_smp_div lists the
+// keys above bhi (A) into the candidate list and those in the bracket (B)
+// into the bucket list; then
 //   k_smp_rank    a few 1024-thread workgroups per row: groups of whole first
-//                 digits of the candidate list, each sorted in LDS at its
-//                 known offset, and the bucket list, cut by its next digits
-//                 and sorted, after them; each races its own slots and the
-//                 row's last workgroup writes the selection.  Rows whose
-//                 bucket is too large take the radix selection from scans of
-//                 the row in one workgroup.
+//                 digits of A, each sorted in LDS at its known offset, and B,
+//                 cut by digits of its own histograms and sorted, after them;
+//                 each races its own slots and the row's last workgroup
+//                 writes the selection.  A row whose lists do not select
+//                 (|A| < top_k <= |A| + |B| fails, or B overflows) takes the
+//                 radix selection from scans of the row in one workgroup.
 // For top_k > kCap the selection runs as k_smp_resolve (one workgroup per
 // row, the ties at T counted per chunk) and k_smp_collect ((row, chunk)
 // workgroups), and the list is sorted as kCap tiles (k_smp_tile_sort),
@@ -111,8 +111,10 @@ struct RowSel {
     uint32_t fast_count; // keys >= fast_key found; > kCap: the radix path decides
     uint32_t ethr_on;    // e_thr found (k_smp_expseg's head workgroup)
     uint32_t ethr_key;   // key of e_thr
+    uint32_t bon;        // the bucket path's bracket [blo, bhi] is set (k_smp_sum)
+    uint32_t blo, bhi;   // keys: A above bhi, B in [blo, bhi] (k_smp_div lists both)
     uint32_t gdone;      // k_smp_rank: workgroups of the row finished
-    uint64_t gfill;      // k_smp_bucket: words listed, above P1 (low half) and at P1 (high half)
+    uint64_t gfill;      // k_smp_div: words listed, A (low half) and B (high half)
 };
 constexpr uint32_t kMaxGroups = 8; // k_smp_rank workgroups per row
 // One k_smp_rank workgroup's result: its greatest race_word and the token of
@@ -121,7 +123,7 @@ struct GroupBest {
     uint64_t word;
     uint64_t idx;
 };
-constexpr uint32_t kBucketCap = 16384; // words a row's bucket list holds (keys at the threshold's first digit)
+constexpr uint32_t kBucketCap = 16384; // words a row's bucket list (B) holds
 
 struct SmpGeo {
     uint32_t rows;
@@ -185,7 +187,8 @@ struct SmpWs {
     uint32_t *ties; // rows * chunks
     uint64_t *cand; // rows * cand_ld
     uint64_t *cand2; // rows * cand_ld (merge ping-pong, top_k > kCap)
-    uint64_t *bucket; // rows * kBucketCap (k_smp_bucket's lists; the bucket path only)
+    uint32_t *ehist;  // rows * kBins: first-digit histogram of e (the bucket path)
+    uint64_t *bucket; // rows * kBucketCap (B lists; the bucket path only)
     GroupBest *gbest; // rows * kMaxGroups (the bucket path only)
 };
 
@@ -386,6 +389,32 @@ __device__ __forceinline__ float approx_exp(float x)
 // FUSED (chunks of at most kFuseSubs sub-chunks) reads the chunk as
 // k_smp_expseg does, lane l of a wave holding elements kPer l .. kPer l +
 // kPer - 1 of a sub-chunk, and also leaves each sub-chunk's maximum and
+constexpr uint32_t kFastPer = 8;         // sub-chunk maxima per lane for the fast threshold
+
+// Whether a launch's rows can take the fast list: the fused path, top_k
+// within kCap and within the row's sub-chunk count, at most kFastPer
+// sub-chunks per lane.
+__host__ __device__ inline bool fast_list_possible(const SmpGeo &g)
+{
+    const uint64_t spc = (g.chunk_cols + kSub - 1) / kSub, nslots = uint64_t{g.chunks} * spc;
+    const uint64_t last = g.card - uint64_t{g.chunks - 1} * g.chunk_cols;
+    const uint64_t nsub = uint64_t{g.chunks - 1} * spc + (last + kSub - 1) / kSub; // sub-chunks with elements
+    return g.chunk_cols <= kFuseCols && g.top_k <= kCap && nslots <= kWave * kFastPer && nsub >= g.top_k;
+}
+
+// The bucket path: top_k <= kCap without the fast list.
+__host__ __device__ inline bool bucket_path(const SmpGeo &g) { return g.top_k <= kCap && !fast_list_possible(g); }
+
+// Adds the LDS histogram of a workgroup to the row's global histogram.
+__device__ __forceinline__ void flush_hist(uint32_t *s_hist, uint32_t nbins, uint32_t *dst)
+{
+    __syncthreads();
+    for (uint32_t b = threadIdx.x; b < nbins; b += blockDim.x) {
+        const uint32_t c = s_hist[b];
+        if (c) atomicAdd(dst + b, c);
+    }
+}
+
 // approximate sum of exp(v - that maximum) in sub, and in psum the chunk's
 // approximate sum of exp(v - chunk maximum): k_smp_expseg's binade
 // predictions start from them.
@@ -396,7 +425,10 @@ __global__ __launch_bounds__(kBlock) void k_smp_max(SmpGeo g, float *logits, Smp
     float *x = logits + static_cast<int64_t>(row) * g.ld;
     if (chunk == 0) {
         // fresh per-row state for this call
-        for (uint32_t b = threadIdx.x; b < kBins; b += blockDim.x) w.hist[static_cast<uint64_t>(row) * kBins + b] = 0;
+        for (uint32_t b = threadIdx.x; b < kBins; b += blockDim.x) {
+            w.hist[static_cast<uint64_t>(row) * kBins + b] = 0;
+            w.ehist[static_cast<uint64_t>(row) * kBins + b] = 0;
+        }
         if (threadIdx.x == 0) {
             RowSel s{};
             s.need = g.top_k;
@@ -515,13 +547,19 @@ __device__ __forceinline__ float row_max(const SmpGeo &g, const SmpWs &w, uint32
 
 // ---- stage 2: e = expf(v - m) in place --------------------------------------
 
+template <bool EH> // the bucket path: also the histogram of e's first digits
 __global__ __launch_bounds__(kBlock) void k_smp_exp(SmpGeo g, float *logits, SmpWs w)
 {
     const uint32_t row = blockIdx.x / g.chunks, chunk = blockIdx.x % g.chunks;
     float *x = logits + static_cast<int64_t>(row) * g.ld;
-    // expf's 2^(i/32) table in LDS, ordered by row_max's barrier
+    // expf's 2^(i/32) table in LDS and the e histogram's reset, ordered by
+    // row_max's barrier
     __shared__ uint64_t s_tab[32];
+    __shared__ uint32_t s_eh[EH ? kBins : 1];
+    constexpr bool eh = EH;
     if (threadIdx.x < 32) s_tab[threadIdx.x] = kExp2Table[threadIdx.x];
+    if constexpr (eh)
+        for (uint32_t b = threadIdx.x; b < kBins; b += blockDim.x) s_eh[b] = 0;
     const float m = row_max(g, w, row);
     uint64_t c0, c1;
     chunk_range(g, chunk, c0, c1);
@@ -534,7 +572,9 @@ __global__ __launch_bounds__(kBlock) void k_smp_exp(SmpGeo g, float *logits, Smp
         const float s = v * scale;
         v = emel_expf(s - m, s_tab, ec);
         acc += static_cast<double>(v);
+        if constexpr (eh) atomicAdd(&s_eh[total_key(v) >> 21], 1u);
     });
+    if constexpr (eh) flush_hist(s_eh, kBins, w.ehist + static_cast<uint64_t>(row) * kBins);
     // f64 chunk sum: only a prediction of where the exact sum's binades
     // change (k_smp_seg); never part of a result
     __shared__ double s_acc[kBlock / kWave];
@@ -846,7 +886,6 @@ __device__ __forceinline__ double readlane_f64(double v, uint32_t l)
     return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
 }
 
-constexpr uint32_t kFastPer = 8;         // sub-chunk maxima per lane for the fast threshold
 constexpr uint32_t kFastBits = 14;       // low key bits the fast threshold leaves 0 (2^-9 of e_thr at most)
 
 // The fast candidate threshold, by one wave.  The top_k largest sub-chunk
@@ -858,17 +897,6 @@ constexpr uint32_t kFastBits = 14;       // low key bits the fast threshold leav
 // those elements directly.  Returns false when the row cannot take it
 // (three-pass chunks, top_k above kCap or above the sub-chunk count, more
 // than kFastPer sub-chunks per lane).
-// Whether a launch's rows can take the fast list: the fused path, top_k
-// within kCap and within the row's sub-chunk count, at most kFastPer
-// sub-chunks per lane.
-__host__ __device__ inline bool fast_list_possible(const SmpGeo &g)
-{
-    const uint64_t spc = (g.chunk_cols + kSub - 1) / kSub, nslots = uint64_t{g.chunks} * spc;
-    const uint64_t last = g.card - uint64_t{g.chunks - 1} * g.chunk_cols;
-    const uint64_t nsub = uint64_t{g.chunks - 1} * spc + (last + kSub - 1) / kSub; // sub-chunks with elements
-    return g.chunk_cols <= kFuseCols && g.top_k <= kCap && nslots <= kWave * kFastPer && nsub >= g.top_k;
-}
-
 __device__ bool fast_threshold(const SmpGeo &g, const SmpWs &w, uint32_t row, uint32_t lane, const uint64_t *tab,
                                uint32_t &ethr_key)
 {
@@ -953,6 +981,7 @@ __device__ __forceinline__ void expseg_head(const SmpGeo &g, const float *logits
 }
 
 // Grid: g.rows head workgroups (expseg_head), then one per (row, chunk).
+template <bool EH> // the bucket path: also the histogram of e's first digits
 __global__ __launch_bounds__(kBlock) void k_smp_expseg(SmpGeo g, float *logits, SmpWs w)
 {
     const uint32_t lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
@@ -980,6 +1009,13 @@ __global__ __launch_bounds__(kBlock) void k_smp_expseg(SmpGeo g, float *logits, 
     float *x = logits + static_cast<int64_t>(row) * g.ld;
     uint64_t c0, c1;
     chunk_range(g, chunk, c0, c1);
+    // the bucket path: the histogram of e's first digits (flushed at the end)
+    __shared__ uint32_t s_eh[EH ? kBins : 1];
+    constexpr bool eh = EH;
+    if constexpr (eh) {
+        for (uint32_t d = threadIdx.x; d < kBins; d += blockDim.x) s_eh[d] = 0;
+        __syncthreads();
+    }
     const uint32_t spc = subs_per_chunk(g);
     const uint32_t nsub = static_cast<uint32_t>((c1 - c0 + kSub - 1) / kSub); // <= kFuseSubs
     auto sub_col = [&](uint32_t k) { return c0 + static_cast<uint64_t>(k) * kSub; };
@@ -1034,10 +1070,17 @@ __global__ __launch_bounds__(kBlock) void k_smp_expseg(SmpGeo g, float *logits, 
         if (a0 + kSub <= c1) { // only a row's last sub-chunk can end early
 #pragma unroll
             for (uint32_t q = 0; q < kPer; ++q) cur[q] = emel_expf(cur[q] * scale - m, tab, ec);
+            if constexpr (eh)
+#pragma unroll
+                for (uint32_t q = 0; q < kPer; ++q) atomicAdd(&s_eh[total_key(cur[q]) >> 21], 1u);
         } else {
 #pragma unroll
-            for (uint32_t q = 0; q < kPer; ++q)
-                cur[q] = split_col(a0, lane, q) < c1 ? emel_expf(cur[q] * scale - m, tab, ec) : 0.0f;
+            for (uint32_t q = 0; q < kPer; ++q) {
+                const bool in = split_col(a0, lane, q) < c1;
+                cur[q] = in ? emel_expf(cur[q] * scale - m, tab, ec) : 0.0f;
+                if constexpr (eh)
+                    if (in) atomicAdd(&s_eh[total_key(cur[q]) >> 21], 1u);
+            }
         }
 #pragma unroll
         for (uint32_t h = 0; h < kSplit; ++h) {
@@ -1059,6 +1102,7 @@ __global__ __launch_bounds__(kBlock) void k_smp_expseg(SmpGeo g, float *logits, 
             for (uint32_t q = 0; q < kPer; ++q) cur[q] = nxt[q];
         }
     }
+    if constexpr (eh) flush_hist(s_eh, kBins, w.ehist + static_cast<uint64_t>(row) * kBins);
 }
 
 // ---- stage 3: the exact sequential sum of e ----------------------------------
@@ -1077,8 +1121,9 @@ constexpr uint32_t kFastWg = 256;        // fast candidates a k_smp_div workgrou
 constexpr uint32_t kStage = 24;          // walked sub-chunks k_smp_sum's second wave stages in LDS
 
 
-// One wave per row walks (wave 0); wave 1 computes the fast candidate
-// threshold beside it, off the walk's path.  The sub-chunks' predictions are
+// One wave per row walks (wave 0); wave 1 stages sub-chunks for it, and on
+// the bucket path a third wave picks e's first digit holding the top_k-th
+// largest e, both off the walk's path.  The sub-chunks' predictions are
 // read a batch at a time (lane i holds sub-chunk kb + i's).  A sub-chunk
 // whose predicted contribution holds on the exact state -- the same binade,
 // and the units (its one tie resolved by the current parity) stay below
@@ -1191,7 +1236,7 @@ __device__ __forceinline__ uint32_t crossing_step(const LaneScan ls, const float
     return kStepDone;
 }
 
-constexpr uint32_t kSumThreads = 2 * kWave;
+constexpr uint32_t kSumThreads = 3 * kWave; // the third wave on the bucket path only
 
 __global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *logits, SmpWs w)
 {
@@ -1203,6 +1248,7 @@ __global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *
     __shared__ LaneScan s_lanes[kStage][kWave]; // with a usable plan: the lane scans (crossing_step)
     __shared__ float4 s_own[kPer / 4][kWave];   // wave 0: a sub-chunk it loaded, for crossing_step
     __shared__ uint32_t s_ready;
+    __shared__ uint32_t s_edig; // the bucket path: e's first digit holding the top_k-th largest e
     const uint32_t row = blockIdx.x;
     const uint32_t lane = threadIdx.x % kWave;
     const float *x = logits + static_cast<int64_t>(row) * g.ld;
@@ -1262,9 +1308,34 @@ __global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *
             for (uint32_t j = 0; j < kPer; ++j) e[j] = c + j < n ? e[j] : 0.0f;
         }
     };
-    if (threadIdx.x == 0) s_ready = 0;
+    if (threadIdx.x == 0) {
+        s_ready = 0;
+        s_edig = kNone;
+    }
     __syncthreads();
-    if (threadIdx.x >= kWave) { // wave 1
+    if (threadIdx.x >= 2 * kWave) { // wave 2 (the bucket path)
+        // e's first digit holding the top_k-th largest e (every e counted
+        // once by the exponential pass), 32 digits per lane
+        const uint4 *eh = reinterpret_cast<const uint4 *>(w.ehist + static_cast<uint64_t>(row) * kBins) + 8 * lane;
+        uint32_t c[32], local = 0;
+#pragma unroll
+        for (uint32_t i = 0; i < 8; ++i) {
+            const uint4 h = eh[i];
+            c[4 * i] = h.x;
+            c[4 * i + 1] = h.y;
+            c[4 * i + 2] = h.z;
+            c[4 * i + 3] = h.w;
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < 32; ++i) local += c[i];
+        const uint32_t incl = wave_incl_scan(local);
+        uint32_t cum = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), kWave - 1)) - incl;
+#pragma unroll
+        for (int i = 31; i >= 0; --i) {
+            if (cum < g.top_k && g.top_k <= cum + c[i]) s_edig = 32 * lane + static_cast<uint32_t>(i);
+            cum += c[i];
+        }
+    } else if (threadIdx.x >= kWave) { // wave 1
         // Stage, in slot order, the sub-chunks marked as probably walked
         // (almost every sub-chunk the walk loads).  The walk takes a staged
         // sub-chunk from LDS when it is ready and loads it itself otherwise,
@@ -1433,29 +1504,31 @@ __global__ __launch_bounds__(kSumThreads) void k_smp_sum(SmpGeo g, const float *
         }
         marked += static_cast<uint32_t>(__builtin_popcountll(wmask));
     }
-    if (lane == 0) {
+    } // wave 0
+    __syncthreads(); // wave 2's digit of e
+    if (threadIdx.x == 0) {
         const float S = s.finite ? seq_value(s.m, s.u) : s.special;
+        const double recip = 1.0 / static_cast<double>(S);
         w.sel[row].total = S;
         // p_thr = e_thr / S, as k_smp_div divides (a NaN or +inf sum takes the radix path)
         if (w.sel[row].ethr_on && s.finite) {
-            w.sel[row].fast_key = total_key(div_by_recip(from_key(w.sel[row].ethr_key), 1.0 / static_cast<double>(S)));
+            w.sel[row].fast_key = total_key(div_by_recip(from_key(w.sel[row].ethr_key), recip));
             w.sel[row].fast_on = 1u;
         }
+        // The bucket path's bracket: p's keys of the digit's least e and of
+        // the next digit's least e.  p is monotone in e, so the top_k-th
+        // largest p lies in [blo, bhi] and fewer than top_k keys exceed bhi;
+        // k_smp_rank relies on neither and checks the counts of its lists.
+        const uint32_t d = s_edig;
+        if (d != kNone && s.finite) {
+            w.sel[row].blo = total_key(div_by_recip(from_key(d << 21), recip));
+            w.sel[row].bhi = d + 1 < kBins ? total_key(div_by_recip(from_key((d + 1) << 21), recip)) : 0xffffffffu;
+            w.sel[row].bon = 1u;
+        }
     }
-    } // wave 0
 }
 
 // ---- stage 4: p = e / S in place, first radix digit -------------------------
-
-// Adds the LDS histogram of a workgroup to the row's global histogram.
-__device__ __forceinline__ void flush_hist(uint32_t *s_hist, uint32_t nbins, uint32_t *dst)
-{
-    __syncthreads();
-    for (uint32_t b = threadIdx.x; b < nbins; b += blockDim.x) {
-        const uint32_t c = s_hist[b];
-        if (c) atomicAdd(dst + b, c);
-    }
-}
 
 // Rows with a fast threshold (k_smp_sum) also list every key >= fast_key:
 // buffered per workgroup in LDS, then placed with one atomic.  A workgroup
@@ -1508,6 +1581,127 @@ __global__ __launch_bounds__(kBlock) void k_smp_div(SmpGeo g, float *logits, Smp
     if (n <= kFastWg)
         for (uint32_t i = threadIdx.x; i < n; i += blockDim.x)
             if (base + i < kCap) list[base + i] = s_fbuf[i];
+}
+
+// The bucket path's division: p = e / S in place and the first-digit
+// histogram, as k_smp_div, and the lists of the row's bracket: A (keys above
+// bhi) into the candidate list, B (keys in [blo, bhi]) into the bucket list.
+// Steps of kDivVec float4 per thread (5120 columns per workgroup: config 5's
+// chunk in one step).  Per step each thread counts its A and B words, a wave
+// prefix sum of the packed counts places them in the workgroup's LDS buffers
+// (kListWg words each, one LDS atomic per wave and list); words past a
+// buffer take a global atomic of their own.  At the end one 64-bit atomic
+// (A low half, B high half) places the buffers.  The counts are exact, the
+// lists complete up to their capacities.
+constexpr uint32_t kDivVec = 5;
+constexpr uint32_t kListWg = 512;
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_smp_divlist(SmpGeo g, float *logits, SmpWs w)
+{
+    __shared__ uint32_t s_hist[kBins];
+    __shared__ uint64_t s_lbuf[2][kListWg];
+    __shared__ uint32_t s_lcnt[2];
+    __shared__ uint64_t s_lbase;
+    const uint32_t row = blockIdx.x / g.chunks, chunk = blockIdx.x % g.chunks;
+    const uint32_t lane = threadIdx.x % kWave;
+    float *x = logits + static_cast<int64_t>(row) * g.ld;
+    for (uint32_t b = threadIdx.x; b < kBins; b += blockDim.x) s_hist[b] = 0;
+    if (threadIdx.x == 0) s_lcnt[0] = s_lcnt[1] = 0;
+    const float total = w.sel[row].total;
+    const bool lst = w.sel[row].bon != 0; // uniform; else no list (k_smp_rank scans the row)
+    const uint32_t blo = w.sel[row].blo, bhi = w.sel[row].bhi;
+    __syncthreads();
+    const double recip = 1.0 / static_cast<double>(total); // as k_smp_div
+    uint64_t *alist = w.cand + static_cast<uint64_t>(row) * g.cand_ld;
+    uint64_t *blist = w.bucket + static_cast<uint64_t>(row) * kBucketCap;
+    unsigned long long *fill = reinterpret_cast<unsigned long long *>(&w.sel[row].gfill);
+    uint64_t c0, c1;
+    chunk_range(g, chunk, c0, c1);
+    const uint32_t e1 = static_cast<uint32_t>(c1); // card < 2^31
+    for (uint64_t blk = c0; blk < c1; blk += 4ull * kDivVec * kBlock) {
+        const uint32_t col0 = static_cast<uint32_t>(blk) + 4u * threadIdx.x; // float4 i at col0 + 4 kBlock i
+        float4 q[kDivVec];
+#pragma unroll
+        for (uint32_t i = 0; i < kDivVec; ++i) {
+            const uint32_t c = col0 + 4u * kBlock * i;
+            if (g.vec && c + 4 <= e1) {
+                q[i] = *reinterpret_cast<const float4 *>(x + c);
+            } else {
+                q[i].x = c < e1 ? x[c] : 0.0f;
+                q[i].y = c + 1 < e1 ? x[c + 1] : 0.0f;
+                q[i].z = c + 2 < e1 ? x[c + 2] : 0.0f;
+                q[i].w = c + 3 < e1 ? x[c + 3] : 0.0f;
+            }
+        }
+        uint32_t key[4 * kDivVec];
+        uint32_t na = 0, nb = 0;
+#pragma unroll
+        for (uint32_t i = 0; i < kDivVec; ++i) {
+            float *f = reinterpret_cast<float *>(&q[i]);
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j) {
+                const bool in = col0 + 4u * kBlock * i + j < e1;
+                f[j] = div_by_recip(f[j], recip);
+                const uint32_t k = total_key(f[j]);
+                key[4 * i + j] = k;
+                if (in) atomicAdd(&s_hist[k >> 21], 1u);
+                na += (lst && in && k > bhi) ? 1u : 0u;
+                nb += (lst && in && k >= blo && k <= bhi) ? 1u : 0u;
+            }
+            const uint32_t c = col0 + 4u * kBlock * i;
+            if (g.vec && c + 4 <= e1) {
+                *reinterpret_cast<float4 *>(x + c) = q[i];
+            } else {
+#pragma unroll
+                for (uint32_t j = 0; j < 4; ++j)
+                    if (c + j < e1) x[c + j] = f[j];
+            }
+        }
+        // per wave: the A and B words of this step (at most 16 each per lane)
+        const uint32_t incl = wave_incl_scan(na | (nb << 16));
+        const uint32_t wtot = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), kWave - 1));
+        if (wtot == 0) continue; // uniform over the wave
+        uint32_t ba = 0, bb = 0;
+        if (lane == kWave - 1) {
+            if (wtot & 0xffffu) ba = atomicAdd(&s_lcnt[0], wtot & 0xffffu);
+            if (wtot >> 16) bb = atomicAdd(&s_lcnt[1], wtot >> 16);
+        }
+        uint32_t sa = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(ba), kWave - 1)) + (incl & 0xffffu) - na;
+        uint32_t sb = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(bb), kWave - 1)) + (incl >> 16) - nb;
+#pragma unroll
+        for (uint32_t j = 0; j < 4 * kDivVec; ++j) {
+            const uint32_t col = col0 + 4u * kBlock * (j / 4) + j % 4;
+            const uint32_t k = key[j];
+            const bool in = lst && col < e1;
+            if (in && k > bhi) {
+                if (sa < kListWg) {
+                    s_lbuf[0][sa] = cand_word(k, col);
+                } else { // past the buffer
+                    const uint32_t at = static_cast<uint32_t>(atomicAdd(fill, 1ull));
+                    if (at < g.cand_ld) alist[at] = cand_word(k, col);
+                }
+                ++sa;
+            } else if (in && k >= blo) {
+                if (sb < kListWg) {
+                    s_lbuf[1][sb] = cand_word(k, col);
+                } else {
+                    const uint32_t at = static_cast<uint32_t>(atomicAdd(fill, 1ull << 32) >> 32);
+                    if (at < kBucketCap) blist[at] = cand_word(k, col);
+                }
+                ++sb;
+            }
+        }
+    }
+    flush_hist(s_hist, kBins, w.hist + static_cast<uint64_t>(row) * kBins); // its barrier orders the buffers
+    const uint32_t na = s_lcnt[0] < kListWg ? s_lcnt[0] : kListWg, nb = s_lcnt[1] < kListWg ? s_lcnt[1] : kListWg;
+    if (na + nb == 0) return; // uniform
+    if (threadIdx.x == 0)
+        s_lbase = atomicAdd(fill, static_cast<unsigned long long>(na) | (static_cast<unsigned long long>(nb) << 32));
+    __syncthreads();
+    const uint32_t ba = static_cast<uint32_t>(s_lbase), bb = static_cast<uint32_t>(s_lbase >> 32);
+    for (uint32_t i = threadIdx.x; i < na; i += blockDim.x)
+        if (ba + i < g.cand_ld) alist[ba + i] = s_lbuf[0][i];
+    for (uint32_t i = threadIdx.x; i < nb; i += blockDim.x)
+        if (bb + i < kBucketCap) blist[bb + i] = s_lbuf[1][i];
 }
 
 // Inclusive prefix sum over a 256-thread workgroup (uses s_tmp[4]).
@@ -1568,7 +1762,7 @@ __device__ __forceinline__ uint32_t block_incl_scan1024(uint32_t v, uint32_t *s_
 
 // The pick over hist[0, 2^bits), bins in increasing key order; returns the
 // advanced selection (the same in every thread).
-__device__ RowSel pick_digit(const RowSel &sel, const uint32_t *hist, uint32_t bits, uint32_t *s_tmp,
+__device__ __forceinline__ RowSel pick_digit(const RowSel &sel, const uint32_t *hist, uint32_t bits, uint32_t *s_tmp,
                              uint32_t *s_pick)
 {
     const uint32_t per = (1u << bits) / kResolveThreads; // 2 or 1 bins per thread
@@ -1768,149 +1962,6 @@ __global__ __launch_bounds__(kBlock) void k_smp_collect(SmpGeo g, float *logits,
     }
 }
 
-
-// ---- the bucket path: top_k <= kCap without the fast list -------------------
-//
-// The first digit P1 of the threshold (the top 11 key bits of the top_k-th
-// largest key) splits a row's keys in two: A, a higher first digit, every key
-// a candidate (fewer than top_k of them), and B, first digit P1, whose
-// largest top_k - |A| keys complete the candidates.  Ranked, A fills the
-// slots [0, |A|) and B the rest.  k_smp_bucket, one (row, chunk) workgroup
-// per chunk, picks P1 from k_smp_div's histogram (every workgroup of the row
-// alike) and lists A into the row's candidate list and B into its bucket list
-// in one pass over the row; k_smp_rank sorts them.
-
-struct FirstDigit {
-    uint32_t digit, above, inb; // P1, |A|, |B|
-};
-
-// P1 from the row's first-digit histogram by a kBlock workgroup, thread t
-// holding digits [8t, 8t + 8) in h0, h1.
-static_assert(kBins == 8 * kBlock, "two uint4 of the histogram per thread");
-__device__ FirstDigit first_digit256(uint4 h0, uint4 h1, uint32_t top_k, uint32_t *s_tmp, uint32_t *s_pick)
-{
-    constexpr uint32_t per = kBins / kBlock;
-    const uint32_t mine[per] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
-    uint32_t local = 0;
-#pragma unroll
-    for (uint32_t i = 0; i < per; ++i) local += mine[i];
-    uint32_t total;
-    const uint32_t incl = block_incl_scan256(local, s_tmp, total);
-    uint32_t cum = total - incl; // keys in the higher threads' (higher) digits
-#pragma unroll
-    for (int i = per - 1; i >= 0; --i) {
-        if (cum < top_k && top_k <= cum + mine[i]) {
-            s_pick[0] = threadIdx.x * per + static_cast<uint32_t>(i);
-            s_pick[1] = cum;
-            s_pick[2] = mine[i];
-        }
-        cum += mine[i];
-    }
-    __syncthreads();
-    return FirstDigit{s_pick[0], s_pick[1], s_pick[2]};
-}
-
-// Steps of kBucketVec float4 per thread (5120 columns per workgroup: config
-// 5's chunk in one step).  The histogram's loads, then the first step's, are
-// issued before P1 is picked, so the pick overlaps the chunk's memory round
-// trip.  One prefix sum of the packed counts (A low, B high half: at most
-// 5120 each) places both lists' words, and one 64-bit atomic per step
-// reserves them.  A has fewer than top_k <= cand_ld words; B is listed when
-// it fits kBucketCap (else k_smp_rank selects from scans of the row).
-constexpr uint32_t kBucketVec = 5;
-__device__ __forceinline__ void bucket_load(const SmpGeo &g, const float *x, uint64_t col0, uint64_t c1,
-                                            float4 (&q)[kBucketVec])
-{
-#pragma unroll
-    for (uint32_t i = 0; i < kBucketVec; ++i) {
-        const uint64_t c = col0 + 4ull * kBlock * i;
-        if (g.vec && c + 4 <= c1) {
-            q[i] = *reinterpret_cast<const float4 *>(x + c);
-        } else {
-            q[i].x = c < c1 ? x[c] : 0.0f;
-            q[i].y = c + 1 < c1 ? x[c + 1] : 0.0f;
-            q[i].z = c + 2 < c1 ? x[c + 2] : 0.0f;
-            q[i].w = c + 3 < c1 ? x[c + 3] : 0.0f;
-        }
-    }
-}
-
-// Lists one step's columns [col0 + 4 kBlock i + j) of q.
-__device__ __forceinline__ void bucket_step(const SmpGeo &g, const SmpWs &w, uint32_t row, const FirstDigit &f,
-                                            const float4 (&q)[kBucketVec], uint32_t col0, uint32_t c1,
-                                            uint32_t *s_tmp, uint64_t *s_base)
-{
-    uint32_t key[4 * kBucketVec];
-#pragma unroll
-    for (uint32_t i = 0; i < kBucketVec; ++i) {
-        key[4 * i] = total_key(q[i].x);
-        key[4 * i + 1] = total_key(q[i].y);
-        key[4 * i + 2] = total_key(q[i].z);
-        key[4 * i + 3] = total_key(q[i].w);
-    }
-    uint32_t na = 0, nb = 0; // columns from c1 on (a row's last step) are not listed
-#pragma unroll
-    for (uint32_t j = 0; j < 4 * kBucketVec; ++j) {
-        const bool in = col0 + 4u * kBlock * (j / 4) + j % 4 < c1; // columns < 2^31
-        const uint32_t d = key[j] >> 21;
-        na += (in && d > f.digit) ? 1u : 0u;
-        nb += (in && d == f.digit) ? 1u : 0u;
-    }
-    uint32_t tot;
-    const uint32_t incl = block_incl_scan256(na | (nb << 16), s_tmp, tot);
-    if (tot == 0) return; // uniform
-    if (threadIdx.x == 0)
-        *s_base = atomicAdd(reinterpret_cast<unsigned long long *>(&w.sel[row].gfill),
-                            static_cast<unsigned long long>(tot & 0xffffu) |
-                                (static_cast<unsigned long long>(tot >> 16) << 32));
-    __syncthreads();
-    const uint64_t base = *s_base;
-    __syncthreads(); // s_base and s_tmp are rewritten by the next step
-    uint32_t sa = static_cast<uint32_t>(base) + (incl & 0xffffu) - na;
-    uint32_t sb = static_cast<uint32_t>(base >> 32) + (incl >> 16) - nb;
-    uint64_t *alist = w.cand + static_cast<uint64_t>(row) * g.cand_ld;
-    uint64_t *blist = w.bucket + static_cast<uint64_t>(row) * kBucketCap;
-    const bool list_b = f.inb <= kBucketCap;
-#pragma unroll
-    for (uint32_t j = 0; j < 4 * kBucketVec; ++j) {
-        const uint32_t col = col0 + 4u * kBlock * (j / 4) + j % 4;
-        const bool in = col < c1;
-        const uint32_t d = key[j] >> 21;
-        if (in && d > f.digit) {
-            if (sa < g.cand_ld) alist[sa] = cand_word(key[j], col);
-            ++sa;
-        } else if (in && d == f.digit) {
-            if (list_b && sb < kBucketCap) blist[sb] = cand_word(key[j], col);
-            ++sb;
-        }
-    }
-}
-
-__global__ __launch_bounds__(kBlock) void k_smp_bucket(SmpGeo g, const float *logits, SmpWs w)
-{
-    __shared__ uint32_t s_tmp[kBlock / kWave];
-    __shared__ uint32_t s_pick[3];
-    __shared__ uint64_t s_base;
-    const uint32_t row = blockIdx.x / g.chunks, chunk = blockIdx.x % g.chunks;
-    const float *x = logits + static_cast<int64_t>(row) * g.ld;
-    uint64_t c0, c1;
-    chunk_range(g, chunk, c0, c1);
-    const uint4 *hist = reinterpret_cast<const uint4 *>(w.hist + static_cast<uint64_t>(row) * kBins);
-    const uint4 h0 = hist[2 * threadIdx.x], h1 = hist[2 * threadIdx.x + 1];
-    constexpr uint64_t step = 4ull * kBucketVec * kBlock;
-    {
-        float4 q[kBucketVec];
-        bucket_load(g, x, c0 + 4ull * threadIdx.x, c1, q);
-        const FirstDigit f = first_digit256(h0, h1, g.top_k, s_tmp, s_pick);
-        const uint32_t e1 = static_cast<uint32_t>(c1); // card < 2^31
-        bucket_step(g, w, row, f, q, static_cast<uint32_t>(c0) + 4u * threadIdx.x, e1, s_tmp, &s_base);
-        for (uint64_t blk = c0 + step; blk < c1; blk += step) {
-            __syncthreads(); // s_tmp: the previous step's scan is read
-            bucket_load(g, x, blk + 4ull * threadIdx.x, c1, q);
-            bucket_step(g, w, row, f, q, static_cast<uint32_t>(blk) + 4u * threadIdx.x, e1, s_tmp, &s_base);
-        }
-    }
-}
 
 // ---- stage 9: ranking and selection -----------------------------------------
 
@@ -2252,18 +2303,19 @@ __device__ void collect_row(const SmpGeo &g, const float *x, uint64_t *list, con
 }
 
 // The bucket path's ranking: `groups` workgroups per row.  Groups q <
-// groups - 1 take A's first digits, digit b > P1 to group floor(cb(b)
-// (groups - 1) / |A|), cb(b) the keys of the higher digits: a group holds
-// whole digits, at most |A| < kCap keys, and its slots start at the least cb
-// of its digits.  The last group takes B from the bucket list, cut by the
-// next digits (histograms of the list, as pick_digit) when it is longer than
-// kSortDirect, and ranks B's first top_k - |A| words after A.  A row whose B
-// was not listed, or whose ties at an exact threshold exceed kCap, is
-// selected by the last group alone from scans of the row (resolve_row,
-// collect_row, in the bucket list's place) and ranked whole; the A groups'
-// slots are then written twice with the same words.  Every workgroup races
-// its own slots; the last one of the row to finish (a count per row) writes
-// the selection from the greatest race word.
+// groups - 1 take A's first digits (those >= the digit d of bhi: above it
+// every key is in A, at d some), digit b to group floor(cb(b) (groups - 1) /
+// |A|), cb(b) the keys of the higher digits (k_smp_div's histogram): a group
+// holds whole digits of A, at most |A| < kCap keys, and its slots start at
+// the least cb of its digits.  The last group takes B from the bucket list,
+// cut by digits of B's own histograms (pick_digit from the top) while it is
+// longer than the top_k - |A| words it needs plus kSortDirect, and ranks
+// those words after A.  A row whose lists do not select, or whose ties at an
+// exact threshold exceed kCap, is selected by the last group alone from
+// scans of the row (resolve_row, collect_row, in the bucket list's place)
+// and ranked whole, the A groups leaving at once.  Every workgroup races its
+// own slots; the last one of the row to finish (a count per row) writes the
+// selection from the greatest race word.
 constexpr uint32_t kSortDirect = 1024;
 
 // Sort, descending, of the n <= kCap distinct words of s (at slot(e)) by
@@ -2456,26 +2508,26 @@ __global__ __launch_bounds__(kRankThreads) void k_smp_rank(SmpGeo g, float *logi
     if (threadIdx.x == 0) {
         s_off = kNone;
         s_n = 0;
+        s_pick[0] = kNone;
     }
+    const uint32_t bon = w.sel[row].bon, bhi = w.sel[row].bhi;
+    const uint64_t gfill = w.sel[row].gfill;
     uint32_t total;
     const uint32_t incl = block_incl_scan1024(h.x + h.y, s_tmp, total); // its barriers order the resets
     const uint32_t cb1 = total - incl, cb0 = cb1 + h.y; // keys in the digits above b1, above b0
-    if (cb1 < g.top_k && g.top_k <= cb1 + h.y) {
-        s_pick[0] = b1;
-        s_pick[1] = cb1;
-        s_pick[2] = h.y;
-    }
-    if (cb0 < g.top_k && g.top_k <= cb0 + h.x) {
-        s_pick[0] = b0;
-        s_pick[1] = cb0;
-        s_pick[2] = h.x;
-    }
-    __syncthreads();
-    const uint32_t p1 = s_pick[0], above = s_pick[1], inb = s_pick[2];
-    const uint64_t fill = w.sel[row].gfill;
+    // k_smp_div's lists hold every key above bhi (A) and in [blo, bhi] (B);
+    // they select exactly when |A| < top_k <= |A| + |B| and B fits its list
+    const uint32_t above = static_cast<uint32_t>(gfill), inb = static_cast<uint32_t>(gfill >> 32);
+    const bool listed = bon && above < g.top_k && g.top_k - above <= inb && inb <= kBucketCap; // uniform
     if (q < ga) { // A
-        const uint32_t g0 = (b0 > p1 && h.x) ? cb0 * ga / above : kNone; // a key above P1: above > 0
-        const uint32_t g1 = (b1 > p1 && h.y) ? cb1 * ga / above : kNone;
+        if (!listed) { // uniform: the last group selects from scans
+            group_finish(g, o, w, row, q, 0ull, s_c, 0, groups);
+            return;
+        }
+        // digits above bhi's hold A keys only; bhi's digit d may hold some
+        const uint32_t d = bhi >> 21;
+        const uint32_t g0 = (b0 >= d && h.x && cb0 < above) ? cb0 * ga / above : kNone;
+        const uint32_t g1 = (b1 >= d && h.y && cb1 < above) ? cb1 * ga / above : kNone;
         s_hist[b0] = g0;
         s_hist[b1] = g1;
         if (g0 == q) atomicMin(&s_off, cb0);
@@ -2486,7 +2538,7 @@ __global__ __launch_bounds__(kRankThreads) void k_smp_rank(SmpGeo g, float *logi
             group_finish(g, o, w, row, q, 0ull, s_c, 0, groups);
             return;
         }
-        const uint32_t na = above < static_cast<uint32_t>(fill) ? above : static_cast<uint32_t>(fill); // < kCap
+        const uint32_t na = above; // < top_k <= kCap
         const uint64_t *alist = w.cand + static_cast<uint64_t>(row) * g.cand_ld;
         uint64_t v[kSortPer];
 #pragma unroll
@@ -2504,42 +2556,62 @@ __global__ __launch_bounds__(kRankThreads) void k_smp_rank(SmpGeo g, float *logi
         rank_group(g, o, w, row, q, s0, s_c, n, n, off, groups, s_d, s_hist, s_tmp, &s_tab, pw);
         return;
     }
-    // B: its largest need words after A's slots
+    // B: its largest need words after A's slots.  Its first digit comes from
+    // the row's histogram: digits strictly inside [blo, bhi]'s hold B keys
+    // only, bhi's digit also the A keys not above it, blo's the rest of B.
+    // Later digits, while B is long, from histograms of the list.
     const uint32_t need = g.top_k - above;
     uint64_t *blist = w.bucket + static_cast<uint64_t>(row) * kBucketCap;
-    if (inb <= kBucketCap) { // uniform
-        const uint32_t nb = inb < static_cast<uint32_t>(fill >> 32) ? inb : static_cast<uint32_t>(fill >> 32);
-        RowSel bs{};
-        bs.prefix = p1;
-        bs.depth = 11;
-        bs.need = need;
-        bs.mode = 1;
-        if (nb > kSortDirect) {
-            bs.mode = 0;
-            for (uint32_t pass = 1; pass <= 2 && bs.mode == 0; ++pass) {
-                const uint32_t bits = pass == 2 ? 10u : 11u, nbins = 1u << bits;
-                const uint32_t dshift = 32u - bs.depth, shift = dshift - bits;
-                for (uint32_t b = threadIdx.x; b < nbins; b += kRankThreads) s_hist[b] = 0;
-                __syncthreads();
-                for (uint32_t i0 = 0; i0 < nb; i0 += kSortPer * kRankThreads) {
-                    uint32_t key[kSortPer];
-#pragma unroll
-                    for (uint32_t k = 0; k < kSortPer; ++k) {
-                        const uint32_t i = i0 + threadIdx.x + k * kRankThreads;
-                        key[k] = i < nb ? static_cast<uint32_t>(blist[i] >> 32) : 0u;
-                    }
-#pragma unroll
-                    for (uint32_t k = 0; k < kSortPer; ++k) {
-                        const uint32_t i = i0 + threadIdx.x + k * kRankThreads;
-                        if (i < nb && (key[k] >> dshift) == bs.prefix) atomicAdd(&s_hist[(key[k] >> shift) & (nbins - 1)], 1u);
-                    }
-                }
-                __syncthreads();
-                bs = pick_digit(bs, s_hist, bits, s_tmp, s_pick);
+    if (listed) { // uniform
+        const uint32_t nb = inb;
+        const uint32_t dlo = w.sel[row].blo >> 21, dhi = bhi >> 21;
+        auto b_digit = [&](uint32_t b, uint32_t hb, uint32_t cb) {
+            if (b < dlo || b > dhi) return;
+            const uint32_t higher = b == dhi ? 0u : cb - above; // B keys in the digits above b
+            const uint32_t here = dlo == dhi ? nb : b == dhi ? hb - (above - cb) : b == dlo ? nb - higher : hb;
+            if (higher < need && need <= higher + here) {
+                s_pick[0] = b;
+                s_pick[1] = higher;
+                s_pick[2] = here;
             }
+        };
+        b_digit(b0, h.x, cb0);
+        b_digit(b1, h.y, cb1);
+        __syncthreads();
+        RowSel bs{};
+        if (s_pick[0] == kNone) bs.mode = 2; // uniform; cannot happen with consistent counts: scans
+        bs.prefix = s_pick[0];
+        bs.depth = 11;
+        bs.above = s_pick[1];
+        bs.need = need - s_pick[1];
+        bs.count = s_pick[1] + s_pick[2];
+        if (bs.mode != 2) bs.mode = bs.count <= kCap ? 1u : 0u;
+        const uint32_t enough = need + kSortDirect < kCap ? need + kSortDirect : kCap; // words worth one sort
+        for (uint32_t pass = 1; pass < 3 && bs.mode != 2 && bs.count > enough; ++pass) {
+            const uint32_t bits = pass == 2 ? 10u : 11u, nbins = 1u << bits;
+            const uint32_t shift = 32u - bs.depth - bits;
+            bs.mode = 0;
+            for (uint32_t b = threadIdx.x; b < nbins; b += kRankThreads) s_hist[b] = 0;
+            __syncthreads();
+            for (uint32_t i0 = 0; i0 < nb; i0 += kSortPer * kRankThreads) {
+                uint32_t key[kSortPer];
+#pragma unroll
+                for (uint32_t k = 0; k < kSortPer; ++k) {
+                    const uint32_t i = i0 + threadIdx.x + k * kRankThreads;
+                    key[k] = i < nb ? static_cast<uint32_t>(blist[i] >> 32) : 0u;
+                }
+#pragma unroll
+                for (uint32_t k = 0; k < kSortPer; ++k) {
+                    const uint32_t i = i0 + threadIdx.x + k * kRankThreads;
+                    const bool match = bs.depth == 0 || (key[k] >> (32u - bs.depth)) == bs.prefix;
+                    if (i < nb && match) atomicAdd(&s_hist[(key[k] >> shift) & (nbins - 1)], 1u);
+                }
+            }
+            __syncthreads();
+            bs = pick_digit(bs, s_hist, bits, s_tmp, s_pick);
+            if (bs.mode == 0) bs.count = nb; // still more than kCap: refine further
         }
         if (bs.mode == 1) { // uniform; else the ties at T exceed kCap
-            const uint32_t dshift = 32u - bs.depth;
             for (uint32_t i0 = 0; i0 < nb; i0 += kSortPer * kRankThreads) {
                 uint64_t v[kSortPer];
 #pragma unroll
@@ -2550,7 +2622,8 @@ __global__ __launch_bounds__(kRankThreads) void k_smp_rank(SmpGeo g, float *logi
 #pragma unroll
                 for (uint32_t k = 0; k < kSortPer; ++k) {
                     const uint32_t i = i0 + threadIdx.x + k * kRankThreads;
-                    wave_append(i < nb && (static_cast<uint32_t>(v[k] >> 32) >> dshift) >= bs.prefix, v[k], &s_n, s_c);
+                    const uint32_t key = static_cast<uint32_t>(v[k] >> 32);
+                    wave_append(i < nb && (bs.depth == 0 || (key >> (32u - bs.depth)) >= bs.prefix), v[k], &s_n, s_c);
                 }
             }
             __syncthreads();
@@ -2754,7 +2827,7 @@ void plan_chunks(uint32_t rows, uint64_t card, uint64_t &chunk_cols, uint32_t &c
 uint64_t align256(uint64_t b) { return (b + 255) & ~uint64_t{255}; }
 
 struct WsLayout {
-    uint64_t part, psum, sub, seg, sel, hist, ties, cand, cand2, bucket, gbest, total;
+    uint64_t part, psum, sub, seg, sel, hist, ehist, ties, cand, cand2, bucket, gbest, total;
 };
 
 // Geometry of a launch (what launch_sampler derives from its arguments).
@@ -2768,9 +2841,6 @@ SmpGeo plan_geo(uint32_t rows, uint64_t card, uint32_t top_k)
     g.cand_ld = top_k > kCap ? top_k : kCap;
     return g;
 }
-
-// The bucket path: top_k <= kCap without the fast list.
-bool bucket_path(const SmpGeo &g) { return g.top_k <= kCap && !fast_list_possible(g); }
 
 // k_smp_rank's workgroups per row: A groups of about 1024 keys (at most
 // kMaxGroups - 1, and at most kRankWgs workgroups in all while there are
@@ -2795,7 +2865,8 @@ WsLayout layout(uint32_t rows, uint32_t chunks, uint64_t chunk_cols, uint64_t ca
     l.seg = l.sub + align256(uint64_t{rows} * chunks * spc * sizeof(SubSum));
     l.sel = l.seg + align256(uint64_t{rows} * chunks * spc * sizeof(SegInfo));
     l.hist = l.sel + align256(uint64_t{rows} * sizeof(RowSel));
-    l.ties = l.hist + align256(uint64_t{rows} * kBins * sizeof(uint32_t));
+    l.ehist = l.hist + align256(uint64_t{rows} * kBins * sizeof(uint32_t));
+    l.ties = l.ehist + align256(uint64_t{rows} * kBins * sizeof(uint32_t));
     l.cand = l.ties + align256(uint64_t{rows} * chunks * sizeof(uint32_t));
     l.cand2 = l.cand + align256(uint64_t{rows} * cand_ld * sizeof(uint64_t));
     l.bucket = merge ? l.cand2 + align256(uint64_t{rows} * cand_ld * sizeof(uint64_t)) : l.cand2;
@@ -2831,6 +2902,7 @@ hipError_t launch_sampler(const SamplerArgs &a, hipStream_t s)
     w.seg = reinterpret_cast<SegInfo *>(base + l.seg);
     w.sel = reinterpret_cast<RowSel *>(base + l.sel);
     w.hist = reinterpret_cast<uint32_t *>(base + l.hist);
+    w.ehist = reinterpret_cast<uint32_t *>(base + l.ehist);
     w.ties = reinterpret_cast<uint32_t *>(base + l.ties);
     w.cand = reinterpret_cast<uint64_t *>(base + l.cand);
     w.cand2 = reinterpret_cast<uint64_t *>(base + l.cand2);
@@ -2840,26 +2912,27 @@ hipError_t launch_sampler(const SamplerArgs &a, hipStream_t s)
     const dim3 grid(a.rows * g.chunks);
     if (g.chunk_cols <= kFuseCols) {
         k_smp_max<true><<<grid, kBlock, 0, s>>>(g, a.logits, w);
-        k_smp_expseg<<<dim3(a.rows + a.rows * g.chunks), kBlock, 0, s>>>(g, a.logits, w);
+        if (bucket) k_smp_expseg<true><<<dim3(a.rows + a.rows * g.chunks), kBlock, 0, s>>>(g, a.logits, w);
+        else k_smp_expseg<false><<<dim3(a.rows + a.rows * g.chunks), kBlock, 0, s>>>(g, a.logits, w);
     } else {
         k_smp_max<false><<<grid, kBlock, 0, s>>>(g, a.logits, w);
-        k_smp_exp<<<grid, kBlock, 0, s>>>(g, a.logits, w);
+        if (bucket) k_smp_exp<true><<<grid, kBlock, 0, s>>>(g, a.logits, w);
+        else k_smp_exp<false><<<grid, kBlock, 0, s>>>(g, a.logits, w);
         k_smp_seg<<<grid, kBlock, 0, s>>>(g, a.logits, w);
     }
-    k_smp_sum<<<a.rows, kSumThreads, 0, s>>>(g, a.logits, w);
-    k_smp_div<<<grid, kBlock, 0, s>>>(g, a.logits, w);
+    k_smp_sum<<<a.rows, bucket ? kSumThreads : 2 * kWave, 0, s>>>(g, a.logits, w);
+    if (bucket) k_smp_divlist<<<grid, kBlock, 0, s>>>(g, a.logits, w);
+    else k_smp_div<<<grid, kBlock, 0, s>>>(g, a.logits, w);
     // Rows resolved by the fast list need no selection: when the fast list
     // applies, k_smp_tail selects (in one workgroup per row, for the rows it
-    // left) and ranks in one launch.  Otherwise, up to kCap, k_smp_bucket
-    // lists the candidates by their first digit and k_smp_rank selects and
+    // left) and ranks in one launch.  Otherwise, up to kCap, k_smp_div has
+    // listed the candidates around the bracket and k_smp_rank selects and
     // ranks in groups; above kCap the selection kernels spread the
     // candidate list over (row, chunk) workgroups for the merge sort.
     const bool tail = !merge && !bucket;
     if (merge) {
         k_smp_resolve<<<a.rows, kResolveThreads, 0, s>>>(g, a.logits, w);
         k_smp_collect<<<grid, kBlock, 0, s>>>(g, a.logits, w);
-    } else if (bucket) {
-        k_smp_bucket<<<grid, kBlock, 0, s>>>(g, a.logits, w);
     }
 
     SmpOut o{};
