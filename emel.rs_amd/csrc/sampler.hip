@@ -405,13 +405,14 @@ __host__ __device__ inline bool fast_list_possible(const SmpGeo &g)
 // The bucket path: top_k <= kCap without the fast list.
 __host__ __device__ inline bool bucket_path(const SmpGeo &g) { return g.top_k <= kCap && !fast_list_possible(g); }
 
-// Adds the LDS histogram of a workgroup to the row's global histogram.
-__device__ __forceinline__ void flush_hist(uint32_t *s_hist, uint32_t nbins, uint32_t *dst)
+// Adds the LDS histogram of a workgroup to the row's global histogram, bin b
+// to dst[(b + rot) mod nbins] (nbins a power of two).
+__device__ __forceinline__ void flush_hist(uint32_t *s_hist, uint32_t nbins, uint32_t *dst, uint32_t rot = 0)
 {
     __syncthreads();
     for (uint32_t b = threadIdx.x; b < nbins; b += blockDim.x) {
         const uint32_t c = s_hist[b];
-        if (c) atomicAdd(dst + b, c);
+        if (c) atomicAdd(dst + ((b + rot) & (nbins - 1)), c);
     }
 }
 
@@ -572,9 +573,9 @@ __global__ __launch_bounds__(kBlock) void k_smp_exp(SmpGeo g, float *logits, Smp
         const float s = v * scale;
         v = emel_expf(s - m, s_tab, ec);
         acc += static_cast<double>(v);
-        if constexpr (eh) atomicAdd(&s_eh[total_key(v) >> 21], 1u);
+        if constexpr (eh) atomicAdd(&s_eh[__builtin_bit_cast(uint32_t, v) >> 21], 1u);
     });
-    if constexpr (eh) flush_hist(s_eh, kBins, w.ehist + static_cast<uint64_t>(row) * kBins);
+    if constexpr (eh) flush_hist(s_eh, kBins, w.ehist + static_cast<uint64_t>(row) * kBins, kBins / 2);
     // f64 chunk sum: only a prediction of where the exact sum's binades
     // change (k_smp_seg); never part of a result
     __shared__ double s_acc[kBlock / kWave];
@@ -1009,7 +1010,9 @@ __global__ __launch_bounds__(kBlock) void k_smp_expseg(SmpGeo g, float *logits, 
     float *x = logits + static_cast<int64_t>(row) * g.ld;
     uint64_t c0, c1;
     chunk_range(g, chunk, c0, c1);
-    // the bucket path: the histogram of e's first digits (flushed at the end)
+    // the bucket path: the histogram of e's first digits (flushed at the end).
+    // e is +0 or more, or NaN, so its key is its bits with the top bit set and
+    // the bins count bits >> 21, which the flush moves up by kBins / 2.
     __shared__ uint32_t s_eh[EH ? kBins : 1];
     constexpr bool eh = EH;
     if constexpr (eh) {
@@ -1072,14 +1075,14 @@ __global__ __launch_bounds__(kBlock) void k_smp_expseg(SmpGeo g, float *logits, 
             for (uint32_t q = 0; q < kPer; ++q) cur[q] = emel_expf(cur[q] * scale - m, tab, ec);
             if constexpr (eh)
 #pragma unroll
-                for (uint32_t q = 0; q < kPer; ++q) atomicAdd(&s_eh[total_key(cur[q]) >> 21], 1u);
+                for (uint32_t q = 0; q < kPer; ++q) atomicAdd(&s_eh[__builtin_bit_cast(uint32_t, cur[q]) >> 21], 1u);
         } else {
 #pragma unroll
             for (uint32_t q = 0; q < kPer; ++q) {
                 const bool in = split_col(a0, lane, q) < c1;
                 cur[q] = in ? emel_expf(cur[q] * scale - m, tab, ec) : 0.0f;
                 if constexpr (eh)
-                    if (in) atomicAdd(&s_eh[total_key(cur[q]) >> 21], 1u);
+                    if (in) atomicAdd(&s_eh[__builtin_bit_cast(uint32_t, cur[q]) >> 21], 1u);
             }
         }
 #pragma unroll
@@ -1102,7 +1105,7 @@ __global__ __launch_bounds__(kBlock) void k_smp_expseg(SmpGeo g, float *logits, 
             for (uint32_t q = 0; q < kPer; ++q) cur[q] = nxt[q];
         }
     }
-    if constexpr (eh) flush_hist(s_eh, kBins, w.ehist + static_cast<uint64_t>(row) * kBins);
+    if constexpr (eh) flush_hist(s_eh, kBins, w.ehist + static_cast<uint64_t>(row) * kBins, kBins / 2);
 }
 
 // ---- stage 3: the exact sequential sum of e ----------------------------------
@@ -2524,10 +2527,17 @@ __global__ __launch_bounds__(kRankThreads) void k_smp_rank(SmpGeo g, float *logi
             group_finish(g, o, w, row, q, 0ull, s_c, 0, groups);
             return;
         }
-        // digits above bhi's hold A keys only; bhi's digit d may hold some
+        // digits above bhi's hold A keys only; bhi's digit d may hold some.  A
+        // digit goes to the group of its A keys' middle (cb plus half of them),
+        // which stays monotone in the digit and balances the groups better
+        // than the digit's start
         const uint32_t d = bhi >> 21;
-        const uint32_t g0 = (b0 >= d && h.x && cb0 < above) ? cb0 * ga / above : kNone;
-        const uint32_t g1 = (b1 >= d && h.y && cb1 < above) ? cb1 * ga / above : kNone;
+        auto group_of = [&](uint32_t b, uint32_t hb, uint32_t cb) {
+            if (b < d || hb == 0 || cb >= above) return kNone;
+            const uint32_t ha = b == d ? above - cb : hb; // A keys of digit b
+            return (cb + ha / 2) * ga / above;
+        };
+        const uint32_t g0 = group_of(b0, h.x, cb0), g1 = group_of(b1, h.y, cb1);
         s_hist[b0] = g0;
         s_hist[b1] = g1;
         if (g0 == q) atomicMin(&s_off, cb0);
