@@ -2307,10 +2307,10 @@ __device__ void collect_row(const SmpGeo &g, const float *x, uint64_t *list, con
 
 // The bucket path's ranking: `groups` workgroups per row.  Groups q <
 // groups - 1 take A's first digits (those >= the digit d of bhi: above it
-// every key is in A, at d some), digit b to group floor(cb(b) (groups - 1) /
-// |A|), cb(b) the keys of the higher digits (k_smp_div's histogram): a group
-// holds whole digits of A, at most |A| < kCap keys, and its slots start at
-// the least cb of its digits.  The last group takes B from the bucket list,
+// every key is in A, at d some), digit b to group floor((cb(b) + a(b) / 2)
+// (groups - 1) / |A|), cb(b) the keys of the higher digits (the division's
+// histogram) and a(b) the digit's A keys: a group holds whole digits of A, at
+// most |A| < kCap keys, and its slots start at the least cb of its digits.  The last group takes B from the bucket list,
 // cut by digits of B's own histograms (pick_digit from the top) while it is
 // longer than the top_k - |A| words it needs plus kSortDirect, and ranks
 // those words after A.  A row whose lists do not select, or whose ties at an
