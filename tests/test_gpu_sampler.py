@@ -114,7 +114,7 @@ def test_config5_vocabulary_batch(gpu):
 @pytest.mark.parametrize("top_k,temperature", [(8192, 1.0), (1, 0.8), (4096, 0.5)])
 def test_config5_vocabulary_large_and_single_top_k(gpu, top_k, temperature):
     """Full 151,936-token rows at the bench's second case (top_k 8192: the
-    threshold needs the later radix digits, found by row scans) and at the
+    bucket path, its bracket's two lists and the grouped ranking) and at the
     extremes of top_k."""
     g = np.random.Generator(np.random.PCG64(502 + top_k))
     x = g.standard_normal((6, 151936), dtype=np.float64).astype(np.float32)
@@ -220,6 +220,16 @@ def test_fast_candidate_list_and_its_fallback(gpu):
     x[1] = 0.0
     x[3, g.choice(card, 10000, replace=False)] = 5.0
     check(gpu, x, 1.0, 40, [11, 13, 17, 19])
+
+
+@pytest.mark.parametrize("rows,top_k", [(1, 8192), (2, 5000), (2, 300)])
+def test_bucket_path_group_counts(gpu, rows, top_k):
+    """The bucket path's ranking with 8 workgroups for one row (7 digit
+    groups of A, then B), 6 for top_k 5000 and 2 for top_k 300 (just above
+    config 5's 297 sub-chunks, so no fast list), on full 151,936-token rows."""
+    g = np.random.Generator(np.random.PCG64(900 + top_k))
+    x = (g.standard_normal((rows, 151936)) * 1.5).astype(np.float32)
+    check(gpu, x, 0.9, top_k, [int(s) for s in g.integers(1, M, rows)])
 
 
 def test_bucket_path_cases(gpu):
