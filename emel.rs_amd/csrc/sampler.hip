@@ -2477,7 +2477,8 @@ __device__ __forceinline__ void wave_append(bool take, uint64_t v, uint32_t *s_n
 }
 
 // Ranks the n <= kCap words staged in s_c, on wave 0 alone when they are few.
-__device__ void rank_group(const SmpGeo &g, const SmpOut &o, const SmpWs &w, uint32_t row, uint32_t q, uint32_t s0,
+__device__ __forceinline__ void rank_group(const SmpGeo &g, const SmpOut &o, const SmpWs &w, uint32_t row, uint32_t q,
+                                           uint32_t s0,
                            uint64_t *s_c, uint32_t n, uint32_t out, uint32_t slot0, uint32_t groups, uint64_t *s_d,
                            uint32_t *s_cnt, uint32_t *s_tmp, const LogfTab *tab, uint32_t pw)
 {
@@ -2515,6 +2516,7 @@ __global__ __launch_bounds__(kRankThreads) void k_smp_rank(SmpGeo g, float *logi
     }
     const uint32_t bon = w.sel[row].bon, bhi = w.sel[row].bhi;
     const uint64_t gfill = w.sel[row].gfill;
+    uint32_t n = 0, out = 0, slot0 = 0; // the words staged in s_c, how many to rank, from which slot
     uint32_t total;
     const uint32_t incl = block_incl_scan1024(h.x + h.y, s_tmp, total); // its barriers order the resets
     const uint32_t cb1 = total - incl, cb0 = cb1 + h.y; // keys in the digits above b1, above b0
@@ -2562,98 +2564,105 @@ __global__ __launch_bounds__(kRankThreads) void k_smp_rank(SmpGeo g, float *logi
             wave_append(i < na && s_hist[static_cast<uint32_t>(v[k] >> 53)] == q, v[k], &s_n, s_c);
         }
         __syncthreads();
-        const uint32_t n = s_n < kCap ? s_n : kCap;
-        rank_group(g, o, w, row, q, s0, s_c, n, n, off, groups, s_d, s_hist, s_tmp, &s_tab, pw);
-        return;
-    }
-    // B: its largest need words after A's slots.  Its first digit comes from
-    // the row's histogram: digits strictly inside [blo, bhi]'s hold B keys
-    // only, bhi's digit also the A keys not above it, blo's the rest of B.
-    // Later digits, while B is long, from histograms of the list.
-    const uint32_t need = g.top_k - above;
-    uint64_t *blist = w.bucket + static_cast<uint64_t>(row) * kBucketCap;
-    if (listed) { // uniform
-        const uint32_t nb = inb;
-        const uint32_t dlo = w.sel[row].blo >> 21, dhi = bhi >> 21;
-        auto b_digit = [&](uint32_t b, uint32_t hb, uint32_t cb) {
-            if (b < dlo || b > dhi) return;
-            const uint32_t higher = b == dhi ? 0u : cb - above; // B keys in the digits above b
-            const uint32_t here = dlo == dhi ? nb : b == dhi ? hb - (above - cb) : b == dlo ? nb - higher : hb;
-            if (higher < need && need <= higher + here) {
-                s_pick[0] = b;
-                s_pick[1] = higher;
-                s_pick[2] = here;
-            }
-        };
-        b_digit(b0, h.x, cb0);
-        b_digit(b1, h.y, cb1);
-        __syncthreads();
-        RowSel bs{};
-        if (s_pick[0] == kNone) bs.mode = 2; // uniform; cannot happen with consistent counts: scans
-        bs.prefix = s_pick[0];
-        bs.depth = 11;
-        bs.above = s_pick[1];
-        bs.need = need - s_pick[1];
-        bs.count = s_pick[1] + s_pick[2];
-        if (bs.mode != 2) bs.mode = bs.count <= kCap ? 1u : 0u;
-        const uint32_t enough = need + kSortDirect < kCap ? need + kSortDirect : kCap; // words worth one sort
-        for (uint32_t pass = 1; pass < 3 && bs.mode != 2 && bs.count > enough; ++pass) {
-            const uint32_t bits = pass == 2 ? 10u : 11u, nbins = 1u << bits;
-            const uint32_t shift = 32u - bs.depth - bits;
-            bs.mode = 0;
-            for (uint32_t b = threadIdx.x; b < nbins; b += kRankThreads) s_hist[b] = 0;
-            __syncthreads();
-            for (uint32_t i0 = 0; i0 < nb; i0 += kSortPer * kRankThreads) {
-                uint32_t key[kSortPer];
-#pragma unroll
-                for (uint32_t k = 0; k < kSortPer; ++k) {
-                    const uint32_t i = i0 + threadIdx.x + k * kRankThreads;
-                    key[k] = i < nb ? static_cast<uint32_t>(blist[i] >> 32) : 0u;
+        n = s_n < kCap ? s_n : kCap;
+        out = n;
+        slot0 = off;
+    } else {
+        // B: its largest need words after A's slots.  Its first digit comes from
+        // the row's histogram: digits strictly inside [blo, bhi]'s hold B keys
+        // only, bhi's digit also the A keys not above it, blo's the rest of B.
+        // Later digits, while B is long, from histograms of the list.
+        const uint32_t need = g.top_k - above;
+        uint64_t *blist = w.bucket + static_cast<uint64_t>(row) * kBucketCap;
+        bool scan = true;
+        if (listed) { // uniform
+            const uint32_t nb = inb;
+            const uint32_t dlo = w.sel[row].blo >> 21, dhi = bhi >> 21;
+            auto b_digit = [&](uint32_t b, uint32_t hb, uint32_t cb) {
+                if (b < dlo || b > dhi) return;
+                const uint32_t higher = b == dhi ? 0u : cb - above; // B keys in the digits above b
+                const uint32_t here = dlo == dhi ? nb : b == dhi ? hb - (above - cb) : b == dlo ? nb - higher : hb;
+                if (higher < need && need <= higher + here) {
+                    s_pick[0] = b;
+                    s_pick[1] = higher;
+                    s_pick[2] = here;
                 }
+            };
+            b_digit(b0, h.x, cb0);
+            b_digit(b1, h.y, cb1);
+            __syncthreads();
+            RowSel bs{};
+            if (s_pick[0] == kNone) bs.mode = 2; // uniform; cannot happen with consistent counts: scans
+            bs.prefix = s_pick[0];
+            bs.depth = 11;
+            bs.above = s_pick[1];
+            bs.need = need - s_pick[1];
+            bs.count = s_pick[1] + s_pick[2];
+            if (bs.mode != 2) bs.mode = bs.count <= kCap ? 1u : 0u;
+            const uint32_t enough = need + kSortDirect < kCap ? need + kSortDirect : kCap; // words worth one sort
+            for (uint32_t pass = 1; pass < 3 && bs.mode != 2 && bs.count > enough; ++pass) {
+                const uint32_t bits = pass == 2 ? 10u : 11u, nbins = 1u << bits;
+                const uint32_t shift = 32u - bs.depth - bits;
+                bs.mode = 0;
+                for (uint32_t b = threadIdx.x; b < nbins; b += kRankThreads) s_hist[b] = 0;
+                __syncthreads();
+                for (uint32_t i0 = 0; i0 < nb; i0 += kSortPer * kRankThreads) {
+                    uint32_t key[kSortPer];
 #pragma unroll
-                for (uint32_t k = 0; k < kSortPer; ++k) {
-                    const uint32_t i = i0 + threadIdx.x + k * kRankThreads;
-                    const bool match = bs.depth == 0 || (key[k] >> (32u - bs.depth)) == bs.prefix;
-                    if (i < nb && match) atomicAdd(&s_hist[(key[k] >> shift) & (nbins - 1)], 1u);
+                    for (uint32_t k = 0; k < kSortPer; ++k) {
+                        const uint32_t i = i0 + threadIdx.x + k * kRankThreads;
+                        key[k] = i < nb ? static_cast<uint32_t>(blist[i] >> 32) : 0u;
+                    }
+#pragma unroll
+                    for (uint32_t k = 0; k < kSortPer; ++k) {
+                        const uint32_t i = i0 + threadIdx.x + k * kRankThreads;
+                        const bool match = bs.depth == 0 || (key[k] >> (32u - bs.depth)) == bs.prefix;
+                        if (i < nb && match) atomicAdd(&s_hist[(key[k] >> shift) & (nbins - 1)], 1u);
+                    }
+                }
+                __syncthreads();
+                bs = pick_digit(bs, s_hist, bits, s_tmp, s_pick);
+                if (bs.mode == 0) bs.count = nb; // still more than kCap: refine further
+            }
+            if (bs.mode == 1) { // uniform; else the ties at T exceed kCap
+                for (uint32_t i0 = 0; i0 < nb; i0 += kSortPer * kRankThreads) {
+                    uint64_t v[kSortPer];
+#pragma unroll
+                    for (uint32_t k = 0; k < kSortPer; ++k) {
+                        const uint32_t i = i0 + threadIdx.x + k * kRankThreads;
+                        v[k] = i < nb ? blist[i] : 0ull;
+                    }
+#pragma unroll
+                    for (uint32_t k = 0; k < kSortPer; ++k) {
+                        const uint32_t i = i0 + threadIdx.x + k * kRankThreads;
+                        const uint32_t key = static_cast<uint32_t>(v[k] >> 32);
+                        wave_append(i < nb && (bs.depth == 0 || (key >> (32u - bs.depth)) >= bs.prefix), v[k], &s_n, s_c);
+                    }
+                }
+                __syncthreads();
+                n = s_n; // bs.count <= kCap
+                if (n <= kCap) { // uniform
+                    out = need < n ? need : n;
+                    slot0 = above;
+                    scan = false;
                 }
             }
-            __syncthreads();
-            bs = pick_digit(bs, s_hist, bits, s_tmp, s_pick);
-            if (bs.mode == 0) bs.count = nb; // still more than kCap: refine further
         }
-        if (bs.mode == 1) { // uniform; else the ties at T exceed kCap
-            for (uint32_t i0 = 0; i0 < nb; i0 += kSortPer * kRankThreads) {
-                uint64_t v[kSortPer];
-#pragma unroll
-                for (uint32_t k = 0; k < kSortPer; ++k) {
-                    const uint32_t i = i0 + threadIdx.x + k * kRankThreads;
-                    v[k] = i < nb ? blist[i] : 0ull;
-                }
-#pragma unroll
-                for (uint32_t k = 0; k < kSortPer; ++k) {
-                    const uint32_t i = i0 + threadIdx.x + k * kRankThreads;
-                    const uint32_t key = static_cast<uint32_t>(v[k] >> 32);
-                    wave_append(i < nb && (bs.depth == 0 || (key >> (32u - bs.depth)) >= bs.prefix), v[k], &s_n, s_c);
-                }
-            }
-            __syncthreads();
-            const uint32_t n = s_n; // bs.count <= kCap
-            if (n <= kCap) { // uniform
-                rank_group(g, o, w, row, q, s0, s_c, n, need < n ? need : n, above, groups, s_d, s_hist, s_tmp, &s_tab, pw);
-                return;
-            }
+        if (scan) { // uniform: the whole row from scans
+            __syncthreads(); // every thread has read s_pick, which resolve_row rewrites
+            RowSel rs{};
+            rs.need = g.top_k;
+            rs = resolve_row(g, logits, w, row, rs, s_hist, s_tmp, s_pick);
+            collect_row(g, logits + static_cast<int64_t>(row) * g.ld, blist, rs, s_tmp);
+            __syncthreads(); // the list, written by the whole workgroup, is staged next
+            n = rs.count < kCap ? rs.count : kCap;
+            stage_words<kRankThreads>(s_c, blist, n, n);
+            out = g.top_k;
+            slot0 = 0;
         }
     }
-    // the whole row from scans
-    __syncthreads(); // every thread has read s_pick, which resolve_row rewrites
-    RowSel rs{};
-    rs.need = g.top_k;
-    rs = resolve_row(g, logits, w, row, rs, s_hist, s_tmp, s_pick);
-    collect_row(g, logits + static_cast<int64_t>(row) * g.ld, blist, rs, s_tmp);
-    __syncthreads(); // the list, written by the whole workgroup, is staged next
-    const uint32_t n = rs.count < kCap ? rs.count : kCap;
-    stage_words<kRankThreads>(s_c, blist, n, n);
-    rank_group(g, o, w, row, q, s0, s_c, n, g.top_k, 0, groups, s_d, s_hist, s_tmp, &s_tab, pw);
+    // one call site: rank_group inlines, so its LDS buffers keep their address space
+    rank_group(g, o, w, row, q, s0, s_c, n, out, slot0, groups, s_d, s_hist, s_tmp, &s_tab, pw);
 }
 
 // A launch whose rows can take the fast list: one workgroup per row
