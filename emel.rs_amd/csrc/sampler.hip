@@ -2533,11 +2533,14 @@ __global__ __launch_bounds__(kRankThreads) void k_smp_rank(SmpGeo g, float *logi
         // digit goes to the group of its A keys' middle (cb plus half of them),
         // which stays monotone in the digit and balances the groups better
         // than the digit's start
+        // (shifted by |A| / (6 ga): the top group spans the widest key range,
+        // whose fine bins are the densest, so it takes a smaller share)
         const uint32_t d = bhi >> 21;
         auto group_of = [&](uint32_t b, uint32_t hb, uint32_t cb) {
             if (b < d || hb == 0 || cb >= above) return kNone;
             const uint32_t ha = b == d ? above - cb : hb; // A keys of digit b
-            return (cb + ha / 2) * ga / above;
+            const uint32_t gq = (cb + ha / 2 + above / (6 * ga)) * ga / above;
+            return gq < ga ? gq : ga - 1;
         };
         const uint32_t g0 = group_of(b0, h.x, cb0), g1 = group_of(b1, h.y, cb1);
         s_hist[b0] = g0;
